@@ -1,0 +1,185 @@
+/* q3h.h - C ABI of libq3h, the MI355X (gfx950) engine of the Qwen3-TTS frame
+ * step: the talker (Qwen3, 28 layers) and the code predictor (Qwen3, 5 layers,
+ * 15 forwards per frame), with device-resident weights and K/V caches.
+ *
+ * Every entry point is extern "C", cdecl, takes plain pointers and sizes, and
+ * returns an int status: 0 on success, a negative Q3H_E* code on failure, with
+ * the message in q3h_last_error() (thread-local, valid until the next call on
+ * the same thread). Ownership follows mormot.ai.tts.qwen.lm.pas:364-368
+ * (TQwenLm.Destroy): contexts and frames before their stacks, stacks before
+ * their device. A stack may serve contexts used from several threads at once;
+ * one context (or frame) is used by one thread at a time
+ * (mormot.ai.tts.qwen.talker.pas:77). Each entry point makes its device
+ * current, so calls may arrive on any thread (mormot.ai.tts.qwen.pas:281-291).
+ *
+ * Each declaration names the reference interface it replaces (paths relative
+ * to the reference checkout). The mormot2-ai engine those Pascal call sites
+ * reach (TQwen3Model, TQwen3Vulkan, TDecoderContext) is an un-vendored
+ * submodule; only its call sites in the reference tree are cited.
+ */
+#ifndef Q3H_H
+#define Q3H_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* weight formats: the host side of q3h_stack_create / q3h_stack_add_head,
+   and the storage of a stack (TInferDType idtF32 / idtQ8_0) */
+#define Q3H_F32 0
+#define Q3H_Q8_0 1 /* ggml block_q8_0 on the host: fp16 scale + 32 int8, 34 B */
+
+/* status codes */
+#define Q3H_OK 0
+#define Q3H_E_ARG (-1)      /* invalid argument or shape */
+#define Q3H_E_HIP (-2)      /* a HIP runtime call failed */
+#define Q3H_E_CAPACITY (-3) /* a context would exceed its positions */
+#define Q3H_E_STATE (-4)    /* call out of order (e.g. step before start) */
+#define Q3H_E_NODEV (-5)    /* no usable gfx950 device */
+
+typedef struct q3h_device q3h_device;
+typedef struct q3h_stack q3h_stack;
+typedef struct q3h_context q3h_context;
+typedef struct q3h_frame q3h_frame;
+
+/* TDecoderConfig (mormot.ai.tts.qwen.lm.pas:184-191) + TQwen3Vulkan.KvF16
+   (lm.pas:353) + the numerics of the Q8_0 products */
+typedef struct {
+  int32_t layers, hidden, heads, kv_heads, head_dim, intermediate;
+  float rms_eps, rope_theta;
+  int32_t dtype;         /* storage: Q3H_F32 or Q3H_Q8_0 (weights and heads) */
+  int32_t kv_f16;        /* K/V cache in half floats (lm.pas:128-130) */
+  int32_t act_q8;        /* Q8_0 only: 1 = activations quantized per 32-block
+                            (int8 products, ggml vec_dot_q8_0_q8_0); 0 = f32
+                            activations times dequantized weights */
+  int32_t max_positions; /* the largest context of this stack (RoPE table) */
+} q3h_stack_config;
+
+/* one layer, host memory, matrices [out][in] row-major in src_dtype */
+typedef struct {
+  const void *wq, *wk, *wv, *wo, *wgate, *wup, *wdown;
+  const float *input_norm, *post_norm; /* [hidden] */
+  const float *q_norm, *k_norm;        /* [head_dim] */
+} q3h_layer_weights;
+
+typedef struct {
+  int32_t src_dtype;               /* Q3H_F32 or Q3H_Q8_0 (ggml blocks) */
+  const q3h_layer_weights *layers; /* [layers] */
+  const float *final_norm;         /* [hidden] */
+} q3h_weights;
+
+/* ---- device: replaces TQwenVulkan (lm.pas:44-62, 202-222) ---- */
+
+/* 1 when a gfx950 device is present (TQwenVulkan.Available, lm.pas:202-205) */
+int q3h_device_available(void);
+/* TQwenVulkan.Create (lm.pas:207-211) */
+int q3h_device_open(int ordinal, q3h_device **out);
+/* TQwenVulkan.DeviceName (lm.pas:219-222); NULL on a NULL device */
+const char *q3h_device_name(const q3h_device *dev);
+/* TQwenVulkan.DeviceBytes (lm.pas:57-59): the weight bytes of its stacks */
+int64_t q3h_device_bytes(const q3h_device *dev);
+/* TQwenVulkan.Destroy (lm.pas:213-217) */
+int q3h_device_close(q3h_device *dev);
+/* the message of the last failure on this thread ("" if none) */
+const char *q3h_last_error(void);
+
+/* ---- stack: replaces TQwen3Model.CreateStack (lm.pas:174-179) followed by
+   TQwen3Vulkan.Create(model, backend) (lm.pas:351); the library copies (and
+   quantizes or repacks) the host weights, so they may be freed on return ---- */
+int q3h_stack_create(q3h_device *dev, const q3h_stack_config *cfg,
+                     const q3h_weights *w, q3h_stack **out);
+/* TQwenLmHeads.Add (lm.pas:277-308): a head [rows][hidden] in src_dtype,
+   stored in the stack's dtype; *index receives its number (0, 1, ...) */
+int q3h_stack_add_head(q3h_stack *s, const void *w, int rows, int src_dtype,
+                       int *index);
+/* StackBytes (lm.pas:182-197) of the layers on the device, heads excluded */
+int64_t q3h_stack_bytes(const q3h_stack *s);
+/* TQwen3Vulkan.Free (lm.pas:366) */
+int q3h_stack_destroy(q3h_stack *s);
+
+/* ---- context: replaces TQwen3Vulkan.NewContext / TDecoderContext ---- */
+
+/* lm.pas:354 (NewContext); max_positions <= the stack's max_positions */
+int q3h_context_create(q3h_stack *s, int max_positions, q3h_context **out);
+/* TQwenLm.Reset (lm.pas:374-378): the next row is at position 0 */
+int q3h_context_reset(q3h_context *c);
+/* TQwenLm.Length (lm.pas:136-138); negative on error */
+int q3h_context_length(const q3h_context *c);
+/* lm.pas:365 (fCtx.Free) */
+int q3h_context_destroy(q3h_context *c);
+/* no reference counterpart (long-context setups and tests): write the K/V of
+   positions [0, len) from host f32 [layers][kv_heads][len][head_dim] (rounded
+   to half floats when kv_f16) and set the length to len */
+int q3h_context_fill_kv(q3h_context *c, const float *k, const float *v, int len);
+/* no reference counterpart (tests): read the K/V cache of one layer for
+   positions [0, length) as f32 [kv_heads][length][head_dim] */
+int q3h_context_read_kv(q3h_context *c, int layer, float *k, float *v);
+
+/* ---- the forward: TQwenLm.Forward (lm.pas:391-408), i.e.
+   TQwen3Vulkan.ForwardEmbeds(ctx, x, rows, nil, false, fLast) (lm.pas:397)
+   followed by fCpu.Linear(fLast, 1, hidden, head, rows) (lm.pas:404-406),
+   with the head on the device. x [rows][hidden] host f32 at positions
+   length..length+rows-1; normed_last [hidden] (nullable) receives the
+   final-normed state of the last row; head: an index of q3h_stack_add_head,
+   or -1 for none; logits [head rows] (nullable). Blocks until the outputs
+   are in host memory. rows <= 0 does nothing (lm.pas:394-395). ---- */
+int q3h_forward_embeds(q3h_context *c, const float *x, int rows, int head,
+                       float *logits, float *normed_last);
+
+/* no reference counterpart (the reference is single-stream): one row per
+   context, n contexts of the same stack at their own positions;
+   x [n][hidden]; heads [n] (or NULL: no logits); logits [n][head rows of
+   heads[0]] (all heads of one call must have the same rows); normed [n][hidden]
+   (nullable). */
+int q3h_forward_embeds_batch(q3h_context *const *ctxs, int n, const float *x,
+                             const int *heads, float *logits, float *normed);
+
+/* ---- the frame step: a device-resident, greedy restatement of
+   TQwenTalker.NextFrame (talker.pas:640-681) with ChooseCode0 (talker.pas:
+   595-630), ChooseCode (talker.pas:632-638) and AddRow (talker.pas:423-429),
+   for n_streams independent sentences, replayed as one hipGraph per step ---- */
+typedef struct {
+  int32_t n_streams;          /* 1..64 */
+  int32_t talker_head;        /* head index in the talker stack */
+  int32_t cp_heads[15];       /* head indices in the code-predictor stack */
+  int32_t vocab, cp_vocab;    /* 3072, 2048 */
+  int32_t groups;             /* 16 */
+  int32_t eos;                /* codec_eos_token_id, -1: none */
+  float repetition_penalty;   /* 1.05 (talker.pas:215) */
+  int32_t max_frames;         /* frames per sentence (history capacity) */
+  int32_t max_positions;      /* talker positions per stream */
+  int32_t use_graph;          /* 1: capture the step once, replay it */
+} q3h_frame_config;
+
+/* TQwenTalker.Create's tables (talker.pas:300-311): codec_emb [vocab][hidden],
+   pred_emb[g] [cp_vocab][hidden] (g = 0..groups-2), tts_pad [hidden];
+   copied to the device */
+int q3h_frame_create(q3h_stack *talker, q3h_stack *cp, const q3h_frame_config *cfg,
+                     const float *codec_emb, const float *const *pred_emb,
+                     const float *tts_pad, q3h_frame **out);
+/* the talker part of TQwenTalker.Start (talker.pas:586-593): reset stream s,
+   prefill its rows, keep the logits and the last normed state; trailing
+   [trailing_rows][hidden] (talker.pas:578-580) follows the frames */
+int q3h_frame_start(q3h_frame *f, int stream, const float *prefill, int rows,
+                    const float *trailing, int trailing_rows);
+/* one NextFrame for every started stream: codes [n_streams][groups] (-1 for a
+   stream that has ended); alive [n_streams] (nullable) 1 while a stream runs,
+   0 once its code 0 was eos. */
+int q3h_frame_step(q3h_frame *f, int32_t *codes, int32_t *alive);
+/* the talker logits [vocab] and normed state [hidden] of stream s (nullable
+   outputs), as fLogits / fPastHidden after the last Start or step */
+int q3h_frame_state(q3h_frame *f, int stream, float *logits, float *past_hidden);
+int q3h_frame_destroy(q3h_frame *f);
+
+/* ---- helpers ---- */
+
+/* ggml quantize_row_q8_0_ref (InferQuantizeRowQ8_0Ref, lm.pas:265-267) on the
+   host: k % 32 == 0, y receives k/32 blocks of 34 bytes */
+int q3h_quantize_row_q8_0(const float *x, void *y, int64_t k);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,705 @@
+// q3h_api.hip - the C ABI of libq3h (include/q3h.h): device, stacks, contexts,
+// the forward and the batched forward. The frame step lives in q3h_frame.hip.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "q3h.h"
+#include "q3h_api_internal.h"
+
+using namespace q3h;
+
+namespace q3h {
+
+thread_local std::string g_last_error;
+
+void check_hip(hipError_t e, const char *what) {
+  if (e != hipSuccess)
+    throw Error{Q3H_E_HIP, std::string(what) + ": " + hipGetErrorString(e)};
+}
+
+void require(bool cond, int code, const std::string &msg) {
+  if (!cond) throw Error{code, msg};
+}
+
+void *dev_alloc(size_t bytes) {
+  void *p = nullptr;
+  if (bytes == 0) bytes = 256;
+  check_hip(hipMalloc(&p, bytes), "hipMalloc");
+  return p;
+}
+
+void dev_free(void *p) {
+  if (p) (void)hipFree(p);
+}
+
+// ---------------------------------------------------------------------------
+// work buffers of a forward over M rows
+
+void Work::ensure(const q3h_stack *s, int rows, int splits, int head_rows) {
+  const q3h_stack_config &c = s->cfg;
+  const int H = c.hidden, NQ = c.heads * c.head_dim, NKV = c.kv_heads * c.head_dim;
+  const int I = c.intermediate;
+  if (rows <= rows_cap && splits <= splits_cap && head_rows <= head_cap) return;
+  release();
+  rows_cap = rows > rows_cap ? rows : rows_cap;
+  splits_cap = splits > splits_cap ? splits : splits_cap;
+  head_cap = head_rows > head_cap ? head_rows : head_cap;
+  const size_t R = rows_cap;
+  h = (float *)dev_alloc(sizeof(float) * R * H);
+  qkv = (float *)dev_alloc(sizeof(float) * R * (NQ + 2 * NKV));
+  att = (float *)dev_alloc(sizeof(float) * R * NQ);
+  act = (float *)dev_alloc(sizeof(float) * R * I);
+  normed = (float *)dev_alloc(sizeof(float) * R * H);
+  logits = (float *)dev_alloc(sizeof(float) * R * (head_cap > 0 ? head_cap : 1));
+  rd = (RowDesc *)dev_alloc(sizeof(RowDesc) * R);
+  part = (float *)dev_alloc(sizeof(float) * R * c.heads * splits_cap * (c.head_dim + 2));
+  ctx_arr = (CtxDev **)dev_alloc(sizeof(CtxDev *) * R);
+}
+
+void Work::release() {
+  dev_free(h);
+  dev_free(qkv);
+  dev_free(att);
+  dev_free(act);
+  dev_free(normed);
+  dev_free(logits);
+  dev_free(rd);
+  dev_free(part);
+  dev_free(ctx_arr);
+  h = qkv = att = act = normed = logits = part = nullptr;
+  rd = nullptr;
+  ctx_arr = nullptr;
+}
+
+int attention_splits(int positions) {
+  const int n = (positions + kAttnChunk - 1) / kAttnChunk;
+  return n < 1 ? 1 : n;
+}
+
+// The layers of a stack over M rows of w.h, n contexts of R rows each (M =
+// n * R), their descriptors already in w.rd: the per-layer kernel sequence.
+void run_layers(const q3h_stack *s, Work &w, int M, int splits, hipStream_t st) {
+  const q3h_stack_config &c = s->cfg;
+  const int H = c.hidden, hd = c.head_dim, NQ = c.heads * hd, NKV = c.kv_heads * hd;
+  const int I = c.intermediate, ldq = NQ + 2 * NKV;
+  const bool q8 = c.dtype == Q3H_Q8_0, kv16 = c.kv_f16 != 0;
+  for (int l = 0; l < c.layers; l++) {
+    const Layer &L = s->layers[l];
+    GemvArgs a{};
+    // RMSNorm + fused q/k/v projection
+    a = make_gemv(L.qkv, w.h, H, M, L.in_norm, c.rms_eps, w.qkv, ldq);
+    launch_gemv(a, EPI_STORE, q8, st);
+    // QK-norm, RoPE, K/V append
+    launch_qk_rope_append(w.qkv, ldq, w.rd, M, l, c.heads, c.kv_heads, hd, L.q_norm, L.k_norm,
+                          c.rms_eps, s->rope_cs, kv16, st);
+    // GQA attention
+    launch_attention(w.qkv, ldq, w.rd, M, l, c.heads, c.kv_heads, hd, splits, kAttnChunk, w.att,
+                     w.part, kv16, st);
+    // o_proj + residual
+    a = make_gemv(L.o, w.att, NQ, M, nullptr, 0.f, w.h, H);
+    launch_gemv(a, EPI_ADD, q8, st);
+    // RMSNorm + gate/up + SwiGLU
+    a = make_gemv(L.gu, w.h, H, M, L.post_norm, c.rms_eps, w.act, I);
+    launch_gemv(a, EPI_SWIGLU, q8, st);
+    // down + residual
+    a = make_gemv(L.down, w.act, I, M, nullptr, 0.f, w.h, H);
+    launch_gemv(a, EPI_ADD, q8, st);
+  }
+}
+
+GemvArgs make_gemv(const Mat &W, const float *x, int ldx, int M, const float *norm_w,
+                   float eps, float *y, int ldy) {
+  GemvArgs a{};
+  a.wq = W.q;
+  a.wd = W.d;
+  a.wf = W.f;
+  a.N = W.N;
+  a.K = W.K;
+  a.x = x;
+  a.ldx = ldx;
+  a.M = M;
+  a.norm_w = norm_w;
+  a.eps = eps;
+  a.y = y;
+  a.ldy = ldy;
+  a.xn_out = nullptr;
+  return a;
+}
+
+}  // namespace q3h
+
+// ---------------------------------------------------------------------------
+// host Q8_0 quantizer (ggml quantize_row_q8_0_ref semantics)
+
+static uint16_t half_bits(float f) {
+  const _Float16 h = (_Float16)f;  // round to nearest even
+  uint16_t b;
+  std::memcpy(&b, &h, 2);
+  return b;
+}
+
+extern "C" int q3h_quantize_row_q8_0(const float *x, void *y, int64_t k) {
+  return guard([&] {
+    require(x && y && k >= 0 && k % 32 == 0, Q3H_E_ARG, "q3h_quantize_row_q8_0: k % 32 != 0");
+    uint8_t *out = (uint8_t *)y;
+    for (int64_t b = 0; b < k / 32; b++) {
+      const float *v = x + b * 32;
+      float amax = 0.f;
+      for (int j = 0; j < 32; j++) {
+        const float a = std::fabs(v[j]);
+        amax = amax > a ? amax : a;
+      }
+      const float d = amax / 127;
+      const float id = d != 0.f ? 1.0f / d : 0.f;
+      const uint16_t db = half_bits(d);
+      out[b * 34] = (uint8_t)(db & 0xff);
+      out[b * 34 + 1] = (uint8_t)(db >> 8);
+      for (int j = 0; j < 32; j++) out[b * 34 + 2 + j] = (uint8_t)(int8_t)std::round(v[j] * id);
+    }
+  });
+}
+
+// ---------------------------------------------------------------------------
+// device
+
+extern "C" const char *q3h_last_error(void) { return g_last_error.c_str(); }
+
+static bool is_gfx950(int ordinal) {
+  hipDeviceProp_t p;
+  if (hipGetDeviceProperties(&p, ordinal) != hipSuccess) return false;
+  return std::strncmp(p.gcnArchName, "gfx950", 6) == 0;
+}
+
+extern "C" int q3h_device_available(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  for (int i = 0; i < n; i++)
+    if (is_gfx950(i)) return 1;
+  return 0;
+}
+
+extern "C" int q3h_device_open(int ordinal, q3h_device **out) {
+  return guard([&] {
+    require(out != nullptr, Q3H_E_ARG, "q3h_device_open: out is NULL");
+    *out = nullptr;
+    int n = 0;
+    require(hipGetDeviceCount(&n) == hipSuccess && n > 0, Q3H_E_NODEV, "no HIP device");
+    require(ordinal >= 0 && ordinal < n, Q3H_E_NODEV, "q3h_device_open: no device " +
+                                                          std::to_string(ordinal));
+    require(is_gfx950(ordinal), Q3H_E_NODEV,
+            "q3h_device_open: device " + std::to_string(ordinal) + " is not gfx950");
+    check_hip(hipSetDevice(ordinal), "hipSetDevice");
+    check_hip(hipFree(nullptr), "hipFree(0)");
+    hipDeviceProp_t p;
+    check_hip(hipGetDeviceProperties(&p, ordinal), "hipGetDeviceProperties");
+    q3h_device *d = new q3h_device();
+    d->ordinal = ordinal;
+    d->name = p.name;
+    d->cus = p.multiProcessorCount;
+    *out = d;
+  });
+}
+
+extern "C" const char *q3h_device_name(const q3h_device *dev) {
+  return dev ? dev->name.c_str() : nullptr;
+}
+
+extern "C" int64_t q3h_device_bytes(const q3h_device *dev) { return dev ? dev->bytes.load() : 0; }
+
+extern "C" int q3h_device_close(q3h_device *dev) {
+  return guard([&] {
+    require(dev != nullptr, Q3H_E_ARG, "q3h_device_close: NULL device");
+    require(dev->stacks.load() == 0, Q3H_E_STATE,
+            "q3h_device_close: stacks are still alive on this device");
+    delete dev;
+  });
+}
+
+// ---------------------------------------------------------------------------
+// stack
+
+namespace {
+
+size_t src_row_bytes(int src_dtype, int K) {
+  return src_dtype == Q3H_Q8_0 ? (size_t)(K / 32) * 34 : (size_t)K * 4;
+}
+
+Mat alloc_mat(int N, int K, int dtype, int64_t &bytes) {
+  Mat m;
+  m.N = N;
+  m.K = K;
+  if (dtype == Q3H_Q8_0) {
+    m.q = (int8_t *)dev_alloc((size_t)N * K);
+    m.d = (_Float16 *)dev_alloc((size_t)N * (K / 32) * 2);
+    bytes += (int64_t)N * (K / 32) * 34;
+  } else {
+    m.f = (float *)dev_alloc((size_t)N * K * 4);
+    bytes += (int64_t)N * K * 4;
+  }
+  return m;
+}
+
+void free_mat(Mat &m) {
+  dev_free(m.q);
+  dev_free(m.d);
+  dev_free(m.f);
+  m = Mat();
+}
+
+// Upload rows x K of host matrix src (src_dtype) into rows r*stride+off of m.
+void upload_rows(Mat &m, int dtype, const void *src, int src_dtype, int rows, int K,
+                 int stride, int off, void *staging, hipStream_t st) {
+  require(src != nullptr, Q3H_E_ARG, "a weight matrix is NULL");
+  const size_t bytes = src_row_bytes(src_dtype, K) * rows;
+  check_hip(hipMemcpyAsync(staging, src, bytes, hipMemcpyHostToDevice, st), "upload");
+  if (dtype == Q3H_Q8_0) {
+    if (src_dtype == Q3H_F32)
+      launch_quantize_q8((const float *)staging, rows, K, m.q, m.d, stride, off, st);
+    else
+      launch_repack_q8((const uint8_t *)staging, rows, K, m.q, m.d, stride, off, st);
+  } else {
+    require(src_dtype == Q3H_F32, Q3H_E_ARG, "f32 stacks take f32 weights");
+    launch_copy_rows_f32((const float *)staging, rows, K, m.f, stride, off, st);
+  }
+  check_hip(hipGetLastError(), "conversion kernel");
+  // the staging buffer is reused by the next matrix
+  check_hip(hipStreamSynchronize(st), "upload sync");
+}
+
+float *upload_vec(const float *src, int n, const char *what) {
+  require(src != nullptr, Q3H_E_ARG, std::string("a norm vector is NULL: ") + what);
+  float *d = (float *)dev_alloc(sizeof(float) * n);
+  check_hip(hipMemcpy(d, src, sizeof(float) * n, hipMemcpyHostToDevice), "upload norm");
+  return d;
+}
+
+void destroy_stack(q3h_stack *s) {
+  for (auto &L : s->layers) {
+    free_mat(L.qkv);
+    free_mat(L.o);
+    free_mat(L.gu);
+    free_mat(L.down);
+    dev_free(L.in_norm);
+    dev_free(L.post_norm);
+    dev_free(L.q_norm);
+    dev_free(L.k_norm);
+  }
+  for (auto &h : s->heads) free_mat(h);
+  dev_free(s->final_norm);
+  dev_free(s->rope_cs);
+  if (s->stream) (void)hipStreamDestroy(s->stream);
+}
+
+}  // namespace
+
+extern "C" int q3h_stack_create(q3h_device *dev, const q3h_stack_config *cfg,
+                                const q3h_weights *w, q3h_stack **out) {
+  q3h_stack *s = nullptr;
+  int rc = guard([&] {
+    require(dev && cfg && w && out, Q3H_E_ARG, "q3h_stack_create: NULL argument");
+    *out = nullptr;
+    const q3h_stack_config &c = *cfg;
+    require(c.layers > 0 && c.hidden > 0 && c.heads > 0 && c.kv_heads > 0 && c.head_dim > 0 &&
+                c.intermediate > 0,
+            Q3H_E_ARG, "q3h_stack_create: non-positive dimension");
+    require(c.hidden % 32 == 0 && c.intermediate % 32 == 0 &&
+                (c.heads * c.head_dim) % 32 == 0,
+            Q3H_E_ARG, "q3h_stack_create: widths must be multiples of 32");
+    require(c.hidden % 16 == 0 && c.intermediate % 16 == 0, Q3H_E_ARG,
+            "q3h_stack_create: widths must be multiples of 16");
+    require(c.heads % c.kv_heads == 0 && c.heads / c.kv_heads <= kMaxGroup, Q3H_E_ARG,
+            "q3h_stack_create: heads / kv_heads must be an integer <= 4");
+    require(c.head_dim == 128, Q3H_E_ARG, "q3h_stack_create: head_dim must be 128");
+    require(c.dtype == Q3H_F32 || c.dtype == Q3H_Q8_0, Q3H_E_ARG,
+            "q3h_stack_create: dtype must be Q3H_F32 or Q3H_Q8_0");
+    require(w->src_dtype == Q3H_F32 || w->src_dtype == Q3H_Q8_0, Q3H_E_ARG,
+            "q3h_stack_create: src_dtype must be Q3H_F32 or Q3H_Q8_0");
+    require(c.dtype == Q3H_Q8_0 || w->src_dtype == Q3H_F32, Q3H_E_ARG,
+            "q3h_stack_create: an f32 stack takes f32 weights");
+    require(c.max_positions > 0, Q3H_E_ARG, "q3h_stack_create: max_positions <= 0");
+    require(c.act_q8 == 0 || c.dtype == Q3H_Q8_0, Q3H_E_ARG,
+            "q3h_stack_create: act_q8 needs Q8_0 weights");
+    require(w->layers != nullptr && w->final_norm != nullptr, Q3H_E_ARG,
+            "q3h_stack_create: NULL layers or final norm");
+    check_hip(hipSetDevice(dev->ordinal), "hipSetDevice");
+    s = new q3h_stack();
+    s->dev = dev;
+    s->cfg = c;
+    check_hip(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate");
+    const int H = c.hidden, hd = c.head_dim, NQ = c.heads * hd, NKV = c.kv_heads * hd;
+    const int I = c.intermediate;
+    const int maxK = std::max(std::max(H, NQ), I), maxN = std::max(std::max(NQ, I), H);
+    void *staging = dev_alloc(src_row_bytes(w->src_dtype, maxK) * maxN);
+    try {
+      s->layers.resize(c.layers);
+      for (int l = 0; l < c.layers; l++) {
+        const q3h_layer_weights &lw = w->layers[l];
+        Layer &L = s->layers[l];
+        L.qkv = alloc_mat(NQ + 2 * NKV, H, c.dtype, s->bytes);
+        L.o = alloc_mat(H, NQ, c.dtype, s->bytes);
+        L.gu = alloc_mat(2 * I, H, c.dtype, s->bytes);
+        L.down = alloc_mat(H, I, c.dtype, s->bytes);
+        upload_rows(L.qkv, c.dtype, lw.wq, w->src_dtype, NQ, H, 1, 0, staging, s->stream);
+        upload_rows(L.qkv, c.dtype, lw.wk, w->src_dtype, NKV, H, 1, NQ, staging, s->stream);
+        upload_rows(L.qkv, c.dtype, lw.wv, w->src_dtype, NKV, H, 1, NQ + NKV, staging,
+                    s->stream);
+        upload_rows(L.o, c.dtype, lw.wo, w->src_dtype, H, NQ, 1, 0, staging, s->stream);
+        upload_rows(L.gu, c.dtype, lw.wgate, w->src_dtype, I, H, 2, 0, staging, s->stream);
+        upload_rows(L.gu, c.dtype, lw.wup, w->src_dtype, I, H, 2, 1, staging, s->stream);
+        upload_rows(L.down, c.dtype, lw.wdown, w->src_dtype, H, I, 1, 0, staging, s->stream);
+        L.in_norm = upload_vec(lw.input_norm, H, "input_layernorm");
+        L.post_norm = upload_vec(lw.post_norm, H, "post_attention_layernorm");
+        L.q_norm = upload_vec(lw.q_norm, hd, "q_norm");
+        L.k_norm = upload_vec(lw.k_norm, hd, "k_norm");
+        s->bytes += (int64_t)(2 * H + 2 * hd) * 4;
+      }
+      s->final_norm = upload_vec(w->final_norm, H, "norm");
+      s->bytes += (int64_t)H * 4;
+      // RoPE table [max_positions][head_dim/2] of (cos, sin): the fp32 angle
+      // pos * inv_freq, its cosine and sine in double rounded to fp32
+      const int half = hd / 2;
+      std::vector<float> cs((size_t)c.max_positions * half * 2);
+      std::vector<float> inv_freq(half);
+      for (int i = 0; i < half; i++)
+        inv_freq[i] = (float)(1.0 / std::pow((double)c.rope_theta, (double)(2 * i) / (double)hd));
+      for (int p = 0; p < c.max_positions; p++)
+        for (int i = 0; i < half; i++) {
+          const float angle = (float)p * inv_freq[i];
+          cs[((size_t)p * half + i) * 2] = (float)std::cos((double)angle);
+          cs[((size_t)p * half + i) * 2 + 1] = (float)std::sin((double)angle);
+        }
+      s->rope_cs = (float *)dev_alloc(sizeof(float) * cs.size());
+      check_hip(hipMemcpy(s->rope_cs, cs.data(), sizeof(float) * cs.size(),
+                          hipMemcpyHostToDevice),
+                "upload rope");
+    } catch (...) {
+      dev_free(staging);
+      throw;
+    }
+    dev_free(staging);
+    dev->bytes += s->bytes;
+    dev->stacks++;
+    *out = s;
+  });
+  if (rc != 0 && s) {
+    destroy_stack(s);
+    delete s;
+  }
+  return rc;
+}
+
+extern "C" int q3h_stack_add_head(q3h_stack *s, const void *w, int rows, int src_dtype,
+                                  int *index) {
+  return guard([&] {
+    require(s && w && index && rows > 0, Q3H_E_ARG, "q3h_stack_add_head: invalid argument");
+    require(src_dtype == Q3H_F32 || src_dtype == Q3H_Q8_0, Q3H_E_ARG,
+            "q3h_stack_add_head: src_dtype must be Q3H_F32 or Q3H_Q8_0");
+    require(s->cfg.dtype == Q3H_Q8_0 || src_dtype == Q3H_F32, Q3H_E_ARG,
+            "q3h_stack_add_head: an f32 stack takes f32 heads");
+    check_hip(hipSetDevice(s->dev->ordinal), "hipSetDevice");
+    std::lock_guard<std::mutex> lock(s->mu);
+    const int H = s->cfg.hidden;
+    int64_t bytes = 0;
+    Mat m = alloc_mat(rows, H, s->cfg.dtype, bytes);
+    void *staging = dev_alloc(src_row_bytes(src_dtype, H) * rows);
+    try {
+      upload_rows(m, s->cfg.dtype, w, src_dtype, rows, H, 1, 0, staging, s->stream);
+    } catch (...) {
+      dev_free(staging);
+      free_mat(m);
+      throw;
+    }
+    dev_free(staging);
+    s->heads.push_back(m);
+    s->head_bytes += bytes;
+    s->dev->bytes += bytes;
+    *index = (int)s->heads.size() - 1;
+  });
+}
+
+extern "C" int64_t q3h_stack_bytes(const q3h_stack *s) { return s ? s->bytes : 0; }
+
+extern "C" int q3h_stack_destroy(q3h_stack *s) {
+  return guard([&] {
+    require(s != nullptr, Q3H_E_ARG, "q3h_stack_destroy: NULL stack");
+    require(s->contexts.load() == 0, Q3H_E_STATE,
+            "q3h_stack_destroy: contexts or frames still use this stack");
+    check_hip(hipSetDevice(s->dev->ordinal), "hipSetDevice");
+    s->dev->bytes -= s->bytes + s->head_bytes;
+    s->dev->stacks--;
+    destroy_stack(s);
+    delete s;
+  });
+}
+
+// ---------------------------------------------------------------------------
+// context
+
+namespace q3h {
+
+q3h_context *new_context(q3h_stack *s, int max_positions) {
+  const q3h_stack_config &c = s->cfg;
+  q3h_context *ctx = new q3h_context();
+  ctx->s = s;
+  ctx->max_pos = max_positions;
+  try {
+    check_hip(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "hipStreamCreate");
+    const size_t n = (size_t)c.layers * c.kv_heads * max_positions * c.head_dim;
+    const size_t esz = c.kv_f16 ? 2 : 4;
+    ctx->k = dev_alloc(n * esz);
+    ctx->v = dev_alloc(n * esz);
+    ctx->dev = (CtxDev *)dev_alloc(sizeof(CtxDev));
+    ctx->dev_arr = (CtxDev **)dev_alloc(sizeof(CtxDev *));
+    CtxDev h{ctx->k, ctx->v, max_positions, 0};
+    check_hip(hipMemcpy(ctx->dev, &h, sizeof(h), hipMemcpyHostToDevice), "ctx init");
+    check_hip(hipMemcpy(ctx->dev_arr, &ctx->dev, sizeof(CtxDev *), hipMemcpyHostToDevice),
+              "ctx init");
+  } catch (...) {
+    free_context(ctx);
+    throw;
+  }
+  s->contexts++;
+  return ctx;
+}
+
+void free_context(q3h_context *ctx) {
+  ctx->w.release();
+  dev_free(ctx->k);
+  dev_free(ctx->v);
+  dev_free(ctx->dev);
+  dev_free(ctx->dev_arr);
+  if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+void set_len(q3h_context *c, int len, hipStream_t st) {
+  check_hip(hipMemcpyAsync(&c->dev->len, &len, sizeof(int), hipMemcpyHostToDevice, st),
+            "set length");
+  check_hip(hipStreamSynchronize(st), "set length sync");
+  c->len = len;
+}
+
+}  // namespace q3h
+
+extern "C" int q3h_context_create(q3h_stack *s, int max_positions, q3h_context **out) {
+  return guard([&] {
+    require(s && out, Q3H_E_ARG, "q3h_context_create: NULL argument");
+    *out = nullptr;
+    require(max_positions > 0 && max_positions <= s->cfg.max_positions, Q3H_E_ARG,
+            "q3h_context_create: max_positions must be in [1, " +
+                std::to_string(s->cfg.max_positions) + "]");
+    check_hip(hipSetDevice(s->dev->ordinal), "hipSetDevice");
+    *out = new_context(s, max_positions);
+  });
+}
+
+extern "C" int q3h_context_reset(q3h_context *c) {
+  return guard([&] {
+    require(c != nullptr, Q3H_E_ARG, "q3h_context_reset: NULL context");
+    check_hip(hipSetDevice(c->s->dev->ordinal), "hipSetDevice");
+    set_len(c, 0, c->stream);
+  });
+}
+
+extern "C" int q3h_context_length(const q3h_context *c) {
+  if (!c) {
+    g_last_error = "q3h_context_length: NULL context";
+    return Q3H_E_ARG;
+  }
+  return c->len;
+}
+
+extern "C" int q3h_context_destroy(q3h_context *c) {
+  return guard([&] {
+    require(c != nullptr, Q3H_E_ARG, "q3h_context_destroy: NULL context");
+    check_hip(hipSetDevice(c->s->dev->ordinal), "hipSetDevice");
+    check_hip(hipStreamSynchronize(c->stream), "context sync");
+    c->s->contexts--;
+    free_context(c);
+  });
+}
+
+extern "C" int q3h_context_fill_kv(q3h_context *c, const float *k, const float *v, int len) {
+  return guard([&] {
+    require(c && k && v, Q3H_E_ARG, "q3h_context_fill_kv: NULL argument");
+    require(len >= 0 && len <= c->max_pos, Q3H_E_CAPACITY,
+            "q3h_context_fill_kv: length beyond the context");
+    const q3h_stack_config &cf = c->s->cfg;
+    check_hip(hipSetDevice(c->s->dev->ordinal), "hipSetDevice");
+    const size_t n = (size_t)cf.layers * cf.kv_heads * len * cf.head_dim;
+    if (n > 0) {
+      float *st = (float *)dev_alloc(n * sizeof(float));
+      try {
+        for (int which = 0; which < 2; which++) {
+          check_hip(hipMemcpyAsync(st, which ? v : k, n * sizeof(float), hipMemcpyHostToDevice,
+                                   c->stream),
+                    "fill kv upload");
+          launch_kv_fill(st, cf.layers, cf.kv_heads, len, cf.head_dim, which ? c->v : c->k,
+                         c->max_pos, cf.kv_f16 != 0, c->stream);
+          check_hip(hipGetLastError(), "kv fill kernel");
+          check_hip(hipStreamSynchronize(c->stream), "fill kv sync");
+        }
+      } catch (...) {
+        dev_free(st);
+        throw;
+      }
+      dev_free(st);
+    }
+    set_len(c, len, c->stream);
+  });
+}
+
+extern "C" int q3h_context_read_kv(q3h_context *c, int layer, float *k, float *v) {
+  return guard([&] {
+    require(c && k && v, Q3H_E_ARG, "q3h_context_read_kv: NULL argument");
+    const q3h_stack_config &cf = c->s->cfg;
+    require(layer >= 0 && layer < cf.layers, Q3H_E_ARG, "q3h_context_read_kv: bad layer");
+    check_hip(hipSetDevice(c->s->dev->ordinal), "hipSetDevice");
+    const size_t n = (size_t)cf.kv_heads * c->len * cf.head_dim;
+    if (n == 0) return;
+    float *st = (float *)dev_alloc(n * sizeof(float));
+    try {
+      for (int which = 0; which < 2; which++) {
+        launch_kv_read(which ? c->v : c->k, layer, cf.kv_heads, c->len, cf.head_dim, c->max_pos,
+                       cf.kv_f16 != 0, st, c->stream);
+        check_hip(hipGetLastError(), "kv read kernel");
+        check_hip(hipMemcpyAsync(which ? v : k, st, n * sizeof(float), hipMemcpyDeviceToHost,
+                                 c->stream),
+                  "kv read download");
+        check_hip(hipStreamSynchronize(c->stream), "kv read sync");
+      }
+    } catch (...) {
+      dev_free(st);
+      throw;
+    }
+    dev_free(st);
+  });
+}
+
+// ---------------------------------------------------------------------------
+// forward
+
+extern "C" int q3h_forward_embeds(q3h_context *c, const float *x, int rows, int head,
+                                  float *logits, float *normed_last) {
+  return guard([&] {
+    require(c != nullptr, Q3H_E_ARG, "q3h_forward_embeds: NULL context");
+    if (rows <= 0) return;
+    require(x != nullptr, Q3H_E_ARG, "q3h_forward_embeds: x is NULL");
+    q3h_stack *s = c->s;
+    const q3h_stack_config &cf = s->cfg;
+    require(head >= -1 && head < (int)s->heads.size(), Q3H_E_ARG,
+            "q3h_forward_embeds: no head " + std::to_string(head));
+    require(c->len + rows <= c->max_pos, Q3H_E_CAPACITY,
+            "q3h_forward_embeds: " + std::to_string(c->len) + " + " + std::to_string(rows) +
+                " positions exceed the context's " + std::to_string(c->max_pos));
+    check_hip(hipSetDevice(s->dev->ordinal), "hipSetDevice");
+    const int H = cf.hidden;
+    const int head_rows = head >= 0 ? s->heads[head].N : 0;
+    const int splits = attention_splits(c->len + rows);
+    Work &w = c->w;
+    w.ensure(s, rows, splits, head_rows);
+    hipStream_t st = c->stream;
+    check_hip(hipMemcpyAsync(w.h, x, sizeof(float) * rows * H, hipMemcpyHostToDevice, st),
+              "upload x");
+    launch_prep(c->dev_arr, nullptr, 1, rows, w.rd, st);
+    run_layers(s, w, rows, splits, st);
+    launch_rmsnorm_rows(w.h + (size_t)(rows - 1) * H, H, 1, H, s->final_norm, cf.rms_eps,
+                        w.normed, H, st);
+    if (head >= 0) {
+      GemvArgs a = make_gemv(s->heads[head], w.normed, H, 1, nullptr, 0.f, w.logits, head_rows);
+      launch_gemv(a, EPI_STORE, cf.dtype == Q3H_Q8_0, st);
+    }
+    launch_advance(c->dev_arr, nullptr, 1, rows, st);
+    check_hip(hipGetLastError(), "forward kernels");
+    if (normed_last)
+      check_hip(hipMemcpyAsync(normed_last, w.normed, sizeof(float) * H, hipMemcpyDeviceToHost,
+                               st),
+                "download state");
+    if (logits && head >= 0)
+      check_hip(hipMemcpyAsync(logits, w.logits, sizeof(float) * head_rows,
+                               hipMemcpyDeviceToHost, st),
+                "download logits");
+    check_hip(hipStreamSynchronize(st), "forward sync");
+    c->len += rows;
+  });
+}
+
+extern "C" int q3h_forward_embeds_batch(q3h_context *const *ctxs, int n, const float *x,
+                                        const int *heads, float *logits, float *normed) {
+  return guard([&] {
+    require(ctxs && n > 0 && x, Q3H_E_ARG, "q3h_forward_embeds_batch: invalid argument");
+    q3h_context *c0 = ctxs[0];
+    require(c0 != nullptr, Q3H_E_ARG, "q3h_forward_embeds_batch: NULL context");
+    q3h_stack *s = c0->s;
+    const q3h_stack_config &cf = s->cfg;
+    int maxlen = 0;
+    for (int i = 0; i < n; i++) {
+      require(ctxs[i] && ctxs[i]->s == s, Q3H_E_ARG,
+              "q3h_forward_embeds_batch: contexts of different stacks");
+      for (int j = 0; j < i; j++)
+        require(ctxs[j] != ctxs[i], Q3H_E_ARG, "q3h_forward_embeds_batch: repeated context");
+      require(ctxs[i]->len + 1 <= ctxs[i]->max_pos, Q3H_E_CAPACITY,
+              "q3h_forward_embeds_batch: a context is full");
+      maxlen = std::max(maxlen, ctxs[i]->len + 1);
+    }
+    int head_rows = 0;
+    if (heads) {
+      for (int i = 0; i < n; i++)
+        require(heads[i] >= 0 && heads[i] < (int)s->heads.size(), Q3H_E_ARG,
+                "q3h_forward_embeds_batch: bad head index");
+      head_rows = s->heads[heads[0]].N;
+      for (int i = 0; i < n; i++)
+        require(s->heads[heads[i]].N == head_rows, Q3H_E_ARG,
+                "q3h_forward_embeds_batch: heads of different sizes");
+    }
+    check_hip(hipSetDevice(s->dev->ordinal), "hipSetDevice");
+    for (int i = 1; i < n; i++) check_hip(hipStreamSynchronize(ctxs[i]->stream), "batch sync");
+    const int H = cf.hidden;
+    const int splits = attention_splits(maxlen);
+    Work &w = c0->w;
+    w.ensure(s, n, splits, head_rows);
+    hipStream_t st = c0->stream;
+    std::vector<CtxDev *> arr(n);
+    for (int i = 0; i < n; i++) arr[i] = ctxs[i]->dev;
+    check_hip(hipMemcpyAsync(w.ctx_arr, arr.data(), sizeof(CtxDev *) * n, hipMemcpyHostToDevice,
+                             st),
+              "upload contexts");
+    check_hip(hipMemcpyAsync(w.h, x, sizeof(float) * n * H, hipMemcpyHostToDevice, st),
+              "upload x");
+    launch_prep(w.ctx_arr, nullptr, n, 1, w.rd, st);
+    run_layers(s, w, n, splits, st);
+    launch_rmsnorm_rows(w.h, H, n, H, s->final_norm, cf.rms_eps, w.normed, H, st);
+    if (heads) {
+      bool same = true;
+      for (int i = 1; i < n; i++) same = same && heads[i] == heads[0];
+      if (same) {
+        GemvArgs a = make_gemv(s->heads[heads[0]], w.normed, H, n, nullptr, 0.f, w.logits,
+                               head_rows);
+        launch_gemv(a, EPI_STORE, cf.dtype == Q3H_Q8_0, st);
+      } else {
+        for (int i = 0; i < n; i++) {
+          GemvArgs a = make_gemv(s->heads[heads[i]], w.normed + (size_t)i * H, H, 1, nullptr,
+                                 0.f, w.logits + (size_t)i * head_rows, head_rows);
+          launch_gemv(a, EPI_STORE, cf.dtype == Q3H_Q8_0, st);
+        }
+      }
+    }
+    launch_advance(w.ctx_arr, nullptr, n, 1, st);
+    check_hip(hipGetLastError(), "batch kernels");
+    if (normed)
+      check_hip(hipMemcpyAsync(normed, w.normed, sizeof(float) * n * H, hipMemcpyDeviceToHost,
+                               st),
+                "download states");
+    if (logits && heads)
+      check_hip(hipMemcpyAsync(logits, w.logits, sizeof(float) * n * head_rows,
+                               hipMemcpyDeviceToHost, st),
+                "download logits");
+    check_hip(hipStreamSynchronize(st), "batch sync");
+    for (int i = 0; i < n; i++) ctxs[i]->len += 1;
+  });
+}

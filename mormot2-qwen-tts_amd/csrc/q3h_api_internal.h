@@ -1,0 +1,115 @@
+// q3h_api_internal.h - host-side objects behind the opaque handles of q3h.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "q3h.h"
+#include "q3h_internal.h"
+
+struct q3h_device {
+  int ordinal = 0;
+  int cus = 0;
+  std::string name;
+  std::atomic<int64_t> bytes{0};
+  std::atomic<int> stacks{0};
+};
+
+namespace q3h {
+
+constexpr int kAttnChunk = 256;  // positions per attention split (k_attention)
+constexpr int kMaxGroup = 4;     // q heads per kv head
+
+struct Error {
+  int code;
+  std::string msg;
+};
+
+extern thread_local std::string g_last_error;
+
+void check_hip(hipError_t e, const char *what);
+void require(bool cond, int code, const std::string &msg);
+void *dev_alloc(size_t bytes);
+void dev_free(void *p);
+
+template <class F>
+int guard(F &&f) {
+  try {
+    f();
+    g_last_error.clear();
+    return Q3H_OK;
+  } catch (const Error &e) {
+    g_last_error = e.msg;
+    return e.code;
+  } catch (const std::exception &e) {
+    g_last_error = e.what();
+    return Q3H_E_HIP;
+  }
+}
+
+struct Layer {
+  Mat qkv;   // [q; k; v] rows
+  Mat o;     // [hidden][heads * head_dim]
+  Mat gu;    // gate and up interleaved: row 2j = gate j, row 2j + 1 = up j
+  Mat down;  // [hidden][intermediate]
+  float *in_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+};
+
+struct q3h_stack_fwd;
+
+// device buffers of one forward over up to rows_cap rows
+struct Work {
+  int rows_cap = 0, splits_cap = 0, head_cap = 0;
+  float *h = nullptr;       // residual stream [rows][hidden]
+  float *qkv = nullptr;     // [rows][q + k + v]
+  float *att = nullptr;     // [rows][heads * head_dim]
+  float *act = nullptr;     // [rows][intermediate]
+  float *normed = nullptr;  // [rows][hidden]
+  float *logits = nullptr;  // [rows][head rows]
+  RowDesc *rd = nullptr;    // [rows]
+  float *part = nullptr;    // attention partials [rows][heads][splits][head_dim + 2]
+  CtxDev **ctx_arr = nullptr;
+  void ensure(const struct ::q3h_stack *s, int rows, int splits, int head_rows);
+  void release();
+};
+
+int attention_splits(int positions);
+GemvArgs make_gemv(const Mat &W, const float *x, int ldx, int M, const float *norm_w, float eps,
+                   float *y, int ldy);
+void run_layers(const struct ::q3h_stack *s, Work &w, int M, int splits, hipStream_t st);
+
+}  // namespace q3h
+
+struct q3h_stack {
+  q3h_device *dev = nullptr;
+  q3h_stack_config cfg{};
+  std::vector<q3h::Layer> layers;
+  float *final_norm = nullptr;
+  float *rope_cs = nullptr;  // [max_positions][head_dim / 2] (cos, sin)
+  std::vector<q3h::Mat> heads;
+  int64_t bytes = 0, head_bytes = 0;
+  std::atomic<int> contexts{0};
+  std::mutex mu;
+  hipStream_t stream = nullptr;  // uploads
+};
+
+struct q3h_context {
+  q3h_stack *s = nullptr;
+  int max_pos = 0;
+  int len = 0;  // host mirror of dev->len
+  void *k = nullptr, *v = nullptr;
+  q3h::CtxDev *dev = nullptr;
+  q3h::CtxDev **dev_arr = nullptr;  // {dev}
+  hipStream_t stream = nullptr;
+  q3h::Work w;
+};
+
+namespace q3h {
+q3h_context *new_context(q3h_stack *s, int max_positions);
+void free_context(q3h_context *ctx);
+void set_len(q3h_context *c, int len, hipStream_t st);
+}  // namespace q3h

@@ -1,0 +1,499 @@
+// q3h_frame.hip - the frame step of q3h.h: a device-resident, greedy
+// restatement of TQwenTalker.NextFrame (mormot.ai.tts.qwen.talker.pas:640-681)
+// for n independent streams. Per step: code 0 from the talker logits with the
+// logits processors of ChooseCode0 (talker.pas:595-630), 15 code-predictor
+// forwards (2 rows, then 14 x 1 row) each with its head and argmax
+// (ChooseCode, talker.pas:632-638), the sum of the 16 embeddings plus the
+// trailing text row (AddRow, talker.pas:423-429, 668-675), one talker forward
+// with its head. No host round trip inside a step; the step is captured once
+// in a hipGraph and replayed (re-captured only when the talker attention
+// needs more position splits).
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <vector>
+
+#include "q3h.h"
+#include "q3h_api_internal.h"
+
+namespace q3h {
+
+// the device view of a frame (kernel argument, by value)
+struct FrameDev {
+  int n, H, vocab, cp_vocab, groups, eos, max_trailing;
+  float penalty;
+  float *logits;          // [n][vocab] talker logits
+  float *past;            // [n][H] normed talker state
+  int *codes;             // [n][groups]
+  uint8_t *seen;          // [n][vocab]: codes already emitted (repetition penalty)
+  int *nframes;           // [n]
+  int *step;              // [n]
+  int *alive;             // [n]
+  float *trailing;        // [n][max_trailing][H]
+  int *trailing_rows;     // [n]
+  const float *codec_emb; // [vocab][H]
+  const float *pred_emb;  // [groups - 1][cp_vocab][H]
+  const float *tts_pad;   // [H]
+  float *cp_h;            // code-predictor input rows [n][2][H] (then [n][H])
+  float *t_h;             // talker input rows [n][H]
+  const float *cp_logits; // [n][cp_vocab]
+  CtxDev *const *cp_ctx;  // [n]
+};
+
+constexpr int kArgBlock = 1024;
+
+// (value, index) maximum with the first index winning ties
+__device__ __forceinline__ void argmax_merge(float &v, int &i, float v2, int i2) {
+  if (v2 > v || (v2 == v && i2 < i)) {
+    v = v2;
+    i = i2;
+  }
+}
+
+__device__ int block_argmax(float v, int i) {
+  __shared__ float sv[kArgBlock / 64];
+  __shared__ int si[kArgBlock / 64];
+  __shared__ int res;
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float v2 = __shfl_xor(v, off, 64);
+    const int i2 = __shfl_xor(i, off, 64);
+    argmax_merge(v, i, v2, i2);
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    sv[wave] = v;
+    si[wave] = i;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float bv = sv[0];
+    int bi = si[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++) argmax_merge(bv, bi, sv[w], si[w]);
+    res = bi;
+  }
+  __syncthreads();
+  return res;
+}
+
+// ChooseCode0 + the code-predictor input [past state; codec_emb[code]] and
+// the reset of the code-predictor context. One block per stream.
+__global__ __launch_bounds__(kArgBlock) void k_choose_code0(FrameDev f) {
+  const int s = blockIdx.x, tid = threadIdx.x;
+  if (!f.alive[s]) return;
+  const float *lg = f.logits + (size_t)s * f.vocab;
+  const uint8_t *seen = f.seen + (size_t)s * f.vocab;
+  const int nf = f.nframes[s];
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = tid; i < f.vocab; i += kArgBlock) {
+    float v = lg[i];
+    // 2048..3071 forbidden but eos; eos forbidden before 2 frames
+    if (i >= f.vocab - 1024 && i != f.eos) v = -INFINITY;
+    if (i == f.eos && nf < 2) v = -INFINITY;
+    // repetition penalty, once per code already returned (not when forbidden)
+    if (seen[i] && v != -INFINITY && f.penalty != 1.0f)
+      v = v > 0.f ? __fdiv_rn(v, f.penalty) : v * f.penalty;
+    argmax_merge(bv, bi, v, i);
+  }
+  const int code = block_argmax(bv, bi);
+  int *codes = f.codes + (size_t)s * f.groups;
+  if (code == f.eos) {
+    if (tid < f.groups) codes[tid] = -1;
+    __syncthreads();
+    if (tid == 0) f.alive[s] = 0;
+    return;
+  }
+  if (tid == 0) {
+    codes[0] = code;
+    f.seen[(size_t)s * f.vocab + code] = 1;
+    f.nframes[s] = nf + 1;
+    f.cp_ctx[s]->len = 0;
+  }
+  float *x = f.cp_h + (size_t)s * 2 * f.H;
+  const float *past = f.past + (size_t)s * f.H;
+  const float *emb = f.codec_emb + (size_t)code * f.H;
+  for (int c = tid; c < f.H; c += kArgBlock) {
+    x[c] = past[c];
+    x[f.H + c] = emb[c];
+  }
+}
+
+// ChooseCode for group g + 1 (argmax of the head-g logits), then the input row
+// of the next code-predictor forward: pred_emb[g][code]. One block per stream.
+__global__ __launch_bounds__(kArgBlock) void k_cp_argmax(FrameDev f, int g) {
+  const int s = blockIdx.x, tid = threadIdx.x;
+  if (!f.alive[s]) return;
+  const float *lg = f.cp_logits + (size_t)s * f.cp_vocab;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = tid; i < f.cp_vocab; i += kArgBlock) argmax_merge(bv, bi, lg[i], i);
+  const int code = block_argmax(bv, bi);
+  if (tid == 0) f.codes[(size_t)s * f.groups + g + 1] = code;
+  if (g + 1 < f.groups - 1) {
+    const float *emb = f.pred_emb + ((size_t)g * f.cp_vocab + code) * f.H;
+    float *x = f.cp_h + (size_t)s * f.H;
+    for (int c = tid; c < f.H; c += kArgBlock) x[c] = emb[c];
+  }
+}
+
+// the next talker input: codec_emb[code 0] + sum_g pred_emb[g-1][code g] +
+// (trailing[step] or tts_pad), summed in that order.
+__global__ void k_talker_input(FrameDev f) {
+  const int s = blockIdx.y;
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= f.H || !f.alive[s]) return;
+  const int *codes = f.codes + (size_t)s * f.groups;
+  float x = f.codec_emb[(size_t)codes[0] * f.H + c];
+  for (int g = 1; g < f.groups; g++)
+    x = x + f.pred_emb[((size_t)(g - 1) * f.cp_vocab + codes[g]) * f.H + c];
+  const int st = f.step[s];
+  if (st < f.trailing_rows[s])
+    x = x + f.trailing[((size_t)s * f.max_trailing + st) * f.H + c];
+  else
+    x = x + f.tts_pad[c];
+  f.t_h[(size_t)s * f.H + c] = x;
+}
+
+__global__ void k_frame_end(FrameDev f) {
+  const int s = blockIdx.x * blockDim.x + threadIdx.x;
+  if (s < f.n && f.alive[s]) f.step[s] += 1;
+}
+
+}  // namespace q3h
+
+using namespace q3h;
+
+struct q3h_frame {
+  q3h_stack *talker = nullptr, *cp = nullptr;
+  q3h_frame_config cfg{};
+  int H = 0;
+  std::vector<q3h_context *> tctx, cctx;
+  CtxDev **t_arr = nullptr, **c_arr = nullptr;
+  Work tw, cw;
+  FrameDev fd{};
+  float *codec_emb = nullptr, *pred_emb = nullptr, *tts_pad = nullptr;
+  std::vector<int> started, host_len, max_trailing_rows;
+  hipStream_t stream = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  int graph_splits = 0;
+  int32_t *pinned = nullptr;  // [n][groups] codes + [n] alive
+  std::vector<void *> allocs;
+};
+
+namespace {
+
+void frame_release(q3h_frame *f) {
+  if (f->exec) (void)hipGraphExecDestroy(f->exec);
+  if (f->graph) (void)hipGraphDestroy(f->graph);
+  for (auto *c : f->tctx) {
+    c->s->contexts--;
+    free_context(c);
+  }
+  for (auto *c : f->cctx) {
+    c->s->contexts--;
+    free_context(c);
+  }
+  f->tw.release();
+  f->cw.release();
+  for (void *p : f->allocs) dev_free(p);
+  if (f->pinned) (void)hipHostFree(f->pinned);
+  if (f->stream) (void)hipStreamDestroy(f->stream);
+}
+
+template <class T>
+T *falloc(q3h_frame *f, size_t n) {
+  T *p = (T *)dev_alloc(sizeof(T) * (n ? n : 1));
+  f->allocs.push_back(p);
+  return p;
+}
+
+// The step's kernel sequence on stream st (captured into the graph).
+void enqueue_step(q3h_frame *f, int splits, hipStream_t st) {
+  const q3h_frame_config &c = f->cfg;
+  const int n = c.n_streams, H = f->H;
+  q3h_stack *cp = f->cp, *tk = f->talker;
+  const bool cq8 = cp->cfg.dtype == Q3H_Q8_0, tq8 = tk->cfg.dtype == Q3H_Q8_0;
+  FrameDev fd = f->fd;
+  hipLaunchKernelGGL(k_choose_code0, dim3(n), dim3(kArgBlock), 0, st, fd);
+  // code predictor: 2 rows per stream, then one row per group
+  for (int g = 0; g < c.groups - 1; g++) {
+    const int R = g == 0 ? 2 : 1;
+    launch_prep(f->c_arr, fd.alive, n, R, f->cw.rd, st);
+    run_layers(cp, f->cw, n * R, 1, st);
+    launch_rmsnorm_rows(f->cw.h + (size_t)(R - 1) * H, R * H, n, H, cp->final_norm,
+                        cp->cfg.rms_eps, f->cw.normed, H, st);
+    const Mat &head = cp->heads[c.cp_heads[g]];
+    GemvArgs a = make_gemv(head, f->cw.normed, H, n, nullptr, 0.f, f->cw.logits, c.cp_vocab);
+    launch_gemv(a, EPI_STORE, cq8, st);
+    launch_advance(f->c_arr, fd.alive, n, R, st);
+    hipLaunchKernelGGL(k_cp_argmax, dim3(n), dim3(kArgBlock), 0, st, fd, g);
+  }
+  // the talker
+  hipLaunchKernelGGL(k_talker_input, dim3((H + 255) / 256, n), dim3(256), 0, st, fd);
+  launch_prep(f->t_arr, fd.alive, n, 1, f->tw.rd, st);
+  run_layers(tk, f->tw, n, splits, st);
+  launch_rmsnorm_rows(f->tw.h, H, n, H, tk->final_norm, tk->cfg.rms_eps, fd.past, H, st);
+  const Mat &th = tk->heads[c.talker_head];
+  GemvArgs a = make_gemv(th, fd.past, H, n, nullptr, 0.f, fd.logits, c.vocab);
+  launch_gemv(a, EPI_STORE, tq8, st);
+  launch_advance(f->t_arr, fd.alive, n, 1, st);
+  hipLaunchKernelGGL(k_frame_end, dim3((n + 63) / 64), dim3(64), 0, st, fd);
+}
+
+}  // namespace
+
+extern "C" int q3h_frame_create(q3h_stack *talker, q3h_stack *cp, const q3h_frame_config *cfg,
+                                const float *codec_emb, const float *const *pred_emb,
+                                const float *tts_pad, q3h_frame **out) {
+  q3h_frame *f = nullptr;
+  int rc = guard([&] {
+    require(talker && cp && cfg && codec_emb && pred_emb && tts_pad && out, Q3H_E_ARG,
+            "q3h_frame_create: NULL argument");
+    *out = nullptr;
+    const q3h_frame_config &c = *cfg;
+    require(talker->dev == cp->dev, Q3H_E_ARG, "q3h_frame_create: stacks on different devices");
+    require(talker->cfg.hidden == cp->cfg.hidden, Q3H_E_ARG,
+            "q3h_frame_create: talker and code predictor widths differ");
+    require(c.n_streams >= 1 && c.n_streams <= 64, Q3H_E_ARG,
+            "q3h_frame_create: n_streams must be in [1, 64]");
+    require(c.groups >= 2 && c.groups <= 16, Q3H_E_ARG, "q3h_frame_create: groups in [2, 16]");
+    require(c.vocab > 1024 && c.cp_vocab > 0, Q3H_E_ARG, "q3h_frame_create: bad vocab sizes");
+    require(c.eos < c.vocab, Q3H_E_ARG, "q3h_frame_create: eos beyond the vocab");
+    require(c.max_frames > 0, Q3H_E_ARG, "q3h_frame_create: max_frames <= 0");
+    require(c.talker_head >= 0 && c.talker_head < (int)talker->heads.size() &&
+                talker->heads[c.talker_head].N == c.vocab,
+            Q3H_E_ARG, "q3h_frame_create: bad talker head");
+    for (int g = 0; g < c.groups - 1; g++) {
+      require(pred_emb[g] != nullptr, Q3H_E_ARG, "q3h_frame_create: NULL pred_emb");
+      require(c.cp_heads[g] >= 0 && c.cp_heads[g] < (int)cp->heads.size() &&
+                  cp->heads[c.cp_heads[g]].N == c.cp_vocab,
+              Q3H_E_ARG, "q3h_frame_create: bad code-predictor head");
+    }
+    require(c.max_positions > 0 && c.max_positions <= talker->cfg.max_positions, Q3H_E_ARG,
+            "q3h_frame_create: max_positions beyond the talker stack");
+    require(cp->cfg.max_positions >= c.groups, Q3H_E_ARG,
+            "q3h_frame_create: the code predictor needs groups positions");
+    check_hip(hipSetDevice(talker->dev->ordinal), "hipSetDevice");
+    f = new q3h_frame();
+    f->talker = talker;
+    f->cp = cp;
+    f->cfg = c;
+    const int n = c.n_streams, H = talker->cfg.hidden;
+    f->H = H;
+    check_hip(hipStreamCreateWithFlags(&f->stream, hipStreamNonBlocking), "hipStreamCreate");
+    for (int s = 0; s < n; s++) {
+      f->tctx.push_back(new_context(talker, c.max_positions));
+      f->cctx.push_back(new_context(cp, c.groups));
+    }
+    f->t_arr = falloc<CtxDev *>(f, n);
+    f->c_arr = falloc<CtxDev *>(f, n);
+    std::vector<CtxDev *> ta(n), ca(n);
+    for (int s = 0; s < n; s++) {
+      ta[s] = f->tctx[s]->dev;
+      ca[s] = f->cctx[s]->dev;
+    }
+    check_hip(hipMemcpy(f->t_arr, ta.data(), sizeof(CtxDev *) * n, hipMemcpyHostToDevice),
+              "frame init");
+    check_hip(hipMemcpy(f->c_arr, ca.data(), sizeof(CtxDev *) * n, hipMemcpyHostToDevice),
+              "frame init");
+    f->tw.ensure(talker, n, attention_splits(c.max_positions), c.vocab);
+    f->cw.ensure(cp, 2 * n, 1, c.cp_vocab);
+    f->codec_emb = falloc<float>(f, (size_t)c.vocab * H);
+    check_hip(hipMemcpy(f->codec_emb, codec_emb, sizeof(float) * c.vocab * H,
+                        hipMemcpyHostToDevice),
+              "upload codec_emb");
+    f->pred_emb = falloc<float>(f, (size_t)(c.groups - 1) * c.cp_vocab * H);
+    for (int g = 0; g < c.groups - 1; g++)
+      check_hip(hipMemcpy(f->pred_emb + (size_t)g * c.cp_vocab * H, pred_emb[g],
+                          sizeof(float) * c.cp_vocab * H, hipMemcpyHostToDevice),
+                "upload pred_emb");
+    f->tts_pad = falloc<float>(f, H);
+    check_hip(hipMemcpy(f->tts_pad, tts_pad, sizeof(float) * H, hipMemcpyHostToDevice),
+              "upload tts_pad");
+    FrameDev &d = f->fd;
+    d.n = n;
+    d.H = H;
+    d.vocab = c.vocab;
+    d.cp_vocab = c.cp_vocab;
+    d.groups = c.groups;
+    d.eos = c.eos;
+    d.penalty = c.repetition_penalty;
+    d.max_trailing = c.max_frames;
+    d.logits = falloc<float>(f, (size_t)n * c.vocab);
+    d.past = falloc<float>(f, (size_t)n * H);
+    d.codes = falloc<int>(f, (size_t)n * c.groups);
+    d.seen = falloc<uint8_t>(f, (size_t)n * c.vocab);
+    d.nframes = falloc<int>(f, n);
+    d.step = falloc<int>(f, n);
+    d.alive = falloc<int>(f, n);
+    d.trailing = falloc<float>(f, (size_t)n * c.max_frames * H);
+    d.trailing_rows = falloc<int>(f, n);
+    d.codec_emb = f->codec_emb;
+    d.pred_emb = f->pred_emb;
+    d.tts_pad = f->tts_pad;
+    d.cp_h = f->cw.h;
+    d.t_h = f->tw.h;
+    d.cp_logits = f->cw.logits;
+    d.cp_ctx = f->c_arr;
+    check_hip(hipMemset(d.alive, 0, sizeof(int) * n), "frame init");
+    check_hip(hipMemset(d.codes, 0xff, sizeof(int) * n * c.groups), "frame init");
+    check_hip(hipHostMalloc((void **)&f->pinned, sizeof(int32_t) * n * (c.groups + 1)),
+              "hipHostMalloc");
+    f->started.assign(n, 0);
+    f->host_len.assign(n, 0);
+    *out = f;
+  });
+  if (rc != 0 && f) {
+    frame_release(f);
+    delete f;
+  }
+  return rc;
+}
+
+extern "C" int q3h_frame_start(q3h_frame *f, int stream, const float *prefill, int rows,
+                               const float *trailing, int trailing_rows) {
+  return guard([&] {
+    require(f != nullptr, Q3H_E_ARG, "q3h_frame_start: NULL frame");
+    const q3h_frame_config &c = f->cfg;
+    require(stream >= 0 && stream < c.n_streams, Q3H_E_ARG, "q3h_frame_start: bad stream");
+    require(prefill != nullptr && rows > 0, Q3H_E_ARG, "q3h_frame_start: empty prefill");
+    require(trailing_rows >= 0 && trailing_rows <= c.max_frames, Q3H_E_ARG,
+            "q3h_frame_start: more trailing rows than max_frames");
+    require(trailing_rows == 0 || trailing != nullptr, Q3H_E_ARG,
+            "q3h_frame_start: trailing is NULL");
+    require(rows <= c.max_positions, Q3H_E_CAPACITY, "q3h_frame_start: prefill too long");
+    check_hip(hipSetDevice(f->talker->dev->ordinal), "hipSetDevice");
+    check_hip(hipStreamSynchronize(f->stream), "frame sync");
+    q3h_context *tc = f->tctx[stream];
+    set_len(tc, 0, tc->stream);
+    // the prefill through the single-context path, outputs kept on the device
+    const int H = f->H;
+    q3h_stack *s = f->talker;
+    const int splits = attention_splits(rows);
+    Work &w = tc->w;
+    w.ensure(s, rows, splits, c.vocab);
+    hipStream_t st = tc->stream;
+    FrameDev &d = f->fd;
+    check_hip(hipMemcpyAsync(w.h, prefill, sizeof(float) * rows * H, hipMemcpyHostToDevice, st),
+              "upload prefill");
+    launch_prep(tc->dev_arr, nullptr, 1, rows, w.rd, st);
+    run_layers(s, w, rows, splits, st);
+    float *past = d.past + (size_t)stream * H;
+    launch_rmsnorm_rows(w.h + (size_t)(rows - 1) * H, H, 1, H, s->final_norm, s->cfg.rms_eps,
+                        past, H, st);
+    GemvArgs a = make_gemv(s->heads[c.talker_head], past, H, 1, nullptr, 0.f,
+                           d.logits + (size_t)stream * c.vocab, c.vocab);
+    launch_gemv(a, EPI_STORE, s->cfg.dtype == Q3H_Q8_0, st);
+    launch_advance(tc->dev_arr, nullptr, 1, rows, st);
+    check_hip(hipGetLastError(), "prefill kernels");
+    if (trailing_rows > 0)
+      check_hip(hipMemcpyAsync(d.trailing + (size_t)stream * c.max_frames * H, trailing,
+                               sizeof(float) * trailing_rows * H, hipMemcpyHostToDevice, st),
+                "upload trailing");
+    const int zero = 0, one = 1;
+    check_hip(hipMemsetAsync(d.seen + (size_t)stream * c.vocab, 0, c.vocab, st), "reset seen");
+    check_hip(hipMemcpyAsync(d.nframes + stream, &zero, 4, hipMemcpyHostToDevice, st), "state");
+    check_hip(hipMemcpyAsync(d.step + stream, &zero, 4, hipMemcpyHostToDevice, st), "state");
+    check_hip(hipMemcpyAsync(d.trailing_rows + stream, &trailing_rows, 4, hipMemcpyHostToDevice,
+                             st),
+              "state");
+    check_hip(hipMemcpyAsync(d.alive + stream, &one, 4, hipMemcpyHostToDevice, st), "state");
+    check_hip(hipStreamSynchronize(st), "prefill sync");
+    tc->len = rows;
+    f->host_len[stream] = rows;
+    f->started[stream] = 1;
+  });
+}
+
+extern "C" int q3h_frame_step(q3h_frame *f, int32_t *codes, int32_t *alive) {
+  return guard([&] {
+    require(f != nullptr, Q3H_E_ARG, "q3h_frame_step: NULL frame");
+    const q3h_frame_config &c = f->cfg;
+    const int n = c.n_streams;
+    bool any = false;
+    int maxlen = 0;
+    for (int s = 0; s < n; s++) {
+      if (!f->started[s]) continue;
+      any = true;
+      require(f->host_len[s] + 1 <= c.max_positions, Q3H_E_CAPACITY,
+              "q3h_frame_step: a stream reached max_positions");
+      maxlen = std::max(maxlen, f->host_len[s] + 1);
+    }
+    require(any, Q3H_E_STATE, "q3h_frame_step: no stream was started");
+    check_hip(hipSetDevice(f->talker->dev->ordinal), "hipSetDevice");
+    const int splits = attention_splits(maxlen);
+    if (c.use_graph) {
+      if (!f->exec || splits > f->graph_splits) {
+        if (f->exec) {
+          (void)hipGraphExecDestroy(f->exec);
+          f->exec = nullptr;
+        }
+        if (f->graph) {
+          (void)hipGraphDestroy(f->graph);
+          f->graph = nullptr;
+        }
+        // capture with some headroom so that the graph is rebuilt rarely
+        const int cap_splits = std::min(attention_splits(c.max_positions), splits + 1);
+        check_hip(hipStreamBeginCapture(f->stream, hipStreamCaptureModeThreadLocal),
+                  "hipStreamBeginCapture");
+        enqueue_step(f, cap_splits, f->stream);
+        check_hip(hipStreamEndCapture(f->stream, &f->graph), "hipStreamEndCapture");
+        check_hip(hipGraphInstantiate(&f->exec, f->graph, nullptr, nullptr, 0),
+                  "hipGraphInstantiate");
+        f->graph_splits = cap_splits;
+      }
+      check_hip(hipGraphLaunch(f->exec, f->stream), "hipGraphLaunch");
+    } else {
+      enqueue_step(f, splits, f->stream);
+      check_hip(hipGetLastError(), "frame kernels");
+    }
+    check_hip(hipMemcpyAsync(f->pinned, f->fd.codes, sizeof(int32_t) * n * c.groups,
+                             hipMemcpyDeviceToHost, f->stream),
+              "download codes");
+    check_hip(hipMemcpyAsync(f->pinned + n * c.groups, f->fd.alive, sizeof(int32_t) * n,
+                             hipMemcpyDeviceToHost, f->stream),
+              "download alive");
+    check_hip(hipStreamSynchronize(f->stream), "frame step sync");
+    for (int s = 0; s < n; s++) {
+      const bool live = f->started[s] && f->pinned[n * c.groups + s] != 0;
+      if (codes)
+        for (int g = 0; g < c.groups; g++)
+          codes[s * c.groups + g] = live ? f->pinned[s * c.groups + g] : -1;
+      if (alive) alive[s] = live ? 1 : 0;
+      if (live) {
+        f->host_len[s] += 1;
+        f->tctx[s]->len += 1;
+      } else {
+        f->started[s] = 0;
+      }
+    }
+  });
+}
+
+extern "C" int q3h_frame_state(q3h_frame *f, int stream, float *logits, float *past_hidden) {
+  return guard([&] {
+    require(f != nullptr, Q3H_E_ARG, "q3h_frame_state: NULL frame");
+    require(stream >= 0 && stream < f->cfg.n_streams, Q3H_E_ARG, "q3h_frame_state: bad stream");
+    check_hip(hipSetDevice(f->talker->dev->ordinal), "hipSetDevice");
+    check_hip(hipStreamSynchronize(f->stream), "frame sync");
+    if (logits)
+      check_hip(hipMemcpy(logits, f->fd.logits + (size_t)stream * f->cfg.vocab,
+                          sizeof(float) * f->cfg.vocab, hipMemcpyDeviceToHost),
+                "download logits");
+    if (past_hidden)
+      check_hip(hipMemcpy(past_hidden, f->fd.past + (size_t)stream * f->H, sizeof(float) * f->H,
+                          hipMemcpyDeviceToHost),
+                "download state");
+  });
+}
+
+extern "C" int q3h_frame_destroy(q3h_frame *f) {
+  return guard([&] {
+    require(f != nullptr, Q3H_E_ARG, "q3h_frame_destroy: NULL frame");
+    check_hip(hipSetDevice(f->talker->dev->ordinal), "hipSetDevice");
+    check_hip(hipStreamSynchronize(f->stream), "frame sync");
+    frame_release(f);
+    delete f;
+  });
+}

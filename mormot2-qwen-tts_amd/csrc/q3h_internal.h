@@ -1,0 +1,101 @@
+// q3h_internal.h - device data structures and kernel launchers of libq3h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace q3h {
+
+// A matrix [N][K] on the device: Q8_0 as int8 quants [N][K] + fp16 scales
+// [N][K/32] (structure of arrays, so a wave reads 1 KB of quants per
+// instruction), or f32 [N][K].
+struct Mat {
+  int N = 0, K = 0;
+  int8_t *q = nullptr;
+  _Float16 *d = nullptr;
+  float *f = nullptr;
+  // a Q8_0 matrix also keeps its quants as one int8 row per 32-block for the
+  // int8 product path when the stack quantizes activations (same buffers)
+};
+
+// Per-row view of a K/V cache for the attention kernels. k, v: the cache of
+// layer 0, [layers][kv_heads][max_pos][head_dim] in f32 or f16; pos: the
+// position of the row (it attends to [0, pos]); pos < 0: inactive row.
+struct RowDesc {
+  void *k;
+  void *v;
+  int max_pos;
+  int pos;
+};
+
+// Context state that kernels read and advance on the device.
+struct CtxDev {
+  void *k;
+  void *v;
+  int max_pos;
+  int len;
+};
+
+enum Epi { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2 };
+
+struct GemvArgs {
+  const int8_t *wq;
+  const _Float16 *wd;
+  const float *wf;
+  int N, K;
+  const float *x;  // [M][ldx]
+  int ldx, M;
+  const float *norm_w;  // RMSNorm prologue over each x row when non-null
+  float eps;
+  float *y;  // [M][ldy]
+  int ldy;
+  float *xn_out;  // optional: the (normed) last x row, [K], written by block 0
+};
+
+// activations quantized per 32-block (int8 path): q [M][K], d [M][K/32] f32
+struct QAct {
+  int8_t *q;
+  float *d;
+};
+
+void launch_gemv(const GemvArgs &a, int epi, bool q8, hipStream_t st);
+void launch_gemv_i8(const GemvArgs &a, const QAct &xa, int epi, hipStream_t st);
+void launch_quantize_act(const float *x, int ldx, int M, int K, const float *norm_w,
+                         float eps, QAct out, hipStream_t st);
+
+// rows of n contexts, R consecutive rows each (R > 1: one context's prefill)
+void launch_prep(CtxDev *const *cs, const int *alive, int n, int R, RowDesc *rd,
+                 hipStream_t st);
+void launch_advance(CtxDev *const *cs, const int *alive, int n, int R, hipStream_t st);
+
+void launch_qk_rope_append(float *qkv, int ldq, const RowDesc *rd, int M, int layer,
+                           int heads, int kvh, int hd, const float *qn, const float *kn,
+                           float eps, const float *rope_cs, bool kv16, hipStream_t st);
+void launch_attention(const float *qkv, int ldq, const RowDesc *rd, int M, int layer,
+                      int heads, int kvh, int hd, int splits, int chunk, float *out,
+                      float *part, bool kv16, hipStream_t st);
+
+void launch_rmsnorm_rows(const float *x, int ldx, int M, int K, const float *w, float eps,
+                         float *y, int ldy, hipStream_t st);
+
+void launch_quantize_q8(const float *src, int rows, int K, int8_t *q, _Float16 *d,
+                        int row_stride, int row_off, hipStream_t st);
+void launch_repack_q8(const uint8_t *blocks, int rows, int K, int8_t *q, _Float16 *d,
+                      int row_stride, int row_off, hipStream_t st);
+void launch_copy_rows_f32(const float *src, int rows, int K, float *dst, int row_stride,
+                          int row_off, hipStream_t st);
+void launch_kv_fill(const float *src, int layers, int kvh, int len, int hd, void *dst,
+                    int max_pos, bool kv16, hipStream_t st);
+void launch_kv_read(const void *src, int layer, int kvh, int len, int hd, int max_pos,
+                    bool kv16, float *dst, hipStream_t st);
+
+// frame step kernels
+struct FrameDev;
+void launch_choose_code0(FrameDev *fd, int n, hipStream_t st);
+void launch_cp_argmax(FrameDev *fd, int n, int g, hipStream_t st);
+void launch_talker_input(FrameDev *fd, int n, hipStream_t st);
+void launch_frame_end(FrameDev *fd, int n, hipStream_t st);
+
+}  // namespace q3h

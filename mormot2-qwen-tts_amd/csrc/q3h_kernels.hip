@@ -1,0 +1,686 @@
+// q3h_kernels.hip - gfx950 kernels of the Qwen3 stack step (decode and small
+// multi-row forwards): fused RMSNorm + GEMV over Q8_0 or f32 weights, QK-norm
+// + RoPE + K/V append, split-K GQA attention, load-time Q8_0 conversion.
+//
+// Layouts (HBM):
+//  - Q8_0 matrix [N][K]: int8 quants row-major + fp16 scales [N][K/32]. A lane
+//    owns 16 consecutive quants of a row per 1024-column chunk, so one
+//    dwordx4 load instruction of a wave covers 1 KB of one row, coalesced.
+//  - f32 matrix [N][K]: a lane owns 4 consecutive floats per 256-column chunk.
+//  - K/V cache: [layers][kv_heads][max_pos][head_dim], f32 or f16: the keys
+//    of one head are contiguous, so a split of positions is one linear read.
+#include <hip/hip_runtime.h>
+
+#include "q3h_internal.h"
+
+namespace q3h {
+
+constexpr int kBlock = 256;
+constexpr int kMaxRows = 4;  // activation rows held in LDS per GEMV pass
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return g / (1.0f + expf(-g)) * u;
+}
+
+// Stage M (<= kMaxRows) activation rows of K floats into LDS, RMS-normalized
+// with weight w when w != nullptr: y = w * (x * inv), inv = 1/sqrt(mean(x^2)+eps)
+// (sum of squares in double). Block 0 may also publish the last staged row.
+__device__ void stage_rows(const float *__restrict__ x, int ldx, int M, int K,
+                           const float *__restrict__ w, float eps, float *xs,
+                           float *xn_out) {
+  __shared__ double red[kBlock / 64][kMaxRows];
+  __shared__ float inv[kMaxRows];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int m = 0; m < M; m++) {
+    const float4 *src = reinterpret_cast<const float4 *>(x + (size_t)m * ldx);
+    float4 *dst = reinterpret_cast<float4 *>(xs + m * K);
+    double ss = 0.0;
+    for (int k = tid; k < (K >> 2); k += kBlock) {
+      const float4 v = src[k];
+      dst[k] = v;
+      ss += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+    }
+    if (w) {
+      ss = wave_sum_d(ss);
+      if (lane == 0) red[wave][m] = ss;
+    }
+  }
+  if (!w) {
+    __syncthreads();
+    if (xn_out && blockIdx.x == 0)
+      for (int k = tid; k < K; k += kBlock) xn_out[k] = xs[(M - 1) * K + k];
+    return;
+  }
+  __syncthreads();
+  if (tid < M) {
+    double t = 0.0;
+    for (int i = 0; i < kBlock / 64; i++) t += red[i][tid];
+    inv[tid] = (float)(1.0 / sqrt(t / K + (double)eps));
+  }
+  __syncthreads();
+  for (int m = 0; m < M; m++) {
+    const float iv = inv[m];
+    for (int k = tid; k < K; k += kBlock) xs[m * K + k] = w[k] * (xs[m * K + k] * iv);
+  }
+  __syncthreads();
+  if (xn_out && blockIdx.x == 0)
+    for (int k = tid; k < K; k += kBlock) xn_out[k] = xs[(M - 1) * K + k];
+}
+
+__device__ __forceinline__ float dot16_i8(const int4 w, const float *x) {
+  const int ws[4] = {w.x, w.y, w.z, w.w};
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int v = ws[i];
+    s0 = fmaf((float)(int8_t)(v), x[4 * i + 0], s0);
+    s1 = fmaf((float)(int8_t)(v >> 8), x[4 * i + 1], s1);
+    s0 = fmaf((float)(int8_t)(v >> 16), x[4 * i + 2], s0);
+    s1 = fmaf((float)(int8_t)(v >> 24), x[4 * i + 3], s1);
+  }
+  return s0 + s1;
+}
+
+template <int RPW, int EPI>
+__device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, float (&acc)[RPW][kMaxRows],
+                                              int row0) {
+  // every lane holds the reduced sums; lane 0 stores
+  if ((threadIdx.x & 63) != 0) return;
+#pragma unroll
+  for (int m = 0; m < kMaxRows; m++) {
+    if (m >= a.M) break;
+    float *y = a.y + (size_t)m * a.ldy;
+    if (EPI == EPI_SWIGLU) {
+#pragma unroll
+      for (int p = 0; p < RPW / 2; p++) {
+        const int j = row0 / 2 + p;
+        if (2 * j + 1 < a.N) y[j] = silu_mul(acc[2 * p][m], acc[2 * p + 1][m]);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < RPW; r++) {
+        const int row = row0 + r;
+        if (row < a.N) {
+          if (EPI == EPI_ADD)
+            y[row] += acc[r][m];
+          else
+            y[row] = acc[r][m];
+        }
+      }
+    }
+  }
+}
+
+// y[m][n] (+)= sum_k W[n][k] xn[m][k]: Q8_0 weights, f32 activations.
+// Each wave owns RPW consecutive rows; a lane owns 16-column segments.
+template <int RPW, int EPI>
+__global__ __launch_bounds__(kBlock) void k_gemv_q8(GemvArgs a) {
+  extern __shared__ float xs[];
+  stage_rows(a.x, a.ldx, a.M, a.K, a.norm_w, a.eps, xs, a.xn_out);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * (kBlock / 64) + wave) * RPW;
+  if (row0 >= a.N) return;
+  const int K = a.K, M = a.M, nseg = K >> 4, nb = K >> 5;
+  float acc[RPW][kMaxRows];
+#pragma unroll
+  for (int r = 0; r < RPW; r++)
+#pragma unroll
+    for (int m = 0; m < kMaxRows; m++) acc[r][m] = 0.f;
+  const int8_t *wq[RPW];
+  const _Float16 *wd[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const int row = min(row0 + r, a.N - 1);
+    wq[r] = a.wq + (size_t)row * K;
+    wd[r] = a.wd + (size_t)row * nb;
+  }
+  for (int seg = lane; seg < nseg; seg += 64) {
+    int4 wv[RPW];
+    float sc[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+      wv[r] = *reinterpret_cast<const int4 *>(wq[r] + seg * 16);
+      sc[r] = (float)wd[r][seg >> 1];
+    }
+#pragma unroll
+    for (int m = 0; m < kMaxRows; m++) {
+      if (m < M) {
+        float xv[16];
+        const float4 *xp = reinterpret_cast<const float4 *>(xs + m * K + seg * 16);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float4 t = xp[i];
+          xv[4 * i] = t.x;
+          xv[4 * i + 1] = t.y;
+          xv[4 * i + 2] = t.z;
+          xv[4 * i + 3] = t.w;
+        }
+#pragma unroll
+        for (int r = 0; r < RPW; r++) acc[r][m] = fmaf(sc[r], dot16_i8(wv[r], xv), acc[r][m]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; r++)
+#pragma unroll
+    for (int m = 0; m < kMaxRows; m++)
+      if (m < M) acc[r][m] = wave_sum(acc[r][m]);
+  gemv_epilogue<RPW, EPI>(a, acc, row0);
+}
+
+// Same over f32 weights: a lane owns 4-column segments (coalesced 1 KB per
+// wave instruction).
+template <int RPW, int EPI>
+__global__ __launch_bounds__(kBlock) void k_gemv_f32(GemvArgs a) {
+  extern __shared__ float xs[];
+  stage_rows(a.x, a.ldx, a.M, a.K, a.norm_w, a.eps, xs, a.xn_out);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * (kBlock / 64) + wave) * RPW;
+  if (row0 >= a.N) return;
+  const int K = a.K, M = a.M, nseg = K >> 2;
+  float acc[RPW][kMaxRows];
+#pragma unroll
+  for (int r = 0; r < RPW; r++)
+#pragma unroll
+    for (int m = 0; m < kMaxRows; m++) acc[r][m] = 0.f;
+  const float *wf[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; r++) wf[r] = a.wf + (size_t)min(row0 + r, a.N - 1) * K;
+  for (int seg = lane; seg < nseg; seg += 64) {
+    float4 wv[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) wv[r] = reinterpret_cast<const float4 *>(wf[r])[seg];
+#pragma unroll
+    for (int m = 0; m < kMaxRows; m++) {
+      if (m < M) {
+        const float4 xv = reinterpret_cast<const float4 *>(xs + m * K)[seg];
+#pragma unroll
+        for (int r = 0; r < RPW; r++) {
+          float s = acc[r][m];
+          s = fmaf(wv[r].x, xv.x, s);
+          s = fmaf(wv[r].y, xv.y, s);
+          s = fmaf(wv[r].z, xv.z, s);
+          s = fmaf(wv[r].w, xv.w, s);
+          acc[r][m] = s;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; r++)
+#pragma unroll
+    for (int m = 0; m < kMaxRows; m++)
+      if (m < M) acc[r][m] = wave_sum(acc[r][m]);
+  gemv_epilogue<RPW, EPI>(a, acc, row0);
+}
+
+template <int RPW>
+static void gemv_dispatch(const GemvArgs &a, int epi, bool q8, hipStream_t st) {
+  const int rows_per_block = (kBlock / 64) * RPW;
+  const dim3 grid((a.N + rows_per_block - 1) / rows_per_block);
+  const size_t lds = sizeof(float) * a.M * a.K;
+#define Q3H_GEMV(KER, E) hipLaunchKernelGGL((KER<RPW, E>), grid, dim3(kBlock), lds, st, a)
+  if (q8) {
+    if (epi == EPI_STORE) Q3H_GEMV(k_gemv_q8, EPI_STORE);
+    else if (epi == EPI_ADD) Q3H_GEMV(k_gemv_q8, EPI_ADD);
+    else Q3H_GEMV(k_gemv_q8, EPI_SWIGLU);
+  } else {
+    if (epi == EPI_STORE) Q3H_GEMV(k_gemv_f32, EPI_STORE);
+    else if (epi == EPI_ADD) Q3H_GEMV(k_gemv_f32, EPI_ADD);
+    else Q3H_GEMV(k_gemv_f32, EPI_SWIGLU);
+  }
+#undef Q3H_GEMV
+}
+
+// Rows per wave: keep >= ~256 blocks on the 256 CUs when the matrix allows;
+// SwiGLU needs gate/up pairs inside one wave.
+void launch_gemv(const GemvArgs &a0, int epi, bool q8, hipStream_t st) {
+  GemvArgs a = a0;
+  for (int m0 = 0; m0 < a0.M; m0 += kMaxRows) {
+    a.M = min(kMaxRows, a0.M - m0);
+    a.x = a0.x + (size_t)m0 * a0.ldx;
+    a.y = a0.y + (size_t)m0 * a0.ldy;
+    a.xn_out = (m0 + a.M == a0.M) ? a0.xn_out : nullptr;
+    const int waves = a.N;  // with RPW = 1
+    if (epi == EPI_SWIGLU || waves >= 8192)
+      gemv_dispatch<4>(a, epi, q8, st);
+    else if (waves >= 2048)
+      gemv_dispatch<2>(a, epi, q8, st);
+    else
+      gemv_dispatch<1>(a, epi, q8, st);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// row descriptors and context lengths
+
+__global__ void k_prep(CtxDev *const *cs, const int *alive, int n, int R, RowDesc *rd) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n * R) return;
+  const int s = i / R, r = i % R;
+  const CtxDev *c = cs[s];
+  RowDesc d;
+  d.k = c->k;
+  d.v = c->v;
+  d.max_pos = c->max_pos;
+  const int pos = c->len + r;
+  d.pos = (alive && !alive[s]) || pos >= c->max_pos ? -1 : pos;
+  rd[i] = d;
+}
+
+__global__ void k_advance(CtxDev *const *cs, const int *alive, int n, int R) {
+  const int s = blockIdx.x * blockDim.x + threadIdx.x;
+  if (s >= n) return;
+  if (alive && !alive[s]) return;
+  CtxDev *c = cs[s];
+  c->len = min(c->len + R, c->max_pos);
+}
+
+void launch_prep(CtxDev *const *cs, const int *alive, int n, int R, RowDesc *rd,
+                 hipStream_t st) {
+  hipLaunchKernelGGL(k_prep, dim3((n * R + 63) / 64), dim3(64), 0, st, cs, alive, n, R, rd);
+}
+
+void launch_advance(CtxDev *const *cs, const int *alive, int n, int R, hipStream_t st) {
+  hipLaunchKernelGGL(k_advance, dim3((n + 63) / 64), dim3(64), 0, st, cs, alive, n, R);
+}
+
+// ---------------------------------------------------------------------------
+// QK-norm, RoPE, K/V append: one wave per head vector (q heads, k heads,
+// v heads of each row); a lane holds elements i and i + head_dim/2, the pair
+// that rotate_half mixes.
+
+template <typename KV>
+__global__ __launch_bounds__(kBlock) void k_qk_rope_append(
+    float *qkv, int ldq, const RowDesc *rd, int layer, int heads, int kvh, int hd,
+    const float *qn, const float *kn, float eps, const float2 *rope_cs) {
+  const int lane = threadIdx.x & 63;
+  const int j = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
+  const int m = blockIdx.y;
+  if (j >= heads + 2 * kvh) return;
+  const RowDesc d = rd[m];
+  if (d.pos < 0) return;
+  const int half = hd >> 1;
+  float *vec = qkv + (size_t)m * ldq + (size_t)j * hd;
+  const bool on = lane < half;
+  float x0 = on ? vec[lane] : 0.f, x1 = on ? vec[lane + half] : 0.f;
+  if (j < heads + kvh) {
+    const float *w = j < heads ? qn : kn;
+    double ss = (double)x0 * x0 + (double)x1 * x1;
+    ss = wave_sum_d(ss);
+    const float inv = (float)(1.0 / sqrt(ss / hd + (double)eps));
+    if (on) {
+      x0 = w[lane] * (x0 * inv);
+      x1 = w[lane + half] * (x1 * inv);
+      const float2 cs = rope_cs[(size_t)d.pos * half + lane];
+      const float y0 = x0 * cs.x - x1 * cs.y;
+      const float y1 = x1 * cs.x + x0 * cs.y;
+      x0 = y0;
+      x1 = y1;
+    }
+  }
+  if (!on) return;
+  if (j < heads) {
+    vec[lane] = x0;
+    vec[lane + half] = x1;
+    return;
+  }
+  const int g = j < heads + kvh ? j - heads : j - heads - kvh;
+  void *base = j < heads + kvh ? d.k : d.v;
+  KV *dst = reinterpret_cast<KV *>(base) +
+            (((size_t)layer * kvh + g) * d.max_pos + d.pos) * hd;
+  dst[lane] = (KV)x0;
+  dst[lane + half] = (KV)x1;
+}
+
+void launch_qk_rope_append(float *qkv, int ldq, const RowDesc *rd, int M, int layer,
+                           int heads, int kvh, int hd, const float *qn, const float *kn,
+                           float eps, const float *rope_cs, bool kv16, hipStream_t st) {
+  const dim3 grid((heads + 2 * kvh + 3) / 4, M);
+  const float2 *cs = reinterpret_cast<const float2 *>(rope_cs);
+  if (kv16)
+    hipLaunchKernelGGL(k_qk_rope_append<_Float16>, grid, dim3(kBlock), 0, st, qkv, ldq, rd,
+                       layer, heads, kvh, hd, qn, kn, eps, cs);
+  else
+    hipLaunchKernelGGL(k_qk_rope_append<float>, grid, dim3(kBlock), 0, st, qkv, ldq, rd,
+                       layer, heads, kvh, hd, qn, kn, eps, cs);
+}
+
+// ---------------------------------------------------------------------------
+// GQA attention over one split of positions for the q heads of one kv head:
+// K/V of the kv head are read once for its grp q heads. 8 lanes per key (16
+// dims each) for the scores, one thread per (q head, dim) for the values.
+
+constexpr int kChunk = 256;  // positions per split
+constexpr int kMaxGrp = 4;   // q heads per kv head
+constexpr int kMaxHd = 128;
+
+__device__ __forceinline__ void load16(const float *p, float *o) {
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float4 t = reinterpret_cast<const float4 *>(p)[i];
+    o[4 * i] = t.x;
+    o[4 * i + 1] = t.y;
+    o[4 * i + 2] = t.z;
+    o[4 * i + 3] = t.w;
+  }
+}
+
+__device__ __forceinline__ void load16(const _Float16 *p, float *o) {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const h8 t = reinterpret_cast<const h8 *>(p)[i];
+#pragma unroll
+    for (int j = 0; j < 8; j++) o[8 * i + j] = (float)t[j];
+  }
+}
+
+template <typename KV>
+__global__ __launch_bounds__(kBlock) void k_attention(const float *qkv, int ldq,
+                                                      const RowDesc *rd, int layer,
+                                                      int heads, int kvh, int hd,
+                                                      int splits, float *out, float *part) {
+  __shared__ float qs[kMaxGrp][kMaxHd];
+  __shared__ float sc[kMaxGrp][kChunk];
+  __shared__ float mx[kMaxGrp], sum[kMaxGrp];
+  const int g = blockIdx.x, m = blockIdx.y, s = blockIdx.z, tid = threadIdx.x;
+  const int grp = heads / kvh;
+  const RowDesc d = rd[m];
+  const int n = d.pos + 1;
+  const int p0 = s * kChunk, p1 = min(n, p0 + kChunk);
+  const int ldo = heads * hd;
+  if (d.pos < 0 || p0 >= p1) {
+    // an inactive row, or an empty split
+    for (int i = tid; i < grp * hd; i += kBlock) {
+      const int hh = i / hd, dd = i % hd, h = g * grp + hh;
+      if (splits == 1) {
+        out[(size_t)m * ldo + h * hd + dd] = 0.f;
+      } else {
+        float *pp = part + (((size_t)m * heads + h) * splits + s) * (hd + 2);
+        pp[dd] = 0.f;
+        if (dd == 0) {
+          pp[hd] = -INFINITY;
+          pp[hd + 1] = 0.f;
+        }
+      }
+    }
+    return;
+  }
+  const float scale = 1.0f / sqrtf((float)hd);
+  for (int i = tid; i < grp * hd; i += kBlock)
+    qs[i / hd][i % hd] = qkv[(size_t)m * ldq + (size_t)(g * grp) * hd + i];
+  __syncthreads();
+  const size_t head_off = ((size_t)layer * kvh + g) * d.max_pos * hd;
+  const KV *kc = reinterpret_cast<const KV *>(d.k) + head_off;
+  const KV *vc = reinterpret_cast<const KV *>(d.v) + head_off;
+  // scores: 8 lanes per key, 16 dims per lane (hd == 128)
+  {
+    const int sub = tid & 7, pg = tid >> 3;
+    for (int p = p0 + pg; p < p1; p += kBlock / 8) {
+      float kv[16];
+      load16(kc + (size_t)p * hd + sub * 16, kv);
+      for (int hh = 0; hh < grp; hh++) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc = fmaf(qs[hh][sub * 16 + i], kv[i], acc);
+        acc += __shfl_xor(acc, 1, 64);
+        acc += __shfl_xor(acc, 2, 64);
+        acc += __shfl_xor(acc, 4, 64);
+        if (sub == 0) sc[hh][p - p0] = acc * scale;
+      }
+    }
+  }
+  __syncthreads();
+  // softmax statistics: wave hh owns q head hh
+  {
+    const int wave = tid >> 6, lane = tid & 63, cnt = p1 - p0;
+    if (wave < grp) {
+      float m0 = -INFINITY;
+      for (int i = lane; i < cnt; i += 64) m0 = fmaxf(m0, sc[wave][i]);
+      m0 = wave_max(m0);
+      float l0 = 0.f;
+      for (int i = lane; i < cnt; i += 64) {
+        const float e = expf(sc[wave][i] - m0);
+        sc[wave][i] = e;
+        l0 += e;
+      }
+      l0 = wave_sum(l0);
+      if (lane == 0) {
+        mx[wave] = m0;
+        sum[wave] = l0;
+      }
+    }
+  }
+  __syncthreads();
+  // values
+  for (int i = tid; i < grp * hd; i += kBlock) {
+    const int hh = i / hd, dd = i % hd, h = g * grp + hh;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    int p = p0;
+    for (; p + 3 < p1; p += 4) {
+      a0 = fmaf(sc[hh][p - p0], (float)vc[(size_t)p * hd + dd], a0);
+      a1 = fmaf(sc[hh][p + 1 - p0], (float)vc[(size_t)(p + 1) * hd + dd], a1);
+      a2 = fmaf(sc[hh][p + 2 - p0], (float)vc[(size_t)(p + 2) * hd + dd], a2);
+      a3 = fmaf(sc[hh][p + 3 - p0], (float)vc[(size_t)(p + 3) * hd + dd], a3);
+    }
+    for (; p < p1; p++) a0 = fmaf(sc[hh][p - p0], (float)vc[(size_t)p * hd + dd], a0);
+    const float o = (a0 + a1) + (a2 + a3);
+    if (splits == 1) {
+      out[(size_t)m * ldo + h * hd + dd] = o / sum[hh];
+    } else {
+      float *pp = part + (((size_t)m * heads + h) * splits + s) * (hd + 2);
+      pp[dd] = o;
+      if (dd == 0) {
+        pp[hd] = mx[hh];
+        pp[hd + 1] = sum[hh];
+      }
+    }
+  }
+}
+
+__global__ void k_attn_combine(const float *part, int heads, int hd, int splits,
+                               float *out) {
+  const int h = blockIdx.x, m = blockIdx.y, dd = threadIdx.x;
+  if (dd >= hd) return;
+  const float *pp = part + ((size_t)m * heads + h) * splits * (hd + 2);
+  float gm = -INFINITY;
+  for (int s = 0; s < splits; s++) gm = fmaxf(gm, pp[s * (hd + 2) + hd]);
+  float l = 0.f, o = 0.f;
+  if (gm > -INFINITY) {
+    for (int s = 0; s < splits; s++) {
+      const float ms = pp[s * (hd + 2) + hd];
+      if (ms == -INFINITY) continue;
+      const float e = expf(ms - gm);
+      l += e * pp[s * (hd + 2) + hd + 1];
+      o += e * pp[s * (hd + 2) + dd];
+    }
+  }
+  out[((size_t)m * heads + h) * hd + dd] = l > 0.f ? o / l : 0.f;
+}
+
+void launch_attention(const float *qkv, int ldq, const RowDesc *rd, int M, int layer,
+                      int heads, int kvh, int hd, int splits, int chunk, float *out,
+                      float *part, bool kv16, hipStream_t st) {
+  (void)chunk;
+  const dim3 grid(kvh, M, splits);
+  if (kv16)
+    hipLaunchKernelGGL(k_attention<_Float16>, grid, dim3(kBlock), 0, st, qkv, ldq, rd, layer,
+                       heads, kvh, hd, splits, out, part);
+  else
+    hipLaunchKernelGGL(k_attention<float>, grid, dim3(kBlock), 0, st, qkv, ldq, rd, layer,
+                       heads, kvh, hd, splits, out, part);
+  if (splits > 1)
+    hipLaunchKernelGGL(k_attn_combine, dim3(heads, M), dim3(hd), 0, st, part, heads, hd,
+                       splits, out);
+}
+
+// ---------------------------------------------------------------------------
+// plain row RMSNorm (the final norm of a stack)
+
+__global__ __launch_bounds__(kBlock) void k_rmsnorm_rows(const float *x, int ldx, int K,
+                                                         const float *w, float eps,
+                                                         float *y, int ldy) {
+  __shared__ double red[kBlock / 64];
+  const int m = blockIdx.x, tid = threadIdx.x;
+  const float *xr = x + (size_t)m * ldx;
+  double ss = 0.0;
+  for (int k = tid; k < K; k += kBlock) ss += (double)xr[k] * xr[k];
+  ss = wave_sum_d(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  double t = 0.0;
+  for (int i = 0; i < kBlock / 64; i++) t += red[i];
+  const float inv = (float)(1.0 / sqrt(t / K + (double)eps));
+  for (int k = tid; k < K; k += kBlock) y[(size_t)m * ldy + k] = w[k] * (xr[k] * inv);
+}
+
+void launch_rmsnorm_rows(const float *x, int ldx, int M, int K, const float *w, float eps,
+                         float *y, int ldy, hipStream_t st) {
+  hipLaunchKernelGGL(k_rmsnorm_rows, dim3(M), dim3(kBlock), 0, st, x, ldx, K, w, eps, y, ldy);
+}
+
+// ---------------------------------------------------------------------------
+// load-time conversion: f32 rows -> Q8_0 (ggml quantize_row_q8_0_ref: d =
+// amax/127 rounded to fp16, q = round(x * (1/d)) half away from zero, both
+// divisions correctly rounded), ggml blocks -> structure of arrays, f32 row
+// copies; dst row = src row * row_stride + row_off (fused QKV, interleaved
+// gate/up).
+
+__global__ void k_quantize_q8(const float *src, int rows, int K, int8_t *q, _Float16 *d,
+                              int row_stride, int row_off) {
+  const int nb = K >> 5;
+  const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= (size_t)rows * nb) return;
+  const int r = (int)(b / nb), i = (int)(b % nb);
+  const float *x = src + (size_t)r * K + i * 32;
+  float v[32];
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < 32; j++) {
+    v[j] = x[j];
+    const float a = fabsf(v[j]);
+    amax = amax > a ? amax : a;
+  }
+  const float dd = __fdiv_rn(amax, 127.0f);
+  const float id = dd != 0.f ? __fdiv_rn(1.0f, dd) : 0.f;
+  const size_t orow = (size_t)r * row_stride + row_off;
+  d[orow * nb + i] = (_Float16)dd;
+  int8_t *qo = q + orow * K + i * 32;
+#pragma unroll
+  for (int j = 0; j < 32; j++) qo[j] = (int8_t)roundf(__fmul_rn(v[j], id));
+}
+
+__global__ void k_repack_q8(const uint8_t *blocks, int rows, int K, int8_t *q, _Float16 *d,
+                            int row_stride, int row_off) {
+  const int nb = K >> 5;
+  const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= (size_t)rows * nb) return;
+  const int r = (int)(b / nb), i = (int)(b % nb);
+  const uint8_t *src = blocks + b * 34;
+  const size_t orow = (size_t)r * row_stride + row_off;
+  const uint16_t bits = (uint16_t)src[0] | ((uint16_t)src[1] << 8);
+  d[orow * nb + i] = __builtin_bit_cast(_Float16, bits);
+  int8_t *qo = q + orow * K + i * 32;
+#pragma unroll
+  for (int j = 0; j < 32; j++) qo[j] = (int8_t)src[2 + j];
+}
+
+__global__ void k_copy_rows_f32(const float *src, int rows, int K, float *dst,
+                                int row_stride, int row_off) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)rows * K) return;
+  const int r = (int)(i / K), k = (int)(i % K);
+  dst[((size_t)r * row_stride + row_off) * K + k] = src[i];
+}
+
+void launch_quantize_q8(const float *src, int rows, int K, int8_t *q, _Float16 *d,
+                        int row_stride, int row_off, hipStream_t st) {
+  const size_t n = (size_t)rows * (K >> 5);
+  hipLaunchKernelGGL(k_quantize_q8, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, src,
+                     rows, K, q, d, row_stride, row_off);
+}
+
+void launch_repack_q8(const uint8_t *blocks, int rows, int K, int8_t *q, _Float16 *d,
+                      int row_stride, int row_off, hipStream_t st) {
+  const size_t n = (size_t)rows * (K >> 5);
+  hipLaunchKernelGGL(k_repack_q8, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, blocks,
+                     rows, K, q, d, row_stride, row_off);
+}
+
+void launch_copy_rows_f32(const float *src, int rows, int K, float *dst, int row_stride,
+                          int row_off, hipStream_t st) {
+  const size_t n = (size_t)rows * K;
+  hipLaunchKernelGGL(k_copy_rows_f32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, src,
+                     rows, K, dst, row_stride, row_off);
+}
+
+// K/V fill / read (long-context setups, tests): src [layers][kvh][len][hd]
+template <typename KV>
+__global__ void k_kv_fill(const float *src, int layers, int kvh, int len, int hd, KV *dst,
+                          int max_pos) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t n = (size_t)layers * kvh * len * hd;
+  if (i >= n) return;
+  const int dd = (int)(i % hd);
+  const size_t t = i / hd;
+  const int p = (int)(t % len);
+  const size_t lg = t / len;  // layer * kvh + g
+  dst[(lg * max_pos + p) * hd + dd] = (KV)src[i];
+}
+
+template <typename KV>
+__global__ void k_kv_read(const KV *src, int layer, int kvh, int len, int hd, int max_pos,
+                          float *dst) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t n = (size_t)kvh * len * hd;
+  if (i >= n) return;
+  const int dd = (int)(i % hd);
+  const size_t t = i / hd;
+  const int p = (int)(t % len), g = (int)(t / len);
+  dst[i] = (float)src[(((size_t)layer * kvh + g) * max_pos + p) * hd + dd];
+}
+
+void launch_kv_fill(const float *src, int layers, int kvh, int len, int hd, void *dst,
+                    int max_pos, bool kv16, hipStream_t st) {
+  const size_t n = (size_t)layers * kvh * len * hd;
+  const dim3 grid((unsigned)((n + 255) / 256));
+  if (kv16)
+    hipLaunchKernelGGL(k_kv_fill<_Float16>, grid, dim3(256), 0, st, src, layers, kvh, len, hd,
+                       (_Float16 *)dst, max_pos);
+  else
+    hipLaunchKernelGGL(k_kv_fill<float>, grid, dim3(256), 0, st, src, layers, kvh, len, hd,
+                       (float *)dst, max_pos);
+}
+
+void launch_kv_read(const void *src, int layer, int kvh, int len, int hd, int max_pos,
+                    bool kv16, float *dst, hipStream_t st) {
+  const size_t n = (size_t)kvh * len * hd;
+  const dim3 grid((unsigned)((n + 255) / 256));
+  if (kv16)
+    hipLaunchKernelGGL(k_kv_read<_Float16>, grid, dim3(256), 0, st, (const _Float16 *)src,
+                       layer, kvh, len, hd, max_pos, dst);
+  else
+    hipLaunchKernelGGL(k_kv_read<float>, grid, dim3(256), 0, st, (const float *)src, layer,
+                       kvh, len, hd, max_pos, dst);
+}
+
+}  // namespace q3h

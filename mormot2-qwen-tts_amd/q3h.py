@@ -1,0 +1,381 @@
+"""ctypes binding of libq3h (include/q3h.h) and a host mirror of the reference's
+stack adapter.
+
+`QwenLm` mirrors TQwenLm of src/tts/mormot.ai.tts.qwen.lm.pas:104-143
+(Create / Reset / Forward / Length); `Talker` drives the device-resident
+frame step that restates TQwenTalker.Start / NextFrame
+(src/tts/mormot.ai.tts.qwen.talker.pas:471-681). Errors raise Q3HError with the
+library's message, as the Pascal binding raises EQwenLm (lm.pas:41).
+
+The library must be built (see __graft_entry__.build); nothing here falls back
+to a CPU path: loading fails loudly when libq3h.so is missing.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libq3h.so")
+
+F32 = 0
+Q8_0 = 1
+
+E_ARG, E_HIP, E_CAPACITY, E_STATE, E_NODEV = -1, -2, -3, -4, -5
+
+
+class Q3HError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"q3h error {code}: {msg}")
+        self.code = code
+
+
+class StackConfig(ctypes.Structure):
+    _fields_ = [
+        ("layers", ctypes.c_int32),
+        ("hidden", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("intermediate", ctypes.c_int32),
+        ("rms_eps", ctypes.c_float),
+        ("rope_theta", ctypes.c_float),
+        ("dtype", ctypes.c_int32),
+        ("kv_f16", ctypes.c_int32),
+        ("act_q8", ctypes.c_int32),
+        ("max_positions", ctypes.c_int32),
+    ]
+
+
+class LayerWeights(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in
+                ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown",
+                 "input_norm", "post_norm", "q_norm", "k_norm")]
+
+
+class Weights(ctypes.Structure):
+    _fields_ = [
+        ("src_dtype", ctypes.c_int32),
+        ("layers", ctypes.POINTER(LayerWeights)),
+        ("final_norm", ctypes.c_void_p),
+    ]
+
+
+class FrameConfig(ctypes.Structure):
+    _fields_ = [
+        ("n_streams", ctypes.c_int32),
+        ("talker_head", ctypes.c_int32),
+        ("cp_heads", ctypes.c_int32 * 15),
+        ("vocab", ctypes.c_int32),
+        ("cp_vocab", ctypes.c_int32),
+        ("groups", ctypes.c_int32),
+        ("eos", ctypes.c_int32),
+        ("repetition_penalty", ctypes.c_float),
+        ("max_frames", ctypes.c_int32),
+        ("max_positions", ctypes.c_int32),
+        ("use_graph", ctypes.c_int32),
+    ]
+
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_FP = ctypes.POINTER(ctypes.c_float)
+_IP = ctypes.POINTER(ctypes.c_int32)
+
+# name -> (restype, argtypes): every entry point of include/q3h.h
+SIGNATURES = {
+    "q3h_device_available": (_I, []),
+    "q3h_device_open": (_I, [_I, ctypes.POINTER(_P)]),
+    "q3h_device_name": (ctypes.c_char_p, [_P]),
+    "q3h_device_bytes": (ctypes.c_int64, [_P]),
+    "q3h_device_close": (_I, [_P]),
+    "q3h_last_error": (ctypes.c_char_p, []),
+    "q3h_stack_create": (_I, [_P, ctypes.POINTER(StackConfig), ctypes.POINTER(Weights),
+                              ctypes.POINTER(_P)]),
+    "q3h_stack_add_head": (_I, [_P, _P, _I, _I, ctypes.POINTER(_I)]),
+    "q3h_stack_bytes": (ctypes.c_int64, [_P]),
+    "q3h_stack_destroy": (_I, [_P]),
+    "q3h_context_create": (_I, [_P, _I, ctypes.POINTER(_P)]),
+    "q3h_context_reset": (_I, [_P]),
+    "q3h_context_length": (_I, [_P]),
+    "q3h_context_destroy": (_I, [_P]),
+    "q3h_context_fill_kv": (_I, [_P, _FP, _FP, _I]),
+    "q3h_context_read_kv": (_I, [_P, _I, _FP, _FP]),
+    "q3h_forward_embeds": (_I, [_P, _FP, _I, _I, _FP, _FP]),
+    "q3h_forward_embeds_batch": (_I, [ctypes.POINTER(_P), _I, _FP, _IP, _FP, _FP]),
+    "q3h_frame_create": (_I, [_P, _P, ctypes.POINTER(FrameConfig), _FP,
+                              ctypes.POINTER(_FP), _FP, ctypes.POINTER(_P)]),
+    "q3h_frame_start": (_I, [_P, _I, _FP, _I, _FP, _I]),
+    "q3h_frame_step": (_I, [_P, _IP, _IP]),
+    "q3h_frame_state": (_I, [_P, _I, _FP, _FP]),
+    "q3h_frame_destroy": (_I, [_P]),
+    "q3h_quantize_row_q8_0": (_I, [_FP, _P, ctypes.c_int64]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded libq3h (raises if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise OSError(f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(rc):
+    if rc != 0:
+        raise Q3HError(rc, lib().q3h_last_error().decode(errors="replace"))
+
+
+def _fp(a):
+    return a.ctypes.data_as(_FP) if a is not None else None
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def available():
+    return bool(lib().q3h_device_available())
+
+
+def quantize_q8_0(x):
+    """ggml quantize_row_q8_0_ref of a float32 matrix [..., k]: uint8 blocks."""
+    x = _f32(x)
+    k = x.size
+    out = np.empty(k // 32 * 34, dtype=np.uint8)
+    _check(lib().q3h_quantize_row_q8_0(_fp(x), out.ctypes.data_as(_P), k))
+    return out.reshape(x.shape[:-1] + (x.shape[-1] // 32 * 34,))
+
+
+class Device:
+    """TQwenVulkan (lm.pas:44-62) for a gfx950 device."""
+
+    def __init__(self, ordinal=0):
+        h = _P()
+        _check(lib().q3h_device_open(ordinal, ctypes.byref(h)))
+        self.h = h
+
+    @property
+    def name(self):
+        return lib().q3h_device_name(self.h).decode()
+
+    @property
+    def bytes(self):
+        return lib().q3h_device_bytes(self.h)
+
+    def close(self):
+        if self.h:
+            _check(lib().q3h_device_close(self.h))
+            self.h = None
+
+
+class Stack:
+    """A Qwen3 stack on the device (TQwen3Model.CreateStack + TQwen3Vulkan.Create)."""
+
+    def __init__(self, dev, cfg, layers, final_norm, src_dtype):
+        """cfg: dict of StackConfig fields; layers: list of dicts with wq..wdown
+        (float32 [out][in] or uint8 Q8_0 blocks [out][in/32*34]) and the norm
+        vectors; src_dtype: F32 or Q8_0."""
+        self.cfg = dict(cfg)
+        c = StackConfig(**{k: cfg[k] for k, _ in StackConfig._fields_})
+        keep = []
+        arr = (LayerWeights * len(layers))()
+        for i, L in enumerate(layers):
+            for name in ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown"):
+                a = np.ascontiguousarray(L[name])
+                keep.append(a)
+                setattr(arr[i], name, a.ctypes.data)
+            for name in ("input_norm", "post_norm", "q_norm", "k_norm"):
+                a = _f32(L[name])
+                keep.append(a)
+                setattr(arr[i], name, a.ctypes.data)
+        fn = _f32(final_norm)
+        w = Weights(src_dtype, arr, fn.ctypes.data)
+        h = _P()
+        _check(lib().q3h_stack_create(dev.h, ctypes.byref(c), ctypes.byref(w), ctypes.byref(h)))
+        self.h = h
+        self.head_rows = []
+
+    def add_head(self, w, src_dtype):
+        a = np.ascontiguousarray(w)
+        rows = a.shape[0]
+        idx = ctypes.c_int()
+        _check(lib().q3h_stack_add_head(self.h, a.ctypes.data_as(_P), rows, src_dtype,
+                                        ctypes.byref(idx)))
+        self.head_rows.append(rows)
+        return idx.value
+
+    @property
+    def bytes(self):
+        return lib().q3h_stack_bytes(self.h)
+
+    def destroy(self):
+        if self.h:
+            _check(lib().q3h_stack_destroy(self.h))
+            self.h = None
+
+
+class Context:
+    """A K/V cache of a stack (NewContext / TDecoderContext)."""
+
+    def __init__(self, stack, max_positions):
+        h = _P()
+        _check(lib().q3h_context_create(stack.h, max_positions, ctypes.byref(h)))
+        self.h = h
+        self.stack = stack
+
+    def reset(self):
+        _check(lib().q3h_context_reset(self.h))
+
+    @property
+    def length(self):
+        n = lib().q3h_context_length(self.h)
+        if n < 0:
+            _check(n)
+        return n
+
+    def forward(self, x, head=-1, want_logits=True, want_normed=True):
+        """x [rows][hidden]; returns (logits or None, normed_last or None)."""
+        x = _f32(x)
+        if x.ndim == 1:
+            x = x[None, :]
+        rows, hidden = x.shape
+        logits = None
+        if head >= 0 and want_logits:
+            logits = np.empty(self.stack.head_rows[head], dtype=np.float32)
+        normed = np.empty(hidden, dtype=np.float32) if want_normed else None
+        _check(lib().q3h_forward_embeds(self.h, _fp(x), rows, head, _fp(logits), _fp(normed)))
+        return logits, normed
+
+    def fill_kv(self, k, v):
+        """k, v: float32 [layers][kv_heads][len][head_dim]."""
+        k, v = _f32(k), _f32(v)
+        _check(lib().q3h_context_fill_kv(self.h, _fp(k), _fp(v), k.shape[2]))
+
+    def read_kv(self, layer):
+        c = self.stack.cfg
+        n = self.length
+        k = np.empty((c["kv_heads"], n, c["head_dim"]), dtype=np.float32)
+        v = np.empty_like(k)
+        _check(lib().q3h_context_read_kv(self.h, layer, _fp(k), _fp(v)))
+        return k, v
+
+    def destroy(self):
+        if self.h:
+            _check(lib().q3h_context_destroy(self.h))
+            self.h = None
+
+
+def forward_batch(ctxs, x, heads=None, want_normed=True):
+    """One row per context: x [n][hidden]; heads: list of head indices or None."""
+    x = _f32(x)
+    n, hidden = x.shape
+    arr = (_P * n)(*[c.h.value for c in ctxs])
+    logits = None
+    hp = None
+    if heads is not None:
+        ha = np.ascontiguousarray(heads, dtype=np.int32)
+        hp = ha.ctypes.data_as(_IP)
+        logits = np.empty((n, ctxs[0].stack.head_rows[heads[0]]), dtype=np.float32)
+    normed = np.empty((n, hidden), dtype=np.float32) if want_normed else None
+    _check(lib().q3h_forward_embeds_batch(arr, n, _fp(x), hp, _fp(logits), _fp(normed)))
+    return logits, normed
+
+
+class QwenLm:
+    """TQwenLm (lm.pas:104-143): one stack, its heads, one context.
+
+    forward(x, rows, output) follows TQwenLm.Forward (lm.pas:391-408): the rows
+    are appended at positions length..length+rows-1, the normed state of the
+    last row and the logits of head `output` come back."""
+
+    def __init__(self, stack, max_positions):
+        self.stack = stack
+        self.ctx = Context(stack, max_positions)
+        self.length = 0
+
+    def reset(self):
+        self.ctx.reset()
+        self.length = 0
+
+    def forward(self, x, output=-1):
+        x = _f32(x)
+        rows = 1 if x.ndim == 1 else x.shape[0]
+        if rows <= 0:
+            return None, None
+        logits, hidden = self.ctx.forward(x, output)
+        self.length += rows
+        return logits, hidden
+
+    def destroy(self):
+        self.ctx.destroy()
+
+
+class Frame:
+    """The device-resident frame step over n streams (q3h_frame_*)."""
+
+    def __init__(self, talker, cp, codec_emb, pred_emb, tts_pad, n_streams=1, talker_head=0,
+                 cp_heads=None, eos=-1, penalty=1.05, max_frames=256, max_positions=1024,
+                 use_graph=True, groups=16):
+        vocab, hidden = codec_emb.shape
+        cp_vocab = pred_emb[0].shape[0]
+        cfg = FrameConfig()
+        cfg.n_streams = n_streams
+        cfg.talker_head = talker_head
+        heads = list(cp_heads) if cp_heads is not None else list(range(groups - 1))
+        for i in range(15):
+            cfg.cp_heads[i] = heads[i] if i < len(heads) else 0
+        cfg.vocab = vocab
+        cfg.cp_vocab = cp_vocab
+        cfg.groups = groups
+        cfg.eos = eos
+        cfg.repetition_penalty = penalty
+        cfg.max_frames = max_frames
+        cfg.max_positions = max_positions
+        cfg.use_graph = 1 if use_graph else 0
+        self.cfg = cfg
+        ce = _f32(codec_emb)
+        pe = [_f32(p) for p in pred_emb]
+        pa = (_FP * len(pe))(*[_fp(p) for p in pe])
+        tp = _f32(tts_pad)
+        h = _P()
+        _check(lib().q3h_frame_create(talker.h, cp.h, ctypes.byref(cfg), _fp(ce), pa, _fp(tp),
+                                      ctypes.byref(h)))
+        self.h = h
+        self.n = n_streams
+        self.groups = groups
+        self.vocab = vocab
+        self.hidden = hidden
+
+    def start(self, stream, prefill, trailing=None):
+        p = _f32(prefill)
+        t = _f32(trailing) if trailing is not None and len(trailing) else None
+        _check(lib().q3h_frame_start(self.h, stream, _fp(p), p.shape[0], _fp(t),
+                                     0 if t is None else t.shape[0]))
+
+    def step(self):
+        codes = np.empty((self.n, self.groups), dtype=np.int32)
+        alive = np.empty(self.n, dtype=np.int32)
+        _check(lib().q3h_frame_step(self.h, codes.ctypes.data_as(_IP),
+                                    alive.ctypes.data_as(_IP)))
+        return codes, alive
+
+    def state(self, stream):
+        logits = np.empty(self.vocab, dtype=np.float32)
+        past = np.empty(self.hidden, dtype=np.float32)
+        _check(lib().q3h_frame_state(self.h, stream, _fp(logits), _fp(past)))
+        return logits, past
+
+    def destroy(self):
+        if self.h:
+            _check(lib().q3h_frame_destroy(self.h))
+            self.h = None

@@ -1,0 +1,112 @@
+"""Seeded synthetic inputs of the Qwen3-TTS frame step.
+
+Weights and embeddings are N(0, std) float32 from numpy's PCG64 with one
+stream per tensor: SeedSequence([seed, crc32(name)]), so any tensor can be
+regenerated alone. Norm weights are 1 by default (the benchmark
+configurations); tests may ask for 1 + N(0, norm_std) to exercise them.
+Model dimensions follow tests/data/infer-ref/qwen3-tts-lm/manifest.json
+("stacks") of the reference: hidden 1024, 16 / 8 heads of 128, FFN 3072,
+eps 1e-6, RoPE theta 1e6; talker 28 layers and 3072 codes, code predictor 5
+layers and 15 heads of 2048 codes.
+"""
+import zlib
+
+import numpy as np
+
+TALKER = dict(layers=28, hidden=1024, heads=16, kv_heads=8, head_dim=128, intermediate=3072,
+              rms_eps=1e-6, rope_theta=1e6)
+PREDICTOR = dict(TALKER, layers=5)
+VOCAB = 3072
+CP_VOCAB = 2048
+GROUPS = 16
+
+
+def normal(seed, name, shape, std=0.02):
+    rng = np.random.Generator(np.random.PCG64(np.random.SeedSequence(
+        [int(seed) & 0xFFFFFFFF, zlib.crc32(name.encode())])))
+    a = rng.standard_normal(size=shape, dtype=np.float32)
+    if std != 1.0:
+        a *= np.float32(std)
+    return a
+
+
+def norm_vector(seed, name, n, norm_std):
+    if norm_std == 0:
+        return np.ones(n, dtype=np.float32)
+    return (1.0 + normal(seed, name, (n,), norm_std)).astype(np.float32)
+
+
+def layer_weights(seed, prefix, dims, l, std=0.02, norm_std=0.0):
+    """f32 weights of layer l: matrices [out][in] and norm vectors."""
+    H, hd = dims["hidden"], dims["head_dim"]
+    NQ, NKV, I = dims["heads"] * hd, dims["kv_heads"] * hd, dims["intermediate"]
+    p = f"{prefix}layers.{l}."
+    return {
+        "wq": normal(seed, p + "self_attn.q_proj.weight", (NQ, H), std),
+        "wk": normal(seed, p + "self_attn.k_proj.weight", (NKV, H), std),
+        "wv": normal(seed, p + "self_attn.v_proj.weight", (NKV, H), std),
+        "wo": normal(seed, p + "self_attn.o_proj.weight", (H, NQ), std),
+        "wgate": normal(seed, p + "mlp.gate_proj.weight", (I, H), std),
+        "wup": normal(seed, p + "mlp.up_proj.weight", (I, H), std),
+        "wdown": normal(seed, p + "mlp.down_proj.weight", (H, I), std),
+        "input_norm": norm_vector(seed, p + "input_layernorm.weight", H, norm_std),
+        "post_norm": norm_vector(seed, p + "post_attention_layernorm.weight", H, norm_std),
+        "q_norm": norm_vector(seed, p + "self_attn.q_norm.weight", hd, norm_std),
+        "k_norm": norm_vector(seed, p + "self_attn.k_norm.weight", hd, norm_std),
+    }
+
+
+MATRICES = ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown")
+
+
+def stack_weights(seed, prefix, dims, std=0.02, norm_std=0.0, quantize=None):
+    """(layers, final_norm); quantize: None (f32) or a function f32 -> Q8_0
+    blocks applied to each matrix as it is generated (keeps the peak memory
+    at one f32 matrix)."""
+    layers = []
+    for l in range(dims["layers"]):
+        L = layer_weights(seed, prefix, dims, l, std, norm_std)
+        if quantize is not None:
+            for k in MATRICES:
+                L[k] = quantize(L[k])
+        layers.append(L)
+    final = norm_vector(seed, prefix + "norm.weight", dims["hidden"], norm_std)
+    return layers, final
+
+
+def talker_head(seed, std=0.02):
+    return normal(seed, "talker.codec_head.weight", (VOCAB, TALKER["hidden"]), std)
+
+
+def cp_head(seed, g, std=0.02):
+    return normal(seed, f"talker.code_predictor.lm_head.{g}.weight",
+                  (CP_VOCAB, TALKER["hidden"]), std)
+
+
+def codec_embedding(seed, std=0.02):
+    return normal(seed, "talker.model.codec_embedding.weight", (VOCAB, TALKER["hidden"]), std)
+
+
+def pred_embedding(seed, g, std=0.02):
+    return normal(seed, f"talker.code_predictor.model.codec_embedding.{g}.weight",
+                  (CP_VOCAB, TALKER["hidden"]), std)
+
+
+def tts_pad(seed, std=0.02):
+    return normal(seed, "tts_pad", (TALKER["hidden"],), std)
+
+
+def prompt(seed, rows, hidden=1024, name="prompt"):
+    """fp32 N(0, 1) prompt embeddings."""
+    return normal(seed, name, (rows, hidden), 1.0)
+
+
+def lcg_rows(count, seed=12345):
+    """The pseudo-random inputs of tests/test.tts.qwen.vulkan.pas:189-199:
+    seed := seed*1664525 + 1013904223 (32-bit), x := ((seed shr 8)/2^24 - 0.5)*0.2."""
+    out = np.empty(count, dtype=np.float32)
+    s = seed & 0xFFFFFFFF
+    for i in range(count):
+        s = (s * 1664525 + 1013904223) & 0xFFFFFFFF
+        out[i] = np.float32((np.float64(s >> 8) / (1 << 24) - 0.5) * 0.2)
+    return out, s

@@ -1,0 +1,563 @@
+/* q3o.c - CPU restatement of the Qwen3-TTS frame step (the oracle).
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker of libq3h, never part of the product
+ * path. See q3o.h for what each function restates (reference file:line) and
+ * how it is pinned.
+ *
+ * Arithmetic conventions (chosen to be a clean restatement, not a copy of any
+ * GPU schedule):
+ *  - dot products: fp32 products, fp32 sums per 32-element block in 8 partial
+ *    lanes, block results accumulated in fp32 in column order;
+ *  - Q8_0 weights with f32 activations: sum_b d_b * (sum_j q_j x_j);
+ *  - Q8_0 weights with Q8_0 activations (ggml vec_dot_q8_0_q8_0):
+ *    sum_b (float)(sum_j qw_j qx_j) * (dw_b * dx_b), both scales via fp16;
+ *  - RMSNorm, softmax sums: double accumulation, results rounded to fp32;
+ *  - RoPE: inv_freq_i = (float)(1 / theta^(2i/d)), angle = (float)pos *
+ *    inv_freq_i in fp32, cos/sin of that angle in double rounded to fp32
+ *    (the HIP library builds its table the same way on the host).
+ */
+#include "q3o.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------ */
+/* threads                                                             */
+
+void q3o_set_threads(int n) {
+#ifdef _OPENMP
+  if (n > 0) omp_set_num_threads(n);
+#else
+  (void)n;
+#endif
+}
+
+int q3o_get_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+/* ------------------------------------------------------------------ */
+/* IEEE half floats, round to nearest even                             */
+
+uint16_t q3o_fp32_to_fp16(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  uint32_t sign = (x >> 16) & 0x8000u;
+  uint32_t a = x & 0x7fffffffu;
+  if (a >= 0x7f800000u) /* inf, nan */
+    return (uint16_t)(sign | 0x7c00u | (a > 0x7f800000u ? 0x200u : 0u));
+  if (a >= 0x477ff000u) /* >= 65520: rounds to inf */
+    return (uint16_t)(sign | 0x7c00u);
+  if (a < 0x38800000u) { /* below 2^-14: half subnormal or zero */
+    if (a < 0x33000000u) return (uint16_t)sign; /* below 2^-25 */
+    uint32_t e = a >> 23;
+    uint32_t m = (a & 0x7fffffu) | 0x800000u;
+    uint32_t shift = 126u - e; /* value / 2^-24 = m * 2^(e-126) */
+    uint32_t r = m >> shift;
+    uint32_t rem = m & ((1u << shift) - 1u);
+    uint32_t half = 1u << (shift - 1u);
+    if (rem > half || (rem == half && (r & 1u))) r++;
+    return (uint16_t)(sign | r);
+  }
+  uint32_t r = (a - 0x38000000u) >> 13; /* rebias 127 -> 15 */
+  uint32_t rem = a & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) r++;
+  return (uint16_t)(sign | r);
+}
+
+float q3o_fp16_to_fp32(uint16_t h) {
+  uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+  uint32_t e = (h >> 10) & 0x1fu;
+  uint32_t m = h & 0x3ffu;
+  uint32_t x;
+  if (e == 0) {
+    if (m == 0) {
+      x = sign;
+    } else { /* subnormal: m * 2^-24 */
+      float v = (float)m * 5.9604644775390625e-8f;
+      memcpy(&x, &v, 4);
+      x |= sign;
+    }
+  } else if (e == 31) {
+    x = sign | 0x7f800000u | (m << 13);
+  } else {
+    x = sign | ((e + 112u) << 23) | (m << 13);
+  }
+  float f;
+  memcpy(&f, &x, 4);
+  return f;
+}
+
+void q3o_fp32_to_fp16_row(const float *x, uint16_t *y, int64_t n) {
+  for (int64_t i = 0; i < n; i++) y[i] = q3o_fp32_to_fp16(x[i]);
+}
+
+void q3o_fp16_to_fp32_row(const uint16_t *x, float *y, int64_t n) {
+  for (int64_t i = 0; i < n; i++) y[i] = q3o_fp16_to_fp32(x[i]);
+}
+
+/* ------------------------------------------------------------------ */
+/* Q8_0: ggml quantize_row_q8_0_ref semantics                          */
+
+void q3o_quantize_row_q8_0(const float *x, void *vy, int64_t k) {
+  q3o_block_q8_0 *y = (q3o_block_q8_0 *)vy;
+  const int64_t nb = k / 32;
+  for (int64_t i = 0; i < nb; i++) {
+    const float *b = x + i * 32;
+    float amax = 0.0f;
+    for (int j = 0; j < 32; j++) {
+      const float v = fabsf(b[j]);
+      amax = amax > v ? amax : v;
+    }
+    const float d = amax / 127;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    y[i].d = q3o_fp32_to_fp16(d);
+    for (int j = 0; j < 32; j++) y[i].qs[j] = (int8_t)roundf(b[j] * id);
+  }
+}
+
+void q3o_dequantize_row_q8_0(const void *vx, float *y, int64_t k) {
+  const q3o_block_q8_0 *x = (const q3o_block_q8_0 *)vx;
+  const int64_t nb = k / 32;
+  for (int64_t i = 0; i < nb; i++) {
+    const float d = q3o_fp16_to_fp32(x[i].d);
+    for (int j = 0; j < 32; j++) y[i * 32 + j] = x[i].qs[j] * d;
+  }
+}
+
+void q3o_quantize_matrix_q8_0(const float *x, void *vy, int64_t rows, int64_t cols) {
+  q3o_block_q8_0 *y = (q3o_block_q8_0 *)vy;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; r++)
+    q3o_quantize_row_q8_0(x + r * cols, y + r * (cols / 32), cols);
+}
+
+/* ------------------------------------------------------------------ */
+/* dot products and the linear layer                                   */
+
+static inline float dot32(const float *w, const float *x) {
+  float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int j = 0; j < 32; j += 8)
+    for (int t = 0; t < 8; t++) s[t] += w[j + t] * x[j + t];
+  return ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+}
+
+static inline int32_t idot32(const int8_t *a, const int8_t *b) {
+  int32_t s = 0;
+  for (int j = 0; j < 32; j++) s += (int32_t)a[j] * (int32_t)b[j];
+  return s;
+}
+
+/* Y[m][n] (+)= W[n] . X[m]; W [N][K] f32 or Q8_0 blocks; X [M][K] */
+static void linear(const void *W, int dtype, int act_q8, int N, int K,
+                   const float *X, int M, float *Y, int ldy, int add) {
+  const int nb = K / 32;
+  q3o_block_q8_0 *xq = NULL;
+  if (dtype == Q3O_Q8_0 && act_q8) {
+    xq = (q3o_block_q8_0 *)malloc(sizeof(q3o_block_q8_0) * (size_t)nb * M);
+    for (int m = 0; m < M; m++) q3o_quantize_row_q8_0(X + (size_t)m * K, xq + (size_t)m * nb, K);
+  }
+#pragma omp parallel
+  {
+    float *wrow = (float *)malloc(sizeof(float) * K);
+    float *scale = (float *)malloc(sizeof(float) * nb);
+#pragma omp for schedule(static)
+    for (int n = 0; n < N; n++) {
+      if (dtype == Q3O_F32) {
+        const float *w = (const float *)W + (size_t)n * K;
+        for (int m = 0; m < M; m++) {
+          const float *x = X + (size_t)m * K;
+          float acc = 0.0f;
+          for (int b = 0; b < nb; b++) acc += dot32(w + b * 32, x + b * 32);
+          if (add)
+            Y[(size_t)m * ldy + n] += acc;
+          else
+            Y[(size_t)m * ldy + n] = acc;
+        }
+      } else {
+        const q3o_block_q8_0 *w = (const q3o_block_q8_0 *)W + (size_t)n * nb;
+        if (!act_q8) {
+          for (int b = 0; b < nb; b++) {
+            scale[b] = q3o_fp16_to_fp32(w[b].d);
+            for (int j = 0; j < 32; j++) wrow[b * 32 + j] = (float)w[b].qs[j];
+          }
+        }
+        for (int m = 0; m < M; m++) {
+          float acc = 0.0f;
+          if (act_q8) {
+            const q3o_block_q8_0 *x = xq + (size_t)m * nb;
+            for (int b = 0; b < nb; b++) {
+              const int32_t s = idot32(w[b].qs, x[b].qs);
+              acc += (float)s * (q3o_fp16_to_fp32(w[b].d) * q3o_fp16_to_fp32(x[b].d));
+            }
+          } else {
+            const float *x = X + (size_t)m * K;
+            for (int b = 0; b < nb; b++) acc += scale[b] * dot32(wrow + b * 32, x + b * 32);
+          }
+          if (add)
+            Y[(size_t)m * ldy + n] += acc;
+          else
+            Y[(size_t)m * ldy + n] = acc;
+        }
+      }
+    }
+    free(wrow);
+    free(scale);
+  }
+  free(xq);
+}
+
+/* ------------------------------------------------------------------ */
+/* norms, RoPE                                                         */
+
+static void rmsnorm(const float *x, const float *w, int n, float eps, float *y) {
+  double ss = 0.0;
+  for (int i = 0; i < n; i++) ss += (double)x[i] * (double)x[i];
+  const float inv = (float)(1.0 / sqrt(ss / n + (double)eps));
+  for (int i = 0; i < n; i++) y[i] = w[i] * (x[i] * inv);
+}
+
+static void rope(float *x, int d, int pos, float theta) {
+  const int half = d / 2;
+  for (int i = 0; i < half; i++) {
+    const float inv_freq = (float)(1.0 / pow((double)theta, (double)(2 * i) / (double)d));
+    const float angle = (float)pos * inv_freq;
+    const float c = (float)cos((double)angle);
+    const float s = (float)sin((double)angle);
+    const float a = x[i], b = x[i + half];
+    x[i] = a * c - b * s;
+    x[i + half] = b * c + a * s;
+  }
+}
+
+/* ------------------------------------------------------------------ */
+/* stack and context                                                   */
+
+struct q3o_stack {
+  q3o_config cfg;
+  q3o_layer *layers;
+  const float *final_norm;
+};
+
+struct q3o_ctx {
+  q3o_stack *s;
+  int len, max_pos;
+  float *k, *v; /* [layers][kv_heads][max_pos][head_dim] */
+};
+
+q3o_stack *q3o_stack_create(const q3o_config *cfg, const q3o_layer *layers,
+                            const float *final_norm) {
+  if (cfg->hidden % 32 || cfg->intermediate % 32 || (cfg->heads * cfg->head_dim) % 32 ||
+      cfg->heads % cfg->kv_heads || cfg->head_dim % 2)
+    return NULL;
+  q3o_stack *s = (q3o_stack *)calloc(1, sizeof(*s));
+  s->cfg = *cfg;
+  s->layers = (q3o_layer *)malloc(sizeof(q3o_layer) * cfg->layers);
+  memcpy(s->layers, layers, sizeof(q3o_layer) * cfg->layers);
+  s->final_norm = final_norm;
+  return s;
+}
+
+void q3o_stack_destroy(q3o_stack *s) {
+  if (!s) return;
+  free(s->layers);
+  free(s);
+}
+
+q3o_ctx *q3o_ctx_create(q3o_stack *s, int max_positions) {
+  q3o_ctx *c = (q3o_ctx *)calloc(1, sizeof(*c));
+  c->s = s;
+  c->max_pos = max_positions;
+  size_t n = (size_t)s->cfg.layers * s->cfg.kv_heads * max_positions * s->cfg.head_dim;
+  c->k = (float *)calloc(n, sizeof(float));
+  c->v = (float *)calloc(n, sizeof(float));
+  return c;
+}
+
+void q3o_ctx_destroy(q3o_ctx *c) {
+  if (!c) return;
+  free(c->k);
+  free(c->v);
+  free(c);
+}
+
+void q3o_ctx_reset(q3o_ctx *c) { c->len = 0; }
+
+int q3o_ctx_length(const q3o_ctx *c) { return c->len; }
+
+static size_t kv_off(const q3o_ctx *c, int layer, int g, int pos) {
+  const q3o_config *q = &c->s->cfg;
+  return (((size_t)layer * q->kv_heads + g) * c->max_pos + pos) * q->head_dim;
+}
+
+const float *q3o_ctx_k(const q3o_ctx *c, int layer) { return c->k + kv_off(c, layer, 0, 0); }
+const float *q3o_ctx_v(const q3o_ctx *c, int layer) { return c->v + kv_off(c, layer, 0, 0); }
+
+static inline float kv_round(const q3o_config *q, float v) {
+  return q->kv_f16 ? q3o_fp16_to_fp32(q3o_fp32_to_fp16(v)) : v;
+}
+
+int q3o_ctx_fill(q3o_ctx *c, const float *k, const float *v, int len) {
+  const q3o_config *q = &c->s->cfg;
+  if (len > c->max_pos || len < 0) return -1;
+  for (int l = 0; l < q->layers; l++)
+    for (int g = 0; g < q->kv_heads; g++)
+      for (int p = 0; p < len; p++)
+        for (int d = 0; d < q->head_dim; d++) {
+          size_t src = (((size_t)l * q->kv_heads + g) * len + p) * q->head_dim + d;
+          c->k[kv_off(c, l, g, p) + d] = kv_round(q, k[src]);
+          c->v[kv_off(c, l, g, p) + d] = kv_round(q, v[src]);
+        }
+  c->len = len;
+  return 0;
+}
+
+int q3o_forward_embeds(q3o_ctx *c, const float *x, int rows, float *normed_last,
+                       float *layer_out) {
+  const q3o_config *q = &c->s->cfg;
+  if (rows <= 0) return 0;
+  if (c->len + rows > c->max_pos) return -1;
+  const int H = q->hidden, D = q->head_dim, NQ = q->heads * D, NKV = q->kv_heads * D;
+  const int I = q->intermediate, grp = q->heads / q->kv_heads;
+  const float scale = (float)(1.0 / sqrt((double)D));
+  float *h = (float *)malloc(sizeof(float) * rows * H);
+  float *xn = (float *)malloc(sizeof(float) * rows * H);
+  float *qb = (float *)malloc(sizeof(float) * rows * NQ);
+  float *kb = (float *)malloc(sizeof(float) * rows * NKV);
+  float *vb = (float *)malloc(sizeof(float) * rows * NKV);
+  float *att = (float *)malloc(sizeof(float) * rows * NQ);
+  float *gb = (float *)malloc(sizeof(float) * rows * I);
+  float *ub = (float *)malloc(sizeof(float) * rows * I);
+  memcpy(h, x, sizeof(float) * rows * H);
+  for (int l = 0; l < q->layers; l++) {
+    const q3o_layer *L = &c->s->layers[l];
+    for (int r = 0; r < rows; r++) rmsnorm(h + r * H, L->input_norm, H, q->rms_eps, xn + r * H);
+    linear(L->wq, q->dtype, q->act_q8, NQ, H, xn, rows, qb, NQ, 0);
+    linear(L->wk, q->dtype, q->act_q8, NKV, H, xn, rows, kb, NKV, 0);
+    linear(L->wv, q->dtype, q->act_q8, NKV, H, xn, rows, vb, NKV, 0);
+    for (int r = 0; r < rows; r++) {
+      const int pos = c->len + r;
+      for (int hh = 0; hh < q->heads; hh++) {
+        float *qh = qb + r * NQ + hh * D;
+        rmsnorm(qh, L->q_norm, D, q->rms_eps, qh);
+        rope(qh, D, pos, q->rope_theta);
+      }
+      for (int g = 0; g < q->kv_heads; g++) {
+        float *kh = kb + r * NKV + g * D;
+        const float *vh = vb + r * NKV + g * D;
+        rmsnorm(kh, L->k_norm, D, q->rms_eps, kh);
+        rope(kh, D, pos, q->rope_theta);
+        float *kc = c->k + kv_off(c, l, g, pos), *vc = c->v + kv_off(c, l, g, pos);
+        for (int d = 0; d < D; d++) {
+          kc[d] = kv_round(q, kh[d]);
+          vc[d] = kv_round(q, vh[d]);
+        }
+      }
+    }
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int r = 0; r < rows; r++) {
+      for (int hh = 0; hh < q->heads; hh++) {
+        const int n = c->len + r + 1, g = hh / grp;
+        const float *qh = qb + r * NQ + hh * D;
+        float *sc = (float *)malloc(sizeof(float) * n);
+        float mx = -INFINITY;
+        for (int p = 0; p < n; p++) {
+          const float *kc = c->k + kv_off(c, l, g, p);
+          float acc = 0.0f;
+          for (int b = 0; b < D; b += 32) acc += dot32(qh + b, kc + b);
+          sc[p] = acc * scale;
+          mx = sc[p] > mx ? sc[p] : mx;
+        }
+        double sum = 0.0;
+        for (int p = 0; p < n; p++) {
+          sc[p] = expf(sc[p] - mx);
+          sum += sc[p];
+        }
+        const float inv = (float)(1.0 / sum);
+        float *o = att + r * NQ + hh * D;
+        for (int d = 0; d < D; d++) o[d] = 0.0f;
+        for (int p = 0; p < n; p++) {
+          const float *vc = c->v + kv_off(c, l, g, p);
+          const float w = sc[p] * inv;
+          for (int d = 0; d < D; d++) o[d] += w * vc[d];
+        }
+        free(sc);
+      }
+    }
+    linear(L->wo, q->dtype, q->act_q8, H, NQ, att, rows, h, H, 1);
+    for (int r = 0; r < rows; r++) rmsnorm(h + r * H, L->post_norm, H, q->rms_eps, xn + r * H);
+    linear(L->wgate, q->dtype, q->act_q8, I, H, xn, rows, gb, I, 0);
+    linear(L->wup, q->dtype, q->act_q8, I, H, xn, rows, ub, I, 0);
+    for (int i = 0; i < rows * I; i++) {
+      const float g = gb[i];
+      gb[i] = g / (1.0f + expf(-g)) * ub[i];
+    }
+    linear(L->wdown, q->dtype, q->act_q8, H, I, gb, rows, h, H, 1);
+    if (layer_out) memcpy(layer_out + (size_t)l * rows * H, h, sizeof(float) * rows * H);
+  }
+  if (normed_last) rmsnorm(h + (size_t)(rows - 1) * H, c->s->final_norm, H, q->rms_eps, normed_last);
+  c->len += rows;
+  free(h);
+  free(xn);
+  free(qb);
+  free(kb);
+  free(vb);
+  free(att);
+  free(gb);
+  free(ub);
+  return 0;
+}
+
+void q3o_head(const void *w, int dtype, int act_q8, int rows_out, int hidden,
+              const float *state, float *logits) {
+  linear(w, dtype, act_q8, rows_out, hidden, state, 1, logits, rows_out, 0);
+}
+
+/* ------------------------------------------------------------------ */
+/* code choice (greedy)                                                */
+
+int q3o_argmax(const float *p, int n) {
+  int r = 0;
+  for (int i = 1; i < n; i++)
+    if (p[i] > p[r]) r = i;
+  return r;
+}
+
+int q3o_choose_code0(const float *logits, int vocab, int eos, const int *history,
+                     int nhistory, float penalty) {
+  float *work = (float *)malloc(sizeof(float) * vocab);
+  memcpy(work, logits, sizeof(float) * vocab);
+  for (int i = vocab - 1024; i < vocab; i++)
+    if (i != eos) work[i] = -INFINITY;
+  if (nhistory < 2 && eos >= 0 && eos < vocab) work[eos] = -INFINITY;
+  if (penalty != 1.0f)
+    for (int j = 0; j < nhistory; j++) {
+      const int i = history[j];
+      const float s = logits[i];
+      if (work[i] != s) continue; /* already penalized (or forbidden) */
+      work[i] = s > 0 ? s / penalty : s * penalty;
+    }
+  const int r = q3o_argmax(work, vocab);
+  free(work);
+  return r;
+}
+
+/* ------------------------------------------------------------------ */
+/* frame step                                                          */
+
+struct q3o_frame {
+  q3o_stack *talker, *cp;
+  q3o_frame_tables t;
+  q3o_ctx *tctx, *cctx;
+  float *logits, *past, *x, *plogits, *trailing;
+  int *history;
+  int nhist, cap_hist, trailing_rows, step;
+};
+
+q3o_frame *q3o_frame_create(q3o_stack *talker, q3o_stack *cp,
+                            const q3o_frame_tables *t, int max_positions) {
+  q3o_frame *f = (q3o_frame *)calloc(1, sizeof(*f));
+  const int H = talker->cfg.hidden;
+  f->talker = talker;
+  f->cp = cp;
+  f->t = *t;
+  f->tctx = q3o_ctx_create(talker, max_positions);
+  f->cctx = q3o_ctx_create(cp, t->groups);
+  f->logits = (float *)calloc(t->vocab, sizeof(float));
+  f->plogits = (float *)calloc(t->cp_vocab, sizeof(float));
+  f->past = (float *)calloc(H, sizeof(float));
+  f->x = (float *)calloc(2 * H, sizeof(float));
+  f->cap_hist = 64;
+  f->history = (int *)malloc(sizeof(int) * f->cap_hist);
+  return f;
+}
+
+void q3o_frame_destroy(q3o_frame *f) {
+  if (!f) return;
+  q3o_ctx_destroy(f->tctx);
+  q3o_ctx_destroy(f->cctx);
+  free(f->logits);
+  free(f->plogits);
+  free(f->past);
+  free(f->x);
+  free(f->history);
+  free(f->trailing);
+  free(f);
+}
+
+int q3o_frame_start(q3o_frame *f, const float *prefill, int rows,
+                    const float *trailing, int trailing_rows) {
+  const int H = f->talker->cfg.hidden;
+  free(f->trailing);
+  f->trailing = NULL;
+  f->trailing_rows = trailing_rows > 0 ? trailing_rows : 0;
+  if (f->trailing_rows) {
+    f->trailing = (float *)malloc(sizeof(float) * f->trailing_rows * H);
+    memcpy(f->trailing, trailing, sizeof(float) * f->trailing_rows * H);
+  }
+  q3o_ctx_reset(f->tctx);
+  if (q3o_forward_embeds(f->tctx, prefill, rows, f->past, NULL)) return -1;
+  q3o_head(f->t.talker_head, f->talker->cfg.dtype, f->talker->cfg.act_q8, f->t.vocab, H,
+           f->past, f->logits);
+  f->nhist = 0;
+  f->step = 0;
+  return 0;
+}
+
+static void add_row(const float *emb, int id, int H, float *y) {
+  for (int c = 0; c < H; c++) y[c] = y[c] + emb[(size_t)id * H + c];
+}
+
+int q3o_frame_next(q3o_frame *f, int *codes) {
+  const int H = f->talker->cfg.hidden;
+  const q3o_frame_tables *t = &f->t;
+  const int code = q3o_choose_code0(f->logits, t->vocab, t->eos, f->history, f->nhist, t->penalty);
+  if (code == t->eos) return 0;
+  codes[0] = code;
+  if (f->nhist == f->cap_hist) {
+    f->cap_hist *= 2;
+    f->history = (int *)realloc(f->history, sizeof(int) * f->cap_hist);
+  }
+  f->history[f->nhist++] = code;
+  /* the code predictor: [talker state, embedding of code 0], then each code */
+  memcpy(f->x, f->past, sizeof(float) * H);
+  memcpy(f->x + H, t->codec_emb + (size_t)code * H, sizeof(float) * H);
+  q3o_ctx_reset(f->cctx);
+  float *normed = (float *)malloc(sizeof(float) * H);
+  const int cdt = f->cp->cfg.dtype, caq = f->cp->cfg.act_q8;
+  for (int g = 0; g < t->groups - 1; g++) {
+    if (g == 0) {
+      q3o_forward_embeds(f->cctx, f->x, 2, normed, NULL);
+    } else {
+      memcpy(f->x, t->pred_emb[g - 1] + (size_t)codes[g] * H, sizeof(float) * H);
+      q3o_forward_embeds(f->cctx, f->x, 1, normed, NULL);
+    }
+    q3o_head(t->cp_heads[g], cdt, caq, t->cp_vocab, H, normed, f->plogits);
+    codes[g + 1] = q3o_argmax(f->plogits, t->cp_vocab);
+  }
+  free(normed);
+  /* the next talker input: the 16 embeddings, plus the text (or tts_pad) */
+  memcpy(f->x, t->codec_emb + (size_t)code * H, sizeof(float) * H);
+  for (int g = 1; g < t->groups; g++) add_row(t->pred_emb[g - 1], codes[g], H, f->x);
+  if (f->step < f->trailing_rows)
+    add_row(f->trailing, f->step, H, f->x);
+  else
+    add_row(t->tts_pad, 0, H, f->x);
+  if (q3o_forward_embeds(f->tctx, f->x, 1, f->past, NULL)) return -1;
+  q3o_head(t->talker_head, f->talker->cfg.dtype, f->talker->cfg.act_q8, t->vocab, H, f->past,
+           f->logits);
+  f->step++;
+  return 1;
+}
+
+const float *q3o_frame_logits(const q3o_frame *f) { return f->logits; }
+const float *q3o_frame_past_hidden(const q3o_frame *f) { return f->past; }
+q3o_ctx *q3o_frame_talker_ctx(q3o_frame *f) { return f->tctx; }

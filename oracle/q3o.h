@@ -1,0 +1,148 @@
+/* q3o.h - CPU restatement of the Qwen3-TTS frame step (the oracle).
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker of the HIP library
+ * (libq3h): only tests/, __graft_entry__.smoke() and the cpu_baseline leg of
+ * bench.py may load it. The product path never links or calls it.
+ *
+ * What it restates (reference files, relative to the reference checkout):
+ *  - Q8_0 block format and quantizer: ggml block_q8_0 / quantize_row_q8_0_ref,
+ *    named at src/tts/mormot.ai.tts.qwen.lm.pas:259-267 (TQwenLmHeads.MatrixRows)
+ *    and sized at lm.pas:182-197 (StackBytes).
+ *  - the Qwen3 stack fed with embedding rows (TDecoderModel.ForwardEmbeds,
+ *    called at lm.pas:391-408; the layer math follows the model note of
+ *    tests/data/infer-ref/qwen3-tts-lm/manifest.json: per-head q_norm/k_norm,
+ *    SwiGLU, no bias, rotate_half RoPE theta 1e6, RMSNorm eps 1e-6).
+ *  - TQwenLm.Forward (lm.pas:391-408): the normed last row and its head.
+ *  - TQwenTalker.ChooseCode0 / ChooseCode / AddRow / NextFrame
+ *    (src/tts/mormot.ai.tts.qwen.talker.pas:423-429, 595-681) in greedy mode.
+ *  - InferArgMax with the first-max rule of tests/test.tts.qwen.lm.pas:109-117.
+ *
+ * How each part is pinned (tests/test_oracle_*.py):
+ *  - fp16 conversion: against numpy float16 (round to nearest even) on every
+ *    finite half value and random floats, subnormals and overflow included;
+ *  - Q8_0 quantizer: closed forms (zeros, the amax element is +-127, halfway
+ *    rounding away from zero), brute force against an independent numpy
+ *    restatement, dequantization error <= d/2;
+ *  - f32 stack: golden vectors from the third-party transformers Qwen3Model
+ *    (tests/golden/make_qwen3_golden.py), incremental calls == one call
+ *    (the causal property the reference fixture states for predictor.logits);
+ *  - argmax / ChooseCode0: the reference fixture's logits rows and codes
+ *    (tests/data/infer-ref/qwen3-tts-lm: predictor.codes = argmax of each row)
+ *    plus brute-force checks of the logits processors on tiny vectors.
+ *  - Q8_0 stack numerics (activation quantization or not) of the un-vendored
+ *    mormot2-ai engine: parity unpinned (both modes are provided).
+ */
+#ifndef Q3O_H
+#define Q3O_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q3O_F32 0
+#define Q3O_Q8_0 1
+
+/* ggml block_q8_0: fp16 scale then 32 int8 quants, 34 bytes */
+typedef struct {
+  uint16_t d;
+  int8_t qs[32];
+} q3o_block_q8_0;
+
+typedef struct {
+  int32_t layers, hidden, heads, kv_heads, head_dim, intermediate;
+  float rms_eps, rope_theta;
+  int32_t dtype;  /* Q3O_F32 or Q3O_Q8_0 (weights and heads) */
+  int32_t kv_f16; /* K/V cache rounded to half floats */
+  int32_t act_q8; /* Q8_0 only: 1 = activations quantized per 32-block
+                     (int32 block dot, ggml vec_dot_q8_0_q8_0), 0 = f32
+                     activations times dequantized weights */
+} q3o_config;
+
+/* one layer: matrices [out][in] row-major, f32 or ggml Q8_0 blocks */
+typedef struct {
+  const void *wq, *wk, *wv, *wo, *wgate, *wup, *wdown;
+  const float *input_norm, *post_norm, *q_norm, *k_norm;
+} q3o_layer;
+
+typedef struct q3o_stack q3o_stack;
+typedef struct q3o_ctx q3o_ctx;
+typedef struct q3o_frame q3o_frame;
+
+void q3o_set_threads(int n);
+int q3o_get_threads(void);
+
+uint16_t q3o_fp32_to_fp16(float f);
+float q3o_fp16_to_fp32(uint16_t h);
+void q3o_fp32_to_fp16_row(const float *x, uint16_t *y, int64_t n);
+void q3o_fp16_to_fp32_row(const uint16_t *x, float *y, int64_t n);
+
+/* k % 32 == 0 */
+void q3o_quantize_row_q8_0(const float *x, void *y, int64_t k);
+void q3o_dequantize_row_q8_0(const void *x, float *y, int64_t k);
+/* rows x cols matrix, rows in parallel (the bytes do not depend on threads) */
+void q3o_quantize_matrix_q8_0(const float *x, void *y, int64_t rows, int64_t cols);
+
+/* the stack keeps the pointers (no copy): they must outlive it */
+q3o_stack *q3o_stack_create(const q3o_config *cfg, const q3o_layer *layers,
+                            const float *final_norm);
+void q3o_stack_destroy(q3o_stack *s);
+
+q3o_ctx *q3o_ctx_create(q3o_stack *s, int max_positions);
+void q3o_ctx_destroy(q3o_ctx *c);
+void q3o_ctx_reset(q3o_ctx *c);
+int q3o_ctx_length(const q3o_ctx *c);
+/* raw K/V rows of one layer: [kv_heads][max_positions][head_dim] f32 */
+const float *q3o_ctx_k(const q3o_ctx *c, int layer);
+const float *q3o_ctx_v(const q3o_ctx *c, int layer);
+/* write K/V of positions [0, len) directly (long-context setups);
+   k, v: [layers][kv_heads][len][head_dim]; sets the length */
+int q3o_ctx_fill(q3o_ctx *c, const float *k, const float *v, int len);
+
+/* x [rows][hidden] at positions length..length+rows-1; normed_last [hidden]
+   (nullable); layer_out [layers][rows][hidden] raw layer outputs (nullable);
+   returns 0, or -1 when the context would overflow */
+int q3o_forward_embeds(q3o_ctx *c, const float *x, int rows, float *normed_last,
+                       float *layer_out);
+
+/* logits[rows_out] = W[rows_out][hidden] . state, W f32 or Q8_0 */
+void q3o_head(const void *w, int dtype, int act_q8, int rows_out, int hidden,
+              const float *state, float *logits);
+
+/* first max wins */
+int q3o_argmax(const float *p, int n);
+
+/* TQwenTalker.ChooseCode0, greedy: logits processors then argmax */
+int q3o_choose_code0(const float *logits, int vocab, int eos, const int *history,
+                     int nhistory, float penalty);
+
+/* frame step: the talker and code-predictor stacks, their heads, the tables */
+typedef struct {
+  const void *talker_head; /* [vocab][hidden] */
+  const void *cp_heads[15]; /* [cp_vocab][hidden] */
+  const float *codec_emb;  /* [vocab][hidden] */
+  const float *pred_emb[15]; /* [cp_vocab][hidden] */
+  int32_t vocab, cp_vocab, groups;
+  int32_t eos; /* -1: none */
+  float penalty;
+  const float *tts_pad; /* [hidden] */
+} q3o_frame_tables;
+
+q3o_frame *q3o_frame_create(q3o_stack *talker, q3o_stack *cp,
+                            const q3o_frame_tables *t, int max_positions);
+void q3o_frame_destroy(q3o_frame *f);
+/* TQwenTalker.Start's talker part: reset, prefill rows, logits + past state;
+   trailing [trailing_rows][hidden] is copied */
+int q3o_frame_start(q3o_frame *f, const float *prefill, int rows,
+                    const float *trailing, int trailing_rows);
+/* TQwenTalker.NextFrame: 1 and codes[groups], or 0 at eos */
+int q3o_frame_next(q3o_frame *f, int *codes);
+const float *q3o_frame_logits(const q3o_frame *f);
+const float *q3o_frame_past_hidden(const q3o_frame *f);
+q3o_ctx *q3o_frame_talker_ctx(q3o_frame *f);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

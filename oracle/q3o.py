@@ -1,0 +1,273 @@
+"""ctypes binding of the oracle (oracle/q3o.c).
+
+TEST INFRASTRUCTURE ONLY: loaded by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker; never by the product path.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "build", "libq3o.so")
+
+F32 = 0
+Q8_0 = 1
+
+_P = ctypes.c_void_p
+_FP = ctypes.POINTER(ctypes.c_float)
+_IP = ctypes.POINTER(ctypes.c_int)
+
+
+class Config(ctypes.Structure):
+    _fields_ = [
+        ("layers", ctypes.c_int32), ("hidden", ctypes.c_int32), ("heads", ctypes.c_int32),
+        ("kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("intermediate", ctypes.c_int32), ("rms_eps", ctypes.c_float),
+        ("rope_theta", ctypes.c_float), ("dtype", ctypes.c_int32), ("kv_f16", ctypes.c_int32),
+        ("act_q8", ctypes.c_int32),
+    ]
+
+
+class Layer(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in
+                ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown",
+                 "input_norm", "post_norm", "q_norm", "k_norm")]
+
+
+class FrameTables(ctypes.Structure):
+    _fields_ = [
+        ("talker_head", ctypes.c_void_p), ("cp_heads", ctypes.c_void_p * 15),
+        ("codec_emb", ctypes.c_void_p), ("pred_emb", ctypes.c_void_p * 15),
+        ("vocab", ctypes.c_int32), ("cp_vocab", ctypes.c_int32), ("groups", ctypes.c_int32),
+        ("eos", ctypes.c_int32), ("penalty", ctypes.c_float), ("tts_pad", ctypes.c_void_p),
+    ]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        L = ctypes.CDLL(LIB_PATH)
+        sig = {
+            "q3o_set_threads": (None, [ctypes.c_int]),
+            "q3o_get_threads": (ctypes.c_int, []),
+            "q3o_fp32_to_fp16": (ctypes.c_uint16, [ctypes.c_float]),
+            "q3o_fp16_to_fp32": (ctypes.c_float, [ctypes.c_uint16]),
+            "q3o_fp32_to_fp16_row": (None, [_FP, _P, ctypes.c_int64]),
+            "q3o_fp16_to_fp32_row": (None, [_P, _FP, ctypes.c_int64]),
+            "q3o_quantize_row_q8_0": (None, [_FP, _P, ctypes.c_int64]),
+            "q3o_dequantize_row_q8_0": (None, [_P, _FP, ctypes.c_int64]),
+            "q3o_quantize_matrix_q8_0": (None, [_FP, _P, ctypes.c_int64, ctypes.c_int64]),
+            "q3o_stack_create": (_P, [ctypes.POINTER(Config), ctypes.POINTER(Layer), _FP]),
+            "q3o_stack_destroy": (None, [_P]),
+            "q3o_ctx_create": (_P, [_P, ctypes.c_int]),
+            "q3o_ctx_destroy": (None, [_P]),
+            "q3o_ctx_reset": (None, [_P]),
+            "q3o_ctx_length": (ctypes.c_int, [_P]),
+            "q3o_ctx_k": (_FP, [_P, ctypes.c_int]),
+            "q3o_ctx_v": (_FP, [_P, ctypes.c_int]),
+            "q3o_ctx_fill": (ctypes.c_int, [_P, _FP, _FP, ctypes.c_int]),
+            "q3o_forward_embeds": (ctypes.c_int, [_P, _FP, ctypes.c_int, _FP, _FP]),
+            "q3o_head": (None, [_P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _FP,
+                                _FP]),
+            "q3o_argmax": (ctypes.c_int, [_FP, ctypes.c_int]),
+            "q3o_choose_code0": (ctypes.c_int, [_FP, ctypes.c_int, ctypes.c_int, _IP,
+                                                ctypes.c_int, ctypes.c_float]),
+            "q3o_frame_create": (_P, [_P, _P, ctypes.POINTER(FrameTables), ctypes.c_int]),
+            "q3o_frame_destroy": (None, [_P]),
+            "q3o_frame_start": (ctypes.c_int, [_P, _FP, ctypes.c_int, _FP, ctypes.c_int]),
+            "q3o_frame_next": (ctypes.c_int, [_P, _IP]),
+            "q3o_frame_logits": (_FP, [_P]),
+            "q3o_frame_past_hidden": (_FP, [_P]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _fp(a):
+    return a.ctypes.data_as(_FP) if a is not None else None
+
+
+def set_threads(n):
+    lib().q3o_set_threads(int(n))
+
+
+def fp32_to_fp16(x):
+    x = _f32(x)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().q3o_fp32_to_fp16_row(_fp(x), out.ctypes.data_as(_P), x.size)
+    return out
+
+
+def fp16_to_fp32(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    lib().q3o_fp16_to_fp32_row(h.ctypes.data_as(_P), _fp(out), h.size)
+    return out
+
+
+def quantize_q8_0(x):
+    """[rows][k] float32 -> [rows][k/32*34] uint8 ggml blocks (rows in parallel)."""
+    x = _f32(x)
+    k = x.shape[-1]
+    rows = x.size // k
+    out = np.empty(x.shape[:-1] + (k // 32 * 34,), dtype=np.uint8)
+    lib().q3o_quantize_matrix_q8_0(_fp(x), out.ctypes.data_as(_P), rows, k)
+    return out
+
+
+def dequantize_q8_0(b, k):
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    rows = b.size // (k // 32 * 34)
+    out = np.empty((rows, k), dtype=np.float32)
+    for r in range(rows):
+        lib().q3o_dequantize_row_q8_0(b[r].ctypes.data_as(_P) if b.ndim > 1 else
+                                      b.ctypes.data_as(_P), _fp(out[r]), k)
+    return out if b.ndim > 1 else out[0]
+
+
+def argmax(p):
+    p = _f32(p)
+    return lib().q3o_argmax(_fp(p), p.size)
+
+
+def choose_code0(logits, eos, history, penalty):
+    lg = _f32(logits)
+    h = np.ascontiguousarray(history, dtype=np.int32)
+    return lib().q3o_choose_code0(_fp(lg), lg.size, eos, h.ctypes.data_as(_IP), h.size,
+                                  ctypes.c_float(penalty))
+
+
+class Stack:
+    def __init__(self, dims, layers, final_norm, dtype, kv_f16=0, act_q8=0):
+        self.dims = dict(dims)
+        self.dtype = dtype
+        self.act_q8 = act_q8
+        self.cfg = Config(dims["layers"], dims["hidden"], dims["heads"], dims["kv_heads"],
+                          dims["head_dim"], dims["intermediate"], dims["rms_eps"],
+                          dims["rope_theta"], dtype, kv_f16, act_q8)
+        self._keep = []
+        arr = (Layer * len(layers))()
+        for i, L in enumerate(layers):
+            for name in Layer._fields_:
+                n = name[0]
+                a = np.ascontiguousarray(L[n]) if n.startswith("w") else _f32(L[n])
+                self._keep.append(a)
+                setattr(arr[i], n, a.ctypes.data)
+        self._arr = arr
+        self._final = _f32(final_norm)
+        self.h = lib().q3o_stack_create(ctypes.byref(self.cfg), arr, _fp(self._final))
+        if not self.h:
+            raise ValueError("q3o_stack_create: invalid dimensions")
+
+    def head(self, w, state):
+        w = np.ascontiguousarray(w)
+        rows = w.shape[0]
+        out = np.empty(rows, dtype=np.float32)
+        st = _f32(state)
+        lib().q3o_head(w.ctypes.data_as(_P), self.dtype, self.act_q8, rows, self.dims["hidden"],
+                       _fp(st), _fp(out))
+        return out
+
+    def destroy(self):
+        if self.h:
+            lib().q3o_stack_destroy(self.h)
+            self.h = None
+
+
+class Ctx:
+    def __init__(self, stack, max_positions):
+        self.stack = stack
+        self.h = lib().q3o_ctx_create(stack.h, max_positions)
+
+    def reset(self):
+        lib().q3o_ctx_reset(self.h)
+
+    @property
+    def length(self):
+        return lib().q3o_ctx_length(self.h)
+
+    def forward(self, x, layer_out=False):
+        x = _f32(x)
+        if x.ndim == 1:
+            x = x[None, :]
+        rows, H = x.shape
+        normed = np.empty(H, dtype=np.float32)
+        lo = np.empty((self.stack.dims["layers"], rows, H), dtype=np.float32) if layer_out \
+            else None
+        rc = lib().q3o_forward_embeds(self.h, _fp(x), rows, _fp(normed), _fp(lo))
+        if rc:
+            raise ValueError("q3o_forward_embeds: context overflow")
+        return (normed, lo) if layer_out else normed
+
+    def fill(self, k, v):
+        k, v = _f32(k), _f32(v)
+        if lib().q3o_ctx_fill(self.h, _fp(k), _fp(v), k.shape[2]):
+            raise ValueError("q3o_ctx_fill: too long")
+
+    def destroy(self):
+        if self.h:
+            lib().q3o_ctx_destroy(self.h)
+            self.h = None
+
+
+class Frame:
+    def __init__(self, talker, cp, talker_head, cp_heads, codec_emb, pred_emb, tts_pad,
+                 eos=-1, penalty=1.05, max_positions=1024, groups=16):
+        t = FrameTables()
+        self._keep = [np.ascontiguousarray(talker_head)] + \
+            [np.ascontiguousarray(h) for h in cp_heads] + [_f32(codec_emb)] + \
+            [_f32(p) for p in pred_emb] + [_f32(tts_pad)]
+        k = self._keep
+        t.talker_head = k[0].ctypes.data
+        for g in range(groups - 1):
+            t.cp_heads[g] = k[1 + g].ctypes.data
+            t.pred_emb[g] = k[2 + (groups - 1) + g].ctypes.data
+        t.codec_emb = k[1 + (groups - 1)].ctypes.data
+        t.vocab = codec_emb.shape[0]
+        t.cp_vocab = pred_emb[0].shape[0]
+        t.groups = groups
+        t.eos = eos
+        t.penalty = penalty
+        t.tts_pad = k[-1].ctypes.data
+        self.t = t
+        self.groups = groups
+        self.vocab = t.vocab
+        self.hidden = codec_emb.shape[1]
+        self.h = lib().q3o_frame_create(talker.h, cp.h, ctypes.byref(t), max_positions)
+
+    def start(self, prefill, trailing=None):
+        p = _f32(prefill)
+        tr = _f32(trailing) if trailing is not None and len(trailing) else None
+        rc = lib().q3o_frame_start(self.h, _fp(p), p.shape[0], _fp(tr),
+                                   0 if tr is None else tr.shape[0])
+        if rc:
+            raise ValueError("q3o_frame_start failed")
+
+    def next(self):
+        codes = np.empty(self.groups, dtype=np.int32)
+        r = lib().q3o_frame_next(self.h, codes.ctypes.data_as(_IP))
+        if r < 0:
+            raise ValueError("q3o_frame_next failed")
+        return (codes if r == 1 else None)
+
+    def state(self):
+        lg = np.ctypeslib.as_array(lib().q3o_frame_logits(self.h), (self.vocab,)).copy()
+        ph = np.ctypeslib.as_array(lib().q3o_frame_past_hidden(self.h), (self.hidden,)).copy()
+        return lg, ph
+
+    def destroy(self):
+        if self.h:
+            lib().q3o_frame_destroy(self.h)
+            self.h = None

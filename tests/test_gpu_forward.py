@@ -1,0 +1,201 @@
+"""GPU parity of q3h_forward_embeds / q3h_forward_embeds_batch against the
+oracle and the transformers goldens, through the C ABI.
+
+Tolerances (max |gpu - ref| / max |ref|, QwenDiff of
+tests/test.tts.qwen.ref.pas): f32 weights 1e-4 (the reference's GPU-vs-CPU
+bar, tests/test.tts.qwen.vulkan.pas:226-231); Q8_0 logits 1e-3 with identical
+greedy codes.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from models import Model, rel, top2_margin
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def golden_dims(g):
+    L, H, heads, kvh, hd, inter = g["dims"].tolist()
+    return dict(layers=L, hidden=H, heads=heads, kv_heads=kvh, head_dim=hd, intermediate=inter,
+                rms_eps=1e-6, rope_theta=1e6)
+
+
+@pytest.mark.parametrize("name", ["qwen3_small_3l", "qwen3_full_2l"])
+def test_f32_stack_matches_transformers(device, q3h, synth, name):
+    print(f"case {name}", flush=True)
+    g = np.load(os.path.join(GOLDEN, name + ".npz"))
+    dims = golden_dims(g)
+    layers, final = synth.stack_weights(int(g["seed"]), "golden.", dims, std=float(g["std"]),
+                                        norm_std=float(g["norm_std"]))
+    st = q3h.Stack(device, dict(dims, dtype=q3h.F32, kv_f16=0, act_q8=0, max_positions=64),
+                   layers, final, q3h.F32)
+    ctx = q3h.Context(st, 64)
+    pos = 0
+    for rows in g["schedule"].tolist():
+        _, normed = ctx.forward(g["x"][pos:pos + rows])
+        pos += rows
+        assert rel(normed, g["normed"][pos - 1]) < 1e-4, (pos, rel(normed, g["normed"][pos - 1]))
+    assert ctx.length == pos
+    ctx.destroy()
+    st.destroy()
+
+
+@pytest.fixture(scope="module")
+def q8model(device):
+    m = Model(device, seed=1, max_positions=8256)
+    yield m
+    m.destroy()
+
+
+def test_q8_talker_prefill_and_greedy_decode(q8model, q3h, q3o, synth):
+    """Talker only, Q8_0, batch 1: 48 prompt rows then greedy steps whose
+    input is codec_emb[code] (the talker-only workload)."""
+    m = q8model
+    ctx = q3h.Context(m.ts, 256)
+    octx = q3o.Ctx(m.ot, 256)
+    x = synth.prompt(5, 48)
+    worst = 0.0
+    for step in range(9):
+        print(f"talker step {step}", flush=True)
+        lg, st = ctx.forward(x, head=0)
+        ost = octx.forward(x)
+        olg = m.ot.head(m.th, ost)
+        r = max(rel(lg, olg), rel(st, ost))
+        worst = max(worst, r)
+        assert r < 1e-3, (step, r)
+        code = int(np.argmax(olg[:2048]))
+        assert int(np.argmax(lg[:2048])) == code, (step, top2_margin(olg[:2048]))
+        x = m.codec_emb[code][None]
+    print(f"worst relative error {worst:.2e}")
+    assert ctx.length == octx.length == 48 + 8
+    ctx.destroy()
+    octx.destroy()
+
+
+@pytest.mark.parametrize("kv_f16", [0, 1])
+def test_predictor_f32_lcg_inputs(device, q3h, q3o, synth, kv_f16):
+    """The reference's PredictorOnGpuMatchesCpu (tests/test.tts.qwen.vulkan.pas:
+    150-232): f32 code predictor, 15 steps of LCG inputs (2 rows, then 1 per
+    group), head g at step g; logits and states within 1e-4 of the CPU path."""
+    print(f"case kv_f16={kv_f16}", flush=True)
+    dims = synth.PREDICTOR
+    L, f = synth.stack_weights(21, "talker.code_predictor.model.", dims, norm_std=0.1)
+    heads = [synth.cp_head(21, g) for g in range(15)]
+    st = q3h.Stack(device, dict(dims, dtype=q3h.F32, kv_f16=kv_f16, act_q8=0, max_positions=16),
+                   L, f, q3h.F32)
+    for h in heads:
+        st.add_head(h, q3h.F32)
+    ost = q3o.Stack(dims, L, f, q3o.F32, kv_f16=kv_f16)
+    ctx, octx = q3h.Context(st, 16), q3o.Ctx(ost, 16)
+    seed = 12345
+    worst = 0.0
+    for g in range(15):
+        rows = 2 if g == 0 else 1
+        x, seed = synth.lcg_rows(rows * 1024, seed)
+        lg, hs = ctx.forward(x.reshape(rows, 1024), head=g)
+        ohs = octx.forward(x.reshape(rows, 1024))
+        olg = ost.head(heads[g], ohs)
+        worst = max(worst, rel(lg, olg), rel(hs, ohs))
+    print(f"predictor f32 kv_f16={kv_f16}: worst {worst:.2e}")
+    assert worst <= 1e-4
+    assert ctx.length == 16
+    for o in (ctx, st):
+        o.destroy()
+    octx.destroy()
+    ost.destroy()
+
+
+def test_batch_equals_single(q8model, q3h, synth):
+    m = q8model
+    lens = [5, 17, 33, 2]
+    a = [q3h.Context(m.ts, 64) for _ in lens]
+    b = [q3h.Context(m.ts, 64) for _ in lens]
+    for i, n in enumerate(lens):
+        p = synth.prompt(30 + i, n)
+        a[i].forward(p, want_normed=False)
+        b[i].forward(p, want_normed=False)
+    x = synth.prompt(40, len(lens))
+    lg, normed = q3h.forward_batch(a, x, heads=[0] * len(lens))
+    for i in range(len(lens)):
+        l1, n1 = b[i].forward(x[i], head=0)
+        assert rel(normed[i], n1) < 1e-6 and rel(lg[i], l1) < 1e-6, i
+        assert a[i].length == b[i].length == lens[i] + 1
+    for c in a + b:
+        c.destroy()
+
+
+@pytest.mark.parametrize("L", [300, 2048])
+def test_long_context_decode(device, q3h, q3o, synth, L):
+    """Split-K attention: K/V prefilled with N(0,1) values (fp16 cache), then
+    decode steps, against the oracle with the same cache."""
+    print(f"case L={L}", flush=True)
+    dims = dict(synth.TALKER, layers=2)
+    layers, f = synth.stack_weights(3, "talker.model.", dims, norm_std=0.1,
+                                    quantize=q3o.quantize_q8_0)
+    st = q3h.Stack(device, dict(dims, dtype=q3h.Q8_0, kv_f16=1, act_q8=0, max_positions=L + 8),
+                   layers, f, q3h.Q8_0)
+    ost = q3o.Stack(dims, layers, f, q3o.Q8_0, kv_f16=1)
+    kv = synth.normal(9, "kv", (2, 2, 8, L, 128), 1.0)
+    ctx, octx = q3h.Context(st, L + 8), q3o.Ctx(ost, L + 8)
+    ctx.fill_kv(kv[0], kv[1])
+    octx.fill(kv[0], kv[1])
+    k0, v0 = ctx.read_kv(1)
+    assert np.array_equal(k0, kv[0][1].astype(np.float16).astype(np.float32))
+    for step in range(3):
+        x = synth.prompt(50 + step, 1)
+        _, s = ctx.forward(x)
+        os_ = octx.forward(x)
+        assert rel(s, os_) < 1e-3, (step, rel(s, os_))
+    assert ctx.length == L + 3
+    ctx.destroy()
+    st.destroy()
+    octx.destroy()
+    ost.destroy()
+
+
+def test_device_quantizer_equals_host_blocks(device, q3h, q3o, synth):
+    """A stack given f32 weights (quantized on the device) computes exactly as
+    one given the oracle's ggml blocks: the device quantizer is bit-exact."""
+    dims = dict(synth.TALKER, layers=1)
+    lf, ff = synth.stack_weights(4, "talker.model.", dims, norm_std=0.1)
+    lq = [{k: (q3o.quantize_q8_0(v) if k.startswith("w") else v) for k, v in L.items()}
+          for L in lf]
+    cfg = dict(dims, dtype=q3h.Q8_0, kv_f16=0, act_q8=0, max_positions=16)
+    a = q3h.Stack(device, cfg, lf, ff, q3h.F32)
+    b = q3h.Stack(device, cfg, lq, ff, q3h.Q8_0)
+    ha = a.add_head(synth.talker_head(4), q3h.F32)
+    hb = b.add_head(q3o.quantize_q8_0(synth.talker_head(4)), q3h.Q8_0)
+    ca, cb = q3h.Context(a, 16), q3h.Context(b, 16)
+    x = synth.prompt(6, 3)
+    la, sa = ca.forward(x, head=ha)
+    lb, sb = cb.forward(x, head=hb)
+    assert np.array_equal(la, lb) and np.array_equal(sa, sb)
+    assert a.bytes == b.bytes == 16720896 + 4096
+    for o in (ca, cb, a, b):
+        o.destroy()
+
+
+def test_context_errors_and_reset(q8model, q3h, synth):
+    m = q8model
+    c = q3h.Context(m.ts, 4)
+    c.forward(synth.prompt(1, 3))
+    with pytest.raises(q3h.Q3HError) as e:
+        c.forward(synth.prompt(2, 2))
+    assert e.value.code == q3h.E_CAPACITY
+    assert c.length == 3
+    with pytest.raises(q3h.Q3HError) as e:
+        c.forward(synth.prompt(2, 1), head=99)
+    assert e.value.code == q3h.E_ARG
+    c.reset()
+    assert c.length == 0
+    # after a reset the positions restart at 0: same result as a fresh context
+    d = q3h.Context(m.ts, 4)
+    x = synth.prompt(3, 2)
+    l1, s1 = c.forward(x, head=0)
+    l2, s2 = d.forward(x, head=0)
+    assert np.array_equal(l1, l2) and np.array_equal(s1, s2)
+    c.destroy()
+    d.destroy()

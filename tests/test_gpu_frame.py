@@ -1,0 +1,126 @@
+"""GPU parity of the frame step (q3h_frame_*) against the oracle's restatement
+of TQwenTalker.NextFrame (talker.pas:640-681): identical greedy codes for
+every frame, talker logits within 1e-3 (max-abs relative)."""
+import numpy as np
+import pytest
+
+from models import Model, rel
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def full(device):
+    m = Model(device, seed=2, max_positions=512)
+    yield m
+    m.destroy()
+
+
+def test_frame_b1_q8_16_frames(full, synth):
+    """The full frame (28-layer talker, 5-layer code predictor, Q8_0), 48
+    prompt rows, 16 frames."""
+    m = full
+    fr = m.frame(n_streams=1, max_positions=512)
+    of = m.oracle_frame(max_positions=512)
+    pre = synth.prompt(8, 48)
+    trailing = synth.normal(8, "trailing", (3, 1024), 0.02)
+    fr.start(0, pre, trailing)
+    of.start(pre, trailing)
+    lg, past = fr.state(0)
+    olg, opast = of.state()
+    assert rel(lg, olg) < 1e-3 and rel(past, opast) < 1e-3
+    worst = 0.0
+    for i in range(16):
+        codes, alive = fr.step()
+        ref = of.next()
+        lg, _ = fr.state(0)
+        olg, _ = of.state()
+        worst = max(worst, rel(lg, olg))
+        print(f"frame {i}: {codes[0].tolist()} rel {rel(lg, olg):.2e}", flush=True)
+        assert alive[0] == 1
+        assert np.array_equal(codes[0], ref), (i, codes[0], ref)
+        assert rel(lg, olg) < 1e-3
+    print(f"worst logits error {worst:.2e}")
+    fr.destroy()
+    of.destroy()
+
+
+def test_frame_graph_equals_eager(full, synth):
+    m = full
+    pre = synth.prompt(9, 20)
+    a = m.frame(use_graph=True, max_positions=64)
+    b = m.frame(use_graph=False, max_positions=64)
+    a.start(0, pre)
+    b.start(0, pre)
+    for i in range(4):
+        ca, _ = a.step()
+        cb, _ = b.step()
+        assert np.array_equal(ca, cb)
+        assert np.array_equal(a.state(0)[0], b.state(0)[0])
+    a.destroy()
+    b.destroy()
+
+
+@pytest.fixture(scope="module")
+def small(device):
+    m = Model(device, seed=3, talker_layers=4, cp_layers=2, norm_std=0.1, max_positions=128)
+    yield m
+    m.destroy()
+
+
+def test_frame_multi_stream(small, synth):
+    m = small
+    lens = [16, 40, 23]
+    fr = m.frame(n_streams=len(lens), max_positions=128)
+    ofs = []
+    for s, n in enumerate(lens):
+        pre = synth.prompt(60 + s, n)
+        tr = synth.normal(60 + s, "trailing", (s + 1, 1024), 0.02)
+        fr.start(s, pre, tr)
+        of = m.oracle_frame(max_positions=128)
+        of.start(pre, tr)
+        ofs.append(of)
+    for i in range(6):
+        codes, alive = fr.step()
+        for s, of in enumerate(ofs):
+            ref = of.next()
+            assert alive[s] == 1
+            assert np.array_equal(codes[s], ref), (i, s)
+            assert rel(fr.state(s)[0], of.state()[0]) < 1e-3
+    fr.destroy()
+    for of in ofs:
+        of.destroy()
+
+
+def test_frame_eos_ends_a_stream(small, synth):
+    """eos is taken as the code 0 that frame 2 would choose: from then on the
+    stream ends, as NextFrame returns false (talker.pas:646-647); eos is
+    forbidden before 2 frames (talker.pas:610-611)."""
+    m = small
+    pre = synth.prompt(70, 12)
+    of = m.oracle_frame(max_positions=128)
+    of.start(pre)
+    first = [of.next()[0] for _ in range(3)]
+    of.destroy()
+    eos = int(first[2])
+    fr = m.frame(n_streams=2, eos=eos, max_positions=128)
+    of = m.oracle_frame(eos=eos, max_positions=128)
+    fr.start(0, pre)
+    fr.start(1, synth.prompt(71, 9))
+    of.start(pre)
+    ended = None
+    for i in range(5):
+        codes, alive = fr.step()
+        ref = of.next()
+        if ref is None:
+            ended = i
+            assert alive[0] == 0 and np.all(codes[0] == -1)
+            break
+        assert alive[0] == 1 and np.array_equal(codes[0], ref)
+    assert ended is not None and ended >= 2
+    # the other stream keeps running
+    assert alive[1] == 1
+    codes, alive = fr.step()
+    assert alive[0] == 0 and alive[1] == 1
+    fr.destroy()
+    of.destroy()

@@ -1,0 +1,163 @@
+"""Pins the oracle's Qwen3 stack (CPU only).
+
+- f32: against golden vectors of the third-party transformers Qwen3 (written by
+  tests/golden/make_qwen3_golden.py), every layer output and every normed row,
+  with the K/V cache carried across calls of the recorded schedule.
+- incremental calls equal one call over the same rows (the causal property that
+  the reference fixture relies on for predictor.logits, manifest.json note).
+- Q8_0 (f32 activations) equals the f32 stack over the dequantized weights.
+- Q8_0 activations (int8 products) stay within the quantization noise.
+- fp16 K/V cache stays close to the f32 cache.
+"""
+import os
+
+import numpy as np
+import pytest
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def rel(a, b):
+    return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
+
+
+def load_golden(name):
+    g = np.load(os.path.join(GOLDEN, name + ".npz"))
+    L, H, heads, kvh, hd, inter = g["dims"].tolist()
+    dims = dict(layers=L, hidden=H, heads=heads, kv_heads=kvh, head_dim=hd, intermediate=inter,
+                rms_eps=1e-6, rope_theta=1e6)
+    return g, dims
+
+
+def rmsnorm(x, w, eps=1e-6):
+    x = x.astype(np.float64)
+    return (w * (x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps))).astype(np.float32)
+
+
+@pytest.mark.parametrize("name", ["qwen3_small_3l", "qwen3_full_2l"])
+def test_f32_stack_matches_transformers(q3o, synth, name):
+    g, dims = load_golden(name)
+    layers, final = synth.stack_weights(int(g["seed"]), "golden.", dims, std=float(g["std"]),
+                                        norm_std=float(g["norm_std"]))
+    st = q3o.Stack(dims, layers, final, q3o.F32)
+    ctx = q3o.Ctx(st, 64)
+    pos = 0
+    for rows in g["schedule"].tolist():
+        normed, lo = ctx.forward(g["x"][pos:pos + rows], layer_out=True)
+        for l in range(dims["layers"] - 1):
+            assert rel(lo[l], g["raw"][l, pos:pos + rows]) < 2e-5, (l, pos)
+        allnormed = rmsnorm(lo[-1], final)
+        assert rel(allnormed, g["normed"][pos:pos + rows]) < 2e-5
+        assert rel(normed, g["normed"][pos + rows - 1]) < 2e-5
+        pos += rows
+    assert ctx.length == pos
+    ctx.destroy()
+    st.destroy()
+
+
+def small_stack(synth, q3o, seed, dtype, act_q8=0, kv_f16=0, layers=3):
+    dims = dict(layers=layers, hidden=256, heads=8, kv_heads=2, head_dim=128, intermediate=512,
+                rms_eps=1e-6, rope_theta=1e6)
+    quant = q3o.quantize_q8_0 if dtype == q3o.Q8_0 else None
+    L, f = synth.stack_weights(seed, "t.", dims, std=0.05, norm_std=0.1, quantize=quant)
+    return dims, L, f, q3o.Stack(dims, L, f, dtype, kv_f16=kv_f16, act_q8=act_q8)
+
+
+@pytest.mark.parametrize("dtype", [0, 1])
+def test_incremental_equals_one_call(q3o, synth, dtype):
+    dims, L, f, st = small_stack(synth, q3o, 11, dtype)
+    x = synth.prompt(11, 9, dims["hidden"])
+    a = q3o.Ctx(st, 16)
+    _, lo_all = a.forward(x, layer_out=True)
+    b = q3o.Ctx(st, 16)
+    pos = 0
+    for rows in (4, 1, 3, 1):
+        nb, lo = b.forward(x[pos:pos + rows], layer_out=True)
+        assert np.array_equal(lo, lo_all[:, pos:pos + rows])
+        pos += rows
+    assert b.length == a.length == 9
+    for o in (a, b, st):
+        o.destroy()
+
+
+def test_q8_0_equals_f32_over_dequantized(q3o, synth):
+    dims, L, f, st = small_stack(synth, q3o, 12, q3o.Q8_0)
+    deq = []
+    for layer in L:
+        d = dict(layer)
+        for k in ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown"):
+            k_in = {"wo": dims["heads"] * 128, "wdown": dims["intermediate"]}.get(k, dims["hidden"])
+            d[k] = q3o.dequantize_q8_0(layer[k], k_in)
+        deq.append(d)
+    sf = q3o.Stack(dims, deq, f, q3o.F32)
+    x = synth.prompt(12, 6, dims["hidden"])
+    a, b = q3o.Ctx(st, 8), q3o.Ctx(sf, 8)
+    na, la = a.forward(x, layer_out=True)
+    nb, lb = b.forward(x, layer_out=True)
+    assert rel(la, lb) < 1e-5 and rel(na, nb) < 1e-5
+    for o in (a, b, st, sf):
+        o.destroy()
+
+
+def test_q8_0_activations_close(q3o, synth):
+    dims, L, f, s0 = small_stack(synth, q3o, 13, q3o.Q8_0, act_q8=0)
+    s1 = q3o.Stack(dims, L, f, q3o.Q8_0, act_q8=1)
+    x = synth.prompt(13, 5, dims["hidden"])
+    a, b = q3o.Ctx(s0, 8), q3o.Ctx(s1, 8)
+    na = a.forward(x)
+    nb = b.forward(x)
+    # int8 activations add ~1/254 relative noise per product
+    assert 0 < rel(nb, na) < 5e-2
+    for o in (a, b, s0, s1):
+        o.destroy()
+
+
+def test_int8_head_is_block_integer_dot(q3o):
+    rng = np.random.default_rng(5)
+    w = q3o.quantize_q8_0((rng.standard_normal((8, 64)) * 0.02).astype(np.float32))
+    x = rng.standard_normal(64).astype(np.float32)
+    dims = dict(layers=1, hidden=64, heads=1, kv_heads=1, head_dim=64, intermediate=64,
+                rms_eps=1e-6, rope_theta=1e6)
+    L = [{k: (w if k.startswith("w") else np.ones(64, np.float32)) for k in
+          ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown", "input_norm", "post_norm",
+           "q_norm", "k_norm")}]
+    st = q3o.Stack(dims, L, np.ones(64, np.float32), q3o.Q8_0, act_q8=1)
+    got = st.head(w, x)
+    xb = q3o.quantize_q8_0(x[None]).reshape(-1, 34)
+    wb = w.reshape(8, -1, 34)
+    exp = np.zeros(8, np.float32)
+    for r in range(8):
+        acc = np.float32(0)
+        for b in range(2):
+            qi = int(np.dot(wb[r, b, 2:].view(np.int8).astype(np.int32),
+                            xb[b, 2:].view(np.int8).astype(np.int32)))
+            dw = np.float32(wb[r, b, :2].copy().view(np.float16)[0])
+            dx = np.float32(xb[b, :2].copy().view(np.float16)[0])
+            acc = np.float32(acc + np.float32(qi) * np.float32(dw * dx))
+        exp[r] = acc
+    # equal up to the fused multiply-add of the accumulation (an ulp of the
+    # block terms); a wrong block or scale index is off by orders more
+    assert np.max(np.abs(got - exp)) <= 1e-6 * np.max(np.abs(exp))
+    st.destroy()
+
+
+def test_kv_f16_close_to_f32(q3o, synth):
+    dims, L, f, s0 = small_stack(synth, q3o, 14, q3o.F32)
+    s1 = q3o.Stack(dims, L, f, q3o.F32, kv_f16=1)
+    x = synth.prompt(14, 7, dims["hidden"])
+    a, b = q3o.Ctx(s0, 8), q3o.Ctx(s1, 8)
+    na, nb = a.forward(x), b.forward(x)
+    assert 0 < rel(nb, na) < 1e-2
+    for o in (a, b, s0, s1):
+        o.destroy()
+
+
+def test_context_overflow_is_refused(q3o, synth):
+    dims, L, f, st = small_stack(synth, q3o, 15, q3o.F32, layers=1)
+    c = q3o.Ctx(st, 4)
+    c.forward(synth.prompt(1, 3, dims["hidden"]))
+    with pytest.raises(ValueError):
+        c.forward(synth.prompt(2, 2, dims["hidden"]))
+    assert c.length == 3
+    c.destroy()
+    st.destroy()
