@@ -1,0 +1,221 @@
+"""Throughput of the Qwen3-TTS frame step on one MI355X.
+
+A step is one frame step (TQwenTalker.NextFrame, src/tts/mormot.ai.tts.qwen.
+talker.pas:640-681): for every stream, code 0 from the talker logits, 15
+code-predictor forwards (5 layers) each with its head and argmax, the sum of
+16 embeddings, one talker forward (28 layers) with the 3072-code head, and
+the 16 codes of each stream copied back to the host.
+
+Workloads (random-init N(0, 0.02) weights from a seed, Q8_0, norm weights 1,
+synthetic N(0, 1) prompt embeddings; nothing is downloaded):
+  frame_b1   1 stream, 48 prompt rows, K frames (156: context 48 -> 204)
+  frame_b32  32 streams, prompt rows uniform in [16, 256] (seeded), K frames
+
+Timed region: K steps after W warm-up steps; the warm-up runs on a first
+prefill, the timed steps restart from a fresh prefill so that the context
+grows exactly as in the workload. Each step returns with its codes in host
+memory, so the wall clock of the K calls is the whole-job time.
+
+Beside it:
+  roofline      the Q8_0 matrix-vector products of one talker decode step (28
+                layers x 4 products + the 3072-row head, 471.5 MB of weights,
+                more than the 256 MB Infinity Cache holds), graph-replayed and
+                timed with hipEvents on their stream inside the library;
+  cpu_baseline  the oracle (the C restatement of the same frame step) on the
+                host cores, on a bounded sample of the same workload.
+
+Prints one JSON line.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "mormot2-qwen-tts_amd")
+sys.path.insert(0, PKG)
+
+import q3h  # noqa: E402
+import synth  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+PROMPT_ROWS = 48
+
+
+def log(msg):
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
+
+
+def build_model(dev, seed, max_positions):
+    """Talker + code predictor + heads on the device, from f32 weights that the
+    library quantizes to Q8_0 (bit-exact ggml quantize_row_q8_0_ref)."""
+    t0 = time.time()
+    tl, tf = synth.stack_weights(seed, "talker.model.", synth.TALKER)
+    ts = q3h.Stack(dev, dict(synth.TALKER, dtype=q3h.Q8_0, kv_f16=0, act_q8=0,
+                             max_positions=max_positions), tl, tf, q3h.F32)
+    cl, cf = synth.stack_weights(seed, "talker.code_predictor.model.", synth.PREDICTOR)
+    cs = q3h.Stack(dev, dict(synth.PREDICTOR, dtype=q3h.Q8_0, kv_f16=0, act_q8=0,
+                             max_positions=16), cl, cf, q3h.F32)
+    th = synth.talker_head(seed)
+    ts.add_head(th, q3h.F32)
+    ch = [synth.cp_head(seed, g) for g in range(15)]
+    for h in ch:
+        cs.add_head(h, q3h.F32)
+    tables = dict(codec_emb=synth.codec_embedding(seed),
+                  pred_emb=[synth.pred_embedding(seed, g) for g in range(15)],
+                  tts_pad=synth.tts_pad(seed))
+    log(f"model on the device in {time.time() - t0:.1f} s "
+        f"({(ts.bytes + cs.bytes) / 1e6:.1f} MB of layers)")
+    f32 = dict(tl=tl, tf=tf, cl=cl, cf=cf, th=th, ch=ch)
+    return ts, cs, tables, f32
+
+
+def prompts(seed, workload, n):
+    if workload == "frame_b1":
+        return [synth.prompt(seed, PROMPT_ROWS)]
+    rng = np.random.Generator(np.random.PCG64(seed))
+    lens = rng.integers(16, 257, size=n)
+    return [synth.prompt(seed + 1000 + s, int(L)) for s, L in enumerate(lens)]
+
+
+def run_gpu(frame, pre, steps, warmup):
+    for s, p in enumerate(pre):
+        frame.start(s, p)
+    for _ in range(warmup):
+        frame.step()
+    for s, p in enumerate(pre):
+        frame.start(s, p)
+    lat = np.empty(steps)
+    codes = []
+    t0 = time.perf_counter()
+    for i in range(steps):
+        a = time.perf_counter()
+        c, alive = frame.step()
+        lat[i] = time.perf_counter() - a
+        codes.append(c)
+    total = time.perf_counter() - t0
+    return total, lat, np.stack(codes)
+
+
+def cpu_baseline(f32, tables, pre, gpu_codes, budget_s, max_frames):
+    """The oracle's frame step on the host cores (same weights, same prompt of
+    stream 0), frames timed until budget_s is spent."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import q3o  # the checker's restatement, timed as the CPU baseline
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    q3o.set_threads(threads)
+    q = q3o.quantize_q8_0
+
+    def qlayers(layers):
+        return [{k: (q(v) if k.startswith("w") else v) for k, v in L.items()} for L in layers]
+
+    ot = q3o.Stack(synth.TALKER, qlayers(f32["tl"]), f32["tf"], q3o.Q8_0)
+    oc = q3o.Stack(synth.PREDICTOR, qlayers(f32["cl"]), f32["cf"], q3o.Q8_0)
+    fr = q3o.Frame(ot, oc, q(f32["th"]), [q(h) for h in f32["ch"]], tables["codec_emb"],
+                   tables["pred_emb"], tables["tts_pad"], max_positions=PROMPT_ROWS + max_frames + 8)
+    fr.start(pre[0])
+    n = 0
+    equal = True
+    t0 = time.perf_counter()
+    while n < max_frames and (n < 2 or time.perf_counter() - t0 < budget_s):
+        c = fr.next()
+        equal = equal and n < len(gpu_codes) and np.array_equal(c, gpu_codes[n][0])
+        n += 1
+    dt = time.perf_counter() - t0
+    for o in (fr, ot, oc):
+        o.destroy()
+    return dict(value=n / dt, unit="frames/s", cores=threads, kind="port",
+                sample=f"frame step B=1 Q8_0 (oracle, C + OpenMP), {PROMPT_ROWS} prompt rows "
+                       f"(prefill untimed), first {n} frames, {dt:.1f} s"), n, equal
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", choices=["frame_b1", "frame_b32"], default="frame_b1")
+    ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--gemv-iters", type=int, default=50)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(independent streams would shard across GPUs with no exchange)", file=sys.stderr)
+        return 2
+    b1 = args.workload == "frame_b1"
+    n = 1 if b1 else 32
+    steps = args.steps if args.steps is not None else (156 if b1 else 128)
+    warmup = args.warmup
+    if not q3h.available():
+        raise RuntimeError("no gfx950 device")
+    pre = prompts(args.seed, args.workload, n)
+    maxlen = max(p.shape[0] for p in pre)
+    max_pos = maxlen + max(steps, warmup) + 8
+    dev = q3h.Device(0)
+    ts, cs, tables, f32 = build_model(dev, args.seed, max_pos)
+    frame = q3h.Frame(ts, cs, tables["codec_emb"], tables["pred_emb"], tables["tts_pad"],
+                      n_streams=n, max_positions=max_pos, max_frames=max(steps, warmup) + 8)
+    log(f"{args.workload}: {n} stream(s), warm-up {warmup}, timing {steps} steps")
+    total, lat, codes = run_gpu(frame, pre, steps, warmup)
+    fps = n * steps / total
+    log(f"{fps:.1f} frames/s, {1e3 * total / steps:.3f} ms per step "
+        f"(p50 {1e6 * np.median(lat):.0f} us, p99 {1e6 * np.percentile(lat, 99):.0f} us)")
+
+    # dominant kernel: the Q8_0 matrix-vector products of a talker decode step
+    us, launches, nbytes = ts.time_gemv(head=0, iters=args.gemv_iters)
+    per_launch = nbytes / launches
+    achieved = per_launch / (us * 1e-6) / 1e9
+    log(f"gemv: {launches} launches/step, {us:.2f} us/launch, {achieved:.0f} GB/s")
+    roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
+                    kernel="k_gemv_q8 (Q8_0 matrix-vector products of one talker decode step)",
+                    bytes_per_launch=int(per_launch), us_per_launch=round(us, 3))
+
+    cpu = None
+    parity = None
+    if not args.no_cpu:
+        cpu, nf, equal = cpu_baseline(f32, tables, pre, codes, args.cpu_seconds, steps)
+        parity = dict(frames=nf, codes_equal_stream0=bool(equal))
+        log(f"cpu baseline: {cpu['value']:.2f} frames/s on {cpu['cores']} threads; "
+            f"codes equal over {nf} frames: {equal}")
+    frame.destroy()
+    ts.destroy()
+    cs.destroy()
+    dev.close()
+
+    out = {
+        "metric": "talker+CP frames/s @B=1 & B=32 (Q8_0); frame-step µs; "
+                  "% HBM/MFMA roofline",
+        "value": round(fps, 2),
+        "unit": "frames/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(1e3 * total / steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) prompt embeddings)",
+        "config": {"workload": args.workload, "streams": n, "prompt_rows":
+                   PROMPT_ROWS if b1 else "U[16,256]", "frames": steps,
+                   "talker_layers": 28, "cp_layers": 5, "hidden": 1024,
+                   "heads": "16q/8kv x 128", "ffn": 3072, "weights": "Q8_0", "kv": "f32"},
+        "step_us_p50": round(1e6 * float(np.median(lat)), 1),
+        "step_us_p99": round(1e6 * float(np.percentile(lat, 99)), 1),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "parity": parity,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

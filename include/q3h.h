@@ -179,6 +179,16 @@ int q3h_frame_destroy(q3h_frame *f);
    host: k % 32 == 0, y receives k/32 blocks of 34 bytes */
 int q3h_quantize_row_q8_0(const float *x, void *y, int64_t k);
 
+/* no reference counterpart (measurement): the weight products of one
+   single-row decode step of stack s - per layer the fused q/k/v, o, gate/up
+   and down matrix-vector products, then head `head` (-1: none) - captured in
+   a hipGraph and replayed iters times between two hipEvents on one stream.
+   us_per_launch: elapsed / (iters * launches); launches: products per step;
+   bytes: algorithmic bytes per step (weights, norm vectors, input and output
+   vectors). The activations are zeros; the stack's contexts are untouched. */
+int q3h_stack_time_gemv(q3h_stack *s, int head, int iters, float *us_per_launch,
+                        int *launches, int64_t *bytes);
+
 #ifdef __cplusplus
 }
 #endif

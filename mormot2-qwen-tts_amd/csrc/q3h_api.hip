@@ -703,3 +703,84 @@ extern "C" int q3h_forward_embeds_batch(q3h_context *const *ctxs, int n, const f
     for (int i = 0; i < n; i++) ctxs[i]->len += 1;
   });
 }
+
+// ---------------------------------------------------------------------------
+// measurement: the weight products of one decode step, graph-replayed
+
+extern "C" int q3h_stack_time_gemv(q3h_stack *s, int head, int iters, float *us_per_launch,
+                                   int *launches, int64_t *bytes) {
+  Work w;
+  hipStream_t st = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  int rc = guard([&] {
+    require(s && us_per_launch && launches && bytes && iters > 0, Q3H_E_ARG,
+            "q3h_stack_time_gemv: invalid argument");
+    require(head >= -1 && head < (int)s->heads.size(), Q3H_E_ARG,
+            "q3h_stack_time_gemv: no head " + std::to_string(head));
+    check_hip(hipSetDevice(s->dev->ordinal), "hipSetDevice");
+    const q3h_stack_config &c = s->cfg;
+    const int H = c.hidden, NQ = c.heads * c.head_dim, NKV = c.kv_heads * c.head_dim;
+    const int I = c.intermediate, ldq = NQ + 2 * NKV;
+    const bool q8 = c.dtype == Q3H_Q8_0;
+    const int head_rows = head >= 0 ? s->heads[head].N : 0;
+    w.ensure(s, 1, 1, head_rows);
+    check_hip(hipStreamCreateWithFlags(&st, hipStreamNonBlocking), "hipStreamCreate");
+    check_hip(hipMemsetAsync(w.h, 0, sizeof(float) * H, st), "zero");
+    check_hip(hipMemsetAsync(w.att, 0, sizeof(float) * NQ, st), "zero");
+    check_hip(hipMemsetAsync(w.act, 0, sizeof(float) * I, st), "zero");
+    check_hip(hipMemsetAsync(w.normed, 0, sizeof(float) * H, st), "zero");
+    check_hip(hipStreamSynchronize(st), "zero sync");
+    auto mat_bytes = [&](const Mat &m) {
+      return q8 ? (int64_t)m.N * (m.K / 32) * 34 : (int64_t)m.N * m.K * 4;
+    };
+    int n = 0;
+    int64_t b = 0;
+    check_hip(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "capture");
+    for (int l = 0; l < c.layers; l++) {
+      const Layer &L = s->layers[l];
+      launch_gemv(make_gemv(L.qkv, w.h, H, 1, L.in_norm, c.rms_eps, w.qkv, ldq), EPI_STORE, q8,
+                  st);
+      launch_gemv(make_gemv(L.o, w.att, NQ, 1, nullptr, 0.f, w.h, H), EPI_ADD, q8, st);
+      launch_gemv(make_gemv(L.gu, w.h, H, 1, L.post_norm, c.rms_eps, w.act, I), EPI_SWIGLU, q8,
+                  st);
+      launch_gemv(make_gemv(L.down, w.act, I, 1, nullptr, 0.f, w.h, H), EPI_ADD, q8, st);
+      n += 4;
+      b += mat_bytes(L.qkv) + mat_bytes(L.o) + mat_bytes(L.gu) + mat_bytes(L.down);
+      // norm vectors, inputs read, outputs written (the residual adds read y too)
+      b += 4 * (int64_t)(2 * H) + 4 * (int64_t)(H + ldq) + 4 * (int64_t)(NQ + 2 * H) +
+           4 * (int64_t)(H + I) + 4 * (int64_t)(I + 2 * H);
+    }
+    if (head >= 0) {
+      launch_gemv(make_gemv(s->heads[head], w.normed, H, 1, nullptr, 0.f, w.logits, head_rows),
+                  EPI_STORE, q8, st);
+      n += 1;
+      b += mat_bytes(s->heads[head]) + 4 * (int64_t)(H + head_rows);
+    }
+    check_hip(hipStreamEndCapture(st, &graph), "end capture");
+    check_hip(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "instantiate");
+    check_hip(hipEventCreate(&e0), "event");
+    check_hip(hipEventCreate(&e1), "event");
+    for (int i = 0; i < 2; i++) check_hip(hipGraphLaunch(exec, st), "warm-up");
+    check_hip(hipEventRecord(e0, st), "event record");
+    for (int i = 0; i < iters; i++) check_hip(hipGraphLaunch(exec, st), "graph launch");
+    check_hip(hipEventRecord(e1, st), "event record");
+    check_hip(hipEventSynchronize(e1), "event sync");
+    float ms = 0.f;
+    check_hip(hipEventElapsedTime(&ms, e0, e1), "elapsed");
+    *us_per_launch = ms * 1000.f / ((float)iters * n);
+    *launches = n;
+    *bytes = b;
+  });
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (exec) (void)hipGraphExecDestroy(exec);
+  if (graph) (void)hipGraphDestroy(graph);
+  if (st) {
+    (void)hipStreamSynchronize(st);
+    (void)hipStreamDestroy(st);
+  }
+  w.release();
+  return rc;
+}

@@ -110,6 +110,8 @@ SIGNATURES = {
     "q3h_frame_state": (_I, [_P, _I, _FP, _FP]),
     "q3h_frame_destroy": (_I, [_P]),
     "q3h_quantize_row_q8_0": (_I, [_FP, _P, ctypes.c_int64]),
+    "q3h_stack_time_gemv": (_I, [_P, _I, _I, _FP, ctypes.POINTER(_I),
+                                 ctypes.POINTER(ctypes.c_int64)]),
 }
 
 _lib = None
@@ -217,6 +219,16 @@ class Stack:
     @property
     def bytes(self):
         return lib().q3h_stack_bytes(self.h)
+
+    def time_gemv(self, head=-1, iters=20):
+        """(us per launch, launches per step, algorithmic bytes per step) of the
+        graph-replayed weight products of one single-row decode step."""
+        us = ctypes.c_float()
+        n = ctypes.c_int()
+        b = ctypes.c_int64()
+        _check(lib().q3h_stack_time_gemv(self.h, head, iters, ctypes.byref(us), ctypes.byref(n),
+                                         ctypes.byref(b)))
+        return us.value, n.value, b.value
 
     def destroy(self):
         if self.h:
