@@ -143,6 +143,9 @@ def main():
     ap.add_argument("--gemv-iters", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch the kernels directly instead of replaying hipGraphs "
+                         "(for tracers that do not follow graph capture)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -160,7 +163,8 @@ def main():
     dev = q3h.Device(0)
     ts, cs, tables, f32 = build_model(dev, args.seed, max_pos)
     frame = q3h.Frame(ts, cs, tables["codec_emb"], tables["pred_emb"], tables["tts_pad"],
-                      n_streams=n, max_positions=max_pos, max_frames=max(steps, warmup) + 8)
+                      n_streams=n, max_positions=max_pos, max_frames=max(steps, warmup) + 8,
+                      use_graph=not args.no_graph)
     log(f"{args.workload}: {n} stream(s), warm-up {warmup}, timing {steps} steps")
     total, lat, codes = run_gpu(frame, pre, steps, warmup)
     fps = n * steps / total
@@ -168,7 +172,8 @@ def main():
         f"(p50 {1e6 * np.median(lat):.0f} us, p99 {1e6 * np.percentile(lat, 99):.0f} us)")
 
     # dominant kernel: the Q8_0 matrix-vector products of a talker decode step
-    us, launches, nbytes = ts.time_gemv(head=0, iters=args.gemv_iters)
+    us, launches, nbytes = ts.time_gemv(head=0, iters=args.gemv_iters,
+                                        use_graph=not args.no_graph)
     per_launch = nbytes / launches
     achieved = per_launch / (us * 1e-6) / 1e9
     log(f"gemv: {launches} launches/step, {us:.2f} us/launch, {achieved:.0f} GB/s")
@@ -203,7 +208,7 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded N(0,0.02) weights, N(0,1) prompt embeddings)",
-        "config": {"workload": args.workload, "streams": n, "prompt_rows":
+        "config": {"workload": args.workload, "graph": not args.no_graph, "streams": n, "prompt_rows":
                    PROMPT_ROWS if b1 else "U[16,256]", "frames": steps,
                    "talker_layers": 28, "cp_layers": 5, "hidden": 1024,
                    "heads": "16q/8kv x 128", "ffn": 3072, "weights": "Q8_0", "kv": "f32"},

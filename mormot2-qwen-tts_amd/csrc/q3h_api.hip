@@ -58,6 +58,8 @@ void Work::ensure(const q3h_stack *s, int rows, int splits, int head_rows) {
   logits = (float *)dev_alloc(sizeof(float) * R * (head_cap > 0 ? head_cap : 1));
   rd = (RowDesc *)dev_alloc(sizeof(RowDesc) * R);
   part = (float *)dev_alloc(sizeof(float) * R * c.heads * splits_cap * (c.head_dim + 2));
+  tickets = (int *)dev_alloc(sizeof(int) * R * c.kv_heads);
+  check_hip(hipMemset(tickets, 0, sizeof(int) * R * c.kv_heads), "zero tickets");
   ctx_arr = (CtxDev **)dev_alloc(sizeof(CtxDev *) * R);
 }
 
@@ -70,20 +72,19 @@ void Work::release() {
   dev_free(logits);
   dev_free(rd);
   dev_free(part);
+  dev_free(tickets);
   dev_free(ctx_arr);
+  tickets = nullptr;
   h = qkv = att = act = normed = logits = part = nullptr;
   rd = nullptr;
   ctx_arr = nullptr;
 }
 
-int attention_splits(int positions) {
-  const int n = (positions + kAttnChunk - 1) / kAttnChunk;
-  return n < 1 ? 1 : n;
-}
+int attention_splits(int positions) { return attn_splits(positions); }
 
 // The layers of a stack over M rows of w.h, n contexts of R rows each (M =
 // n * R), their descriptors already in w.rd: the per-layer kernel sequence.
-void run_layers(const q3h_stack *s, Work &w, int M, int splits, hipStream_t st) {
+void run_layers(const q3h_stack *s, Work &w, int M, int splits, bool fused, hipStream_t st) {
   const q3h_stack_config &c = s->cfg;
   const int H = c.hidden, hd = c.head_dim, NQ = c.heads * hd, NKV = c.kv_heads * hd;
   const int I = c.intermediate, ldq = NQ + 2 * NKV;
@@ -94,12 +95,26 @@ void run_layers(const q3h_stack *s, Work &w, int M, int splits, hipStream_t st) 
     // RMSNorm + fused q/k/v projection
     a = make_gemv(L.qkv, w.h, H, M, L.in_norm, c.rms_eps, w.qkv, ldq);
     launch_gemv(a, EPI_STORE, q8, st);
-    // QK-norm, RoPE, K/V append
-    launch_qk_rope_append(w.qkv, ldq, w.rd, M, l, c.heads, c.kv_heads, hd, L.q_norm, L.k_norm,
-                          c.rms_eps, s->rope_cs, kv16, st);
+    // QK-norm, RoPE, K/V append (in the attention prologue when fused)
+    if (!fused)
+      launch_qk_rope_append(w.qkv, ldq, w.rd, M, l, c.heads, c.kv_heads, hd, L.q_norm,
+                            L.k_norm, c.rms_eps, s->rope_cs, kv16, st);
     // GQA attention
-    launch_attention(w.qkv, ldq, w.rd, M, l, c.heads, c.kv_heads, hd, splits, kAttnChunk, w.att,
-                     w.part, kv16, st);
+    AttnArgs at{};
+    at.qkv = w.qkv;
+    at.ldq = ldq;
+    at.rd = w.rd;
+    at.layer = l;
+    at.heads = c.heads;
+    at.kvh = c.kv_heads;
+    at.qn = L.q_norm;
+    at.kn = L.k_norm;
+    at.eps = c.rms_eps;
+    at.rope_cs = reinterpret_cast<const float2 *>(s->rope_cs);
+    at.out = w.att;
+    at.part = w.part;
+    at.tickets = w.tickets;
+    launch_attn(at, M, splits, c.max_positions, fused, kv16, st);
     // o_proj + residual
     a = make_gemv(L.o, w.att, NQ, M, nullptr, 0.f, w.h, H);
     launch_gemv(a, EPI_ADD, q8, st);
@@ -109,6 +124,27 @@ void run_layers(const q3h_stack *s, Work &w, int M, int splits, hipStream_t st) 
     // down + residual
     a = make_gemv(L.down, w.act, I, M, nullptr, 0.f, w.h, H);
     launch_gemv(a, EPI_ADD, q8, st);
+  }
+}
+
+void run_cp_fused(const q3h_stack *s, Work &w, const q3h_context *ctx, int pos, hipStream_t st) {
+  const q3h_stack_config &c = s->cfg;
+  const int H = c.hidden, hd = c.head_dim, NQ = c.heads * hd, NKV = c.kv_heads * hd;
+  const int I = c.intermediate, ldq = NQ + 2 * NKV;
+  const bool kv16 = c.kv_f16 != 0;
+  const size_t per_layer = (size_t)c.kv_heads * ctx->max_pos * hd;  // K/V elements per layer
+  const int v_off = (int)(per_layer * c.layers);
+  const size_t esz = kv16 ? 2 : 4;
+  const float *rope_row = s->rope_cs + (size_t)pos * hd;  // (cos, sin) x head_dim / 2
+  for (int l = 0; l < c.layers; l++) {
+    const Layer &L = s->layers[l];
+    launch_gemv(make_gemv(L.qkv, w.h, H, 1, L.in_norm, c.rms_eps, w.qkv, ldq), EPI_STORE, true,
+                st);
+    void *kl = static_cast<char *>(ctx->k) + l * per_layer * esz;
+    launch_attn_o_cp(L.o, w.qkv, kl, v_off, w.h, L.q_norm, rope_row, pos, c.rms_eps, kv16, st);
+    launch_gemv(make_gemv(L.gu, w.h, H, 1, L.post_norm, c.rms_eps, w.act, I), EPI_SWIGLU, true,
+                st);
+    launch_gemv(make_gemv(L.down, w.act, I, 1, nullptr, 0.f, w.h, H), EPI_ADD, true, st);
   }
 }
 
@@ -234,8 +270,10 @@ Mat alloc_mat(int N, int K, int dtype, int64_t &bytes) {
   m.N = N;
   m.K = K;
   if (dtype == Q3H_Q8_0) {
-    m.q = (int8_t *)dev_alloc((size_t)N * K);
-    m.d = (_Float16 *)dev_alloc((size_t)N * (K / 32) * 2);
+    // one allocation: the quants, then the scales (kernels that take one
+    // pointer find the scales at q + N * K)
+    m.q = (int8_t *)dev_alloc((size_t)N * K + (size_t)N * (K / 32) * 2);
+    m.d = reinterpret_cast<_Float16 *>(m.q + (size_t)N * K);
     bytes += (int64_t)N * (K / 32) * 34;
   } else {
     m.f = (float *)dev_alloc((size_t)N * K * 4);
@@ -245,8 +283,7 @@ Mat alloc_mat(int N, int K, int dtype, int64_t &bytes) {
 }
 
 void free_mat(Mat &m) {
-  dev_free(m.q);
-  dev_free(m.d);
+  dev_free(m.q);  // the scales share this allocation
   dev_free(m.f);
   m = Mat();
 }
@@ -286,8 +323,7 @@ void destroy_stack(q3h_stack *s) {
     free_mat(L.down);
     dev_free(L.in_norm);
     dev_free(L.post_norm);
-    dev_free(L.q_norm);
-    dev_free(L.k_norm);
+    dev_free(L.q_norm);  // k_norm shares this allocation
   }
   for (auto &h : s->heads) free_mat(h);
   dev_free(s->final_norm);
@@ -312,8 +348,10 @@ extern "C" int q3h_stack_create(q3h_device *dev, const q3h_stack_config *cfg,
             Q3H_E_ARG, "q3h_stack_create: widths must be multiples of 32");
     require(c.hidden % 16 == 0 && c.intermediate % 16 == 0, Q3H_E_ARG,
             "q3h_stack_create: widths must be multiples of 16");
-    require(c.heads % c.kv_heads == 0 && c.heads / c.kv_heads <= kMaxGroup, Q3H_E_ARG,
-            "q3h_stack_create: heads / kv_heads must be an integer <= 4");
+    require(c.heads % c.kv_heads == 0 &&
+                (c.heads / c.kv_heads == 1 || c.heads / c.kv_heads == 2 ||
+                 c.heads / c.kv_heads == 4),
+            Q3H_E_ARG, "q3h_stack_create: heads / kv_heads must be 1, 2 or 4");
     require(c.head_dim == 128, Q3H_E_ARG, "q3h_stack_create: head_dim must be 128");
     require(c.dtype == Q3H_F32 || c.dtype == Q3H_Q8_0, Q3H_E_ARG,
             "q3h_stack_create: dtype must be Q3H_F32 or Q3H_Q8_0");
@@ -354,8 +392,15 @@ extern "C" int q3h_stack_create(q3h_device *dev, const q3h_stack_config *cfg,
         upload_rows(L.down, c.dtype, lw.wdown, w->src_dtype, H, I, 1, 0, staging, s->stream);
         L.in_norm = upload_vec(lw.input_norm, H, "input_layernorm");
         L.post_norm = upload_vec(lw.post_norm, H, "post_attention_layernorm");
-        L.q_norm = upload_vec(lw.q_norm, hd, "q_norm");
-        L.k_norm = upload_vec(lw.k_norm, hd, "k_norm");
+        // q_norm and k_norm side by side: [q_norm | k_norm]
+        require(lw.q_norm != nullptr && lw.k_norm != nullptr, Q3H_E_ARG,
+                "a norm vector is NULL: q_norm / k_norm");
+        L.q_norm = (float *)dev_alloc(sizeof(float) * 2 * hd);
+        L.k_norm = L.q_norm + hd;
+        check_hip(hipMemcpy(L.q_norm, lw.q_norm, sizeof(float) * hd, hipMemcpyHostToDevice),
+                  "upload q_norm");
+        check_hip(hipMemcpy(L.k_norm, lw.k_norm, sizeof(float) * hd, hipMemcpyHostToDevice),
+                  "upload k_norm");
         s->bytes += (int64_t)(2 * H + 2 * hd) * 4;
       }
       s->final_norm = upload_vec(w->final_norm, H, "norm");
@@ -451,8 +496,9 @@ q3h_context *new_context(q3h_stack *s, int max_positions) {
     check_hip(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "hipStreamCreate");
     const size_t n = (size_t)c.layers * c.kv_heads * max_positions * c.head_dim;
     const size_t esz = c.kv_f16 ? 2 : 4;
-    ctx->k = dev_alloc(n * esz);
-    ctx->v = dev_alloc(n * esz);
+    // keys then values in one allocation: v = k + n elements
+    ctx->k = dev_alloc(2 * n * esz);
+    ctx->v = static_cast<char *>(ctx->k) + n * esz;
     ctx->dev = (CtxDev *)dev_alloc(sizeof(CtxDev));
     ctx->dev_arr = (CtxDev **)dev_alloc(sizeof(CtxDev *));
     CtxDev h{ctx->k, ctx->v, max_positions, 0};
@@ -469,8 +515,7 @@ q3h_context *new_context(q3h_stack *s, int max_positions) {
 
 void free_context(q3h_context *ctx) {
   ctx->w.release();
-  dev_free(ctx->k);
-  dev_free(ctx->v);
+  dev_free(ctx->k);  // the values share this allocation
   dev_free(ctx->dev);
   dev_free(ctx->dev_arr);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
@@ -607,12 +652,16 @@ extern "C" int q3h_forward_embeds(q3h_context *c, const float *x, int rows, int 
     check_hip(hipMemcpyAsync(w.h, x, sizeof(float) * rows * H, hipMemcpyHostToDevice, st),
               "upload x");
     launch_prep(c->dev_arr, nullptr, 1, rows, w.rd, st);
-    run_layers(s, w, rows, splits, st);
-    launch_rmsnorm_rows(w.h + (size_t)(rows - 1) * H, H, 1, H, s->final_norm, cf.rms_eps,
-                        w.normed, H, st);
+    run_layers(s, w, rows, splits, rows == 1, st);
+    // final norm of the last row, fused into the head product when there is one
     if (head >= 0) {
-      GemvArgs a = make_gemv(s->heads[head], w.normed, H, 1, nullptr, 0.f, w.logits, head_rows);
+      GemvArgs a = make_gemv(s->heads[head], w.h + (size_t)(rows - 1) * H, H, 1, s->final_norm,
+                             cf.rms_eps, w.logits, head_rows);
+      a.xn_out = w.normed;
       launch_gemv(a, EPI_STORE, cf.dtype == Q3H_Q8_0, st);
+    } else {
+      launch_rmsnorm_rows(w.h + (size_t)(rows - 1) * H, H, 1, H, s->final_norm, cf.rms_eps,
+                          w.normed, H, st);
     }
     launch_advance(c->dev_arr, nullptr, 1, rows, st);
     check_hip(hipGetLastError(), "forward kernels");
@@ -672,7 +721,7 @@ extern "C" int q3h_forward_embeds_batch(q3h_context *const *ctxs, int n, const f
     check_hip(hipMemcpyAsync(w.h, x, sizeof(float) * n * H, hipMemcpyHostToDevice, st),
               "upload x");
     launch_prep(w.ctx_arr, nullptr, n, 1, w.rd, st);
-    run_layers(s, w, n, splits, st);
+    run_layers(s, w, n, splits, true, st);
     launch_rmsnorm_rows(w.h, H, n, H, s->final_norm, cf.rms_eps, w.normed, H, st);
     if (heads) {
       bool same = true;
@@ -707,8 +756,8 @@ extern "C" int q3h_forward_embeds_batch(q3h_context *const *ctxs, int n, const f
 // ---------------------------------------------------------------------------
 // measurement: the weight products of one decode step, graph-replayed
 
-extern "C" int q3h_stack_time_gemv(q3h_stack *s, int head, int iters, float *us_per_launch,
-                                   int *launches, int64_t *bytes) {
+extern "C" int q3h_stack_time_gemv(q3h_stack *s, int head, int iters, int use_graph,
+                                   float *us_per_launch, int *launches, int64_t *bytes) {
   Work w;
   hipStream_t st = nullptr;
   hipGraph_t graph = nullptr;
@@ -737,36 +786,50 @@ extern "C" int q3h_stack_time_gemv(q3h_stack *s, int head, int iters, float *us_
     };
     int n = 0;
     int64_t b = 0;
-    check_hip(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "capture");
-    for (int l = 0; l < c.layers; l++) {
-      const Layer &L = s->layers[l];
-      launch_gemv(make_gemv(L.qkv, w.h, H, 1, L.in_norm, c.rms_eps, w.qkv, ldq), EPI_STORE, q8,
-                  st);
-      launch_gemv(make_gemv(L.o, w.att, NQ, 1, nullptr, 0.f, w.h, H), EPI_ADD, q8, st);
-      launch_gemv(make_gemv(L.gu, w.h, H, 1, L.post_norm, c.rms_eps, w.act, I), EPI_SWIGLU, q8,
-                  st);
-      launch_gemv(make_gemv(L.down, w.act, I, 1, nullptr, 0.f, w.h, H), EPI_ADD, q8, st);
-      n += 4;
-      b += mat_bytes(L.qkv) + mat_bytes(L.o) + mat_bytes(L.gu) + mat_bytes(L.down);
-      // norm vectors, inputs read, outputs written (the residual adds read y too)
-      b += 4 * (int64_t)(2 * H) + 4 * (int64_t)(H + ldq) + 4 * (int64_t)(NQ + 2 * H) +
-           4 * (int64_t)(H + I) + 4 * (int64_t)(I + 2 * H);
+    auto enqueue = [&] {
+      n = 0;
+      b = 0;
+      for (int l = 0; l < c.layers; l++) {
+        const Layer &L = s->layers[l];
+        launch_gemv(make_gemv(L.qkv, w.h, H, 1, L.in_norm, c.rms_eps, w.qkv, ldq), EPI_STORE,
+                    q8, st);
+        launch_gemv(make_gemv(L.o, w.att, NQ, 1, nullptr, 0.f, w.h, H), EPI_ADD, q8, st);
+        launch_gemv(make_gemv(L.gu, w.h, H, 1, L.post_norm, c.rms_eps, w.act, I), EPI_SWIGLU,
+                    q8, st);
+        launch_gemv(make_gemv(L.down, w.act, I, 1, nullptr, 0.f, w.h, H), EPI_ADD, q8, st);
+        n += 4;
+        b += mat_bytes(L.qkv) + mat_bytes(L.o) + mat_bytes(L.gu) + mat_bytes(L.down);
+        // norm vectors, inputs read, outputs written (the residual adds read y too)
+        b += 4 * (int64_t)(2 * H) + 4 * (int64_t)(H + ldq) + 4 * (int64_t)(NQ + 2 * H) +
+             4 * (int64_t)(H + I) + 4 * (int64_t)(I + 2 * H);
+      }
+      if (head >= 0) {
+        launch_gemv(make_gemv(s->heads[head], w.normed, H, 1, nullptr, 0.f, w.logits, head_rows),
+                    EPI_STORE, q8, st);
+        n += 1;
+        b += mat_bytes(s->heads[head]) + 4 * (int64_t)(H + head_rows);
+      }
+    };
+    if (use_graph) {
+      check_hip(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "capture");
+      enqueue();
+      check_hip(hipStreamEndCapture(st, &graph), "end capture");
+      check_hip(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "instantiate");
     }
-    if (head >= 0) {
-      launch_gemv(make_gemv(s->heads[head], w.normed, H, 1, nullptr, 0.f, w.logits, head_rows),
-                  EPI_STORE, q8, st);
-      n += 1;
-      b += mat_bytes(s->heads[head]) + 4 * (int64_t)(H + head_rows);
-    }
-    check_hip(hipStreamEndCapture(st, &graph), "end capture");
-    check_hip(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "instantiate");
+    auto once = [&] {
+      if (use_graph)
+        check_hip(hipGraphLaunch(exec, st), "graph launch");
+      else
+        enqueue();
+    };
     check_hip(hipEventCreate(&e0), "event");
     check_hip(hipEventCreate(&e1), "event");
-    for (int i = 0; i < 2; i++) check_hip(hipGraphLaunch(exec, st), "warm-up");
+    for (int i = 0; i < 2; i++) once();
     check_hip(hipEventRecord(e0, st), "event record");
-    for (int i = 0; i < iters; i++) check_hip(hipGraphLaunch(exec, st), "graph launch");
+    for (int i = 0; i < iters; i++) once();
     check_hip(hipEventRecord(e1, st), "event record");
     check_hip(hipEventSynchronize(e1), "event sync");
+    check_hip(hipGetLastError(), "gemv kernels");
     float ms = 0.f;
     check_hip(hipEventElapsedTime(&ms, e0, e1), "elapsed");
     *us_per_launch = ms * 1000.f / ((float)iters * n);

@@ -22,7 +22,7 @@ struct q3h_device {
 namespace q3h {
 
 constexpr int kAttnChunk = 256;  // positions per attention split (k_attention)
-constexpr int kMaxGroup = 4;     // q heads per kv head
+constexpr int kMaxGroup = 4;     // q heads per kv head (1, 2 or 4)
 
 struct Error {
   int code;
@@ -72,6 +72,7 @@ struct Work {
   float *logits = nullptr;  // [rows][head rows]
   RowDesc *rd = nullptr;    // [rows]
   float *part = nullptr;    // attention partials [rows][heads][splits][head_dim + 2]
+  int *tickets = nullptr;   // attention split tickets [rows][kv_heads], zero
   CtxDev **ctx_arr = nullptr;
   void ensure(const struct ::q3h_stack *s, int rows, int splits, int head_rows);
   void release();
@@ -80,7 +81,19 @@ struct Work {
 int attention_splits(int positions);
 GemvArgs make_gemv(const Mat &W, const float *x, int ldx, int M, const float *norm_w, float eps,
                    float *y, int ldy);
-void run_layers(const struct ::q3h_stack *s, Work &w, int M, int splits, hipStream_t st);
+// the shapes the fused code-predictor kernel takes (Q8_0, hidden 1024,
+// 16 / 8 heads of 128)
+bool cp_fused_supported(const q3h_stack_config &c);
+
+// one new row at position pos of a code-predictor context (16 positions)
+// through the layers of stack s, attention fused into o_proj; the row is in
+// w.h and stays there (cp_fused_supported(s->cfg), ctx->max_pos == 16)
+void run_cp_fused(const struct ::q3h_stack *s, Work &w, const struct ::q3h_context *ctx,
+                  int pos, hipStream_t st);
+
+// fused: every row is the single new position of its own context
+void run_layers(const struct ::q3h_stack *s, Work &w, int M, int splits, bool fused,
+                hipStream_t st);
 
 }  // namespace q3h
 

@@ -1,0 +1,249 @@
+// q3h_cp.hip - the code predictor's single-row step, attention fused into the
+// output projection.
+//
+// A code-predictor context holds at most 16 positions (one frame's codes), so
+// its attention is cheap enough to be recomputed by every workgroup of the
+// o_proj product. One launch does, for the new row at position pos of one
+// context:
+//   QK-norm + RoPE of the 16 query heads and 8 keys (rows of the raw q/k/v
+//   product), the K/V append at pos (workgroup 0 writes it; every workgroup
+//   uses its own copy for that position), causal softmax attention over
+//   positions 0..pos, then h[rows] += Wo[rows] . attention for the workgroup's
+//   16 rows of Wo (Q8_0).
+// That is one launch instead of two (attention, o_proj) and no attention
+// output round trip through memory; every workgroup computes the same
+// attention, so the result does not depend on scheduling.
+//
+// Shape (the Qwen3-TTS code predictor): hidden 1024, 16 query heads and 8 kv
+// heads of 128, 16 positions. 64 workgroups of 8 waves; wave w serves kv head
+// w for the attention, then rows row0 + 2w, row0 + 2w + 1 of Wo.
+//
+// Layouts: K/V cache of the layer [8][16][128] (kl), values at kl + v_off;
+// q_norm then k_norm (qkn); the RoPE (cos, sin) row of pos (rope); Wo quants
+// [1024][2048] followed by their fp16 scales [1024][64].
+#include <hip/hip_runtime.h>
+
+#include "q3h.h"
+#include "q3h_internal.h"
+#include "q3h_wave.h"
+
+namespace q3h {
+
+namespace {
+
+constexpr int HD = 128, KVH = 8, GRP = 2, NQ = KVH * GRP * HD, HID = 1024;
+constexpr int P = 16;     // positions of a code-predictor context
+constexpr int ROWS = 16;  // o_proj rows per workgroup
+constexpr int NT = 512;   // 8 waves
+constexpr int NBO = NQ / 32;
+
+__device__ __forceinline__ void ld32(const float *p, float *o) {
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const float4 t = reinterpret_cast<const float4 *>(p)[i];
+    o[4 * i] = t.x;
+    o[4 * i + 1] = t.y;
+    o[4 * i + 2] = t.z;
+    o[4 * i + 3] = t.w;
+  }
+}
+
+__device__ __forceinline__ void ld32(const _Float16 *p, float *o) {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const h8 t = reinterpret_cast<const h8 *>(p)[i];
+#pragma unroll
+    for (int j = 0; j < 8; j++) o[8 * i + j] = (float)t[j];
+  }
+}
+
+__device__ __forceinline__ float2 ld2(const float *p) { return *reinterpret_cast<const float2 *>(p); }
+
+__device__ __forceinline__ float2 ld2(const _Float16 *p) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 t = *reinterpret_cast<const h2 *>(p);
+  return make_float2((float)t[0], (float)t[1]);
+}
+
+__device__ __forceinline__ float dot4(int w, float4 x, float acc) {
+  acc = fmaf((float)(int8_t)(w), x.x, acc);
+  acc = fmaf((float)(int8_t)(w >> 8), x.y, acc);
+  acc = fmaf((float)(int8_t)(w >> 16), x.z, acc);
+  acc = fmaf((float)(int8_t)(w >> 24), x.w, acc);
+  return acc;
+}
+
+// RMSNorm over a head (lanes hold elements lane, lane + 64), weight (w0, w1),
+// then rotate_half RoPE with (cos, sin) = cs
+__device__ __forceinline__ void norm_rope(float &x0, float &x1, float w0, float w1, float2 cs,
+                                          float eps) {
+  const double ss = wave_sum_dpp_d((double)x0 * x0 + (double)x1 * x1);
+  const float inv = (float)(1.0 / sqrt(ss / HD + (double)eps));
+  const float a = w0 * (x0 * inv), b = w1 * (x1 * inv);
+  x0 = a * cs.x - b * cs.y;
+  x1 = b * cs.x + a * cs.y;
+}
+
+template <typename KV>
+__global__ __launch_bounds__(NT) void k_attn_o_cp(const int8_t *__restrict__ wo,
+                                                  const float *__restrict__ qkv,
+                                                  KV *__restrict__ kl, float *__restrict__ h,
+                                                  const float *__restrict__ qkn,
+                                                  const float2 *__restrict__ rope, int pos,
+                                                  int v_off, float eps) {
+  __shared__ float att[NQ];
+  __shared__ float qs[KVH][GRP][HD];
+  __shared__ float kvs[KVH][2][HD];  // the new key and value of each kv head
+  __shared__ float ps[KVH][GRP][P];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int row0 = blockIdx.x * ROWS + 2 * w;
+  const _Float16 *wd = reinterpret_cast<const _Float16 *>(wo + (size_t)HID * NQ);
+
+  // 1. every load up front: Wo rows, the residual, the raw q/k/v of kv head
+  // w, the norm weights, the RoPE row, the cached keys and values
+  int4 wv[2][2];
+  float sc[2][2];
+#pragma unroll
+  for (int r = 0; r < 2; r++)
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      wv[r][c] = *reinterpret_cast<const int4 *>(wo + (size_t)(row0 + r) * NQ + c * 1024 + lane * 16);
+      sc[r][c] = (float)wd[(size_t)(row0 + r) * NBO + c * 32 + (lane >> 1)];
+    }
+  const float h0 = h[row0], h1 = h[row0 + 1];
+  float xq[GRP][2], xk[2], xv[2];
+#pragma unroll
+  for (int j = 0; j < GRP; j++) {
+    xq[j][0] = qkv[(w * GRP + j) * HD + lane];
+    xq[j][1] = qkv[(w * GRP + j) * HD + lane + 64];
+  }
+  xk[0] = qkv[NQ + w * HD + lane];
+  xk[1] = qkv[NQ + w * HD + lane + 64];
+  xv[0] = qkv[NQ + KVH * HD + w * HD + lane];
+  xv[1] = qkv[NQ + KVH * HD + w * HD + lane + 64];
+  const float qn0 = qkn[lane], qn1 = qkn[lane + 64];
+  const float kn0 = qkn[HD + lane], kn1 = qkn[HD + lane + 64];
+  const float2 cs = rope[lane];
+  KV *kh = kl + (size_t)w * P * HD;
+  KV *vh = kl + v_off + (size_t)w * P * HD;
+  // keys: lane 4p + j holds dims 32j .. 32j + 31 of key p
+  const int kp = lane >> 2, kj = lane & 3;
+  float kk[32];
+  if (kp < pos) ld32(kh + (size_t)kp * HD + kj * 32, kk);
+  // values: lane holds dims 2 lane, 2 lane + 1 of every cached position
+  float2 vv[P];
+#pragma unroll
+  for (int p = 0; p < P; p++)
+    if (p < pos) vv[p] = ld2(vh + (size_t)p * HD + 2 * lane);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. QK-norm + RoPE; the new key and value rounded as the cache holds them
+#pragma unroll
+  for (int j = 0; j < GRP; j++) {
+    float x0 = xq[j][0], x1 = xq[j][1];
+    norm_rope(x0, x1, qn0, qn1, cs, eps);
+    qs[w][j][lane] = x0;
+    qs[w][j][lane + 64] = x1;
+  }
+  {
+    float x0 = xk[0], x1 = xk[1];
+    norm_rope(x0, x1, kn0, kn1, cs, eps);
+    const KV k0 = (KV)x0, k1 = (KV)x1, v0 = (KV)xv[0], v1 = (KV)xv[1];
+    kvs[w][0][lane] = (float)k0;
+    kvs[w][0][lane + 64] = (float)k1;
+    kvs[w][1][lane] = (float)v0;
+    kvs[w][1][lane + 64] = (float)v1;
+    if (blockIdx.x == 0) {
+      kh[(size_t)pos * HD + lane] = k0;
+      kh[(size_t)pos * HD + lane + 64] = k1;
+      vh[(size_t)pos * HD + lane] = v0;
+      vh[(size_t)pos * HD + lane + 64] = v1;
+    }
+  }
+  __syncthreads();
+
+  // 3. scores of key kp for both query heads, softmax over positions 0..pos
+  const float scale = (float)(1.0 / sqrt((double)HD));
+  const bool live = kp <= pos;
+#pragma unroll
+  for (int j = 0; j < GRP; j++) {
+    const float *q = &qs[w][j][kj * 32];
+    const float *knew = &kvs[w][0][kj * 32];
+    float a = 0.f;
+    if (kp < pos) {
+#pragma unroll
+      for (int i = 0; i < 32; i++) a = fmaf(q[i], kk[i], a);
+    } else if (kp == pos) {
+#pragma unroll
+      for (int i = 0; i < 32; i++) a = fmaf(q[i], knew[i], a);
+    }
+    a += dpp_f<kQuadXor1>(a);
+    a += dpp_f<kQuadXor2>(a);
+    const float s = live ? a * scale : -INFINITY;
+    const float mx = wave_max_dpp(s);
+    const float e = live ? expf(s - mx) : 0.f;
+    const float sum = wave_sum_dpp(kj == 0 ? e : 0.f);
+    if (kj == 0) ps[w][j][kp] = e * (1.0f / sum);
+  }
+  __syncthreads();
+
+  // 4. outputs of both heads: lane holds dims 2 lane, 2 lane + 1
+#pragma unroll
+  for (int j = 0; j < GRP; j++) {
+    float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+      if (p < pos) {
+        const float pw = ps[w][j][p];
+        o0 = fmaf(pw, vv[p].x, o0);
+        o1 = fmaf(pw, vv[p].y, o1);
+      }
+    }
+    const float pw = ps[w][j][pos];
+    o0 = fmaf(pw, kvs[w][1][2 * lane], o0);
+    o1 = fmaf(pw, kvs[w][1][2 * lane + 1], o1);
+    att[(w * GRP + j) * HD + 2 * lane] = o0;
+    att[(w * GRP + j) * HD + 2 * lane + 1] = o1;
+  }
+  __syncthreads();
+
+  // 5. h[row] += Wo[row] . att for this wave's two rows
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const float4 *xp = reinterpret_cast<const float4 *>(att + c * 1024 + lane * 16);
+      float p0 = dot4(wv[r][c].x, xp[0], 0.f);
+      float p1 = dot4(wv[r][c].y, xp[1], 0.f);
+      p0 = dot4(wv[r][c].z, xp[2], p0);
+      p1 = dot4(wv[r][c].w, xp[3], p1);
+      acc = fmaf(sc[r][c], p0 + p1, acc);
+    }
+    acc = wave_sum_dpp(acc);
+    if (lane == 0) h[row0 + r] = (r == 0 ? h0 : h1) + acc;
+  }
+}
+
+}  // namespace
+
+bool cp_fused_supported(const q3h_stack_config &c) {
+  return c.dtype == Q3H_Q8_0 && c.hidden == HID && c.heads == KVH * GRP && c.kv_heads == KVH &&
+         c.head_dim == HD;
+}
+
+void launch_attn_o_cp(const Mat &wo, const float *qkv, void *k_layer, int v_off, float *h,
+                      const float *qkn, const float *rope_row, int pos, float eps, bool kv16,
+                      hipStream_t st) {
+  const dim3 grid(HID / ROWS), block(NT);
+  const float2 *rope = reinterpret_cast<const float2 *>(rope_row);
+  if (kv16)
+    hipLaunchKernelGGL(k_attn_o_cp<_Float16>, grid, block, 0, st, wo.q, qkv,
+                       static_cast<_Float16 *>(k_layer), h, qkn, rope, pos, v_off, eps);
+  else
+    hipLaunchKernelGGL(k_attn_o_cp<float>, grid, block, 0, st, wo.q, qkv,
+                       static_cast<float *>(k_layer), h, qkn, rope, pos, v_off, eps);
+}
+
+}  // namespace q3h

@@ -120,19 +120,25 @@ __global__ __launch_bounds__(kArgBlock) void k_choose_code0(FrameDev f) {
 
 // ChooseCode for group g + 1 (argmax of the head-g logits), then the input row
 // of the next code-predictor forward: pred_emb[g][code]. One block per stream.
-__global__ __launch_bounds__(kArgBlock) void k_cp_argmax(FrameDev f, int g) {
+// Plain scalar arguments (preloaded into SGPRs).
+__global__ __launch_bounds__(kArgBlock) void k_cp_argmax(const float *__restrict__ cp_logits,
+                                                         const int *__restrict__ alive,
+                                                         const float *__restrict__ pred_emb,
+                                                         float *__restrict__ cp_h,
+                                                         int *__restrict__ codes, int cp_vocab,
+                                                         int groups, int H, int g) {
   const int s = blockIdx.x, tid = threadIdx.x;
-  if (!f.alive[s]) return;
-  const float *lg = f.cp_logits + (size_t)s * f.cp_vocab;
+  if (!alive[s]) return;
+  const float *lg = cp_logits + (size_t)s * cp_vocab;
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int i = tid; i < f.cp_vocab; i += kArgBlock) argmax_merge(bv, bi, lg[i], i);
+  for (int i = tid; i < cp_vocab; i += kArgBlock) argmax_merge(bv, bi, lg[i], i);
   const int code = block_argmax(bv, bi);
-  if (tid == 0) f.codes[(size_t)s * f.groups + g + 1] = code;
-  if (g + 1 < f.groups - 1) {
-    const float *emb = f.pred_emb + ((size_t)g * f.cp_vocab + code) * f.H;
-    float *x = f.cp_h + (size_t)s * f.H;
-    for (int c = tid; c < f.H; c += kArgBlock) x[c] = emb[c];
+  if (tid == 0) codes[(size_t)s * groups + g + 1] = code;
+  if (g + 1 < groups - 1) {
+    const float *emb = pred_emb + ((size_t)g * cp_vocab + code) * H;
+    float *x = cp_h + (size_t)s * H;
+    for (int c = tid; c < H; c += kArgBlock) x[c] = emb[c];
   }
 }
 
@@ -217,26 +223,40 @@ void enqueue_step(q3h_frame *f, int splits, hipStream_t st) {
   FrameDev fd = f->fd;
   hipLaunchKernelGGL(k_choose_code0, dim3(n), dim3(kArgBlock), 0, st, fd);
   // code predictor: 2 rows per stream, then one row per group
+  // one stream on the Qwen3-TTS shapes: steps 1.. run the fused single-row
+  // path (positions are fixed: step g adds position g + 1)
+  const bool fused = n == 1 && cp_fused_supported(cp->cfg) && f->cctx[0]->max_pos == 16;
   for (int g = 0; g < c.groups - 1; g++) {
     const int R = g == 0 ? 2 : 1;
-    launch_prep(f->c_arr, fd.alive, n, R, f->cw.rd, st);
-    run_layers(cp, f->cw, n * R, 1, st);
-    launch_rmsnorm_rows(f->cw.h + (size_t)(R - 1) * H, R * H, n, H, cp->final_norm,
-                        cp->cfg.rms_eps, f->cw.normed, H, st);
+    if (fused && g > 0) {
+      run_cp_fused(cp, f->cw, f->cctx[0], g + 1, st);
+    } else {
+      launch_prep(f->c_arr, fd.alive, n, R, f->cw.rd, st);
+      run_layers(cp, f->cw, n * R, 1, R == 1, st);
+      launch_advance(f->c_arr, fd.alive, n, R, st);
+    }
+    // final norm of each stream's last row + head g, one launch
     const Mat &head = cp->heads[c.cp_heads[g]];
-    GemvArgs a = make_gemv(head, f->cw.normed, H, n, nullptr, 0.f, f->cw.logits, c.cp_vocab);
+    GemvArgs a = make_gemv(head, f->cw.h + (size_t)(R - 1) * H, R * H, n, cp->final_norm,
+                           cp->cfg.rms_eps, f->cw.logits, c.cp_vocab);
     launch_gemv(a, EPI_STORE, cq8, st);
-    launch_advance(f->c_arr, fd.alive, n, R, st);
-    hipLaunchKernelGGL(k_cp_argmax, dim3(n), dim3(kArgBlock), 0, st, fd, g);
+    hipLaunchKernelGGL(k_cp_argmax, dim3(n), dim3(kArgBlock), 0, st, fd.cp_logits, fd.alive,
+                       fd.pred_emb, fd.cp_h, fd.codes, fd.cp_vocab, fd.groups, fd.H, g);
   }
   // the talker
   hipLaunchKernelGGL(k_talker_input, dim3((H + 255) / 256, n), dim3(256), 0, st, fd);
   launch_prep(f->t_arr, fd.alive, n, 1, f->tw.rd, st);
-  run_layers(tk, f->tw, n, splits, st);
-  launch_rmsnorm_rows(f->tw.h, H, n, H, tk->final_norm, tk->cfg.rms_eps, fd.past, H, st);
+  run_layers(tk, f->tw, n, splits, true, st);
   const Mat &th = tk->heads[c.talker_head];
-  GemvArgs a = make_gemv(th, fd.past, H, n, nullptr, 0.f, fd.logits, c.vocab);
-  launch_gemv(a, EPI_STORE, tq8, st);
+  if (n == 1) {  // final norm fused into the head, the normed state written alongside
+    GemvArgs a = make_gemv(th, f->tw.h, H, 1, tk->final_norm, tk->cfg.rms_eps, fd.logits, c.vocab);
+    a.xn_out = fd.past;
+    launch_gemv(a, EPI_STORE, tq8, st);
+  } else {
+    launch_rmsnorm_rows(f->tw.h, H, n, H, tk->final_norm, tk->cfg.rms_eps, fd.past, H, st);
+    GemvArgs a = make_gemv(th, fd.past, H, n, nullptr, 0.f, fd.logits, c.vocab);
+    launch_gemv(a, EPI_STORE, tq8, st);
+  }
   launch_advance(f->t_arr, fd.alive, n, 1, st);
   hipLaunchKernelGGL(k_frame_end, dim3((n + 63) / 64), dim3(64), 0, st, fd);
 }
@@ -378,12 +398,12 @@ extern "C" int q3h_frame_start(q3h_frame *f, int stream, const float *prefill, i
     check_hip(hipMemcpyAsync(w.h, prefill, sizeof(float) * rows * H, hipMemcpyHostToDevice, st),
               "upload prefill");
     launch_prep(tc->dev_arr, nullptr, 1, rows, w.rd, st);
-    run_layers(s, w, rows, splits, st);
+    run_layers(s, w, rows, splits, rows == 1, st);
     float *past = d.past + (size_t)stream * H;
-    launch_rmsnorm_rows(w.h + (size_t)(rows - 1) * H, H, 1, H, s->final_norm, s->cfg.rms_eps,
-                        past, H, st);
-    GemvArgs a = make_gemv(s->heads[c.talker_head], past, H, 1, nullptr, 0.f,
-                           d.logits + (size_t)stream * c.vocab, c.vocab);
+    GemvArgs a = make_gemv(s->heads[c.talker_head], w.h + (size_t)(rows - 1) * H, H, 1,
+                           s->final_norm, s->cfg.rms_eps, d.logits + (size_t)stream * c.vocab,
+                           c.vocab);
+    a.xn_out = past;
     launch_gemv(a, EPI_STORE, s->cfg.dtype == Q3H_Q8_0, st);
     launch_advance(tc->dev_arr, nullptr, 1, rows, st);
     check_hip(hipGetLastError(), "prefill kernels");

@@ -1,0 +1,366 @@
+// q3h_gemv.hip - the Q8_0 matrix-vector product of the decode step on gfx950,
+// for the widths of the Qwen3-TTS stacks: K = 1024, 2048 or 3072 columns and
+// N a multiple of 256 rows (q/k/v 4096 x 1024, o 1024 x 2048, gate/up
+// 6144 x 1024, down 1024 x 3072, heads 3072 / 2048 x 1024).
+//
+// One launch is 256 workgroups, one per CU: workgroup b owns N/256 consecutive
+// rows, spread over its waves (R rows per wave). The kernel is latency-bound
+// at these sizes (2-7 MB per launch), so its order of work is chosen to keep a
+// single memory round trip on the critical path:
+//   1. every lane issues all its weight loads first: for each of its rows and
+//      each 1024-column chunk, 16 quants (one dwordx4: a wave reads 1 KB of a
+//      row per instruction, coalesced) and the fp16 scale of their block;
+//   2. then the activation rows (and the RMSNorm weight) are loaded, w * x is
+//      staged in LDS and the sum of squares of x is reduced, while the weight
+//      loads are in flight;
+//   3. one barrier, then the dot products from registers and LDS, a wave
+//      reduction, and the epilogue (store, residual add, or SwiGLU of an
+//      interleaved gate/up row pair). The RMSNorm factor multiplies the dot:
+//      W (w * x * inv) = inv * (W (w * x)).
+// LDS layout of the staged rows: element c*1024 + l*16 + 4*i + j of a row sits
+// in float4 slot (c*4 + i)*64 + l, so the 64 lanes of a wave read 64
+// consecutive float4 (no bank conflict).
+//
+// A single activation row (the batch-1 decode step) takes a variant with no
+// LDS and no barrier: each lane loads the 16 activations of each chunk that
+// its own quants multiply (a wave reads the whole row, from L2), the RMSNorm
+// sum of squares is a wave reduction, and every wave is independent. The
+// normed row can also be written out (xn_out, by the first wave), so the
+// final norm of a stack and its head are one launch.
+#include <hip/hip_runtime.h>
+
+#include "q3h_internal.h"
+#include "q3h_wave.h"
+
+namespace q3h {
+
+namespace {
+
+constexpr int kMaxWaves = 16;
+constexpr int kMaxRowsX = 4;  // activation rows per launch
+#ifdef Q3H_GEMV_LDS_M1
+constexpr bool kLdsSingleRow = true;  // single rows staged in LDS too
+#else
+constexpr bool kLdsSingleRow = false;
+#endif
+
+__device__ __forceinline__ float wave_sum_f(float v) { return wave_sum_dpp(v); }
+
+__device__ __forceinline__ double wave_sum_dd(double v) { return wave_sum_dpp_d(v); }
+
+__device__ __forceinline__ float dot4_i8(int w, float4 x, float acc) {
+  acc = fmaf((float)(int8_t)(w), x.x, acc);
+  acc = fmaf((float)(int8_t)(w >> 8), x.y, acc);
+  acc = fmaf((float)(int8_t)(w >> 16), x.z, acc);
+  acc = fmaf((float)(int8_t)(w >> 24), x.w, acc);
+  return acc;
+}
+
+template <int R, int C, int MR, int EPI>
+__global__ __launch_bounds__(1024) void k_gemv_q8w(GemvArgs a) {
+  extern __shared__ float4 xs4[];  // [MR][C * 256], permuted
+  __shared__ double ssp[kMaxWaves][MR];
+  constexpr int K = C * 1024, NB = K / 32;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int W = blockDim.x >> 6;
+  const int row0 = (blockIdx.x * W + wave) * R;
+  const int M = a.M;
+
+  // 1. weights of this wave's rows
+  int4 wv[R][C];
+  float sc[R][C];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int row = min(row0 + r, a.N - 1);
+    const int8_t *q = a.wq + (size_t)row * K + lane * 16;
+    const _Float16 *d = a.wd + (size_t)row * NB + (lane >> 1);
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+      wv[r][c] = *reinterpret_cast<const int4 *>(q + c * 1024);
+      sc[r][c] = (float)d[c * 32];
+    }
+  }
+
+  // 2. stage w * x, sum of squares of x
+  const bool nrm = a.norm_w != nullptr;
+  double ss[MR];
+#pragma unroll
+  for (int m = 0; m < MR; m++) ss[m] = 0.0;
+  for (int f = tid; f < K / 4; f += 64 * W) {
+    const int li = (((f >> 8) * 4 + (f & 3)) << 6) + ((f & 255) >> 2);
+    const float4 wn = nrm ? reinterpret_cast<const float4 *>(a.norm_w)[f]
+                          : make_float4(1.f, 1.f, 1.f, 1.f);
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      if (m < M) {
+        const float4 v = reinterpret_cast<const float4 *>(a.x + (size_t)m * a.ldx)[f];
+        ss[m] += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z +
+                 (double)v.w * v.w;
+        xs4[m * (C * 256) + li] = make_float4(wn.x * v.x, wn.y * v.y, wn.z * v.z, wn.w * v.w);
+      }
+    }
+  }
+  if (nrm) {
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      const double t = wave_sum_dd(ss[m]);
+      if (lane == 0) ssp[wave][m] = t;
+    }
+  }
+  __syncthreads();
+  float inv[MR];
+#pragma unroll
+  for (int m = 0; m < MR; m++) {
+    inv[m] = 1.f;
+    if (nrm && m < M) {
+      double t = 0.0;
+      for (int i = 0; i < W; i++) t += ssp[i][m];
+      inv[m] = (float)(1.0 / sqrt(t / K + (double)a.eps));
+    }
+  }
+  if (a.xn_out != nullptr && blockIdx.x == 0) {
+    // the normed last row: w * x * inv, back from the permuted layout
+    const int m = M - 1;
+    for (int f = tid; f < K / 4; f += 64 * W) {
+      const int li = (((f >> 8) * 4 + (f & 3)) << 6) + ((f & 255) >> 2);
+      const float4 v = xs4[m * (C * 256) + li];
+      const float iv = inv[0];  // xn_out is taken with a single row only
+      reinterpret_cast<float4 *>(a.xn_out)[f] = make_float4(v.x * iv, v.y * iv, v.z * iv, v.w * iv);
+    }
+  }
+  if (row0 >= a.N) return;
+
+  // 3. dot products
+  float acc[R][MR];
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int m = 0; m < MR; m++) acc[r][m] = 0.f;
+#pragma unroll
+  for (int c = 0; c < C; c++) {
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      if (m < M) {
+        const float4 *xp = xs4 + m * (C * 256) + c * 256 + lane;
+        const float4 x0 = xp[0], x1 = xp[64], x2 = xp[128], x3 = xp[192];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          float p0 = dot4_i8(wv[r][c].x, x0, 0.f);
+          float p1 = dot4_i8(wv[r][c].y, x1, 0.f);
+          p0 = dot4_i8(wv[r][c].z, x2, p0);
+          p1 = dot4_i8(wv[r][c].w, x3, p1);
+          acc[r][m] = fmaf(sc[r][c], p0 + p1, acc[r][m]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int m = 0; m < MR; m++) acc[r][m] = wave_sum_f(acc[r][m]) * inv[m];
+
+  // 4. epilogue (every lane holds the sums; lane 0 stores)
+  if (lane != 0) return;
+#pragma unroll
+  for (int m = 0; m < MR; m++) {
+    if (m >= M) break;
+    float *y = a.y + (size_t)m * a.ldy;
+    if (EPI == EPI_SWIGLU) {
+#pragma unroll
+      for (int p = 0; p < R / 2; p++) {
+        const float g = acc[2 * p][m], u = acc[2 * p + 1][m];
+        y[row0 / 2 + p] = g / (1.0f + expf(-g)) * u;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        if (row0 + r < a.N) {
+          if (EPI == EPI_ADD)
+            y[row0 + r] += acc[r][m];
+          else
+            y[row0 + r] = acc[r][m];
+        }
+      }
+    }
+  }
+}
+
+// one activation row: no LDS, no barrier (see the header). Plain scalar
+// arguments, the pointers first: the first 16 argument dwords reach the waves
+// preloaded in SGPRs, so the weight loads issue without waiting on a scalar
+// memory read. W (waves per workgroup) is an argument: blockDim is not read.
+template <int R, int C, int EPI>
+__global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq,
+                                                   const _Float16 *__restrict__ wd,
+                                                   const float *__restrict__ x,
+                                                   const float *__restrict__ norm_w,
+                                                   float *__restrict__ y, float *__restrict__ xn_out,
+                                                   int N, int W, float eps) {
+  constexpr int K = C * 1024, NB = K / 32;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * W + wave) * R;
+
+  int4 wv[R][C];
+  float sc[R][C];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int row = min(row0 + r, N - 1);
+    const int8_t *q = wq + (size_t)row * K + lane * 16;
+    const _Float16 *d = wd + (size_t)row * NB + (lane >> 1);
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+      wv[r][c] = *reinterpret_cast<const int4 *>(q + c * 1024);
+      sc[r][c] = (float)d[c * 32];
+    }
+  }
+  float4 xv[C][4];
+#pragma unroll
+  for (int c = 0; c < C; c++)
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      xv[c][i] = reinterpret_cast<const float4 *>(x + c * 1024 + lane * 16)[i];
+  const bool nrm = norm_w != nullptr;
+  float4 wn[C][4];
+  if (nrm) {
+#pragma unroll
+    for (int c = 0; c < C; c++)
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        wn[c][i] = reinterpret_cast<const float4 *>(norm_w + c * 1024 + lane * 16)[i];
+  }
+  // every load above is issued before any arithmetic
+  __builtin_amdgcn_sched_barrier(0);
+  float inv = 1.f;
+  if (nrm) {
+    double ss = 0.0;
+#pragma unroll
+    for (int c = 0; c < C; c++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float4 v = xv[c][i];
+        ss += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+      }
+    ss = wave_sum_dpp_d(ss);
+    inv = (float)(1.0 / sqrt(ss / K + (double)eps));
+#pragma unroll
+    for (int c = 0; c < C; c++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float4 v = xv[c][i], w = wn[c][i];
+        xv[c][i] = make_float4(w.x * v.x, w.y * v.y, w.z * v.z, w.w * v.w);
+      }
+  }
+  if (xn_out != nullptr && blockIdx.x == 0 && wave == 0) {
+#pragma unroll
+    for (int c = 0; c < C; c++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float4 v = xv[c][i];
+        reinterpret_cast<float4 *>(xn_out + c * 1024 + lane * 16)[i] =
+            make_float4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
+      }
+  }
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    acc[r] = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+      float p0 = dot4_i8(wv[r][c].x, xv[c][0], 0.f);
+      float p1 = dot4_i8(wv[r][c].y, xv[c][1], 0.f);
+      p0 = dot4_i8(wv[r][c].z, xv[c][2], p0);
+      p1 = dot4_i8(wv[r][c].w, xv[c][3], p1);
+      acc[r] = fmaf(sc[r][c], p0 + p1, acc[r]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; r++) acc[r] = wave_sum_dpp(acc[r]) * inv;
+  if (lane != 0 || row0 >= N) return;
+  if (EPI == EPI_SWIGLU) {
+#pragma unroll
+    for (int p = 0; p < R / 2; p++) {
+      const float g = acc[2 * p], u = acc[2 * p + 1];
+      y[row0 / 2 + p] = g / (1.0f + expf(-g)) * u;
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      if (row0 + r < N) {
+        if (EPI == EPI_ADD)
+          y[row0 + r] += acc[r];
+        else
+          y[row0 + r] = acc[r];
+      }
+    }
+  }
+}
+
+template <int R, int C>
+void launch_v(const GemvArgs &a, int epi, int waves, hipStream_t st) {
+  const dim3 grid(a.N / (waves * R)), block(64 * waves);
+#define Q3H_V(E)                                                                              \
+  hipLaunchKernelGGL((k_gemv_q8v<R, C, E>), grid, block, 0, st, a.wq, a.wd, a.x, a.norm_w, a.y, \
+                     a.xn_out, a.N, waves, a.eps)
+  if (epi == EPI_STORE)
+    Q3H_V(EPI_STORE);
+  else if (epi == EPI_ADD)
+    Q3H_V(EPI_ADD);
+  else if (R % 2 == 0)
+    Q3H_V(EPI_SWIGLU);
+#undef Q3H_V
+}
+
+template <int R, int C, int MR>
+void launch_w(const GemvArgs &a, int epi, int waves, hipStream_t st) {
+  const dim3 grid(a.N / (waves * R)), block(64 * waves);
+  const size_t lds = sizeof(float4) * MR * C * 256;
+  if (epi == EPI_STORE)
+    hipLaunchKernelGGL((k_gemv_q8w<R, C, MR, EPI_STORE>), grid, block, lds, st, a);
+  else if (epi == EPI_ADD)
+    hipLaunchKernelGGL((k_gemv_q8w<R, C, MR, EPI_ADD>), grid, block, lds, st, a);
+  else if (R % 2 == 0)
+    hipLaunchKernelGGL((k_gemv_q8w<R, C, MR, EPI_SWIGLU>), grid, block, lds, st, a);
+}
+
+template <int R, int MR>
+void launch_rc(const GemvArgs &a, int epi, int waves, hipStream_t st) {
+  if (MR == 1 && !kLdsSingleRow) {
+    switch (a.K) {
+      case 1024: launch_v<R, 1>(a, epi, waves, st); break;
+      case 2048: launch_v<R, 2>(a, epi, waves, st); break;
+      default: launch_v<R, 3>(a, epi, waves, st); break;
+    }
+    return;
+  }
+  switch (a.K) {
+    case 1024: launch_w<R, 1, MR>(a, epi, waves, st); break;
+    case 2048: launch_w<R, 2, MR>(a, epi, waves, st); break;
+    default: launch_w<R, 3, MR>(a, epi, waves, st); break;
+  }
+}
+
+}  // namespace
+
+bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st) {
+  if (a.M < 1 || a.M > kMaxRowsX || (a.xn_out != nullptr && a.M != 1)) return false;
+  if (a.K != 1024 && a.K != 2048 && a.K != 3072) return false;
+  if (a.N % 256 != 0) return false;
+  const int rpb = a.N / 256;  // rows per workgroup, 256 workgroups
+  const int R = (epi == EPI_SWIGLU || rpb > 8) ? 2 : 1;
+  if (rpb % R != 0) return false;
+  const int waves = rpb / R;
+  if (waves < 1 || waves > kMaxWaves) return false;
+  const int MR = a.M == 1 ? 1 : (a.M == 2 ? 2 : 4);
+  if (R == 1) {
+    if (MR == 1) launch_rc<1, 1>(a, epi, waves, st);
+    else if (MR == 2) launch_rc<1, 2>(a, epi, waves, st);
+    else launch_rc<1, 4>(a, epi, waves, st);
+  } else {
+    if (MR == 1) launch_rc<2, 1>(a, epi, waves, st);
+    else if (MR == 2) launch_rc<2, 2>(a, epi, waves, st);
+    else launch_rc<2, 4>(a, epi, waves, st);
+  }
+  return true;
+}
+
+}  // namespace q3h

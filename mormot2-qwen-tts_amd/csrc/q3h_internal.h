@@ -8,20 +8,19 @@
 
 namespace q3h {
 
-// A matrix [N][K] on the device: Q8_0 as int8 quants [N][K] + fp16 scales
-// [N][K/32] (structure of arrays, so a wave reads 1 KB of quants per
-// instruction), or f32 [N][K].
+// A matrix [N][K] on the device: Q8_0 as int8 quants [N][K] followed, in the
+// same allocation, by the fp16 scales [N][K/32] (d == q + N*K; structure of
+// arrays, so a wave reads 1 KB of quants per instruction), or f32 [N][K].
 struct Mat {
   int N = 0, K = 0;
   int8_t *q = nullptr;
   _Float16 *d = nullptr;
   float *f = nullptr;
-  // a Q8_0 matrix also keeps its quants as one int8 row per 32-block for the
-  // int8 product path when the stack quantizes activations (same buffers)
 };
 
 // Per-row view of a K/V cache for the attention kernels. k, v: the cache of
-// layer 0, [layers][kv_heads][max_pos][head_dim] in f32 or f16; pos: the
+// layer 0, [layers][kv_heads][max_pos][head_dim] in f32 or f16 (one
+// allocation: v = k + layers*kv_heads*max_pos*head_dim elements); pos: the
 // position of the row (it attends to [0, pos]); pos < 0: inactive row.
 struct RowDesc {
   void *k;
@@ -61,6 +60,9 @@ struct QAct {
 };
 
 void launch_gemv(const GemvArgs &a, int epi, bool q8, hipStream_t st);
+// the wide Q8_0 kernel (K in {1024, 2048, 3072}, N % 256 == 0, M <= 4);
+// false when the shape is not one it takes (nothing launched)
+bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st);
 void launch_gemv_i8(const GemvArgs &a, const QAct &xa, int epi, hipStream_t st);
 void launch_quantize_act(const float *x, int ldx, int M, int K, const float *norm_w,
                          float eps, QAct out, hipStream_t st);
@@ -76,6 +78,36 @@ void launch_qk_rope_append(float *qkv, int ldq, const RowDesc *rd, int M, int la
 void launch_attention(const float *qkv, int ldq, const RowDesc *rd, int M, int layer,
                       int heads, int kvh, int hd, int splits, int chunk, float *out,
                       float *part, bool kv16, hipStream_t st);
+
+// decode attention (q3h_attn.hip): rows m of qkv [M][ldq] with descriptors
+// rd; fused: each row is the one new position of its own context (QK-norm,
+// RoPE and the K/V append in the prologue); otherwise q is already normed and
+// rotated in qkv and the cache holds every position (launch_qk_rope_append).
+struct AttnArgs {
+  const float *qkv;
+  int ldq;
+  const RowDesc *rd;
+  int layer, heads, kvh;
+  const float *qn, *kn;
+  float eps;
+  const float2 *rope_cs;
+  float *out;    // [M][heads * head_dim]
+  float *part;   // [M][heads][splits][head_dim + 2]
+  int *tickets;  // [M][kvh], zero between launches
+  int chunk;     // positions per split (0: the default, 256)
+};
+int attn_splits(int positions);
+// max_positions: the capacity of the stack's contexts (chooses the workgroup size)
+void launch_attn(const AttnArgs &a, int M, int splits, int max_positions, bool fused, bool kv16,
+                 hipStream_t st);
+
+// the code predictor's fused attention + o_proj + residual (q3h_cp.hip):
+// one context of 16 positions, the new row at pos; k_layer: the layer's keys,
+// values at k_layer + v_off elements; qkn: q_norm then k_norm; rope_row: the
+// (cos, sin) row of pos
+void launch_attn_o_cp(const Mat &wo, const float *qkv, void *k_layer, int v_off, float *h,
+                      const float *qkn, const float *rope_row, int pos, float eps, bool kv16,
+                      hipStream_t st);
 
 void launch_rmsnorm_rows(const float *x, int ldx, int M, int K, const float *w, float eps,
                          float *y, int ldy, hipStream_t st);

@@ -259,6 +259,8 @@ void launch_gemv(const GemvArgs &a0, int epi, bool q8, hipStream_t st) {
     a.x = a0.x + (size_t)m0 * a0.ldx;
     a.y = a0.y + (size_t)m0 * a0.ldy;
     a.xn_out = (m0 + a.M == a0.M) ? a0.xn_out : nullptr;
+    // the Qwen3-TTS widths: one workgroup per CU, loads issued up front
+    if (q8 && launch_gemv_q8_wide(a, epi, st)) continue;
     const int waves = a.N;  // with RPW = 1
     if (epi == EPI_SWIGLU || waves >= 8192)
       gemv_dispatch<4>(a, epi, q8, st);

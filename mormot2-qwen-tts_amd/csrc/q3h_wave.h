@@ -1,0 +1,92 @@
+// q3h_wave.h - wavefront (64-lane) reductions for gfx950 built on DPP row
+// operations instead of LDS permutes: a sum is six DPP adds (quad swaps,
+// half-row and row mirrors, row broadcasts 15 and 31) and a read of lane 63.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace q3h {
+
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf, false));
+}
+
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ int dpp_i(int v, int old) {
+  return __builtin_amdgcn_update_dpp(old, v, CTRL, ROW_MASK, 0xf, false);
+}
+
+// DPP controls (gfx9)
+constexpr int kQuadXor1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kHalfMirror = 0x141;
+constexpr int kRowMirror = 0x140;
+constexpr int kBcast15 = 0x142;
+constexpr int kBcast31 = 0x143;
+
+// sum over the 64 lanes, returned in every lane (all lanes must be active)
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_f<kQuadXor1>(v);
+  v += dpp_f<kQuadXor2>(v);
+  v += dpp_f<kHalfMirror>(v);
+  v += dpp_f<kRowMirror>(v);
+  v += dpp_f<kBcast15, 0xa>(v);
+  v += dpp_f<kBcast31, 0xc>(v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+__device__ __forceinline__ double dpp_d_step(double v, int which) {
+  // one DPP step on both halves of a double; which selects the control
+  const long long b = __builtin_bit_cast(long long, v);
+  int lo = (int)b, hi = (int)(b >> 32);
+  switch (which) {
+    case 0: lo = dpp_i<kQuadXor1>(lo, 0); hi = dpp_i<kQuadXor1>(hi, 0); break;
+    case 1: lo = dpp_i<kQuadXor2>(lo, 0); hi = dpp_i<kQuadXor2>(hi, 0); break;
+    case 2: lo = dpp_i<kHalfMirror>(lo, 0); hi = dpp_i<kHalfMirror>(hi, 0); break;
+    case 3: lo = dpp_i<kRowMirror>(lo, 0); hi = dpp_i<kRowMirror>(hi, 0); break;
+    case 4: lo = dpp_i<kBcast15, 0xa>(lo, 0); hi = dpp_i<kBcast15, 0xa>(hi, 0); break;
+    default: lo = dpp_i<kBcast31, 0xc>(lo, 0); hi = dpp_i<kBcast31, 0xc>(hi, 0); break;
+  }
+  return __builtin_bit_cast(double, ((long long)hi << 32) | (unsigned int)lo);
+}
+
+// double sum over the 64 lanes, returned in every lane
+__device__ __forceinline__ double wave_sum_dpp_d(double v) {
+#pragma unroll
+  for (int i = 0; i < 6; i++) v += dpp_d_step(v, i);
+  const long long b = __builtin_bit_cast(long long, v);
+  const int lo = __builtin_amdgcn_readlane((int)b, 63);
+  const int hi = __builtin_amdgcn_readlane((int)(b >> 32), 63);
+  return __builtin_bit_cast(double, ((long long)hi << 32) | (unsigned int)lo);
+}
+
+// DPP move where lanes outside the row mask keep their own value (the
+// identity of max)
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_f_keep(float v) {
+  const int b = __builtin_bit_cast(int, v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(b, b, CTRL, ROW_MASK, 0xf, false));
+}
+
+// maximum over the 64 lanes, returned in every lane
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_f_keep<kQuadXor1>(v));
+  v = fmaxf(v, dpp_f_keep<kQuadXor2>(v));
+  v = fmaxf(v, dpp_f_keep<kHalfMirror>(v));
+  v = fmaxf(v, dpp_f_keep<kRowMirror>(v));
+  v = fmaxf(v, dpp_f_keep<kBcast15, 0xa>(v));
+  v = fmaxf(v, dpp_f_keep<kBcast31, 0xc>(v));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// sum over aligned groups of 8 lanes (lanes 8k..8k+7), in every lane of the group
+__device__ __forceinline__ float group8_sum_dpp(float v) {
+  v += dpp_f<kQuadXor1>(v);
+  v += dpp_f<kQuadXor2>(v);
+  v += dpp_f<kHalfMirror>(v);
+  return v;
+}
+
+}  // namespace q3h

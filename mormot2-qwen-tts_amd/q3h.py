@@ -110,7 +110,7 @@ SIGNATURES = {
     "q3h_frame_state": (_I, [_P, _I, _FP, _FP]),
     "q3h_frame_destroy": (_I, [_P]),
     "q3h_quantize_row_q8_0": (_I, [_FP, _P, ctypes.c_int64]),
-    "q3h_stack_time_gemv": (_I, [_P, _I, _I, _FP, ctypes.POINTER(_I),
+    "q3h_stack_time_gemv": (_I, [_P, _I, _I, _I, _FP, ctypes.POINTER(_I),
                                  ctypes.POINTER(ctypes.c_int64)]),
 }
 
@@ -220,13 +220,14 @@ class Stack:
     def bytes(self):
         return lib().q3h_stack_bytes(self.h)
 
-    def time_gemv(self, head=-1, iters=20):
+    def time_gemv(self, head=-1, iters=20, use_graph=True):
         """(us per launch, launches per step, algorithmic bytes per step) of the
-        graph-replayed weight products of one single-row decode step."""
+        weight products of one single-row decode step, graph-replayed or
+        launched directly."""
         us = ctypes.c_float()
         n = ctypes.c_int()
         b = ctypes.c_int64()
-        _check(lib().q3h_stack_time_gemv(self.h, head, iters, ctypes.byref(us), ctypes.byref(n),
+        _check(lib().q3h_stack_time_gemv(self.h, head, iters, int(use_graph), ctypes.byref(us), ctypes.byref(n),
                                          ctypes.byref(b)))
         return us.value, n.value, b.value
 
@@ -262,9 +263,10 @@ class Context:
             x = x[None, :]
         rows, hidden = x.shape
         logits = None
-        if head >= 0 and want_logits:
+        if 0 <= head < len(self.stack.head_rows) and want_logits:
             logits = np.empty(self.stack.head_rows[head], dtype=np.float32)
         normed = np.empty(hidden, dtype=np.float32) if want_normed else None
+        # an unknown head index goes to the library, which reports it
         _check(lib().q3h_forward_embeds(self.h, _fp(x), rows, head, _fp(logits), _fp(normed)))
         return logits, normed
 

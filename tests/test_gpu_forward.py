@@ -79,33 +79,49 @@ def test_q8_talker_prefill_and_greedy_decode(q8model, q3h, q3o, synth):
 def test_predictor_f32_lcg_inputs(device, q3h, q3o, synth, kv_f16):
     """The reference's PredictorOnGpuMatchesCpu (tests/test.tts.qwen.vulkan.pas:
     150-232): f32 code predictor, 15 steps of LCG inputs (2 rows, then 1 per
-    group), head g at step g; logits and states within 1e-4 of the CPU path."""
+    group), head g at step g, logits and states relative to peak.
+
+    fp32 cache: 1e-4 against the oracle (the reference's bar). fp16 cache: the
+    reference's bar is 5e-2 against an fp32-cache CPU path (vulkan.pas:229);
+    here it is checked both ways: 5e-2 against the fp32-cache oracle and 1e-3
+    against the oracle that rounds its cache to half floats as well (one K/V
+    element rounded the other way is a 2^-11 relative step)."""
     print(f"case kv_f16={kv_f16}", flush=True)
     dims = synth.PREDICTOR
     L, f = synth.stack_weights(21, "talker.code_predictor.model.", dims, norm_std=0.1)
     heads = [synth.cp_head(21, g) for g in range(15)]
     st = q3h.Stack(device, dict(dims, dtype=q3h.F32, kv_f16=kv_f16, act_q8=0, max_positions=16),
                    L, f, q3h.F32)
-    for h in heads:
-        st.add_head(h, q3h.F32)
     ost = q3o.Stack(dims, L, f, q3o.F32, kv_f16=kv_f16)
-    ctx, octx = q3h.Context(st, 16), q3o.Ctx(ost, 16)
-    seed = 12345
-    worst = 0.0
-    for g in range(15):
-        rows = 2 if g == 0 else 1
-        x, seed = synth.lcg_rows(rows * 1024, seed)
-        lg, hs = ctx.forward(x.reshape(rows, 1024), head=g)
-        ohs = octx.forward(x.reshape(rows, 1024))
-        olg = ost.head(heads[g], ohs)
-        worst = max(worst, rel(lg, olg), rel(hs, ohs))
-    print(f"predictor f32 kv_f16={kv_f16}: worst {worst:.2e}")
-    assert worst <= 1e-4
-    assert ctx.length == 16
-    for o in (ctx, st):
-        o.destroy()
-    octx.destroy()
-    ost.destroy()
+    o32 = q3o.Stack(dims, L, f, q3o.F32, kv_f16=0)
+    ctx = octx = c32 = None
+    try:
+        for h in heads:
+            st.add_head(h, q3h.F32)
+        ctx, octx, c32 = q3h.Context(st, 16), q3o.Ctx(ost, 16), q3o.Ctx(o32, 16)
+        seed = 12345
+        worst = worst32 = 0.0
+        for g in range(15):
+            rows = 2 if g == 0 else 1
+            x, seed = synth.lcg_rows(rows * 1024, seed)
+            lg, hs = ctx.forward(x.reshape(rows, 1024), head=g)
+            ohs = octx.forward(x.reshape(rows, 1024))
+            olg = ost.head(heads[g], ohs)
+            worst = max(worst, rel(lg, olg), rel(hs, ohs))
+            h32 = c32.forward(x.reshape(rows, 1024))
+            worst32 = max(worst32, rel(lg, o32.head(heads[g], h32)), rel(hs, h32))
+        print(f"predictor f32 kv_f16={kv_f16}: worst {worst:.2e}, vs fp32 cache {worst32:.2e}")
+        if kv_f16:
+            assert worst <= 1e-3 and worst32 <= 5e-2
+        else:
+            assert worst <= 1e-4
+        assert ctx.length == 16
+    finally:
+        for o in (ctx, octx, c32):
+            if o is not None:
+                o.destroy()
+        for o in (st, ost, o32):
+            o.destroy()
 
 
 def test_batch_equals_single(q8model, q3h, synth):
