@@ -19,8 +19,10 @@ memory, so the wall clock of the K calls is the whole-job time.
 Beside it:
   roofline      the Q8_0 matrix-vector products of one talker decode step (28
                 layers x 4 products + the 3072-row head, 471.5 MB of weights,
-                more than the 256 MB Infinity Cache holds), graph-replayed and
-                timed with hipEvents on their stream inside the library;
+                more than the 256 MB Infinity Cache holds): the kernels' own
+                execution time from hipEvents attached to each launch on their
+                stream (the figure rocprofv3 reports per dispatch), and the
+                graph-replayed wall time per launch beside it;
   cpu_baseline  the oracle (the C restatement of the same frame step) on the
                 host cores, on a bounded sample of the same workload.
 
@@ -133,6 +135,25 @@ def cpu_baseline(f32, tables, pre, gpu_codes, budget_s, max_frames):
                        f"(prefill untimed), first {n} frames, {dt:.1f} s"), n, equal
 
 
+def gemv_roofline(ts, args):
+    """The dominant kernel: the Q8_0 matrix-vector products of one talker
+    decode step. achieved = algorithmic bytes per launch / the kernels' own
+    average execution time (events attached to each launch)."""
+    us, launches, nbytes = ts.time_gemv(head=0, iters=args.gemv_iters, mode=2)
+    per_launch = nbytes / launches
+    achieved = per_launch / (us * 1e-6) / 1e9
+    wall = None
+    if not args.no_graph:
+        wall, _, _ = ts.time_gemv(head=0, iters=args.gemv_iters, mode=1)
+    log(f"gemv: {launches} launches/step, kernel {us:.2f} us/launch "
+        f"({achieved:.0f} GB/s), graph wall {wall if wall is None else round(wall, 2)} us/launch")
+    return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
+                kernel="k_gemv_q8v (Q8_0 matrix-vector products of one talker decode step)",
+                bytes_per_launch=int(per_launch), us_per_launch=round(us, 3),
+                graph_wall_us_per_launch=None if wall is None else round(wall, 3))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -146,6 +167,8 @@ def main():
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the kernels directly instead of replaying hipGraphs "
                          "(for tracers that do not follow graph capture)")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="only the matrix-vector roofline measurement (profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -162,6 +185,13 @@ def main():
     max_pos = maxlen + max(steps, warmup) + 8
     dev = q3h.Device(0)
     ts, cs, tables, f32 = build_model(dev, args.seed, max_pos)
+    if args.gemv_only:
+        roofline = gemv_roofline(ts, args)
+        print(json.dumps({"roofline": roofline}), flush=True)
+        ts.destroy()
+        cs.destroy()
+        dev.close()
+        return 0
     frame = q3h.Frame(ts, cs, tables["codec_emb"], tables["pred_emb"], tables["tts_pad"],
                       n_streams=n, max_positions=max_pos, max_frames=max(steps, warmup) + 8,
                       use_graph=not args.no_graph)
@@ -171,16 +201,7 @@ def main():
     log(f"{fps:.1f} frames/s, {1e3 * total / steps:.3f} ms per step "
         f"(p50 {1e6 * np.median(lat):.0f} us, p99 {1e6 * np.percentile(lat, 99):.0f} us)")
 
-    # dominant kernel: the Q8_0 matrix-vector products of a talker decode step
-    us, launches, nbytes = ts.time_gemv(head=0, iters=args.gemv_iters,
-                                        use_graph=not args.no_graph)
-    per_launch = nbytes / launches
-    achieved = per_launch / (us * 1e-6) / 1e9
-    log(f"gemv: {launches} launches/step, {us:.2f} us/launch, {achieved:.0f} GB/s")
-    roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
-                    kernel="k_gemv_q8 (Q8_0 matrix-vector products of one talker decode step)",
-                    bytes_per_launch=int(per_launch), us_per_launch=round(us, 3))
+    roofline = gemv_roofline(ts, args)
 
     cpu = None
     parity = None

@@ -181,13 +181,15 @@ int q3h_quantize_row_q8_0(const float *x, void *y, int64_t k);
 
 /* no reference counterpart (measurement): the weight products of one
    single-row decode step of stack s - per layer the fused q/k/v, o, gate/up
-   and down matrix-vector products, then head `head` (-1: none) - captured in
-   a hipGraph and replayed iters times (use_graph = 1), or launched directly
-   iters times (use_graph = 0), between two hipEvents on one stream.
-   us_per_launch: elapsed / (iters * launches); launches: products per step;
-   bytes: algorithmic bytes per step (weights, norm vectors, input and output
-   vectors). The activations are zeros; the stack's contexts are untouched. */
-int q3h_stack_time_gemv(q3h_stack *s, int head, int iters, int use_graph, float *us_per_launch,
+   and down matrix-vector products, then head `head` (-1: none) - run iters
+   times on one stream. mode 0: launched directly, us_per_launch = wall time
+   between two hipEvents / launches; mode 1: captured in a hipGraph and
+   replayed, same wall-time measure; mode 2: every launch carries its own
+   start / end events (hipExtLaunchKernelGGL), us_per_launch = the average
+   execution time of the kernels themselves (Q8_0 stacks). launches: products
+   per step; bytes: algorithmic bytes per step (weights, norm vectors, input
+   and output vectors). The activations are zeros; contexts are untouched. */
+int q3h_stack_time_gemv(q3h_stack *s, int head, int iters, int mode, float *us_per_launch,
                         int *launches, int64_t *bytes);
 
 #ifdef __cplusplus

@@ -58,8 +58,8 @@ void Work::ensure(const q3h_stack *s, int rows, int splits, int head_rows) {
   logits = (float *)dev_alloc(sizeof(float) * R * (head_cap > 0 ? head_cap : 1));
   rd = (RowDesc *)dev_alloc(sizeof(RowDesc) * R);
   part = (float *)dev_alloc(sizeof(float) * R * c.heads * splits_cap * (c.head_dim + 2));
-  tickets = (int *)dev_alloc(sizeof(int) * R * c.kv_heads);
-  check_hip(hipMemset(tickets, 0, sizeof(int) * R * c.kv_heads), "zero tickets");
+  tickets = (int *)dev_alloc(sizeof(int) * R * c.heads);
+  check_hip(hipMemset(tickets, 0, sizeof(int) * R * c.heads), "zero tickets");
   ctx_arr = (CtxDev **)dev_alloc(sizeof(CtxDev *) * R);
 }
 
@@ -114,7 +114,7 @@ void run_layers(const q3h_stack *s, Work &w, int M, int splits, bool fused, hipS
     at.out = w.att;
     at.part = w.part;
     at.tickets = w.tickets;
-    launch_attn(at, M, splits, c.max_positions, fused, kv16, st);
+    launch_attn(at, M, splits, fused, kv16, st);
     // o_proj + residual
     a = make_gemv(L.o, w.att, NQ, M, nullptr, 0.f, w.h, H);
     launch_gemv(a, EPI_ADD, q8, st);
@@ -756,16 +756,18 @@ extern "C" int q3h_forward_embeds_batch(q3h_context *const *ctxs, int n, const f
 // ---------------------------------------------------------------------------
 // measurement: the weight products of one decode step, graph-replayed
 
-extern "C" int q3h_stack_time_gemv(q3h_stack *s, int head, int iters, int use_graph,
+extern "C" int q3h_stack_time_gemv(q3h_stack *s, int head, int iters, int mode,
                                    float *us_per_launch, int *launches, int64_t *bytes) {
   Work w;
   hipStream_t st = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   hipEvent_t e0 = nullptr, e1 = nullptr;
+  std::vector<hipEvent_t> kev;  // mode 2: a start and an end event per launch
   int rc = guard([&] {
     require(s && us_per_launch && launches && bytes && iters > 0, Q3H_E_ARG,
             "q3h_stack_time_gemv: invalid argument");
+    require(mode >= 0 && mode <= 2, Q3H_E_ARG, "q3h_stack_time_gemv: mode must be 0, 1 or 2");
     require(head >= -1 && head < (int)s->heads.size(), Q3H_E_ARG,
             "q3h_stack_time_gemv: no head " + std::to_string(head));
     check_hip(hipSetDevice(s->dev->ordinal), "hipSetDevice");
@@ -773,6 +775,8 @@ extern "C" int q3h_stack_time_gemv(q3h_stack *s, int head, int iters, int use_gr
     const int H = c.hidden, NQ = c.heads * c.head_dim, NKV = c.kv_heads * c.head_dim;
     const int I = c.intermediate, ldq = NQ + 2 * NKV;
     const bool q8 = c.dtype == Q3H_Q8_0;
+    require(mode != 2 || q8, Q3H_E_ARG,
+            "q3h_stack_time_gemv: kernel-attached timing needs a Q8_0 stack");
     const int head_rows = head >= 0 ? s->heads[head].N : 0;
     w.ensure(s, 1, 1, head_rows);
     check_hip(hipStreamCreateWithFlags(&st, hipStreamNonBlocking), "hipStreamCreate");
@@ -784,58 +788,85 @@ extern "C" int q3h_stack_time_gemv(q3h_stack *s, int head, int iters, int use_gr
     auto mat_bytes = [&](const Mat &m) {
       return q8 ? (int64_t)m.N * (m.K / 32) * 34 : (int64_t)m.N * m.K * 4;
     };
-    int n = 0;
-    int64_t b = 0;
-    auto enqueue = [&] {
-      n = 0;
-      b = 0;
-      for (int l = 0; l < c.layers; l++) {
-        const Layer &L = s->layers[l];
-        launch_gemv(make_gemv(L.qkv, w.h, H, 1, L.in_norm, c.rms_eps, w.qkv, ldq), EPI_STORE,
-                    q8, st);
-        launch_gemv(make_gemv(L.o, w.att, NQ, 1, nullptr, 0.f, w.h, H), EPI_ADD, q8, st);
-        launch_gemv(make_gemv(L.gu, w.h, H, 1, L.post_norm, c.rms_eps, w.act, I), EPI_SWIGLU,
-                    q8, st);
-        launch_gemv(make_gemv(L.down, w.act, I, 1, nullptr, 0.f, w.h, H), EPI_ADD, q8, st);
-        n += 4;
-        b += mat_bytes(L.qkv) + mat_bytes(L.o) + mat_bytes(L.gu) + mat_bytes(L.down);
-        // norm vectors, inputs read, outputs written (the residual adds read y too)
-        b += 4 * (int64_t)(2 * H) + 4 * (int64_t)(H + ldq) + 4 * (int64_t)(NQ + 2 * H) +
-             4 * (int64_t)(H + I) + 4 * (int64_t)(I + 2 * H);
-      }
-      if (head >= 0) {
-        launch_gemv(make_gemv(s->heads[head], w.normed, H, 1, nullptr, 0.f, w.logits, head_rows),
-                    EPI_STORE, q8, st);
-        n += 1;
-        b += mat_bytes(s->heads[head]) + 4 * (int64_t)(H + head_rows);
-      }
+    // the products of one step, in order, with their algorithmic bytes
+    struct Op {
+      GemvArgs a;
+      int epi;
     };
-    if (use_graph) {
-      check_hip(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "capture");
-      enqueue();
-      check_hip(hipStreamEndCapture(st, &graph), "end capture");
-      check_hip(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "instantiate");
+    std::vector<Op> ops;
+    int64_t b = 0;
+    for (int l = 0; l < c.layers; l++) {
+      const Layer &L = s->layers[l];
+      ops.push_back({make_gemv(L.qkv, w.h, H, 1, L.in_norm, c.rms_eps, w.qkv, ldq), EPI_STORE});
+      ops.push_back({make_gemv(L.o, w.att, NQ, 1, nullptr, 0.f, w.h, H), EPI_ADD});
+      ops.push_back({make_gemv(L.gu, w.h, H, 1, L.post_norm, c.rms_eps, w.act, I), EPI_SWIGLU});
+      ops.push_back({make_gemv(L.down, w.act, I, 1, nullptr, 0.f, w.h, H), EPI_ADD});
+      b += mat_bytes(L.qkv) + mat_bytes(L.o) + mat_bytes(L.gu) + mat_bytes(L.down);
+      // norm vectors, inputs read, outputs written (the residual adds read y too)
+      b += 4 * (int64_t)(2 * H) + 4 * (int64_t)(H + ldq) + 4 * (int64_t)(NQ + 2 * H) +
+           4 * (int64_t)(H + I) + 4 * (int64_t)(I + 2 * H);
     }
-    auto once = [&] {
-      if (use_graph)
-        check_hip(hipGraphLaunch(exec, st), "graph launch");
-      else
-        enqueue();
+    if (head >= 0) {
+      ops.push_back(
+          {make_gemv(s->heads[head], w.normed, H, 1, nullptr, 0.f, w.logits, head_rows), EPI_STORE});
+      b += mat_bytes(s->heads[head]) + 4 * (int64_t)(H + head_rows);
+    }
+    const int n = (int)ops.size();
+    auto enqueue = [&](bool timed) {
+      for (int i = 0; i < n; i++) {
+        if (timed)
+          require(launch_gemv_q8_wide(ops[i].a, ops[i].epi, st, kev[2 * i], kev[2 * i + 1]),
+                  Q3H_E_ARG, "q3h_stack_time_gemv: a product outside the single-row kernel");
+        else
+          launch_gemv(ops[i].a, ops[i].epi, q8, st);
+      }
     };
     check_hip(hipEventCreate(&e0), "event");
     check_hip(hipEventCreate(&e1), "event");
-    for (int i = 0; i < 2; i++) once();
-    check_hip(hipEventRecord(e0, st), "event record");
-    for (int i = 0; i < iters; i++) once();
-    check_hip(hipEventRecord(e1, st), "event record");
-    check_hip(hipEventSynchronize(e1), "event sync");
-    check_hip(hipGetLastError(), "gemv kernels");
     float ms = 0.f;
-    check_hip(hipEventElapsedTime(&ms, e0, e1), "elapsed");
+    if (mode == 2) {
+      kev.assign(2 * n, nullptr);
+      for (auto &e : kev) check_hip(hipEventCreate(&e), "event");
+      enqueue(true);  // warm-up
+      check_hip(hipStreamSynchronize(st), "warm-up sync");
+      double total = 0.0;
+      for (int it = 0; it < iters; it++) {
+        enqueue(true);
+        check_hip(hipStreamSynchronize(st), "timed sync");
+        for (int i = 0; i < n; i++) {
+          float t = 0.f;
+          check_hip(hipEventElapsedTime(&t, kev[2 * i], kev[2 * i + 1]), "elapsed");
+          total += t;
+        }
+      }
+      ms = (float)total;
+    } else {
+      if (mode == 1) {
+        check_hip(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "capture");
+        enqueue(false);
+        check_hip(hipStreamEndCapture(st, &graph), "end capture");
+        check_hip(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "instantiate");
+      }
+      auto once = [&] {
+        if (mode == 1)
+          check_hip(hipGraphLaunch(exec, st), "graph launch");
+        else
+          enqueue(false);
+      };
+      for (int i = 0; i < 2; i++) once();
+      check_hip(hipEventRecord(e0, st), "event record");
+      for (int i = 0; i < iters; i++) once();
+      check_hip(hipEventRecord(e1, st), "event record");
+      check_hip(hipEventSynchronize(e1), "event sync");
+      check_hip(hipEventElapsedTime(&ms, e0, e1), "elapsed");
+    }
+    check_hip(hipGetLastError(), "gemv kernels");
     *us_per_launch = ms * 1000.f / ((float)iters * n);
     *launches = n;
     *bytes = b;
   });
+  for (auto e : kev)
+    if (e) (void)hipEventDestroy(e);
   if (e0) (void)hipEventDestroy(e0);
   if (e1) (void)hipEventDestroy(e1);
   if (exec) (void)hipGraphExecDestroy(exec);

@@ -72,7 +72,7 @@ struct Work {
   float *logits = nullptr;  // [rows][head rows]
   RowDesc *rd = nullptr;    // [rows]
   float *part = nullptr;    // attention partials [rows][heads][splits][head_dim + 2]
-  int *tickets = nullptr;   // attention split tickets [rows][kv_heads], zero
+  int *tickets = nullptr;   // attention split tickets [rows][heads], zero
   CtxDev **ctx_arr = nullptr;
   void ensure(const struct ::q3h_stack *s, int rows, int splits, int head_rows);
   void release();

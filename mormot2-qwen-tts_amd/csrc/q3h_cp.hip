@@ -15,8 +15,8 @@
 // attention, so the result does not depend on scheduling.
 //
 // Shape (the Qwen3-TTS code predictor): hidden 1024, 16 query heads and 8 kv
-// heads of 128, 16 positions. 64 workgroups of 8 waves; wave w serves kv head
-// w for the attention, then rows row0 + 2w, row0 + 2w + 1 of Wo.
+// heads of 128, 16 positions. 128 workgroups of 8 waves; wave w serves kv
+// head w for the attention, then one row of Wo.
 //
 // Layouts: K/V cache of the layer [8][16][128] (kl), values at kl + v_off;
 // q_norm then k_norm (qkn); the RoPE (cos, sin) row of pos (rope); Wo quants
@@ -33,7 +33,7 @@ namespace {
 
 constexpr int HD = 128, KVH = 8, GRP = 2, NQ = KVH * GRP * HD, HID = 1024;
 constexpr int P = 16;     // positions of a code-predictor context
-constexpr int ROWS = 16;  // o_proj rows per workgroup
+constexpr int ROWS = 8;   // o_proj rows per workgroup: one per wave
 constexpr int NT = 512;   // 8 waves
 constexpr int NBO = NQ / 32;
 
@@ -75,14 +75,21 @@ __device__ __forceinline__ float dot4(int w, float4 x, float acc) {
 }
 
 // RMSNorm over a head (lanes hold elements lane, lane + 64), weight (w0, w1),
-// then rotate_half RoPE with (cos, sin) = cs
+// then rotate_half RoPE with (cos, sin) = cs; fp32 throughout
 __device__ __forceinline__ void norm_rope(float &x0, float &x1, float w0, float w1, float2 cs,
                                           float eps) {
-  const double ss = wave_sum_dpp_d((double)x0 * x0 + (double)x1 * x1);
-  const float inv = (float)(1.0 / sqrt(ss / HD + (double)eps));
+  const float ss = wave_sum_dpp(fmaf(x0, x0, x1 * x1));
+  const float inv = 1.0f / sqrtf(ss * (1.0f / HD) + eps);
   const float a = w0 * (x0 * inv), b = w1 * (x1 * inv);
   x0 = a * cs.x - b * cs.y;
   x1 = b * cs.x + a * cs.y;
+}
+
+// LDS written by some lanes of a wave and read by others of the same wave
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 template <typename KV>
@@ -95,23 +102,20 @@ __global__ __launch_bounds__(NT) void k_attn_o_cp(const int8_t *__restrict__ wo,
   __shared__ float att[NQ];
   __shared__ float qs[KVH][GRP][HD];
   __shared__ float kvs[KVH][2][HD];  // the new key and value of each kv head
-  __shared__ float ps[KVH][GRP][P];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int row0 = blockIdx.x * ROWS + 2 * w;
+  const int row = blockIdx.x * ROWS + w;  // this wave's o_proj row
   const _Float16 *wd = reinterpret_cast<const _Float16 *>(wo + (size_t)HID * NQ);
 
-  // 1. every load up front: Wo rows, the residual, the raw q/k/v of kv head
-  // w, the norm weights, the RoPE row, the cached keys and values
-  int4 wv[2][2];
-  float sc[2][2];
+  // 1. every load up front: the Wo row, the residual, the raw q/k/v of kv
+  // head w, the norm weights, the RoPE row, the cached keys and values
+  int4 wv[2];
+  float sc[2];
 #pragma unroll
-  for (int r = 0; r < 2; r++)
-#pragma unroll
-    for (int c = 0; c < 2; c++) {
-      wv[r][c] = *reinterpret_cast<const int4 *>(wo + (size_t)(row0 + r) * NQ + c * 1024 + lane * 16);
-      sc[r][c] = (float)wd[(size_t)(row0 + r) * NBO + c * 32 + (lane >> 1)];
-    }
-  const float h0 = h[row0], h1 = h[row0 + 1];
+  for (int c = 0; c < 2; c++) {
+    wv[c] = *reinterpret_cast<const int4 *>(wo + (size_t)row * NQ + c * 1024 + lane * 16);
+    sc[c] = (float)wd[(size_t)row * NBO + c * 32 + (lane >> 1)];
+  }
+  const float hr = h[row];
   float xq[GRP][2], xk[2], xv[2];
 #pragma unroll
   for (int j = 0; j < GRP; j++) {
@@ -161,69 +165,80 @@ __global__ __launch_bounds__(NT) void k_attn_o_cp(const int8_t *__restrict__ wo,
       vh[(size_t)pos * HD + lane + 64] = v1;
     }
   }
-  __syncthreads();
+  wave_lds_sync();
 
-  // 3. scores of key kp for both query heads, softmax over positions 0..pos
+  // 3. scores of key kp (the new key from LDS), softmax over 0..pos; the
+  // probability of key p ends up in lanes 4p .. 4p + 3
+  if (kp == pos) {
+#pragma unroll
+    for (int i = 0; i < 32; i++) kk[i] = kvs[w][0][kj * 32 + i];
+  }
   const float scale = (float)(1.0 / sqrt((double)HD));
   const bool live = kp <= pos;
+  float pr[GRP];
 #pragma unroll
   for (int j = 0; j < GRP; j++) {
     const float *q = &qs[w][j][kj * 32];
-    const float *knew = &kvs[w][0][kj * 32];
-    float a = 0.f;
-    if (kp < pos) {
+    float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-      for (int i = 0; i < 32; i++) a = fmaf(q[i], kk[i], a);
-    } else if (kp == pos) {
-#pragma unroll
-      for (int i = 0; i < 32; i++) a = fmaf(q[i], knew[i], a);
+    for (int i = 0; i < 32; i += 2) {
+      a0 = fmaf(q[i], kk[i], a0);
+      a1 = fmaf(q[i + 1], kk[i + 1], a1);
     }
+    float a = a0 + a1;
     a += dpp_f<kQuadXor1>(a);
     a += dpp_f<kQuadXor2>(a);
-    const float s = live ? a * scale : -INFINITY;
-    const float mx = wave_max_dpp(s);
-    const float e = live ? expf(s - mx) : 0.f;
+    const float sv = live ? a * scale : -INFINITY;
+    const float mx = wave_max_dpp(sv);
+    const float e = live ? expf(sv - mx) : 0.f;
     const float sum = wave_sum_dpp(kj == 0 ? e : 0.f);
-    if (kj == 0) ps[w][j][kp] = e * (1.0f / sum);
+    pr[j] = e * (1.0f / sum);
   }
-  __syncthreads();
 
-  // 4. outputs of both heads: lane holds dims 2 lane, 2 lane + 1
+  // 4. outputs (lane holds dims 2 lane, 2 lane + 1), probabilities read
+  // from lane 4p
+  float o[GRP][2];
 #pragma unroll
-  for (int j = 0; j < GRP; j++) {
-    float o0 = 0.f, o1 = 0.f;
+  for (int j = 0; j < GRP; j++) o[j][0] = o[j][1] = 0.f;
 #pragma unroll
-    for (int p = 0; p < P; p++) {
-      if (p < pos) {
-        const float pw = ps[w][j][p];
-        o0 = fmaf(pw, vv[p].x, o0);
-        o1 = fmaf(pw, vv[p].y, o1);
+  for (int p = 0; p < P; p++) {
+    if (p < pos) {
+#pragma unroll
+      for (int j = 0; j < GRP; j++) {
+        const float pw = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pr[j]), 4 * p));
+        o[j][0] = fmaf(pw, vv[p].x, o[j][0]);
+        o[j][1] = fmaf(pw, vv[p].y, o[j][1]);
       }
     }
-    const float pw = ps[w][j][pos];
-    o0 = fmaf(pw, kvs[w][1][2 * lane], o0);
-    o1 = fmaf(pw, kvs[w][1][2 * lane + 1], o1);
-    att[(w * GRP + j) * HD + 2 * lane] = o0;
-    att[(w * GRP + j) * HD + 2 * lane + 1] = o1;
+  }
+  {
+    const float2 vn = make_float2(kvs[w][1][2 * lane], kvs[w][1][2 * lane + 1]);
+#pragma unroll
+    for (int j = 0; j < GRP; j++) {
+      const float pw = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pr[j]), 4 * pos));
+      o[j][0] = fmaf(pw, vn.x, o[j][0]);
+      o[j][1] = fmaf(pw, vn.y, o[j][1]);
+      att[(w * GRP + j) * HD + 2 * lane] = o[j][0];
+      att[(w * GRP + j) * HD + 2 * lane + 1] = o[j][1];
+    }
   }
   __syncthreads();
 
-  // 5. h[row] += Wo[row] . att for this wave's two rows
+  // 5. h[row] += Wo[row] . att
+  float acc = 0.f;
 #pragma unroll
-  for (int r = 0; r < 2; r++) {
-    float acc = 0.f;
-#pragma unroll
-    for (int c = 0; c < 2; c++) {
-      const float4 *xp = reinterpret_cast<const float4 *>(att + c * 1024 + lane * 16);
-      float p0 = dot4(wv[r][c].x, xp[0], 0.f);
-      float p1 = dot4(wv[r][c].y, xp[1], 0.f);
-      p0 = dot4(wv[r][c].z, xp[2], p0);
-      p1 = dot4(wv[r][c].w, xp[3], p1);
-      acc = fmaf(sc[r][c], p0 + p1, acc);
-    }
-    acc = wave_sum_dpp(acc);
-    if (lane == 0) h[row0 + r] = (r == 0 ? h0 : h1) + acc;
+  for (int c = 0; c < 2; c++) {
+    const float4 *xp = reinterpret_cast<const float4 *>(att + c * 1024 + lane * 16);
+    float p0 = dot4(wv[c].x, xp[0], 0.f);
+    float p1 = dot4(wv[c].y, xp[1], 0.f);
+    p0 = dot4(wv[c].z, xp[2], p0);
+    p1 = dot4(wv[c].w, xp[3], p1);
+    acc = fmaf(sc[c], p0 + p1, acc);
   }
+  acc = wave_sum_dpp(acc);
+  if (lane == 0) h[row] = hr + acc;
 }
 
 }  // namespace

@@ -27,6 +27,7 @@
 // sum of squares is a wave reduction, and every wave is independent. The
 // normed row can also be written out (xn_out, by the first wave), so the
 // final norm of a stack and its head are one launch.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include "q3h_internal.h"
@@ -232,16 +233,19 @@ __global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq
   __builtin_amdgcn_sched_barrier(0);
   float inv = 1.f;
   if (nrm) {
-    double ss = 0.0;
+    // sum of squares in fp32 (16 C terms per lane, then the wave), the
+    // factor as 1 / sqrt in fp32
+    float ss0 = 0.f, ss1 = 0.f;
 #pragma unroll
     for (int c = 0; c < C; c++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const float4 v = xv[c][i];
-        ss += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+        ss0 = fmaf(v.x, v.x, fmaf(v.y, v.y, ss0));
+        ss1 = fmaf(v.z, v.z, fmaf(v.w, v.w, ss1));
       }
-    ss = wave_sum_dpp_d(ss);
-    inv = (float)(1.0 / sqrt(ss / K + (double)eps));
+    const float ss = wave_sum_dpp(ss0 + ss1);
+    inv = 1.0f / sqrtf(ss * (1.0f / K) + eps);
 #pragma unroll
     for (int c = 0; c < C; c++)
 #pragma unroll
@@ -295,12 +299,21 @@ __global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq
   }
 }
 
+// ev0 / ev1 (optional): events recorded at the start and the end of the
+// kernel's own execution (hipExtLaunchKernelGGL), for measurement
 template <int R, int C>
-void launch_v(const GemvArgs &a, int epi, int waves, hipStream_t st) {
+void launch_v(const GemvArgs &a, int epi, int waves, hipStream_t st, hipEvent_t ev0 = nullptr,
+              hipEvent_t ev1 = nullptr) {
   const dim3 grid(a.N / (waves * R)), block(64 * waves);
-#define Q3H_V(E)                                                                              \
-  hipLaunchKernelGGL((k_gemv_q8v<R, C, E>), grid, block, 0, st, a.wq, a.wd, a.x, a.norm_w, a.y, \
-                     a.xn_out, a.N, waves, a.eps)
+#define Q3H_V(E)                                                                                \
+  do {                                                                                          \
+    if (ev0)                                                                                    \
+      hipExtLaunchKernelGGL((k_gemv_q8v<R, C, E>), grid, block, 0, st, ev0, ev1, 0, a.wq, a.wd, \
+                            a.x, a.norm_w, a.y, a.xn_out, a.N, waves, a.eps);                   \
+    else                                                                                        \
+      hipLaunchKernelGGL((k_gemv_q8v<R, C, E>), grid, block, 0, st, a.wq, a.wd, a.x, a.norm_w,  \
+                         a.y, a.xn_out, a.N, waves, a.eps);                                     \
+  } while (0)
   if (epi == EPI_STORE)
     Q3H_V(EPI_STORE);
   else if (epi == EPI_ADD)
@@ -322,16 +335,19 @@ void launch_w(const GemvArgs &a, int epi, int waves, hipStream_t st) {
     hipLaunchKernelGGL((k_gemv_q8w<R, C, MR, EPI_SWIGLU>), grid, block, lds, st, a);
 }
 
-template <int R, int MR>
-void launch_rc(const GemvArgs &a, int epi, int waves, hipStream_t st) {
-  if (MR == 1 && !kLdsSingleRow) {
-    switch (a.K) {
-      case 1024: launch_v<R, 1>(a, epi, waves, st); break;
-      case 2048: launch_v<R, 2>(a, epi, waves, st); break;
-      default: launch_v<R, 3>(a, epi, waves, st); break;
-    }
-    return;
+// the single-row kernel with W waves of R rows
+template <int R>
+void launch_k(const GemvArgs &a, int epi, int W, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+  switch (a.K) {
+    case 1024: launch_v<R, 1>(a, epi, W, st, ev0, ev1); break;
+    case 2048: launch_v<R, 2>(a, epi, W, st, ev0, ev1); break;
+    default: launch_v<R, 3>(a, epi, W, st, ev0, ev1); break;
   }
+}
+
+template <int R, int MR>
+void launch_rc(const GemvArgs &a, int epi, int waves, hipStream_t st, hipEvent_t ev0,
+               hipEvent_t ev1) {
   switch (a.K) {
     case 1024: launch_w<R, 1, MR>(a, epi, waves, st); break;
     case 2048: launch_w<R, 2, MR>(a, epi, waves, st); break;
@@ -341,24 +357,44 @@ void launch_rc(const GemvArgs &a, int epi, int waves, hipStream_t st) {
 
 }  // namespace
 
-bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st) {
+bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st, hipEvent_t ev0,
+                         hipEvent_t ev1) {
+  if (ev0 != nullptr && a.M != 1) return false;  // events: single-row kernel only
   if (a.M < 1 || a.M > kMaxRowsX || (a.xn_out != nullptr && a.M != 1)) return false;
   if (a.K != 1024 && a.K != 2048 && a.K != 3072) return false;
   if (a.N % 256 != 0) return false;
   const int rpb = a.N / 256;  // rows per workgroup, 256 workgroups
+  if (a.M == 1 && !kLdsSingleRow) {
+    // measured on the Qwen3-TTS shapes: one wave per SIMD (R = rpb / 4 rows
+    // per wave) for the plain products; the gate/up pairs (SwiGLU) run as
+    // 2-row waves (12 per workgroup), which keeps more loads in flight
+    int R1 = rpb / 4, W = 4;
+    if (epi == EPI_SWIGLU) {
+      R1 = 2;
+      W = rpb / 2;
+    }
+    if (R1 * W != rpb || W > kMaxWaves) return false;
+    switch (R1) {
+      case 1: launch_k<1>(a, epi, W, st, ev0, ev1); return true;
+      case 2: launch_k<2>(a, epi, W, st, ev0, ev1); return true;
+      case 3: launch_k<3>(a, epi, W, st, ev0, ev1); return true;
+      case 4: launch_k<4>(a, epi, W, st, ev0, ev1); return true;
+      default: return false;
+    }
+  }
   const int R = (epi == EPI_SWIGLU || rpb > 8) ? 2 : 1;
   if (rpb % R != 0) return false;
   const int waves = rpb / R;
   if (waves < 1 || waves > kMaxWaves) return false;
   const int MR = a.M == 1 ? 1 : (a.M == 2 ? 2 : 4);
   if (R == 1) {
-    if (MR == 1) launch_rc<1, 1>(a, epi, waves, st);
-    else if (MR == 2) launch_rc<1, 2>(a, epi, waves, st);
-    else launch_rc<1, 4>(a, epi, waves, st);
+    if (MR == 1) launch_rc<1, 1>(a, epi, waves, st, ev0, ev1);
+    else if (MR == 2) launch_rc<1, 2>(a, epi, waves, st, ev0, ev1);
+    else launch_rc<1, 4>(a, epi, waves, st, ev0, ev1);
   } else {
-    if (MR == 1) launch_rc<2, 1>(a, epi, waves, st);
-    else if (MR == 2) launch_rc<2, 2>(a, epi, waves, st);
-    else launch_rc<2, 4>(a, epi, waves, st);
+    if (MR == 1) launch_rc<2, 1>(a, epi, waves, st, ev0, ev1);
+    else if (MR == 2) launch_rc<2, 2>(a, epi, waves, st, ev0, ev1);
+    else launch_rc<2, 4>(a, epi, waves, st, ev0, ev1);
   }
   return true;
 }

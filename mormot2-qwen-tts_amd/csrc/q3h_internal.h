@@ -62,7 +62,8 @@ struct QAct {
 void launch_gemv(const GemvArgs &a, int epi, bool q8, hipStream_t st);
 // the wide Q8_0 kernel (K in {1024, 2048, 3072}, N % 256 == 0, M <= 4);
 // false when the shape is not one it takes (nothing launched)
-bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st);
+bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st, hipEvent_t ev0 = nullptr,
+                         hipEvent_t ev1 = nullptr);
 void launch_gemv_i8(const GemvArgs &a, const QAct &xa, int epi, hipStream_t st);
 void launch_quantize_act(const float *x, int ldx, int M, int K, const float *norm_w,
                          float eps, QAct out, hipStream_t st);
@@ -93,13 +94,10 @@ struct AttnArgs {
   const float2 *rope_cs;
   float *out;    // [M][heads * head_dim]
   float *part;   // [M][heads][splits][head_dim + 2]
-  int *tickets;  // [M][kvh], zero between launches
-  int chunk;     // positions per split (0: the default, 256)
+  int *tickets;  // [M][heads], zero between launches
 };
 int attn_splits(int positions);
-// max_positions: the capacity of the stack's contexts (chooses the workgroup size)
-void launch_attn(const AttnArgs &a, int M, int splits, int max_positions, bool fused, bool kv16,
-                 hipStream_t st);
+void launch_attn(const AttnArgs &a, int M, int splits, bool fused, bool kv16, hipStream_t st);
 
 // the code predictor's fused attention + o_proj + residual (q3h_cp.hip):
 // one context of 16 positions, the new row at pos; k_layer: the layer's keys,

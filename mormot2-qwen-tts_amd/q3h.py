@@ -220,15 +220,16 @@ class Stack:
     def bytes(self):
         return lib().q3h_stack_bytes(self.h)
 
-    def time_gemv(self, head=-1, iters=20, use_graph=True):
+    def time_gemv(self, head=-1, iters=20, mode=1):
         """(us per launch, launches per step, algorithmic bytes per step) of the
-        weight products of one single-row decode step, graph-replayed or
-        launched directly."""
+        weight products of one single-row decode step. mode 0: direct launches,
+        wall time; 1: hipGraph replay, wall time; 2: the kernels' own execution
+        time (events attached to each launch)."""
         us = ctypes.c_float()
         n = ctypes.c_int()
         b = ctypes.c_int64()
-        _check(lib().q3h_stack_time_gemv(self.h, head, iters, int(use_graph), ctypes.byref(us), ctypes.byref(n),
-                                         ctypes.byref(b)))
+        _check(lib().q3h_stack_time_gemv(self.h, head, iters, int(mode), ctypes.byref(us),
+                                         ctypes.byref(n), ctypes.byref(b)))
         return us.value, n.value, b.value
 
     def destroy(self):
