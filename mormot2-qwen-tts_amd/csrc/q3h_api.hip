@@ -107,9 +107,7 @@ void run_layers(const q3h_stack *s, Work &w, int M, int splits, bool fused, hipS
     at.layer = l;
     at.heads = c.heads;
     at.kvh = c.kv_heads;
-    at.qn = L.q_norm;
-    at.kn = L.k_norm;
-    at.eps = c.rms_eps;
+    at.qkn = L.q_norm;
     at.rope_cs = reinterpret_cast<const float2 *>(s->rope_cs);
     at.out = w.att;
     at.part = w.part;
@@ -141,7 +139,7 @@ void run_cp_fused(const q3h_stack *s, Work &w, const q3h_context *ctx, int pos, 
     launch_gemv(make_gemv(L.qkv, w.h, H, 1, L.in_norm, c.rms_eps, w.qkv, ldq), EPI_STORE, true,
                 st);
     void *kl = static_cast<char *>(ctx->k) + l * per_layer * esz;
-    launch_attn_o_cp(L.o, w.qkv, kl, v_off, w.h, L.q_norm, rope_row, pos, c.rms_eps, kv16, st);
+    launch_attn_o_cp(L.o, w.qkv, kl, v_off, w.h, L.q_norm, rope_row, pos, kv16, st);
     launch_gemv(make_gemv(L.gu, w.h, H, 1, L.post_norm, c.rms_eps, w.act, I), EPI_SWIGLU, true,
                 st);
     launch_gemv(make_gemv(L.down, w.act, I, 1, nullptr, 0.f, w.h, H), EPI_ADD, true, st);
@@ -392,15 +390,20 @@ extern "C" int q3h_stack_create(q3h_device *dev, const q3h_stack_config *cfg,
         upload_rows(L.down, c.dtype, lw.wdown, w->src_dtype, H, I, 1, 0, staging, s->stream);
         L.in_norm = upload_vec(lw.input_norm, H, "input_layernorm");
         L.post_norm = upload_vec(lw.post_norm, H, "post_attention_layernorm");
-        // q_norm and k_norm side by side: [q_norm | k_norm]
+        // q_norm and k_norm side by side, then the RMSNorm epsilon:
+        // [q_norm | k_norm | eps] (the attention kernels read all three from
+        // one pointer)
         require(lw.q_norm != nullptr && lw.k_norm != nullptr, Q3H_E_ARG,
                 "a norm vector is NULL: q_norm / k_norm");
-        L.q_norm = (float *)dev_alloc(sizeof(float) * 2 * hd);
+        L.q_norm = (float *)dev_alloc(sizeof(float) * (2 * hd + 4));
         L.k_norm = L.q_norm + hd;
         check_hip(hipMemcpy(L.q_norm, lw.q_norm, sizeof(float) * hd, hipMemcpyHostToDevice),
                   "upload q_norm");
         check_hip(hipMemcpy(L.k_norm, lw.k_norm, sizeof(float) * hd, hipMemcpyHostToDevice),
                   "upload k_norm");
+        const float eps4[4] = {c.rms_eps, 0.f, 0.f, 0.f};
+        check_hip(hipMemcpy(L.q_norm + 2 * hd, eps4, sizeof(eps4), hipMemcpyHostToDevice),
+                  "upload eps");
         s->bytes += (int64_t)(2 * H + 2 * hd) * 4;
       }
       s->final_norm = upload_vec(w->final_norm, H, "norm");

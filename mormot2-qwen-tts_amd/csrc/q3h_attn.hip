@@ -82,14 +82,14 @@ __device__ __forceinline__ float rescale(float m, float mn) {
 }
 
 // Plain scalar arguments, those of the prologue first (the first 14 argument
-// dwords are preloaded into SGPRs); the split buffers come last.
+// dwords are preloaded into SGPRs); the split buffers come last. qkn holds
+// [q_norm | k_norm | eps] of the layer.
 template <typename KV, bool FUSED, int GRP>
 __global__ __launch_bounds__(NT) void k_attn(const RowDesc *__restrict__ rd,
                                              const float *__restrict__ qkv,
                                              const float2 *__restrict__ rope_cs,
-                                             const float *__restrict__ qn,
-                                             const float *__restrict__ kn, float *__restrict__ outp,
-                                             int layer, int kvh, float eps, int S,
+                                             const float *__restrict__ qkn,
+                                             float *__restrict__ outp, int layer, int kvh, int S,
                                              float *__restrict__ part, int *__restrict__ tickets) {
   __shared__ float qs[HD];
   __shared__ float kvn[2][HD];  // the new key and value, as the cache holds them
@@ -134,12 +134,13 @@ __global__ __launch_bounds__(NT) void k_attn(const RowDesc *__restrict__ rd,
     if (p < p1 && !(FUSED && p == d.pos)) vv[i] = ld4(vc + (size_t)p * HD + 4 * dg);
   }
   float2 cs = make_float2(1.f, 0.f);
-  float w0 = 1.f, w1 = 1.f;
+  float w0 = 1.f, w1 = 1.f, eps = 0.f;
   if (FUSED && wave < 2) {
     cs = rope_cs[(size_t)d.pos * (HD / 2) + lane];
-    const float *w = wave == 0 ? qn : kn;
+    const float *w = qkn + wave * HD;
     w0 = w[lane];
     w1 = w[lane + 64];
+    eps = qkn[2 * HD];
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -270,7 +271,7 @@ template <typename KV, bool FUSED>
 void launch_grp(const AttnArgs &a, int grp, dim3 grid, hipStream_t st) {
 #define Q3H_A(G)                                                                               \
   hipLaunchKernelGGL((k_attn<KV, FUSED, G>), grid, dim3(NT), 0, st, a.rd, a.qkv, a.rope_cs,     \
-                     a.qn, a.kn, a.out, a.layer, a.kvh, a.eps, (int)grid.z, a.part, a.tickets)
+                     a.qkn, a.out, a.layer, a.kvh, (int)grid.z, a.part, a.tickets)
   if (grp == 1)
     Q3H_A(1);
   else if (grp == 2)

@@ -19,7 +19,7 @@
 // head w for the attention, then one row of Wo.
 //
 // Layouts: K/V cache of the layer [8][16][128] (kl), values at kl + v_off;
-// q_norm then k_norm (qkn); the RoPE (cos, sin) row of pos (rope); Wo quants
+// q_norm, k_norm, then the RMSNorm epsilon (qkn); the RoPE (cos, sin) row of pos (rope); Wo quants
 // [1024][2048] followed by their fp16 scales [1024][64].
 #include <hip/hip_runtime.h>
 
@@ -98,7 +98,7 @@ __global__ __launch_bounds__(NT) void k_attn_o_cp(const int8_t *__restrict__ wo,
                                                   KV *__restrict__ kl, float *__restrict__ h,
                                                   const float *__restrict__ qkn,
                                                   const float2 *__restrict__ rope, int pos,
-                                                  int v_off, float eps) {
+                                                  int v_off) {
   __shared__ float att[NQ];
   __shared__ float qs[KVH][GRP][HD];
   __shared__ float kvs[KVH][2][HD];  // the new key and value of each kv head
@@ -128,6 +128,7 @@ __global__ __launch_bounds__(NT) void k_attn_o_cp(const int8_t *__restrict__ wo,
   xv[1] = qkv[NQ + KVH * HD + w * HD + lane + 64];
   const float qn0 = qkn[lane], qn1 = qkn[lane + 64];
   const float kn0 = qkn[HD + lane], kn1 = qkn[HD + lane + 64];
+  const float eps = qkn[2 * HD];
   const float2 cs = rope[lane];
   KV *kh = kl + (size_t)w * P * HD;
   KV *vh = kl + v_off + (size_t)w * P * HD;
@@ -249,16 +250,16 @@ bool cp_fused_supported(const q3h_stack_config &c) {
 }
 
 void launch_attn_o_cp(const Mat &wo, const float *qkv, void *k_layer, int v_off, float *h,
-                      const float *qkn, const float *rope_row, int pos, float eps, bool kv16,
+                      const float *qkn, const float *rope_row, int pos, bool kv16,
                       hipStream_t st) {
   const dim3 grid(HID / ROWS), block(NT);
   const float2 *rope = reinterpret_cast<const float2 *>(rope_row);
   if (kv16)
     hipLaunchKernelGGL(k_attn_o_cp<_Float16>, grid, block, 0, st, wo.q, qkv,
-                       static_cast<_Float16 *>(k_layer), h, qkn, rope, pos, v_off, eps);
+                       static_cast<_Float16 *>(k_layer), h, qkn, rope, pos, v_off);
   else
     hipLaunchKernelGGL(k_attn_o_cp<float>, grid, block, 0, st, wo.q, qkv,
-                       static_cast<float *>(k_layer), h, qkn, rope, pos, v_off, eps);
+                       static_cast<float *>(k_layer), h, qkn, rope, pos, v_off);
 }
 
 }  // namespace q3h

@@ -187,12 +187,12 @@ __global__ __launch_bounds__(1024) void k_gemv_q8w(GemvArgs a) {
 }
 
 // one activation row: no LDS, no barrier (see the header). Plain scalar
-// arguments, the pointers first: the first 16 argument dwords reach the waves
-// preloaded in SGPRs, so the weight loads issue without waiting on a scalar
-// memory read. W (waves per workgroup) is an argument: blockDim is not read.
+// arguments (13 dwords, all preloaded in SGPRs), so the weight loads issue
+// without waiting on a scalar memory read; the scales are found after the
+// quants (wq + N*K). W (waves per workgroup) is an argument: blockDim is not
+// read. The residual of EPI_ADD is loaded with the weights, not at the end.
 template <int R, int C, int EPI>
 __global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq,
-                                                   const _Float16 *__restrict__ wd,
                                                    const float *__restrict__ x,
                                                    const float *__restrict__ norm_w,
                                                    float *__restrict__ y, float *__restrict__ xn_out,
@@ -200,6 +200,7 @@ __global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq
   constexpr int K = C * 1024, NB = K / 32;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row0 = (blockIdx.x * W + wave) * R;
+  const _Float16 *__restrict__ wd = reinterpret_cast<const _Float16 *>(wq + (size_t)N * K);
 
   int4 wv[R][C];
   float sc[R][C];
@@ -228,6 +229,11 @@ __global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq
 #pragma unroll
       for (int i = 0; i < 4; i++)
         wn[c][i] = reinterpret_cast<const float4 *>(norm_w + c * 1024 + lane * 16)[i];
+  }
+  float yres[R];
+  if (EPI == EPI_ADD) {
+#pragma unroll
+    for (int r = 0; r < R; r++) yres[r] = y[min(row0 + r, N - 1)];
   }
   // every load above is issued before any arithmetic
   __builtin_amdgcn_sched_barrier(0);
@@ -291,7 +297,7 @@ __global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq
     for (int r = 0; r < R; r++) {
       if (row0 + r < N) {
         if (EPI == EPI_ADD)
-          y[row0 + r] += acc[r];
+          y[row0 + r] = yres[r] + acc[r];
         else
           y[row0 + r] = acc[r];
       }
@@ -308,11 +314,11 @@ void launch_v(const GemvArgs &a, int epi, int waves, hipStream_t st, hipEvent_t 
 #define Q3H_V(E)                                                                                \
   do {                                                                                          \
     if (ev0)                                                                                    \
-      hipExtLaunchKernelGGL((k_gemv_q8v<R, C, E>), grid, block, 0, st, ev0, ev1, 0, a.wq, a.wd, \
-                            a.x, a.norm_w, a.y, a.xn_out, a.N, waves, a.eps);                   \
+      hipExtLaunchKernelGGL((k_gemv_q8v<R, C, E>), grid, block, 0, st, ev0, ev1, 0, a.wq, a.x,  \
+                            a.norm_w, a.y, a.xn_out, a.N, waves, a.eps);                        \
     else                                                                                        \
-      hipLaunchKernelGGL((k_gemv_q8v<R, C, E>), grid, block, 0, st, a.wq, a.wd, a.x, a.norm_w,  \
-                         a.y, a.xn_out, a.N, waves, a.eps);                                     \
+      hipLaunchKernelGGL((k_gemv_q8v<R, C, E>), grid, block, 0, st, a.wq, a.x, a.norm_w, a.y,   \
+                         a.xn_out, a.N, waves, a.eps);                                          \
   } while (0)
   if (epi == EPI_STORE)
     Q3H_V(EPI_STORE);
@@ -359,6 +365,8 @@ void launch_rc(const GemvArgs &a, int epi, int waves, hipStream_t st, hipEvent_t
 
 bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st, hipEvent_t ev0,
                          hipEvent_t ev1) {
+  // the kernels find the scales right after the quants
+  if (reinterpret_cast<const int8_t *>(a.wd) != a.wq + (size_t)a.N * a.K) return false;
   if (ev0 != nullptr && a.M != 1) return false;  // events: single-row kernel only
   if (a.M < 1 || a.M > kMaxRowsX || (a.xn_out != nullptr && a.M != 1)) return false;
   if (a.K != 1024 && a.K != 2048 && a.K != 3072) return false;

@@ -89,8 +89,7 @@ struct AttnArgs {
   int ldq;
   const RowDesc *rd;
   int layer, heads, kvh;
-  const float *qn, *kn;
-  float eps;
+  const float *qkn;  // [q_norm | k_norm | eps] of the layer
   const float2 *rope_cs;
   float *out;    // [M][heads * head_dim]
   float *part;   // [M][heads][splits][head_dim + 2]
@@ -101,10 +100,10 @@ void launch_attn(const AttnArgs &a, int M, int splits, bool fused, bool kv16, hi
 
 // the code predictor's fused attention + o_proj + residual (q3h_cp.hip):
 // one context of 16 positions, the new row at pos; k_layer: the layer's keys,
-// values at k_layer + v_off elements; qkn: q_norm then k_norm; rope_row: the
-// (cos, sin) row of pos
+// values at k_layer + v_off elements; qkn: [q_norm | k_norm | eps]; rope_row:
+// the (cos, sin) row of pos
 void launch_attn_o_cp(const Mat &wo, const float *qkv, void *k_layer, int v_off, float *h,
-                      const float *qkn, const float *rope_row, int pos, float eps, bool kv16,
+                      const float *qkn, const float *rope_row, int pos, bool kv16,
                       hipStream_t st);
 
 void launch_rmsnorm_rows(const float *x, int ldx, int M, int K, const float *w, float eps,
