@@ -9,7 +9,8 @@ the 16 codes of each stream copied back to the host.
 Workloads (random-init N(0, 0.02) weights from a seed, Q8_0, norm weights 1,
 synthetic N(0, 1) prompt embeddings; nothing is downloaded):
   frame_b1   1 stream, 48 prompt rows, K frames (156: context 48 -> 204)
-  frame_b32  32 streams, prompt rows uniform in [16, 256] (seeded), K frames
+  frame_b32  32 streams, prompt rows uniform in [16, 256] (seeded), K frames;
+             activations quantized per 32-block (int8 MFMA products)
 
 Timed region: K steps after W warm-up steps; the warm-up runs on a first
 prefill, the timed steps restart from a fresh prefill so that the context
@@ -51,15 +52,16 @@ def log(msg):
     print(f"bench: {msg}", file=sys.stderr, flush=True)
 
 
-def build_model(dev, seed, max_positions):
+def build_model(dev, seed, max_positions, act_q8):
     """Talker + code predictor + heads on the device, from f32 weights that the
-    library quantizes to Q8_0 (bit-exact ggml quantize_row_q8_0_ref)."""
+    library quantizes to Q8_0 (bit-exact ggml quantize_row_q8_0_ref); act_q8:
+    activations quantized per 32-block too (int8 MFMA products)."""
     t0 = time.time()
     tl, tf = synth.stack_weights(seed, "talker.model.", synth.TALKER)
-    ts = q3h.Stack(dev, dict(synth.TALKER, dtype=q3h.Q8_0, kv_f16=0, act_q8=0,
+    ts = q3h.Stack(dev, dict(synth.TALKER, dtype=q3h.Q8_0, kv_f16=0, act_q8=act_q8,
                              max_positions=max_positions), tl, tf, q3h.F32)
     cl, cf = synth.stack_weights(seed, "talker.code_predictor.model.", synth.PREDICTOR)
-    cs = q3h.Stack(dev, dict(synth.PREDICTOR, dtype=q3h.Q8_0, kv_f16=0, act_q8=0,
+    cs = q3h.Stack(dev, dict(synth.PREDICTOR, dtype=q3h.Q8_0, kv_f16=0, act_q8=act_q8,
                              max_positions=16), cl, cf, q3h.F32)
     th = synth.talker_head(seed)
     ts.add_head(th, q3h.F32)
@@ -102,9 +104,9 @@ def run_gpu(frame, pre, steps, warmup):
     return total, lat, np.stack(codes)
 
 
-def cpu_baseline(f32, tables, pre, gpu_codes, budget_s, max_frames):
+def cpu_baseline(f32, tables, pre, gpu_codes, budget_s, max_frames, act_q8):
     """The oracle's frame step on the host cores (same weights, same prompt of
-    stream 0), frames timed until budget_s is spent."""
+    stream 0, same activation mode), frames timed until budget_s is spent."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import q3o  # the checker's restatement, timed as the CPU baseline
 
@@ -115,10 +117,11 @@ def cpu_baseline(f32, tables, pre, gpu_codes, budget_s, max_frames):
     def qlayers(layers):
         return [{k: (q(v) if k.startswith("w") else v) for k, v in L.items()} for L in layers]
 
-    ot = q3o.Stack(synth.TALKER, qlayers(f32["tl"]), f32["tf"], q3o.Q8_0)
-    oc = q3o.Stack(synth.PREDICTOR, qlayers(f32["cl"]), f32["cf"], q3o.Q8_0)
+    ot = q3o.Stack(synth.TALKER, qlayers(f32["tl"]), f32["tf"], q3o.Q8_0, act_q8=act_q8)
+    oc = q3o.Stack(synth.PREDICTOR, qlayers(f32["cl"]), f32["cf"], q3o.Q8_0, act_q8=act_q8)
     fr = q3o.Frame(ot, oc, q(f32["th"]), [q(h) for h in f32["ch"]], tables["codec_emb"],
-                   tables["pred_emb"], tables["tts_pad"], max_positions=PROMPT_ROWS + max_frames + 8)
+                   tables["pred_emb"], tables["tts_pad"],
+                   max_positions=pre[0].shape[0] + max_frames + 8)
     fr.start(pre[0])
     n = 0
     equal = True
@@ -130,9 +133,11 @@ def cpu_baseline(f32, tables, pre, gpu_codes, budget_s, max_frames):
     dt = time.perf_counter() - t0
     for o in (fr, ot, oc):
         o.destroy()
+    act = "int8 activations" if act_q8 else "f32 activations"
     return dict(value=n / dt, unit="frames/s", cores=threads, kind="port",
-                sample=f"frame step B=1 Q8_0 (oracle, C + OpenMP), {PROMPT_ROWS} prompt rows "
-                       f"(prefill untimed), first {n} frames, {dt:.1f} s"), n, equal
+                sample=f"frame step of stream 0, Q8_0 weights, {act} (oracle, C + OpenMP), "
+                       f"{pre[0].shape[0]} prompt rows (prefill untimed), first {n} frames, "
+                       f"{dt:.1f} s"), n, equal
 
 
 def gemv_roofline(ts, args):
@@ -184,7 +189,8 @@ def main():
     maxlen = max(p.shape[0] for p in pre)
     max_pos = maxlen + max(steps, warmup) + 8
     dev = q3h.Device(0)
-    ts, cs, tables, f32 = build_model(dev, args.seed, max_pos)
+    act_q8 = 0 if b1 else 1
+    ts, cs, tables, f32 = build_model(dev, args.seed, max_pos, act_q8)
     if args.gemv_only:
         roofline = gemv_roofline(ts, args)
         print(json.dumps({"roofline": roofline}), flush=True)
@@ -206,7 +212,7 @@ def main():
     cpu = None
     parity = None
     if not args.no_cpu:
-        cpu, nf, equal = cpu_baseline(f32, tables, pre, codes, args.cpu_seconds, steps)
+        cpu, nf, equal = cpu_baseline(f32, tables, pre, codes, args.cpu_seconds, steps, act_q8)
         parity = dict(frames=nf, codes_equal_stream0=bool(equal))
         log(f"cpu baseline: {cpu['value']:.2f} frames/s on {cpu['cores']} threads; "
             f"codes equal over {nf} frames: {equal}")
@@ -232,7 +238,8 @@ def main():
         "config": {"workload": args.workload, "graph": not args.no_graph, "streams": n, "prompt_rows":
                    PROMPT_ROWS if b1 else "U[16,256]", "frames": steps,
                    "talker_layers": 28, "cp_layers": 5, "hidden": 1024,
-                   "heads": "16q/8kv x 128", "ffn": 3072, "weights": "Q8_0", "kv": "f32"},
+                   "heads": "16q/8kv x 128", "ffn": 3072, "weights": "Q8_0", "kv": "f32",
+                   "activations": "q8_0 (int8 MFMA)" if act_q8 else "f32"},
         "step_us_p50": round(1e6 * float(np.median(lat)), 1),
         "step_us_p99": round(1e6 * float(np.percentile(lat, 99)), 1),
         "roofline": roofline,

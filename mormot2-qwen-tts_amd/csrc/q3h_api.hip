@@ -61,6 +61,11 @@ void Work::ensure(const q3h_stack *s, int rows, int splits, int head_rows) {
   tickets = (int *)dev_alloc(sizeof(int) * R * c.heads);
   check_hip(hipMemset(tickets, 0, sizeof(int) * R * c.heads), "zero tickets");
   ctx_arr = (CtxDev **)dev_alloc(sizeof(CtxDev *) * R);
+  if (c.act_q8) {
+    const size_t Mp = (R + 15) & ~(size_t)15, maxK = std::max(std::max(H, NQ), I);
+    xa.q = (int8_t *)dev_alloc(Mp * maxK);
+    xa.d = (float *)dev_alloc(sizeof(float) * Mp * (maxK / 32));
+  }
 }
 
 void Work::release() {
@@ -74,6 +79,9 @@ void Work::release() {
   dev_free(part);
   dev_free(tickets);
   dev_free(ctx_arr);
+  dev_free(xa.q);
+  dev_free(xa.d);
+  xa = QAct{};
   tickets = nullptr;
   h = qkv = att = act = normed = logits = part = nullptr;
   rd = nullptr;
@@ -82,19 +90,50 @@ void Work::release() {
 
 int attention_splits(int positions) { return attn_splits(positions); }
 
+void linear(const q3h_stack *s, Work &w, const Mat &W, const float *x, int ldx, int M,
+            const float *norm_w, float *y, int ldy, int epi, float *xn_out, hipStream_t st) {
+  const q3h_stack_config &c = s->cfg;
+  if (c.act_q8) {
+    launch_quantize_act(x, ldx, M, W.K, norm_w, c.rms_eps, w.xa, xn_out, st);
+    launch_gemm_i8(W, w.xa, M, epi, y, ldy, st);
+  } else {
+    GemvArgs a = make_gemv(W, x, ldx, M, norm_w, c.rms_eps, y, ldy);
+    a.xn_out = xn_out;
+    launch_gemv(a, epi, c.dtype == Q3H_Q8_0, st);
+  }
+}
+
 // The layers of a stack over M rows of w.h, n contexts of R rows each (M =
 // n * R), their descriptors already in w.rd: the per-layer kernel sequence.
 void run_layers(const q3h_stack *s, Work &w, int M, int splits, bool fused, hipStream_t st) {
   const q3h_stack_config &c = s->cfg;
   const int H = c.hidden, hd = c.head_dim, NQ = c.heads * hd, NKV = c.kv_heads * hd;
   const int I = c.intermediate, ldq = NQ + 2 * NKV;
-  const bool q8 = c.dtype == Q3H_Q8_0, kv16 = c.kv_f16 != 0;
+  const bool kv16 = c.kv_f16 != 0;
   for (int l = 0; l < c.layers; l++) {
     const Layer &L = s->layers[l];
-    GemvArgs a{};
     // RMSNorm + fused q/k/v projection
-    a = make_gemv(L.qkv, w.h, H, M, L.in_norm, c.rms_eps, w.qkv, ldq);
-    launch_gemv(a, EPI_STORE, q8, st);
+    linear(s, w, L.qkv, w.h, H, M, L.in_norm, w.qkv, ldq, EPI_STORE, nullptr, st);
+    if (c.act_q8) {
+      // the int8 path: attention in its fixed order, output quantized for o_proj
+      if (!fused)
+        launch_qk_rope_append(w.qkv, ldq, w.rd, M, l, c.heads, c.kv_heads, hd, L.q_norm,
+                              L.k_norm, c.rms_eps, s->rope_cs, kv16, st);
+      AttnArgs at{};
+      at.qkv = w.qkv;
+      at.ldq = ldq;
+      at.rd = w.rd;
+      at.layer = l;
+      at.heads = c.heads;
+      at.kvh = c.kv_heads;
+      at.qkn = L.q_norm;
+      at.rope_cs = reinterpret_cast<const float2 *>(s->rope_cs);
+      launch_attn_x(at, M, fused, kv16, w.xa, c.max_positions, st);
+      launch_gemm_i8(L.o, w.xa, M, EPI_ADD, w.h, H, st);
+      linear(s, w, L.gu, w.h, H, M, L.post_norm, w.act, I, EPI_SWIGLU, nullptr, st);
+      linear(s, w, L.down, w.act, I, M, nullptr, w.h, H, EPI_ADD, nullptr, st);
+      continue;
+    }
     // QK-norm, RoPE, K/V append (in the attention prologue when fused)
     if (!fused)
       launch_qk_rope_append(w.qkv, ldq, w.rd, M, l, c.heads, c.kv_heads, hd, L.q_norm,
@@ -114,14 +153,11 @@ void run_layers(const q3h_stack *s, Work &w, int M, int splits, bool fused, hipS
     at.tickets = w.tickets;
     launch_attn(at, M, splits, fused, kv16, st);
     // o_proj + residual
-    a = make_gemv(L.o, w.att, NQ, M, nullptr, 0.f, w.h, H);
-    launch_gemv(a, EPI_ADD, q8, st);
+    linear(s, w, L.o, w.att, NQ, M, nullptr, w.h, H, EPI_ADD, nullptr, st);
     // RMSNorm + gate/up + SwiGLU
-    a = make_gemv(L.gu, w.h, H, M, L.post_norm, c.rms_eps, w.act, I);
-    launch_gemv(a, EPI_SWIGLU, q8, st);
+    linear(s, w, L.gu, w.h, H, M, L.post_norm, w.act, I, EPI_SWIGLU, nullptr, st);
     // down + residual
-    a = make_gemv(L.down, w.act, I, M, nullptr, 0.f, w.h, H);
-    launch_gemv(a, EPI_ADD, q8, st);
+    linear(s, w, L.down, w.act, I, M, nullptr, w.h, H, EPI_ADD, nullptr, st);
   }
 }
 
@@ -360,6 +396,17 @@ extern "C" int q3h_stack_create(q3h_device *dev, const q3h_stack_config *cfg,
     require(c.max_positions > 0, Q3H_E_ARG, "q3h_stack_create: max_positions <= 0");
     require(c.act_q8 == 0 || c.dtype == Q3H_Q8_0, Q3H_E_ARG,
             "q3h_stack_create: act_q8 needs Q8_0 weights");
+    require(c.act_q8 == 0 ||
+                (gemm_i8_supported(c.heads * c.head_dim + 2 * c.kv_heads * c.head_dim, c.hidden) &&
+                 gemm_i8_supported(c.hidden, c.heads * c.head_dim) &&
+                 gemm_i8_supported(2 * c.intermediate, c.hidden) &&
+                 gemm_i8_supported(c.hidden, c.intermediate)),
+            Q3H_E_ARG, "q3h_stack_create: act_q8 takes widths up to 3072");
+    require(c.act_q8 == 0 ||
+                attn_x_supported(c.heads, c.kv_heads, c.head_dim, c.max_positions),
+            Q3H_E_ARG,
+            "q3h_stack_create: act_q8 takes up to " + std::to_string(kAttnXMaxPositions) +
+                " positions");
     require(w->layers != nullptr && w->final_norm != nullptr, Q3H_E_ARG,
             "q3h_stack_create: NULL layers or final norm");
     check_hip(hipSetDevice(dev->ordinal), "hipSetDevice");
@@ -449,6 +496,8 @@ extern "C" int q3h_stack_add_head(q3h_stack *s, const void *w, int rows, int src
             "q3h_stack_add_head: src_dtype must be Q3H_F32 or Q3H_Q8_0");
     require(s->cfg.dtype == Q3H_Q8_0 || src_dtype == Q3H_F32, Q3H_E_ARG,
             "q3h_stack_add_head: an f32 stack takes f32 heads");
+    require(!s->cfg.act_q8 || rows % 16 == 0, Q3H_E_ARG,
+            "q3h_stack_add_head: an act_q8 stack takes heads of a multiple of 16 rows");
     check_hip(hipSetDevice(s->dev->ordinal), "hipSetDevice");
     std::lock_guard<std::mutex> lock(s->mu);
     const int H = s->cfg.hidden;
@@ -658,10 +707,8 @@ extern "C" int q3h_forward_embeds(q3h_context *c, const float *x, int rows, int 
     run_layers(s, w, rows, splits, rows == 1, st);
     // final norm of the last row, fused into the head product when there is one
     if (head >= 0) {
-      GemvArgs a = make_gemv(s->heads[head], w.h + (size_t)(rows - 1) * H, H, 1, s->final_norm,
-                             cf.rms_eps, w.logits, head_rows);
-      a.xn_out = w.normed;
-      launch_gemv(a, EPI_STORE, cf.dtype == Q3H_Q8_0, st);
+      linear(s, w, s->heads[head], w.h + (size_t)(rows - 1) * H, H, 1, s->final_norm, w.logits,
+             head_rows, EPI_STORE, w.normed, st);
     } else {
       launch_rmsnorm_rows(w.h + (size_t)(rows - 1) * H, H, 1, H, s->final_norm, cf.rms_eps,
                           w.normed, H, st);
@@ -730,15 +777,12 @@ extern "C" int q3h_forward_embeds_batch(q3h_context *const *ctxs, int n, const f
       bool same = true;
       for (int i = 1; i < n; i++) same = same && heads[i] == heads[0];
       if (same) {
-        GemvArgs a = make_gemv(s->heads[heads[0]], w.normed, H, n, nullptr, 0.f, w.logits,
-                               head_rows);
-        launch_gemv(a, EPI_STORE, cf.dtype == Q3H_Q8_0, st);
+        linear(s, w, s->heads[heads[0]], w.normed, H, n, nullptr, w.logits, head_rows,
+               EPI_STORE, nullptr, st);
       } else {
-        for (int i = 0; i < n; i++) {
-          GemvArgs a = make_gemv(s->heads[heads[i]], w.normed + (size_t)i * H, H, 1, nullptr,
-                                 0.f, w.logits + (size_t)i * head_rows, head_rows);
-          launch_gemv(a, EPI_STORE, cf.dtype == Q3H_Q8_0, st);
-        }
+        for (int i = 0; i < n; i++)
+          linear(s, w, s->heads[heads[i]], w.normed + (size_t)i * H, H, 1, nullptr,
+                 w.logits + (size_t)i * head_rows, head_rows, EPI_STORE, nullptr, st);
       }
     }
     launch_advance(w.ctx_arr, nullptr, n, 1, st);

@@ -74,11 +74,17 @@ struct Work {
   float *part = nullptr;    // attention partials [rows][heads][splits][head_dim + 2]
   int *tickets = nullptr;   // attention split tickets [rows][heads], zero
   CtxDev **ctx_arr = nullptr;
+  QAct xa;                  // quantized activations (act_q8 stacks)
   void ensure(const struct ::q3h_stack *s, int rows, int splits, int head_rows);
   void release();
 };
 
 int attention_splits(int positions);
+// y [M][ldy] (+)= W . x (x RMS-normed with norm_w when non-null; epi: EPI_*):
+// the f32-activation GEMV, or for act_q8 stacks the quantizer and the int8
+// product; xn_out, when non-null, receives the (normed) row M - 1
+void linear(const struct ::q3h_stack *s, Work &w, const Mat &W, const float *x, int ldx, int M,
+            const float *norm_w, float *y, int ldy, int epi, float *xn_out, hipStream_t st);
 GemvArgs make_gemv(const Mat &W, const float *x, int ldx, int M, const float *norm_w, float eps,
                    float *y, int ldy);
 // the shapes the fused code-predictor kernel takes (Q8_0, hidden 1024,

@@ -24,6 +24,7 @@
 #include <hip/hip_runtime.h>
 
 #include "q3h_internal.h"
+#include "q3h_math.h"
 #include "q3h_wave.h"
 
 namespace q3h {
@@ -73,8 +74,9 @@ __device__ __forceinline__ void norm_rope(float &x0, float &x1, float w0, float 
   const float ss = wave_sum_dpp(fmaf(x0, x0, x1 * x1));
   const float inv = 1.0f / sqrtf(ss * (1.0f / HD) + eps);
   const float a = w0 * (x0 * inv), b = w1 * (x1 * inv);
-  x0 = a * cs.x - b * cs.y;
-  x1 = b * cs.x + a * cs.y;
+  x0 = a;
+  x1 = b;
+  rope_pair(x0, x1, cs.x, cs.y);
 }
 
 __device__ __forceinline__ float rescale(float m, float mn) {

@@ -25,6 +25,7 @@
 
 #include "q3h.h"
 #include "q3h_internal.h"
+#include "q3h_math.h"
 #include "q3h_wave.h"
 
 namespace q3h {
@@ -81,8 +82,9 @@ __device__ __forceinline__ void norm_rope(float &x0, float &x1, float w0, float 
   const float ss = wave_sum_dpp(fmaf(x0, x0, x1 * x1));
   const float inv = 1.0f / sqrtf(ss * (1.0f / HD) + eps);
   const float a = w0 * (x0 * inv), b = w1 * (x1 * inv);
-  x0 = a * cs.x - b * cs.y;
-  x1 = b * cs.x + a * cs.y;
+  x0 = a;
+  x1 = b;
+  rope_pair(x0, x1, cs.x, cs.y);
 }
 
 // LDS written by some lanes of a wave and read by others of the same wave
@@ -245,7 +247,7 @@ __global__ __launch_bounds__(NT) void k_attn_o_cp(const int8_t *__restrict__ wo,
 }  // namespace
 
 bool cp_fused_supported(const q3h_stack_config &c) {
-  return c.dtype == Q3H_Q8_0 && c.hidden == HID && c.heads == KVH * GRP && c.kv_heads == KVH &&
+  return c.dtype == Q3H_Q8_0 && !c.act_q8 && c.hidden == HID && c.heads == KVH * GRP && c.kv_heads == KVH &&
          c.head_dim == HD;
 }
 

@@ -219,7 +219,6 @@ void enqueue_step(q3h_frame *f, int splits, hipStream_t st) {
   const q3h_frame_config &c = f->cfg;
   const int n = c.n_streams, H = f->H;
   q3h_stack *cp = f->cp, *tk = f->talker;
-  const bool cq8 = cp->cfg.dtype == Q3H_Q8_0, tq8 = tk->cfg.dtype == Q3H_Q8_0;
   FrameDev fd = f->fd;
   hipLaunchKernelGGL(k_choose_code0, dim3(n), dim3(kArgBlock), 0, st, fd);
   // code predictor: 2 rows per stream, then one row per group
@@ -236,10 +235,8 @@ void enqueue_step(q3h_frame *f, int splits, hipStream_t st) {
       launch_advance(f->c_arr, fd.alive, n, R, st);
     }
     // final norm of each stream's last row + head g, one launch
-    const Mat &head = cp->heads[c.cp_heads[g]];
-    GemvArgs a = make_gemv(head, f->cw.h + (size_t)(R - 1) * H, R * H, n, cp->final_norm,
-                           cp->cfg.rms_eps, f->cw.logits, c.cp_vocab);
-    launch_gemv(a, EPI_STORE, cq8, st);
+    linear(cp, f->cw, cp->heads[c.cp_heads[g]], f->cw.h + (size_t)(R - 1) * H, R * H, n,
+           cp->final_norm, f->cw.logits, c.cp_vocab, EPI_STORE, nullptr, st);
     hipLaunchKernelGGL(k_cp_argmax, dim3(n), dim3(kArgBlock), 0, st, fd.cp_logits, fd.alive,
                        fd.pred_emb, fd.cp_h, fd.codes, fd.cp_vocab, fd.groups, fd.H, g);
   }
@@ -249,13 +246,11 @@ void enqueue_step(q3h_frame *f, int splits, hipStream_t st) {
   run_layers(tk, f->tw, n, splits, true, st);
   const Mat &th = tk->heads[c.talker_head];
   if (n == 1) {  // final norm fused into the head, the normed state written alongside
-    GemvArgs a = make_gemv(th, f->tw.h, H, 1, tk->final_norm, tk->cfg.rms_eps, fd.logits, c.vocab);
-    a.xn_out = fd.past;
-    launch_gemv(a, EPI_STORE, tq8, st);
+    linear(tk, f->tw, th, f->tw.h, H, 1, tk->final_norm, fd.logits, c.vocab, EPI_STORE, fd.past,
+           st);
   } else {
     launch_rmsnorm_rows(f->tw.h, H, n, H, tk->final_norm, tk->cfg.rms_eps, fd.past, H, st);
-    GemvArgs a = make_gemv(th, fd.past, H, n, nullptr, 0.f, fd.logits, c.vocab);
-    launch_gemv(a, EPI_STORE, tq8, st);
+    linear(tk, f->tw, th, fd.past, H, n, nullptr, fd.logits, c.vocab, EPI_STORE, nullptr, st);
   }
   launch_advance(f->t_arr, fd.alive, n, 1, st);
   hipLaunchKernelGGL(k_frame_end, dim3((n + 63) / 64), dim3(64), 0, st, fd);
@@ -400,11 +395,8 @@ extern "C" int q3h_frame_start(q3h_frame *f, int stream, const float *prefill, i
     launch_prep(tc->dev_arr, nullptr, 1, rows, w.rd, st);
     run_layers(s, w, rows, splits, rows == 1, st);
     float *past = d.past + (size_t)stream * H;
-    GemvArgs a = make_gemv(s->heads[c.talker_head], w.h + (size_t)(rows - 1) * H, H, 1,
-                           s->final_norm, s->cfg.rms_eps, d.logits + (size_t)stream * c.vocab,
-                           c.vocab);
-    a.xn_out = past;
-    launch_gemv(a, EPI_STORE, s->cfg.dtype == Q3H_Q8_0, st);
+    linear(s, w, s->heads[c.talker_head], w.h + (size_t)(rows - 1) * H, H, 1, s->final_norm,
+           d.logits + (size_t)stream * c.vocab, c.vocab, EPI_STORE, past, st);
     launch_advance(tc->dev_arr, nullptr, 1, rows, st);
     check_hip(hipGetLastError(), "prefill kernels");
     if (trailing_rows > 0)

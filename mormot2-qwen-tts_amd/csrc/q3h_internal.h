@@ -53,10 +53,14 @@ struct GemvArgs {
   float *xn_out;  // optional: the (normed) last x row, [K], written by block 0
 };
 
-// activations quantized per 32-block (int8 path): q [M][K], d [M][K/32] f32
+// Activations quantized per 32-block for the int8 products, over M rows
+// padded to Mp = M rounded up to 16: q holds the 16-row tiles in MFMA operand
+// order (tile (b, m / 16) is 64 lanes x 8 bytes, lane g * 16 + m % 16 holding
+// k = 32b + 8g .. 32b + 8g + 7 of row m), d the fp16-rounded block scales
+// [Mp][K/32] as f32.
 struct QAct {
-  int8_t *q;
-  float *d;
+  int8_t *q = nullptr;
+  float *d = nullptr;
 };
 
 void launch_gemv(const GemvArgs &a, int epi, bool q8, hipStream_t st);
@@ -64,9 +68,16 @@ void launch_gemv(const GemvArgs &a, int epi, bool q8, hipStream_t st);
 // false when the shape is not one it takes (nothing launched)
 bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st, hipEvent_t ev0 = nullptr,
                          hipEvent_t ev1 = nullptr);
-void launch_gemv_i8(const GemvArgs &a, const QAct &xa, int epi, hipStream_t st);
-void launch_quantize_act(const float *x, int ldx, int M, int K, const float *norm_w,
-                         float eps, QAct out, hipStream_t st);
+// the int8 path (q3h_gemm.hip): shapes it takes (N % 16 == 0, K % 32 == 0,
+// K <= 3072)
+bool gemm_i8_supported(int N, int K);
+// rows x [M][ldx] (RMS-normed with norm_w when non-null) quantized into out;
+// xn_out, when non-null, receives the (normed) row M - 1
+void launch_quantize_act(const float *x, int ldx, int M, int K, const float *norm_w, float eps,
+                         QAct out, float *xn_out, hipStream_t st);
+// y [M][ldy] (+)= W . x over the quantized rows xa (Q8_0 W)
+void launch_gemm_i8(const Mat &W, const QAct &xa, int M, int epi, float *y, int ldy,
+                    hipStream_t st);
 
 // rows of n contexts, R consecutive rows each (R > 1: one context's prefill)
 void launch_prep(CtxDev *const *cs, const int *alive, int n, int R, RowDesc *rd,
@@ -97,6 +108,15 @@ struct AttnArgs {
 };
 int attn_splits(int positions);
 void launch_attn(const AttnArgs &a, int M, int splits, bool fused, bool kv16, hipStream_t st);
+
+// attention of the int8 path (q3h_attnx.hip): the rows of a (fused: each the
+// one new position of its own context, QK-norm / RoPE / K/V append in the
+// prologue), outputs quantized into xa for the o_proj product; positions up
+// to kAttnXMaxPositions (scores held in LDS)
+constexpr int kAttnXMaxPositions = 8192;
+bool attn_x_supported(int heads, int kvh, int head_dim, int max_positions);
+void launch_attn_x(const AttnArgs &a, int M, bool fused, bool kv16, const QAct &xa,
+                   int max_positions, hipStream_t st);
 
 // the code predictor's fused attention + o_proj + residual (q3h_cp.hip):
 // one context of 16 positions, the new row at pos; k_layer: the layer's keys,

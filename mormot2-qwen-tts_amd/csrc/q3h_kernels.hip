@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include "q3h_internal.h"
+#include "q3h_math.h"
 
 namespace q3h {
 
@@ -333,10 +334,7 @@ __global__ __launch_bounds__(kBlock) void k_qk_rope_append(
       x0 = w[lane] * (x0 * inv);
       x1 = w[lane + half] * (x1 * inv);
       const float2 cs = rope_cs[(size_t)d.pos * half + lane];
-      const float y0 = x0 * cs.x - x1 * cs.y;
-      const float y1 = x1 * cs.x + x0 * cs.y;
-      x0 = y0;
-      x1 = y1;
+      rope_pair(x0, x1, cs.x, cs.y);
     }
   }
   if (!on) return;

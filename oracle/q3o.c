@@ -4,17 +4,28 @@
  * path. See q3o.h for what each function restates (reference file:line) and
  * how it is pinned.
  *
- * Arithmetic conventions (chosen to be a clean restatement, not a copy of any
- * GPU schedule):
- *  - dot products: fp32 products, fp32 sums per 32-element block in 8 partial
- *    lanes, block results accumulated in fp32 in column order;
+ * Arithmetic conventions. The mathematics is the reference's; the order of
+ * the fp32 operations is fixed explicitly (fused multiply-adds written out)
+ * so that a device implementation can follow it to the bit:
+ *  - dot products of the linear layers: fp32 fused multiply-adds per 32-element
+ *    block in 8 partial lanes, block results accumulated in fp32 in column
+ *    order;
  *  - Q8_0 weights with f32 activations: sum_b d_b * (sum_j q_j x_j);
- *  - Q8_0 weights with Q8_0 activations (ggml vec_dot_q8_0_q8_0):
- *    sum_b (float)(sum_j qw_j qx_j) * (dw_b * dx_b), both scales via fp16;
- *  - RMSNorm, softmax sums: double accumulation, results rounded to fp32;
+ *  - Q8_0 weights with Q8_0 activations (ggml vec_dot_q8_0_q8_0): per block
+ *    the exact int32 dot, times (dw_b * dx_b) (both scales via fp16), fused
+ *    into a chain over the 8 blocks of each 256-column chunk; the chunk sums
+ *    added in chunk order;
+ *  - attention scores: q . k as 16 partial chains (dims 8l .. 8l + 7) joined
+ *    by a balanced pairwise tree; weighted values: 4 chains over the
+ *    positions p = j mod 4, joined as (c0 + c1) + (c2 + c3);
+ *  - e^x: q3o_expf (Cody-Waite reduction, Taylor series), in the softmax and
+ *    in SiLU;
+ *  - RMSNorm, softmax sums: double accumulation, results rounded to fp32 (the
+ *    order of a double sum does not reach the fp32 result in practice);
  *  - RoPE: inv_freq_i = (float)(1 / theta^(2i/d)), angle = (float)pos *
  *    inv_freq_i in fp32, cos/sin of that angle in double rounded to fp32
- *    (the HIP library builds its table the same way on the host).
+ *    (the HIP library builds its table the same way on the host);
+ *    a' = fma(a, c, -(b s)), b' = fma(b, c, a s).
  */
 #include "q3o.h"
 
@@ -105,6 +116,36 @@ void q3o_fp16_to_fp32_row(const uint16_t *x, float *y, int64_t n) {
 }
 
 /* ------------------------------------------------------------------ */
+/* e^x in fp32 from IEEE operations only                                */
+
+/* Cody & Waite (1980) argument reduction x = k ln2 + r, k = rint(x log2 e),
+ * with ln 2 split in a 16-bit head and its tail; e^r by its Taylor series to
+ * r^7 (|r| <= 0.35: truncation < 6e-9 relative), Horner form with fused
+ * multiply-adds; times 2^k from the exponent bits. Each step is one
+ * correctly rounded IEEE operation, so any IEEE machine gives the same bits.
+ * Error < 2 ulp; 0 below -86 (no subnormal results), +inf above 88. */
+float q3o_expf(float x) {
+  if (x != x) return x;
+  if (x < -86.0f) return 0.0f;
+  if (x > 88.0f) return INFINITY;
+  const float k = rintf(x * 0x1.715476p+0f);
+  float r = fmaf(k, -0x1.62e4p-1f, x);
+  r = fmaf(k, -0x1.7f7d1cp-20f, r);
+  float p = 0x1.a01a02p-13f;       /* 1/7! */
+  p = fmaf(p, r, 0x1.6c16c2p-10f); /* 1/6! */
+  p = fmaf(p, r, 0x1.111112p-7f);  /* 1/5! */
+  p = fmaf(p, r, 0x1.555556p-5f);  /* 1/4! */
+  p = fmaf(p, r, 0x1.555556p-3f);  /* 1/3! */
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  const uint32_t bits = (uint32_t)((int)k + 127) << 23;
+  float scale;
+  memcpy(&scale, &bits, 4);
+  return p * scale;
+}
+
+/* ------------------------------------------------------------------ */
 /* Q8_0: ggml quantize_row_q8_0_ref semantics                          */
 
 void q3o_quantize_row_q8_0(const float *x, void *vy, int64_t k) {
@@ -146,8 +187,23 @@ void q3o_quantize_matrix_q8_0(const float *x, void *vy, int64_t rows, int64_t co
 static inline float dot32(const float *w, const float *x) {
   float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   for (int j = 0; j < 32; j += 8)
-    for (int t = 0; t < 8; t++) s[t] += w[j + t] * x[j + t];
+    for (int t = 0; t < 8; t++) s[t] = fmaf(w[j + t], x[j + t], s[t]);
   return ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+}
+
+/* q . k over one head of D = 16 * n dims: 16 partial chains (partial l over
+ * dims l*n .. l*n + n - 1), then a balanced pairwise tree over l */
+static inline float head_dot(const float *q, const float *k, int D) {
+  const int n = D / 16;
+  float t[16];
+  for (int l = 0; l < 16; l++) {
+    float a = 0.0f;
+    for (int e = 0; e < n; e++) a = fmaf(q[l * n + e], k[l * n + e], a);
+    t[l] = a;
+  }
+  for (int w = 8; w >= 1; w /= 2)
+    for (int l = 0; l < w; l++) t[l] = t[2 * l] + t[2 * l + 1];
+  return t[0];
 }
 
 static inline int32_t idot32(const int8_t *a, const int8_t *b) {
@@ -194,9 +250,14 @@ static void linear(const void *W, int dtype, int act_q8, int N, int K,
           float acc = 0.0f;
           if (act_q8) {
             const q3o_block_q8_0 *x = xq + (size_t)m * nb;
-            for (int b = 0; b < nb; b++) {
-              const int32_t s = idot32(w[b].qs, x[b].qs);
-              acc += (float)s * (q3o_fp16_to_fp32(w[b].d) * q3o_fp16_to_fp32(x[b].d));
+            for (int b0 = 0; b0 < nb; b0 += 8) {
+              float part = 0.0f;
+              for (int b = b0; b < b0 + 8 && b < nb; b++) {
+                const int32_t s = idot32(w[b].qs, x[b].qs);
+                part = fmaf((float)s, q3o_fp16_to_fp32(w[b].d) * q3o_fp16_to_fp32(x[b].d),
+                            part);
+              }
+              acc += part;
             }
           } else {
             const float *x = X + (size_t)m * K;
@@ -233,8 +294,8 @@ static void rope(float *x, int d, int pos, float theta) {
     const float c = (float)cos((double)angle);
     const float s = (float)sin((double)angle);
     const float a = x[i], b = x[i + half];
-    x[i] = a * c - b * s;
-    x[i + half] = b * c + a * s;
+    x[i] = fmaf(a, c, -(b * s));
+    x[i + half] = fmaf(b, c, a * s);
   }
 }
 
@@ -256,7 +317,7 @@ struct q3o_ctx {
 q3o_stack *q3o_stack_create(const q3o_config *cfg, const q3o_layer *layers,
                             const float *final_norm) {
   if (cfg->hidden % 32 || cfg->intermediate % 32 || (cfg->heads * cfg->head_dim) % 32 ||
-      cfg->heads % cfg->kv_heads || cfg->head_dim % 2)
+      cfg->heads % cfg->kv_heads || cfg->head_dim % 16)
     return NULL;
   q3o_stack *s = (q3o_stack *)calloc(1, sizeof(*s));
   s->cfg = *cfg;
@@ -370,25 +431,25 @@ int q3o_forward_embeds(q3o_ctx *c, const float *x, int rows, float *normed_last,
         float *sc = (float *)malloc(sizeof(float) * n);
         float mx = -INFINITY;
         for (int p = 0; p < n; p++) {
-          const float *kc = c->k + kv_off(c, l, g, p);
-          float acc = 0.0f;
-          for (int b = 0; b < D; b += 32) acc += dot32(qh + b, kc + b);
-          sc[p] = acc * scale;
+          sc[p] = head_dot(qh, c->k + kv_off(c, l, g, p), D) * scale;
           mx = sc[p] > mx ? sc[p] : mx;
         }
         double sum = 0.0;
         for (int p = 0; p < n; p++) {
-          sc[p] = expf(sc[p] - mx);
+          sc[p] = q3o_expf(sc[p] - mx);
           sum += sc[p];
         }
         const float inv = (float)(1.0 / sum);
         float *o = att + r * NQ + hh * D;
-        for (int d = 0; d < D; d++) o[d] = 0.0f;
+        float *ch = (float *)calloc((size_t)4 * D, sizeof(float));
         for (int p = 0; p < n; p++) {
           const float *vc = c->v + kv_off(c, l, g, p);
           const float w = sc[p] * inv;
-          for (int d = 0; d < D; d++) o[d] += w * vc[d];
+          float *cj = ch + (size_t)(p & 3) * D;
+          for (int d = 0; d < D; d++) cj[d] = fmaf(w, vc[d], cj[d]);
         }
+        for (int d = 0; d < D; d++) o[d] = (ch[d] + ch[D + d]) + (ch[2 * D + d] + ch[3 * D + d]);
+        free(ch);
         free(sc);
       }
     }
@@ -398,7 +459,7 @@ int q3o_forward_embeds(q3o_ctx *c, const float *x, int rows, float *normed_last,
     linear(L->wup, q->dtype, q->act_q8, I, H, xn, rows, ub, I, 0);
     for (int i = 0; i < rows * I; i++) {
       const float g = gb[i];
-      gb[i] = g / (1.0f + expf(-g)) * ub[i];
+      gb[i] = g / (1.0f + q3o_expf(-g)) * ub[i];
     }
     linear(L->wdown, q->dtype, q->act_q8, H, I, gb, rows, h, H, 1);
     if (layer_out) memcpy(layer_out + (size_t)l * rows * H, h, sizeof(float) * rows * H);

@@ -113,6 +113,11 @@ void q3o_head(const void *w, int dtype, int act_q8, int rows_out, int hidden,
 /* first max wins */
 int q3o_argmax(const float *p, int n);
 
+/* e^x from IEEE operations only (Cody-Waite reduction, Taylor series to r^7),
+   the exponential of the attention softmax and of SiLU; < 2 ulp, 0 below
+   -86, +inf above 88 */
+float q3o_expf(float x);
+
 /* TQwenTalker.ChooseCode0, greedy: logits processors then argmax */
 int q3o_choose_code0(const float *logits, int vocab, int eos, const int *history,
                      int nhistory, float penalty);

@@ -74,6 +74,7 @@ def lib():
             "q3o_head": (None, [_P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _FP,
                                 _FP]),
             "q3o_argmax": (ctypes.c_int, [_FP, ctypes.c_int]),
+            "q3o_expf": (ctypes.c_float, [ctypes.c_float]),
             "q3o_choose_code0": (ctypes.c_int, [_FP, ctypes.c_int, ctypes.c_int, _IP,
                                                 ctypes.c_int, ctypes.c_float]),
             "q3o_frame_create": (_P, [_P, _P, ctypes.POINTER(FrameTables), ctypes.c_int]),
@@ -135,6 +136,13 @@ def dequantize_q8_0(b, k):
         lib().q3o_dequantize_row_q8_0(b[r].ctypes.data_as(_P) if b.ndim > 1 else
                                       b.ctypes.data_as(_P), _fp(out[r]), k)
     return out if b.ndim > 1 else out[0]
+
+
+def expf(x):
+    """q3o_expf elementwise over x (float32)."""
+    f = lib().q3o_expf
+    return np.array([f(float(v)) for v in np.asarray(x, np.float32).ravel()],
+                    np.float32).reshape(np.shape(x))
 
 
 def argmax(p):

@@ -183,3 +183,23 @@ def test_choose_code0_penalty_once_per_code(q3o):
     lg[8] = -1.04
     # a negative logit is multiplied: -1.05 < -1.04
     assert q3o.choose_code0(lg, -1, [7], 1.05) == 8
+
+
+def test_expf_accuracy_and_special_values(q3o):
+    """q3o_expf (Cody-Waite reduction + Taylor series) against double-precision
+    exp: < 2 ulp over the range it returns normal numbers, exact at 0, and the
+    documented cut-offs (0 below -86, +inf above 88, NaN kept)."""
+    x = np.concatenate([np.linspace(-86.0, 88.0, 40001, dtype=np.float32),
+                        np.float32([-1e-30, 1e-30, -0.5, 0.5, 0.34657359, -0.34657359])])
+    got = q3o.expf(x).astype(np.float64)
+    ref = np.exp(x.astype(np.float64))
+    ulp = np.spacing(ref.astype(np.float32)).astype(np.float64)
+    err = np.abs(got - ref) / ulp
+    assert err.max() < 2.0, (float(err.max()), float(x[np.argmax(err)]))
+    assert q3o.expf(np.float32([0.0]))[0] == 1.0
+    assert np.all(q3o.expf(np.float32([-86.5, -100.0, -np.inf])) == 0.0)
+    assert np.all(np.isposinf(q3o.expf(np.float32([88.5, 1000.0, np.inf]))))
+    assert np.isnan(q3o.expf(np.float32([np.nan]))[0])
+    # monotone where it matters for the softmax (x <= 0)
+    neg = q3o.expf(np.linspace(-20.0, 0.0, 20001, dtype=np.float32))
+    assert np.all(np.diff(neg) >= 0)

@@ -6,7 +6,9 @@
 - incremental calls equal one call over the same rows (the causal property that
   the reference fixture relies on for predictor.logits, manifest.json note).
 - Q8_0 (f32 activations) equals the f32 stack over the dequantized weights.
-- Q8_0 activations (int8 products) stay within the quantization noise.
+- Q8_0 activations (int8 products) stay within the quantization noise, and
+  turn fp32-level input differences into much larger output differences (the
+  reason the GPU int8 path is checked bit for bit).
 - fp16 K/V cache stays close to the f32 cache.
 """
 import os
@@ -161,3 +163,27 @@ def test_context_overflow_is_refused(q3o, synth):
     assert c.length == 3
     c.destroy()
     st.destroy()
+
+
+def test_int8_activations_amplify_rounding_differences(q3o, synth):
+    """Why the int8 path is checked bit for bit: with quantized activations a
+    1e-7 relative change of the input (an fp32 rounding) moves the output by
+    orders more, because elements land on the other side of a rounding
+    boundary of their block; with f32 activations it stays at the fp32
+    level."""
+    dims, L, f, s1 = small_stack(synth, q3o, 17, q3o.Q8_0, act_q8=1, layers=4)
+    s0 = q3o.Stack(dims, L, f, q3o.Q8_0, act_q8=0)
+    x = synth.prompt(17, 24, dims["hidden"])
+    rng = np.random.default_rng(0)
+    xp = (x * (1 + 1e-7 * rng.standard_normal(x.shape))).astype(np.float32)
+    moved = {}
+    for name, st in (("int8", s1), ("f32", s0)):
+        a, b = q3o.Ctx(st, 32), q3o.Ctx(st, 32)
+        moved[name] = rel(b.forward(xp), a.forward(x))
+        a.destroy()
+        b.destroy()
+    print(f"output moved by a 1e-7 input change: {moved}")
+    assert moved["int8"] > 1e-4 and moved["f32"] < 1e-5
+    assert moved["int8"] > 100 * moved["f32"]
+    s0.destroy()
+    s1.destroy()
