@@ -62,9 +62,15 @@ void Work::ensure(const q3h_stack *s, int rows, int splits, int head_rows) {
   check_hip(hipMemset(tickets, 0, sizeof(int) * R * c.heads), "zero tickets");
   ctx_arr = (CtxDev **)dev_alloc(sizeof(CtxDev *) * R);
   if (c.act_q8) {
-    const size_t Mp = (R + 15) & ~(size_t)15, maxK = std::max(std::max(H, NQ), I);
-    xa.q = (int8_t *)dev_alloc(Mp * maxK);
-    xa.d = (float *)dev_alloc(sizeof(float) * Mp * (maxK / 32));
+    const int maxK = std::max(std::max(H, NQ), I);
+    xa.q = (int8_t *)dev_alloc(qact_bytes((int)R, maxK));
+    // chunk partials of the products over up to kPartialRows rows
+    const size_t pr = std::min<size_t>(R, kPartialRows);
+    const size_t ldq = NQ + 2 * NKV;
+    size_t pn = (size_t)gemm_i8_chunks(H) * pr * std::max(ldq, (size_t)2 * I);
+    pn = std::max(pn, (size_t)gemm_i8_chunks(NQ) * pr * H);
+    pn = std::max(pn, (size_t)gemm_i8_chunks(I) * pr * H);
+    gpart = (float *)dev_alloc(sizeof(float) * pn);
   }
 }
 
@@ -80,8 +86,9 @@ void Work::release() {
   dev_free(tickets);
   dev_free(ctx_arr);
   dev_free(xa.q);
-  dev_free(xa.d);
+  dev_free(gpart);
   xa = QAct{};
+  gpart = nullptr;
   tickets = nullptr;
   h = qkv = att = act = normed = logits = part = nullptr;
   rd = nullptr;
@@ -103,6 +110,53 @@ void linear(const q3h_stack *s, Work &w, const Mat &W, const float *x, int ldx, 
   }
 }
 
+// The int8 path over M <= kPartialRows rows: every product leaves its chunk
+// partials (one wave per 16 rows and 256 columns over the whole chip), and
+// the consumer adds them in chunk order: the attention prologue (q/k/v, decode
+// rows), the residual add + RMSNorm + quantization of the next input (o_proj,
+// down), SiLU(gate) * up + quantization (gate/up). Results equal the
+// workgroup-reduced schedule of run_layers to the bit.
+static void run_layers_partial(const q3h_stack *s, Work &w, int M, bool fused, hipStream_t st) {
+  const q3h_stack_config &c = s->cfg;
+  const int H = c.hidden, hd = c.head_dim, NQ = c.heads * hd, NKV = c.kv_heads * hd;
+  const int I = c.intermediate, ldq = NQ + 2 * NKV;
+  const bool kv16 = c.kv_f16 != 0;
+  const float eps = c.rms_eps;
+  launch_quantize_act(w.h, H, M, H, s->layers[0].in_norm, eps, w.xa, nullptr, st);
+  for (int l = 0; l < c.layers; l++) {
+    const Layer &L = s->layers[l];
+    AttnArgs at{};
+    at.ldq = ldq;
+    at.rd = w.rd;
+    at.layer = l;
+    at.heads = c.heads;
+    at.kvh = c.kv_heads;
+    at.qkn = L.q_norm;
+    at.rope_cs = reinterpret_cast<const float2 *>(s->rope_cs);
+    if (fused) {
+      launch_gemm_i8_partial(L.qkv, w.xa, M, w.gpart, st);
+      at.qkv = w.gpart;
+      launch_attn_x(at, M, true, kv16, gemm_i8_chunks(H), w.xa, c.max_positions, st);
+    } else {
+      launch_gemm_i8(L.qkv, w.xa, M, EPI_STORE, w.qkv, ldq, st);
+      launch_qk_rope_append(w.qkv, ldq, w.rd, M, l, c.heads, c.kv_heads, hd, L.q_norm,
+                            L.k_norm, eps, s->rope_cs, kv16, st);
+      at.qkv = w.qkv;
+      launch_attn_x(at, M, false, kv16, 0, w.xa, c.max_positions, st);
+    }
+    launch_gemm_i8_partial(L.o, w.xa, M, w.gpart, st);
+    launch_residual_quantize(w.h, w.gpart, gemm_i8_chunks(NQ), M, H, L.post_norm, eps, &w.xa,
+                             st);
+    launch_gemm_i8_partial(L.gu, w.xa, M, w.gpart, st);
+    launch_swiglu_quantize(w.gpart, gemm_i8_chunks(H), M, I, w.xa, st);
+    launch_gemm_i8_partial(L.down, w.xa, M, w.gpart, st);
+    const bool next = l + 1 < c.layers;
+    launch_residual_quantize(w.h, w.gpart, gemm_i8_chunks(I), M, H,
+                             next ? s->layers[l + 1].in_norm : nullptr, eps,
+                             next ? &w.xa : nullptr, st);
+  }
+}
+
 // The layers of a stack over M rows of w.h, n contexts of R rows each (M =
 // n * R), their descriptors already in w.rd: the per-layer kernel sequence.
 void run_layers(const q3h_stack *s, Work &w, int M, int splits, bool fused, hipStream_t st) {
@@ -110,6 +164,10 @@ void run_layers(const q3h_stack *s, Work &w, int M, int splits, bool fused, hipS
   const int H = c.hidden, hd = c.head_dim, NQ = c.heads * hd, NKV = c.kv_heads * hd;
   const int I = c.intermediate, ldq = NQ + 2 * NKV;
   const bool kv16 = c.kv_f16 != 0;
+  if (c.act_q8 && M <= kPartialRows) {
+    run_layers_partial(s, w, M, fused, st);
+    return;
+  }
   for (int l = 0; l < c.layers; l++) {
     const Layer &L = s->layers[l];
     // RMSNorm + fused q/k/v projection
@@ -128,7 +186,7 @@ void run_layers(const q3h_stack *s, Work &w, int M, int splits, bool fused, hipS
       at.kvh = c.kv_heads;
       at.qkn = L.q_norm;
       at.rope_cs = reinterpret_cast<const float2 *>(s->rope_cs);
-      launch_attn_x(at, M, fused, kv16, w.xa, c.max_positions, st);
+      launch_attn_x(at, M, fused, kv16, 0, w.xa, c.max_positions, st);
       launch_gemm_i8(L.o, w.xa, M, EPI_ADD, w.h, H, st);
       linear(s, w, L.gu, w.h, H, M, L.post_norm, w.act, I, EPI_SWIGLU, nullptr, st);
       linear(s, w, L.down, w.act, I, M, nullptr, w.h, H, EPI_ADD, nullptr, st);
@@ -405,7 +463,8 @@ extern "C" int q3h_stack_create(q3h_device *dev, const q3h_stack_config *cfg,
     require(c.act_q8 == 0 ||
                 attn_x_supported(c.heads, c.kv_heads, c.head_dim, c.max_positions),
             Q3H_E_ARG,
-            "q3h_stack_create: act_q8 takes up to " + std::to_string(kAttnXMaxPositions) +
+            "q3h_stack_create: act_q8 takes up to " +
+                std::to_string(kAttnXMaxPositions / std::max(1, c.heads / std::max(1, c.kv_heads))) +
                 " positions");
     require(w->layers != nullptr && w->final_norm != nullptr, Q3H_E_ARG,
             "q3h_stack_create: NULL layers or final norm");

@@ -8,10 +8,12 @@
 // instead of to a tolerance.
 //
 // One workgroup of 256 threads per (query head, row):
-//  - prologue (a decode row, one new position of its own context): RMSNorm
-//    of q and of the new k (double sum of squares), RoPE as rope_pair, v
-//    copied; the first query head of the kv group appends k, v to the cache;
-//    the others use their own copy for the new position;
+//  - prologue (a decode row, one new position of its own context): q, k, v
+//    of the row (from the product's chunk partials, added in chunk order,
+//    when the product left them as partials); RMSNorm of q and of the new k
+//    (double sum of squares), RoPE as rope_pair, v copied; the first query
+//    head of the kv group appends k, v to the cache, the others use their
+//    own copy for the new position;
 //  - scores: 16 lanes per key, lane l a fused multiply-add chain over dims
 //    8l .. 8l + 7, a balanced pairwise tree over the 16 lanes (DPP row
 //    operations), times 1/sqrt(128);
@@ -35,7 +37,7 @@ namespace q3h {
 namespace {
 
 constexpr int HD = 128;
-constexpr int NT = 256;
+constexpr int NT = 512;
 
 template <typename KV>
 __device__ __forceinline__ void load8(const KV *p, float (&o)[8]) {
@@ -63,6 +65,16 @@ __device__ __forceinline__ float2 load2(const KV *p) {
   }
 }
 
+// element col of row m: the product's output, or its chunk partials
+// [nch][M][ld] added in chunk order
+__device__ __forceinline__ float qkv_at(const float *qkv, int ld, int nch, int M, int m, int col) {
+  if (nch == 0) return qkv[(size_t)m * ld + col];
+  float s = 0.f;
+#pragma unroll 4
+  for (int c = 0; c < nch; c++) s = __fadd_rn(s, qkv[((size_t)c * M + m) * ld + col]);
+  return s;
+}
+
 // sum over a 16-lane DPP row, the balanced pairwise tree in lane order
 // ((l0 + l1) + (l2 + l3)) + ..., the same value in all 16 lanes
 __device__ __forceinline__ float row16_tree(float v) {
@@ -73,183 +85,247 @@ __device__ __forceinline__ float row16_tree(float v) {
   return v;
 }
 
-template <typename KV, bool FUSED>
-__global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *qkv, int ldq,
+// grid (kv heads, M): the GRP query heads of kv head g = blockIdx.x share one
+// read of its K/V. NCH > 0: the q/k/v come as NCH chunk partials.
+template <typename KV, bool FUSED, int GRP>
+__global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *qkv,
                                                const float *qkn, const float2 *rope_cs,
-                                               int layer, int heads, int kvh, int8_t *xq,
-                                               float *dx, int M) {
-  extern __shared__ float sc[];  // per position: score, then e^(score - max)
-  __shared__ float qs[HD], kn[HD], vn[HD];
-  __shared__ float cv[4][HD];
-  __shared__ float redf[NT / 64];
-  __shared__ double redd[NT / 64];
-  const int h = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
+                                               int8_t *xq, int ldq, int layer, int nch) {
+  extern __shared__ float sc[];  // [GRP][L]: scores, then e^(score - max)
+  __shared__ float qs[GRP][HD], kn[HD], vn[HD];
+  __shared__ float cv[4][GRP][HD];
+  __shared__ float redf[GRP][NT / 64];
+  __shared__ double redd[GRP][NT / 64];
+  const int g = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
+  const int kvh = gridDim.x, heads = kvh * GRP, M = gridDim.y;
   const int lane = t & 63, wave = t >> 6;
-  const int grp = heads / kvh, g = h / grp;
   const int NQ = heads * HD, nbq = NQ >> 5, mt16 = (M + 15) >> 4;
+  float *dx = reinterpret_cast<float *>(xq + (size_t)mt16 * 16 * NQ);
+  // output k of query head h, row m: byte ((b * mt16 + m / 16) * 64 + (k % 32) / 8
+  // * 16 + m % 16) * 8 + k % 8 of the operand tiles, b = 4 h + k / 32
+  auto qoff = [&](int h, int k) {
+    return (((size_t)(4 * h + (k >> 5)) * mt16 + (m >> 4)) * 64 + ((k & 31) >> 3) * 16 +
+            (m & 15)) * 8 + (k & 7);
+  };
   const RowDesc d = rd[m];
-  // this head's 4 output blocks in the operand tiles: byte of element k of
-  // row m at ((b * mt16 + m / 16) * 64 + (k % 32) / 8 * 16 + m % 16) * 8 + k % 8
-  const int kk = t & 31, bg = h * 4 + (t >> 5);
-  const size_t qoff =
-      (((size_t)bg * mt16 + (m >> 4)) * 64 + (kk >> 3) * 16 + (m & 15)) * 8 + (kk & 7);
   if (d.pos < 0) {  // inactive row: zero blocks
-    if (t < HD) {
-      xq[qoff] = 0;
-      if (kk == 0) dx[(size_t)m * nbq + bg] = 0.f;
+    for (int i = t; i < GRP * HD; i += NT) {
+      const int h = g * GRP + i / HD, k = i % HD;
+      xq[qoff(h, k)] = 0;
+      if ((k & 31) == 0) dx[(size_t)m * nbq + 4 * h + (k >> 5)] = 0.f;
     }
     return;
   }
   const int pos = d.pos, L = pos + 1;
-  const float *row = qkv + (size_t)m * ldq;
   const size_t head_off = ((size_t)layer * kvh + g) * d.max_pos * HD;
   const KV *kc = reinterpret_cast<const KV *>(d.k) + head_off;
   const KV *vc = reinterpret_cast<const KV *>(d.v) + head_off;
 
   if (FUSED) {
-    if (wave < 2) {  // wave 0: q, wave 1: the new k
-      const float *src = wave == 0 ? row + (size_t)h * HD : row + NQ + (size_t)g * HD;
-      const float *w = qkn + (wave == 0 ? 0 : HD);
-      const float eps = qkn[2 * HD];
-      float x0 = src[lane], x1 = src[lane + 64];
-      double ss = (double)x0 * (double)x0 + (double)x1 * (double)x1;
-      ss = wave_sum_dpp_d(ss);
-      const float inv = (float)(1.0 / sqrt(ss / HD + (double)eps));
-      x0 = w[lane] * (x0 * inv);
-      x1 = w[lane + 64] * (x1 * inv);
-      const float2 cs = rope_cs[(size_t)pos * (HD / 2) + lane];
-      rope_pair(x0, x1, cs.x, cs.y);
-      if (wave == 0) {
-        qs[lane] = x0;
-        qs[lane + 64] = x1;
-      } else {
-        const KV k0 = (KV)x0, k1 = (KV)x1;  // the cache's precision
-        kn[lane] = (float)k0;
-        kn[lane + 64] = (float)k1;
-        if (h % grp == 0) {
-          KV *dst = const_cast<KV *>(kc) + (size_t)pos * HD;
-          dst[lane] = k0;
-          dst[lane + 64] = k1;
-        }
+    // vector j: query head g GRP + j (j < GRP), the new k (j == GRP), v (GRP + 1)
+    for (int j = wave; j < GRP + 2; j += NT / 64) {
+      const int col = j < GRP ? (g * GRP + j) * HD : j == GRP ? NQ + g * HD : NQ + (kvh + g) * HD;
+      float x0 = qkv_at(qkv, ldq, nch, M, m, col + lane);
+      float x1 = qkv_at(qkv, ldq, nch, M, m, col + lane + 64);
+      if (j <= GRP) {
+        const float *w = qkn + (j < GRP ? 0 : HD);
+        const float eps = qkn[2 * HD];
+        double ss = (double)x0 * (double)x0 + (double)x1 * (double)x1;
+        ss = wave_sum_dpp_d(ss);
+        const float inv = (float)(1.0 / sqrt(ss / HD + (double)eps));
+        x0 = w[lane] * (x0 * inv);
+        x1 = w[lane + 64] * (x1 * inv);
+        const float2 cs = rope_cs[(size_t)pos * (HD / 2) + lane];
+        rope_pair(x0, x1, cs.x, cs.y);
       }
-    } else if (wave == 2) {  // the new v
-      const float *src = row + NQ + (size_t)(kvh + g) * HD;
-      const KV v0 = (KV)src[lane], v1 = (KV)src[lane + 64];
-      vn[lane] = (float)v0;
-      vn[lane + 64] = (float)v1;
-      if (h % grp == 0) {
-        KV *dst = const_cast<KV *>(vc) + (size_t)pos * HD;
-        dst[lane] = v0;
-        dst[lane + 64] = v1;
+      if (j < GRP) {
+        qs[j][lane] = x0;
+        qs[j][lane + 64] = x1;
+      } else {
+        const KV a0 = (KV)x0, a1 = (KV)x1;  // the cache's precision
+        float *own = j == GRP ? kn : vn;
+        own[lane] = (float)a0;
+        own[lane + 64] = (float)a1;
+        KV *dst = const_cast<KV *>(j == GRP ? kc : vc) + (size_t)pos * HD;
+        dst[lane] = a0;
+        dst[lane + 64] = a1;
       }
     }
-  } else if (t < HD) {
-    qs[t] = row[(size_t)h * HD + t];  // normed and rotated by the append kernel
+  } else {
+    for (int i = t; i < GRP * HD; i += NT)  // normed and rotated by the append kernel
+      qs[i / HD][i % HD] = qkv[(size_t)m * ldq + (g * GRP + i / HD) * HD + i % HD];
   }
   __syncthreads();
 
-  // scores: key group kg = t / 16 takes positions kg, kg + 16, ...
+  // scores: key group kg = t / 16 takes positions kg, kg + 32, ...; the loads
+  // of SU positions are issued together
   const float scale = (float)(1.0 / __builtin_sqrt((double)HD));
   {
+    constexpr int KG = NT / 16, SU = 4;
     const int kg = t >> 4, li = t & 15;
-    float qv[8];
+    float qv[GRP][8];
 #pragma unroll
-    for (int e = 0; e < 8; e++) qv[e] = qs[8 * li + e];
-    for (int p0 = 0; p0 < L; p0 += NT / 16) {
-      const int p = p0 + kg;
-      float a = 0.f;
-      if (p < L) {
-        float k8[8];
-        if (FUSED && p == pos) {
+    for (int j = 0; j < GRP; j++)
 #pragma unroll
-          for (int e = 0; e < 8; e++) k8[e] = kn[8 * li + e];
+      for (int e = 0; e < 8; e++) qv[j][e] = qs[j][8 * li + e];
+    for (int p0 = 0; p0 < L; p0 += KG * SU) {
+      float k8[SU][8];
+#pragma unroll
+      for (int u = 0; u < SU; u++) {
+        const int p = p0 + u * KG + kg;
+        if (p < L && !(FUSED && p == pos)) {
+          load8(kc + (size_t)p * HD + 8 * li, k8[u]);
         } else {
-          load8(kc + (size_t)p * HD + 8 * li, k8);
-        }
 #pragma unroll
-        for (int e = 0; e < 8; e++) a = fmaf(qv[e], k8[e], a);
+          for (int e = 0; e < 8; e++) k8[u][e] = FUSED && p == pos ? kn[8 * li + e] : 0.f;
+        }
       }
-      a = row16_tree(a);
-      if (p < L && li == 0) sc[p] = __fmul_rn(a, scale);
+#pragma unroll
+      for (int u = 0; u < SU; u++) {
+        const int p = p0 + u * KG + kg;
+#pragma unroll
+        for (int j = 0; j < GRP; j++) {
+          float a = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; e++) a = fmaf(qv[j][e], k8[u][e], a);
+          a = row16_tree(a);
+          if (p < L && li == 0) sc[j * L + p] = __fmul_rn(a, scale);
+        }
+      }
     }
   }
   __syncthreads();
 
-  // softmax
-  float mx = -INFINITY;
-  for (int p = t; p < L; p += NT) mx = fmaxf(mx, sc[p]);
-  mx = wave_max_dpp(mx);
-  if (lane == 0) redf[wave] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
-  double sum = 0.0;
-  for (int p = t; p < L; p += NT) {
-    const float e = exp_ieee(__fsub_rn(sc[p], mx));
-    sc[p] = e;
-    sum += (double)e;
-  }
-  sum = wave_sum_dpp_d(sum);
-  if (lane == 0) redd[wave] = sum;
-  __syncthreads();
-  const float inv = (float)(1.0 / ((redd[0] + redd[1]) + (redd[2] + redd[3])));
-
-  // values: chain j = wave over positions p = j mod 4, dims 2 lane, 2 lane + 1
+  // softmax per head
+  float inv[GRP];
   {
-    float c0 = 0.f, c1 = 0.f;
-    for (int p = wave; p < L; p += 4) {
-      const float w = __fmul_rn(sc[p], inv);
-      float2 v;
-      if (FUSED && p == pos)
-        v = make_float2(vn[2 * lane], vn[2 * lane + 1]);
-      else
-        v = load2(vc + (size_t)p * HD + 2 * lane);
-      c0 = fmaf(w, v.x, c0);
-      c1 = fmaf(w, v.y, c1);
+    float mx[GRP];
+#pragma unroll
+    for (int j = 0; j < GRP; j++) mx[j] = -INFINITY;
+    for (int p = t; p < L; p += NT)
+#pragma unroll
+      for (int j = 0; j < GRP; j++) mx[j] = fmaxf(mx[j], sc[j * L + p]);
+#pragma unroll
+    for (int j = 0; j < GRP; j++) {
+      mx[j] = wave_max_dpp(mx[j]);
+      if (lane == 0) redf[j][wave] = mx[j];
     }
-    cv[wave][2 * lane] = c0;
-    cv[wave][2 * lane + 1] = c1;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < GRP; j++) {
+      float v = redf[j][0];
+#pragma unroll
+      for (int w = 1; w < NT / 64; w++) v = fmaxf(v, redf[j][w]);
+      mx[j] = v;
+    }
+    double sum[GRP];
+#pragma unroll
+    for (int j = 0; j < GRP; j++) sum[j] = 0.0;
+    for (int p = t; p < L; p += NT)
+#pragma unroll
+      for (int j = 0; j < GRP; j++) {
+        const float e = exp_ieee(__fsub_rn(sc[j * L + p], mx[j]));
+        sc[j * L + p] = e;
+        sum[j] += (double)e;
+      }
+#pragma unroll
+    for (int j = 0; j < GRP; j++) {
+      sum[j] = wave_sum_dpp_d(sum[j]);
+      if (lane == 0) redd[j][wave] = sum[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < GRP; j++) {
+      double s2 = 0.0;
+#pragma unroll
+      for (int w = 0; w < NT / 64; w++) s2 += redd[j][w];
+      inv[j] = (float)(1.0 / s2);
+    }
+  }
+
+  // values: chain ch = wave % 4 over positions p = ch mod 4, dim (wave / 4) 64
+  // + lane, every head of the group; the loads of VU positions issued together
+  {
+    constexpr int VU = 8;
+    const int ch = wave & 3, dim = (wave >> 2) * 64 + lane;
+    float c[GRP];
+#pragma unroll
+    for (int j = 0; j < GRP; j++) c[j] = 0.f;
+    for (int p0 = ch; p0 < L; p0 += 4 * VU) {
+      float v[VU];
+#pragma unroll
+      for (int u = 0; u < VU; u++) {
+        const int p = p0 + 4 * u;
+        v[u] = p < L ? (FUSED && p == pos ? vn[dim] : (float)vc[(size_t)p * HD + dim]) : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < VU; u++) {
+        const int p = p0 + 4 * u;
+        if (p < L)
+#pragma unroll
+          for (int j = 0; j < GRP; j++) c[j] = fmaf(__fmul_rn(sc[j * L + p], inv[j]), v[u], c[j]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < GRP; j++) cv[ch][j][dim] = c[j];
   }
   __syncthreads();
 
-  // quantize the head's 128 outputs per 32-block
-  if (t < HD) {
-    const float o = __fadd_rn(__fadd_rn(cv[0][t], cv[1][t]), __fadd_rn(cv[2][t], cv[3][t]));
+  // quantize each head's 128 outputs per 32-block (a 32-lane half-wave each)
+  for (int i = t; i < GRP * HD; i += NT) {
+    const int j = i / HD, k = i % HD, h = g * GRP + j;
+    const float o =
+        __fadd_rn(__fadd_rn(cv[0][j][k], cv[1][j][k]), __fadd_rn(cv[2][j][k], cv[3][j][k]));
     float amax = fabsf(o);
 #pragma unroll
-    for (int s = 16; s >= 1; s >>= 1) amax = fmaxf(amax, __shfl_xor(amax, s));
+    for (int s2 = 16; s2 >= 1; s2 >>= 1) amax = fmaxf(amax, __shfl_xor(amax, s2));
     const float dq = __fdiv_rn(amax, 127.0f);
     const float id = dq != 0.f ? __fdiv_rn(1.0f, dq) : 0.f;
-    xq[qoff] = (int8_t)(int)roundf(__fmul_rn(o, id));
-    if (kk == 0) dx[(size_t)m * nbq + bg] = (float)(_Float16)dq;
+    xq[qoff(h, k)] = (int8_t)(int)roundf(__fmul_rn(o, id));
+    if ((k & 31) == 0) dx[(size_t)m * nbq + 4 * h + (k >> 5)] = (float)(_Float16)dq;
   }
 }
 
 }  // namespace
 
 bool attn_x_supported(int heads, int kvh, int head_dim, int max_positions) {
-  return head_dim == HD && kvh > 0 && heads % kvh == 0 && max_positions > 0 &&
-         max_positions <= kAttnXMaxPositions;
+  return head_dim == HD && kvh > 0 && heads % kvh == 0 &&
+         (heads / kvh == 1 || heads / kvh == 2 || heads / kvh == 4) && max_positions > 0 &&
+         (size_t)max_positions * (heads / kvh) <= (size_t)kAttnXMaxPositions;
 }
 
-void launch_attn_x(const AttnArgs &a, int M, bool fused, bool kv16, const QAct &xa,
-                   int max_positions, hipStream_t st) {
-  const dim3 grid(a.heads, M);
-  const size_t lds = sizeof(float) * (size_t)max_positions;
-#define Q3H_ATTNX(KV, F)                                                                    \
-  hipLaunchKernelGGL((k_attn_x<KV, F>), grid, dim3(NT), lds, st, a.rd, a.qkv, a.ldq, a.qkn, \
-                     a.rope_cs, a.layer, a.heads, a.kvh, xa.q, xa.d, M)
+template <typename KV, bool F>
+void attn_x_grp(const AttnArgs &a, int M, int nch, const QAct &xa, int max_positions,
+                hipStream_t st) {
+  const dim3 grid(a.kvh, M);
+  const int grp = a.heads / a.kvh;
+  const size_t lds = sizeof(float) * (size_t)grp * max_positions;
+#define Q3H_ATTNX(G)                                                                           \
+  hipLaunchKernelGGL((k_attn_x<KV, F, G>), grid, dim3(NT), lds, st, a.rd, a.qkv, a.qkn,       \
+                     a.rope_cs, xa.q, a.ldq, a.layer, nch)
+  if (grp == 1)
+    Q3H_ATTNX(1);
+  else if (grp == 2)
+    Q3H_ATTNX(2);
+  else
+    Q3H_ATTNX(4);
+#undef Q3H_ATTNX
+}
+
+void launch_attn_x(const AttnArgs &a, int M, bool fused, bool kv16, int qkv_chunks,
+                   const QAct &xa, int max_positions, hipStream_t st) {
+  const int nch = fused ? qkv_chunks : 0;
   if (kv16) {
     if (fused)
-      Q3H_ATTNX(_Float16, true);
+      attn_x_grp<_Float16, true>(a, M, nch, xa, max_positions, st);
     else
-      Q3H_ATTNX(_Float16, false);
+      attn_x_grp<_Float16, false>(a, M, nch, xa, max_positions, st);
   } else {
     if (fused)
-      Q3H_ATTNX(float, true);
+      attn_x_grp<float, true>(a, M, nch, xa, max_positions, st);
     else
-      Q3H_ATTNX(float, false);
+      attn_x_grp<float, false>(a, M, nch, xa, max_positions, st);
   }
-#undef Q3H_ATTNX
 }
 
 }  // namespace q3h

@@ -15,8 +15,16 @@
 // row l % 16 of A and of column l % 16 of B, k = 8 * (l / 16) .. + 7; the
 // result C[4 * (l / 16) + r][l % 16], r < 4, lands in lane l. A is 16 weight
 // rows read straight from the row-major Q8_0 matrix; B is 16 activation rows,
-// which the quantizer writes already in operand order, so each B operand is
+// which the quantizers write already in operand order, so each B operand is
 // one coalesced 512-byte load.
+//
+// Two schedules of the same chains:
+//  - k_gemm_i8: a workgroup per 16 weight rows, its waves taking the chunks
+//    and adding them through LDS; any number of rows (prefill);
+//  - k_gemm_i8p (up to 64 rows, the batched decode step): one wave per (16
+//    weight rows, chunk) over the whole chip, the chunk sums written out as
+//    partials that the consumer adds in chunk order (k_quant_act with a
+//    partial source, or the attention prologue).
 #include "q3h_internal.h"
 #include "q3h_math.h"
 #include "q3h_wave.h"
@@ -30,40 +38,119 @@ constexpr int kQuantThreads = 128;
 constexpr int kQuantChunks = 3;  // 8-element chunks per thread: K <= 3072
 constexpr int kMaxChunks = 12;   // 256-column chunks of a product: K <= 3072
 
-// One workgroup per activation row m < Mp (gridDim.x == Mp, M rounded up to
-// 16); a thread owns 8-element chunks j = t, t + 128, ... and the four chunks
-// of a lane quad make one 32-block. Rows M..Mp-1 are written as zeros.
-// RMSNorm first when norm_w != nullptr: y = w * (x * inv), inv =
-// 1/sqrt(mean(x^2) + eps) with the sum of squares in double. xn_out, when
-// non-null, receives the (normed) row M - 1.
-__global__ __launch_bounds__(kQuantThreads) void k_quant_act(const float *x, int ldx, int M,
-                                                              int K, const float *norm_w,
-                                                              float eps, int8_t *xq, float *dx,
-                                                              float *xn_out) {
+__device__ __forceinline__ float *scales_of(int8_t *xq, int M, int K) {
+  return reinterpret_cast<float *>(xq + (size_t)((M + 15) & ~15) * K);
+}
+
+// The quantizer. One workgroup per activation row m < Mp and slice of its
+// 8-element chunks (gridDim.x == Mp, M rounded up to 16; gridDim.y slices): a
+// thread owns chunks j = blockIdx.y * 128 + t + i * 128 * gridDim.y, and the
+// four chunks of a lane quad make one 32-block. Rows M..Mp-1 are written as
+// zeros. The row is
+//  SRC_X:      x[m][0..K) (row stride ld);
+//  SRC_ADD:    x[m] + sum_c part[c][m] (c < ld <= kMaxChunks chunk partials
+//              of a product with N = K, added in chunk order), written back
+//              to x (the residual stream, row stride K);
+//  SRC_SWIGLU: silu(sum_c part[c][m][2k]) * sum_c part[c][m][2k + 1] (gate /
+//              up interleaved, N = 2K).
+// Then RMSNorm when norm_w != nullptr (one slice only): y = w * (x * inv),
+// inv = 1/sqrt(mean(x^2) + eps) with the sum of squares in double; xn_out,
+// when non-null, receives the (normed) row M - 1; and the Q8_0 blocks
+// (skipped when xq == nullptr). Partial loads are all issued before the sums.
+enum { SRC_X = 0, SRC_ADD = 1, SRC_SWIGLU = 2 };
+
+template <int SRC>
+__global__ __launch_bounds__(kQuantThreads) void k_quant_act(float *x, const float *part,
+                                                              int8_t *xq, const float *norm_w,
+                                                              float *xn_out, int M, int K,
+                                                              int ld, float eps) {
   const int m = blockIdx.x, t = threadIdx.x;
   const int mt16 = gridDim.x >> 4, nch = K >> 3, nb = K >> 5;
+  const int j0 = blockIdx.y * kQuantThreads + t, js = kQuantThreads * gridDim.y;
   long *xq8 = reinterpret_cast<long *>(xq);
+  float *dx = xq ? scales_of(xq, M, K) : nullptr;
   const size_t slot = (size_t)(m >> 4) * 64 + (m & 15);  // + (b * mt16 * 64 + g * 16)
   if (m >= M) {
-    for (int j = t; j < nch; j += kQuantThreads) {
-      const int b = j >> 2, g = j & 3;
-      xq8[(size_t)b * mt16 * 64 + slot + g * 16] = 0;
-      if (g == 0) dx[(size_t)m * nb + b] = 0.f;
-    }
+    if (xq)
+      for (int j = j0; j < nch; j += js) {
+        const int b = j >> 2, g = j & 3;
+        xq8[(size_t)b * mt16 * 64 + slot + g * 16] = 0;
+        if (g == 0) dx[(size_t)m * nb + b] = 0.f;
+      }
     return;
   }
-  const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)m * ldx);
   float v[kQuantChunks][8];
 #pragma unroll
   for (int i = 0; i < kQuantChunks; i++) {
-    const int j = t + i * kQuantThreads;
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
-    if (j < nch) {
-      a = xr[2 * j];
-      b = xr[2 * j + 1];
+    const int j = j0 + i * js;
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[i][e] = 0.f;
+    if (j >= nch) continue;
+    if (SRC == SRC_X) {
+      const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)m * ld);
+      const float4 a = xr[2 * j], b = xr[2 * j + 1];
+      v[i][0] = a.x, v[i][1] = a.y, v[i][2] = a.z, v[i][3] = a.w;
+      v[i][4] = b.x, v[i][5] = b.y, v[i][6] = b.z, v[i][7] = b.w;
+    } else if (SRC == SRC_ADD) {
+      float4 pa[kMaxChunks], pb[kMaxChunks];
+#pragma unroll
+      for (int c = 0; c < kMaxChunks; c++) {
+        if (c < ld) {
+          const float4 *pr = reinterpret_cast<const float4 *>(part + ((size_t)c * M + m) * K);
+          pa[c] = pr[2 * j];
+          pb[c] = pr[2 * j + 1];
+        }
+      }
+      float4 *xr = reinterpret_cast<float4 *>(x + (size_t)m * K);
+      const float4 a = xr[2 * j], b = xr[2 * j + 1];
+      float s[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) s[e] = 0.f;
+#pragma unroll
+      for (int c = 0; c < kMaxChunks; c++) {
+        if (c < ld) {
+          const float p8[8] = {pa[c].x, pa[c].y, pa[c].z, pa[c].w,
+                               pb[c].x, pb[c].y, pb[c].z, pb[c].w};
+#pragma unroll
+          for (int e = 0; e < 8; e++) s[e] = __fadd_rn(s[e], p8[e]);
+        }
+      }
+      const float h8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[i][e] = __fadd_rn(h8[e], s[e]);
+      xr[2 * j] = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
+      xr[2 * j + 1] = make_float4(v[i][4], v[i][5], v[i][6], v[i][7]);
+    } else {
+      constexpr int MC = 4;  // gate/up partials loaded per round
+      float gs[8], us[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) gs[e] = us[e] = 0.f;
+      for (int c0 = 0; c0 < ld; c0 += MC) {
+        float4 pr[MC][4];
+#pragma unroll
+        for (int c = 0; c < MC; c++)
+          if (c0 + c < ld) {
+            const float4 *pp =
+                reinterpret_cast<const float4 *>(part + ((size_t)(c0 + c) * M + m) * (2 * K)) +
+                4 * j;
+#pragma unroll
+            for (int q = 0; q < 4; q++) pr[c][q] = pp[q];
+          }
+#pragma unroll
+        for (int c = 0; c < MC; c++)
+          if (c0 + c < ld) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {  // gate, up of outputs 8j + 2q, 8j + 2q + 1
+              gs[2 * q] = __fadd_rn(gs[2 * q], pr[c][q].x);
+              us[2 * q] = __fadd_rn(us[2 * q], pr[c][q].y);
+              gs[2 * q + 1] = __fadd_rn(gs[2 * q + 1], pr[c][q].z);
+              us[2 * q + 1] = __fadd_rn(us[2 * q + 1], pr[c][q].w);
+            }
+          }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[i][e] = silu_mul_ieee(gs[e], us[e]);
     }
-    v[i][0] = a.x, v[i][1] = a.y, v[i][2] = a.z, v[i][3] = a.w;
-    v[i][4] = b.x, v[i][5] = b.y, v[i][6] = b.z, v[i][7] = b.w;
   }
   if (norm_w) {
     double ss = 0.0;
@@ -72,15 +159,15 @@ __global__ __launch_bounds__(kQuantThreads) void k_quant_act(const float *x, int
 #pragma unroll
       for (int e = 0; e < 8; e++) ss += (double)v[i][e] * (double)v[i][e];
     ss = wave_sum_dpp_d(ss);
-    __shared__ double part[kQuantThreads / 64];
-    if ((t & 63) == 0) part[t >> 6] = ss;
+    __shared__ double red[kQuantThreads / 64];
+    if ((t & 63) == 0) red[t >> 6] = ss;
     __syncthreads();
-    ss = part[0] + part[1];
+    ss = red[0] + red[1];
     const float inv = (float)(1.0 / sqrt(ss / K + (double)eps));
     const float4 *wr = reinterpret_cast<const float4 *>(norm_w);
 #pragma unroll
     for (int i = 0; i < kQuantChunks; i++) {
-      const int j = t + i * kQuantThreads;
+      const int j = j0 + i * js;
       if (j < nch) {
         const float4 a = wr[2 * j], b = wr[2 * j + 1];
         const float w8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
@@ -93,20 +180,22 @@ __global__ __launch_bounds__(kQuantThreads) void k_quant_act(const float *x, int
     float4 *xo = reinterpret_cast<float4 *>(xn_out);
 #pragma unroll
     for (int i = 0; i < kQuantChunks; i++) {
-      const int j = t + i * kQuantThreads;
+      const int j = j0 + i * js;
       if (j < nch) {
         xo[2 * j] = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
         xo[2 * j + 1] = make_float4(v[i][4], v[i][5], v[i][6], v[i][7]);
       }
     }
   }
+  if (!xq) return;
 #pragma unroll
   for (int i = 0; i < kQuantChunks; i++) {
-    const int j = t + i * kQuantThreads;
+    const int j = j0 + i * js;
     float amax = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[i][e]));
-    // nch is a multiple of 4, so a quad is wholly inside or outside the row
+    // nch and the slice starts are multiples of 4, so a quad is wholly inside
+    // or outside the row
     amax = fmaxf(amax, __shfl_xor(amax, 1));
     amax = fmaxf(amax, __shfl_xor(amax, 2));
     if (j >= nch) continue;
@@ -124,95 +213,104 @@ __global__ __launch_bounds__(kQuantThreads) void k_quant_act(const float *x, int
   }
 }
 
+// The chains of one 256-column chunk (blocks b0 .. b0 + 7) for 16 weight rows
+// from n0 and the activation tiles mt0 .. mt0 + TM - 1: acc[t][r] = output
+// (n0 + 4 (lane / 16) + r, 16 (mt0 + t) + lane % 16). Every load of the chunk
+// is issued before the first MFMA.
+template <int TM>
+__device__ __forceinline__ void chunk_chains(const int8_t *wq, const int8_t *xq, const float *dx,
+                                             int N, int K, int n0, int mt0, int mt16, int b0,
+                                             float (&acc)[TM][4]) {
+  const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  const int nb = K >> 5;
+  const _Float16 *wd = reinterpret_cast<const _Float16 *>(wq + (size_t)N * K);
+  const long *xq8 = reinterpret_cast<const long *>(xq);
+  const bool full = (nb & 7) == 0;
+  long av[8], bv[TM][8];
+  float dwv[4][8], dxv[TM][8];
+  const int8_t *wr = wq + (size_t)(n0 + c) * K + 8 * g;
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+    av[i] = b0 + i < nb ? *reinterpret_cast<const long *>(wr + 32 * (b0 + i)) : 0;
+#pragma unroll
+  for (int t = 0; t < TM; t++) {
+    const bool on = mt0 + t < mt16;
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      bv[t][i] = on && b0 + i < nb ? xq8[((size_t)(b0 + i) * mt16 + mt0 + t) * 64 + lane] : 0;
+  }
+  if (full) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const uint4 u = *reinterpret_cast<const uint4 *>(wd + (size_t)(n0 + 4 * g + r) * nb + b0);
+      const unsigned uw[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        dwv[r][2 * i] = (float)__builtin_bit_cast(_Float16, (unsigned short)(uw[i] & 0xffff));
+        dwv[r][2 * i + 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(uw[i] >> 16));
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+      float4 p = make_float4(0.f, 0.f, 0.f, 0.f), q = p;
+      if (mt0 + t < mt16) {
+        const float4 *dp =
+            reinterpret_cast<const float4 *>(dx + (size_t)((mt0 + t) * 16 + c) * nb + b0);
+        p = dp[0];
+        q = dp[1];
+      }
+      dxv[t][0] = p.x, dxv[t][1] = p.y, dxv[t][2] = p.z, dxv[t][3] = p.w;
+      dxv[t][4] = q.x, dxv[t][5] = q.y, dxv[t][6] = q.z, dxv[t][7] = q.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const bool on = b0 + i < nb;
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        dwv[r][i] = on ? (float)wd[(size_t)(n0 + 4 * g + r) * nb + b0 + i] : 0.f;
+#pragma unroll
+      for (int t = 0; t < TM; t++)
+        dxv[t][i] = on && mt0 + t < mt16 ? dx[(size_t)((mt0 + t) * 16 + c) * nb + b0 + i] : 0.f;
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int t = 0; t < TM; t++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) acc[t][r] = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+      const v4i ci =
+          __builtin_amdgcn_mfma_i32_16x16x32_i8(av[i], bv[t][i], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        acc[t][r] = fmaf((float)ci[r], __fmul_rn(dwv[r][i], dxv[t][i]), acc[t][r]);
+    }
+  }
+}
+
 // y[m][n] (+)= sum_b d_w[n][b] d_x[m][b] sum_{k in b} q_w[n][k] q_x[m][k].
 // A workgroup owns 16 weight rows (blockIdx.x) and TM 16-column activation
-// tiles (blockIdx.y); its KW waves take the chunks of 8 blocks (256 k) in
-// turn, each chunk's chain lands in its own LDS slot, and the slots are
-// added in chunk order. Each wave issues every load of a chunk before its
-// first MFMA. EPI_SWIGLU: rows 2j / 2j + 1 are gate / up of output j.
+// tiles (blockIdx.y); its KW waves take the chunks in turn, each chunk's
+// chains land in their own LDS slot, and the slots are added in chunk order.
+// EPI_SWIGLU: rows 2j / 2j + 1 are gate / up of output j.
 template <int TM, int KW, int EPI>
 __global__ __launch_bounds__(KW * 64) void k_gemm_i8(const int8_t *wq, const int8_t *xq,
-                                                      const float *dx, float *y, int N, int K,
-                                                      int M, int ldy) {
+                                                      float *y, int N, int K, int M, int ldy) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int g = lane >> 4, c = lane & 15;
   const int nb = K >> 5, nch = (nb + 7) >> 3;
   const int mt16 = (M + 15) >> 4;
   const int n0 = blockIdx.x * 16, mt0 = blockIdx.y * TM;
-  const _Float16 *wd = reinterpret_cast<const _Float16 *>(wq + (size_t)N * K);
-  const long *xq8 = reinterpret_cast<const long *>(xq);
-  const bool full = (nb & 7) == 0;
+  const float *dx = scales_of(const_cast<int8_t *>(xq), M, K);
   constexpr int LD = TM * 16 + 4;
   __shared__ float red[kMaxChunks][16][LD];
-
   for (int ch = w; ch < nch; ch += KW) {
     float acc[TM][4];
-#pragma unroll
-    for (int t = 0; t < TM; t++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) acc[t][r] = 0.f;
-    const int b0 = ch * 8;
-    long av[8], bv[TM][8];
-    float dwv[4][8], dxv[TM][8];
-    const int8_t *wr = wq + (size_t)(n0 + c) * K + 8 * g;
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-      av[i] = b0 + i < nb ? *reinterpret_cast<const long *>(wr + 32 * (b0 + i)) : 0;
-#pragma unroll
-    for (int t = 0; t < TM; t++) {
-      const bool on = mt0 + t < mt16;
-#pragma unroll
-      for (int i = 0; i < 8; i++)
-        bv[t][i] = on && b0 + i < nb ? xq8[((size_t)(b0 + i) * mt16 + mt0 + t) * 64 + lane] : 0;
-    }
-    if (full) {
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const uint4 u = *reinterpret_cast<const uint4 *>(wd + (size_t)(n0 + 4 * g + r) * nb + b0);
-        const unsigned uw[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          dwv[r][2 * i] = (float)__builtin_bit_cast(_Float16, (unsigned short)(uw[i] & 0xffff));
-          dwv[r][2 * i + 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(uw[i] >> 16));
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < TM; t++) {
-        float4 p = make_float4(0.f, 0.f, 0.f, 0.f), q = p;
-        if (mt0 + t < mt16) {
-          const float4 *dp =
-              reinterpret_cast<const float4 *>(dx + (size_t)((mt0 + t) * 16 + c) * nb + b0);
-          p = dp[0];
-          q = dp[1];
-        }
-        dxv[t][0] = p.x, dxv[t][1] = p.y, dxv[t][2] = p.z, dxv[t][3] = p.w;
-        dxv[t][4] = q.x, dxv[t][5] = q.y, dxv[t][6] = q.z, dxv[t][7] = q.w;
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const bool on = b0 + i < nb;
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-          dwv[r][i] = on ? (float)wd[(size_t)(n0 + 4 * g + r) * nb + b0 + i] : 0.f;
-#pragma unroll
-        for (int t = 0; t < TM; t++)
-          dxv[t][i] =
-              on && mt0 + t < mt16 ? dx[(size_t)((mt0 + t) * 16 + c) * nb + b0 + i] : 0.f;
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-#pragma unroll
-      for (int t = 0; t < TM; t++) {
-        const v4i ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[i], bv[t][i], v4i{0, 0, 0, 0},
-                                                             0, 0, 0);
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-          acc[t][r] = fmaf((float)ci[r], __fmul_rn(dwv[r][i], dxv[t][i]), acc[t][r]);
-      }
-    }
+    chunk_chains<TM>(wq, xq, dx, N, K, n0, mt0, mt16, ch * 8, acc);
 #pragma unroll
     for (int t = 0; t < TM; t++)
 #pragma unroll
@@ -245,14 +343,34 @@ __global__ __launch_bounds__(KW * 64) void k_gemm_i8(const int8_t *wq, const int
   }
 }
 
+// One wave per (16 weight rows, chunk), every activation row (M <= 16 TM):
+// part[chunk][m][n] = the chunk's chains.
+template <int TM>
+__global__ __launch_bounds__(64) void k_gemm_i8p(const int8_t *wq, const int8_t *xq,
+                                                  float *part, int N, int K, int M) {
+  const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  const int n0 = blockIdx.x * 16, ch = blockIdx.y;
+  const int mt16 = (M + 15) >> 4;
+  const float *dx = scales_of(const_cast<int8_t *>(xq), M, K);
+  float acc[TM][4];
+  chunk_chains<TM>(wq, xq, dx, N, K, n0, 0, mt16, ch * 8, acc);
+#pragma unroll
+  for (int t = 0; t < TM; t++) {
+    const int m = t * 16 + c;
+    if (m < M)
+      *reinterpret_cast<float4 *>(part + ((size_t)ch * M + m) * N + n0 + 4 * g) =
+          make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+  }
+}
+
 template <int TM, int KW>
 void gemm_launch(const Mat &W, const QAct &xa, int M, int epi, float *y, int ldy,
                  hipStream_t st) {
   const int mt16 = (M + 15) >> 4;
   const dim3 grid(W.N / 16, (mt16 + TM - 1) / TM), block(KW * 64);
-#define Q3H_GEMM(E)                                                                        \
-  hipLaunchKernelGGL((k_gemm_i8<TM, KW, E>), grid, block, 0, st, W.q, xa.q, xa.d, y, W.N, \
-                     W.K, M, ldy)
+#define Q3H_GEMM(E)                                                                           \
+  hipLaunchKernelGGL((k_gemm_i8<TM, KW, E>), grid, block, 0, st, W.q, xa.q, y, W.N, W.K, M, \
+                     ldy)
   if (epi == EPI_STORE)
     Q3H_GEMM(EPI_STORE);
   else if (epi == EPI_ADD)
@@ -273,17 +391,42 @@ void gemm_by_k(const Mat &W, const QAct &xa, int M, int epi, float *y, int ldy, 
     gemm_launch<TM, 4>(W, xa, M, epi, y, ldy, st);
 }
 
+// slices > 1 only without a norm (each slice a whole number of 32-blocks)
+template <int SRC>
+void quant_launch(float *x, const float *part, int ld, int M, int K, const float *norm_w,
+                  float eps, const QAct &out, float *xn_out, hipStream_t st, int slices = 1) {
+  const int Mp = (M + 15) & ~15;
+  hipLaunchKernelGGL(k_quant_act<SRC>, dim3(Mp, slices), dim3(kQuantThreads), 0, st, x, part,
+                     out.q, norm_w, xn_out, M, K, ld, eps);
+}
+
 }  // namespace
 
 bool gemm_i8_supported(int N, int K) {
   return N > 0 && N % 16 == 0 && K > 0 && K % 32 == 0 && K <= kQuantThreads * kQuantChunks * 8;
 }
 
+int gemm_i8_chunks(int K) { return (K / 32 + 7) / 8; }
+
+size_t qact_bytes(int M, int K) {
+  const size_t Mp = (M + 15) & ~15;
+  return Mp * K + sizeof(float) * Mp * (K / 32);
+}
+
 void launch_quantize_act(const float *x, int ldx, int M, int K, const float *norm_w, float eps,
                          QAct out, float *xn_out, hipStream_t st) {
-  const int Mp = (M + 15) & ~15;
-  hipLaunchKernelGGL(k_quant_act, dim3(Mp), dim3(kQuantThreads), 0, st, x, ldx, M, K, norm_w,
-                     eps, out.q, out.d, xn_out);
+  quant_launch<SRC_X>(const_cast<float *>(x), nullptr, ldx, M, K, norm_w, eps, out, xn_out, st);
+}
+
+void launch_residual_quantize(float *h, const float *part, int chunks, int M, int K,
+                              const float *norm_w, float eps, const QAct *out, hipStream_t st) {
+  quant_launch<SRC_ADD>(h, part, chunks, M, K, norm_w, eps, out ? *out : QAct{}, nullptr, st);
+}
+
+void launch_swiglu_quantize(const float *part, int chunks, int M, int K, QAct out,
+                            hipStream_t st) {
+  const int slices = (K / 8 + kQuantThreads - 1) / kQuantThreads;
+  quant_launch<SRC_SWIGLU>(nullptr, part, chunks, M, K, nullptr, 0.f, out, nullptr, st, slices);
 }
 
 void launch_gemm_i8(const Mat &W, const QAct &xa, int M, int epi, float *y, int ldy,
@@ -294,6 +437,16 @@ void launch_gemm_i8(const Mat &W, const QAct &xa, int M, int epi, float *y, int 
     gemm_by_k<2>(W, xa, M, epi, y, ldy, st);
   else
     gemm_by_k<4>(W, xa, M, epi, y, ldy, st);
+}
+
+void launch_gemm_i8_partial(const Mat &W, const QAct &xa, int M, float *part, hipStream_t st) {
+  const dim3 grid(W.N / 16, gemm_i8_chunks(W.K));
+  if (M <= 16)
+    hipLaunchKernelGGL(k_gemm_i8p<1>, grid, dim3(64), 0, st, W.q, xa.q, part, W.N, W.K, M);
+  else if (M <= 32)
+    hipLaunchKernelGGL(k_gemm_i8p<2>, grid, dim3(64), 0, st, W.q, xa.q, part, W.N, W.K, M);
+  else
+    hipLaunchKernelGGL(k_gemm_i8p<4>, grid, dim3(64), 0, st, W.q, xa.q, part, W.N, W.K, M);
 }
 
 }  // namespace q3h

@@ -53,15 +53,15 @@ struct GemvArgs {
   float *xn_out;  // optional: the (normed) last x row, [K], written by block 0
 };
 
-// Activations quantized per 32-block for the int8 products, over M rows
-// padded to Mp = M rounded up to 16: q holds the 16-row tiles in MFMA operand
+// Activations quantized per 32-block for the int8 products, M rows padded to
+// Mp = M rounded up to 16, one buffer: the int8 values at q, in MFMA operand
 // order (tile (b, m / 16) is 64 lanes x 8 bytes, lane g * 16 + m % 16 holding
-// k = 32b + 8g .. 32b + 8g + 7 of row m), d the fp16-rounded block scales
-// [Mp][K/32] as f32.
+// k = 32b + 8g .. 32b + 8g + 7 of row m), then the fp16-rounded block scales
+// [Mp][K/32] as f32 at q + Mp * K (qact_bytes(M, K) in all).
 struct QAct {
   int8_t *q = nullptr;
-  float *d = nullptr;
 };
+size_t qact_bytes(int M, int K);
 
 void launch_gemv(const GemvArgs &a, int epi, bool q8, hipStream_t st);
 // the wide Q8_0 kernel (K in {1024, 2048, 3072}, N % 256 == 0, M <= 4);
@@ -78,6 +78,19 @@ void launch_quantize_act(const float *x, int ldx, int M, int K, const float *nor
 // y [M][ldy] (+)= W . x over the quantized rows xa (Q8_0 W)
 void launch_gemm_i8(const Mat &W, const QAct &xa, int M, int epi, float *y, int ldy,
                     hipStream_t st);
+// the same chains for M <= kPartialRows, one wave per (16 rows, chunk):
+// part[gemm_i8_chunks(K)][M][N], to be added in chunk order by the consumer
+constexpr int kPartialRows = 64;
+int gemm_i8_chunks(int K);
+void launch_gemm_i8_partial(const Mat &W, const QAct &xa, int M, float *part, hipStream_t st);
+// h [M][K] += the chunk partials of a product (in chunk order); then RMSNorm
+// with norm_w (when non-null) and quantization into *out (when non-null)
+void launch_residual_quantize(float *h, const float *part, int chunks, int M, int K,
+                              const float *norm_w, float eps, const QAct *out, hipStream_t st);
+// silu(gate) * up from the chunk partials of the gate/up product (N = 2K),
+// quantized into out
+void launch_swiglu_quantize(const float *part, int chunks, int M, int K, QAct out,
+                            hipStream_t st);
 
 // rows of n contexts, R consecutive rows each (R > 1: one context's prefill)
 void launch_prep(CtxDev *const *cs, const int *alive, int n, int R, RowDesc *rd,
@@ -112,11 +125,14 @@ void launch_attn(const AttnArgs &a, int M, int splits, bool fused, bool kv16, hi
 // attention of the int8 path (q3h_attnx.hip): the rows of a (fused: each the
 // one new position of its own context, QK-norm / RoPE / K/V append in the
 // prologue), outputs quantized into xa for the o_proj product; positions up
-// to kAttnXMaxPositions (scores held in LDS)
+// to kAttnXMaxPositions / (heads / kv_heads) (the scores of a kv group held
+// in LDS). qkv_chunks > 0 (fused only):
+// a.qkv holds the chunk partials [qkv_chunks][M][a.ldq] of the q/k/v product
+// instead of its rows, added in chunk order in the prologue.
 constexpr int kAttnXMaxPositions = 8192;
 bool attn_x_supported(int heads, int kvh, int head_dim, int max_positions);
-void launch_attn_x(const AttnArgs &a, int M, bool fused, bool kv16, const QAct &xa,
-                   int max_positions, hipStream_t st);
+void launch_attn_x(const AttnArgs &a, int M, bool fused, bool kv16, int qkv_chunks,
+                   const QAct &xa, int max_positions, hipStream_t st);
 
 // the code predictor's fused attention + o_proj + residual (q3h_cp.hip):
 // one context of 16 positions, the new row at pos; k_layer: the layer's keys,
