@@ -164,7 +164,7 @@ void run_layers(const q3h_stack *s, Work &w, int M, int splits, bool fused, hipS
   const int H = c.hidden, hd = c.head_dim, NQ = c.heads * hd, NKV = c.kv_heads * hd;
   const int I = c.intermediate, ldq = NQ + 2 * NKV;
   const bool kv16 = c.kv_f16 != 0;
-  if (c.act_q8 && M <= kPartialRows) {
+  if (c.act_q8 && M <= kPartialRows && gemm_i8_chunks(c.hidden) <= 4) {
     run_layers_partial(s, w, M, fused, st);
     return;
   }

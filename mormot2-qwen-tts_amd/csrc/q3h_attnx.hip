@@ -86,8 +86,10 @@ __device__ __forceinline__ float row16_tree(float v) {
 }
 
 // grid (kv heads, M): the GRP query heads of kv head g = blockIdx.x share one
-// read of its K/V. NCH > 0: the q/k/v come as NCH chunk partials.
-template <typename KV, bool FUSED, int GRP>
+// read of its K/V; nch > 0: the q/k/v come as nch chunk partials. SU / VU:
+// the key rounds of the score loop / the positions of the value chains whose
+// loads are issued together (deeper for long contexts).
+template <typename KV, bool FUSED, int GRP, int SU, int VU>
 __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *qkv,
                                                const float *qkn, const float2 *rope_cs,
                                                int8_t *xq, int ldq, int layer, int nch) {
@@ -101,12 +103,8 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
   const int lane = t & 63, wave = t >> 6;
   const int NQ = heads * HD, nbq = NQ >> 5, mt16 = (M + 15) >> 4;
   float *dx = reinterpret_cast<float *>(xq + (size_t)mt16 * 16 * NQ);
-  // output k of query head h, row m: byte ((b * mt16 + m / 16) * 64 + (k % 32) / 8
-  // * 16 + m % 16) * 8 + k % 8 of the operand tiles, b = 4 h + k / 32
-  auto qoff = [&](int h, int k) {
-    return (((size_t)(4 * h + (k >> 5)) * mt16 + (m >> 4)) * 64 + ((k & 31) >> 3) * 16 +
-            (m & 15)) * 8 + (k & 7);
-  };
+  // output k of query head h, row m: element (m, h * 128 + k) of the operand tiles
+  auto qoff = [&](int h, int k) { return qtile_offset(m, h * HD + k, mt16); };
   const RowDesc d = rd[m];
   if (d.pos < 0) {  // inactive row: zero blocks
     for (int i = t; i < GRP * HD; i += NT) {
@@ -161,24 +159,27 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
   // of SU positions are issued together
   const float scale = (float)(1.0 / __builtin_sqrt((double)HD));
   {
-    constexpr int KG = NT / 16, SU = 4;
+    constexpr int KG = NT / 16;
     const int kg = t >> 4, li = t & 15;
-    float qv[GRP][8];
+    float qv[GRP][8], kn8[8];
 #pragma unroll
     for (int j = 0; j < GRP; j++)
 #pragma unroll
       for (int e = 0; e < 8; e++) qv[j][e] = qs[j][8 * li + e];
+#pragma unroll
+    for (int e = 0; e < 8; e++) kn8[e] = FUSED ? kn[8 * li + e] : 0.f;
     for (int p0 = 0; p0 < L; p0 += KG * SU) {
+      // unconditional loads from clamped positions (a guarded load would be
+      // waited for on its own), then the new position's own k, zeros past L
       float k8[SU][8];
+#pragma unroll
+      for (int u = 0; u < SU; u++) load8(kc + (size_t)min(p0 + u * KG + kg, L - 1) * HD + 8 * li, k8[u]);
 #pragma unroll
       for (int u = 0; u < SU; u++) {
         const int p = p0 + u * KG + kg;
-        if (p < L && !(FUSED && p == pos)) {
-          load8(kc + (size_t)p * HD + 8 * li, k8[u]);
-        } else {
 #pragma unroll
-          for (int e = 0; e < 8; e++) k8[u][e] = FUSED && p == pos ? kn[8 * li + e] : 0.f;
-        }
+        for (int e = 0; e < 8; e++)
+          k8[u][e] = p >= L ? 0.f : FUSED && p == pos ? kn8[e] : k8[u][e];
       }
 #pragma unroll
       for (int u = 0; u < SU; u++) {
@@ -246,25 +247,35 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
   // values: chain ch = wave % 4 over positions p = ch mod 4, dim (wave / 4) 64
   // + lane, every head of the group; the loads of VU positions issued together
   {
-    constexpr int VU = 8;
     const int ch = wave & 3, dim = (wave >> 2) * 64 + lane;
     float c[GRP];
 #pragma unroll
     for (int j = 0; j < GRP; j++) c[j] = 0.f;
+    const float vnd = FUSED ? vn[dim] : 0.f;
     for (int p0 = ch; p0 < L; p0 += 4 * VU) {
       float v[VU];
 #pragma unroll
-      for (int u = 0; u < VU; u++) {
-        const int p = p0 + 4 * u;
-        v[u] = p < L ? (FUSED && p == pos ? vn[dim] : (float)vc[(size_t)p * HD + dim]) : 0.f;
+      for (int u = 0; u < VU; u++) v[u] = (float)vc[(size_t)min(p0 + 4 * u, L - 1) * HD + dim];
+      if (FUSED) {
+#pragma unroll
+        for (int u = 0; u < VU; u++) v[u] = p0 + 4 * u == pos ? vnd : v[u];  // its own v
       }
+      // weights of the round read together; past L a zero weight adds an exact
+      // zero to the chain (finite v from the clamped position)
+      float wgt[VU][GRP];
 #pragma unroll
       for (int u = 0; u < VU; u++) {
-        const int p = p0 + 4 * u;
-        if (p < L)
+        const int p = p0 + 4 * u;  // the same for the whole wave
 #pragma unroll
-          for (int j = 0; j < GRP; j++) c[j] = fmaf(__fmul_rn(sc[j * L + p], inv[j]), v[u], c[j]);
+        for (int j = 0; j < GRP; j++) {
+          const float e = sc[j * L + min(p, L - 1)];
+          wgt[u][j] = p < L ? __fmul_rn(e, inv[j]) : 0.f;
+        }
       }
+#pragma unroll
+      for (int u = 0; u < VU; u++)
+#pragma unroll
+        for (int j = 0; j < GRP; j++) c[j] = fmaf(wgt[u][j], v[u], c[j]);
     }
 #pragma unroll
     for (int j = 0; j < GRP; j++) cv[ch][j][dim] = c[j];
@@ -294,15 +305,15 @@ bool attn_x_supported(int heads, int kvh, int head_dim, int max_positions) {
          (size_t)max_positions * (heads / kvh) <= (size_t)kAttnXMaxPositions;
 }
 
-template <typename KV, bool F>
+template <typename KV, bool F, int SU, int VU>
 void attn_x_grp(const AttnArgs &a, int M, int nch, const QAct &xa, int max_positions,
                 hipStream_t st) {
   const dim3 grid(a.kvh, M);
   const int grp = a.heads / a.kvh;
   const size_t lds = sizeof(float) * (size_t)grp * max_positions;
 #define Q3H_ATTNX(G)                                                                           \
-  hipLaunchKernelGGL((k_attn_x<KV, F, G>), grid, dim3(NT), lds, st, a.rd, a.qkv, a.qkn,       \
-                     a.rope_cs, xa.q, a.ldq, a.layer, nch)
+  hipLaunchKernelGGL((k_attn_x<KV, F, G, SU, VU>), grid, dim3(NT), lds, st, a.rd, a.qkv,      \
+                     a.qkn, a.rope_cs, xa.q, a.ldq, a.layer, nch)
   if (grp == 1)
     Q3H_ATTNX(1);
   else if (grp == 2)
@@ -312,19 +323,29 @@ void attn_x_grp(const AttnArgs &a, int M, int nch, const QAct &xa, int max_posit
 #undef Q3H_ATTNX
 }
 
+// short contexts (the code predictor's 16 positions): one round of each loop
+template <typename KV, bool F>
+void attn_x_len(const AttnArgs &a, int M, int nch, const QAct &xa, int max_positions,
+                hipStream_t st) {
+  if (max_positions <= NT / 16)
+    attn_x_grp<KV, F, 1, 4>(a, M, nch, xa, max_positions, st);
+  else
+    attn_x_grp<KV, F, 8, 32>(a, M, nch, xa, max_positions, st);
+}
+
 void launch_attn_x(const AttnArgs &a, int M, bool fused, bool kv16, int qkv_chunks,
                    const QAct &xa, int max_positions, hipStream_t st) {
   const int nch = fused ? qkv_chunks : 0;
   if (kv16) {
     if (fused)
-      attn_x_grp<_Float16, true>(a, M, nch, xa, max_positions, st);
+      attn_x_len<_Float16, true>(a, M, nch, xa, max_positions, st);
     else
-      attn_x_grp<_Float16, false>(a, M, nch, xa, max_positions, st);
+      attn_x_len<_Float16, false>(a, M, nch, xa, max_positions, st);
   } else {
     if (fused)
-      attn_x_grp<float, true>(a, M, nch, xa, max_positions, st);
+      attn_x_len<float, true>(a, M, nch, xa, max_positions, st);
     else
-      attn_x_grp<float, false>(a, M, nch, xa, max_positions, st);
+      attn_x_len<float, false>(a, M, nch, xa, max_positions, st);
   }
 }
 

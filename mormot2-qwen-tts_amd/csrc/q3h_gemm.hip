@@ -14,9 +14,9 @@
 // Operand layouts (v_mfma_i32_16x16x32_i8, wave64): lane l holds 8 int8 of
 // row l % 16 of A and of column l % 16 of B, k = 8 * (l / 16) .. + 7; the
 // result C[4 * (l / 16) + r][l % 16], r < 4, lands in lane l. A is 16 weight
-// rows read straight from the row-major Q8_0 matrix; B is 16 activation rows,
-// which the quantizers write already in operand order, so each B operand is
-// one coalesced 512-byte load.
+// rows of the row-major Q8_0 matrix; B is 16 activation rows, which the
+// quantizers write already in operand order (qtile_offset), so one coalesced
+// 1 KB load gives the B operands of two blocks.
 //
 // Two schedules of the same chains:
 //  - k_gemm_i8: a workgroup per 16 weight rows, its waves taking the chunks
@@ -51,15 +51,17 @@ __device__ __forceinline__ float *scales_of(int8_t *xq, int M, int K) {
 //  SRC_ADD:    x[m] + sum_c part[c][m] (c < ld <= kMaxChunks chunk partials
 //              of a product with N = K, added in chunk order), written back
 //              to x (the residual stream, row stride K);
-//  SRC_SWIGLU: silu(sum_c part[c][m][2k]) * sum_c part[c][m][2k + 1] (gate /
-//              up interleaved, N = 2K).
+//  SRC_SWIGLU: silu(sum_c part[c][m][2k]) * sum_c part[c][m][2k + 1] (c < ld
+//              <= 4 partials; gate / up interleaved, N = 2K).
 // Then RMSNorm when norm_w != nullptr (one slice only): y = w * (x * inv),
 // inv = 1/sqrt(mean(x^2) + eps) with the sum of squares in double; xn_out,
 // when non-null, receives the (normed) row M - 1; and the Q8_0 blocks
 // (skipped when xq == nullptr). Partial loads are all issued before the sums.
 enum { SRC_X = 0, SRC_ADD = 1, SRC_SWIGLU = 2 };
 
-template <int SRC>
+// KC: chunks per thread (the row's chunks / (128 slices), rounded up); NC: the
+// partial slots read (ld <= NC; SRC_ADD and SRC_SWIGLU)
+template <int SRC, int KC, int NC>
 __global__ __launch_bounds__(kQuantThreads) void k_quant_act(float *x, const float *part,
                                                               int8_t *xq, const float *norm_w,
                                                               float *xn_out, int M, int K,
@@ -67,95 +69,89 @@ __global__ __launch_bounds__(kQuantThreads) void k_quant_act(float *x, const flo
   const int m = blockIdx.x, t = threadIdx.x;
   const int mt16 = gridDim.x >> 4, nch = K >> 3, nb = K >> 5;
   const int j0 = blockIdx.y * kQuantThreads + t, js = kQuantThreads * gridDim.y;
-  long *xq8 = reinterpret_cast<long *>(xq);
   float *dx = xq ? scales_of(xq, M, K) : nullptr;
-  const size_t slot = (size_t)(m >> 4) * 64 + (m & 15);  // + (b * mt16 * 64 + g * 16)
   if (m >= M) {
     if (xq)
       for (int j = j0; j < nch; j += js) {
-        const int b = j >> 2, g = j & 3;
-        xq8[(size_t)b * mt16 * 64 + slot + g * 16] = 0;
-        if (g == 0) dx[(size_t)m * nb + b] = 0.f;
+        *reinterpret_cast<long *>(xq + qtile_offset(m, 8 * j, mt16)) = 0;
+        if ((j & 3) == 0) dx[(size_t)m * nb + (j >> 2)] = 0.f;
       }
     return;
   }
-  float v[kQuantChunks][8];
+  // loads from clamped chunk / partial indices (a guarded load would be waited
+  // for on its own); chunks past the row and partials past ld contribute zeros
+  float v[KC][8];
 #pragma unroll
-  for (int i = 0; i < kQuantChunks; i++) {
-    const int j = j0 + i * js;
-#pragma unroll
-    for (int e = 0; e < 8; e++) v[i][e] = 0.f;
-    if (j >= nch) continue;
+  for (int i = 0; i < KC; i++) {
+    const int j = j0 + i * js, jc = min(j, nch - 1);
+    const bool on = j < nch;
     if (SRC == SRC_X) {
       const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)m * ld);
-      const float4 a = xr[2 * j], b = xr[2 * j + 1];
-      v[i][0] = a.x, v[i][1] = a.y, v[i][2] = a.z, v[i][3] = a.w;
-      v[i][4] = b.x, v[i][5] = b.y, v[i][6] = b.z, v[i][7] = b.w;
-    } else if (SRC == SRC_ADD) {
-      float4 pa[kMaxChunks], pb[kMaxChunks];
+      const float4 a = xr[2 * jc], b = xr[2 * jc + 1];
+      const float x8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-      for (int c = 0; c < kMaxChunks; c++) {
-        if (c < ld) {
-          const float4 *pr = reinterpret_cast<const float4 *>(part + ((size_t)c * M + m) * K);
-          pa[c] = pr[2 * j];
-          pb[c] = pr[2 * j + 1];
-        }
+      for (int e = 0; e < 8; e++) v[i][e] = on ? x8[e] : 0.f;
+    } else if (SRC == SRC_ADD) {
+      float4 pa[NC], pb[NC];
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        const float4 *pr =
+            reinterpret_cast<const float4 *>(part + ((size_t)min(c, ld - 1) * M + m) * K);
+        pa[c] = pr[2 * jc];
+        pb[c] = pr[2 * jc + 1];
       }
       float4 *xr = reinterpret_cast<float4 *>(x + (size_t)m * K);
-      const float4 a = xr[2 * j], b = xr[2 * j + 1];
+      const float4 a = xr[2 * jc], b = xr[2 * jc + 1];
       float s[8];
 #pragma unroll
       for (int e = 0; e < 8; e++) s[e] = 0.f;
 #pragma unroll
-      for (int c = 0; c < kMaxChunks; c++) {
-        if (c < ld) {
-          const float p8[8] = {pa[c].x, pa[c].y, pa[c].z, pa[c].w,
-                               pb[c].x, pb[c].y, pb[c].z, pb[c].w};
+      for (int c = 0; c < NC; c++) {
+        const float p8[8] = {pa[c].x, pa[c].y, pa[c].z, pa[c].w,
+                             pb[c].x, pb[c].y, pb[c].z, pb[c].w};
 #pragma unroll
-          for (int e = 0; e < 8; e++) s[e] = __fadd_rn(s[e], p8[e]);
-        }
+        for (int e = 0; e < 8; e++) s[e] = c < ld ? __fadd_rn(s[e], p8[e]) : s[e];
       }
       const float h8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-      for (int e = 0; e < 8; e++) v[i][e] = __fadd_rn(h8[e], s[e]);
-      xr[2 * j] = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
-      xr[2 * j + 1] = make_float4(v[i][4], v[i][5], v[i][6], v[i][7]);
+      for (int e = 0; e < 8; e++) v[i][e] = on ? __fadd_rn(h8[e], s[e]) : 0.f;
+      if (on) {
+        xr[2 * j] = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
+        xr[2 * j + 1] = make_float4(v[i][4], v[i][5], v[i][6], v[i][7]);
+      }
     } else {
-      constexpr int MC = 4;  // gate/up partials loaded per round
+      constexpr int MC = NC;
+      float4 pr[MC][4];
+#pragma unroll
+      for (int c = 0; c < MC; c++) {
+        const float4 *pp =
+            reinterpret_cast<const float4 *>(part + ((size_t)min(c, ld - 1) * M + m) * (2 * K)) +
+            4 * jc;
+#pragma unroll
+        for (int q = 0; q < 4; q++) pr[c][q] = pp[q];
+      }
       float gs[8], us[8];
 #pragma unroll
       for (int e = 0; e < 8; e++) gs[e] = us[e] = 0.f;
-      for (int c0 = 0; c0 < ld; c0 += MC) {
-        float4 pr[MC][4];
 #pragma unroll
-        for (int c = 0; c < MC; c++)
-          if (c0 + c < ld) {
-            const float4 *pp =
-                reinterpret_cast<const float4 *>(part + ((size_t)(c0 + c) * M + m) * (2 * K)) +
-                4 * j;
+      for (int c = 0; c < MC; c++) {
+        if (c >= ld) break;  // uniform
 #pragma unroll
-            for (int q = 0; q < 4; q++) pr[c][q] = pp[q];
-          }
-#pragma unroll
-        for (int c = 0; c < MC; c++)
-          if (c0 + c < ld) {
-#pragma unroll
-            for (int q = 0; q < 4; q++) {  // gate, up of outputs 8j + 2q, 8j + 2q + 1
-              gs[2 * q] = __fadd_rn(gs[2 * q], pr[c][q].x);
-              us[2 * q] = __fadd_rn(us[2 * q], pr[c][q].y);
-              gs[2 * q + 1] = __fadd_rn(gs[2 * q + 1], pr[c][q].z);
-              us[2 * q + 1] = __fadd_rn(us[2 * q + 1], pr[c][q].w);
-            }
-          }
+        for (int q = 0; q < 4; q++) {  // gate, up of outputs 8j + 2q, 8j + 2q + 1
+          gs[2 * q] = __fadd_rn(gs[2 * q], pr[c][q].x);
+          us[2 * q] = __fadd_rn(us[2 * q], pr[c][q].y);
+          gs[2 * q + 1] = __fadd_rn(gs[2 * q + 1], pr[c][q].z);
+          us[2 * q + 1] = __fadd_rn(us[2 * q + 1], pr[c][q].w);
+        }
       }
 #pragma unroll
-      for (int e = 0; e < 8; e++) v[i][e] = silu_mul_ieee(gs[e], us[e]);
+      for (int e = 0; e < 8; e++) v[i][e] = on ? silu_mul_ieee(gs[e], us[e]) : 0.f;
     }
   }
   if (norm_w) {
     double ss = 0.0;
 #pragma unroll
-    for (int i = 0; i < kQuantChunks; i++)
+    for (int i = 0; i < KC; i++)
 #pragma unroll
       for (int e = 0; e < 8; e++) ss += (double)v[i][e] * (double)v[i][e];
     ss = wave_sum_dpp_d(ss);
@@ -166,7 +162,7 @@ __global__ __launch_bounds__(kQuantThreads) void k_quant_act(float *x, const flo
     const float inv = (float)(1.0 / sqrt(ss / K + (double)eps));
     const float4 *wr = reinterpret_cast<const float4 *>(norm_w);
 #pragma unroll
-    for (int i = 0; i < kQuantChunks; i++) {
+    for (int i = 0; i < KC; i++) {
       const int j = j0 + i * js;
       if (j < nch) {
         const float4 a = wr[2 * j], b = wr[2 * j + 1];
@@ -179,7 +175,7 @@ __global__ __launch_bounds__(kQuantThreads) void k_quant_act(float *x, const flo
   if (xn_out && m == M - 1) {
     float4 *xo = reinterpret_cast<float4 *>(xn_out);
 #pragma unroll
-    for (int i = 0; i < kQuantChunks; i++) {
+    for (int i = 0; i < KC; i++) {
       const int j = j0 + i * js;
       if (j < nch) {
         xo[2 * j] = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
@@ -189,7 +185,7 @@ __global__ __launch_bounds__(kQuantThreads) void k_quant_act(float *x, const flo
   }
   if (!xq) return;
 #pragma unroll
-  for (int i = 0; i < kQuantChunks; i++) {
+  for (int i = 0; i < KC; i++) {
     const int j = j0 + i * js;
     float amax = 0.f;
 #pragma unroll
@@ -207,72 +203,80 @@ __global__ __launch_bounds__(kQuantThreads) void k_quant_act(float *x, const flo
       const int q = (int)roundf(__fmul_rn(v[i][e], id));
       packed |= (unsigned long long)(uint8_t)(int8_t)q << (8 * e);
     }
-    const int b = j >> 2, g = j & 3;
-    xq8[(size_t)b * mt16 * 64 + slot + g * 16] = (long)packed;
-    if (g == 0) dx[(size_t)m * nb + b] = (float)(_Float16)d;
+    *reinterpret_cast<long *>(xq + qtile_offset(m, 8 * j, mt16)) = (long)packed;
+    if ((j & 3) == 0) dx[(size_t)m * nb + (j >> 2)] = (float)(_Float16)d;
   }
 }
 
-// The chains of one 256-column chunk (blocks b0 .. b0 + 7) for 16 weight rows
-// from n0 and the activation tiles mt0 .. mt0 + TM - 1: acc[t][r] = output
-// (n0 + 4 (lane / 16) + r, 16 (mt0 + t) + lane % 16). Every load of the chunk
-// is issued before the first MFMA.
-template <int TM>
+// The chains of one 256-column chunk (blocks b0 .. b0 + 7, K % 256 == 0) for
+// 16 weight rows from n0 and the activation tiles mt0 .. mt0 + TM - 1:
+// acc[t][r] = output (n0 + 4 (lane / 16) + r, 16 (mt0 + t) + lane % 16); a
+// tile past the last (mt16) repeats the last one and its outputs are not
+// stored. All loads are unconditional and issued before the first MFMA (a
+// guarded load would make the compiler wait for each one). LDSA: the weight
+// tile is read with 16-byte loads (4 rows x 256 bytes per instruction instead
+// of 16 rows x 32 bytes) and rearranged through the wave's own 16 x 33 longs
+// of LDS (at).
+template <int TM, bool LDSA>
 __device__ __forceinline__ void chunk_chains(const int8_t *wq, const int8_t *xq, const float *dx,
                                              int N, int K, int n0, int mt0, int mt16, int b0,
-                                             float (&acc)[TM][4]) {
+                                             long (*at)[33], float (&acc)[TM][4]) {
   const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
   const int nb = K >> 5;
   const _Float16 *wd = reinterpret_cast<const _Float16 *>(wq + (size_t)N * K);
-  const long *xq8 = reinterpret_cast<const long *>(xq);
-  const bool full = (nb & 7) == 0;
+  const int4 *xq16 = reinterpret_cast<const int4 *>(xq);
   long av[8], bv[TM][8];
   float dwv[4][8], dxv[TM][8];
-  const int8_t *wr = wq + (size_t)(n0 + c) * K + 8 * g;
+  int4 araw[4];
+  if (LDSA) {
 #pragma unroll
-  for (int i = 0; i < 8; i++)
-    av[i] = b0 + i < nb ? *reinterpret_cast<const long *>(wr + 32 * (b0 + i)) : 0;
+    for (int i = 0; i < 4; i++)  // rows 4i + lane / 16, bytes 16 (lane % 16) of the chunk
+      araw[i] = *reinterpret_cast<const int4 *>(wq + (size_t)(n0 + 4 * i + (lane >> 4)) * K +
+                                                b0 * 32 + 16 * (lane & 15));
+  } else {
+    const int8_t *wr = wq + (size_t)(n0 + c) * K + 8 * g;
+#pragma unroll
+    for (int i = 0; i < 8; i++) av[i] = *reinterpret_cast<const long *>(wr + 32 * (b0 + i));
+  }
 #pragma unroll
   for (int t = 0; t < TM; t++) {
-    const bool on = mt0 + t < mt16;
+    const int tt = min(mt0 + t, mt16 - 1);
 #pragma unroll
-    for (int i = 0; i < 8; i++)
-      bv[t][i] = on && b0 + i < nb ? xq8[((size_t)(b0 + i) * mt16 + mt0 + t) * 64 + lane] : 0;
+    for (int q = 0; q < 4; q++) {  // blocks b0 + 2q, b0 + 2q + 1
+      const int4 v = xq16[((size_t)((b0 >> 1) + q) * mt16 + tt) * 64 + lane];
+      bv[t][2 * q] = ((long)(unsigned)v.y << 32) | (unsigned)v.x;
+      bv[t][2 * q + 1] = ((long)(unsigned)v.w << 32) | (unsigned)v.z;
+    }
   }
-  if (full) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const uint4 u = *reinterpret_cast<const uint4 *>(wd + (size_t)(n0 + 4 * g + r) * nb + b0);
-      const unsigned uw[4] = {u.x, u.y, u.z, u.w};
+  for (int r = 0; r < 4; r++) {
+    const uint4 u = *reinterpret_cast<const uint4 *>(wd + (size_t)(n0 + 4 * g + r) * nb + b0);
+    const unsigned uw[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        dwv[r][2 * i] = (float)__builtin_bit_cast(_Float16, (unsigned short)(uw[i] & 0xffff));
-        dwv[r][2 * i + 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(uw[i] >> 16));
-      }
+    for (int i = 0; i < 4; i++) {
+      dwv[r][2 * i] = (float)__builtin_bit_cast(_Float16, (unsigned short)(uw[i] & 0xffff));
+      dwv[r][2 * i + 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(uw[i] >> 16));
     }
+  }
 #pragma unroll
-    for (int t = 0; t < TM; t++) {
-      float4 p = make_float4(0.f, 0.f, 0.f, 0.f), q = p;
-      if (mt0 + t < mt16) {
-        const float4 *dp =
-            reinterpret_cast<const float4 *>(dx + (size_t)((mt0 + t) * 16 + c) * nb + b0);
-        p = dp[0];
-        q = dp[1];
-      }
-      dxv[t][0] = p.x, dxv[t][1] = p.y, dxv[t][2] = p.z, dxv[t][3] = p.w;
-      dxv[t][4] = q.x, dxv[t][5] = q.y, dxv[t][6] = q.z, dxv[t][7] = q.w;
+  for (int t = 0; t < TM; t++) {
+    const int tt = min(mt0 + t, mt16 - 1);
+    const float4 *dp = reinterpret_cast<const float4 *>(dx + (size_t)(tt * 16 + c) * nb + b0);
+    const float4 p = dp[0], q = dp[1];
+    dxv[t][0] = p.x, dxv[t][1] = p.y, dxv[t][2] = p.z, dxv[t][3] = p.w;
+    dxv[t][4] = q.x, dxv[t][5] = q.y, dxv[t][6] = q.z, dxv[t][7] = q.w;
+  }
+  if (LDSA) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int row = 4 * i + (lane >> 4), l2 = 2 * (lane & 15);
+      at[row][l2] = ((long)(unsigned)araw[i].y << 32) | (unsigned)araw[i].x;
+      at[row][l2 + 1] = ((long)(unsigned)araw[i].w << 32) | (unsigned)araw[i].z;
     }
-  } else {
+    // the wave reads back only what it wrote itself (LDS keeps a wave's order)
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const bool on = b0 + i < nb;
-#pragma unroll
-      for (int r = 0; r < 4; r++)
-        dwv[r][i] = on ? (float)wd[(size_t)(n0 + 4 * g + r) * nb + b0 + i] : 0.f;
-#pragma unroll
-      for (int t = 0; t < TM; t++)
-        dxv[t][i] = on && mt0 + t < mt16 ? dx[(size_t)((mt0 + t) * 16 + c) * nb + b0 + i] : 0.f;
-    }
+    for (int i = 0; i < 8; i++) av[i] = at[c][4 * i + g];  // row c, bytes 32 i + 8 g
   }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -310,7 +314,7 @@ __global__ __launch_bounds__(KW * 64) void k_gemm_i8(const int8_t *wq, const int
   __shared__ float red[kMaxChunks][16][LD];
   for (int ch = w; ch < nch; ch += KW) {
     float acc[TM][4];
-    chunk_chains<TM>(wq, xq, dx, N, K, n0, mt0, mt16, ch * 8, acc);
+    chunk_chains<TM, false>(wq, xq, dx, N, K, n0, mt0, mt16, ch * 8, nullptr, acc);
 #pragma unroll
     for (int t = 0; t < TM; t++)
 #pragma unroll
@@ -352,8 +356,9 @@ __global__ __launch_bounds__(64) void k_gemm_i8p(const int8_t *wq, const int8_t 
   const int n0 = blockIdx.x * 16, ch = blockIdx.y;
   const int mt16 = (M + 15) >> 4;
   const float *dx = scales_of(const_cast<int8_t *>(xq), M, K);
+  __shared__ long at[16][33];
   float acc[TM][4];
-  chunk_chains<TM>(wq, xq, dx, N, K, n0, 0, mt16, ch * 8, acc);
+  chunk_chains<TM, true>(wq, xq, dx, N, K, n0, 0, mt16, ch * 8, at, acc);
 #pragma unroll
   for (int t = 0; t < TM; t++) {
     const int m = t * 16 + c;
@@ -392,21 +397,42 @@ void gemm_by_k(const Mat &W, const QAct &xa, int M, int epi, float *y, int ldy, 
 }
 
 // slices > 1 only without a norm (each slice a whole number of 32-blocks)
+template <int SRC, int NC>
+void quant_launch_nc(float *x, const float *part, int ld, int M, int K, const float *norm_w,
+                     float eps, const QAct &out, float *xn_out, hipStream_t st, int slices) {
+  const int Mp = (M + 15) & ~15;
+  const int kc = (K / 8 + kQuantThreads * slices - 1) / (kQuantThreads * slices);
+  const dim3 grid(Mp, slices);
+#define Q3H_QUANT(KC)                                                                          \
+  hipLaunchKernelGGL((k_quant_act<SRC, KC, NC>), grid, dim3(kQuantThreads), 0, st, x, part,    \
+                     out.q, norm_w, xn_out, M, K, ld, eps)
+  if (kc <= 1)
+    Q3H_QUANT(1);
+  else if (kc == 2)
+    Q3H_QUANT(2);
+  else
+    Q3H_QUANT(3);
+#undef Q3H_QUANT
+}
+
 template <int SRC>
 void quant_launch(float *x, const float *part, int ld, int M, int K, const float *norm_w,
                   float eps, const QAct &out, float *xn_out, hipStream_t st, int slices = 1) {
-  const int Mp = (M + 15) & ~15;
-  hipLaunchKernelGGL(k_quant_act<SRC>, dim3(Mp, slices), dim3(kQuantThreads), 0, st, x, part,
-                     out.q, norm_w, xn_out, M, K, ld, eps);
+  if (SRC == SRC_X || ld <= 4)
+    quant_launch_nc<SRC, 4>(x, part, ld, M, K, norm_w, eps, out, xn_out, st, slices);
+  else if (ld <= 8)
+    quant_launch_nc<SRC, 8>(x, part, ld, M, K, norm_w, eps, out, xn_out, st, slices);
+  else
+    quant_launch_nc<SRC, 12>(x, part, ld, M, K, norm_w, eps, out, xn_out, st, slices);
 }
 
 }  // namespace
 
 bool gemm_i8_supported(int N, int K) {
-  return N > 0 && N % 16 == 0 && K > 0 && K % 32 == 0 && K <= kQuantThreads * kQuantChunks * 8;
+  return N > 0 && N % 16 == 0 && K > 0 && K % 256 == 0 && K <= kQuantThreads * kQuantChunks * 8;
 }
 
-int gemm_i8_chunks(int K) { return (K / 32 + 7) / 8; }
+int gemm_i8_chunks(int K) { return K / 256; }
 
 size_t qact_bytes(int M, int K) {
   const size_t Mp = (M + 15) & ~15;

@@ -54,13 +54,21 @@ struct GemvArgs {
 };
 
 // Activations quantized per 32-block for the int8 products, M rows padded to
-// Mp = M rounded up to 16, one buffer: the int8 values at q, in MFMA operand
-// order (tile (b, m / 16) is 64 lanes x 8 bytes, lane g * 16 + m % 16 holding
-// k = 32b + 8g .. 32b + 8g + 7 of row m), then the fp16-rounded block scales
-// [Mp][K/32] as f32 at q + Mp * K (qact_bytes(M, K) in all).
+// Mp = M rounded up to 16, one buffer: the int8 values at q in MFMA operand
+// order (qtile_offset), then the fp16-rounded block scales [Mp][K/32] as f32
+// at q + Mp * K (qact_bytes(M, K) in all).
 struct QAct {
   int8_t *q = nullptr;
 };
+// byte of element (m, k) (mt16 = Mp / 16): 16-row tiles per pair of 32-blocks
+// b = k / 32 = 2p + h, each 64 lanes x 16 bytes; lane g * 16 + m % 16, g =
+// (k % 32) / 8, holds elements 32b + 8g .. + 7 of row m at bytes 8h .. 8h + 7,
+// so one 16-byte load per lane gives the B operands of two blocks
+__host__ __device__ inline size_t qtile_offset(int m, int k, int mt16) {
+  const int b = k >> 5, g = (k & 31) >> 3;
+  return ((((size_t)(b >> 1) * mt16 + (m >> 4)) * 64 + g * 16 + (m & 15)) * 16) + (b & 1) * 8 +
+         (k & 7);
+}
 size_t qact_bytes(int M, int K);
 
 void launch_gemv(const GemvArgs &a, int epi, bool q8, hipStream_t st);
@@ -68,7 +76,7 @@ void launch_gemv(const GemvArgs &a, int epi, bool q8, hipStream_t st);
 // false when the shape is not one it takes (nothing launched)
 bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st, hipEvent_t ev0 = nullptr,
                          hipEvent_t ev1 = nullptr);
-// the int8 path (q3h_gemm.hip): shapes it takes (N % 16 == 0, K % 32 == 0,
+// the int8 path (q3h_gemm.hip): shapes it takes (N % 16 == 0, K % 256 == 0,
 // K <= 3072)
 bool gemm_i8_supported(int N, int K);
 // rows x [M][ldx] (RMS-normed with norm_w when non-null) quantized into out;
@@ -87,8 +95,8 @@ void launch_gemm_i8_partial(const Mat &W, const QAct &xa, int M, float *part, hi
 // with norm_w (when non-null) and quantization into *out (when non-null)
 void launch_residual_quantize(float *h, const float *part, int chunks, int M, int K,
                               const float *norm_w, float eps, const QAct *out, hipStream_t st);
-// silu(gate) * up from the chunk partials of the gate/up product (N = 2K),
-// quantized into out
+// silu(gate) * up from the chunk partials (chunks <= 4) of the gate/up
+// product (N = 2K), quantized into out
 void launch_swiglu_quantize(const float *part, int chunks, int M, int K, QAct out,
                             hipStream_t st);
 
