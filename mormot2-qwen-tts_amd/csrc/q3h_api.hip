@@ -64,6 +64,7 @@ void Work::ensure(const q3h_stack *s, int rows, int splits, int head_rows) {
   if (c.act_q8) {
     const int maxK = std::max(std::max(H, NQ), I);
     xa.q = (int8_t *)dev_alloc(qact_bytes((int)R, maxK));
+    xb.q = (int8_t *)dev_alloc(qact_bytes((int)R, maxK));
     // chunk partials of the products over up to kPartialRows rows
     const size_t pr = std::min<size_t>(R, kPartialRows);
     const size_t ldq = NQ + 2 * NKV;
@@ -86,8 +87,10 @@ void Work::release() {
   dev_free(tickets);
   dev_free(ctx_arr);
   dev_free(xa.q);
+  dev_free(xb.q);
   dev_free(gpart);
   xa = QAct{};
+  xb = QAct{};
   gpart = nullptr;
   tickets = nullptr;
   h = qkv = att = act = normed = logits = part = nullptr;
@@ -147,9 +150,13 @@ static void run_layers_partial(const q3h_stack *s, Work &w, int M, bool fused, h
     launch_gemm_i8_partial(L.o, w.xa, M, w.gpart, st);
     launch_residual_quantize(w.h, w.gpart, gemm_i8_chunks(NQ), M, H, L.post_norm, eps, &w.xa,
                              st);
-    launch_gemm_i8_partial(L.gu, w.xa, M, w.gpart, st);
-    launch_swiglu_quantize(w.gpart, gemm_i8_chunks(H), M, I, w.xa, st);
-    launch_gemm_i8_partial(L.down, w.xa, M, w.gpart, st);
+    const QAct *act = &w.xb;
+    if (!launch_gemm_i8_swiglu_quantize(L.gu, w.xa, M, w.xb, st)) {
+      launch_gemm_i8_partial(L.gu, w.xa, M, w.gpart, st);
+      launch_swiglu_quantize(w.gpart, gemm_i8_chunks(H), M, I, w.xa, st);
+      act = &w.xa;
+    }
+    launch_gemm_i8_partial(L.down, *act, M, w.gpart, st);
     const bool next = l + 1 < c.layers;
     launch_residual_quantize(w.h, w.gpart, gemm_i8_chunks(I), M, H,
                              next ? s->layers[l + 1].in_norm : nullptr, eps,

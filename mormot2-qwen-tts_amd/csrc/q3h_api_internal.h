@@ -74,7 +74,7 @@ struct Work {
   float *part = nullptr;    // attention partials [rows][heads][splits][head_dim + 2]
   int *tickets = nullptr;   // attention split tickets [rows][heads], zero
   CtxDev **ctx_arr = nullptr;
-  QAct xa;                  // quantized activations (act_q8 stacks)
+  QAct xa, xb;              // quantized activations (act_q8 stacks)
   float *gpart = nullptr;   // chunk partials of the int8 products (act_q8)
   void ensure(const struct ::q3h_stack *s, int rows, int splits, int head_rows);
   void release();

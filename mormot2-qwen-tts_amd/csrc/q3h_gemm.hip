@@ -368,6 +368,56 @@ __global__ __launch_bounds__(64) void k_gemm_i8p(const int8_t *wq, const int8_t 
   }
 }
 
+// The gate/up product with SiLU(gate) * up and the quantization of the result
+// fused: a workgroup owns 64 gate/up rows, i.e. one 32-block of the output,
+// and its 4 chunks (a wave per (16 rows, chunk), K == 1024); the chunk chains
+// meet in LDS and are added in chunk order, then each row's block is
+// quantized into yq (M <= 16 TM rows; yq must not alias xq). The same values
+// as k_gemm_i8p followed by k_quant_act<SRC_SWIGLU>.
+template <int TM>
+__global__ __launch_bounds__(1024) void k_gemm_i8_swq(const int8_t *wq, const int8_t *xq,
+                                                      int8_t *yq, int N, int M) {
+  constexpr int K = 1024, LD = TM * 16 + 4;
+  __shared__ float red[4][64][LD];
+  __shared__ long at[16][16][33];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int mt16 = (M + 15) >> 4;
+  const int tile = w & 3, ch = w >> 2;  // 16-row tile of the 64, chunk
+  const int n0 = blockIdx.x * 64 + tile * 16;
+  const float *dx = scales_of(const_cast<int8_t *>(xq), M, K);
+  float acc[TM][4];
+  chunk_chains<TM, true>(wq, xq, dx, N, K, n0, 0, mt16, ch * 8, at[w], acc);
+#pragma unroll
+  for (int t = 0; t < TM; t++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) red[ch][tile * 16 + 4 * g + r][t * 16 + c] = acc[t][r];
+  __syncthreads();
+  // output block b = blockIdx.x of every row, 32 lanes per row
+  const int KO = N >> 1, nbo = KO >> 5, b = blockIdx.x;
+  float *dy = scales_of(yq, M, KO);
+  for (int idx = threadIdx.x; idx < mt16 * 16 * 32; idx += 1024) {
+    const int m = idx >> 5, j = idx & 31;
+    float o = 0.f;
+    if (m < M) {
+      float gs = 0.f, us = 0.f;
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        gs = __fadd_rn(gs, red[v][2 * j][m]);
+        us = __fadd_rn(us, red[v][2 * j + 1][m]);
+      }
+      o = silu_mul_ieee(gs, us);
+    }
+    float amax = fabsf(o);
+#pragma unroll
+    for (int s2 = 16; s2 >= 1; s2 >>= 1) amax = fmaxf(amax, __shfl_xor(amax, s2));
+    const float d = __fdiv_rn(amax, 127.0f);
+    const float id = d != 0.f ? __fdiv_rn(1.0f, d) : 0.f;
+    yq[qtile_offset(m, 32 * b + j, mt16)] = (int8_t)(int)roundf(__fmul_rn(o, id));
+    if (j == 0) dy[(size_t)m * nbo + b] = (float)(_Float16)d;
+  }
+}
+
 template <int TM, int KW>
 void gemm_launch(const Mat &W, const QAct &xa, int M, int epi, float *y, int ldy,
                  hipStream_t st) {
@@ -463,6 +513,18 @@ void launch_gemm_i8(const Mat &W, const QAct &xa, int M, int epi, float *y, int 
     gemm_by_k<2>(W, xa, M, epi, y, ldy, st);
   else
     gemm_by_k<4>(W, xa, M, epi, y, ldy, st);
+}
+
+bool launch_gemm_i8_swiglu_quantize(const Mat &W, const QAct &xa, int M, QAct out,
+                                    hipStream_t st) {
+  if (M > 32 || W.K != 1024 || W.N % 64 != 0) return false;
+  if (M <= 16)
+    hipLaunchKernelGGL(k_gemm_i8_swq<1>, dim3(W.N / 64), dim3(1024), 0, st, W.q, xa.q, out.q,
+                       W.N, M);
+  else
+    hipLaunchKernelGGL(k_gemm_i8_swq<2>, dim3(W.N / 64), dim3(1024), 0, st, W.q, xa.q, out.q,
+                       W.N, M);
+  return true;
 }
 
 void launch_gemm_i8_partial(const Mat &W, const QAct &xa, int M, float *part, hipStream_t st) {
