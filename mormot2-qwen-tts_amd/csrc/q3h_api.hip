@@ -119,13 +119,15 @@ void linear(const q3h_stack *s, Work &w, const Mat &W, const float *x, int ldx, 
 // rows), the residual add + RMSNorm + quantization of the next input (o_proj,
 // down), SiLU(gate) * up + quantization (gate/up). Results equal the
 // workgroup-reduced schedule of run_layers to the bit.
-static void run_layers_partial(const q3h_stack *s, Work &w, int M, bool fused, hipStream_t st) {
+static void run_layers_partial(const q3h_stack *s, Work &w, int M, bool fused,
+                               const LayerIO &io, hipStream_t st) {
   const q3h_stack_config &c = s->cfg;
   const int H = c.hidden, hd = c.head_dim, NQ = c.heads * hd, NKV = c.kv_heads * hd;
   const int I = c.intermediate, ldq = NQ + 2 * NKV;
   const bool kv16 = c.kv_f16 != 0;
   const float eps = c.rms_eps;
-  launch_quantize_act(w.h, H, M, H, s->layers[0].in_norm, eps, w.xa, nullptr, st);
+  if (!io.input_quantized)
+    launch_quantize_act(w.h, H, M, H, s->layers[0].in_norm, eps, w.xa, nullptr, st);
   for (int l = 0; l < c.layers; l++) {
     const Layer &L = s->layers[l];
     AttnArgs at{};
@@ -158,21 +160,26 @@ static void run_layers_partial(const q3h_stack *s, Work &w, int M, bool fused, h
     }
     launch_gemm_i8_partial(L.down, *act, M, w.gpart, st);
     const bool next = l + 1 < c.layers;
-    launch_residual_quantize(w.h, w.gpart, gemm_i8_chunks(I), M, H,
-                             next ? s->layers[l + 1].in_norm : nullptr, eps,
-                             next ? &w.xa : nullptr, st);
+    const float *nw = next ? s->layers[l + 1].in_norm : io.final_norm;
+    launch_residual_quantize(w.h, w.gpart, gemm_i8_chunks(I), M, H, nw, eps,
+                             nw ? &w.xa : nullptr, st);
   }
 }
 
 // The layers of a stack over M rows of w.h, n contexts of R rows each (M =
 // n * R), their descriptors already in w.rd: the per-layer kernel sequence.
-void run_layers(const q3h_stack *s, Work &w, int M, int splits, bool fused, hipStream_t st) {
+bool partial_path(const q3h_stack *s, int M) {
+  return s->cfg.act_q8 && M <= kPartialRows && gemm_i8_chunks(s->cfg.hidden) <= 4;
+}
+
+void run_layers(const q3h_stack *s, Work &w, int M, int splits, bool fused, hipStream_t st,
+                const LayerIO &io) {
   const q3h_stack_config &c = s->cfg;
   const int H = c.hidden, hd = c.head_dim, NQ = c.heads * hd, NKV = c.kv_heads * hd;
   const int I = c.intermediate, ldq = NQ + 2 * NKV;
   const bool kv16 = c.kv_f16 != 0;
-  if (c.act_q8 && M <= kPartialRows && gemm_i8_chunks(c.hidden) <= 4) {
-    run_layers_partial(s, w, M, fused, st);
+  if (partial_path(s, M)) {
+    run_layers_partial(s, w, M, fused, io, st);
     return;
   }
   for (int l = 0; l < c.layers; l++) {

@@ -15,6 +15,7 @@
 
 #include "q3h.h"
 #include "q3h_api_internal.h"
+#include "q3h_quant.h"
 
 namespace q3h {
 
@@ -38,6 +39,19 @@ struct FrameDev {
   float *t_h;             // talker input rows [n][H]
   const float *cp_logits; // [n][cp_vocab]
   CtxDev *const *cp_ctx;  // [n]
+  // the int8 path over few rows (partial products): the row descriptors and
+  // the layer-0 inputs (normed, quantized) of both stacks are written by the
+  // kernels that build the rows, the talker length advanced at the frame end,
+  // and the code-predictor head left as chunk partials (nullptr / 0: the
+  // separate kernels do it)
+  RowDesc *cp_rd;          // [2n] rows of the code-predictor step
+  RowDesc *t_rd;           // [n]
+  CtxDev *const *t_ctx;    // [n]
+  int8_t *cp_xq, *t_xq;    // operand tiles of layer 0 of each stack
+  const float *cp_norm0, *t_norm0;
+  float cp_eps, t_eps;
+  const float *cp_part;    // head partials [cp_hch][rows][cp_vocab]
+  int cp_hch;
 };
 
 constexpr int kArgBlock = 1024;
@@ -75,46 +89,71 @@ __device__ int block_argmax(float v, int i) {
   return res;
 }
 
+// the descriptor of a row at position pos of context c (pos < 0: inactive)
+__device__ __forceinline__ RowDesc row_desc(const CtxDev *c, int pos) {
+  RowDesc d;
+  d.k = c->k;
+  d.v = c->v;
+  d.max_pos = c->max_pos;
+  d.pos = pos < c->max_pos ? pos : -1;
+  return d;
+}
+
 // ChooseCode0 + the code-predictor input [past state; codec_emb[code]] and
-// the reset of the code-predictor context. One block per stream.
+// the reset of the code-predictor context. One block per stream. The int8
+// path: also the descriptors (positions 0, 1) and the quantized layer-0
+// inputs of both rows (zeros for a stream that does not run).
 __global__ __launch_bounds__(kArgBlock) void k_choose_code0(FrameDev f) {
+  __shared__ double red[kArgBlock / 64];
   const int s = blockIdx.x, tid = threadIdx.x;
-  if (!f.alive[s]) return;
-  const float *lg = f.logits + (size_t)s * f.vocab;
-  const uint8_t *seen = f.seen + (size_t)s * f.vocab;
-  const int nf = f.nframes[s];
-  float bv = -INFINITY;
-  int bi = 0x7fffffff;
-  for (int i = tid; i < f.vocab; i += kArgBlock) {
-    float v = lg[i];
-    // 2048..3071 forbidden but eos; eos forbidden before 2 frames
-    if (i >= f.vocab - 1024 && i != f.eos) v = -INFINITY;
-    if (i == f.eos && nf < 2) v = -INFINITY;
-    // repetition penalty, once per code already returned (not when forbidden)
-    if (seen[i] && v != -INFINITY && f.penalty != 1.0f)
-      v = v > 0.f ? __fdiv_rn(v, f.penalty) : v * f.penalty;
-    argmax_merge(bv, bi, v, i);
+  int code = -1;
+  if (f.alive[s]) {
+    const float *lg = f.logits + (size_t)s * f.vocab;
+    const uint8_t *seen = f.seen + (size_t)s * f.vocab;
+    const int nf = f.nframes[s];
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = tid; i < f.vocab; i += kArgBlock) {
+      float v = lg[i];
+      // 2048..3071 forbidden but eos; eos forbidden before 2 frames
+      if (i >= f.vocab - 1024 && i != f.eos) v = -INFINITY;
+      if (i == f.eos && nf < 2) v = -INFINITY;
+      // repetition penalty, once per code already returned (not when forbidden)
+      if (seen[i] && v != -INFINITY && f.penalty != 1.0f)
+        v = v > 0.f ? __fdiv_rn(v, f.penalty) : v * f.penalty;
+      argmax_merge(bv, bi, v, i);
+    }
+    code = block_argmax(bv, bi);
+    int *codes = f.codes + (size_t)s * f.groups;
+    if (code == f.eos) {
+      if (tid < f.groups) codes[tid] = -1;
+      __syncthreads();
+      if (tid == 0) f.alive[s] = 0;
+      code = -1;
+    } else {
+      if (tid == 0) {
+        codes[0] = code;
+        f.seen[(size_t)s * f.vocab + code] = 1;
+        f.nframes[s] = nf + 1;
+        f.cp_ctx[s]->len = 0;
+      }
+      float *x = f.cp_h + (size_t)s * 2 * f.H;
+      const float *past = f.past + (size_t)s * f.H;
+      const float *emb = f.codec_emb + (size_t)code * f.H;
+      for (int c = tid; c < f.H; c += kArgBlock) {
+        x[c] = past[c];
+        x[f.H + c] = emb[c];
+      }
+    }
   }
-  const int code = block_argmax(bv, bi);
-  int *codes = f.codes + (size_t)s * f.groups;
-  if (code == f.eos) {
-    if (tid < f.groups) codes[tid] = -1;
+  if (f.cp_xq) {
+    const bool live = code >= 0;
+    if (tid < 2) f.cp_rd[2 * s + tid] = row_desc(f.cp_ctx[s], live ? tid : -1);
+    quant_row_block(live ? f.past + (size_t)s * f.H : nullptr, f.cp_norm0, f.cp_eps, f.H,
+                    2 * s, 2 * f.n, f.cp_xq, red);
     __syncthreads();
-    if (tid == 0) f.alive[s] = 0;
-    return;
-  }
-  if (tid == 0) {
-    codes[0] = code;
-    f.seen[(size_t)s * f.vocab + code] = 1;
-    f.nframes[s] = nf + 1;
-    f.cp_ctx[s]->len = 0;
-  }
-  float *x = f.cp_h + (size_t)s * 2 * f.H;
-  const float *past = f.past + (size_t)s * f.H;
-  const float *emb = f.codec_emb + (size_t)code * f.H;
-  for (int c = tid; c < f.H; c += kArgBlock) {
-    x[c] = past[c];
-    x[f.H + c] = emb[c];
+    quant_row_block(live ? f.codec_emb + (size_t)code * f.H : nullptr, f.cp_norm0, f.cp_eps,
+                    f.H, 2 * s + 1, 2 * f.n, f.cp_xq, red);
   }
 }
 
@@ -142,6 +181,41 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_argmax(const float *__restrict
   }
 }
 
+// The int8 path's k_cp_argmax: the head-g logits as the sum of the head's
+// chunk partials in chunk order (row R s + R - 1 of the step's R n rows),
+// ChooseCode for group g + 1, then the next step's input row pred_emb[g][code]
+// (to cp_h), its descriptor (position g + 2) and its quantized layer-0 input.
+__global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
+  __shared__ double red[kArgBlock / 64];
+  const int s = blockIdx.x, tid = threadIdx.x;
+  const bool next = g + 1 < f.groups - 1;
+  if (!f.alive[s]) {
+    if (next) {
+      if (tid == 0) f.cp_rd[s] = row_desc(f.cp_ctx[s], -1);
+      quant_row_block(nullptr, nullptr, 0.f, f.H, s, f.n, f.cp_xq, red);
+    }
+    return;
+  }
+  const int R = g == 0 ? 2 : 1, rows = R * f.n, row = R * s + R - 1;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = tid; i < f.cp_vocab; i += kArgBlock) {
+    float v = 0.f;
+    for (int c = 0; c < f.cp_hch; c++)
+      v = __fadd_rn(v, f.cp_part[((size_t)c * rows + row) * f.cp_vocab + i]);
+    argmax_merge(bv, bi, v, i);
+  }
+  const int code = block_argmax(bv, bi);
+  if (tid == 0) f.codes[(size_t)s * f.groups + g + 1] = code;
+  if (next) {
+    const float *emb = f.pred_emb + ((size_t)g * f.cp_vocab + code) * f.H;
+    float *x = f.cp_h + (size_t)s * f.H;
+    for (int c = tid; c < f.H; c += kArgBlock) x[c] = emb[c];
+    if (tid == 0) f.cp_rd[s] = row_desc(f.cp_ctx[s], g + 2);
+    quant_row_block(emb, f.cp_norm0, f.cp_eps, f.H, s, f.n, f.cp_xq, red);
+  }
+}
+
 // the next talker input: codec_emb[code 0] + sum_g pred_emb[g-1][code g] +
 // (trailing[step] or tts_pad), summed in that order.
 __global__ void k_talker_input(FrameDev f) {
@@ -160,9 +234,47 @@ __global__ void k_talker_input(FrameDev f) {
   f.t_h[(size_t)s * f.H + c] = x;
 }
 
+// The int8 path's k_talker_input: one block per stream, the row also kept in
+// LDS for its descriptor (position = the context length) and its quantized
+// layer-0 input (H <= 4096).
+__global__ __launch_bounds__(kArgBlock) void k_talker_input_q(FrameDev f) {
+  __shared__ double red[kArgBlock / 64];
+  __shared__ float xs[4096];
+  const int s = blockIdx.x, tid = threadIdx.x;
+  if (!f.alive[s]) {
+    if (tid == 0) f.t_rd[s] = row_desc(f.t_ctx[s], -1);
+    quant_row_block(nullptr, nullptr, 0.f, f.H, s, f.n, f.t_xq, red);
+    return;
+  }
+  const int *codes = f.codes + (size_t)s * f.groups;
+  const int st = f.step[s];
+  for (int c = tid; c < f.H; c += kArgBlock) {
+    float x = f.codec_emb[(size_t)codes[0] * f.H + c];
+    for (int g = 1; g < f.groups; g++)
+      x = x + f.pred_emb[((size_t)(g - 1) * f.cp_vocab + codes[g]) * f.H + c];
+    if (st < f.trailing_rows[s])
+      x = x + f.trailing[((size_t)s * f.max_trailing + st) * f.H + c];
+    else
+      x = x + f.tts_pad[c];
+    f.t_h[(size_t)s * f.H + c] = x;
+    xs[c] = x;
+  }
+  if (tid == 0) f.t_rd[s] = row_desc(f.t_ctx[s], f.t_ctx[s]->len);
+  __syncthreads();
+  quant_row_block(xs, f.t_norm0, f.t_eps, f.H, s, f.n, f.t_xq, red);
+}
+
+// the end of a step: the frame count of every running stream; the int8 path
+// also advances the talker length here (as launch_advance does otherwise)
 __global__ void k_frame_end(FrameDev f) {
   const int s = blockIdx.x * blockDim.x + threadIdx.x;
-  if (s < f.n && f.alive[s]) f.step[s] += 1;
+  if (s < f.n && f.alive[s]) {
+    f.step[s] += 1;
+    if (f.t_xq) {
+      CtxDev *c = f.t_ctx[s];
+      c->len = min(c->len + 1, c->max_pos);
+    }
+  }
 }
 
 }  // namespace q3h
@@ -220,6 +332,7 @@ void enqueue_step(q3h_frame *f, int splits, hipStream_t st) {
   const int n = c.n_streams, H = f->H;
   q3h_stack *cp = f->cp, *tk = f->talker;
   FrameDev fd = f->fd;
+  const bool cq = fd.cp_xq != nullptr, tq = fd.t_xq != nullptr;  // the folded int8 paths
   hipLaunchKernelGGL(k_choose_code0, dim3(n), dim3(kArgBlock), 0, st, fd);
   // code predictor: 2 rows per stream, then one row per group
   // one stream on the Qwen3-TTS shapes: steps 1.. run the fused single-row
@@ -227,6 +340,18 @@ void enqueue_step(q3h_frame *f, int splits, hipStream_t st) {
   const bool fused = n == 1 && cp_fused_supported(cp->cfg) && f->cctx[0]->max_pos == 16;
   for (int g = 0; g < c.groups - 1; g++) {
     const int R = g == 0 ? 2 : 1;
+    if (cq) {
+      // inputs and descriptors written by k_choose_code0 / k_cp_next; the
+      // last layer's residual kernel applies the final norm and quantizes the
+      // head input; k_cp_next adds the head's chunk partials
+      LayerIO io;
+      io.input_quantized = true;
+      io.final_norm = cp->final_norm;
+      run_layers(cp, f->cw, n * R, 1, R == 1, st, io);
+      launch_gemm_i8_partial(cp->heads[c.cp_heads[g]], f->cw.xa, n * R, f->cw.gpart, st);
+      hipLaunchKernelGGL(k_cp_next, dim3(n), dim3(kArgBlock), 0, st, fd, g);
+      continue;
+    }
     if (fused && g > 0) {
       run_cp_fused(cp, f->cw, f->cctx[0], g + 1, st);
     } else {
@@ -241,9 +366,16 @@ void enqueue_step(q3h_frame *f, int splits, hipStream_t st) {
                        fd.pred_emb, fd.cp_h, fd.codes, fd.cp_vocab, fd.groups, fd.H, g);
   }
   // the talker
-  hipLaunchKernelGGL(k_talker_input, dim3((H + 255) / 256, n), dim3(256), 0, st, fd);
-  launch_prep(f->t_arr, fd.alive, n, 1, f->tw.rd, st);
-  run_layers(tk, f->tw, n, splits, true, st);
+  if (tq) {
+    hipLaunchKernelGGL(k_talker_input_q, dim3(n), dim3(kArgBlock), 0, st, fd);
+    LayerIO io;
+    io.input_quantized = true;
+    run_layers(tk, f->tw, n, splits, true, st, io);
+  } else {
+    hipLaunchKernelGGL(k_talker_input, dim3((H + 255) / 256, n), dim3(256), 0, st, fd);
+    launch_prep(f->t_arr, fd.alive, n, 1, f->tw.rd, st);
+    run_layers(tk, f->tw, n, splits, true, st);
+  }
   const Mat &th = tk->heads[c.talker_head];
   if (n == 1) {  // final norm fused into the head, the normed state written alongside
     linear(tk, f->tw, th, f->tw.h, H, 1, tk->final_norm, fd.logits, c.vocab, EPI_STORE, fd.past,
@@ -252,7 +384,7 @@ void enqueue_step(q3h_frame *f, int splits, hipStream_t st) {
     launch_rmsnorm_rows(f->tw.h, H, n, H, tk->final_norm, tk->cfg.rms_eps, fd.past, H, st);
     linear(tk, f->tw, th, fd.past, H, n, nullptr, fd.logits, c.vocab, EPI_STORE, nullptr, st);
   }
-  launch_advance(f->t_arr, fd.alive, n, 1, st);
+  if (!tq) launch_advance(f->t_arr, fd.alive, n, 1, st);
   hipLaunchKernelGGL(k_frame_end, dim3((n + 63) / 64), dim3(64), 0, st, fd);
 }
 
@@ -351,6 +483,21 @@ extern "C" int q3h_frame_create(q3h_stack *talker, q3h_stack *cp, const q3h_fram
     d.t_h = f->tw.h;
     d.cp_logits = f->cw.logits;
     d.cp_ctx = f->c_arr;
+    d.cp_rd = f->cw.rd;
+    d.t_rd = f->tw.rd;
+    d.t_ctx = f->t_arr;
+    if (partial_path(cp, 2 * n) && cp->heads[c.cp_heads[0]].N % 16 == 0) {
+      d.cp_xq = f->cw.xa.q;
+      d.cp_norm0 = cp->layers[0].in_norm;
+      d.cp_eps = cp->cfg.rms_eps;
+      d.cp_part = f->cw.gpart;
+      d.cp_hch = gemm_i8_chunks(H);
+    }
+    if (partial_path(talker, n) && H <= 4096) {
+      d.t_xq = f->tw.xa.q;
+      d.t_norm0 = talker->layers[0].in_norm;
+      d.t_eps = talker->cfg.rms_eps;
+    }
     check_hip(hipMemset(d.alive, 0, sizeof(int) * n), "frame init");
     check_hip(hipMemset(d.codes, 0xff, sizeof(int) * n * c.groups), "frame init");
     check_hip(hipHostMalloc((void **)&f->pinned, sizeof(int32_t) * n * (c.groups + 1)),
