@@ -65,14 +65,29 @@ __device__ __forceinline__ float2 load2(const KV *p) {
   }
 }
 
-// element col of row m: the product's output, or its chunk partials
-// [nch][M][ld] added in chunk order
-__device__ __forceinline__ float qkv_at(const float *qkv, int ld, int nch, int M, int m, int col) {
-  if (nch == 0) return qkv[(size_t)m * ld + col];
-  float s = 0.f;
-#pragma unroll 4
-  for (int c = 0; c < nch; c++) s = __fadd_rn(s, qkv[((size_t)c * M + m) * ld + col]);
-  return s;
+// elements col and col + 64 of row m: the product's output, or (nch > 0)
+// its chunk partials [nch][M][ld] (nch <= 4) added in chunk order; all loads
+// issued together (clamped chunk indices, the extra ones not added)
+__device__ __forceinline__ void qkv_pair(const float *qkv, int ld, int nch, int M, int m, int col,
+                                         float &x0, float &x1) {
+  if (nch == 0) {
+    x0 = qkv[(size_t)m * ld + col];
+    x1 = qkv[(size_t)m * ld + col + 64];
+    return;
+  }
+  float a[4], b[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const float *r = qkv + ((size_t)min(c, nch - 1) * M + m) * ld + col;
+    a[c] = r[0];
+    b[c] = r[64];
+  }
+  x0 = x1 = 0.f;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    x0 = c < nch ? __fadd_rn(x0, a[c]) : x0;
+    x1 = c < nch ? __fadd_rn(x1, b[c]) : x1;
+  }
 }
 
 // sum over a 16-lane DPP row, the balanced pairwise tree in lane order
@@ -118,13 +133,16 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
   const size_t head_off = ((size_t)layer * kvh + g) * d.max_pos * HD;
   const KV *kc = reinterpret_cast<const KV *>(d.k) + head_off;
   const KV *vc = reinterpret_cast<const KV *>(d.v) + head_off;
+  constexpr int KG = NT / 16;
+  const int kg = t >> 4, li = t & 15;
+  const int ch = wave & 3, dim = (wave >> 2) * 64 + lane;
 
   if (FUSED) {
     // vector j: query head g GRP + j (j < GRP), the new k (j == GRP), v (GRP + 1)
     for (int j = wave; j < GRP + 2; j += NT / 64) {
       const int col = j < GRP ? (g * GRP + j) * HD : j == GRP ? NQ + g * HD : NQ + (kvh + g) * HD;
-      float x0 = qkv_at(qkv, ldq, nch, M, m, col + lane);
-      float x1 = qkv_at(qkv, ldq, nch, M, m, col + lane + 64);
+      float x0, x1;
+      qkv_pair(qkv, ldq, nch, M, m, col + lane, x0, x1);
       if (j <= GRP) {
         const float *w = qkn + (j < GRP ? 0 : HD);
         const float eps = qkn[2 * HD];
@@ -159,8 +177,6 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
   // of SU positions are issued together
   const float scale = (float)(1.0 / __builtin_sqrt((double)HD));
   {
-    constexpr int KG = NT / 16;
-    const int kg = t >> 4, li = t & 15;
     float qv[GRP][8], kn8[8];
 #pragma unroll
     for (int j = 0; j < GRP; j++)
@@ -173,7 +189,8 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
       // waited for on its own), then the new position's own k, zeros past L
       float k8[SU][8];
 #pragma unroll
-      for (int u = 0; u < SU; u++) load8(kc + (size_t)min(p0 + u * KG + kg, L - 1) * HD + 8 * li, k8[u]);
+      for (int u = 0; u < SU; u++)
+        load8(kc + (size_t)min(p0 + u * KG + kg, L - 1) * HD + 8 * li, k8[u]);
 #pragma unroll
       for (int u = 0; u < SU; u++) {
         const int p = p0 + u * KG + kg;
@@ -247,7 +264,6 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
   // values: chain ch = wave % 4 over positions p = ch mod 4, dim (wave / 4) 64
   // + lane, every head of the group; the loads of VU positions issued together
   {
-    const int ch = wave & 3, dim = (wave >> 2) * 64 + lane;
     float c[GRP];
 #pragma unroll
     for (int j = 0; j < GRP; j++) c[j] = 0.f;
@@ -256,12 +272,15 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
       float v[VU];
 #pragma unroll
       for (int u = 0; u < VU; u++) v[u] = (float)vc[(size_t)min(p0 + 4 * u, L - 1) * HD + dim];
-      if (FUSED) {
+      // the new position: its own v; past L: zero (the clamped load may have
+      // read the new row before it was written)
 #pragma unroll
-        for (int u = 0; u < VU; u++) v[u] = p0 + 4 * u == pos ? vnd : v[u];  // its own v
+      for (int u = 0; u < VU; u++) {
+        const int p = p0 + 4 * u;
+        v[u] = p >= L ? 0.f : FUSED && p == pos ? vnd : v[u];
       }
-      // weights of the round read together; past L a zero weight adds an exact
-      // zero to the chain (finite v from the clamped position)
+      // weights of the round read together; past L a zero weight times a zero
+      // value adds an exact zero to the chain
       float wgt[VU][GRP];
 #pragma unroll
       for (int u = 0; u < VU; u++) {

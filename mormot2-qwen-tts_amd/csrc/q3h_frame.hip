@@ -200,9 +200,14 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
   float bv = -INFINITY;
   int bi = 0x7fffffff;
   for (int i = tid; i < f.cp_vocab; i += kArgBlock) {
+    // the chunk partials (cp_hch <= 4) loaded together, added in chunk order
+    float p4[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+      p4[c] = f.cp_part[((size_t)min(c, f.cp_hch - 1) * rows + row) * f.cp_vocab + i];
     float v = 0.f;
-    for (int c = 0; c < f.cp_hch; c++)
-      v = __fadd_rn(v, f.cp_part[((size_t)c * rows + row) * f.cp_vocab + i]);
+#pragma unroll
+    for (int c = 0; c < 4; c++) v = c < f.cp_hch ? __fadd_rn(v, p4[c]) : v;
     argmax_merge(bv, bi, v, i);
   }
   const int code = block_argmax(bv, bi);

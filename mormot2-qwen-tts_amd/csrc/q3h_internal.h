@@ -139,7 +139,7 @@ void launch_attn(const AttnArgs &a, int M, int splits, bool fused, bool kv16, hi
 // one new position of its own context, QK-norm / RoPE / K/V append in the
 // prologue), outputs quantized into xa for the o_proj product; positions up
 // to kAttnXMaxPositions / (heads / kv_heads) (the scores of a kv group held
-// in LDS). qkv_chunks > 0 (fused only):
+// in LDS). qkv_chunks in 1..4 (fused only):
 // a.qkv holds the chunk partials [qkv_chunks][M][a.ldq] of the q/k/v product
 // instead of its rows, added in chunk order in the prologue.
 constexpr int kAttnXMaxPositions = 8192;
