@@ -25,7 +25,10 @@ Beside it:
                 stream (the figure rocprofv3 reports per dispatch), and the
                 graph-replayed wall time per launch beside it;
   cpu_baseline  the oracle (the C restatement of the same frame step) on the
-                host cores, on a bounded sample of the same workload.
+                host cores, on a bounded sample of the same workload;
+  long_context_attention (frame_b1)  the talker with an f16 K/V cache
+                prefilled to 2048 / 4096 / 8192 positions: 32 decode steps
+                each, and the decode attention kernels' GB/s.
 
 Prints one JSON line.
 """
@@ -159,6 +162,53 @@ def gemv_roofline(ts, args):
                 graph_wall_us_per_launch=None if wall is None else round(wall, 3))
 
 
+LONG_LENGTHS = (2048, 4096, 8192)
+
+
+def long_context_attention(dev, f32, tables, seed, steps=32, iters=10):
+    """Talker Q8_0 at batch 1 with an f16 K/V cache prefilled to 2048, 4096 and
+    8192 positions (N(0,1) values from a seed): 32 greedy decode steps at each
+    length (q3h_forward_embeds, host row in and logits out, so PCIe-inclusive),
+    then the decode attention kernels alone (events attached to each launch):
+    algorithmic bytes = the f16 K/V of every position read once (8 kv heads x
+    128 dims x 2 x 2 B = 4 KB per position and layer)."""
+    t0 = time.time()
+    cap = max(LONG_LENGTHS) + steps + 8
+    ts = q3h.Stack(dev, dict(synth.TALKER, dtype=q3h.Q8_0, kv_f16=1, act_q8=0,
+                             max_positions=cap), f32["tl"], f32["tf"], q3h.F32)
+    ts.add_head(f32["th"], q3h.F32)
+    codec = tables["codec_emb"]
+    rng = np.random.Generator(np.random.PCG64(seed + 77))
+    shape = (synth.TALKER["layers"], synth.TALKER["kv_heads"])
+    out = []
+    for L in LONG_LENGTHS:
+        k = rng.standard_normal(shape + (L, 128), dtype=np.float32)
+        v = rng.standard_normal(shape + (L, 128), dtype=np.float32)
+        ctx = q3h.Context(ts, cap)
+        ctx.fill_kv(k, v)
+        del k, v
+        x = synth.prompt(seed + L, 1)
+        lat = np.empty(steps)
+        for i in range(steps):
+            a = time.perf_counter()
+            lg, _ = ctx.forward(x, head=0, want_normed=False)
+            lat[i] = time.perf_counter() - a
+            x = codec[int(np.argmax(lg[:2048]))][None]
+        us, nbytes = ctx.time_attention(iters=iters)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out.append(dict(positions=ctx.length, attention_us_per_layer=round(us, 3),
+                        attention_bytes_per_layer=int(nbytes), attention_gbs=round(gbs, 1),
+                        frac=round(gbs / HBM_PEAK_GBS, 4),
+                        decode_step_us_p50=round(1e6 * float(np.median(lat)), 1)))
+        log(f"long context {L}: attention {us:.2f} us/layer ({gbs:.0f} GB/s), "
+            f"decode step p50 {1e6 * np.median(lat):.0f} us")
+        ctx.destroy()
+    ts.destroy()
+    log(f"long-context attention in {time.time() - t0:.1f} s")
+    return dict(kernel="k_attn_split + k_attn_merge (f16 K/V, talker decode, per layer)",
+                kv="f16", steps_per_length=steps, results=out)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -172,6 +222,8 @@ def main():
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the kernels directly instead of replaying hipGraphs "
                          "(for tracers that do not follow graph capture)")
+    ap.add_argument("--no-long-attn", action="store_true",
+                    help="skip the long-context attention measurement (frame_b1)")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the matrix-vector roofline measurement (profiling runs)")
     args = ap.parse_args()
@@ -209,6 +261,11 @@ def main():
 
     roofline = gemv_roofline(ts, args)
 
+    frame.destroy()
+    long_attn = None
+    if b1 and not args.no_long_attn:
+        long_attn = long_context_attention(dev, f32, tables, args.seed)
+
     cpu = None
     parity = None
     if not args.no_cpu:
@@ -216,7 +273,6 @@ def main():
         parity = dict(frames=nf, codes_equal_stream0=bool(equal))
         log(f"cpu baseline: {cpu['value']:.2f} frames/s on {cpu['cores']} threads; "
             f"codes equal over {nf} frames: {equal}")
-    frame.destroy()
     ts.destroy()
     cs.destroy()
     dev.close()
@@ -245,6 +301,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "parity": parity,
+        "long_context_attention": long_attn,
     }
     print(json.dumps(out), flush=True)
     return 0

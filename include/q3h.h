@@ -116,6 +116,19 @@ int q3h_context_fill_kv(q3h_context *c, const float *k, const float *v, int len)
 /* no reference counterpart (tests): read the K/V cache of one layer for
    positions [0, length) as f32 [kv_heads][length][head_dim] */
 int q3h_context_read_kv(q3h_context *c, int layer, float *k, float *v);
+/* no reference counterpart (measurement): the decode attention of every
+   layer for one new row at position length (the attention kernels of
+   q3h_forward_embeds with rows = 1, fused QK-norm / RoPE / K/V append), run
+   iters times with events attached to each launch. us_per_launch: the
+   kernels' own average execution time per layer (with the merge of the
+   splits on long contexts: the sum of the two kernels, the launch gap
+   between them excluded); bytes_per_launch: algorithmic bytes
+   (the cache of length positions read, the new key and value written, the
+   q / k / v row read, the outputs written). The row's q / k / v are zeros;
+   the key and value written at position length are scratch (the length does
+   not change). Stacks with f32 activations (act_q8 = 0). */
+int q3h_context_time_attention(q3h_context *c, int iters, float *us_per_launch,
+                               int64_t *bytes_per_launch);
 
 /* ---- the forward: TQwenLm.Forward (lm.pas:391-408), i.e.
    TQwen3Vulkan.ForwardEmbeds(ctx, x, rows, nil, false, fLast) (lm.pas:397)

@@ -58,8 +58,6 @@ void Work::ensure(const q3h_stack *s, int rows, int splits, int head_rows) {
   logits = (float *)dev_alloc(sizeof(float) * R * (head_cap > 0 ? head_cap : 1));
   rd = (RowDesc *)dev_alloc(sizeof(RowDesc) * R);
   part = (float *)dev_alloc(sizeof(float) * R * c.heads * splits_cap * (c.head_dim + 2));
-  tickets = (int *)dev_alloc(sizeof(int) * R * c.heads);
-  check_hip(hipMemset(tickets, 0, sizeof(int) * R * c.heads), "zero tickets");
   ctx_arr = (CtxDev **)dev_alloc(sizeof(CtxDev *) * R);
   if (c.act_q8) {
     const int maxK = std::max(std::max(H, NQ), I);
@@ -84,7 +82,6 @@ void Work::release() {
   dev_free(logits);
   dev_free(rd);
   dev_free(part);
-  dev_free(tickets);
   dev_free(ctx_arr);
   dev_free(xa.q);
   dev_free(xb.q);
@@ -92,13 +89,23 @@ void Work::release() {
   xa = QAct{};
   xb = QAct{};
   gpart = nullptr;
-  tickets = nullptr;
   h = qkv = att = act = normed = logits = part = nullptr;
   rd = nullptr;
   ctx_arr = nullptr;
 }
 
-int attention_splits(int positions) { return attn_splits(positions); }
+int attention_splits(const q3h_stack *s, int positions) {
+  return attn_splits(positions, s->cfg.kv_f16 != 0);
+}
+
+int attention_splits_upto(const q3h_stack *s, int positions) {
+  // the split length grows with the context, so the count peaks at the top
+  // of each length's range
+  int n = 1;
+  for (int p : {2048, 4096, positions})
+    n = std::max(n, attention_splits(s, std::min(p, positions)));
+  return n;
+}
 
 void linear(const q3h_stack *s, Work &w, const Mat &W, const float *x, int ldx, int M,
             const float *norm_w, float *y, int ldy, int epi, float *xn_out, hipStream_t st) {
@@ -172,7 +179,7 @@ bool partial_path(const q3h_stack *s, int M) {
   return s->cfg.act_q8 && M <= kPartialRows && gemm_i8_chunks(s->cfg.hidden) <= 4;
 }
 
-void run_layers(const q3h_stack *s, Work &w, int M, int splits, bool fused, hipStream_t st,
+void run_layers(const q3h_stack *s, Work &w, int M, int positions, bool fused, hipStream_t st,
                 const LayerIO &io) {
   const q3h_stack_config &c = s->cfg;
   const int H = c.hidden, hd = c.head_dim, NQ = c.heads * hd, NKV = c.kv_heads * hd;
@@ -222,8 +229,7 @@ void run_layers(const q3h_stack *s, Work &w, int M, int splits, bool fused, hipS
     at.rope_cs = reinterpret_cast<const float2 *>(s->rope_cs);
     at.out = w.att;
     at.part = w.part;
-    at.tickets = w.tickets;
-    launch_attn(at, M, splits, fused, kv16, st);
+    launch_attn(at, M, positions, fused, kv16, st);
     // o_proj + residual
     linear(s, w, L.o, w.att, NQ, M, nullptr, w.h, H, EPI_ADD, nullptr, st);
     // RMSNorm + gate/up + SwiGLU
@@ -466,6 +472,9 @@ extern "C" int q3h_stack_create(q3h_device *dev, const q3h_stack_config *cfg,
     require(c.dtype == Q3H_Q8_0 || w->src_dtype == Q3H_F32, Q3H_E_ARG,
             "q3h_stack_create: an f32 stack takes f32 weights");
     require(c.max_positions > 0, Q3H_E_ARG, "q3h_stack_create: max_positions <= 0");
+    require(c.max_positions <= attn_max_positions(c.kv_f16 != 0), Q3H_E_ARG,
+            "q3h_stack_create: max_positions above " +
+                std::to_string(attn_max_positions(c.kv_f16 != 0)));
     require(c.act_q8 == 0 || c.dtype == Q3H_Q8_0, Q3H_E_ARG,
             "q3h_stack_create: act_q8 needs Q8_0 weights");
     require(c.act_q8 == 0 ||
@@ -624,6 +633,9 @@ q3h_context *new_context(q3h_stack *s, int max_positions) {
     // keys then values in one allocation: v = k + n elements
     ctx->k = dev_alloc(2 * n * esz);
     ctx->v = static_cast<char *>(ctx->k) + n * esz;
+    // zeros: a position is finite before it is first written (the long-context
+    // attention reads rows past the context with weight 0)
+    check_hip(hipMemset(ctx->k, 0, 2 * n * esz), "zero K/V");
     ctx->dev = (CtxDev *)dev_alloc(sizeof(CtxDev));
     ctx->dev_arr = (CtxDev **)dev_alloc(sizeof(CtxDev *));
     CtxDev h{ctx->k, ctx->v, max_positions, 0};
@@ -751,6 +763,80 @@ extern "C" int q3h_context_read_kv(q3h_context *c, int layer, float *k, float *v
   });
 }
 
+extern "C" int q3h_context_time_attention(q3h_context *c, int iters, float *us_per_launch,
+                                          int64_t *bytes_per_launch) {
+  Work w;
+  hipStream_t st = nullptr;
+  std::vector<hipEvent_t> ev;  // a start and an end event per layer
+  int rc = guard([&] {
+    require(c && us_per_launch && bytes_per_launch && iters > 0, Q3H_E_ARG,
+            "q3h_context_time_attention: invalid argument");
+    q3h_stack *s = c->s;
+    const q3h_stack_config &cf = s->cfg;
+    require(!cf.act_q8, Q3H_E_ARG,
+            "q3h_context_time_attention: a stack with f32 activations is required");
+    require(c->len + 1 <= c->max_pos, Q3H_E_CAPACITY, "q3h_context_time_attention: context full");
+    check_hip(hipSetDevice(s->dev->ordinal), "hipSetDevice");
+    const int positions = c->len + 1;
+    const int NQ = cf.heads * cf.head_dim, NKV = cf.kv_heads * cf.head_dim;
+    const int ldq = NQ + 2 * NKV;
+    const bool kv16 = cf.kv_f16 != 0;
+    w.ensure(s, 1, attention_splits(s, positions), 0);
+    check_hip(hipStreamCreateWithFlags(&st, hipStreamNonBlocking), "hipStreamCreate");
+    check_hip(hipMemsetAsync(w.qkv, 0, sizeof(float) * ldq, st), "zero");
+    launch_prep(c->dev_arr, nullptr, 1, 1, w.rd, st);
+    AttnArgs at{};
+    at.qkv = w.qkv;
+    at.ldq = ldq;
+    at.rd = w.rd;
+    at.heads = cf.heads;
+    at.kvh = cf.kv_heads;
+    at.rope_cs = reinterpret_cast<const float2 *>(s->rope_cs);
+    at.out = w.att;
+    at.part = w.part;
+    ev.assign(4 * cf.layers, nullptr);
+    for (auto &e : ev) check_hip(hipEventCreate(&e), "event");
+    int kernels = 1;
+    auto pass = [&](bool timed) {
+      for (int l = 0; l < cf.layers; l++) {
+        at.layer = l;
+        at.qkn = s->layers[l].q_norm;
+        kernels = launch_attn(at, 1, positions, true, kv16, st, timed ? &ev[4 * l] : nullptr);
+      }
+    };
+    pass(false);  // warm-up
+    check_hip(hipStreamSynchronize(st), "warm-up sync");
+    double total = 0.0;
+    for (int it = 0; it < iters; it++) {
+      pass(true);
+      check_hip(hipStreamSynchronize(st), "timed sync");
+      for (int l = 0; l < cf.layers; l++) {
+        float t = 0.f;
+        // the kernels' own execution (the split merge's included)
+        for (int k = 0; k < kernels; k++) {
+          check_hip(hipEventElapsedTime(&t, ev[4 * l + 2 * k], ev[4 * l + 2 * k + 1]), "elapsed");
+          total += t;
+        }
+      }
+    }
+    check_hip(hipGetLastError(), "attention kernels");
+    *us_per_launch = (float)(total * 1000.0 / ((double)iters * cf.layers));
+    const int64_t es = kv16 ? 2 : 4;
+    // the cache read for len positions, the new key and value written, the
+    // q / k / v row read, the head outputs written
+    *bytes_per_launch = 2 * es * (int64_t)NKV * c->len + 2 * es * NKV + 4 * (int64_t)ldq +
+                        4 * (int64_t)NQ;
+  });
+  for (auto e : ev)
+    if (e) (void)hipEventDestroy(e);
+  if (st) {
+    (void)hipStreamSynchronize(st);
+    (void)hipStreamDestroy(st);
+  }
+  w.release();
+  return rc;
+}
+
 // ---------------------------------------------------------------------------
 // forward
 
@@ -770,14 +856,14 @@ extern "C" int q3h_forward_embeds(q3h_context *c, const float *x, int rows, int 
     check_hip(hipSetDevice(s->dev->ordinal), "hipSetDevice");
     const int H = cf.hidden;
     const int head_rows = head >= 0 ? s->heads[head].N : 0;
-    const int splits = attention_splits(c->len + rows);
+    const int positions = c->len + rows;
     Work &w = c->w;
-    w.ensure(s, rows, splits, head_rows);
+    w.ensure(s, rows, attention_splits(s, positions), head_rows);
     hipStream_t st = c->stream;
     check_hip(hipMemcpyAsync(w.h, x, sizeof(float) * rows * H, hipMemcpyHostToDevice, st),
               "upload x");
     launch_prep(c->dev_arr, nullptr, 1, rows, w.rd, st);
-    run_layers(s, w, rows, splits, rows == 1, st);
+    run_layers(s, w, rows, positions, rows == 1, st);
     // final norm of the last row, fused into the head product when there is one
     if (head >= 0) {
       linear(s, w, s->heads[head], w.h + (size_t)(rows - 1) * H, H, 1, s->final_norm, w.logits,
@@ -832,9 +918,8 @@ extern "C" int q3h_forward_embeds_batch(q3h_context *const *ctxs, int n, const f
     check_hip(hipSetDevice(s->dev->ordinal), "hipSetDevice");
     for (int i = 1; i < n; i++) check_hip(hipStreamSynchronize(ctxs[i]->stream), "batch sync");
     const int H = cf.hidden;
-    const int splits = attention_splits(maxlen);
     Work &w = c0->w;
-    w.ensure(s, n, splits, head_rows);
+    w.ensure(s, n, attention_splits(s, maxlen), head_rows);
     hipStream_t st = c0->stream;
     std::vector<CtxDev *> arr(n);
     for (int i = 0; i < n; i++) arr[i] = ctxs[i]->dev;
@@ -844,7 +929,7 @@ extern "C" int q3h_forward_embeds_batch(q3h_context *const *ctxs, int n, const f
     check_hip(hipMemcpyAsync(w.h, x, sizeof(float) * n * H, hipMemcpyHostToDevice, st),
               "upload x");
     launch_prep(w.ctx_arr, nullptr, n, 1, w.rd, st);
-    run_layers(s, w, n, splits, true, st);
+    run_layers(s, w, n, maxlen, true, st);
     launch_rmsnorm_rows(w.h, H, n, H, s->final_norm, cf.rms_eps, w.normed, H, st);
     if (heads) {
       bool same = true;

@@ -72,7 +72,6 @@ struct Work {
   float *logits = nullptr;  // [rows][head rows]
   RowDesc *rd = nullptr;    // [rows]
   float *part = nullptr;    // attention partials [rows][heads][splits][head_dim + 2]
-  int *tickets = nullptr;   // attention split tickets [rows][heads], zero
   CtxDev **ctx_arr = nullptr;
   QAct xa, xb;              // quantized activations (act_q8 stacks)
   float *gpart = nullptr;   // chunk partials of the int8 products (act_q8)
@@ -80,7 +79,10 @@ struct Work {
   void release();
 };
 
-int attention_splits(int positions);
+// attention splits (the partial buffer) for contexts of up to `positions`
+int attention_splits(const struct ::q3h_stack *s, int positions);
+// the most splits of any context of up to `positions` positions
+int attention_splits_upto(const struct ::q3h_stack *s, int positions);
 // y [M][ldy] (+)= W . x (x RMS-normed with norm_w when non-null; epi: EPI_*):
 // the f32-activation GEMV, or for act_q8 stacks the quantizer and the int8
 // product; xn_out, when non-null, receives the (normed) row M - 1
@@ -106,8 +108,10 @@ struct LayerIO {
 // whether run_layers takes the int8 partial-product path for M rows of stack s
 bool partial_path(const struct ::q3h_stack *s, int M);
 
-// fused: every row is the single new position of its own context
-void run_layers(const struct ::q3h_stack *s, Work &w, int M, int splits, bool fused,
+// fused: every row is the single new position of its own context; positions:
+// the most positions any row attends to (its own included), Work sized for
+// attention_splits(s, positions)
+void run_layers(const struct ::q3h_stack *s, Work &w, int M, int positions, bool fused,
                 hipStream_t st, const LayerIO &io = LayerIO{});
 
 }  // namespace q3h

@@ -1,14 +1,14 @@
 // q3h_attn.hip - GQA decode attention of the Qwen3 stacks on gfx950.
 //
-// One workgroup of 512 threads per (query head h, row m, split s); a split is
-// up to 256 consecutive positions (one split for the contexts of the frame
-// step). Query head h reads the keys and values of kv head h / GRP. The
-// kernel is short and latency-bound, so it is laid out to issue every load of
-// the split at once and to keep the per-CU instruction count low:
+// Contexts of up to 256 positions (the frame step): k_attn, one workgroup of
+// 512 threads per (query head h, row m). Query head h reads the keys and
+// values of kv head h / GRP. The kernel is short and latency-bound, so it is
+// laid out to issue every load at once and to keep the per-CU instruction
+// count low:
 //   - keys: 2 lanes per position (64 dims each), each lane loads its half
 //     row; the score is a 64-term dot + one DPP add;
 //   - values: lane (dg, kg) = (t % 32, t / 32) holds dims 4dg..4dg+3 of
-//     positions p0 + kg + 16 i; its 16 float4 loads are issued with the keys;
+//     positions kg + 16 i; its 16 float4 loads are issued with the keys;
 //   - softmax in two passes over the block (max, then sum), no rescaling;
 //   - outputs: 16 partial sums per dim merged in LDS.
 // Fused prologue (FUSED: each row is the one new position of its own context):
@@ -18,9 +18,9 @@
 // pos is read from LDS (other positions from the cache, written by earlier
 // launches). Rows that add several positions of one context at once
 // (prefill) run the separate append kernel first and this kernel unfused.
-// Splits (contexts beyond 256 positions): each workgroup leaves (max, sum,
-// unnormalized output) in the partial buffer and takes a ticket; the last
-// workgroup of (m, h) merges the splits in split order and clears the ticket.
+// Longer contexts: k_attn_split (below), splits of 64-256 positions merged
+// by the last workgroup of each kv head.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include "q3h_internal.h"
@@ -80,7 +80,7 @@ __device__ __forceinline__ void norm_rope(float &x0, float &x1, float w0, float 
 }
 
 __device__ __forceinline__ float rescale(float m, float mn) {
-  return m == -INFINITY ? 0.f : expf(m - mn);
+  return m == -INFINITY ? 0.f : __expf(m - mn);
 }
 
 // Plain scalar arguments, those of the prologue first (the first 14 argument
@@ -91,16 +91,14 @@ __global__ __launch_bounds__(NT) void k_attn(const RowDesc *__restrict__ rd,
                                              const float *__restrict__ qkv,
                                              const float2 *__restrict__ rope_cs,
                                              const float *__restrict__ qkn,
-                                             float *__restrict__ outp, int layer, int kvh, int S,
-                                             float *__restrict__ part, int *__restrict__ tickets) {
+                                             float *__restrict__ outp, int layer, int kvh) {
   __shared__ float qs[HD];
   __shared__ float kvn[2][HD];  // the new key and value, as the cache holds them
   __shared__ float red[NW];
   __shared__ float pr[kSplit];
   __shared__ float po[KG][HD];
-  __shared__ int last;
   const int heads = GRP * kvh, ldq = (heads + 2 * kvh) * HD;
-  const int h = blockIdx.x, m = blockIdx.y, s = blockIdx.z, g = h / GRP;
+  const int h = blockIdx.x, m = blockIdx.y, g = h / GRP;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const float *row = qkv + (size_t)m * ldq;
 
@@ -114,11 +112,11 @@ __global__ __launch_bounds__(NT) void k_attn(const RowDesc *__restrict__ rd,
   const RowDesc d = rd[m];
   float *out = outp + ((size_t)m * heads + h) * HD;
   if (d.pos < 0) {  // inactive row: zeros, no ticket
-    if (s == 0 && t < HD) out[t] = 0.f;
+    if (t < HD) out[t] = 0.f;
     return;
   }
   const int n = d.pos + 1;
-  const int p0 = s * kSplit, p1 = min(n, p0 + kSplit);
+  const int p0 = 0, p1 = min(n, kSplit);
   const size_t head_off = ((size_t)layer * kvh + g) * d.max_pos * HD;
   KV *kc = reinterpret_cast<KV *>(d.k) + head_off;
   KV *vc = reinterpret_cast<KV *>(d.v) + head_off;
@@ -156,8 +154,8 @@ __global__ __launch_bounds__(NT) void k_attn(const RowDesc *__restrict__ rd,
       const KV y0 = (KV)x0, y1 = (KV)x1;
       kvn[wave - 1][lane] = (float)y0;
       kvn[wave - 1][lane + 64] = (float)y1;
-      // the group's first query head appends, in the split holding pos
-      if (h % GRP == 0 && d.pos >= p0 && d.pos < p0 + kSplit) {
+      // the group's first query head appends
+      if (h % GRP == 0) {
         KV *dst = (wave == 1 ? kc : vc) + (size_t)d.pos * HD;
         dst[lane] = y0;
         dst[lane + 64] = y1;
@@ -230,80 +228,448 @@ __global__ __launch_bounds__(NT) void k_attn(const RowDesc *__restrict__ rd,
     float acc = 0.f;
 #pragma unroll
     for (int i = 0; i < KG; i++) acc += po[i][t];
-    if (S == 1) {
-      out[t] = sum > 0.f ? acc / sum : 0.f;
-    } else {
-      float *pp = part + (((size_t)m * heads + h) * S + s) * (HD + 2);
-      pp[t] = acc;
-      if (t == 0) {
-        pp[HD] = sum > 0.f ? mx : -INFINITY;
-        pp[HD + 1] = sum;
+    out[t] = sum > 0.f ? acc / sum : 0.f;
+  }
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// a 16-byte load from device memory through a global-address-space pointer
+// (global_load, not flat_load: the cache pointers come from row descriptors
+// in memory, which the compiler cannot place in an address space itself)
+__device__ __forceinline__ u32x4 gload16(const void *p) {
+  return *reinterpret_cast<const __attribute__((address_space(1))) u32x4 *>(
+      reinterpret_cast<uintptr_t>(p));
+}
+
+// 8 cache elements (one 16-byte load of f16, two of f32) as f32
+__device__ __forceinline__ void cvt8(const u32x4 (&r)[1], float (&o)[8]) {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  const h8 v = __builtin_bit_cast(h8, r[0]);
+#pragma unroll
+  for (int e = 0; e < 8; e++) o[e] = (float)v[e];
+}
+
+__device__ __forceinline__ void cvt8(const u32x4 (&r)[2], float (&o)[8]) {
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) o[4 * i + e] = __uint_as_float(r[i][e]);
+}
+
+constexpr int kMaxSplitsLong = 256;
+
+// Long contexts (more than 256 positions): k_attn_split, one workgroup of NT
+// threads per (kv head g, split s, row m) for all GRP query heads of g, so
+// that every key and value of the cache is read once per step, then
+// k_attn_merge. A split is P positions, and P grows with the context so that
+// a step launches a few hundred workgroups and the merge stays short.
+// The context is cut into blocks of NT / 16 consecutive positions dealt out
+// to the S splits in turn (block b to split b % S): at any moment the
+// workgroups of a kv head read one contiguous stretch of the cache. Thread t
+// owns dims 8 (t % 16) .. + 7 of position t / 16 of each of its blocks: one
+// load instruction of a wave reads 4 whole consecutive rows, and a
+// position's key and value sit in the same lanes, so its softmax weights
+// never leave the registers.
+//   - the split covers the positions before pos (FUSED: the new position
+//     pos is added by the merge) or up to pos (rows whose K/V were appended
+//     beforehand); every key and value is loaded before the prologue, at
+//     positions clamped into the covered range (a context's cache starts as
+//     zeros, so a row read there is finite, and its weight is 0);
+//   - prologue (FUSED): waves take the GRP query heads, and in split 0 the
+//     new key and value of the row (RMSNorm with q_norm / k_norm, RoPE);
+//     split 0 appends the key and value to the cache and leaves the normed
+//     query heads in the partial buffer for the merge;
+//   - scores: an 8-term chain per lane, summed over the 16 lanes of a DPP
+//     row, one DPP stage at a time over all of the thread's sums;
+//   - softmax per query head over the split (maximum, exp, sum);
+//   - values: 8 dims x GRP heads of partial outputs per lane, summed over the
+//     position groups of a wave (lane shuffles), then over the waves in LDS;
+//   - (max, sum, unnormalized output) per query head and split go to the
+//     partial buffer [M][heads][S + 1][HD + 2] (slot S: the query head).
+// The kernel boundary makes the partials of every workgroup visible to the
+// merge (a device-scope fence and ticket per workgroup, the alternative, was
+// measured here at 10-30 us per launch on long contexts).
+template <typename KV, bool FUSED, int GRP, int P, int NTL>
+__global__ __launch_bounds__(NTL) void k_attn_split(const RowDesc *__restrict__ rd,
+                                                    const float *__restrict__ qkv,
+                                                    const float2 *__restrict__ rope_cs,
+                                                    const float *__restrict__ qkn, int layer,
+                                                    int kvh, int S, float *__restrict__ part) {
+  constexpr int PG = NTL / 16;        // position groups
+  constexpr int NJ = P / PG;          // positions per thread
+  constexpr int LW = sizeof(KV) / 2;  // 16-byte loads per 8 elements
+  constexpr int NWV = NTL / 64;
+  constexpr int IT = GRP + 2, RND = (IT + NWV - 1) / NWV;  // prologue items, rounds
+  static_assert(NJ * PG == P, "split size");
+  __shared__ float qs[GRP][HD];
+  __shared__ float red[2][GRP][NWV];
+  __shared__ float po[NWV][GRP][HD];
+  const int g = blockIdx.x, s = blockIdx.y, m = blockIdx.z;
+  const int heads = GRP * kvh, ldq = (heads + 2 * kvh) * HD;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int r16 = t & 15, pg = t >> 4;
+  const float *row = qkv + (size_t)m * ldq;
+  // loads in the order of their use: the prologue's (the q / k / v row needs
+  // no descriptor), the keys, the values
+  float x0[RND], x1[RND];
+  float wq0 = 1.f, wq1 = 1.f, wk0 = 1.f, wk1 = 1.f, eps = 0.f;
+  if (FUSED) {
+#pragma unroll
+    for (int r = 0; r < RND; r++) {
+      const int it = min(wave + NWV * r, IT - 1);
+      const int col = it < GRP ? (g * GRP + it) * HD : (heads + (it - GRP) * kvh + g) * HD;
+      x0[r] = row[col + lane];
+      x1[r] = row[col + lane + 64];
+    }
+    wq0 = qkn[lane];
+    wq1 = qkn[lane + 64];
+    wk0 = qkn[HD + lane];
+    wk1 = qkn[HD + lane + 64];
+    eps = qkn[2 * HD];
+  }
+  const RowDesc d = rd[m];
+  if (d.pos < 0) return;  // inactive row (the merge writes its zeros)
+  const int pos = d.pos;
+  const int n = FUSED ? pos : pos + 1;  // positions covered here
+  const int last = max(n - 1, 0);
+  const size_t head_off = ((size_t)layer * kvh + g) * d.max_pos * HD;
+  KV *kc = reinterpret_cast<KV *>(d.k) + head_off;
+  KV *vc = reinterpret_cast<KV *>(d.v) + head_off;
+  // block j of this split: positions (j S + s) PG .. + PG - 1
+  auto position = [&](int j) { return (j * S + s) * PG + pg; };
+  const float2 cs = FUSED ? rope_cs[(size_t)pos * (HD / 2) + lane] : make_float2(1.f, 0.f);
+
+  u32x4 kr[NJ][LW], vr[NJ][LW];
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    const KV *p = kc + (size_t)min(position(j), last) * HD + 8 * r16;
+#pragma unroll
+    for (int e = 0; e < LW; e++) kr[j][e] = gload16(p + e * 4);
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    const KV *p = vc + (size_t)min(position(j), last) * HD + 8 * r16;
+#pragma unroll
+    for (int e = 0; e < LW; e++) vr[j][e] = gload16(p + e * 4);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  const size_t slot = (HD + 2);
+  float *pm = part + ((size_t)m * heads + g * GRP) * (S + 1) * slot;  // head h at h (S + 1) slot
+  if (FUSED) {
+#pragma unroll
+    for (int r = 0; r < RND; r++) {
+      const int it = wave + NWV * r;
+      if (it < GRP) {
+        norm_rope(x0[r], x1[r], wq0, wq1, cs, eps);
+        qs[it][lane] = x0[r];
+        qs[it][lane + 64] = x1[r];
+        if (s == 0) {
+          float *qo = pm + ((size_t)it * (S + 1) + S) * slot;
+          qo[lane] = x0[r];
+          qo[lane + 64] = x1[r];
+        }
+      } else if (it < IT && s == 0) {
+        if (it == GRP) norm_rope(x0[r], x1[r], wk0, wk1, cs, eps);
+        KV *dst = (it == GRP ? kc : vc) + (size_t)pos * HD;
+        dst[lane] = (KV)x0[r];
+        dst[lane + 64] = (KV)x1[r];
       }
     }
+  } else {
+    for (int i = t; i < GRP * HD; i += NTL) qs[i / HD][i % HD] = row[(size_t)g * GRP * HD + i];
   }
-  if (S == 1) return;
+  __syncthreads();
 
-  // splits: the last workgroup of (m, h) merges them
-  __threadfence();
-  __syncthreads();
-  if (t == 0) {
-    int *ticket = tickets + (size_t)m * heads + h;
-    const int old = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    last = old == S - 1;
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  if (t < HD) {
-    const float *pp = part + ((size_t)m * heads + h) * S * (HD + 2);
-    float mn = -INFINITY;
-    for (int i = 0; i < S; i++) mn = fmaxf(mn, pp[i * (HD + 2) + HD]);
-    float l = 0.f, acc = 0.f;
-    for (int i = 0; i < S; i++) {
-      const float c = rescale(pp[i * (HD + 2) + HD], mn);
-      l += pp[i * (HD + 2) + HD + 1] * c;
-      acc += pp[i * (HD + 2) + t] * c;
+  // scores
+  const float scale = (float)(1.0 / sqrt((double)HD));
+  float q[GRP][8];
+#pragma unroll
+  for (int h = 0; h < GRP; h++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) q[h][e] = qs[h][8 * r16 + e];
+  float sc[GRP][NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    float k8[8];
+    cvt8(kr[j], k8);
+#pragma unroll
+    for (int h = 0; h < GRP; h++) {
+      float a = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) a = fmaf(q[h][e], k8[e], a);
+      sc[h][j] = a;
     }
-    out[t] = l > 0.f ? acc / l : 0.f;
   }
-  if (t == 0) tickets[(size_t)m * heads + h] = 0;
+#pragma unroll
+  for (int h = 0; h < GRP; h++)
+#pragma unroll
+    for (int j = 0; j < NJ; j++) sc[h][j] += dpp_f<kQuadXor1>(sc[h][j]);
+#pragma unroll
+  for (int h = 0; h < GRP; h++)
+#pragma unroll
+    for (int j = 0; j < NJ; j++) sc[h][j] += dpp_f<kQuadXor2>(sc[h][j]);
+#pragma unroll
+  for (int h = 0; h < GRP; h++)
+#pragma unroll
+    for (int j = 0; j < NJ; j++) sc[h][j] += dpp_f<kHalfMirror>(sc[h][j]);
+#pragma unroll
+  for (int h = 0; h < GRP; h++)
+#pragma unroll
+    for (int j = 0; j < NJ; j++) sc[h][j] += dpp_f<kRowMirror>(sc[h][j]);
+  // softmax over the split, per query head
+  float mx[GRP], sum[GRP];
+#pragma unroll
+  for (int h = 0; h < GRP; h++) {
+    float v = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+      sc[h][j] = position(j) < n ? sc[h][j] * scale : -INFINITY;
+      v = fmaxf(v, sc[h][j]);
+    }
+    v = wave_max_dpp(v);
+    if (lane == 0) red[0][h][wave] = v;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < GRP; h++) {
+    float v = red[0][h][0];
+#pragma unroll
+    for (int w = 1; w < NWV; w++) v = fmaxf(v, red[0][h][w]);
+    mx[h] = v;
+    const float ref = v == -INFINITY ? 0.f : v;  // an empty split: weights 0
+    float ls = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+      sc[h][j] = __expf(sc[h][j] - ref);
+      ls += sc[h][j];
+    }
+    ls = wave_sum_dpp(r16 == 0 ? ls : 0.f);
+    if (lane == 0) red[1][h][wave] = ls;
+  }
+  // values
+  float o[GRP][8];
+#pragma unroll
+  for (int h = 0; h < GRP; h++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) o[h][e] = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    float v8[8];
+    cvt8(vr[j], v8);
+#pragma unroll
+    for (int h = 0; h < GRP; h++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) o[h][e] = fmaf(sc[h][j], v8[e], o[h][e]);
+  }
+  // the 4 position groups of a wave (lanes l, l + 16, l + 32, l + 48), then
+  // the waves through LDS
+#pragma unroll
+  for (int h = 0; h < GRP; h++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      o[h][e] += __shfl_xor(o[h][e], 16);
+      o[h][e] += __shfl_xor(o[h][e], 32);
+    }
+  if (lane < 16) {
+#pragma unroll
+    for (int h = 0; h < GRP; h++) {
+      float4 *dst = reinterpret_cast<float4 *>(&po[wave][h][8 * r16]);
+      dst[0] = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
+      dst[1] = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < GRP; h++) {
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWV; w++) v += red[1][h][w];
+    sum[h] = v;
+  }
+  for (int i = t; i < GRP * HD; i += NTL) {
+    const int h = i / HD, dd = i % HD;
+    float acc = 0.f;
+#pragma unroll
+    for (int u = 0; u < NWV; u++) acc += po[u][h][dd];
+    float *pp = pm + ((size_t)h * (S + 1) + s) * slot;
+    pp[dd] = acc;
+    if (dd == 0) {
+      pp[HD] = sum[h] > 0.f ? mx[h] : -INFINITY;
+      pp[HD + 1] = sum[h];
+    }
+  }
+}
+
+// The splits of (kv head g, row m) merged, with the new position of a fused
+// row: out = sum_s c_s acc_s / sum_s c_s sum_s, c_s = exp(max_s - max).
+// 1024 threads: thread (q, h, d) adds the splits q, q + Q, ... (Q = 1024 /
+// (GRP * 128)) for dim d of query head h, 16 loads at a time; the maxima
+// and the c_s are computed once per (head, split) in LDS; the Q partial sums
+// meet in LDS. The new position (FUSED): its key and value from the cache
+// (appended by split 0), the query head from slot S; its score is the
+// 128-dim dot of the two (wave sums), its weight exp(score - max).
+template <typename KV, bool FUSED, int GRP>
+__global__ __launch_bounds__(1024) void k_attn_merge(const RowDesc *__restrict__ rd,
+                                                     const float *__restrict__ part,
+                                                     float *__restrict__ outp, int layer, int kvh,
+                                                     int S) {
+  constexpr int NO = GRP * HD, Q = 1024 / NO, U = 16;
+  __shared__ float cw[GRP][kMaxSplitsLong], cl[GRP][kMaxSplitsLong];
+  __shared__ float red[Q][NO];
+  __shared__ float qk[GRP][2], mxs[GRP], den[GRP];
+  const int g = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
+  const int q = t / NO, o = t % NO, h = o / HD, dd = o % HD;
+  const int lane = t & 63, wave = t >> 6;
+  const int heads = GRP * kvh;
+  const size_t slot = HD + 2;
+  const float *pm = part + ((size_t)m * heads + g * GRP) * (S + 1) * slot;
+  const float *ph = pm + (size_t)h * (S + 1) * slot + dd;
+  float *out = outp + ((size_t)m * heads + g * GRP) * HD;
+  // the first U splits of this thread, issued with the maxima and sums
+  float a[U];
+#pragma unroll
+  for (int u = 0; u < U; u++) a[u] = ph[(size_t)min(q + Q * u, S - 1) * slot];
+  float qv = 0.f;
+  if (FUSED) qv = ph[(size_t)S * slot];
+  for (int i = t; i < GRP * S; i += 1024) {
+    const float *pp = pm + ((size_t)(i / S) * (S + 1) + i % S) * slot;
+    cw[i / S][i % S] = pp[HD];
+    cl[i / S][i % S] = pp[HD + 1];
+  }
+  const RowDesc d = rd[m];
+  if (d.pos < 0) {  // inactive row: zeros
+    if (q == 0) out[o] = 0.f;
+    return;
+  }
+  float kn = 0.f, vn = 0.f;
+  if (FUSED) {
+    const size_t off = (((size_t)layer * kvh + g) * d.max_pos + d.pos) * HD + dd;
+    kn = (float)reinterpret_cast<const KV *>(d.k)[off];
+    vn = (float)reinterpret_cast<const KV *>(d.v)[off];
+    // threads of group q = 0: head h's dims in waves 2h and 2h + 1
+    const float v = wave_sum_dpp(qv * kn);
+    if (q == 0 && lane == 0) qk[h][dd >> 6] = v;
+  }
+  __syncthreads();
+  const float scale = (float)(1.0 / sqrt((double)HD));
+  // wave hh < GRP: the maximum of head hh over its splits and the new position
+  if (wave < GRP) {
+    float v = FUSED ? (qk[wave][0] + qk[wave][1]) * scale : -INFINITY;
+    for (int i = lane; i < S; i += 64) v = fmaxf(v, cw[wave][i]);
+    v = wave_max_dpp(v);
+    if (lane == 0) mxs[wave] = v;
+  }
+  __syncthreads();
+  for (int i = t; i < GRP * S; i += 1024) {
+    const int hh = i / S, k = i % S;
+    cw[hh][k] = rescale(cw[hh][k], mxs[hh]);
+  }
+  __syncthreads();
+  if (wave < GRP) {
+    float v = 0.f;
+    for (int i = lane; i < S; i += 64) v = fmaf(cl[wave][i], cw[wave][i], v);
+    v = wave_sum_dpp(v);
+    if (lane == 0) den[wave] = v;
+  }
+  float acc = 0.f;
+  for (int k0 = 0;; k0 += U) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int sp = q + Q * (k0 + u);
+      acc = sp < S ? fmaf(a[u], cw[h][min(sp, S - 1)], acc) : acc;
+    }
+    if (q + Q * (k0 + U) >= S) break;
+#pragma unroll
+    for (int u = 0; u < U; u++) a[u] = ph[(size_t)min(q + Q * (k0 + U + u), S - 1) * slot];
+  }
+  red[q][o] = acc;
+  __syncthreads();
+  if (q == 0) {
+#pragma unroll
+    for (int i = 1; i < Q; i++) acc += red[i][o];
+    float l = den[h];
+    if (FUSED) {
+      const float c = __expf((qk[h][0] + qk[h][1]) * scale - mxs[h]);
+      l += c;
+      acc = fmaf(c, vn, acc);
+    }
+    out[o] = l > 0.f ? acc / l : 0.f;
+  }
+}
+
+#define Q3H_LAUNCH(KERNEL, GRID, BLOCK, ST, EV0, EV1, ...)                                      \
+  do {                                                                                          \
+    if (EV0)                                                                                    \
+      hipExtLaunchKernelGGL(KERNEL, GRID, BLOCK, 0, ST, EV0, EV1, 0, __VA_ARGS__);              \
+    else                                                                                        \
+      hipLaunchKernelGGL(KERNEL, GRID, BLOCK, 0, ST, __VA_ARGS__);                              \
+  } while (0)
+
+template <typename KV, bool FUSED, int G>
+int launch_g(const AttnArgs &a, int M, int positions, hipStream_t st, const hipEvent_t *ev) {
+  const hipEvent_t ev0 = ev ? ev[0] : nullptr, ev1 = ev ? ev[1] : nullptr;
+  const SplitShape sh = attn_split_shape(positions, sizeof(KV) == 2);
+  const int S = (positions + sh.len - 1) / sh.len;
+#define Q3H_S(P, T)                                                                           \
+  Q3H_LAUNCH((k_attn_split<KV, FUSED, G, P, T>), dim3(a.kvh, S, M), dim3(T), st, ev0, ev1,      \
+             a.rd, a.qkv, a.rope_cs, a.qkn, a.layer, a.kvh, S, a.part)
+  if (sh.len == kSplit && sh.threads == 0) {
+    Q3H_LAUNCH((k_attn<KV, FUSED, G>), dim3(a.heads, M), dim3(NT), st, ev0, ev1, a.rd, a.qkv,
+               a.rope_cs, a.qkn, a.out, a.layer, a.kvh);
+  } else if (sh.len == 64) {
+    Q3H_S(64, 256);
+  } else if constexpr (sizeof(KV) == 2) {
+    if (sh.len == 128)
+      Q3H_S(128, 256);
+    else
+      Q3H_S(256, 512);
+  } else {
+    Q3H_S(128, 512);
+  }
+#undef Q3H_S
+  if (sh.threads == 0) return 1;
+  Q3H_LAUNCH((k_attn_merge<KV, FUSED, G>), dim3(a.kvh, M), dim3(1024), st, ev ? ev[2] : nullptr,
+             ev ? ev[3] : nullptr, a.rd, a.part, a.out, a.layer, a.kvh, S);
+  return 2;
 }
 
 template <typename KV, bool FUSED>
-void launch_grp(const AttnArgs &a, int grp, dim3 grid, hipStream_t st) {
-#define Q3H_A(G)                                                                               \
-  hipLaunchKernelGGL((k_attn<KV, FUSED, G>), grid, dim3(NT), 0, st, a.rd, a.qkv, a.rope_cs,     \
-                     a.qkn, a.out, a.layer, a.kvh, (int)grid.z, a.part, a.tickets)
-  if (grp == 1)
-    Q3H_A(1);
-  else if (grp == 2)
-    Q3H_A(2);
-  else
-    Q3H_A(4);
-#undef Q3H_A
+int launch_kv(const AttnArgs &a, int M, int positions, hipStream_t st, const hipEvent_t *ev) {
+  const int grp = a.heads / a.kvh;
+  if (grp == 1) return launch_g<KV, FUSED, 1>(a, M, positions, st, ev);
+  if (grp == 2) return launch_g<KV, FUSED, 2>(a, M, positions, st, ev);
+  return launch_g<KV, FUSED, 4>(a, M, positions, st, ev);
 }
 
 }  // namespace
 
-int attn_splits(int positions) {
-  const int n = (positions + kSplit - 1) / kSplit;
-  return n < 1 ? 1 : n;
+SplitShape attn_split_shape(int positions, bool kv16) {
+  if (positions <= kSplit) return {kSplit, 0};  // one workgroup per query head
+  if (positions <= 2048) return {64, 256};
+  if (kv16) return positions <= 4096 ? SplitShape{128, 256} : SplitShape{256, 512};
+  return {128, 512};
 }
 
-void launch_attn(const AttnArgs &a, int M, int splits, bool fused, bool kv16, hipStream_t st) {
-  const int grp = a.heads / a.kvh;
-  const dim3 grid(a.heads, M, splits);
-  if (kv16) {
-    if (fused)
-      launch_grp<_Float16, true>(a, grp, grid, st);
-    else
-      launch_grp<_Float16, false>(a, grp, grid, st);
-  } else {
-    if (fused)
-      launch_grp<float, true>(a, grp, grid, st);
-    else
-      launch_grp<float, false>(a, grp, grid, st);
-  }
+int attn_splits(int positions, bool kv16) {
+  if (positions < 1) return 1;
+  const SplitShape sh = attn_split_shape(positions, kv16);
+  // the split kernel's partial slots: one per split and one for the query head
+  return sh.threads == 0 ? 1 : (positions + sh.len - 1) / sh.len + 1;
+}
+
+int attn_max_positions(bool kv16) {
+  return kMaxSplitsLong * attn_split_shape(1 << 30, kv16).len;
+}
+
+int launch_attn(const AttnArgs &a, int M, int positions, bool fused, bool kv16, hipStream_t st,
+                const hipEvent_t *ev) {
+  if (kv16)
+    return fused ? launch_kv<_Float16, true>(a, M, positions, st, ev)
+                 : launch_kv<_Float16, false>(a, M, positions, st, ev);
+  return fused ? launch_kv<float, true>(a, M, positions, st, ev)
+               : launch_kv<float, false>(a, M, positions, st, ev);
 }
 
 }  // namespace q3h

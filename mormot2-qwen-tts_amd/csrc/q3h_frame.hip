@@ -299,7 +299,7 @@ struct q3h_frame {
   hipStream_t stream = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
-  int graph_splits = 0;
+  int graph_positions = 0;  // attention positions the captured graph covers
   int32_t *pinned = nullptr;  // [n][groups] codes + [n] alive
   std::vector<void *> allocs;
 };
@@ -332,7 +332,7 @@ T *falloc(q3h_frame *f, size_t n) {
 }
 
 // The step's kernel sequence on stream st (captured into the graph).
-void enqueue_step(q3h_frame *f, int splits, hipStream_t st) {
+void enqueue_step(q3h_frame *f, int positions, hipStream_t st) {
   const q3h_frame_config &c = f->cfg;
   const int n = c.n_streams, H = f->H;
   q3h_stack *cp = f->cp, *tk = f->talker;
@@ -352,7 +352,7 @@ void enqueue_step(q3h_frame *f, int splits, hipStream_t st) {
       LayerIO io;
       io.input_quantized = true;
       io.final_norm = cp->final_norm;
-      run_layers(cp, f->cw, n * R, 1, R == 1, st, io);
+      run_layers(cp, f->cw, n * R, c.groups, R == 1, st, io);
       launch_gemm_i8_partial(cp->heads[c.cp_heads[g]], f->cw.xa, n * R, f->cw.gpart, st);
       hipLaunchKernelGGL(k_cp_next, dim3(n), dim3(kArgBlock), 0, st, fd, g);
       continue;
@@ -361,7 +361,7 @@ void enqueue_step(q3h_frame *f, int splits, hipStream_t st) {
       run_cp_fused(cp, f->cw, f->cctx[0], g + 1, st);
     } else {
       launch_prep(f->c_arr, fd.alive, n, R, f->cw.rd, st);
-      run_layers(cp, f->cw, n * R, 1, R == 1, st);
+      run_layers(cp, f->cw, n * R, c.groups, R == 1, st);
       launch_advance(f->c_arr, fd.alive, n, R, st);
     }
     // final norm of each stream's last row + head g, one launch
@@ -375,11 +375,11 @@ void enqueue_step(q3h_frame *f, int splits, hipStream_t st) {
     hipLaunchKernelGGL(k_talker_input_q, dim3(n), dim3(kArgBlock), 0, st, fd);
     LayerIO io;
     io.input_quantized = true;
-    run_layers(tk, f->tw, n, splits, true, st, io);
+    run_layers(tk, f->tw, n, positions, true, st, io);
   } else {
     hipLaunchKernelGGL(k_talker_input, dim3((H + 255) / 256, n), dim3(256), 0, st, fd);
     launch_prep(f->t_arr, fd.alive, n, 1, f->tw.rd, st);
-    run_layers(tk, f->tw, n, splits, true, st);
+    run_layers(tk, f->tw, n, positions, true, st);
   }
   const Mat &th = tk->heads[c.talker_head];
   if (n == 1) {  // final norm fused into the head, the normed state written alongside
@@ -449,7 +449,7 @@ extern "C" int q3h_frame_create(q3h_stack *talker, q3h_stack *cp, const q3h_fram
               "frame init");
     check_hip(hipMemcpy(f->c_arr, ca.data(), sizeof(CtxDev *) * n, hipMemcpyHostToDevice),
               "frame init");
-    f->tw.ensure(talker, n, attention_splits(c.max_positions), c.vocab);
+    f->tw.ensure(talker, n, attention_splits_upto(talker, c.max_positions), c.vocab);
     f->cw.ensure(cp, 2 * n, 1, c.cp_vocab);
     f->codec_emb = falloc<float>(f, (size_t)c.vocab * H);
     check_hip(hipMemcpy(f->codec_emb, codec_emb, sizeof(float) * c.vocab * H,
@@ -537,15 +537,14 @@ extern "C" int q3h_frame_start(q3h_frame *f, int stream, const float *prefill, i
     // the prefill through the single-context path, outputs kept on the device
     const int H = f->H;
     q3h_stack *s = f->talker;
-    const int splits = attention_splits(rows);
     Work &w = tc->w;
-    w.ensure(s, rows, splits, c.vocab);
+    w.ensure(s, rows, attention_splits(s, rows), c.vocab);
     hipStream_t st = tc->stream;
     FrameDev &d = f->fd;
     check_hip(hipMemcpyAsync(w.h, prefill, sizeof(float) * rows * H, hipMemcpyHostToDevice, st),
               "upload prefill");
     launch_prep(tc->dev_arr, nullptr, 1, rows, w.rd, st);
-    run_layers(s, w, rows, splits, rows == 1, st);
+    run_layers(s, w, rows, rows, rows == 1, st);
     float *past = d.past + (size_t)stream * H;
     linear(s, w, s->heads[c.talker_head], w.h + (size_t)(rows - 1) * H, H, 1, s->final_norm,
            d.logits + (size_t)stream * c.vocab, c.vocab, EPI_STORE, past, st);
@@ -586,9 +585,8 @@ extern "C" int q3h_frame_step(q3h_frame *f, int32_t *codes, int32_t *alive) {
     }
     require(any, Q3H_E_STATE, "q3h_frame_step: no stream was started");
     check_hip(hipSetDevice(f->talker->dev->ordinal), "hipSetDevice");
-    const int splits = attention_splits(maxlen);
     if (c.use_graph) {
-      if (!f->exec || splits > f->graph_splits) {
+      if (!f->exec || maxlen > f->graph_positions) {
         if (f->exec) {
           (void)hipGraphExecDestroy(f->exec);
           f->exec = nullptr;
@@ -597,19 +595,23 @@ extern "C" int q3h_frame_step(q3h_frame *f, int32_t *codes, int32_t *alive) {
           (void)hipGraphDestroy(f->graph);
           f->graph = nullptr;
         }
-        // capture with some headroom so that the graph is rebuilt rarely
-        const int cap_splits = std::min(attention_splits(c.max_positions), splits + 1);
+        // capture with headroom so that the graph is rebuilt rarely: the
+        // attention covers up to 256 positions in one split, beyond that up
+        // to 256 positions more than the longest context (rows shorter than
+        // the capture leave their extra splits empty)
+        const int cap = maxlen <= 256 ? 256 : ((maxlen + 255) / 256 + 1) * 256;
+        const int cap_positions = std::min(c.max_positions, cap);
         check_hip(hipStreamBeginCapture(f->stream, hipStreamCaptureModeThreadLocal),
                   "hipStreamBeginCapture");
-        enqueue_step(f, cap_splits, f->stream);
+        enqueue_step(f, cap_positions, f->stream);
         check_hip(hipStreamEndCapture(f->stream, &f->graph), "hipStreamEndCapture");
         check_hip(hipGraphInstantiate(&f->exec, f->graph, nullptr, nullptr, 0),
                   "hipGraphInstantiate");
-        f->graph_splits = cap_splits;
+        f->graph_positions = cap_positions;
       }
       check_hip(hipGraphLaunch(f->exec, f->stream), "hipGraphLaunch");
     } else {
-      enqueue_step(f, splits, f->stream);
+      enqueue_step(f, maxlen, f->stream);
       check_hip(hipGetLastError(), "frame kernels");
     }
     check_hip(hipMemcpyAsync(f->pinned, f->fd.codes, sizeof(int32_t) * n * c.groups,

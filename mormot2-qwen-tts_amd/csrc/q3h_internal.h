@@ -113,9 +113,6 @@ void launch_advance(CtxDev *const *cs, const int *alive, int n, int R, hipStream
 void launch_qk_rope_append(float *qkv, int ldq, const RowDesc *rd, int M, int layer,
                            int heads, int kvh, int hd, const float *qn, const float *kn,
                            float eps, const float *rope_cs, bool kv16, hipStream_t st);
-void launch_attention(const float *qkv, int ldq, const RowDesc *rd, int M, int layer,
-                      int heads, int kvh, int hd, int splits, int chunk, float *out,
-                      float *part, bool kv16, hipStream_t st);
 
 // decode attention (q3h_attn.hip): rows m of qkv [M][ldq] with descriptors
 // rd; fused: each row is the one new position of its own context (QK-norm,
@@ -129,11 +126,26 @@ struct AttnArgs {
   const float *qkn;  // [q_norm | k_norm | eps] of the layer
   const float2 *rope_cs;
   float *out;    // [M][heads * head_dim]
-  float *part;   // [M][heads][splits][head_dim + 2]
-  int *tickets;  // [M][heads], zero between launches
+  float *part;   // [M][heads][attn_splits slots][head_dim + 2]
 };
-int attn_splits(int positions);
-void launch_attn(const AttnArgs &a, int M, int splits, bool fused, bool kv16, hipStream_t st);
+// how the decode attention cuts contexts of up to `positions` positions: len
+// positions per split, threads per workgroup (0: one workgroup per query
+// head over at most 256 positions, no split)
+struct SplitShape {
+  int len, threads;
+};
+SplitShape attn_split_shape(int positions, bool kv16);
+// partial-buffer slots per (row, query head): the splits and the query head
+// (1 when one workgroup covers the context)
+int attn_splits(int positions, bool kv16);
+// the most positions the split kernel merges (splits per kv head are bounded)
+int attn_max_positions(bool kv16);
+// positions: the most positions any of the M rows attends to (its own
+// included). Returns the kernels launched (1, or 2 with the split merge); ev
+// (optional, measurement): 4 events, the start and end of each kernel's own
+// execution
+int launch_attn(const AttnArgs &a, int M, int positions, bool fused, bool kv16, hipStream_t st,
+                const hipEvent_t *ev = nullptr);
 
 // attention of the int8 path (q3h_attnx.hip): the rows of a (fused: each the
 // one new position of its own context, QK-norm / RoPE / K/V append in the

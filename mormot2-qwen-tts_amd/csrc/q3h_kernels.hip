@@ -1,6 +1,6 @@
 // q3h_kernels.hip - gfx950 kernels of the Qwen3 stack step (decode and small
 // multi-row forwards): fused RMSNorm + GEMV over Q8_0 or f32 weights, QK-norm
-// + RoPE + K/V append, split-K GQA attention, load-time Q8_0 conversion.
+// + RoPE + K/V append, load-time Q8_0 conversion.
 //
 // Layouts (HBM):
 //  - Q8_0 matrix [N][K]: int8 quants row-major + fp16 scales [N][K/32]. A lane
@@ -362,175 +362,6 @@ void launch_qk_rope_append(float *qkv, int ldq, const RowDesc *rd, int M, int la
   else
     hipLaunchKernelGGL(k_qk_rope_append<float>, grid, dim3(kBlock), 0, st, qkv, ldq, rd,
                        layer, heads, kvh, hd, qn, kn, eps, cs);
-}
-
-// ---------------------------------------------------------------------------
-// GQA attention over one split of positions for the q heads of one kv head:
-// K/V of the kv head are read once for its grp q heads. 8 lanes per key (16
-// dims each) for the scores, one thread per (q head, dim) for the values.
-
-constexpr int kChunk = 256;  // positions per split
-constexpr int kMaxGrp = 4;   // q heads per kv head
-constexpr int kMaxHd = 128;
-
-__device__ __forceinline__ void load16(const float *p, float *o) {
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const float4 t = reinterpret_cast<const float4 *>(p)[i];
-    o[4 * i] = t.x;
-    o[4 * i + 1] = t.y;
-    o[4 * i + 2] = t.z;
-    o[4 * i + 3] = t.w;
-  }
-}
-
-__device__ __forceinline__ void load16(const _Float16 *p, float *o) {
-  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-#pragma unroll
-  for (int i = 0; i < 2; i++) {
-    const h8 t = reinterpret_cast<const h8 *>(p)[i];
-#pragma unroll
-    for (int j = 0; j < 8; j++) o[8 * i + j] = (float)t[j];
-  }
-}
-
-template <typename KV>
-__global__ __launch_bounds__(kBlock) void k_attention(const float *qkv, int ldq,
-                                                      const RowDesc *rd, int layer,
-                                                      int heads, int kvh, int hd,
-                                                      int splits, float *out, float *part) {
-  __shared__ float qs[kMaxGrp][kMaxHd];
-  __shared__ float sc[kMaxGrp][kChunk];
-  __shared__ float mx[kMaxGrp], sum[kMaxGrp];
-  const int g = blockIdx.x, m = blockIdx.y, s = blockIdx.z, tid = threadIdx.x;
-  const int grp = heads / kvh;
-  const RowDesc d = rd[m];
-  const int n = d.pos + 1;
-  const int p0 = s * kChunk, p1 = min(n, p0 + kChunk);
-  const int ldo = heads * hd;
-  if (d.pos < 0 || p0 >= p1) {
-    // an inactive row, or an empty split
-    for (int i = tid; i < grp * hd; i += kBlock) {
-      const int hh = i / hd, dd = i % hd, h = g * grp + hh;
-      if (splits == 1) {
-        out[(size_t)m * ldo + h * hd + dd] = 0.f;
-      } else {
-        float *pp = part + (((size_t)m * heads + h) * splits + s) * (hd + 2);
-        pp[dd] = 0.f;
-        if (dd == 0) {
-          pp[hd] = -INFINITY;
-          pp[hd + 1] = 0.f;
-        }
-      }
-    }
-    return;
-  }
-  const float scale = 1.0f / sqrtf((float)hd);
-  for (int i = tid; i < grp * hd; i += kBlock)
-    qs[i / hd][i % hd] = qkv[(size_t)m * ldq + (size_t)(g * grp) * hd + i];
-  __syncthreads();
-  const size_t head_off = ((size_t)layer * kvh + g) * d.max_pos * hd;
-  const KV *kc = reinterpret_cast<const KV *>(d.k) + head_off;
-  const KV *vc = reinterpret_cast<const KV *>(d.v) + head_off;
-  // scores: 8 lanes per key, 16 dims per lane (hd == 128)
-  {
-    const int sub = tid & 7, pg = tid >> 3;
-    for (int p = p0 + pg; p < p1; p += kBlock / 8) {
-      float kv[16];
-      load16(kc + (size_t)p * hd + sub * 16, kv);
-      for (int hh = 0; hh < grp; hh++) {
-        float acc = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; i++) acc = fmaf(qs[hh][sub * 16 + i], kv[i], acc);
-        acc += __shfl_xor(acc, 1, 64);
-        acc += __shfl_xor(acc, 2, 64);
-        acc += __shfl_xor(acc, 4, 64);
-        if (sub == 0) sc[hh][p - p0] = acc * scale;
-      }
-    }
-  }
-  __syncthreads();
-  // softmax statistics: wave hh owns q head hh
-  {
-    const int wave = tid >> 6, lane = tid & 63, cnt = p1 - p0;
-    if (wave < grp) {
-      float m0 = -INFINITY;
-      for (int i = lane; i < cnt; i += 64) m0 = fmaxf(m0, sc[wave][i]);
-      m0 = wave_max(m0);
-      float l0 = 0.f;
-      for (int i = lane; i < cnt; i += 64) {
-        const float e = expf(sc[wave][i] - m0);
-        sc[wave][i] = e;
-        l0 += e;
-      }
-      l0 = wave_sum(l0);
-      if (lane == 0) {
-        mx[wave] = m0;
-        sum[wave] = l0;
-      }
-    }
-  }
-  __syncthreads();
-  // values
-  for (int i = tid; i < grp * hd; i += kBlock) {
-    const int hh = i / hd, dd = i % hd, h = g * grp + hh;
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    int p = p0;
-    for (; p + 3 < p1; p += 4) {
-      a0 = fmaf(sc[hh][p - p0], (float)vc[(size_t)p * hd + dd], a0);
-      a1 = fmaf(sc[hh][p + 1 - p0], (float)vc[(size_t)(p + 1) * hd + dd], a1);
-      a2 = fmaf(sc[hh][p + 2 - p0], (float)vc[(size_t)(p + 2) * hd + dd], a2);
-      a3 = fmaf(sc[hh][p + 3 - p0], (float)vc[(size_t)(p + 3) * hd + dd], a3);
-    }
-    for (; p < p1; p++) a0 = fmaf(sc[hh][p - p0], (float)vc[(size_t)p * hd + dd], a0);
-    const float o = (a0 + a1) + (a2 + a3);
-    if (splits == 1) {
-      out[(size_t)m * ldo + h * hd + dd] = o / sum[hh];
-    } else {
-      float *pp = part + (((size_t)m * heads + h) * splits + s) * (hd + 2);
-      pp[dd] = o;
-      if (dd == 0) {
-        pp[hd] = mx[hh];
-        pp[hd + 1] = sum[hh];
-      }
-    }
-  }
-}
-
-__global__ void k_attn_combine(const float *part, int heads, int hd, int splits,
-                               float *out) {
-  const int h = blockIdx.x, m = blockIdx.y, dd = threadIdx.x;
-  if (dd >= hd) return;
-  const float *pp = part + ((size_t)m * heads + h) * splits * (hd + 2);
-  float gm = -INFINITY;
-  for (int s = 0; s < splits; s++) gm = fmaxf(gm, pp[s * (hd + 2) + hd]);
-  float l = 0.f, o = 0.f;
-  if (gm > -INFINITY) {
-    for (int s = 0; s < splits; s++) {
-      const float ms = pp[s * (hd + 2) + hd];
-      if (ms == -INFINITY) continue;
-      const float e = expf(ms - gm);
-      l += e * pp[s * (hd + 2) + hd + 1];
-      o += e * pp[s * (hd + 2) + dd];
-    }
-  }
-  out[((size_t)m * heads + h) * hd + dd] = l > 0.f ? o / l : 0.f;
-}
-
-void launch_attention(const float *qkv, int ldq, const RowDesc *rd, int M, int layer,
-                      int heads, int kvh, int hd, int splits, int chunk, float *out,
-                      float *part, bool kv16, hipStream_t st) {
-  (void)chunk;
-  const dim3 grid(kvh, M, splits);
-  if (kv16)
-    hipLaunchKernelGGL(k_attention<_Float16>, grid, dim3(kBlock), 0, st, qkv, ldq, rd, layer,
-                       heads, kvh, hd, splits, out, part);
-  else
-    hipLaunchKernelGGL(k_attention<float>, grid, dim3(kBlock), 0, st, qkv, ldq, rd, layer,
-                       heads, kvh, hd, splits, out, part);
-  if (splits > 1)
-    hipLaunchKernelGGL(k_attn_combine, dim3(heads, M), dim3(hd), 0, st, part, heads, hd,
-                       splits, out);
 }
 
 // ---------------------------------------------------------------------------

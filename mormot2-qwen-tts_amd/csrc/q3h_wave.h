@@ -89,4 +89,13 @@ __device__ __forceinline__ float group8_sum_dpp(float v) {
   return v;
 }
 
+// sum over the 16 lanes of a DPP row (lanes 16k..16k+15), in every lane of the row
+__device__ __forceinline__ float group16_sum_dpp(float v) {
+  v += dpp_f<kQuadXor1>(v);
+  v += dpp_f<kQuadXor2>(v);
+  v += dpp_f<kHalfMirror>(v);
+  v += dpp_f<kRowMirror>(v);
+  return v;
+}
+
 }  // namespace q3h

@@ -101,6 +101,7 @@ SIGNATURES = {
     "q3h_context_destroy": (_I, [_P]),
     "q3h_context_fill_kv": (_I, [_P, _FP, _FP, _I]),
     "q3h_context_read_kv": (_I, [_P, _I, _FP, _FP]),
+    "q3h_context_time_attention": (_I, [_P, _I, _FP, ctypes.POINTER(ctypes.c_int64)]),
     "q3h_forward_embeds": (_I, [_P, _FP, _I, _I, _FP, _FP]),
     "q3h_forward_embeds_batch": (_I, [ctypes.POINTER(_P), _I, _FP, _IP, _FP, _FP]),
     "q3h_frame_create": (_I, [_P, _P, ctypes.POINTER(FrameConfig), _FP,
@@ -275,6 +276,15 @@ class Context:
         """k, v: float32 [layers][kv_heads][len][head_dim]."""
         k, v = _f32(k), _f32(v)
         _check(lib().q3h_context_fill_kv(self.h, _fp(k), _fp(v), k.shape[2]))
+
+    def time_attention(self, iters=20):
+        """(us per launch, algorithmic bytes per launch) of the decode attention
+        of one new row at position length, averaged over the layers and iters
+        (events attached to each launch); the length does not change."""
+        us = ctypes.c_float()
+        b = ctypes.c_int64()
+        _check(lib().q3h_context_time_attention(self.h, iters, ctypes.byref(us), ctypes.byref(b)))
+        return us.value, b.value
 
     def read_kv(self, layer):
         c = self.stack.cfg

@@ -143,33 +143,81 @@ def test_batch_equals_single(q8model, q3h, synth):
         c.destroy()
 
 
-@pytest.mark.parametrize("L", [300, 2048])
-def test_long_context_decode(device, q3h, q3o, synth, L):
-    """Split-K attention: K/V prefilled with N(0,1) values (fp16 cache), then
-    decode steps, against the oracle with the same cache."""
-    print(f"case L={L}", flush=True)
+# (positions, f16 cache): every split shape of the long-context kernel -
+# 64-position splits up to 2048 positions (2048 + 1 is the first 128-split
+# case), 128 up to 4096, then 256 (f16) / 128 (f32); 8192 + 1 positions leave
+# a last split of one position
+@pytest.mark.parametrize("L,kv16", [(300, 1), (2048, 1), (2100, 1), (4100, 1), (8192, 1),
+                                    (2100, 0)])
+def test_long_context_decode(device, q3h, q3o, synth, L, kv16):
+    """Split attention: K/V prefilled with N(0,1) values, then decode steps,
+    against the oracle with the same cache."""
+    print(f"case L={L} kv16={kv16}", flush=True)
     dims = dict(synth.TALKER, layers=2)
     layers, f = synth.stack_weights(3, "talker.model.", dims, norm_std=0.1,
                                     quantize=q3o.quantize_q8_0)
-    st = q3h.Stack(device, dict(dims, dtype=q3h.Q8_0, kv_f16=1, act_q8=0, max_positions=L + 8),
-                   layers, f, q3h.Q8_0)
-    ost = q3o.Stack(dims, layers, f, q3o.Q8_0, kv_f16=1)
+    st = q3h.Stack(device, dict(dims, dtype=q3h.Q8_0, kv_f16=kv16, act_q8=0,
+                                max_positions=L + 8), layers, f, q3h.Q8_0)
+    ost = q3o.Stack(dims, layers, f, q3o.Q8_0, kv_f16=kv16)
     kv = synth.normal(9, "kv", (2, 2, 8, L, 128), 1.0)
     ctx, octx = q3h.Context(st, L + 8), q3o.Ctx(ost, L + 8)
     ctx.fill_kv(kv[0], kv[1])
     octx.fill(kv[0], kv[1])
     k0, v0 = ctx.read_kv(1)
-    assert np.array_equal(k0, kv[0][1].astype(np.float16).astype(np.float32))
+    want = kv[0][1].astype(np.float16).astype(np.float32) if kv16 else kv[0][1]
+    assert np.array_equal(k0, want)
+    tol = 1e-3 if kv16 else 1e-4
     for step in range(3):
         x = synth.prompt(50 + step, 1)
         _, s = ctx.forward(x)
         os_ = octx.forward(x)
-        assert rel(s, os_) < 1e-3, (step, rel(s, os_))
+        assert rel(s, os_) < tol, (step, rel(s, os_))
     assert ctx.length == L + 3
+    # the timing entry leaves the context as it was
+    us, nbytes = ctx.time_attention(iters=2)
+    assert us > 0 and nbytes == 2 * (2 if kv16 else 4) * 1024 * (L + 4) + 4 * (4096 + 2048)
+    assert ctx.length == L + 3
+    x = synth.prompt(60, 1)
+    _, s = ctx.forward(x)
+    assert rel(s, octx.forward(x)) < tol
     ctx.destroy()
     st.destroy()
     octx.destroy()
     ost.destroy()
+
+
+def test_long_context_batch_ragged(device, q3h, q3o, synth):
+    """One batched decode step over contexts of 40, 700, 2500 and 5000
+    positions: the split count follows the longest, the shorter contexts
+    leave their extra splits empty."""
+    dims = dict(synth.TALKER, layers=2)
+    layers, f = synth.stack_weights(4, "talker.model.", dims, norm_std=0.1,
+                                    quantize=q3o.quantize_q8_0)
+    lens = [40, 700, 2500, 5000]
+    cap = max(lens) + 8
+    st = q3h.Stack(device, dict(dims, dtype=q3h.Q8_0, kv_f16=1, act_q8=0, max_positions=cap),
+                   layers, f, q3h.Q8_0)
+    ost = q3o.Stack(dims, layers, f, q3o.Q8_0, kv_f16=1)
+    ctxs, octxs = [], []
+    try:
+        for i, L in enumerate(lens):
+            kv = synth.normal(20 + i, "kv", (2, 2, 8, L, 128), 1.0)
+            c, oc = q3h.Context(st, cap), q3o.Ctx(ost, cap)
+            c.fill_kv(kv[0], kv[1])
+            oc.fill(kv[0], kv[1])
+            ctxs.append(c)
+            octxs.append(oc)
+        for step in range(2):
+            x = synth.prompt(70 + step, len(lens))
+            _, normed = q3h.forward_batch(ctxs, x)
+            for i, oc in enumerate(octxs):
+                o = oc.forward(x[i:i + 1])
+                assert rel(normed[i], o) < 1e-3, (step, i, rel(normed[i], o))
+    finally:
+        for c in ctxs + octxs:
+            c.destroy()
+        st.destroy()
+        ost.destroy()
 
 
 def test_device_quantizer_equals_host_blocks(device, q3h, q3o, synth):
