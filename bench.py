@@ -48,6 +48,10 @@ import q3h  # noqa: E402
 import synth  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the single-row Q8_0 products of one talker decode
+# step, from rocprofv3 FETCH_SIZE + WRITE_SIZE passes scaled by a plain copy
+# kernel of known size (profiles/gemv_q8_decode_step_traffic.md)
+GEMV_TRAFFIC_PER_LAUNCH = 4321175
 PROMPT_ROWS = 48
 
 
@@ -156,7 +160,8 @@ def gemv_roofline(ts, args):
     log(f"gemv: {launches} launches/step, kernel {us:.2f} us/launch "
         f"({achieved:.0f} GB/s), graph wall {wall if wall is None else round(wall, 2)} us/launch")
     return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
+                frac=round(achieved / HBM_PEAK_GBS, 4), traffic=GEMV_TRAFFIC_PER_LAUNCH,
+                traffic_source="profiles/gemv_q8_decode_step_traffic.md",
                 kernel="k_gemv_q8v (Q8_0 matrix-vector products of one talker decode step)",
                 bytes_per_launch=int(per_launch), us_per_launch=round(us, 3),
                 graph_wall_us_per_launch=None if wall is None else round(wall, 3))
@@ -209,6 +214,24 @@ def long_context_attention(dev, f32, tables, seed, steps=32, iters=10):
                 kv="f16", steps_per_length=steps, results=out)
 
 
+COPY_BYTES = 256 << 20
+
+
+def copy_calibration(iters=5):
+    """A plain copy of COPY_BYTES (read once, written once) by an elementwise
+    kernel, iters times: the bytes the FETCH_SIZE / WRITE_SIZE counters report
+    per dispatch of it scale the counters of the kernels under study."""
+    import torch
+    x = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(iters):
+        torch.mul(x, 1.0, out=y)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": COPY_BYTES, "copy_bytes_written": COPY_BYTES,
+                      "dispatches": iters}), flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -226,11 +249,29 @@ def main():
                     help="skip the long-context attention measurement (frame_b1)")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the matrix-vector roofline measurement (profiling runs)")
+    ap.add_argument("--long-attn-only", action="store_true",
+                    help="only the long-context attention measurement (profiling runs)")
+    ap.add_argument("--copy-only", action="store_true",
+                    help="only a plain copy kernel of known size (calibrates the FETCH_SIZE "
+                         "and WRITE_SIZE counters of profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(independent streams would shard across GPUs with no exchange)", file=sys.stderr)
         return 2
+    if args.copy_only:
+        return copy_calibration()
+    if args.long_attn_only:
+        if not q3h.available():
+            raise RuntimeError("no gfx950 device")
+        dev = q3h.Device(0)
+        tl, tf = synth.stack_weights(args.seed, "talker.model.", synth.TALKER)
+        f32 = dict(tl=tl, tf=tf, th=synth.talker_head(args.seed))
+        tables = dict(codec_emb=synth.codec_embedding(args.seed))
+        print(json.dumps({"long_context_attention":
+                          long_context_attention(dev, f32, tables, args.seed)}), flush=True)
+        dev.close()
+        return 0
     b1 = args.workload == "frame_b1"
     n = 1 if b1 else 32
     steps = args.steps if args.steps is not None else (156 if b1 else 128)

@@ -645,10 +645,12 @@ int launch_kv(const AttnArgs &a, int M, int positions, hipStream_t st, const hip
 
 }  // namespace
 
+// (split length, threads) measured best on the talker shapes (28 layers, so
+// that the cache streams from HBM) among 64-256 positions x 256-1024 threads
 SplitShape attn_split_shape(int positions, bool kv16) {
   if (positions <= kSplit) return {kSplit, 0};  // one workgroup per query head
-  if (positions <= 2048) return {64, 256};
-  if (kv16) return positions <= 4096 ? SplitShape{128, 256} : SplitShape{256, 512};
+  if (positions <= 1024) return {64, 256};
+  if (kv16) return positions <= 12288 ? SplitShape{128, 256} : SplitShape{256, 512};
   return {128, 512};
 }
 

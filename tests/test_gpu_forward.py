@@ -143,12 +143,12 @@ def test_batch_equals_single(q8model, q3h, synth):
         c.destroy()
 
 
-# (positions, f16 cache): every split shape of the long-context kernel -
-# 64-position splits up to 2048 positions (2048 + 1 is the first 128-split
-# case), 128 up to 4096, then 256 (f16) / 128 (f32); 8192 + 1 positions leave
-# a last split of one position
-@pytest.mark.parametrize("L,kv16", [(300, 1), (2048, 1), (2100, 1), (4100, 1), (8192, 1),
-                                    (2100, 0)])
+# (positions, f16 cache): the split shapes of the long-context kernel -
+# 64-position splits up to 1024 positions, then 128 (f16 up to 12288, f32);
+# 1024 + 1 and 8192 + 1 positions leave a last split of one position; 12300
+# takes the 256-position f16 splits
+@pytest.mark.parametrize("L,kv16", [(300, 1), (1024, 1), (2100, 1), (8192, 1), (12300, 1),
+                                    (300, 0), (2100, 0)])
 def test_long_context_decode(device, q3h, q3o, synth, L, kv16):
     """Split attention: K/V prefilled with N(0,1) values, then decode steps,
     against the oracle with the same cache."""
