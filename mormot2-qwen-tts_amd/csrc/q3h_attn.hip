@@ -1,25 +1,18 @@
-// q3h_attn.hip - GQA decode attention of the Qwen3 stacks on gfx950.
+// q3h_attn.hip - GQA decode attention of the Qwen3 stacks on gfx950 (the
+// f32-activation path; the int8 path has its own in q3h_attnx.hip).
 //
-// Contexts of up to 256 positions (the frame step): k_attn, one workgroup of
-// 512 threads per (query head h, row m). Query head h reads the keys and
-// values of kv head h / GRP. The kernel is short and latency-bound, so it is
-// laid out to issue every load at once and to keep the per-CU instruction
-// count low:
-//   - keys: 2 lanes per position (64 dims each), each lane loads its half
-//     row; the score is a 64-term dot + one DPP add;
-//   - values: lane (dg, kg) = (t % 32, t / 32) holds dims 4dg..4dg+3 of
-//     positions kg + 16 i; its 16 float4 loads are issued with the keys;
-//   - softmax in two passes over the block (max, then sum), no rescaling;
-//   - outputs: 16 partial sums per dim merged in LDS.
-// Fused prologue (FUSED: each row is the one new position of its own context):
-// the q head and the key get their RMSNorm (q_norm / k_norm) and RoPE here,
-// the new key and value are rounded as the cache stores them, the workgroup
-// of the group's first query head appends them to the cache, and position
-// pos is read from LDS (other positions from the cache, written by earlier
-// launches). Rows that add several positions of one context at once
-// (prefill) run the separate append kernel first and this kernel unfused.
-// Longer contexts: k_attn_split (below), splits of 64-256 positions merged
-// by the last workgroup of each kv head.
+//  - up to 256 positions (the frame step): k_attn_short, one workgroup per
+//    query head and row, one launch;
+//  - longer contexts: k_attn_split, one workgroup per (kv head, split) for
+//    both query heads of the group, then k_attn_merge.
+// Both read the cache with the same thread mapping: 16 lanes per cache row, 8
+// dims per lane, so every load instruction of a wave covers 4 whole rows
+// (a layout with 2 lanes per row, each walking its own half row, touched 64
+// separate segments per instruction and took 1.5-3 us to issue the loads of
+// a 256-position workgroup). Fused rows (each the one new position of its
+// own context) get the QK-norm (q_norm / k_norm), RoPE and the K/V append in
+// the prologue; rows that add several positions of one context at once
+// (prefill) run the separate append kernel first and these kernels unfused.
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
@@ -32,40 +25,7 @@ namespace q3h {
 namespace {
 
 constexpr int HD = 128;  // head_dim (checked at stack creation)
-constexpr int NT = 512;
-constexpr int NW = NT / 64;
-constexpr int kSplit = 256;  // positions per split
-constexpr int KG = NT / 32;  // value key groups
-constexpr int VK = kSplit / KG;  // value positions per lane
-
-__device__ __forceinline__ void ld64(const float *p, float *o) {
-#pragma unroll
-  for (int i = 0; i < 16; i++) {
-    const float4 t = reinterpret_cast<const float4 *>(p)[i];
-    o[4 * i] = t.x;
-    o[4 * i + 1] = t.y;
-    o[4 * i + 2] = t.z;
-    o[4 * i + 3] = t.w;
-  }
-}
-
-__device__ __forceinline__ void ld64(const _Float16 *p, float *o) {
-  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const h8 t = reinterpret_cast<const h8 *>(p)[i];
-#pragma unroll
-    for (int j = 0; j < 8; j++) o[8 * i + j] = (float)t[j];
-  }
-}
-
-__device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
-
-__device__ __forceinline__ float4 ld4(const _Float16 *p) {
-  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-  const h4 t = *reinterpret_cast<const h4 *>(p);
-  return make_float4((float)t[0], (float)t[1], (float)t[2], (float)t[3]);
-}
+constexpr int kSplit = 256;  // positions of the single-launch kernel
 
 // RMSNorm over a head held as (x0, x1) = elements (lane, lane + 64), weight
 // (w0, w1), then rotate_half RoPE with (cos, sin) = cs
@@ -81,155 +41,6 @@ __device__ __forceinline__ void norm_rope(float &x0, float &x1, float w0, float 
 
 __device__ __forceinline__ float rescale(float m, float mn) {
   return m == -INFINITY ? 0.f : __expf(m - mn);
-}
-
-// Plain scalar arguments, those of the prologue first (the first 14 argument
-// dwords are preloaded into SGPRs); the split buffers come last. qkn holds
-// [q_norm | k_norm | eps] of the layer.
-template <typename KV, bool FUSED, int GRP>
-__global__ __launch_bounds__(NT) void k_attn(const RowDesc *__restrict__ rd,
-                                             const float *__restrict__ qkv,
-                                             const float2 *__restrict__ rope_cs,
-                                             const float *__restrict__ qkn,
-                                             float *__restrict__ outp, int layer, int kvh) {
-  __shared__ float qs[HD];
-  __shared__ float kvn[2][HD];  // the new key and value, as the cache holds them
-  __shared__ float red[NW];
-  __shared__ float pr[kSplit];
-  __shared__ float po[KG][HD];
-  const int heads = GRP * kvh, ldq = (heads + 2 * kvh) * HD;
-  const int h = blockIdx.x, m = blockIdx.y, g = h / GRP;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const float *row = qkv + (size_t)m * ldq;
-
-  // raw q of head h (wave 0), key (wave 1), value (wave 2) of kv head g
-  float x0 = 0.f, x1 = 0.f;
-  if (FUSED && wave < 3) {
-    const size_t off = wave == 0 ? (size_t)h * HD : (size_t)(heads + (wave - 1) * kvh + g) * HD;
-    x0 = row[off + lane];
-    x1 = row[off + lane + 64];
-  }
-  const RowDesc d = rd[m];
-  float *out = outp + ((size_t)m * heads + h) * HD;
-  if (d.pos < 0) {  // inactive row: zeros, no ticket
-    if (t < HD) out[t] = 0.f;
-    return;
-  }
-  const int n = d.pos + 1;
-  const int p0 = 0, p1 = min(n, kSplit);
-  const size_t head_off = ((size_t)layer * kvh + g) * d.max_pos * HD;
-  KV *kc = reinterpret_cast<KV *>(d.k) + head_off;
-  KV *vc = reinterpret_cast<KV *>(d.v) + head_off;
-
-  // every key and value of the split, loaded before the prologue
-  const int kp = p0 + (t >> 1), kh = (t & 1) * 64;
-  const bool kown = kp < p1 && !(FUSED && kp == d.pos);
-  float kk[64];
-  if (kown) ld64(kc + (size_t)kp * HD + kh, kk);
-  const int dg = t & 31, kg = t >> 5;
-  float4 vv[VK];
-#pragma unroll
-  for (int i = 0; i < VK; i++) {
-    const int p = p0 + kg + KG * i;
-    if (p < p1 && !(FUSED && p == d.pos)) vv[i] = ld4(vc + (size_t)p * HD + 4 * dg);
-  }
-  float2 cs = make_float2(1.f, 0.f);
-  float w0 = 1.f, w1 = 1.f, eps = 0.f;
-  if (FUSED && wave < 2) {
-    cs = rope_cs[(size_t)d.pos * (HD / 2) + lane];
-    const float *w = qkn + wave * HD;
-    w0 = w[lane];
-    w1 = w[lane + 64];
-    eps = qkn[2 * HD];
-  }
-  __builtin_amdgcn_sched_barrier(0);
-
-  if (FUSED) {
-    if (wave == 0) {
-      norm_rope(x0, x1, w0, w1, cs, eps);
-      qs[lane] = x0;
-      qs[lane + 64] = x1;
-    } else if (wave < 3) {
-      if (wave == 1) norm_rope(x0, x1, w0, w1, cs, eps);
-      const KV y0 = (KV)x0, y1 = (KV)x1;
-      kvn[wave - 1][lane] = (float)y0;
-      kvn[wave - 1][lane + 64] = (float)y1;
-      // the group's first query head appends
-      if (h % GRP == 0) {
-        KV *dst = (wave == 1 ? kc : vc) + (size_t)d.pos * HD;
-        dst[lane] = y0;
-        dst[lane + 64] = y1;
-      }
-    }
-  } else if (t < HD) {
-    qs[t] = row[(size_t)h * HD + t];
-  }
-  __syncthreads();
-
-  // scores: 2 lanes per key
-  const float scale = (float)(1.0 / sqrt((double)HD));
-  const bool klive = kp < p1;
-  if (FUSED && kp == d.pos) {
-#pragma unroll
-    for (int i = 0; i < 64; i++) kk[i] = kvn[0][kh + i];
-  }
-  float a0 = 0.f, a1 = 0.f;
-  if (klive) {
-#pragma unroll
-    for (int i = 0; i < 64; i += 2) {
-      a0 = fmaf(qs[kh + i], kk[i], a0);
-      a1 = fmaf(qs[kh + i + 1], kk[i + 1], a1);
-    }
-  }
-  float sc = a0 + a1;
-  sc += dpp_f<kQuadXor1>(sc);
-  sc = klive ? sc * scale : -INFINITY;
-  // block max
-  float mx = wave_max_dpp(sc);
-  if (lane == 0) red[wave] = mx;
-  __syncthreads();
-  mx = red[0];
-#pragma unroll
-  for (int i = 1; i < NW; i++) mx = fmaxf(mx, red[i]);
-  const float e = klive ? expf(sc - mx) : 0.f;
-  if ((t & 1) == 0 && kp - p0 < kSplit) pr[kp - p0] = e;
-  float sum = wave_sum_dpp((t & 1) == 0 ? e : 0.f);
-  __syncthreads();
-  if (lane == 0) red[wave] = sum;
-  __syncthreads();
-  sum = 0.f;
-#pragma unroll
-  for (int i = 0; i < NW; i++) sum += red[i];
-
-  // values: dims 4dg..4dg+3 over this lane's positions
-  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-  for (int i = 0; i < VK; i++) {
-    const int p = p0 + kg + KG * i;
-    if (p < p1) {
-      const float pw = pr[p - p0];
-      float4 v;
-      if (FUSED && p == d.pos)
-        v = make_float4(kvn[1][4 * dg], kvn[1][4 * dg + 1], kvn[1][4 * dg + 2], kvn[1][4 * dg + 3]);
-      else
-        v = vv[i];
-      o.x = fmaf(pw, v.x, o.x);
-      o.y = fmaf(pw, v.y, o.y);
-      o.z = fmaf(pw, v.z, o.z);
-      o.w = fmaf(pw, v.w, o.w);
-    }
-  }
-  po[kg][4 * dg] = o.x;
-  po[kg][4 * dg + 1] = o.y;
-  po[kg][4 * dg + 2] = o.z;
-  po[kg][4 * dg + 3] = o.w;
-  __syncthreads();
-  if (t < HD) {
-    float acc = 0.f;
-#pragma unroll
-    for (int i = 0; i < KG; i++) acc += po[i][t];
-    out[t] = sum > 0.f ? acc / sum : 0.f;
-  }
 }
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -255,6 +66,191 @@ __device__ __forceinline__ void cvt8(const u32x4 (&r)[2], float (&o)[8]) {
   for (int i = 0; i < 2; i++)
 #pragma unroll
     for (int e = 0; e < 4; e++) o[4 * i + e] = __uint_as_float(r[i][e]);
+}
+
+// Contexts of up to 256 positions (the frame step's talker and code
+// predictor at batch sizes that take the f32 path): one workgroup of NTS
+// threads per (query head h, row m), kv head h / GRP. The thread mapping of
+// the split kernel below: thread t owns dims 8 (t % 16) .. + 7 of positions
+// t / 16 + (NTS / 16) j, so each load instruction of a wave reads 4 whole
+// consecutive cache rows (coalesced), scores are 8-term chains summed over a
+// 16-lane DPP row, and a position's key and value sit in the same lanes.
+//   - loads first: the prologue's (q head, key, value of the row), then the
+//     keys and values of positions [0, n) clamped into range (a context's
+//     cache starts as zeros, so a row read past the context is finite, and
+//     its weight is 0);
+//   - FUSED (each row the one new position pos of its own context): waves 0,
+//     1, 2 norm and rotate the q head and the key, round key and value as the
+//     cache stores them; the group's first query head appends them; the new
+//     position joins the softmax as one more score (its 128-dim dot from the
+//     prologue's vectors) instead of through the cache, so the cache rows
+//     read here are the positions before pos;
+//   - softmax in two passes over the workgroup (maximum, then sum).
+template <typename KV, bool FUSED, int GRP, int NTS>
+__global__ __launch_bounds__(NTS) void k_attn_short(const RowDesc *__restrict__ rd,
+                                                    const float *__restrict__ qkv,
+                                                    const float2 *__restrict__ rope_cs,
+                                                    const float *__restrict__ qkn,
+                                                    float *__restrict__ outp, int layer, int kvh) {
+  constexpr int PG = NTS / 16;         // position groups
+  constexpr int NJ = kSplit / PG;      // positions per thread
+  constexpr int LW = sizeof(KV) / 2;   // 16-byte loads per 8 elements
+  constexpr int NWV = NTS / 64;
+  static_assert(NWV >= 3, "prologue waves");
+  __shared__ float qs[HD], kvn[2][HD];
+  __shared__ float red[2][NWV];
+  __shared__ float po[NWV][HD];
+  const int heads = GRP * kvh, ldq = (heads + 2 * kvh) * HD;
+  const int h = blockIdx.x, m = blockIdx.y, g = h / GRP;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int r16 = t & 15, pg = t >> 4;
+  const float *row = qkv + (size_t)m * ldq;
+  float *out = outp + ((size_t)m * heads + h) * HD;
+
+  // raw q of head h (wave 0), key (wave 1), value (wave 2) of kv head g
+  float x0 = 0.f, x1 = 0.f, w0 = 1.f, w1 = 1.f, eps = 0.f;
+  if (FUSED && wave < 3) {
+    const size_t off = wave == 0 ? (size_t)h * HD : (size_t)(heads + (wave - 1) * kvh + g) * HD;
+    x0 = row[off + lane];
+    x1 = row[off + lane + 64];
+    const float *w = qkn + min(wave, 1) * HD;
+    w0 = w[lane];
+    w1 = w[lane + 64];
+    eps = qkn[2 * HD];
+  }
+  const RowDesc d = rd[m];
+  if (d.pos < 0) {  // inactive row: zeros
+    if (t < HD) out[t] = 0.f;
+    return;
+  }
+  const int pos = d.pos;
+  const int n = FUSED ? pos : pos + 1;  // positions read from the cache
+  const int last = max(n - 1, 0);
+  const size_t head_off = ((size_t)layer * kvh + g) * d.max_pos * HD;
+  KV *kc = reinterpret_cast<KV *>(d.k) + head_off;
+  KV *vc = reinterpret_cast<KV *>(d.v) + head_off;
+  const float2 cs =
+      FUSED && wave < 2 ? rope_cs[(size_t)pos * (HD / 2) + lane] : make_float2(1.f, 0.f);
+  u32x4 kr[NJ][LW], vr[NJ][LW];
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    const KV *p = kc + (size_t)min(pg + PG * j, last) * HD + 8 * r16;
+#pragma unroll
+    for (int e = 0; e < LW; e++) kr[j][e] = gload16(p + e * 4);
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    const KV *p = vc + (size_t)min(pg + PG * j, last) * HD + 8 * r16;
+#pragma unroll
+    for (int e = 0; e < LW; e++) vr[j][e] = gload16(p + e * 4);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  if (FUSED) {
+    if (wave == 0) {
+      norm_rope(x0, x1, w0, w1, cs, eps);
+      qs[lane] = x0;
+      qs[lane + 64] = x1;
+    } else if (wave < 3) {
+      if (wave == 1) norm_rope(x0, x1, w0, w1, cs, eps);
+      const KV y0 = (KV)x0, y1 = (KV)x1;
+      kvn[wave - 1][lane] = (float)y0;
+      kvn[wave - 1][lane + 64] = (float)y1;
+      if (h % GRP == 0) {  // the group's first query head appends
+        KV *dst = (wave == 1 ? kc : vc) + (size_t)pos * HD;
+        dst[lane] = y0;
+        dst[lane + 64] = y1;
+      }
+    }
+  } else if (t < HD) {
+    qs[t] = row[(size_t)h * HD + t];
+  }
+  __syncthreads();
+
+  const float scale = (float)(1.0 / sqrt((double)HD));
+  float q[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) q[e] = qs[8 * r16 + e];
+  float sc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    float k8[8];
+    cvt8(kr[j], k8);
+    float a = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) a = fmaf(q[e], k8[e], a);
+    sc[j] = a;
+  }
+  float sn = -INFINITY;  // the new position's score (FUSED)
+  if (FUSED) {
+    float a = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) a = fmaf(q[e], kvn[0][8 * r16 + e], a);
+    sn = group16_sum_dpp(a) * scale;
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; j++) sc[j] += dpp_f<kQuadXor1>(sc[j]);
+#pragma unroll
+  for (int j = 0; j < NJ; j++) sc[j] += dpp_f<kQuadXor2>(sc[j]);
+#pragma unroll
+  for (int j = 0; j < NJ; j++) sc[j] += dpp_f<kHalfMirror>(sc[j]);
+#pragma unroll
+  for (int j = 0; j < NJ; j++) sc[j] += dpp_f<kRowMirror>(sc[j]);
+  float mx = sn;
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    sc[j] = pg + PG * j < n ? sc[j] * scale : -INFINITY;
+    mx = fmaxf(mx, sc[j]);
+  }
+  mx = wave_max_dpp(mx);
+  if (lane == 0) red[0][wave] = mx;
+  __syncthreads();
+  mx = red[0][0];
+#pragma unroll
+  for (int w = 1; w < NWV; w++) mx = fmaxf(mx, red[0][w]);
+  float ls = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    sc[j] = __expf(sc[j] - mx);
+    ls += sc[j];
+  }
+  ls = wave_sum_dpp(r16 == 0 ? ls : 0.f);
+  if (lane == 0) red[1][wave] = ls;
+  float o[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) o[e] = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    float v8[8];
+    cvt8(vr[j], v8);
+#pragma unroll
+    for (int e = 0; e < 8; e++) o[e] = fmaf(sc[j], v8[e], o[e]);
+  }
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    o[e] += __shfl_xor(o[e], 16);
+    o[e] += __shfl_xor(o[e], 32);
+  }
+  if (lane < 16) {
+    float4 *dst = reinterpret_cast<float4 *>(&po[wave][8 * r16]);
+    dst[0] = make_float4(o[0], o[1], o[2], o[3]);
+    dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+  }
+  __syncthreads();
+  if (t < HD) {
+    float sum = 0.f, acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWV; w++) {
+      sum += red[1][w];
+      acc += po[w][t];
+    }
+    if (FUSED) {
+      const float c = __expf(sn - mx);
+      sum += c;
+      acc = fmaf(c, kvn[1][t], acc);
+    }
+    out[t] = sum > 0.f ? acc / sum : 0.f;
+  }
 }
 
 constexpr int kMaxSplitsLong = 256;
@@ -616,8 +612,8 @@ int launch_g(const AttnArgs &a, int M, int positions, hipStream_t st, const hipE
   Q3H_LAUNCH((k_attn_split<KV, FUSED, G, P, T>), dim3(a.kvh, S, M), dim3(T), st, ev0, ev1,      \
              a.rd, a.qkv, a.rope_cs, a.qkn, a.layer, a.kvh, S, a.part)
   if (sh.len == kSplit && sh.threads == 0) {
-    Q3H_LAUNCH((k_attn<KV, FUSED, G>), dim3(a.heads, M), dim3(NT), st, ev0, ev1, a.rd, a.qkv,
-               a.rope_cs, a.qkn, a.out, a.layer, a.kvh);
+    Q3H_LAUNCH((k_attn_short<KV, FUSED, G, 512>), dim3(a.heads, M), dim3(512), st, ev0, ev1,
+               a.rd, a.qkv, a.rope_cs, a.qkn, a.out, a.layer, a.kvh);
   } else if (sh.len == 64) {
     Q3H_S(64, 256);
   } else if constexpr (sizeof(KV) == 2) {

@@ -38,35 +38,6 @@ constexpr int ROWS = 8;   // o_proj rows per workgroup: one per wave
 constexpr int NT = 512;   // 8 waves
 constexpr int NBO = NQ / 32;
 
-__device__ __forceinline__ void ld32(const float *p, float *o) {
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const float4 t = reinterpret_cast<const float4 *>(p)[i];
-    o[4 * i] = t.x;
-    o[4 * i + 1] = t.y;
-    o[4 * i + 2] = t.z;
-    o[4 * i + 3] = t.w;
-  }
-}
-
-__device__ __forceinline__ void ld32(const _Float16 *p, float *o) {
-  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const h8 t = reinterpret_cast<const h8 *>(p)[i];
-#pragma unroll
-    for (int j = 0; j < 8; j++) o[8 * i + j] = (float)t[j];
-  }
-}
-
-__device__ __forceinline__ float2 ld2(const float *p) { return *reinterpret_cast<const float2 *>(p); }
-
-__device__ __forceinline__ float2 ld2(const _Float16 *p) {
-  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-  const h2 t = *reinterpret_cast<const h2 *>(p);
-  return make_float2((float)t[0], (float)t[1]);
-}
-
 __device__ __forceinline__ float dot4(int w, float4 x, float acc) {
   acc = fmaf((float)(int8_t)(w), x.x, acc);
   acc = fmaf((float)(int8_t)(w >> 8), x.y, acc);
@@ -94,6 +65,23 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// 8 cache elements from one 16-byte load (f16) or two (f32), as f32
+__device__ __forceinline__ void cvt8(const u32x4 (&r)[1], float (&o)[8]) {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  const h8 v = __builtin_bit_cast(h8, r[0]);
+#pragma unroll
+  for (int e = 0; e < 8; e++) o[e] = (float)v[e];
+}
+
+__device__ __forceinline__ void cvt8(const u32x4 (&r)[2], float (&o)[8]) {
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) o[4 * i + e] = __uint_as_float(r[i][e]);
+}
+
 template <typename KV>
 __global__ __launch_bounds__(NT) void k_attn_o_cp(const int8_t *__restrict__ wo,
                                                   const float *__restrict__ qkv,
@@ -101,10 +89,13 @@ __global__ __launch_bounds__(NT) void k_attn_o_cp(const int8_t *__restrict__ wo,
                                                   const float *__restrict__ qkn,
                                                   const float2 *__restrict__ rope, int pos,
                                                   int v_off) {
+  constexpr int LW = sizeof(KV) / 2;  // 16-byte loads per 8 elements
+  constexpr int NJ = P / 4;           // positions per lane
   __shared__ float att[NQ];
   __shared__ float qs[KVH][GRP][HD];
   __shared__ float kvs[KVH][2][HD];  // the new key and value of each kv head
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int r16 = lane & 15, rg = lane >> 4;
   const int row = blockIdx.x * ROWS + w;  // this wave's o_proj row
   const _Float16 *wd = reinterpret_cast<const _Float16 *>(wo + (size_t)HID * NQ);
 
@@ -134,15 +125,24 @@ __global__ __launch_bounds__(NT) void k_attn_o_cp(const int8_t *__restrict__ wo,
   const float2 cs = rope[lane];
   KV *kh = kl + (size_t)w * P * HD;
   KV *vh = kl + v_off + (size_t)w * P * HD;
-  // keys: lane 4p + j holds dims 32j .. 32j + 31 of key p
-  const int kp = lane >> 2, kj = lane & 3;
-  float kk[32];
-  if (kp < pos) ld32(kh + (size_t)kp * HD + kj * 32, kk);
-  // values: lane holds dims 2 lane, 2 lane + 1 of every cached position
-  float2 vv[P];
+  // cached keys and values of positions 0 .. pos - 1: lane holds dims
+  // 8 (lane % 16) .. + 7 of positions lane / 16 + 4 j, so each load
+  // instruction reads 4 whole rows; positions at or past pos are read at
+  // pos - 1 (a context's cache starts as zeros: finite) and weighted 0
+  const int last = max(pos - 1, 0);
+  u32x4 kr[NJ][LW], vr[NJ][LW];
 #pragma unroll
-  for (int p = 0; p < P; p++)
-    if (p < pos) vv[p] = ld2(vh + (size_t)p * HD + 2 * lane);
+  for (int j = 0; j < NJ; j++) {
+    const size_t off = (size_t)min(rg + 4 * j, last) * HD + 8 * r16;
+#pragma unroll
+    for (int e = 0; e < LW; e++) kr[j][e] = *reinterpret_cast<const u32x4 *>(kh + off + 4 * e);
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    const size_t off = (size_t)min(rg + 4 * j, last) * HD + 8 * r16;
+#pragma unroll
+    for (int e = 0; e < LW; e++) vr[j][e] = *reinterpret_cast<const u32x4 *>(vh + off + 4 * e);
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   // 2. QK-norm + RoPE; the new key and value rounded as the cache holds them
@@ -170,61 +170,111 @@ __global__ __launch_bounds__(NT) void k_attn_o_cp(const int8_t *__restrict__ wo,
   }
   wave_lds_sync();
 
-  // 3. scores of key kp (the new key from LDS), softmax over 0..pos; the
-  // probability of key p ends up in lanes 4p .. 4p + 3
-  if (kp == pos) {
-#pragma unroll
-    for (int i = 0; i < 32; i++) kk[i] = kvs[w][0][kj * 32 + i];
-  }
+  // 3. scores: an 8-term chain per lane summed over its 16-lane row; the
+  // new position's score from the prologue's key
   const float scale = (float)(1.0 / sqrt((double)HD));
-  const bool live = kp <= pos;
-  float pr[GRP];
+  float q[GRP][8], s[GRP][NJ], sn[GRP];
 #pragma unroll
-  for (int j = 0; j < GRP; j++) {
-    const float *q = &qs[w][j][kj * 32];
-    float a0 = 0.f, a1 = 0.f;
+  for (int j = 0; j < GRP; j++)
 #pragma unroll
-    for (int i = 0; i < 32; i += 2) {
-      a0 = fmaf(q[i], kk[i], a0);
-      a1 = fmaf(q[i + 1], kk[i + 1], a1);
-    }
-    float a = a0 + a1;
-    a += dpp_f<kQuadXor1>(a);
-    a += dpp_f<kQuadXor2>(a);
-    const float sv = live ? a * scale : -INFINITY;
-    const float mx = wave_max_dpp(sv);
-    const float e = live ? expf(sv - mx) : 0.f;
-    const float sum = wave_sum_dpp(kj == 0 ? e : 0.f);
-    pr[j] = e * (1.0f / sum);
-  }
-
-  // 4. outputs (lane holds dims 2 lane, 2 lane + 1), probabilities read
-  // from lane 4p
-  float o[GRP][2];
+    for (int e = 0; e < 8; e++) q[j][e] = qs[w][j][8 * r16 + e];
 #pragma unroll
-  for (int j = 0; j < GRP; j++) o[j][0] = o[j][1] = 0.f;
-#pragma unroll
-  for (int p = 0; p < P; p++) {
-    if (p < pos) {
-#pragma unroll
-      for (int j = 0; j < GRP; j++) {
-        const float pw = __builtin_bit_cast(
-            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pr[j]), 4 * p));
-        o[j][0] = fmaf(pw, vv[p].x, o[j][0]);
-        o[j][1] = fmaf(pw, vv[p].y, o[j][1]);
-      }
-    }
-  }
-  {
-    const float2 vn = make_float2(kvs[w][1][2 * lane], kvs[w][1][2 * lane + 1]);
+  for (int i = 0; i < NJ; i++) {
+    float k8[8];
+    cvt8(kr[i], k8);
 #pragma unroll
     for (int j = 0; j < GRP; j++) {
-      const float pw = __builtin_bit_cast(
-          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pr[j]), 4 * pos));
-      o[j][0] = fmaf(pw, vn.x, o[j][0]);
-      o[j][1] = fmaf(pw, vn.y, o[j][1]);
-      att[(w * GRP + j) * HD + 2 * lane] = o[j][0];
-      att[(w * GRP + j) * HD + 2 * lane + 1] = o[j][1];
+      float a = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) a = fmaf(q[j][e], k8[e], a);
+      s[j][i] = a;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < GRP; j++) {
+    float a = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) a = fmaf(q[j][e], kvs[w][0][8 * r16 + e], a);
+    sn[j] = a;
+  }
+#pragma unroll
+  for (int j = 0; j < GRP; j++) {
+#pragma unroll
+    for (int i = 0; i < NJ; i++) s[j][i] += dpp_f<kQuadXor1>(s[j][i]);
+    sn[j] += dpp_f<kQuadXor1>(sn[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < GRP; j++) {
+#pragma unroll
+    for (int i = 0; i < NJ; i++) s[j][i] += dpp_f<kQuadXor2>(s[j][i]);
+    sn[j] += dpp_f<kQuadXor2>(sn[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < GRP; j++) {
+#pragma unroll
+    for (int i = 0; i < NJ; i++) s[j][i] += dpp_f<kHalfMirror>(s[j][i]);
+    sn[j] += dpp_f<kHalfMirror>(sn[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < GRP; j++) {
+#pragma unroll
+    for (int i = 0; i < NJ; i++) s[j][i] += dpp_f<kRowMirror>(s[j][i]);
+    sn[j] += dpp_f<kRowMirror>(sn[j]);
+  }
+
+  // 4. softmax over 0 .. pos and the outputs: lane holds 8 dims of its
+  // positions, the 4 row groups summed by lane shuffles
+  const float4 vn0 = *reinterpret_cast<const float4 *>(&kvs[w][1][8 * r16]);
+  const float4 vn1 = *reinterpret_cast<const float4 *>(&kvs[w][1][8 * r16 + 4]);
+  const float vn[8] = {vn0.x, vn0.y, vn0.z, vn0.w, vn1.x, vn1.y, vn1.z, vn1.w};
+  float o[GRP][8], den[GRP];
+#pragma unroll
+  for (int j = 0; j < GRP; j++) {
+    sn[j] *= scale;
+    float mx = sn[j];
+#pragma unroll
+    for (int i = 0; i < NJ; i++) {
+      s[j][i] = rg + 4 * i < pos ? s[j][i] * scale : -INFINITY;
+      mx = fmaxf(mx, s[j][i]);
+    }
+    mx = wave_max_dpp(mx);
+    float ls = 0.f;
+#pragma unroll
+    for (int i = 0; i < NJ; i++) {
+      s[j][i] = __expf(s[j][i] - mx);
+      ls += s[j][i];
+    }
+    sn[j] = __expf(sn[j] - mx);
+    den[j] = wave_sum_dpp(r16 == 0 ? ls : 0.f) + sn[j];
+#pragma unroll
+    for (int e = 0; e < 8; e++) o[j][e] = 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < NJ; i++) {
+    float v8[8];
+    cvt8(vr[i], v8);
+#pragma unroll
+    for (int j = 0; j < GRP; j++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) o[j][e] = fmaf(s[j][i], v8[e], o[j][e]);
+  }
+#pragma unroll
+  for (int j = 0; j < GRP; j++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      o[j][e] += __shfl_xor(o[j][e], 16);
+      o[j][e] += __shfl_xor(o[j][e], 32);
+    }
+  if (lane < 16) {
+#pragma unroll
+    for (int j = 0; j < GRP; j++) {
+      const float inv = 1.0f / den[j];
+      float r[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) r[e] = fmaf(sn[j], vn[e], o[j][e]) * inv;
+      float4 *dst = reinterpret_cast<float4 *>(&att[(w * GRP + j) * HD + 8 * r16]);
+      dst[0] = make_float4(r[0], r[1], r[2], r[3]);
+      dst[1] = make_float4(r[4], r[5], r[6], r[7]);
     }
   }
   __syncthreads();
