@@ -48,6 +48,7 @@ import q3h  # noqa: E402
 import synth  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+F32_PROMPT_ROWS = 512
 # HBM bytes per launch of the single-row Q8_0 products of one talker decode
 # step, from rocprofv3 FETCH_SIZE + WRITE_SIZE passes scaled by a plain copy
 # kernel of known size (profiles/gemv_q8_decode_step_traffic.md)
@@ -59,16 +60,17 @@ def log(msg):
     print(f"bench: {msg}", file=sys.stderr, flush=True)
 
 
-def build_model(dev, seed, max_positions, act_q8):
+def build_model(dev, seed, max_positions, act_q8, dtype=q3h.Q8_0):
     """Talker + code predictor + heads on the device, from f32 weights that the
-    library quantizes to Q8_0 (bit-exact ggml quantize_row_q8_0_ref); act_q8:
-    activations quantized per 32-block too (int8 MFMA products)."""
+    library quantizes to Q8_0 (bit-exact ggml quantize_row_q8_0_ref) or keeps
+    in f32 (dtype F32); act_q8: activations quantized per 32-block too (int8
+    MFMA products)."""
     t0 = time.time()
     tl, tf = synth.stack_weights(seed, "talker.model.", synth.TALKER)
-    ts = q3h.Stack(dev, dict(synth.TALKER, dtype=q3h.Q8_0, kv_f16=0, act_q8=act_q8,
+    ts = q3h.Stack(dev, dict(synth.TALKER, dtype=dtype, kv_f16=0, act_q8=act_q8,
                              max_positions=max_positions), tl, tf, q3h.F32)
     cl, cf = synth.stack_weights(seed, "talker.code_predictor.model.", synth.PREDICTOR)
-    cs = q3h.Stack(dev, dict(synth.PREDICTOR, dtype=q3h.Q8_0, kv_f16=0, act_q8=act_q8,
+    cs = q3h.Stack(dev, dict(synth.PREDICTOR, dtype=dtype, kv_f16=0, act_q8=act_q8,
                              max_positions=16), cl, cf, q3h.F32)
     th = synth.talker_head(seed)
     ts.add_head(th, q3h.F32)
@@ -87,6 +89,8 @@ def build_model(dev, seed, max_positions, act_q8):
 def prompts(seed, workload, n):
     if workload == "frame_b1":
         return [synth.prompt(seed, PROMPT_ROWS)]
+    if workload == "f32_b8":
+        return [synth.prompt(seed + 2000 + s, F32_PROMPT_ROWS) for s in range(n)]
     rng = np.random.Generator(np.random.PCG64(seed))
     lens = rng.integers(16, 257, size=n)
     return [synth.prompt(seed + 1000 + s, int(L)) for s, L in enumerate(lens)]
@@ -97,8 +101,10 @@ def run_gpu(frame, pre, steps, warmup):
         frame.start(s, p)
     for _ in range(warmup):
         frame.step()
+    t0 = time.perf_counter()
     for s, p in enumerate(pre):
         frame.start(s, p)
+    run_gpu.prefill_s = time.perf_counter() - t0
     lat = np.empty(steps)
     codes = []
     t0 = time.perf_counter()
@@ -111,9 +117,10 @@ def run_gpu(frame, pre, steps, warmup):
     return total, lat, np.stack(codes)
 
 
-def cpu_baseline(f32, tables, pre, gpu_codes, budget_s, max_frames, act_q8):
+def cpu_baseline(f32, tables, pre, gpu_codes, budget_s, max_frames, act_q8, f32w=False):
     """The oracle's frame step on the host cores (same weights, same prompt of
-    stream 0, same activation mode), frames timed until budget_s is spent."""
+    stream 0, same weight and activation modes), frames timed until budget_s
+    is spent."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import q3o  # the checker's restatement, timed as the CPU baseline
 
@@ -121,11 +128,15 @@ def cpu_baseline(f32, tables, pre, gpu_codes, budget_s, max_frames, act_q8):
     q3o.set_threads(threads)
     q = q3o.quantize_q8_0
 
+    if f32w:
+        q = lambda v: v  # noqa: E731
+
     def qlayers(layers):
         return [{k: (q(v) if k.startswith("w") else v) for k, v in L.items()} for L in layers]
 
-    ot = q3o.Stack(synth.TALKER, qlayers(f32["tl"]), f32["tf"], q3o.Q8_0, act_q8=act_q8)
-    oc = q3o.Stack(synth.PREDICTOR, qlayers(f32["cl"]), f32["cf"], q3o.Q8_0, act_q8=act_q8)
+    wt = q3o.F32 if f32w else q3o.Q8_0
+    ot = q3o.Stack(synth.TALKER, qlayers(f32["tl"]), f32["tf"], wt, act_q8=act_q8)
+    oc = q3o.Stack(synth.PREDICTOR, qlayers(f32["cl"]), f32["cf"], wt, act_q8=act_q8)
     fr = q3o.Frame(ot, oc, q(f32["th"]), [q(h) for h in f32["ch"]], tables["codec_emb"],
                    tables["pred_emb"], tables["tts_pad"],
                    max_positions=pre[0].shape[0] + max_frames + 8)
@@ -141,8 +152,9 @@ def cpu_baseline(f32, tables, pre, gpu_codes, budget_s, max_frames, act_q8):
     for o in (fr, ot, oc):
         o.destroy()
     act = "int8 activations" if act_q8 else "f32 activations"
+    wts = "f32 weights" if f32w else "Q8_0 weights"
     return dict(value=n / dt, unit="frames/s", cores=threads, kind="port",
-                sample=f"frame step of stream 0, Q8_0 weights, {act} (oracle, C + OpenMP), "
+                sample=f"frame step of stream 0, {wts}, {act} (oracle, C + OpenMP), "
                        f"{pre[0].shape[0]} prompt rows (prefill untimed), first {n} frames, "
                        f"{dt:.1f} s"), n, equal
 
@@ -237,7 +249,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["frame_b1", "frame_b32"], default="frame_b1")
+    ap.add_argument("--workload", choices=["frame_b1", "frame_b32", "f32_b8"], default="frame_b1")
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--gemv-iters", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -273,8 +285,9 @@ def main():
         dev.close()
         return 0
     b1 = args.workload == "frame_b1"
-    n = 1 if b1 else 32
-    steps = args.steps if args.steps is not None else (156 if b1 else 128)
+    f32w = args.workload == "f32_b8"
+    n = 1 if b1 else (8 if f32w else 32)
+    steps = args.steps if args.steps is not None else (156 if b1 else (256 if f32w else 128))
     warmup = args.warmup
     if not q3h.available():
         raise RuntimeError("no gfx950 device")
@@ -282,8 +295,9 @@ def main():
     maxlen = max(p.shape[0] for p in pre)
     max_pos = maxlen + max(steps, warmup) + 8
     dev = q3h.Device(0)
-    act_q8 = 0 if b1 else 1
-    ts, cs, tables, f32 = build_model(dev, args.seed, max_pos, act_q8)
+    act_q8 = 0 if (b1 or f32w) else 1
+    ts, cs, tables, f32 = build_model(dev, args.seed, max_pos, act_q8,
+                                      q3h.F32 if f32w else q3h.Q8_0)
     if args.gemv_only:
         roofline = gemv_roofline(ts, args)
         print(json.dumps({"roofline": roofline}), flush=True)
@@ -298,9 +312,10 @@ def main():
     total, lat, codes = run_gpu(frame, pre, steps, warmup)
     fps = n * steps / total
     log(f"{fps:.1f} frames/s, {1e3 * total / steps:.3f} ms per step "
-        f"(p50 {1e6 * np.median(lat):.0f} us, p99 {1e6 * np.percentile(lat, 99):.0f} us)")
+        f"(p50 {1e6 * np.median(lat):.0f} us, p99 {1e6 * np.percentile(lat, 99):.0f} us); "
+        f"prefill of {n} stream(s) {1e3 * run_gpu.prefill_s:.1f} ms")
 
-    roofline = gemv_roofline(ts, args)
+    roofline = gemv_roofline(ts, args) if not f32w else None
 
     frame.destroy()
     long_attn = None
@@ -310,7 +325,8 @@ def main():
     cpu = None
     parity = None
     if not args.no_cpu:
-        cpu, nf, equal = cpu_baseline(f32, tables, pre, codes, args.cpu_seconds, steps, act_q8)
+        cpu, nf, equal = cpu_baseline(f32, tables, pre, codes, args.cpu_seconds, steps, act_q8,
+                                      f32w)
         parity = dict(frames=nf, codes_equal_stream0=bool(equal))
         log(f"cpu baseline: {cpu['value']:.2f} frames/s on {cpu['cores']} threads; "
             f"codes equal over {nf} frames: {equal}")
@@ -333,10 +349,11 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded N(0,0.02) weights, N(0,1) prompt embeddings)",
         "config": {"workload": args.workload, "graph": not args.no_graph, "streams": n, "prompt_rows":
-                   PROMPT_ROWS if b1 else "U[16,256]", "frames": steps,
-                   "talker_layers": 28, "cp_layers": 5, "hidden": 1024,
-                   "heads": "16q/8kv x 128", "ffn": 3072, "weights": "Q8_0", "kv": "f32",
-                   "activations": "q8_0 (int8 MFMA)" if act_q8 else "f32"},
+                   PROMPT_ROWS if b1 else (F32_PROMPT_ROWS if f32w else "U[16,256]"),
+                   "frames": steps, "talker_layers": 28, "cp_layers": 5, "hidden": 1024,
+                   "heads": "16q/8kv x 128", "ffn": 3072, "weights": "f32" if f32w else "Q8_0",
+                   "kv": "f32", "activations": "q8_0 (int8 MFMA)" if act_q8 else "f32"},
+        "prefill_ms": round(1e3 * run_gpu.prefill_s, 2),
         "step_us_p50": round(1e6 * float(np.median(lat)), 1),
         "step_us_p99": round(1e6 * float(np.percentile(lat, 99)), 1),
         "roofline": roofline,

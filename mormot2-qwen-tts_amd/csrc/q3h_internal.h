@@ -76,6 +76,12 @@ void launch_gemv(const GemvArgs &a, int epi, bool q8, hipStream_t st);
 // false when the shape is not one it takes (nothing launched)
 bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st, hipEvent_t ev0 = nullptr,
                          hipEvent_t ev1 = nullptr);
+// the f32 matrix-core products (q3h_gemm_f32.hip): y[m][n] (+)= W[n] . x[m]
+// for f32 W [N][K] (N % 16 == 0, K in {1024, 2048, 3072}); epi EPI_* (SwiGLU:
+// interleaved gate / up rows, y [M][N / 2])
+bool gemm_f32_supported(int N, int K);
+void launch_gemm_f32(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
+                     hipStream_t st);
 // the int8 path (q3h_gemm.hip): shapes it takes (N % 16 == 0, K % 256 == 0,
 // K <= 3072)
 bool gemm_i8_supported(int N, int K);

@@ -4,6 +4,7 @@ every frame, talker logits within 1e-3 (max-abs relative)."""
 import numpy as np
 import pytest
 
+import q3h
 from models import Model, rel
 
 pytestmark = pytest.mark.gpu
@@ -124,3 +125,43 @@ def test_frame_eos_ends_a_stream(small, synth):
     assert alive[0] == 0 and alive[1] == 1
     fr.destroy()
     of.destroy()
+
+
+def test_f32_prefill_512_and_batch8_frames(device, synth):
+    """The f32-weight path at the shapes of the batch-8 f32 workload (2 talker
+    layers and 1 code-predictor layer at full width): prefills of 512 and
+    ragged rows (matrix-core products over 16-row tiles, row counts that are
+    not multiples of 16), then batched frames of 8 streams (products over 8
+    and 16 rows), against the f32 oracle: identical codes, talker logits and
+    states within 1e-4 (the reference's f32 GPU-vs-CPU bar,
+    tests/test.tts.qwen.vulkan.pas:226-231)."""
+    m = Model(device, seed=21, talker_layers=2, cp_layers=1, dtype=q3h.F32, norm_std=0.1,
+              max_positions=600)
+    lens = [512, 300, 17, 64, 100, 5, 250, 33]
+    fr = m.frame(n_streams=len(lens), max_positions=600, max_frames=8)
+    ofs = []
+    try:
+        for s, n in enumerate(lens):
+            print(f"prefill stream {s}: {n} rows", flush=True)
+            pre = synth.prompt(500 + s, n)
+            fr.start(s, pre)
+            of = m.oracle_frame(max_positions=600)
+            of.start(pre)
+            ofs.append(of)
+            lg, past = fr.state(s)
+            olg, opast = of.state()
+            assert rel(lg, olg) < 1e-4 and rel(past, opast) < 1e-4, (s, rel(lg, olg))
+        for i in range(3):
+            codes, alive = fr.step()
+            print(f"frame {i}", flush=True)
+            for s, of in enumerate(ofs):
+                ref = of.next()
+                assert np.array_equal(codes[s], ref), (i, s, codes[s], ref)
+                lg, past = fr.state(s)
+                olg, opast = of.state()
+                assert rel(lg, olg) < 1e-4 and rel(past, opast) < 1e-4, (i, s, rel(lg, olg))
+    finally:
+        fr.destroy()
+        for of in ofs:
+            of.destroy()
+        m.destroy()
