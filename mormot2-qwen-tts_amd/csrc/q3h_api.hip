@@ -70,6 +70,9 @@ void Work::ensure(const q3h_stack *s, int rows, int splits, int head_rows) {
     pn = std::max(pn, (size_t)gemm_i8_chunks(NQ) * pr * H);
     pn = std::max(pn, (size_t)gemm_i8_chunks(I) * pr * H);
     gpart = (float *)dev_alloc(sizeof(float) * pn);
+  } else if (c.dtype == Q3H_F32) {
+    // K-slice sums of the f32 products over up to 16 rows
+    gpart = (float *)dev_alloc(sizeof(float) * kF32Slices * std::min<size_t>(R, 16) * H);
   }
 }
 
@@ -183,6 +186,55 @@ static void run_layers_partial(const q3h_stack *s, Work &w, int M, bool fused,
   }
 }
 
+// f32 stacks over a few rows (batched decode): the matrix-core products, with
+// o_proj and down (N = hidden, 64 tiles of 16 rows) cut into K slices so that
+// they fill the chip; each slice sum is added to the residual in slice order
+// by the kernel that also applies the next RMSNorm, whose output feeds the
+// next product directly.
+bool f32_slice_path(const q3h_stack *s, int M) {
+  const q3h_stack_config &c = s->cfg;
+  const int NQ = c.heads * c.head_dim, I = c.intermediate, H = c.hidden;
+  const int ldq = NQ + 2 * c.kv_heads * c.head_dim;
+  return c.dtype == Q3H_F32 && !c.act_q8 && M <= 16 && gemm_f32_supported(ldq, H) &&
+         gemm_f32_supported(2 * I, H) && gemm_f32_slices_supported(H, NQ) &&
+         gemm_f32_slices_supported(H, I);
+}
+
+static void run_layers_f32(const q3h_stack *s, Work &w, int M, int positions, bool fused,
+                           hipStream_t st) {
+  const q3h_stack_config &c = s->cfg;
+  const int H = c.hidden, hd = c.head_dim, NQ = c.heads * hd, NKV = c.kv_heads * hd;
+  const int I = c.intermediate, ldq = NQ + 2 * NKV;
+  const bool kv16 = c.kv_f16 != 0;
+  const float eps = c.rms_eps;
+  launch_rmsnorm_rows(w.h, H, M, H, s->layers[0].in_norm, eps, w.normed, H, st);
+  for (int l = 0; l < c.layers; l++) {
+    const Layer &L = s->layers[l];
+    launch_gemm_f32(L.qkv, w.normed, H, M, EPI_STORE, w.qkv, ldq, st);
+    if (!fused)
+      launch_qk_rope_append(w.qkv, ldq, w.rd, M, l, c.heads, c.kv_heads, hd, L.q_norm,
+                            L.k_norm, eps, s->rope_cs, kv16, st);
+    AttnArgs at{};
+    at.qkv = w.qkv;
+    at.ldq = ldq;
+    at.rd = w.rd;
+    at.layer = l;
+    at.heads = c.heads;
+    at.kvh = c.kv_heads;
+    at.qkn = L.q_norm;
+    at.rope_cs = reinterpret_cast<const float2 *>(s->rope_cs);
+    at.out = w.att;
+    at.part = w.part;
+    launch_attn(at, M, positions, fused, kv16, st);
+    launch_gemm_f32_part(L.o, w.att, NQ, M, w.gpart, st);
+    launch_resid_norm(w.h, w.gpart, M, H, L.post_norm, eps, w.normed, st);
+    launch_gemm_f32(L.gu, w.normed, H, M, EPI_SWIGLU, w.act, I, st);
+    launch_gemm_f32_part(L.down, w.act, I, M, w.gpart, st);
+    const float *next = l + 1 < c.layers ? s->layers[l + 1].in_norm : nullptr;
+    launch_resid_norm(w.h, w.gpart, M, H, next, eps, w.normed, st);
+  }
+}
+
 // The layers of a stack over M rows of w.h, n contexts of R rows each (M =
 // n * R), their descriptors already in w.rd: the per-layer kernel sequence.
 bool partial_path(const q3h_stack *s, int M) {
@@ -197,6 +249,10 @@ void run_layers(const q3h_stack *s, Work &w, int M, int positions, bool fused, h
   const bool kv16 = c.kv_f16 != 0;
   if (partial_path(s, M)) {
     run_layers_partial(s, w, M, fused, io, st);
+    return;
+  }
+  if (f32_slice_path(s, M)) {
+    run_layers_f32(s, w, M, positions, fused, st);
     return;
   }
   for (int l = 0; l < c.layers; l++) {

@@ -36,18 +36,21 @@ __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast
 
 __device__ __forceinline__ float silu_mul_f(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
-template <int TM, int K, int EPI>
-__global__ __launch_bounds__(64 * (K / KC)) void k_gemm_f32(const float *__restrict__ w,
-                                                            const float *__restrict__ x, int ldx,
-                                                            int M, int N, float *__restrict__ y,
-                                                            int ldy) {
-  constexpr int KW = K / KC;   // waves
+// KK: the columns of one workgroup (K / gridDim.z; 256 per wave), K: the
+// row stride of W. EPI_PART: the workgroup's sums go to slice blockIdx.z of
+// y [gridDim.z][M][ldy] for a consumer that adds the slices in order.
+template <int TM, int KK, int EPI>
+__global__ __launch_bounds__(64 * (KK / KC)) void k_gemm_f32(const float *__restrict__ w,
+                                                             const float *__restrict__ x,
+                                                             int ldx, int M, int N, int K,
+                                                             float *__restrict__ y, int ldy) {
+  constexpr int KW = KK / KC;  // waves
   constexpr int ST = KC / 16;  // 16-column steps per wave
   __shared__ float red[KW][TM][4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n0 = blockIdx.x * 16, m0 = blockIdx.y * (TM * 16);
   const int r = lane & 15, g = lane >> 4;
-  const int kb = wave * KC + 4 * g;
+  const int kb = blockIdx.z * KK + wave * KC + 4 * g;
   const float *wr = w + (size_t)min(n0 + r, N - 1) * K + kb;
   const float *xr[TM];
 #pragma unroll
@@ -111,34 +114,73 @@ __global__ __launch_bounds__(64 * (K / KC)) void k_gemm_f32(const float *__restr
       if ((l & 1) == 0) y[(size_t)m * ldy + n / 2] = silu_mul_f(v, u);
     } else if (EPI == EPI_ADD) {
       y[(size_t)m * ldy + n] += v;
+    } else if (EPI == EPI_PART) {
+      y[((size_t)blockIdx.z * M + m) * ldy + n] = v;
     } else {
       y[(size_t)m * ldy + n] = v;
     }
   }
 }
 
-template <int TM, int K>
-void launch_tk(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
+// h[m] += slices 0 .. S-1 of part [S][M][K], added in slice order; then, with
+// a norm weight, xn[m] = w * (h[m] * inv), inv = 1 / sqrt(mean(h[m]^2) + eps)
+// (sum of squares in double). One workgroup per row.
+template <int S>
+__global__ __launch_bounds__(256) void k_resid_norm(float *__restrict__ h,
+                                                    const float *__restrict__ part, int M,
+                                                    int K, const float *__restrict__ w,
+                                                    float eps, float *__restrict__ xn) {
+  __shared__ double red[4];
+  const int m = blockIdx.x, t = threadIdx.x;
+  float *hr = h + (size_t)m * K;
+  double ss = 0.0;
+  for (int k = t; k < K; k += 256) {
+    float a[S];
+#pragma unroll
+    for (int s = 0; s < S; s++) a[s] = part[((size_t)s * M + m) * K + k];
+    float v = hr[k];
+#pragma unroll
+    for (int s = 0; s < S; s++) v += a[s];
+    hr[k] = v;
+    ss += (double)v * v;
+  }
+  if (w == nullptr) return;
+  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+  if ((t & 63) == 0) red[t >> 6] = ss;
+  __syncthreads();
+  const double tot = red[0] + red[1] + red[2] + red[3];
+  const float inv = (float)(1.0 / sqrt(tot / K + (double)eps));
+  for (int k = t; k < K; k += 256) xn[(size_t)m * K + k] = w[k] * (hr[k] * inv);
+}
+
+template <int TM, int KK>
+void launch_tk(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy, int ks,
                hipStream_t st) {
-  const dim3 grid(W.N / 16, (M + 16 * TM - 1) / (16 * TM)), block(64 * (K / KC));
+  const dim3 grid(W.N / 16, (M + 16 * TM - 1) / (16 * TM), ks), block(64 * (KK / KC));
+#define Q3H_G(E)                                                                              \
+  hipLaunchKernelGGL((k_gemm_f32<TM, KK, E>), grid, block, 0, st, W.f, x, ldx, M, W.N, W.K, y, \
+                     ldy)
   if (epi == EPI_STORE)
-    hipLaunchKernelGGL((k_gemm_f32<TM, K, EPI_STORE>), grid, block, 0, st, W.f, x, ldx, M, W.N,
-                       y, ldy);
+    Q3H_G(EPI_STORE);
   else if (epi == EPI_ADD)
-    hipLaunchKernelGGL((k_gemm_f32<TM, K, EPI_ADD>), grid, block, 0, st, W.f, x, ldx, M, W.N, y,
-                       ldy);
+    Q3H_G(EPI_ADD);
+  else if (epi == EPI_SWIGLU)
+    Q3H_G(EPI_SWIGLU);
   else
-    hipLaunchKernelGGL((k_gemm_f32<TM, K, EPI_SWIGLU>), grid, block, 0, st, W.f, x, ldx, M, W.N,
-                       y, ldy);
+    Q3H_G(EPI_PART);
+#undef Q3H_G
 }
 
 template <int TM>
-void launch_t(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
+void launch_t(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy, int ks,
               hipStream_t st) {
-  switch (W.K) {
-    case 1024: launch_tk<TM, 1024>(W, x, ldx, M, epi, y, ldy, st); break;
-    case 2048: launch_tk<TM, 2048>(W, x, ldx, M, epi, y, ldy, st); break;
-    default: launch_tk<TM, 3072>(W, x, ldx, M, epi, y, ldy, st); break;
+  switch (W.K / ks) {
+    case 256: launch_tk<TM, 256>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 512: launch_tk<TM, 512>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 768: launch_tk<TM, 768>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 1024: launch_tk<TM, 1024>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 2048: launch_tk<TM, 2048>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    default: launch_tk<TM, 3072>(W, x, ldx, M, epi, y, ldy, ks, st); break;
   }
 }
 
@@ -151,11 +193,27 @@ bool gemm_f32_supported(int N, int K) {
 void launch_gemm_f32(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
                      hipStream_t st) {
   if (M <= 16)
-    launch_t<1>(W, x, ldx, M, epi, y, ldy, st);
+    launch_t<1>(W, x, ldx, M, epi, y, ldy, 1, st);
   else if (M <= 32)
-    launch_t<2>(W, x, ldx, M, epi, y, ldy, st);
+    launch_t<2>(W, x, ldx, M, epi, y, ldy, 1, st);
   else
-    launch_t<4>(W, x, ldx, M, epi, y, ldy, st);
+    launch_t<4>(W, x, ldx, M, epi, y, ldy, 1, st);
+}
+
+bool gemm_f32_slices_supported(int N, int K) {
+  const int kk = K / kF32Slices;
+  return N % 16 == 0 && K % kF32Slices == 0 && (kk == 256 || kk == 512 || kk == 768 || kk == 1024);
+}
+
+void launch_gemm_f32_part(const Mat &W, const float *x, int ldx, int M, float *part,
+                          hipStream_t st) {
+  launch_t<1>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
+}
+
+void launch_resid_norm(float *h, const float *part, int M, int K, const float *norm_w,
+                       float eps, float *xn, hipStream_t st) {
+  hipLaunchKernelGGL(k_resid_norm<kF32Slices>, dim3(M), dim3(256), 0, st, h, part, M, K, norm_w,
+                     eps, xn);
 }
 
 }  // namespace q3h

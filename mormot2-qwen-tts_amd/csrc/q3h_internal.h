@@ -37,7 +37,8 @@ struct CtxDev {
   int len;
 };
 
-enum Epi { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2 };
+// EPI_PART (f32 matrix-core products only): sums to a slice of a partial buffer
+enum Epi { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2, EPI_PART = 3 };
 
 struct GemvArgs {
   const int8_t *wq;
@@ -82,6 +83,18 @@ bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st, hipEvent_t 
 bool gemm_f32_supported(int N, int K);
 void launch_gemm_f32(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
                      hipStream_t st);
+// the same over M <= 16 rows with K cut into kF32Slices slices, one
+// workgroup per (16 rows, slice): the slices' sums go to part
+// [kF32Slices][M][N] (fills the chip when N / 16 is small)
+constexpr int kF32Slices = 4;
+bool gemm_f32_slices_supported(int N, int K);
+void launch_gemm_f32_part(const Mat &W, const float *x, int ldx, int M, float *part,
+                          hipStream_t st);
+// h [M][K] += the kF32Slices slices of part, in slice order; then, when
+// norm_w != nullptr, xn [M][K] = RMSNorm(h) with norm_w (double sum of
+// squares)
+void launch_resid_norm(float *h, const float *part, int M, int K, const float *norm_w,
+                       float eps, float *xn, hipStream_t st);
 // the int8 path (q3h_gemm.hip): shapes it takes (N % 16 == 0, K % 256 == 0,
 // K <= 3072)
 bool gemm_i8_supported(int N, int K);
