@@ -201,7 +201,7 @@ bool f32_slice_path(const q3h_stack *s, int M) {
 }
 
 static void run_layers_f32(const q3h_stack *s, Work &w, int M, int positions, bool fused,
-                           hipStream_t st) {
+                           bool single_context, hipStream_t st) {
   const q3h_stack_config &c = s->cfg;
   const int H = c.hidden, hd = c.head_dim, NQ = c.heads * hd, NKV = c.kv_heads * hd;
   const int I = c.intermediate, ldq = NQ + 2 * NKV;
@@ -225,7 +225,10 @@ static void run_layers_f32(const q3h_stack *s, Work &w, int M, int positions, bo
     at.rope_cs = reinterpret_cast<const float2 *>(s->rope_cs);
     at.out = w.att;
     at.part = w.part;
-    launch_attn(at, M, positions, fused, kv16, st);
+    if (!fused && single_context && M >= kPrefillRows)
+      launch_attn_prefill(at, M, kv16, st);
+    else
+      launch_attn(at, M, positions, fused, kv16, st);
     launch_gemm_f32_part(L.o, w.att, NQ, M, w.gpart, st);
     launch_resid_norm(w.h, w.gpart, M, H, L.post_norm, eps, w.normed, st);
     launch_gemm_f32(L.gu, w.normed, H, M, EPI_SWIGLU, w.act, I, st);
@@ -252,7 +255,7 @@ void run_layers(const q3h_stack *s, Work &w, int M, int positions, bool fused, h
     return;
   }
   if (f32_slice_path(s, M)) {
-    run_layers_f32(s, w, M, positions, fused, st);
+    run_layers_f32(s, w, M, positions, fused, io.single_context, st);
     return;
   }
   for (int l = 0; l < c.layers; l++) {
@@ -295,7 +298,10 @@ void run_layers(const q3h_stack *s, Work &w, int M, int positions, bool fused, h
     at.rope_cs = reinterpret_cast<const float2 *>(s->rope_cs);
     at.out = w.att;
     at.part = w.part;
-    launch_attn(at, M, positions, fused, kv16, st);
+    if (!fused && io.single_context && M >= kPrefillRows)
+      launch_attn_prefill(at, M, kv16, st);
+    else
+      launch_attn(at, M, positions, fused, kv16, st);
     // o_proj + residual
     linear(s, w, L.o, w.att, NQ, M, nullptr, w.h, H, EPI_ADD, nullptr, st);
     // RMSNorm + gate/up + SwiGLU
@@ -929,7 +935,9 @@ extern "C" int q3h_forward_embeds(q3h_context *c, const float *x, int rows, int 
     check_hip(hipMemcpyAsync(w.h, x, sizeof(float) * rows * H, hipMemcpyHostToDevice, st),
               "upload x");
     launch_prep(c->dev_arr, nullptr, 1, rows, w.rd, st);
-    run_layers(s, w, rows, positions, rows == 1, st);
+    LayerIO io;
+    io.single_context = true;
+    run_layers(s, w, rows, positions, rows == 1, st, io);
     // final norm of the last row, fused into the head product when there is one
     if (head >= 0) {
       linear(s, w, s->heads[head], w.h + (size_t)(rows - 1) * H, H, 1, s->final_norm, w.logits,

@@ -100,10 +100,11 @@ bool cp_fused_supported(const q3h_stack_config &c);
 void run_cp_fused(const struct ::q3h_stack *s, Work &w, const struct ::q3h_context *ctx,
                   int pos, hipStream_t st);
 
-// options of run_layers for the int8 path over few rows (partial_path)
+// options of run_layers (the first two: the int8 path over few rows, partial_path)
 struct LayerIO {
   bool input_quantized = false;       // w.xa already holds layer 0's normed, quantized input
   const float *final_norm = nullptr;  // after the last layer: RMSNorm with it, quantized into w.xa
+  bool single_context = false;        // the rows are consecutive positions of one context
 };
 // whether run_layers takes the int8 partial-product path for M rows of stack s
 bool partial_path(const struct ::q3h_stack *s, int M);

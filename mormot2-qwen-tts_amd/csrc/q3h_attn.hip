@@ -595,6 +595,147 @@ __global__ __launch_bounds__(1024) void k_attn_merge(const RowDesc *__restrict__
   }
 }
 
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// 4 cache elements as f32 (16 bytes of f32, 8 of f16)
+__device__ __forceinline__ float4 ld4kv(const float *p) {
+  return *reinterpret_cast<const float4 *>(p);
+}
+__device__ __forceinline__ float4 ld4kv(const _Float16 *p) {
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  const h4 v = *reinterpret_cast<const h4 *>(p);
+  return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
+}
+
+// Prefill attention (rows m = 0 .. M-1 of one context at positions pos0 + m,
+// their keys and values already in the cache, q already normed and rotated):
+// causal softmax(q K^T / sqrt(128)) V on the matrix cores,
+// v_mfma_f32_16x16x4_f32 (fp32 operands and sums).
+// One workgroup of 4 waves per (query head h, tile of 16 query rows); wave w
+// takes the key blocks w, w + 4, ... (16 positions each) up to the tile's
+// last position and keeps its own running maximum, sum and output:
+//   - scores S^T = K Q^T: A = 16 keys, B = the 16 queries (both loaded 16
+//     bytes per lane, columns 4 (l / 16) .. + 3 of each 16-dim step, as the
+//     f32 products do); lane l receives S[query l % 16][key 4 (l / 16) + r];
+//   - online softmax per query (the 16 keys of a block are the 4 registers
+//     of lanes l, l ^ 16, l ^ 32, l ^ 48); keys after the query's position
+//     are masked;
+//   - O += P V: lane l's scores are already P in the A layout (query l % 16,
+//     k slot l / 16 = key 4 (l / 16) + r for k step r), B = V[key][dim]; the
+//     output tile (query 4 (l / 16) + r, dim 16 t + l % 16) is rescaled by
+//     the factor of its query, read from lane 4 (l / 16) + r;
+//   - the 4 waves' (max, sum, output) merged in LDS.
+template <typename KV, int GRP>
+__global__ __launch_bounds__(256) void k_attn_prefill(const RowDesc *__restrict__ rd,
+                                                      const float *__restrict__ qkv, int ldq,
+                                                      int layer, int kvh, int M,
+                                                      float *__restrict__ outp) {
+  __shared__ float ms[4][16], ls[4][16];
+  __shared__ float os[4][8][4][64];
+  const int h = blockIdx.x, q0 = blockIdx.y * 16, g = h / GRP;
+  const int heads = GRP * kvh;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int r16 = lane & 15, gq = lane >> 4;
+  const RowDesc d = rd[0];
+  const int pos0 = d.pos;
+  const int p_hi = pos0 + min(q0 + 15, M - 1);  // the tile's last position
+  const int pq = pos0 + q0 + r16;              // this lane's query position
+  const size_t head_off = ((size_t)layer * kvh + g) * d.max_pos * HD;
+  const KV *kc = reinterpret_cast<const KV *>(d.k) + head_off;
+  const KV *vc = reinterpret_cast<const KV *>(d.v) + head_off;
+  // this lane's query: row min(q0 + r16, M - 1), dims 16 s + 4 gq .. + 3
+  const float *qr = qkv + (size_t)min(q0 + r16, M - 1) * ldq + h * HD + 4 * gq;
+  float4 qf[8];
+#pragma unroll
+  for (int s = 0; s < 8; s++) qf[s] = *reinterpret_cast<const float4 *>(qr + 16 * s);
+  const float scale = (float)(1.0 / sqrt((double)HD));
+  float m_run = -INFINITY, l_run = 0.f;
+  v4f o[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) o[i] = v4f{0.f, 0.f, 0.f, 0.f};
+  const int nblk = p_hi / 16 + 1;
+  for (int b = wave; b < nblk; b += 4) {
+    const int kb = 16 * b;
+    float4 kf[8];
+    const KV *kr = kc + (size_t)min(kb + r16, p_hi) * HD + 4 * gq;
+#pragma unroll
+    for (int s = 0; s < 8; s++) kf[s] = ld4kv(kr + 16 * s);
+    float vv[4][8];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const KV *vr = vc + (size_t)min(kb + 4 * gq + r, p_hi) * HD + r16;
+#pragma unroll
+      for (int i = 0; i < 8; i++) vv[r][i] = (float)vr[16 * i];
+    }
+    v4f sa = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+      sa = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s].x, qf[s].x, sa, 0, 0, 0);
+      sa = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s].y, qf[s].y, sa, 0, 0, 0);
+      sa = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s].z, qf[s].z, sa, 0, 0, 0);
+      sa = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s].w, qf[s].w, sa, 0, 0, 0);
+    }
+    float sc[4], bm = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      sc[r] = kb + 4 * gq + r <= pq ? sa[r] * scale : -INFINITY;
+      bm = fmaxf(bm, sc[r]);
+    }
+    bm = fmaxf(bm, __shfl_xor(bm, 16));
+    bm = fmaxf(bm, __shfl_xor(bm, 32));
+    const float m_new = fmaxf(m_run, bm);
+    const float ref = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = m_run == -INFINITY ? 0.f : __expf(m_run - ref);
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      sc[r] = __expf(sc[r] - ref);
+      ps += sc[r];
+    }
+    ps += __shfl_xor(ps, 16);
+    ps += __shfl_xor(ps, 32);
+    l_run = fmaf(l_run, alpha, ps);
+    m_run = m_new;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float ar = __shfl(alpha, 4 * gq + r);
+#pragma unroll
+      for (int i = 0; i < 8; i++) o[i][r] *= ar;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(sc[r], vv[r][i], o[i], 0, 0, 0);
+  }
+  if (gq == 0) {
+    ms[wave][r16] = m_run;
+    ls[wave][r16] = l_run;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) os[wave][i][r][lane] = o[i][r];
+  __syncthreads();
+  // output (query q, dim k): tile i = k / 16, lane 16 (q / 4) + k % 16, r = q % 4
+  for (int e = t; e < 16 * HD; e += 256) {
+    const int q = e / HD, k = e % HD;
+    if (q0 + q >= M) break;
+    const int i = k >> 4, l = 16 * (q >> 2) + (k & 15), r = q & 3;
+    float mx = ms[0][q];
+#pragma unroll
+    for (int w = 1; w < 4; w++) mx = fmaxf(mx, ms[w][q]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+      const float c = ms[w][q] == -INFINITY ? 0.f : __expf(ms[w][q] - mx);
+      num = fmaf(os[w][i][r][l], c, num);
+      den = fmaf(ls[w][q], c, den);
+    }
+    outp[(size_t)(q0 + q) * (heads * HD) + h * HD + k] = den > 0.f ? num / den : 0.f;
+  }
+}
+
 #define Q3H_LAUNCH(KERNEL, GRID, BLOCK, ST, EV0, EV1, ...)                                      \
   do {                                                                                          \
     if (EV0)                                                                                    \
@@ -670,4 +811,24 @@ int launch_attn(const AttnArgs &a, int M, int positions, bool fused, bool kv16, 
                : launch_kv<float, false>(a, M, positions, st, ev);
 }
 
+}  // namespace q3h
+
+namespace q3h {
+void launch_attn_prefill(const AttnArgs &a, int M, bool kv16, hipStream_t st) {
+  const dim3 grid(a.heads, (M + 15) / 16), block(256);
+  const int grp = a.heads / a.kvh;
+#define Q3H_P(KV, G)                                                                         \
+  hipLaunchKernelGGL((k_attn_prefill<KV, G>), grid, block, 0, st, a.rd, a.qkv, a.ldq, a.layer, \
+                     a.kvh, M, a.out)
+  if (kv16) {
+    if (grp == 1) Q3H_P(_Float16, 1);
+    else if (grp == 2) Q3H_P(_Float16, 2);
+    else Q3H_P(_Float16, 4);
+  } else {
+    if (grp == 1) Q3H_P(float, 1);
+    else if (grp == 2) Q3H_P(float, 2);
+    else Q3H_P(float, 4);
+  }
+#undef Q3H_P
+}
 }  // namespace q3h

@@ -544,7 +544,9 @@ extern "C" int q3h_frame_start(q3h_frame *f, int stream, const float *prefill, i
     check_hip(hipMemcpyAsync(w.h, prefill, sizeof(float) * rows * H, hipMemcpyHostToDevice, st),
               "upload prefill");
     launch_prep(tc->dev_arr, nullptr, 1, rows, w.rd, st);
-    run_layers(s, w, rows, rows, rows == 1, st);
+    LayerIO io;
+    io.single_context = true;
+    run_layers(s, w, rows, rows, rows == 1, st, io);
     float *past = d.past + (size_t)stream * H;
     linear(s, w, s->heads[c.talker_head], w.h + (size_t)(rows - 1) * H, H, 1, s->final_norm,
            d.logits + (size_t)stream * c.vocab, c.vocab, EPI_STORE, past, st);

@@ -108,6 +108,8 @@ void launch_gemm_i8(const Mat &W, const QAct &xa, int M, int epi, float *y, int 
 // the same chains for M <= kPartialRows, one wave per (16 rows, chunk):
 // part[gemm_i8_chunks(K)][M][N], to be added in chunk order by the consumer
 constexpr int kPartialRows = 64;
+// rows from which a one-context forward takes the matrix-core prefill attention
+constexpr int kPrefillRows = 16;
 int gemm_i8_chunks(int K);
 void launch_gemm_i8_partial(const Mat &W, const QAct &xa, int M, float *part, hipStream_t st);
 // h [M][K] += the chunk partials of a product (in chunk order); then RMSNorm
@@ -157,6 +159,9 @@ SplitShape attn_split_shape(int positions, bool kv16);
 // partial-buffer slots per (row, query head): the splits and the query head
 // (1 when one workgroup covers the context)
 int attn_splits(int positions, bool kv16);
+// prefill attention on the matrix cores: the M rows of one context at
+// positions rd[0].pos + m, their K/V already appended, q normed and rotated
+void launch_attn_prefill(const AttnArgs &a, int M, bool kv16, hipStream_t st);
 // the most positions the split kernel merges (splits per kv head are bounded)
 int attn_max_positions(bool kv16);
 // positions: the most positions any of the M rows attends to (its own
