@@ -116,9 +116,12 @@ void linear(const q3h_stack *s, Work &w, const Mat &W, const float *x, int ldx, 
   if (c.act_q8) {
     launch_quantize_act(x, ldx, M, W.K, norm_w, c.rms_eps, w.xa, xn_out, st);
     launch_gemm_i8(W, w.xa, M, epi, y, ldy, st);
-  } else if (c.dtype == Q3H_F32 && gemm_f32_supported(W.N, W.K) && (xn_out == nullptr || M == 1)) {
-    // f32 weights on the matrix cores, the RMSNorm of the rows first (into
-    // the work buffer, or into xn_out, the one row the caller wants back)
+  } else if ((c.dtype == Q3H_F32 || M > kGemvRows) && gemm_f32_supported(W.N, W.K) &&
+             (xn_out == nullptr || M == 1)) {
+    // f32 weights (or Q8_0 weights over more rows than the matrix-vector
+    // kernels take in one pass) on the matrix cores, with f32 activations; the
+    // RMSNorm of the rows first (into the work buffer, or into xn_out, the one
+    // row the caller wants back)
     if (norm_w) {
       float *xn = xn_out ? xn_out : w.normed;
       launch_rmsnorm_rows(x, ldx, M, W.K, norm_w, c.rms_eps, xn, W.K, st);

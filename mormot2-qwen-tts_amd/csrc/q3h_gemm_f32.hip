@@ -36,6 +36,35 @@ __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast
 
 __device__ __forceinline__ float silu_mul_f(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
+// the sums of a tile, met in LDS (red[wave][t][q][lane]: the MFMA result
+// layout), added in wave order and stored / added / SwiGLU'd / kept as a slice
+template <int TM, int KW, int EPI>
+__device__ __forceinline__ void epilogue(const float (&red)[KW][TM][4][64], int m0, int n0, int M,
+                                         float *__restrict__ y, int ldy) {
+  // output (m, n) of this tile: t, lane' = 16 (m / 4 % 4) + n % 16, q = m % 4
+  for (int o = threadIdx.x; o < TM * 256; o += 64 * KW) {
+    const int t = o >> 8, q = (o >> 6) & 3, l = o & 63;
+    const int m = m0 + 16 * t + 4 * (l >> 4) + q, n = n0 + (l & 15);
+    if (m >= M) continue;
+    float v = 0.f;
+#pragma unroll
+    for (int i = 0; i < KW; i++) v += red[i][t][q][l];
+    if (EPI == EPI_SWIGLU) {
+      // gate in even rows, up in the odd row after it (the next lane)
+      float u = 0.f;
+#pragma unroll
+      for (int i = 0; i < KW; i++) u += red[i][t][q][l ^ 1];
+      if ((l & 1) == 0) y[(size_t)m * ldy + n / 2] = silu_mul_f(v, u);
+    } else if (EPI == EPI_ADD) {
+      y[(size_t)m * ldy + n] += v;
+    } else if (EPI == EPI_PART) {
+      y[((size_t)blockIdx.z * M + m) * ldy + n] = v;
+    } else {
+      y[(size_t)m * ldy + n] = v;
+    }
+  }
+}
+
 // KK: the columns of one workgroup (K / gridDim.z; 256 per wave), K: the
 // row stride of W. EPI_PART: the workgroup's sums go to slice blockIdx.z of
 // y [gridDim.z][M][ldy] for a consumer that adds the slices in order.
@@ -98,28 +127,87 @@ __global__ __launch_bounds__(64 * (KK / KC)) void k_gemm_f32(const float *__rest
     for (int q = 0; q < 4; q++) red[wave][t][q][lane] = acc[t][q];
   __syncthreads();
 
-  // output (m, n) of this tile: t, lane' = 16 (m / 4 % 4) + n % 16, q = m % 4
-  for (int o = threadIdx.x; o < TM * 256; o += 64 * KW) {
-    const int t = o >> 8, q = (o >> 6) & 3, l = o & 63;
-    const int m = m0 + 16 * t + 4 * (l >> 4) + q, n = n0 + (l & 15);
-    if (m >= M) continue;
-    float v = 0.f;
+  epilogue<TM, KW, EPI>(red, m0, n0, M, y, ldy);
+}
+
+// The same products with Q8_0 weights (int8 quants [N][K], then fp16 scales
+// [N][K/32]) and f32 activations: a 64-column step per load, lane l taking
+// the 16 quants 16 (l / 16) .. + 15 of its row (one 16-byte load) and the
+// scale of their 32-block, the 16 activations of the same columns of its
+// activation row (four 16-byte loads); MFMA i of the step takes column
+// 16 (l / 16) + i in k slot l / 16, the weight as quant x scale in fp32 (the
+// dequantized weight, exactly). The epilogues are those of k_gemm_f32.
+template <int TM, int KK, int EPI>
+__global__ __launch_bounds__(64 * (KK / KC)) void k_gemm_q8f(const int8_t *__restrict__ wq,
+                                                             const float *__restrict__ x,
+                                                             int ldx, int M, int N, int K,
+                                                             float *__restrict__ y, int ldy) {
+  constexpr int KW = KK / KC;  // waves
+  constexpr int ST = KC / 64;  // 64-column steps per wave
+  constexpr int D = TM == 1 ? ST : 2;
+  __shared__ float red[KW][TM][4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n0 = blockIdx.x * 16, m0 = blockIdx.y * (TM * 16);
+  const int r = lane & 15, g = lane >> 4;
+  const int kb = blockIdx.z * KK + wave * KC + 16 * g;
+  const int row = min(n0 + r, N - 1);
+  const int8_t *wr = wq + (size_t)row * K + kb;
+  const _Float16 *dr = reinterpret_cast<const _Float16 *>(wq + (size_t)N * K) + (size_t)row * (K / 32) +
+                       kb / 32;
+  const float *xr[TM];
 #pragma unroll
-    for (int i = 0; i < KW; i++) v += red[i][t][q][l];
-    if (EPI == EPI_SWIGLU) {
-      // gate in even rows, up in the odd row after it (the next lane)
-      float u = 0.f;
+  for (int t = 0; t < TM; t++) xr[t] = x + (size_t)min(m0 + 16 * t + r, M - 1) * ldx + kb;
+
+  v4f acc[TM];
 #pragma unroll
-      for (int i = 0; i < KW; i++) u += red[i][t][q][l ^ 1];
-      if ((l & 1) == 0) y[(size_t)m * ldy + n / 2] = silu_mul_f(v, u);
-    } else if (EPI == EPI_ADD) {
-      y[(size_t)m * ldy + n] += v;
-    } else if (EPI == EPI_PART) {
-      y[((size_t)blockIdx.z * M + m) * ldy + n] = v;
-    } else {
-      y[(size_t)m * ldy + n] = v;
+  for (int t = 0; t < TM; t++) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+  int4 wb[D];
+  _Float16 db[D];
+  float4 xb[D][TM][4];
+  auto load = [&](int s, int c) {
+    wb[c] = *reinterpret_cast<const int4 *>(wr + 64 * s);
+    db[c] = dr[2 * s];
+#pragma unroll
+    for (int t = 0; t < TM; t++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) xb[c][t][i] = ld4(xr[t] + 64 * s + 4 * i);
+  };
+#pragma unroll
+  for (int s = 0; s < D; s++) load(s, s);
+#pragma unroll
+  for (int s = 0; s < ST; s++) {
+    const int c = s % D;
+    const int4 wc = wb[c];
+    const float dc = (float)db[c];
+    float4 xc[TM][4];
+#pragma unroll
+    for (int t = 0; t < TM; t++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) xc[t][i] = xb[c][t][i];
+    if (s + D < ST) load(s + D, c);
+    __builtin_amdgcn_sched_barrier(0);
+    const int wv[4] = {wc.x, wc.y, wc.z, wc.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      float wf[4];
+#pragma unroll
+      for (int b = 0; b < 4; b++) wf[b] = (float)(int8_t)(wv[i] >> (8 * b)) * dc;
+#pragma unroll
+      for (int t = 0; t < TM; t++) {
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[t][i].x, wf[0], acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[t][i].y, wf[1], acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[t][i].z, wf[2], acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[t][i].w, wf[3], acc[t], 0, 0, 0);
+      }
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
+#pragma unroll
+  for (int t = 0; t < TM; t++)
+#pragma unroll
+    for (int q = 0; q < 4; q++) red[wave][t][q][lane] = acc[t][q];
+  __syncthreads();
+  epilogue<TM, KW, EPI>(red, m0, n0, M, y, ldy);
 }
 
 // h[m] += slices 0 .. S-1 of part [S][M][K], added in slice order; then, with
@@ -153,13 +241,19 @@ __global__ __launch_bounds__(256) void k_resid_norm(float *__restrict__ h,
   for (int k = t; k < K; k += 256) xn[(size_t)m * K + k] = w[k] * (hr[k] * inv);
 }
 
-template <int TM, int KK>
+template <int TM, int KK, bool Q8>
 void launch_tk(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy, int ks,
                hipStream_t st) {
   const dim3 grid(W.N / 16, (M + 16 * TM - 1) / (16 * TM), ks), block(64 * (KK / KC));
 #define Q3H_G(E)                                                                              \
-  hipLaunchKernelGGL((k_gemm_f32<TM, KK, E>), grid, block, 0, st, W.f, x, ldx, M, W.N, W.K, y, \
-                     ldy)
+  do {                                                                                        \
+    if constexpr (Q8)                                                                         \
+      hipLaunchKernelGGL((k_gemm_q8f<TM, KK, E>), grid, block, 0, st, W.q, x, ldx, M, W.N, W.K, \
+                         y, ldy);                                                             \
+    else                                                                                      \
+      hipLaunchKernelGGL((k_gemm_f32<TM, KK, E>), grid, block, 0, st, W.f, x, ldx, M, W.N, W.K, \
+                         y, ldy);                                                             \
+  } while (0)
   if (epi == EPI_STORE)
     Q3H_G(EPI_STORE);
   else if (epi == EPI_ADD)
@@ -171,17 +265,29 @@ void launch_tk(const Mat &W, const float *x, int ldx, int M, int epi, float *y, 
 #undef Q3H_G
 }
 
-template <int TM>
+template <int TM, bool Q8>
 void launch_t(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy, int ks,
               hipStream_t st) {
   switch (W.K / ks) {
-    case 256: launch_tk<TM, 256>(W, x, ldx, M, epi, y, ldy, ks, st); break;
-    case 512: launch_tk<TM, 512>(W, x, ldx, M, epi, y, ldy, ks, st); break;
-    case 768: launch_tk<TM, 768>(W, x, ldx, M, epi, y, ldy, ks, st); break;
-    case 1024: launch_tk<TM, 1024>(W, x, ldx, M, epi, y, ldy, ks, st); break;
-    case 2048: launch_tk<TM, 2048>(W, x, ldx, M, epi, y, ldy, ks, st); break;
-    default: launch_tk<TM, 3072>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 256: launch_tk<TM, 256, Q8>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 512: launch_tk<TM, 512, Q8>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 768: launch_tk<TM, 768, Q8>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 1024: launch_tk<TM, 1024, Q8>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 2048: launch_tk<TM, 2048, Q8>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    default: launch_tk<TM, 3072, Q8>(W, x, ldx, M, epi, y, ldy, ks, st); break;
   }
+}
+
+template <bool Q8>
+void launch_m(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
+              hipStream_t st) {
+  // (Q8_0, K = 3072: 32-row tiles, the 64-row tile's registers would spill)
+  if (M <= 16)
+    launch_t<1, Q8>(W, x, ldx, M, epi, y, ldy, 1, st);
+  else if (M <= 32 || (Q8 && W.K == 3072))
+    launch_t<2, Q8>(W, x, ldx, M, epi, y, ldy, 1, st);
+  else
+    launch_t<4, Q8>(W, x, ldx, M, epi, y, ldy, 1, st);
 }
 
 }  // namespace
@@ -192,12 +298,10 @@ bool gemm_f32_supported(int N, int K) {
 
 void launch_gemm_f32(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
                      hipStream_t st) {
-  if (M <= 16)
-    launch_t<1>(W, x, ldx, M, epi, y, ldy, 1, st);
-  else if (M <= 32)
-    launch_t<2>(W, x, ldx, M, epi, y, ldy, 1, st);
+  if (W.f)
+    launch_m<false>(W, x, ldx, M, epi, y, ldy, st);
   else
-    launch_t<4>(W, x, ldx, M, epi, y, ldy, 1, st);
+    launch_m<true>(W, x, ldx, M, epi, y, ldy, st);
 }
 
 bool gemm_f32_slices_supported(int N, int K) {
@@ -207,7 +311,10 @@ bool gemm_f32_slices_supported(int N, int K) {
 
 void launch_gemm_f32_part(const Mat &W, const float *x, int ldx, int M, float *part,
                           hipStream_t st) {
-  launch_t<1>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
+  if (W.f)
+    launch_t<1, false>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
+  else
+    launch_t<1, true>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
 }
 
 void launch_resid_norm(float *h, const float *part, int M, int K, const float *norm_w,

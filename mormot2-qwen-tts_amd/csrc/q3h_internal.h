@@ -80,7 +80,10 @@ bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st, hipEvent_t 
 // the f32 matrix-core products (q3h_gemm_f32.hip): y[m][n] (+)= W[n] . x[m]
 // for f32 W [N][K] (N % 16 == 0, K in {1024, 2048, 3072}); epi EPI_* (SwiGLU:
 // interleaved gate / up rows, y [M][N / 2])
+// (Q8_0 weights, f32 activations: the same products, weights dequantized as
+// they load; taken for more than kGemvRows rows)
 bool gemm_f32_supported(int N, int K);
+constexpr int kGemvRows = 4;
 void launch_gemm_f32(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
                      hipStream_t st);
 // the same over M <= 16 rows with K cut into kF32Slices slices, one
