@@ -130,6 +130,95 @@ __global__ __launch_bounds__(64 * (KK / KC)) void k_gemm_f32(const float *__rest
   epilogue<TM, KW, EPI>(red, m0, n0, M, y, ldy);
 }
 
+// Many rows (prefill): a workgroup per 64 activation rows x 16 WN weight rows
+// over the whole K, so that each activation chunk is read once per 16 WN
+// weight rows instead of once per 16. Wave w owns weight rows n0 + 16 w ..
+// + 15 and all 4 tiles of 16 activation rows. Per 32-column chunk: the
+// activations (64 x 32) go through LDS (double buffered, one barrier per
+// chunk), each wave's weights straight to registers; the loads of chunk c + 1
+// are issued before the MFMAs of chunk c. Operands as in k_gemm_f32 (lane l:
+// row l % 16, columns 4 (l / 16) .. + 3 of each 16-column step); the result
+// tile of a wave is complete, so the epilogue needs no reduction.
+template <int WN, int EPI>
+__global__ __launch_bounds__(64 * WN) void k_gemm_f32_m64(const float *__restrict__ w,
+                                                          const float *__restrict__ x, int ldx,
+                                                          int M, int N, int K,
+                                                          float *__restrict__ y, int ldy) {
+  constexpr int NT = 64 * WN, XS = 36;  // threads; LDS row stride (floats, padded)
+  constexpr int XF4 = 64 * 32 / 4 / NT;  // float4 of an activation chunk per thread
+  __shared__ float xs[2][64 * XS];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16 * WN + 16 * wave, m0 = blockIdx.y * 64;
+  const float *wr = w + (size_t)min(n0 + r, N - 1) * K + 4 * g;
+  // activation chunk loads: float4 f = t + NT i of the 64 x 8 float4 chunk
+  const float *xr[XF4];
+  int xo[XF4];
+#pragma unroll
+  for (int i = 0; i < XF4; i++) {
+    const int f = t + NT * i, row = f >> 3, c4 = f & 7;
+    xr[i] = x + (size_t)min(m0 + row, M - 1) * ldx + 4 * c4;
+    xo[i] = row * XS + 4 * c4;
+  }
+  float4 xn[XF4], wn[2], wc[2];
+  auto load = [&](int kc) {
+#pragma unroll
+    for (int i = 0; i < XF4; i++) xn[i] = ld4(xr[i] + kc);
+    wn[0] = ld4(wr + kc);
+    wn[1] = ld4(wr + kc + 16);
+  };
+  v4f acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+  load(0);
+#pragma unroll
+  for (int i = 0; i < XF4; i++) *reinterpret_cast<float4 *>(&xs[0][xo[i]]) = xn[i];
+  wc[0] = wn[0];
+  wc[1] = wn[1];
+  __syncthreads();
+  const int nc = K / 32;
+  for (int c = 0; c < nc; c++) {
+    const int b = c & 1;
+    if (c + 1 < nc) load(32 * (c + 1));
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+#pragma unroll
+      for (int tm = 0; tm < 4; tm++) {
+        const float4 xa = *reinterpret_cast<const float4 *>(&xs[b][(16 * tm + r) * XS + 16 * s + 4 * g]);
+        acc[tm] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.x, wc[s].x, acc[tm], 0, 0, 0);
+        acc[tm] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.y, wc[s].y, acc[tm], 0, 0, 0);
+        acc[tm] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.z, wc[s].z, acc[tm], 0, 0, 0);
+        acc[tm] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.w, wc[s].w, acc[tm], 0, 0, 0);
+      }
+    }
+    if (c + 1 < nc) {
+#pragma unroll
+      for (int i = 0; i < XF4; i++) *reinterpret_cast<float4 *>(&xs[b ^ 1][xo[i]]) = xn[i];
+      wc[0] = wn[0];
+      wc[1] = wn[1];
+    }
+    __syncthreads();
+  }
+  // lane l holds (m = m0 + 16 tm + 4 g + q, n = n0 + r)
+  const int n = n0 + r;
+#pragma unroll
+  for (int tm = 0; tm < 4; tm++)
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int m = m0 + 16 * tm + 4 * g + q;
+      const float v = acc[tm][q];
+      if (EPI == EPI_SWIGLU) {
+        const float u = __shfl_xor(v, 1);  // up: the odd row after its gate
+        if (m < M && (r & 1) == 0) y[(size_t)m * ldy + n / 2] = silu_mul_f(v, u);
+      } else if (m < M) {
+        if (EPI == EPI_ADD)
+          y[(size_t)m * ldy + n] += v;
+        else
+          y[(size_t)m * ldy + n] = v;
+      }
+    }
+}
+
 // The same products with Q8_0 weights (int8 quants [N][K], then fp16 scales
 // [N][K/32]) and f32 activations: a 64-column step per load, lane l taking
 // the 16 quants 16 (l / 16) .. + 15 of its row (one 16-byte load) and the
@@ -278,9 +367,34 @@ void launch_t(const Mat &W, const float *x, int ldx, int M, int epi, float *y, i
   }
 }
 
+template <int WN>
+void launch_m64(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
+                hipStream_t st) {
+  const dim3 grid(W.N / (16 * WN), (M + 63) / 64), block(64 * WN);
+#define Q3H_G(E)                                                                               \
+  hipLaunchKernelGGL((k_gemm_f32_m64<WN, E>), grid, block, 0, st, W.f, x, ldx, M, W.N, W.K, y, \
+                     ldy)
+  if (epi == EPI_STORE)
+    Q3H_G(EPI_STORE);
+  else if (epi == EPI_ADD)
+    Q3H_G(EPI_ADD);
+  else
+    Q3H_G(EPI_SWIGLU);
+#undef Q3H_G
+}
+
 template <bool Q8>
 void launch_m(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
               hipStream_t st) {
+  if (!Q8 && M > 32 && epi != EPI_PART && W.N % 32 == 0) {
+    // many rows: 64-row tiles over the whole K, 4 or 2 waves of weight rows
+    // (keeping a few hundred workgroups)
+    if (W.N % 64 == 0 && (W.N / 64) * ((M + 63) / 64) >= 256)
+      launch_m64<4>(W, x, ldx, M, epi, y, ldy, st);
+    else
+      launch_m64<2>(W, x, ldx, M, epi, y, ldy, st);
+    return;
+  }
   // (Q8_0, K = 3072: 32-row tiles, the 64-row tile's registers would spill)
   if (M <= 16)
     launch_t<1, Q8>(W, x, ldx, M, epi, y, ldy, 1, st);
