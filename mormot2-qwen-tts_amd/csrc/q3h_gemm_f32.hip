@@ -386,13 +386,11 @@ void launch_m64(const Mat &W, const float *x, int ldx, int M, int epi, float *y,
 template <bool Q8>
 void launch_m(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
               hipStream_t st) {
-  if (!Q8 && M > 32 && epi != EPI_PART && W.N % 32 == 0) {
-    // many rows: 64-row tiles over the whole K, 4 or 2 waves of weight rows
-    // (keeping a few hundred workgroups)
-    if (W.N % 64 == 0 && (W.N / 64) * ((M + 63) / 64) >= 256)
-      launch_m64<4>(W, x, ldx, M, epi, y, ldy, st);
-    else
-      launch_m64<2>(W, x, ldx, M, epi, y, ldy, st);
+  if (!Q8 && M > 32 && epi != EPI_PART && W.N % 64 == 0 && (W.N / 64) * ((M + 63) / 64) >= 256) {
+    // many rows and wide products: 64-row tiles over the whole K (at least
+    // 1024 waves; narrower products keep the K split over waves below, whose
+    // waves each take a quarter to a twelfth of K)
+    launch_m64<4>(W, x, ldx, M, epi, y, ldy, st);
     return;
   }
   // (Q8_0, K = 3072: 32-row tiles, the 64-row tile's registers would spill)
