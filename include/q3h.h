@@ -30,6 +30,7 @@ extern "C" {
    and the storage of a stack (TInferDType idtF32 / idtQ8_0) */
 #define Q3H_F32 0
 #define Q3H_Q8_0 1 /* ggml block_q8_0 on the host: fp16 scale + 32 int8, 34 B */
+#define Q3H_BF16 2 /* bfloat16 (the text embedding table) */
 
 /* status codes */
 #define Q3H_OK 0
@@ -43,6 +44,7 @@ typedef struct q3h_device q3h_device;
 typedef struct q3h_stack q3h_stack;
 typedef struct q3h_context q3h_context;
 typedef struct q3h_frame q3h_frame;
+typedef struct q3h_text_proj q3h_text_proj;
 
 /* TDecoderConfig (mormot.ai.tts.qwen.lm.pas:184-191) + TQwen3Vulkan.KvF16
    (lm.pas:353) + the numerics of the Q8_0 products */
@@ -185,6 +187,53 @@ int q3h_frame_step(q3h_frame *f, int32_t *codes, int32_t *alive);
    outputs), as fLogits / fPastHidden after the last Start or step */
 int q3h_frame_state(q3h_frame *f, int stream, float *logits, float *past_hidden);
 int q3h_frame_destroy(q3h_frame *f);
+
+/* ---- the text projection and the device-side prefill ---- */
+typedef struct {
+  int32_t text_vocab;  /* rows of the text embedding (talker text_vocab_size, 151936) */
+  int32_t text_hidden; /* text_hidden_size, 2048 (1024, 2048 or 3072) */
+  int32_t hidden;      /* the talker's hidden_size, 1024 (a multiple of 16) */
+  int32_t emb_dtype;   /* Q3H_BF16 (as in the safetensors file) or Q3H_F32 */
+} q3h_text_config;
+
+/* TQwenTalker's text projection weights (talker.pas:302-307): emb
+   [text_vocab][text_hidden] (talker.model.text_embedding), fc1 [text_hidden]
+   [text_hidden] + b1 [text_hidden], fc2 [hidden][text_hidden] + b2 [hidden]
+   (talker.text_projection.linear_fc1 / fc2, widened to f32); copied to the
+   device as given (the products stay in f32) */
+int q3h_text_create(q3h_device *dev, const q3h_text_config *cfg, const void *emb,
+                    const float *fc1_w, const float *fc1_b, const float *fc2_w,
+                    const float *fc2_b, q3h_text_proj **out);
+/* TQwenTalker.TextProject (talker.pas:390-421): y [n][hidden] =
+   fc2 . SiLU(fc1 . emb[ids[r]] + b1) + b2, SiLU 0 below -80. n == 0 does
+   nothing; an id outside [0, text_vocab) is Q3H_E_ARG ("text token out of
+   range", nothing computed) */
+int q3h_text_project(q3h_text_proj *t, const int32_t *ids, int n, float *y);
+int q3h_text_destroy(q3h_text_proj *t);
+
+/* the special ids TQwenTalker.Start uses (talker.pas:256-261): text ids
+   tts_bos / tts_eos / tts_pad (config tts_*_token_id), codec ids codec_pad /
+   codec_bos (talker_config codec_pad_id / codec_bos_id) */
+typedef struct {
+  int32_t tts_bos, tts_eos, tts_pad;
+  int32_t codec_pad, codec_bos;
+} q3h_start_ids;
+
+/* TQwenTalker.Start (talker.pas:471-593) from its token ids, on the device:
+   ids [n_ids] = PromptIds (im_start, assistant, \n, the text, im_end, \n,
+   im_start, assistant, \n; n_ids >= 9), codec [n_codec] = the think /
+   language / speaker ids then codec_pad, codec_bos (n_codec >= 2). The
+   prefill rows (the role, tts_pad / tts_bos over the codec ids, then the text
+   over codec_pad and tts_eos, tts_pad over codec_bos when non_streaming, else
+   the first text token over codec_bos) and the trailing rows are built on the
+   device from t's projection and the frame's codec_emb, then stream s starts
+   as q3h_frame_start does with them. tts_bos / tts_eos / tts_pad are
+   projected with the text. Errors: an id out of range (Q3H_E_ARG), more
+   rows than max_positions (Q3H_E_CAPACITY) or trailing rows than max_frames
+   (Q3H_E_ARG). */
+int q3h_frame_start_text(q3h_frame *f, int stream, q3h_text_proj *t, const q3h_start_ids *sp,
+                         const int32_t *ids, int n_ids, const int32_t *codec, int n_codec,
+                         int non_streaming);
 
 /* ---- helpers ---- */
 

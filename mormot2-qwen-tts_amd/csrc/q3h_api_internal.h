@@ -141,7 +141,32 @@ struct q3h_context {
   q3h::Work w;
 };
 
+// the text projection (q3h_text.hip)
+struct q3h_text_proj {
+  q3h_device *dev = nullptr;
+  q3h_text_config cfg{};
+  void *emb = nullptr;  // [text_vocab][text_hidden], BF16 or f32
+  q3h::Mat fc1, fc2;    // f32
+  float *b1 = nullptr, *b2 = nullptr;
+  int cap = 0;               // rows of the work buffers
+  int32_t *ids = nullptr;    // [cap]
+  float *e = nullptr;        // [cap][text_hidden] embedding rows
+  float *h = nullptr;        // [cap][text_hidden] SiLU(fc1 . e + b1)
+  float *y = nullptr;        // [cap][hidden]
+  int64_t bytes = 0;
+  hipStream_t stream = nullptr;
+  std::mutex mu;
+};
+
 namespace q3h {
+// the work buffers of t for n rows (grows, synchronizing t->stream first)
+void text_ensure(q3h_text_proj *t, int n);
+// y [n][ldy] = the projection of the n ids at ids_dev (device, each in
+// [0, text_vocab): the caller checks), on stream st; uses t->e and t->h
+// (text_ensure(t, n) first)
+void text_project_dev(q3h_text_proj *t, const int32_t *ids_dev, int n, float *y, int ldy,
+                      hipStream_t st);
+
 q3h_context *new_context(q3h_stack *s, int max_positions);
 void free_context(q3h_context *ctx);
 void set_len(q3h_context *c, int len, hipStream_t st);

@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstring>
+#include <string>
 #include <vector>
 
 #include "q3h.h"
@@ -269,6 +270,23 @@ __global__ __launch_bounds__(kArgBlock) void k_talker_input_q(FrameDev f) {
   quant_row_block(xs, f.t_norm0, f.t_eps, f.H, s, f.n, f.t_xq, red);
 }
 
+// The rows of a device-side Start (TQwenTalker.Start, talker.pas:536-573):
+// row i = proj[plan[i].x] (+ codec_emb[plan[i].y] when plan[i].y >= 0, the
+// AddRow of talker.pas:423-429, added in that order); rows 0 .. rows - 1 go
+// to the prefill, the next ones to the stream's trailing rows.
+__global__ __launch_bounds__(256) void k_start_rows(const int2 *__restrict__ plan, int rows,
+                                                    const float *__restrict__ proj,
+                                                    const float *__restrict__ codec_emb, int H,
+                                                    float *__restrict__ prefill,
+                                                    float *__restrict__ trailing) {
+  const int i = blockIdx.x;
+  const int2 p = plan[i];
+  const float *src = proj + (size_t)p.x * H;
+  const float *add = p.y >= 0 ? codec_emb + (size_t)p.y * H : nullptr;
+  float *dst = i < rows ? prefill + (size_t)i * H : trailing + (size_t)(i - rows) * H;
+  for (int c = threadIdx.x; c < H; c += 256) dst[c] = add ? src[c] + add[c] : src[c];
+}
+
 // the end of a step: the frame count of every running stream; the int8 path
 // also advances the talker length here (as launch_advance does otherwise)
 __global__ void k_frame_end(FrameDev f) {
@@ -302,6 +320,10 @@ struct q3h_frame {
   int graph_positions = 0;  // attention positions the captured graph covers
   int32_t *pinned = nullptr;  // [n][groups] codes + [n] alive
   std::vector<void *> allocs;
+  // device-side Start: the row plan and the projected rows
+  int start_cap = 0;
+  int2 *start_plan = nullptr;  // [start_cap]
+  float *start_proj = nullptr; // [start_cap][H]
 };
 
 namespace {
@@ -320,6 +342,8 @@ void frame_release(q3h_frame *f) {
   f->tw.release();
   f->cw.release();
   for (void *p : f->allocs) dev_free(p);
+  dev_free(f->start_plan);
+  dev_free(f->start_proj);
   if (f->pinned) (void)hipHostFree(f->pinned);
   if (f->stream) (void)hipStreamDestroy(f->stream);
 }
@@ -518,56 +542,158 @@ extern "C" int q3h_frame_create(q3h_stack *talker, q3h_stack *cp, const q3h_fram
   return rc;
 }
 
+namespace {
+
+// The talker part of TQwenTalker.Start (talker.pas:586-593) for stream
+// `stream`: reset, fill(prefill, trailing, st) writes the rows prefill
+// [rows][H] (the talker work buffer) and trailing [trailing_rows][H] (the
+// stream's trailing rows) on stream st, then the prefill runs and the
+// stream's state is reset.
+template <class Fill>
+void start_stream(q3h_frame *f, int stream, int rows, int trailing_rows, Fill &&fill) {
+  const q3h_frame_config &c = f->cfg;
+  require(stream >= 0 && stream < c.n_streams, Q3H_E_ARG, "q3h_frame_start: bad stream");
+  require(rows > 0, Q3H_E_ARG, "q3h_frame_start: empty prefill");
+  require(trailing_rows >= 0 && trailing_rows <= c.max_frames, Q3H_E_ARG,
+          "q3h_frame_start: more trailing rows than max_frames");
+  require(rows <= c.max_positions, Q3H_E_CAPACITY, "q3h_frame_start: prefill too long");
+  check_hip(hipSetDevice(f->talker->dev->ordinal), "hipSetDevice");
+  check_hip(hipStreamSynchronize(f->stream), "frame sync");
+  q3h_context *tc = f->tctx[stream];
+  set_len(tc, 0, tc->stream);
+  // the prefill through the single-context path, outputs kept on the device
+  const int H = f->H;
+  q3h_stack *s = f->talker;
+  Work &w = tc->w;
+  w.ensure(s, rows, attention_splits(s, rows), c.vocab);
+  hipStream_t st = tc->stream;
+  FrameDev &d = f->fd;
+  fill(w.h, d.trailing + (size_t)stream * c.max_frames * H, st);
+  launch_prep(tc->dev_arr, nullptr, 1, rows, w.rd, st);
+  LayerIO io;
+  io.single_context = true;
+  run_layers(s, w, rows, rows, rows == 1, st, io);
+  float *past = d.past + (size_t)stream * H;
+  linear(s, w, s->heads[c.talker_head], w.h + (size_t)(rows - 1) * H, H, 1, s->final_norm,
+         d.logits + (size_t)stream * c.vocab, c.vocab, EPI_STORE, past, st);
+  launch_advance(tc->dev_arr, nullptr, 1, rows, st);
+  check_hip(hipGetLastError(), "prefill kernels");
+  const int zero = 0, one = 1;
+  check_hip(hipMemsetAsync(d.seen + (size_t)stream * c.vocab, 0, c.vocab, st), "reset seen");
+  check_hip(hipMemcpyAsync(d.nframes + stream, &zero, 4, hipMemcpyHostToDevice, st), "state");
+  check_hip(hipMemcpyAsync(d.step + stream, &zero, 4, hipMemcpyHostToDevice, st), "state");
+  check_hip(hipMemcpyAsync(d.trailing_rows + stream, &trailing_rows, 4, hipMemcpyHostToDevice,
+                           st),
+            "state");
+  check_hip(hipMemcpyAsync(d.alive + stream, &one, 4, hipMemcpyHostToDevice, st), "state");
+  check_hip(hipStreamSynchronize(st), "prefill sync");
+  tc->len = rows;
+  f->host_len[stream] = rows;
+  f->started[stream] = 1;
+}
+
+}  // namespace
+
 extern "C" int q3h_frame_start(q3h_frame *f, int stream, const float *prefill, int rows,
                                const float *trailing, int trailing_rows) {
   return guard([&] {
     require(f != nullptr, Q3H_E_ARG, "q3h_frame_start: NULL frame");
-    const q3h_frame_config &c = f->cfg;
-    require(stream >= 0 && stream < c.n_streams, Q3H_E_ARG, "q3h_frame_start: bad stream");
     require(prefill != nullptr && rows > 0, Q3H_E_ARG, "q3h_frame_start: empty prefill");
-    require(trailing_rows >= 0 && trailing_rows <= c.max_frames, Q3H_E_ARG,
-            "q3h_frame_start: more trailing rows than max_frames");
     require(trailing_rows == 0 || trailing != nullptr, Q3H_E_ARG,
             "q3h_frame_start: trailing is NULL");
-    require(rows <= c.max_positions, Q3H_E_CAPACITY, "q3h_frame_start: prefill too long");
+    const size_t H = f->H;
+    start_stream(f, stream, rows, trailing_rows, [&](float *pre, float *trail, hipStream_t st) {
+      check_hip(hipMemcpyAsync(pre, prefill, sizeof(float) * rows * H, hipMemcpyHostToDevice, st),
+                "upload prefill");
+      if (trailing_rows > 0)
+        check_hip(hipMemcpyAsync(trail, trailing, sizeof(float) * trailing_rows * H,
+                                 hipMemcpyHostToDevice, st),
+                  "upload trailing");
+    });
+  });
+}
+
+extern "C" int q3h_frame_start_text(q3h_frame *f, int stream, q3h_text_proj *t,
+                                    const q3h_start_ids *sp, const int32_t *ids, int n_ids,
+                                    const int32_t *codec, int n_codec, int non_streaming) {
+  return guard([&] {
+    require(f != nullptr && t != nullptr && sp != nullptr, Q3H_E_ARG,
+            "q3h_frame_start_text: NULL frame, projection or ids");
+    require(t->dev == f->talker->dev, Q3H_E_ARG,
+            "q3h_frame_start_text: the projection is on another device");
+    require(t->cfg.hidden == f->H, Q3H_E_ARG,
+            "q3h_frame_start_text: the projection's hidden size is not the talker's");
+    // PromptIds: [im_start, assistant, \n] text [im_end, \n, im_start, assistant, \n]
+    require(ids != nullptr && n_ids >= 9, Q3H_E_ARG, "q3h_frame_start_text: empty text");
+    require(codec != nullptr && n_codec >= 2, Q3H_E_ARG,
+            "q3h_frame_start_text: the codec ids end with codec_pad, codec_bos");
+    const int TV = t->cfg.text_vocab, V = f->cfg.vocab;
+    auto text_ok = [&](int id) { return id >= 0 && id < TV; };
+    auto codec_ok = [&](int id) { return id >= 0 && id < V; };
+    for (int i = 0; i < n_ids; i++)
+      require(text_ok(ids[i]), Q3H_E_ARG,
+              "q3h_frame_start_text: text token " + std::to_string(ids[i]) + " out of range");
+    require(text_ok(sp->tts_bos) && text_ok(sp->tts_eos) && text_ok(sp->tts_pad), Q3H_E_ARG,
+            "q3h_frame_start_text: tts_bos / tts_eos / tts_pad out of range");
+    for (int i = 0; i < n_codec; i++)
+      require(codec_ok(codec[i]), Q3H_E_ARG,
+              "q3h_frame_start_text: codec id " + std::to_string(codec[i]) + " out of range");
+    require(codec_ok(sp->codec_pad) && codec_ok(sp->codec_bos), Q3H_E_ARG,
+            "q3h_frame_start_text: codec_pad / codec_bos out of range");
+    const int nt = n_ids - 8, nc = n_codec;
+    // the projected rows: the role (ids 0..2), tts_pad, tts_bos, tts_eos, the text
+    std::vector<int32_t> proj_ids = {ids[0], ids[1], ids[2], sp->tts_pad, sp->tts_bos,
+                                     sp->tts_eos};
+    proj_ids.insert(proj_ids.end(), ids + 3, ids + 3 + nt);
+    const int P_PAD = 3, P_BOS = 4, P_EOS = 5, P_TEXT = 6;
+    // the rows: (projected row, codec id or -1)
+    std::vector<int2> plan;
+    for (int r = 0; r < 3; r++) plan.push_back(make_int2(r, -1));
+    for (int i = 0; i < nc - 1; i++) plan.push_back(make_int2(i < nc - 2 ? P_PAD : P_BOS, codec[i]));
+    if (non_streaming) {
+      for (int i = 0; i < nt; i++) plan.push_back(make_int2(P_TEXT + i, sp->codec_pad));
+      plan.push_back(make_int2(P_EOS, sp->codec_pad));
+      plan.push_back(make_int2(P_PAD, sp->codec_bos));
+    } else {
+      plan.push_back(make_int2(P_TEXT, sp->codec_bos));
+    }
+    const int rows = (int)plan.size();
+    if (non_streaming) {
+      plan.push_back(make_int2(P_PAD, -1));
+    } else {
+      for (int i = 1; i < nt; i++) plan.push_back(make_int2(P_TEXT + i, -1));
+      plan.push_back(make_int2(P_EOS, -1));
+    }
+    const int trailing_rows = (int)plan.size() - rows;
+    const int np = (int)proj_ids.size();
+    std::lock_guard<std::mutex> lk(t->mu);
     check_hip(hipSetDevice(f->talker->dev->ordinal), "hipSetDevice");
-    check_hip(hipStreamSynchronize(f->stream), "frame sync");
-    q3h_context *tc = f->tctx[stream];
-    set_len(tc, 0, tc->stream);
-    // the prefill through the single-context path, outputs kept on the device
-    const int H = f->H;
-    q3h_stack *s = f->talker;
-    Work &w = tc->w;
-    w.ensure(s, rows, attention_splits(s, rows), c.vocab);
-    hipStream_t st = tc->stream;
-    FrameDev &d = f->fd;
-    check_hip(hipMemcpyAsync(w.h, prefill, sizeof(float) * rows * H, hipMemcpyHostToDevice, st),
-              "upload prefill");
-    launch_prep(tc->dev_arr, nullptr, 1, rows, w.rd, st);
-    LayerIO io;
-    io.single_context = true;
-    run_layers(s, w, rows, rows, rows == 1, st, io);
-    float *past = d.past + (size_t)stream * H;
-    linear(s, w, s->heads[c.talker_head], w.h + (size_t)(rows - 1) * H, H, 1, s->final_norm,
-           d.logits + (size_t)stream * c.vocab, c.vocab, EPI_STORE, past, st);
-    launch_advance(tc->dev_arr, nullptr, 1, rows, st);
-    check_hip(hipGetLastError(), "prefill kernels");
-    if (trailing_rows > 0)
-      check_hip(hipMemcpyAsync(d.trailing + (size_t)stream * c.max_frames * H, trailing,
-                               sizeof(float) * trailing_rows * H, hipMemcpyHostToDevice, st),
-                "upload trailing");
-    const int zero = 0, one = 1;
-    check_hip(hipMemsetAsync(d.seen + (size_t)stream * c.vocab, 0, c.vocab, st), "reset seen");
-    check_hip(hipMemcpyAsync(d.nframes + stream, &zero, 4, hipMemcpyHostToDevice, st), "state");
-    check_hip(hipMemcpyAsync(d.step + stream, &zero, 4, hipMemcpyHostToDevice, st), "state");
-    check_hip(hipMemcpyAsync(d.trailing_rows + stream, &trailing_rows, 4, hipMemcpyHostToDevice,
-                             st),
-              "state");
-    check_hip(hipMemcpyAsync(d.alive + stream, &one, 4, hipMemcpyHostToDevice, st), "state");
-    check_hip(hipStreamSynchronize(st), "prefill sync");
-    tc->len = rows;
-    f->host_len[stream] = rows;
-    f->started[stream] = 1;
+    text_ensure(t, np);
+    const int need = std::max(np, (int)plan.size());
+    if (need > f->start_cap) {
+      check_hip(hipStreamSynchronize(f->stream), "frame sync");
+      dev_free(f->start_plan);
+      dev_free(f->start_proj);
+      f->start_plan = nullptr;
+      f->start_proj = nullptr;
+      f->start_cap = 0;
+      const int cap = std::max(need, 64);
+      f->start_plan = (int2 *)dev_alloc(sizeof(int2) * cap);
+      f->start_proj = (float *)dev_alloc(sizeof(float) * cap * f->H);
+      f->start_cap = cap;
+    }
+    start_stream(f, stream, rows, trailing_rows, [&](float *pre, float *trail, hipStream_t st) {
+      check_hip(hipMemcpyAsync(t->ids, proj_ids.data(), sizeof(int32_t) * np,
+                               hipMemcpyHostToDevice, st),
+                "upload ids");
+      check_hip(hipMemcpyAsync(f->start_plan, plan.data(), sizeof(int2) * plan.size(),
+                               hipMemcpyHostToDevice, st),
+                "upload plan");
+      text_project_dev(t, t->ids, np, f->start_proj, f->H, st);
+      hipLaunchKernelGGL(k_start_rows, dim3((unsigned)plan.size()), dim3(256), 0, st,
+                         f->start_plan, rows, f->start_proj, f->codec_emb, f->H, pre, trail);
+      check_hip(hipGetLastError(), "start rows");
+    });
   });
 }
 

@@ -23,7 +23,7 @@
 // the later tiles find in L2 / Infinity Cache.
 #include <hip/hip_runtime.h>
 
-#include "q3h_internal.h"
+#include "q3h_api_internal.h"
 
 namespace q3h {
 namespace {
@@ -35,6 +35,11 @@ constexpr int KC = 256;  // columns per wave
 __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 
 __device__ __forceinline__ float silu_mul_f(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
+// SiLU of the text projection: 0 below -80 (where e^-v would overflow)
+__device__ __forceinline__ float silu_clamp_f(float v) {
+  return v < -80.0f ? 0.0f : v / (1.0f + expf(-v));
+}
 
 // the sums of a tile, met in LDS (red[wave][t][q][lane]: the MFMA result
 // layout), added in wave order and stored / added / SwiGLU'd / kept as a slice
@@ -57,6 +62,9 @@ __device__ __forceinline__ void epilogue(const float (&red)[KW][TM][4][64], int 
       if ((l & 1) == 0) y[(size_t)m * ldy + n / 2] = silu_mul_f(v, u);
     } else if (EPI == EPI_ADD) {
       y[(size_t)m * ldy + n] += v;
+    } else if (EPI == EPI_ADD_SILU) {
+      float *p = y + (size_t)m * ldy + n;
+      *p = silu_clamp_f(*p + v);
     } else if (EPI == EPI_PART) {
       y[((size_t)blockIdx.z * M + m) * ldy + n] = v;
     } else {
@@ -213,6 +221,8 @@ __global__ __launch_bounds__(64 * WN) void k_gemm_f32_m64(const float *__restric
       } else if (m < M) {
         if (EPI == EPI_ADD)
           y[(size_t)m * ldy + n] += v;
+        else if (EPI == EPI_ADD_SILU)
+          y[(size_t)m * ldy + n] = silu_clamp_f(y[(size_t)m * ldy + n] + v);
         else
           y[(size_t)m * ldy + n] = v;
       }
@@ -349,8 +359,13 @@ void launch_tk(const Mat &W, const float *x, int ldx, int M, int epi, float *y, 
     Q3H_G(EPI_ADD);
   else if (epi == EPI_SWIGLU)
     Q3H_G(EPI_SWIGLU);
-  else
+  else if (epi == EPI_PART)
     Q3H_G(EPI_PART);
+  else if constexpr (!Q8 && KK >= 1024)
+    hipLaunchKernelGGL((k_gemm_f32<TM, KK, EPI_ADD_SILU>), grid, block, 0, st, W.f, x, ldx, M,
+                       W.N, W.K, y, ldy);
+  else
+    require(false, Q3H_E_ARG, "EPI_ADD_SILU takes f32 weights over the whole K");
 #undef Q3H_G
 }
 
@@ -378,6 +393,8 @@ void launch_m64(const Mat &W, const float *x, int ldx, int M, int epi, float *y,
     Q3H_G(EPI_STORE);
   else if (epi == EPI_ADD)
     Q3H_G(EPI_ADD);
+  else if (epi == EPI_ADD_SILU)
+    Q3H_G(EPI_ADD_SILU);
   else
     Q3H_G(EPI_SWIGLU);
 #undef Q3H_G

@@ -38,7 +38,9 @@ struct CtxDev {
 };
 
 // EPI_PART (f32 matrix-core products only): sums to a slice of a partial buffer
-enum Epi { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2, EPI_PART = 3 };
+// EPI_ADD_SILU (f32 matrix-core products, f32 weights): y = SiLU(y + sum),
+// 0 where y + sum < -80 (the text projection's fc1, its bias in y)
+enum Epi { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2, EPI_PART = 3, EPI_ADD_SILU = 4 };
 
 struct GemvArgs {
   const int8_t *wq;

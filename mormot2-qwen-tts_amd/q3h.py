@@ -20,6 +20,7 @@ LIB_PATH = os.path.join(HERE, "libq3h.so")
 
 F32 = 0
 Q8_0 = 1
+BF16 = 2
 
 E_ARG, E_HIP, E_CAPACITY, E_STATE, E_NODEV = -1, -2, -3, -4, -5
 
@@ -77,6 +78,20 @@ class FrameConfig(ctypes.Structure):
     ]
 
 
+class TextConfig(ctypes.Structure):
+    _fields_ = [
+        ("text_vocab", ctypes.c_int32),
+        ("text_hidden", ctypes.c_int32),
+        ("hidden", ctypes.c_int32),
+        ("emb_dtype", ctypes.c_int32),
+    ]
+
+
+class StartIds(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in
+                ("tts_bos", "tts_eos", "tts_pad", "codec_pad", "codec_bos")]
+
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _FP = ctypes.POINTER(ctypes.c_float)
@@ -110,6 +125,11 @@ SIGNATURES = {
     "q3h_frame_step": (_I, [_P, _IP, _IP]),
     "q3h_frame_state": (_I, [_P, _I, _FP, _FP]),
     "q3h_frame_destroy": (_I, [_P]),
+    "q3h_text_create": (_I, [_P, ctypes.POINTER(TextConfig), _P, _FP, _FP, _FP, _FP,
+                             ctypes.POINTER(_P)]),
+    "q3h_text_project": (_I, [_P, _IP, _I, _FP]),
+    "q3h_text_destroy": (_I, [_P]),
+    "q3h_frame_start_text": (_I, [_P, _I, _P, ctypes.POINTER(StartIds), _IP, _I, _IP, _I, _I]),
     "q3h_quantize_row_q8_0": (_I, [_FP, _P, ctypes.c_int64]),
     "q3h_stack_time_gemv": (_I, [_P, _I, _I, _I, _FP, ctypes.POINTER(_I),
                                  ctypes.POINTER(ctypes.c_int64)]),
@@ -345,6 +365,37 @@ class QwenLm:
         self.ctx.destroy()
 
 
+class TextProj:
+    """The talker's text projection on the device (TQwenTalker.TextProject,
+    talker.pas:390-421): emb float32 [vocab][text_hidden] or uint16 (the BF16
+    bits), fc1 [text_hidden][text_hidden], fc2 [hidden][text_hidden] + biases."""
+
+    def __init__(self, dev, emb, fc1_w, fc1_b, fc2_w, fc2_b):
+        emb = np.ascontiguousarray(emb)
+        dt = BF16 if emb.dtype == np.uint16 else F32
+        if dt == F32:
+            emb = _f32(emb)
+        self._w = [_f32(fc1_w), _f32(fc1_b), _f32(fc2_w), _f32(fc2_b)]
+        cfg = TextConfig(emb.shape[0], emb.shape[1], self._w[2].shape[0], dt)
+        h = _P()
+        _check(lib().q3h_text_create(dev.h, ctypes.byref(cfg), emb.ctypes.data_as(_P),
+                                     *[_fp(a) for a in self._w], ctypes.byref(h)))
+        self._w = None
+        self.h = h
+        self.hidden = cfg.hidden
+
+    def project(self, ids):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        y = np.empty((len(ids), self.hidden), dtype=np.float32)
+        _check(lib().q3h_text_project(self.h, ids.ctypes.data_as(_IP), len(ids), _fp(y)))
+        return y
+
+    def destroy(self):
+        if self.h:
+            _check(lib().q3h_text_destroy(self.h))
+            self.h = None
+
+
 class Frame:
     """The device-resident frame step over n streams (q3h_frame_*)."""
 
@@ -386,6 +437,18 @@ class Frame:
         t = _f32(trailing) if trailing is not None and len(trailing) else None
         _check(lib().q3h_frame_start(self.h, stream, _fp(p), p.shape[0], _fp(t),
                                      0 if t is None else t.shape[0]))
+
+    def start_text(self, stream, proj, ids, codec, tts_bos, tts_eos, tts_pad, codec_pad,
+                   codec_bos, non_streaming):
+        """TQwenTalker.Start from token ids (talker.pas:471-593): the prefill
+        and trailing rows built on the device with proj (a TextProj)."""
+        sp = StartIds(tts_bos, tts_eos, tts_pad, codec_pad, codec_bos)
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        c = np.ascontiguousarray(codec, dtype=np.int32)
+        _check(lib().q3h_frame_start_text(self.h, stream, proj.h, ctypes.byref(sp),
+                                          a.ctypes.data_as(_IP), len(a),
+                                          c.ctypes.data_as(_IP), len(c),
+                                          1 if non_streaming else 0))
 
     def step(self):
         codes = np.empty((self.n, self.groups), dtype=np.int32)

@@ -96,6 +96,34 @@ def tts_pad(seed, std=0.02):
     return normal(seed, "tts_pad", (TALKER["hidden"],), std)
 
 
+TEXT_VOCAB = 151936  # talker text_vocab_size
+TEXT_HIDDEN = 2048   # talker text_hidden_size
+
+
+def to_bf16_bits(x):
+    """float32 -> bfloat16 bits (round to nearest even), uint16."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def text_projection(seed, text_vocab=TEXT_VOCAB, std=0.02, emb_std=1.0):
+    """The text embedding as BF16 bits [text_vocab][2048] (N(0, emb_std)) and
+    the projection fc1 [2048][2048] + b1, fc2 [1024][2048] + b2 in f32
+    (talker.model.text_embedding, talker.text_projection.linear_fc1 / fc2)."""
+    TH, H = TEXT_HIDDEN, TALKER["hidden"]
+    emb = np.empty((text_vocab, TH), dtype=np.uint16)
+    step = 8192  # rows per chunk: bounded peak memory for the full table
+    for r0 in range(0, text_vocab, step):
+        n = min(step, text_vocab - r0)
+        emb[r0:r0 + n] = to_bf16_bits(normal(seed, f"talker.model.text_embedding.{r0}",
+                                             (n, TH), emb_std))
+    w1 = normal(seed, "talker.text_projection.linear_fc1.weight", (TH, TH), std)
+    b1 = normal(seed, "talker.text_projection.linear_fc1.bias", (TH,), std)
+    w2 = normal(seed, "talker.text_projection.linear_fc2.weight", (H, TH), std)
+    b2 = normal(seed, "talker.text_projection.linear_fc2.bias", (H,), std)
+    return emb, w1, b1, w2, b2
+
+
 def prompt(seed, rows, hidden=1024, name="prompt"):
     """fp32 N(0, 1) prompt embeddings."""
     return normal(seed, name, (rows, hidden), 1.0)

@@ -483,6 +483,52 @@ void q3o_head(const void *w, int dtype, int act_q8, int rows_out, int hidden,
 }
 
 /* ------------------------------------------------------------------ */
+/* text projection                                                     */
+
+/* InferRowToF32 of one text-embedding row: f32 as is, BF16 = the high half
+ * of an f32 (exact) */
+static void text_row(const void *emb, int emb_dtype, int id, int cols, float *out) {
+  if (emb_dtype == Q3O_BF16) {
+    const uint16_t *r = (const uint16_t *)emb + (size_t)id * cols;
+    for (int c = 0; c < cols; c++) {
+      const uint32_t u = (uint32_t)r[c] << 16;
+      memcpy(out + c, &u, 4);
+    }
+  } else {
+    memcpy(out, (const float *)emb + (size_t)id * cols, sizeof(float) * cols);
+  }
+}
+
+/* TQwenTalker.TextProject (talker.pas:390-421): e = embedding rows of ids,
+ * h = fc1 . e + b1, SiLU(h) (0 below -80, else v / (1 + Exp(-v)) with the
+ * exponential and the quotient in double, as Pascal's Exp on x86-64 returns
+ * a double), y = fc2 . h + b2. Each bias is the start of its row's sum. */
+int q3o_text_project(const void *emb, int emb_dtype, int vocab, int text_hidden, int hidden,
+                     const float *fc1_w, const float *fc1_b, const float *fc2_w,
+                     const float *fc2_b, const int32_t *ids, int n, float *y) {
+  if (n <= 0) return 0;
+  for (int r = 0; r < n; r++)
+    if (ids[r] < 0 || ids[r] >= vocab) return -1;
+  const int TH = text_hidden;
+  float *e = (float *)malloc(sizeof(float) * (size_t)n * TH);
+  float *h = (float *)malloc(sizeof(float) * (size_t)n * TH);
+  for (int r = 0; r < n; r++) {
+    text_row(emb, emb_dtype, ids[r], TH, e + (size_t)r * TH);
+    memcpy(h + (size_t)r * TH, fc1_b, sizeof(float) * TH);
+    memcpy(y + (size_t)r * hidden, fc2_b, sizeof(float) * hidden);
+  }
+  linear(fc1_w, Q3O_F32, 0, TH, TH, e, n, h, TH, 1);
+  for (size_t i = 0; i < (size_t)n * TH; i++) {
+    const float v = h[i];
+    h[i] = v < -80.0f ? 0.0f : (float)((double)v / (1.0 + exp(-(double)v)));
+  }
+  linear(fc2_w, Q3O_F32, 0, hidden, TH, h, n, y, hidden, 1);
+  free(e);
+  free(h);
+  return 0;
+}
+
+/* ------------------------------------------------------------------ */
 /* code choice (greedy)                                                */
 
 int q3o_argmax(const float *p, int n) {

@@ -43,6 +43,7 @@ extern "C" {
 
 #define Q3O_F32 0
 #define Q3O_Q8_0 1
+#define Q3O_BF16 2 /* text embedding only */
 
 /* ggml block_q8_0: fp16 scale then 32 int8 quants, 34 bytes */
 typedef struct {
@@ -109,6 +110,15 @@ int q3o_forward_embeds(q3o_ctx *c, const float *x, int rows, float *normed_last,
 /* logits[rows_out] = W[rows_out][hidden] . state, W f32 or Q8_0 */
 void q3o_head(const void *w, int dtype, int act_q8, int rows_out, int hidden,
               const float *state, float *logits);
+
+/* TQwenTalker.TextProject (talker.pas:390-421): y [n][hidden] =
+   fc2 . SiLU(fc1 . emb[ids[r]] + b1) + b2, SiLU 0 below -80; emb
+   [vocab][text_hidden] in Q3O_F32 or Q3O_BF16, fc1 [text_hidden][text_hidden],
+   fc2 [hidden][text_hidden] f32. Returns 0, or -1 (nothing written) when an
+   id is out of range. */
+int q3o_text_project(const void *emb, int emb_dtype, int vocab, int text_hidden, int hidden,
+                     const float *fc1_w, const float *fc1_b, const float *fc2_w,
+                     const float *fc2_b, const int32_t *ids, int n, float *y);
 
 /* first max wins */
 int q3o_argmax(const float *p, int n);

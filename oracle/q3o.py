@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(HERE, "build", "libq3o.so")
 
 F32 = 0
 Q8_0 = 1
+BF16 = 2
 
 _P = ctypes.c_void_p
 _FP = ctypes.POINTER(ctypes.c_float)
@@ -83,6 +84,9 @@ def lib():
             "q3o_frame_next": (ctypes.c_int, [_P, _IP]),
             "q3o_frame_logits": (_FP, [_P]),
             "q3o_frame_past_hidden": (_FP, [_P]),
+            "q3o_text_project": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                ctypes.c_int, _FP, _FP, _FP, _FP, _IP,
+                                                ctypes.c_int, _FP]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -155,6 +159,59 @@ def choose_code0(logits, eos, history, penalty):
     h = np.ascontiguousarray(history, dtype=np.int32)
     return lib().q3o_choose_code0(_fp(lg), lg.size, eos, h.ctypes.data_as(_IP), h.size,
                                   ctypes.c_float(penalty))
+
+
+def text_project(emb, fc1_w, fc1_b, fc2_w, fc2_b, ids):
+    """TQwenTalker.TextProject (talker.pas:390-421) over ids: float32
+    [n][hidden]. emb: float32 [vocab][text_hidden], or uint16 (the BF16 bits).
+    Raises IndexError for an id out of range, as the reference raises."""
+    emb = np.ascontiguousarray(emb)
+    dt = BF16 if emb.dtype == np.uint16 else F32
+    if dt == F32:
+        emb = _f32(emb)
+    vocab, th = emb.shape
+    fc1_w, fc1_b, fc2_w, fc2_b = _f32(fc1_w), _f32(fc1_b), _f32(fc2_w), _f32(fc2_b)
+    hidden = fc2_w.shape[0]
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    y = np.empty((len(ids), hidden), dtype=np.float32)
+    rc = lib().q3o_text_project(emb.ctypes.data, dt, vocab, th, hidden, _fp(fc1_w), _fp(fc1_b),
+                                _fp(fc2_w), _fp(fc2_b), ids.ctypes.data_as(_IP), len(ids),
+                                _fp(y))
+    if rc != 0:
+        raise IndexError("text token out of range")
+    return y
+
+
+def start_rows(project, codec_emb, ids, codec, tts_bos, tts_eos, tts_pad, codec_pad,
+               codec_bos, non_streaming):
+    """The rows TQwenTalker.Start (talker.pas:520-580) builds from the prompt
+    ids [im_start, assistant, \\n] text [im_end, \\n, im_start, assistant, \\n]
+    and the codec ids (think / language / speaker ..., codec_pad, codec_bos):
+    (prefill [rows][hidden], trailing [trailing_rows][hidden]). project(ids)
+    is the text projection; tts_bos / tts_eos / tts_pad are text ids, projected
+    one by one as TQwenTalker.Create does (talker.pas:339-344)."""
+    ids = list(ids)
+    codec = list(codec)
+    if len(ids) < 9:
+        raise ValueError("empty text")
+    ce = np.asarray(codec_emb, dtype=np.float32)
+    bos, eos, pad = (project([t])[0] for t in (tts_bos, tts_eos, tts_pad))
+    text = ids[3:len(ids) - 5]
+    nc, nt = len(codec), len(text)
+    rows = [r for r in project(ids[:3])]
+    for i in range(nc - 1):
+        rows.append((pad if i < nc - 2 else bos) + ce[codec[i]])
+    if non_streaming:
+        for r in project(text):
+            rows.append(r + ce[codec_pad])
+        rows.append(eos + ce[codec_pad])
+        rows.append(pad + ce[codec_bos])
+        trailing = [pad]
+    else:
+        rows.append(project(text[:1])[0] + ce[codec_bos])
+        trailing = [r for r in project(text[1:])] if nt > 1 else []
+        trailing.append(eos)
+    return (np.stack(rows).astype(np.float32), np.stack(trailing).astype(np.float32))
 
 
 class Stack:

@@ -46,6 +46,10 @@ def test_null_arguments_are_errors(q3h):
     assert L.q3h_frame_step(None, None, None) == q3h.E_ARG
     assert L.q3h_device_close(None) == q3h.E_ARG
     assert L.q3h_device_name(None) is None
+    assert L.q3h_text_create(None, None, None, None, None, None, None, None) == q3h.E_ARG
+    assert L.q3h_text_project(None, None, 1, None) == q3h.E_ARG
+    assert L.q3h_text_destroy(None) == 0
+    assert L.q3h_frame_start_text(None, 0, None, None, None, 9, None, 5, 0) == q3h.E_ARG
 
 
 def test_quantizer_rejects_ragged_rows(q3h):
