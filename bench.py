@@ -28,7 +28,10 @@ Beside it:
                 host cores, on a bounded sample of the same workload;
   long_context_attention (frame_b1)  the talker with an f16 K/V cache
                 prefilled to 2048 / 4096 / 8192 positions: 32 decode steps
-                each, and the decode attention kernels' GB/s.
+                each, and the decode attention kernels' GB/s;
+  start_from_text (frame_b1)  time to the first frame from token ids: the
+                text projection, the prefill rows built on the device, the
+                talker prefill and one frame step (a 40-token sentence).
 
 Prints one JSON line.
 """
@@ -226,6 +229,89 @@ def long_context_attention(dev, f32, tables, seed, steps=32, iters=10):
                 kv="f16", steps_per_length=steps, results=out)
 
 
+TEXT_VOCAB_BENCH = 16384  # rows of the synthetic text table (one row gathered per token)
+TEXT_TOKENS = 40
+
+
+def start_ids(seed, n_text):
+    """PromptIds (talker.pas:430-452) of a sentence of n_text tokens: im_start,
+    assistant, \\n, the text, im_end, \\n, im_start, assistant, \\n; the codec
+    ids of the Auto language with no speaker (nothink, think_bos, think_eos,
+    codec_pad, codec_bos, talker.pas:512-521) and the special ids."""
+    rng = np.random.Generator(np.random.PCG64(seed + 55))
+    text = rng.integers(0, TEXT_VOCAB_BENCH - 16, n_text).tolist()
+    im_start, im_end, assistant, nl = TEXT_VOCAB_BENCH - 1, TEXT_VOCAB_BENCH - 2, 77, 198
+    ids = [im_start, assistant, nl] + text + [im_end, nl, im_start, assistant, nl]
+    special = dict(tts_bos=TEXT_VOCAB_BENCH - 5, tts_eos=TEXT_VOCAB_BENCH - 4,
+                   tts_pad=TEXT_VOCAB_BENCH - 3, codec_pad=2148, codec_bos=2149)
+    return ids, [2155, 2156, 2157, 2148, 2149], special
+
+
+def start_from_text(dev, ts, cs, tables, seed, max_pos, iters=10, use_graph=True):
+    """Time to the first frame from token ids (TQwenTalker.Start then the first
+    NextFrame): q3h_frame_start_text projects the prompt's 48 text rows
+    (TextProject, fc1 2048 x 2048 + SiLU + fc2 2048 -> 1024 in f32 on the matrix
+    cores), assembles the prefill and trailing rows on the device and prefills
+    the talker; then one frame step. Wall clock, host ids in and codes out;
+    median of iters after 2 warm-ups, non-streaming (49 prefill rows) and
+    streaming (8 prefill rows + 40 trailing). Also the projection alone
+    (q3h_text_project of the 48 ids, host ids in, host rows out)."""
+    emb, w1, b1, w2, b2 = synth.text_projection(seed, TEXT_VOCAB_BENCH)
+    proj = q3h.TextProj(dev, emb, w1, b1, w2, b2)
+    fr = q3h.Frame(ts, cs, tables["codec_emb"], tables["pred_emb"], tables["tts_pad"],
+                   n_streams=1, max_positions=max_pos, max_frames=64, use_graph=use_graph)
+    ids, codec, sp = start_ids(seed, TEXT_TOKENS)
+    out = dict(text_tokens=TEXT_TOKENS, prompt_ids=len(ids), text_vocab=TEXT_VOCAB_BENCH)
+    for ns in (True, False):
+        st, ff = [], []
+        for i in range(iters + 2):
+            a = time.perf_counter()
+            fr.start_text(0, proj, ids, codec, non_streaming=ns, **sp)
+            b = time.perf_counter()
+            fr.step()
+            c = time.perf_counter()
+            if i >= 2:
+                st.append(b - a)
+                ff.append(c - a)
+        key = "non_streaming" if ns else "streaming"
+        out[key] = dict(start_ms_p50=round(1e3 * float(np.median(st)), 3),
+                        first_frame_ms_p50=round(1e3 * float(np.median(ff)), 3))
+        log(f"start from text ({key}): start {1e3 * np.median(st):.2f} ms, "
+            f"first frame {1e3 * np.median(ff):.2f} ms")
+    pid = np.array(ids, np.int32)
+    lat = []
+    for i in range(iters + 2):
+        a = time.perf_counter()
+        proj.project(pid)
+        if i >= 2:
+            lat.append(time.perf_counter() - a)
+    out["project_48_rows_us_p50"] = round(1e6 * float(np.median(lat)), 1)
+    log(f"text projection of {len(ids)} rows: {1e6 * np.median(lat):.0f} us")
+    fr.destroy()
+    proj.destroy()
+    start_from_text.tables = (emb, w1, b1, w2, b2)
+    start_from_text.ids = pid
+    return out
+
+
+def cpu_text_projection(tables, ids, budget_s=2.0):
+    """The oracle's TextProject of the same ids on the host cores (the
+    reference's CPU text projection), timed until budget_s is spent."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import q3o  # the checker's restatement, timed as the CPU baseline
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    q3o.set_threads(threads)
+    n = 0
+    t0 = time.perf_counter()
+    while n < 2 or time.perf_counter() - t0 < budget_s:
+        q3o.text_project(*tables, ids)
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    return dict(value=round(1e6 * dt, 1), unit="us per projection", cores=threads, kind="port",
+                sample=f"TextProject of {len(ids)} ids (oracle, C + OpenMP), {n} runs")
+
+
 COPY_BYTES = 256 << 20
 
 
@@ -259,6 +345,11 @@ def main():
                          "(for tracers that do not follow graph capture)")
     ap.add_argument("--no-long-attn", action="store_true",
                     help="skip the long-context attention measurement (frame_b1)")
+    ap.add_argument("--no-text", action="store_true",
+                    help="skip the time-to-first-frame measurement from token ids (frame_b1)")
+    ap.add_argument("--no-roofline", action="store_true",
+                    help="skip the matrix-vector roofline measurement (its kernel-attached "
+                         "events are not for runs under a kernel tracer)")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the matrix-vector roofline measurement (profiling runs)")
     ap.add_argument("--long-attn-only", action="store_true",
@@ -315,9 +406,13 @@ def main():
         f"(p50 {1e6 * np.median(lat):.0f} us, p99 {1e6 * np.percentile(lat, 99):.0f} us); "
         f"prefill of {n} stream(s) {1e3 * run_gpu.prefill_s:.1f} ms")
 
-    roofline = gemv_roofline(ts, args) if not f32w else None
+    roofline = gemv_roofline(ts, args) if not (f32w or args.no_roofline) else None
 
     frame.destroy()
+    text_start = None
+    if b1 and not args.no_text:
+        text_start = start_from_text(dev, ts, cs, tables, args.seed, max_pos,
+                                     use_graph=not args.no_graph)
     long_attn = None
     if b1 and not args.no_long_attn:
         long_attn = long_context_attention(dev, f32, tables, args.seed)
@@ -330,6 +425,10 @@ def main():
         parity = dict(frames=nf, codes_equal_stream0=bool(equal))
         log(f"cpu baseline: {cpu['value']:.2f} frames/s on {cpu['cores']} threads; "
             f"codes equal over {nf} frames: {equal}")
+        if text_start is not None:
+            text_start["cpu_baseline"] = cpu_text_projection(start_from_text.tables,
+                                                             start_from_text.ids)
+            log(f"cpu text projection: {text_start['cpu_baseline']['value']:.0f} us")
     ts.destroy()
     cs.destroy()
     dev.close()
@@ -360,6 +459,7 @@ def main():
         "cpu_baseline": cpu,
         "parity": parity,
         "long_context_attention": long_attn,
+        "start_from_text": text_start,
     }
     print(json.dumps(out), flush=True)
     return 0
