@@ -401,12 +401,24 @@ def main():
                       use_graph=not args.no_graph)
     log(f"{args.workload}: {n} stream(s), warm-up {warmup}, timing {steps} steps")
     total, lat, codes = run_gpu(frame, pre, steps, warmup)
+    prefill_s = run_gpu.prefill_s
     fps = n * steps / total
     log(f"{fps:.1f} frames/s, {1e3 * total / steps:.3f} ms per step "
         f"(p50 {1e6 * np.median(lat):.0f} us, p99 {1e6 * np.percentile(lat, 99):.0f} us); "
-        f"prefill of {n} stream(s) {1e3 * run_gpu.prefill_s:.1f} ms")
+        f"prefill of {n} stream(s) {1e3 * prefill_s:.1f} ms")
 
     roofline = gemv_roofline(ts, args) if not (f32w or args.no_roofline) else None
+
+    # the same frames drawn with the qwen_tts default sampling (temperature 0.9,
+    # top-k 50 on both choosers, talker.pas:208-216): the sampler's cost
+    frame.set_sampling(True, 0.9, 50, 1.0, True, 0.9, 50, 1.0, seed=args.seed + 1)
+    s_total, s_lat, _ = run_gpu(frame, pre, steps, warmup)
+    frame.set_sampling()
+    sampled = dict(frames_per_s=round(n * steps / s_total, 2),
+                   ms_per_step=round(1e3 * s_total / steps, 4),
+                   step_us_p50=round(1e6 * float(np.median(s_lat)), 1),
+                   sampling="temperature 0.9, top-k 50, top-p 1 (talker and code predictor)")
+    log(f"sampled: {sampled['frames_per_s']:.1f} frames/s, {sampled['ms_per_step']:.3f} ms per step")
 
     frame.destroy()
     text_start = None
@@ -452,7 +464,7 @@ def main():
                    "frames": steps, "talker_layers": 28, "cp_layers": 5, "hidden": 1024,
                    "heads": "16q/8kv x 128", "ffn": 3072, "weights": "f32" if f32w else "Q8_0",
                    "kv": "f32", "activations": "q8_0 (int8 MFMA)" if act_q8 else "f32"},
-        "prefill_ms": round(1e3 * run_gpu.prefill_s, 2),
+        "prefill_ms": round(1e3 * prefill_s, 2),
         "step_us_p50": round(1e6 * float(np.median(lat)), 1),
         "step_us_p99": round(1e6 * float(np.percentile(lat, 99)), 1),
         "roofline": roofline,
@@ -460,6 +472,7 @@ def main():
         "parity": parity,
         "long_context_attention": long_attn,
         "start_from_text": text_start,
+        "sampled": sampled,
     }
     print(json.dumps(out), flush=True)
     return 0

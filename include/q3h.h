@@ -188,6 +188,34 @@ int q3h_frame_step(q3h_frame *f, int32_t *codes, int32_t *alive);
 int q3h_frame_state(q3h_frame *f, int stream, float *logits, float *past_hidden);
 int q3h_frame_destroy(q3h_frame *f);
 
+/* TQwenSampling (talker.pas:60-70) without the repetition penalty (a frame
+   setting): the choosers of code 0 (talker) and of codes 1..15 (code
+   predictor, the sub-sampler). do_sample 0: argmax, as QwenGreedy. Else the
+   scores (code 0: after ChooseCode0's processors) / temperature, top-k (0:
+   off; ties at the k-th value kept), top-p (1: off; < 1 needs 1 <= top_k <=
+   64), then one uniform through the inverse distribution (the logits warpers
+   of Hugging Face generate(), which NewSampler, talker.pas:455-469,
+   configures). Uniforms: Philox4x64-10 of counter (frame, group, 0, 0) under
+   key (seed, 0) for code 0 (group 0), (seed xor 0x5DEECE66D, 0) for code g
+   (group g), frame = frames of the sentence before this one. seed: the
+   sentence seed of every q3h_frame_start* (0: a fresh random one per start,
+   as talker.pas:582-584). At most 3072 codes per chooser. */
+typedef struct {
+  int32_t do_sample;
+  float temperature;
+  int32_t top_k;
+  float top_p;
+  int32_t sub_do_sample;
+  float sub_temperature;
+  int32_t sub_top_k;
+  float sub_top_p;
+  uint64_t seed;
+} q3h_sampling;
+
+/* property TQwenTalker.Sampling (talker.pas:150-151) for every stream of the
+   frame; takes effect at the next step (its seed at the next start) */
+int q3h_frame_set_sampling(q3h_frame *f, const q3h_sampling *s);
+
 /* ---- the text projection and the device-side prefill ---- */
 typedef struct {
   int32_t text_vocab;  /* rows of the text embedding (talker text_vocab_size, 151936) */

@@ -11,12 +11,15 @@
 #include <hip/hip_runtime.h>
 
 #include <cstring>
+#include <random>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "q3h.h"
 #include "q3h_api_internal.h"
 #include "q3h_quant.h"
+#include "q3h_sample.h"
 
 namespace q3h {
 
@@ -53,6 +56,10 @@ struct FrameDev {
   float cp_eps, t_eps;
   const float *cp_part;    // head partials [cp_hch][rows][cp_vocab]
   int cp_hch;
+  // the choosers (argmax when do_sample == 0) and the sentence seed of each
+  // stream (the code predictor's: seed ^ kSubSeedXor)
+  SampleParams sp0, sp;
+  const uint64_t *seeds;   // [n]
 };
 
 constexpr int kArgBlock = 1024;
@@ -104,17 +111,18 @@ __device__ __forceinline__ RowDesc row_desc(const CtxDev *c, int pos) {
 // the reset of the code-predictor context. One block per stream. The int8
 // path: also the descriptors (positions 0, 1) and the quantized layer-0
 // inputs of both rows (zeros for a stream that does not run).
+template <bool SAMPLE>
 __global__ __launch_bounds__(kArgBlock) void k_choose_code0(FrameDev f) {
   __shared__ double red[kArgBlock / 64];
+  __shared__ std::conditional_t<SAMPLE, SampleShared, char> sh;
   const int s = blockIdx.x, tid = threadIdx.x;
   int code = -1;
   if (f.alive[s]) {
     const float *lg = f.logits + (size_t)s * f.vocab;
     const uint8_t *seen = f.seen + (size_t)s * f.vocab;
     const int nf = f.nframes[s];
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    for (int i = tid; i < f.vocab; i += kArgBlock) {
+    // the scores of ChooseCode0's logits processors
+    auto score = [&](int i) {
       float v = lg[i];
       // 2048..3071 forbidden but eos; eos forbidden before 2 frames
       if (i >= f.vocab - 1024 && i != f.eos) v = -INFINITY;
@@ -122,9 +130,22 @@ __global__ __launch_bounds__(kArgBlock) void k_choose_code0(FrameDev f) {
       // repetition penalty, once per code already returned (not when forbidden)
       if (seen[i] && v != -INFINITY && f.penalty != 1.0f)
         v = v > 0.f ? __fdiv_rn(v, f.penalty) : v * f.penalty;
-      argmax_merge(bv, bi, v, i);
+      return v;
+    };
+    if constexpr (SAMPLE) {
+      float x[3];
+#pragma unroll
+      for (int j = 0; j < 3; j++) {
+        const int i = 3 * tid + j;
+        x[j] = i < f.vocab ? score(i) : -INFINITY;
+      }
+      code = block_sample<3>(x, f.vocab, f.sp0, draw_uniform(f.seeds[s], (uint64_t)nf, 0), sh);
+    } else {
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+      for (int i = tid; i < f.vocab; i += kArgBlock) argmax_merge(bv, bi, score(i), i);
+      code = block_argmax(bv, bi);
     }
-    code = block_argmax(bv, bi);
     int *codes = f.codes + (size_t)s * f.groups;
     if (code == f.eos) {
       if (tid < f.groups) codes[tid] = -1;
@@ -158,6 +179,30 @@ __global__ __launch_bounds__(kArgBlock) void k_choose_code0(FrameDev f) {
   }
 }
 
+// the code predictor's draw for code g + 1 of stream s from its logits (a
+// row that thread t reads at indices t NPT ..)
+template <class Get>
+__device__ int cp_draw(Get get, int cp_vocab, const SampleParams &sp, uint64_t seed,
+                       int frame, int g, SampleShared &sh) {
+  const float u = draw_uniform(seed ^ kSubSeedXor, (uint64_t)frame, (uint64_t)(g + 1));
+  if (cp_vocab <= 2 * kArgBlock) {
+    float x[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int i = 2 * threadIdx.x + j;
+      x[j] = i < cp_vocab ? get(i) : -INFINITY;
+    }
+    return block_sample<2>(x, cp_vocab, sp, u, sh);
+  }
+  float x[3];
+#pragma unroll
+  for (int j = 0; j < 3; j++) {
+    const int i = 3 * threadIdx.x + j;
+    x[j] = i < cp_vocab ? get(i) : -INFINITY;
+  }
+  return block_sample<3>(x, cp_vocab, sp, u, sh);
+}
+
 // ChooseCode for group g + 1 (argmax of the head-g logits), then the input row
 // of the next code-predictor forward: pred_emb[g][code]. One block per stream.
 // Plain scalar arguments (preloaded into SGPRs).
@@ -182,12 +227,38 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_argmax(const float *__restrict
   }
 }
 
+// k_cp_argmax with the sub-sampler's draw (the code predictor's sampling)
+__global__ __launch_bounds__(kArgBlock) void k_cp_sample(const float *__restrict__ cp_logits,
+                                                         const int *__restrict__ alive,
+                                                         const float *__restrict__ pred_emb,
+                                                         float *__restrict__ cp_h,
+                                                         int *__restrict__ codes, int cp_vocab,
+                                                         int groups, int H, int g,
+                                                         SampleParams sp,
+                                                         const uint64_t *__restrict__ seeds,
+                                                         const int *__restrict__ nframes) {
+  __shared__ SampleShared sh;
+  const int s = blockIdx.x, tid = threadIdx.x;
+  if (!alive[s]) return;
+  const float *lg = cp_logits + (size_t)s * cp_vocab;
+  const int code =
+      cp_draw([&](int i) { return lg[i]; }, cp_vocab, sp, seeds[s], nframes[s] - 1, g, sh);
+  if (tid == 0) codes[(size_t)s * groups + g + 1] = code;
+  if (g + 1 < groups - 1) {
+    const float *emb = pred_emb + ((size_t)g * cp_vocab + code) * H;
+    float *x = cp_h + (size_t)s * H;
+    for (int c = tid; c < H; c += kArgBlock) x[c] = emb[c];
+  }
+}
+
 // The int8 path's k_cp_argmax: the head-g logits as the sum of the head's
 // chunk partials in chunk order (row R s + R - 1 of the step's R n rows),
 // ChooseCode for group g + 1, then the next step's input row pred_emb[g][code]
 // (to cp_h), its descriptor (position g + 2) and its quantized layer-0 input.
+template <bool SAMPLE>
 __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
   __shared__ double red[kArgBlock / 64];
+  __shared__ std::conditional_t<SAMPLE, SampleShared, char> sh_cp;
   const int s = blockIdx.x, tid = threadIdx.x;
   const bool next = g + 1 < f.groups - 1;
   if (!f.alive[s]) {
@@ -198,10 +269,9 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
     return;
   }
   const int R = g == 0 ? 2 : 1, rows = R * f.n, row = R * s + R - 1;
-  float bv = -INFINITY;
-  int bi = 0x7fffffff;
-  for (int i = tid; i < f.cp_vocab; i += kArgBlock) {
-    // the chunk partials (cp_hch <= 4) loaded together, added in chunk order
+  // the head's logit i: the chunk partials (cp_hch <= 4) loaded together,
+  // added in chunk order
+  auto logit = [&](int i) {
     float p4[4];
 #pragma unroll
     for (int c = 0; c < 4; c++)
@@ -209,9 +279,17 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
     float v = 0.f;
 #pragma unroll
     for (int c = 0; c < 4; c++) v = c < f.cp_hch ? __fadd_rn(v, p4[c]) : v;
-    argmax_merge(bv, bi, v, i);
+    return v;
+  };
+  int code;
+  if constexpr (SAMPLE) {
+    code = cp_draw(logit, f.cp_vocab, f.sp, f.seeds[s], f.nframes[s] - 1, g, sh_cp);
+  } else {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = tid; i < f.cp_vocab; i += kArgBlock) argmax_merge(bv, bi, logit(i), i);
+    code = block_argmax(bv, bi);
   }
-  const int code = block_argmax(bv, bi);
   if (tid == 0) f.codes[(size_t)s * f.groups + g + 1] = code;
   if (next) {
     const float *emb = f.pred_emb + ((size_t)g * f.cp_vocab + code) * f.H;
@@ -320,6 +398,10 @@ struct q3h_frame {
   int graph_positions = 0;  // attention positions the captured graph covers
   int32_t *pinned = nullptr;  // [n][groups] codes + [n] alive
   std::vector<void *> allocs;
+  // the choosers (TQwenTalker.Sampling) and the source of sentence seeds when
+  // its seed is 0 (a fresh one per Start, talker.pas:582-584)
+  q3h_sampling sampling{};
+  std::mt19937_64 seed_rng{std::random_device{}()};
   // device-side Start: the row plan and the projected rows
   int start_cap = 0;
   int2 *start_plan = nullptr;  // [start_cap]
@@ -362,7 +444,10 @@ void enqueue_step(q3h_frame *f, int positions, hipStream_t st) {
   q3h_stack *cp = f->cp, *tk = f->talker;
   FrameDev fd = f->fd;
   const bool cq = fd.cp_xq != nullptr, tq = fd.t_xq != nullptr;  // the folded int8 paths
-  hipLaunchKernelGGL(k_choose_code0, dim3(n), dim3(kArgBlock), 0, st, fd);
+  if (fd.sp0.do_sample)
+    hipLaunchKernelGGL(k_choose_code0<true>, dim3(n), dim3(kArgBlock), 0, st, fd);
+  else
+    hipLaunchKernelGGL(k_choose_code0<false>, dim3(n), dim3(kArgBlock), 0, st, fd);
   // code predictor: 2 rows per stream, then one row per group
   // one stream on the Qwen3-TTS shapes: steps 1.. run the fused single-row
   // path (positions are fixed: step g adds position g + 1)
@@ -378,7 +463,10 @@ void enqueue_step(q3h_frame *f, int positions, hipStream_t st) {
       io.final_norm = cp->final_norm;
       run_layers(cp, f->cw, n * R, c.groups, R == 1, st, io);
       launch_gemm_i8_partial(cp->heads[c.cp_heads[g]], f->cw.xa, n * R, f->cw.gpart, st);
-      hipLaunchKernelGGL(k_cp_next, dim3(n), dim3(kArgBlock), 0, st, fd, g);
+      if (fd.sp.do_sample)
+        hipLaunchKernelGGL(k_cp_next<true>, dim3(n), dim3(kArgBlock), 0, st, fd, g);
+      else
+        hipLaunchKernelGGL(k_cp_next<false>, dim3(n), dim3(kArgBlock), 0, st, fd, g);
       continue;
     }
     if (fused && g > 0) {
@@ -391,8 +479,13 @@ void enqueue_step(q3h_frame *f, int positions, hipStream_t st) {
     // final norm of each stream's last row + head g, one launch
     linear(cp, f->cw, cp->heads[c.cp_heads[g]], f->cw.h + (size_t)(R - 1) * H, R * H, n,
            cp->final_norm, f->cw.logits, c.cp_vocab, EPI_STORE, nullptr, st);
-    hipLaunchKernelGGL(k_cp_argmax, dim3(n), dim3(kArgBlock), 0, st, fd.cp_logits, fd.alive,
-                       fd.pred_emb, fd.cp_h, fd.codes, fd.cp_vocab, fd.groups, fd.H, g);
+    if (fd.sp.do_sample)
+      hipLaunchKernelGGL(k_cp_sample, dim3(n), dim3(kArgBlock), 0, st, fd.cp_logits, fd.alive,
+                         fd.pred_emb, fd.cp_h, fd.codes, fd.cp_vocab, fd.groups, fd.H, g, fd.sp,
+                         fd.seeds, (const int *)fd.nframes);
+    else
+      hipLaunchKernelGGL(k_cp_argmax, dim3(n), dim3(kArgBlock), 0, st, fd.cp_logits, fd.alive,
+                         fd.pred_emb, fd.cp_h, fd.codes, fd.cp_vocab, fd.groups, fd.H, g);
   }
   // the talker
   if (tq) {
@@ -500,6 +593,10 @@ extern "C" int q3h_frame_create(q3h_stack *talker, q3h_stack *cp, const q3h_fram
     d.past = falloc<float>(f, (size_t)n * H);
     d.codes = falloc<int>(f, (size_t)n * c.groups);
     d.seen = falloc<uint8_t>(f, (size_t)n * c.vocab);
+    d.seeds = falloc<uint64_t>(f, n);
+    d.sp0 = d.sp = SampleParams{0, 1.0f, 0, 1.0f};  // greedy until q3h_frame_set_sampling
+    f->sampling.temperature = f->sampling.sub_temperature = 1.0f;
+    f->sampling.top_p = f->sampling.sub_top_p = 1.0f;
     d.nframes = falloc<int>(f, n);
     d.step = falloc<int>(f, n);
     d.alive = falloc<int>(f, n);
@@ -528,6 +625,7 @@ extern "C" int q3h_frame_create(q3h_stack *talker, q3h_stack *cp, const q3h_fram
       d.t_eps = talker->cfg.rms_eps;
     }
     check_hip(hipMemset(d.alive, 0, sizeof(int) * n), "frame init");
+    check_hip(hipMemset(const_cast<uint64_t *>(d.seeds), 0, sizeof(uint64_t) * n), "frame init");
     check_hip(hipMemset(d.codes, 0xff, sizeof(int) * n * c.groups), "frame init");
     check_hip(hipHostMalloc((void **)&f->pinned, sizeof(int32_t) * n * (c.groups + 1)),
               "hipHostMalloc");
@@ -579,6 +677,11 @@ void start_stream(q3h_frame *f, int stream, int rows, int trailing_rows, Fill &&
   launch_advance(tc->dev_arr, nullptr, 1, rows, st);
   check_hip(hipGetLastError(), "prefill kernels");
   const int zero = 0, one = 1;
+  // the sentence seed: the one of the settings, or a fresh one (Random64 shr 1)
+  const uint64_t seed = f->sampling.seed ? f->sampling.seed : (f->seed_rng() >> 1);
+  check_hip(hipMemcpyAsync(const_cast<uint64_t *>(d.seeds) + stream, &seed, 8,
+                           hipMemcpyHostToDevice, st),
+            "seed");
   check_hip(hipMemsetAsync(d.seen + (size_t)stream * c.vocab, 0, c.vocab, st), "reset seen");
   check_hip(hipMemcpyAsync(d.nframes + stream, &zero, 4, hipMemcpyHostToDevice, st), "state");
   check_hip(hipMemcpyAsync(d.step + stream, &zero, 4, hipMemcpyHostToDevice, st), "state");
@@ -593,6 +696,39 @@ void start_stream(q3h_frame *f, int stream, int rows, int trailing_rows, Fill &&
 }
 
 }  // namespace
+
+extern "C" int q3h_frame_set_sampling(q3h_frame *f, const q3h_sampling *sp) {
+  return guard([&] {
+    require(f != nullptr && sp != nullptr, Q3H_E_ARG, "q3h_frame_set_sampling: NULL argument");
+    const q3h_frame_config &c = f->cfg;
+    auto check = [&](int on, float t, int k, float p, int vocab, const char *who) {
+      if (!on) return;
+      const std::string w = std::string("q3h_frame_set_sampling: ") + who;
+      require(t > 0.0f, Q3H_E_ARG, w + " temperature must be positive");
+      require(k >= 0, Q3H_E_ARG, w + " top_k must be >= 0");
+      require(p > 0.0f && p <= 1.0f, Q3H_E_ARG, w + " top_p must be in (0, 1]");
+      require(p == 1.0f || (k >= 1 && k <= 64), Q3H_E_ARG,
+              w + " top_p < 1 needs 1 <= top_k <= 64");
+      require(vocab <= 3 * kSampleThreads, Q3H_E_ARG, w + " sampling takes at most 3072 codes");
+    };
+    check(sp->do_sample, sp->temperature, sp->top_k, sp->top_p, c.vocab, "talker");
+    check(sp->sub_do_sample, sp->sub_temperature, sp->sub_top_k, sp->sub_top_p, c.cp_vocab,
+          "code predictor");
+    check_hip(hipSetDevice(f->talker->dev->ordinal), "hipSetDevice");
+    check_hip(hipStreamSynchronize(f->stream), "frame sync");
+    f->sampling = *sp;
+    auto params = [](int on, float t, int k, float p) {
+      return on ? SampleParams{1, t, k, p} : SampleParams{0, 1.0f, 0, 1.0f};
+    };
+    f->fd.sp0 = params(sp->do_sample, sp->temperature, sp->top_k, sp->top_p);
+    f->fd.sp = params(sp->sub_do_sample, sp->sub_temperature, sp->sub_top_k, sp->sub_top_p);
+    // the parameters are kernel arguments of the captured step: capture again
+    if (f->exec) (void)hipGraphExecDestroy(f->exec);
+    if (f->graph) (void)hipGraphDestroy(f->graph);
+    f->exec = nullptr;
+    f->graph = nullptr;
+  });
+}
 
 extern "C" int q3h_frame_start(q3h_frame *f, int stream, const float *prefill, int rows,
                                const float *trailing, int trailing_rows) {

@@ -87,6 +87,16 @@ class TextConfig(ctypes.Structure):
     ]
 
 
+class Sampling(ctypes.Structure):
+    _fields_ = [
+        ("do_sample", ctypes.c_int32), ("temperature", ctypes.c_float),
+        ("top_k", ctypes.c_int32), ("top_p", ctypes.c_float),
+        ("sub_do_sample", ctypes.c_int32), ("sub_temperature", ctypes.c_float),
+        ("sub_top_k", ctypes.c_int32), ("sub_top_p", ctypes.c_float),
+        ("seed", ctypes.c_uint64),
+    ]
+
+
 class StartIds(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in
                 ("tts_bos", "tts_eos", "tts_pad", "codec_pad", "codec_bos")]
@@ -129,6 +139,7 @@ SIGNATURES = {
                              ctypes.POINTER(_P)]),
     "q3h_text_project": (_I, [_P, _IP, _I, _FP]),
     "q3h_text_destroy": (_I, [_P]),
+    "q3h_frame_set_sampling": (_I, [_P, ctypes.POINTER(Sampling)]),
     "q3h_frame_start_text": (_I, [_P, _I, _P, ctypes.POINTER(StartIds), _IP, _I, _IP, _I, _I]),
     "q3h_quantize_row_q8_0": (_I, [_FP, _P, ctypes.c_int64]),
     "q3h_stack_time_gemv": (_I, [_P, _I, _I, _I, _FP, ctypes.POINTER(_I),
@@ -437,6 +448,15 @@ class Frame:
         t = _f32(trailing) if trailing is not None and len(trailing) else None
         _check(lib().q3h_frame_start(self.h, stream, _fp(p), p.shape[0], _fp(t),
                                      0 if t is None else t.shape[0]))
+
+    def set_sampling(self, do_sample=False, temperature=1.0, top_k=0, top_p=1.0,
+                     sub_do_sample=False, sub_temperature=1.0, sub_top_k=0, sub_top_p=1.0,
+                     seed=0):
+        """TQwenTalker.Sampling (talker.pas:150): the talker's and the code
+        predictor's choosers; seed 0 draws a fresh sentence seed per start."""
+        sp = Sampling(int(do_sample), temperature, top_k, top_p, int(sub_do_sample),
+                      sub_temperature, sub_top_k, sub_top_p, seed)
+        _check(lib().q3h_frame_set_sampling(self.h, ctypes.byref(sp)))
 
     def start_text(self, stream, proj, ids, codec, tts_bos, tts_eos, tts_pad, codec_pad,
                    codec_bos, non_streaming):

@@ -538,9 +538,206 @@ int q3o_argmax(const float *p, int n) {
   return r;
 }
 
+static void code0_scores(const float *logits, int vocab, int eos, const int *history,
+                         int nhistory, float penalty, float *work);
+
 int q3o_choose_code0(const float *logits, int vocab, int eos, const int *history,
                      int nhistory, float penalty) {
   float *work = (float *)malloc(sizeof(float) * vocab);
+  code0_scores(logits, vocab, eos, history, nhistory, penalty, work);
+  const int r = q3o_argmax(work, vocab);
+  free(work);
+  return r;
+}
+
+/* ------------------------------------------------------------------ */
+/* sampling                                                            */
+
+/* Philox4x64-10 (Salmon, Moraes, Dror, Shaw, SC 2011): 10 rounds of the
+ * two 64 x 64 -> 128-bit products, the key bumped by the Weyl constants */
+void q3o_philox4x64(const uint64_t ctr[4], const uint64_t key[2], uint64_t out[4]) {
+  uint64_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3], k0 = key[0], k1 = key[1];
+  for (int r = 0; r < 10; r++) {
+    const unsigned __int128 p0 = (unsigned __int128)0xD2E7470EE14C6C93ull * c0;
+    const unsigned __int128 p1 = (unsigned __int128)0xCA5A826395121157ull * c2;
+    const uint64_t hi0 = (uint64_t)(p0 >> 64), lo0 = (uint64_t)p0;
+    const uint64_t hi1 = (uint64_t)(p1 >> 64), lo1 = (uint64_t)p1;
+    c0 = hi1 ^ c1 ^ k0;
+    c1 = lo1;
+    c2 = hi0 ^ c3 ^ k1;
+    c3 = lo0;
+    k0 += 0x9E3779B97F4A7C15ull;
+    k1 += 0xBB67AE8584CAA73Bull;
+  }
+  out[0] = c0;
+  out[1] = c1;
+  out[2] = c2;
+  out[3] = c3;
+}
+
+float q3o_draw_uniform(uint64_t seed, uint64_t frame, uint64_t group) {
+  const uint64_t ctr[4] = {frame, group, 0, 0}, key[2] = {seed, 0};
+  uint64_t out[4];
+  q3o_philox4x64(ctr, key, out);
+  return (float)(uint32_t)(out[0] >> 40) * 0x1p-24f;
+}
+
+static uint32_t order_key(float v) {
+  uint32_t b;
+  memcpy(&b, &v, 4);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+typedef struct {
+  uint32_t key;
+  int idx;
+  float v;
+} cand_t;
+
+/* descending key, then ascending index */
+static int cand_cmp(const void *a, const void *b) {
+  const cand_t *x = (const cand_t *)a, *y = (const cand_t *)b;
+  if (x->key != y->key) return x->key > y->key ? -1 : 1;
+  return x->idx < y->idx ? -1 : (x->idx > y->idx);
+}
+
+static int u32_desc(const void *a, const void *b) {
+  const uint32_t x = *(const uint32_t *)a, y = *(const uint32_t *)b;
+  return x > y ? -1 : (x < y);
+}
+
+static int last_positive(const float *W, int lo, int hi) {
+  int best = -1;
+  for (int i = lo; i < hi; i++)
+    if (W[i] > 0.0f) best = i;
+  return best;
+}
+
+/* The draw of the library's sampler (temperature, top-k, top-p, one uniform
+ * through the inverse distribution), with its fixed evaluation order: the
+ * values in 1024 threads of NPT = ceil(n / 1024) consecutive indices, sums by
+ * thread, by 64 segments of 16 threads, then over the segments; top-p over
+ * at most 64 values kept by a top-k of at most 64. */
+int q3o_sample(const float *x, int n, float temperature, int top_k, float top_p, float u) {
+  if (n <= 0 || n > 3 * 1024) return -1;
+  const int NPT = (n + 1023) / 1024, N = 1024 * NPT;
+  float *v = (float *)malloc(sizeof(float) * N);
+  float *W = (float *)malloc(sizeof(float) * N);
+  uint32_t *key = (uint32_t *)malloc(sizeof(uint32_t) * N);
+  uint8_t *kept = (uint8_t *)malloc(N);
+  for (int i = 0; i < N; i++) {
+    const int in = i < n;
+    const float a = in ? x[i] : -INFINITY;
+    v[i] = temperature == 1.0f ? a : a / temperature;
+    key[i] = order_key(v[i]);
+    kept[i] = (uint8_t)in;
+  }
+  const int topk = top_k >= 1 && top_k < n;
+  if (topk) {
+    uint32_t *ks = (uint32_t *)malloc(sizeof(uint32_t) * n);
+    memcpy(ks, key, sizeof(uint32_t) * n);
+    qsort(ks, n, sizeof(uint32_t), u32_desc);
+    const uint32_t tau = ks[top_k - 1];
+    free(ks);
+    for (int i = 0; i < n; i++) kept[i] = kept[i] && key[i] >= tau;
+  }
+  float M = -INFINITY;
+  for (int i = 0; i < n; i++)
+    if (kept[i] && v[i] > M) M = v[i];
+  if (top_p < 1.0f && topk && top_k <= 64) {
+    cand_t c[64];
+    int cnt = 0;
+    for (int i = 0; i < n; i++)
+      if (kept[i]) {
+        if (cnt < 64) {
+          c[cnt].key = key[i];
+          c[cnt].idx = i;
+          c[cnt].v = v[i];
+        }
+        cnt++;
+      }
+    if (cnt <= 64) {
+      qsort(c, cnt, sizeof(cand_t), cand_cmp);
+      float w[64], S = 0.0f;
+      for (int q = 0; q < cnt; q++) w[q] = q3o_expf(c[q].v - M);
+      for (int q = cnt - 1; q >= 0; q--) S = S + w[q];
+      const float lim = 1.0f - top_p;
+      float cum = 0.0f;
+      int last = 0;
+      for (int q = cnt - 1; q >= 1; q--) {
+        cum = cum + w[q] / S;
+        if (cum > lim) {
+          last = q;
+          break;
+        }
+      }
+      const uint32_t tk = c[last].key;
+      const int ti = c[last].idx;
+      for (int i = 0; i < n; i++)
+        kept[i] = kept[i] && (key[i] > tk || (key[i] == tk && i <= ti));
+    }
+  }
+  float A[1024], B[64];
+  for (int i = 0; i < N; i++) W[i] = kept[i] ? q3o_expf(v[i] - M) : 0.0f;
+  for (int t = 0; t < 1024; t++) {
+    float a = 0.0f;
+    for (int j = 0; j < NPT; j++) a = a + W[t * NPT + j];
+    A[t] = a;
+  }
+  for (int s = 0; s < 64; s++) {
+    float b = 0.0f;
+    for (int q = 0; q < 16; q++) b = b + A[16 * s + q];
+    B[s] = b;
+  }
+  float S = 0.0f;
+  for (int s = 0; s < 64; s++) S = S + B[s];
+  const float target = u * S;
+  float r = 0.0f;
+  int seg = -1, pick = -1;
+  for (int s = 0; s < 64; s++) {
+    if (r + B[s] > target) {
+      seg = s;
+      break;
+    }
+    r = r + B[s];
+  }
+  if (seg < 0) {
+    pick = last_positive(W, 0, N);
+  } else {
+    int th = -1;
+    for (int q = 0; q < 16; q++) {
+      const float aq = A[16 * seg + q];
+      if (r + aq > target) {
+        th = 16 * seg + q;
+        break;
+      }
+      r = r + aq;
+    }
+    if (th < 0) {
+      pick = last_positive(W, 16 * seg * NPT, 16 * (seg + 1) * NPT);
+    } else {
+      for (int j = 0; j < NPT; j++) {
+        const float wj = W[th * NPT + j];
+        if (r + wj > target) {
+          pick = th * NPT + j;
+          break;
+        }
+        r = r + wj;
+      }
+      if (pick < 0) pick = last_positive(W, th * NPT, th * NPT + NPT);
+    }
+  }
+  free(v);
+  free(W);
+  free(key);
+  free(kept);
+  return pick;
+}
+
+/* the scores ChooseCode0 hands to the argmax or the sampler (talker.pas:
+ * 603-626) */
+static void code0_scores(const float *logits, int vocab, int eos, const int *history,
+                         int nhistory, float penalty, float *work) {
   memcpy(work, logits, sizeof(float) * vocab);
   for (int i = vocab - 1024; i < vocab; i++)
     if (i != eos) work[i] = -INFINITY;
@@ -552,9 +749,6 @@ int q3o_choose_code0(const float *logits, int vocab, int eos, const int *history
       if (work[i] != s) continue; /* already penalized (or forbidden) */
       work[i] = s > 0 ? s / penalty : s * penalty;
     }
-  const int r = q3o_argmax(work, vocab);
-  free(work);
-  return r;
 }
 
 /* ------------------------------------------------------------------ */
@@ -564,10 +758,13 @@ struct q3o_frame {
   q3o_stack *talker, *cp;
   q3o_frame_tables t;
   q3o_ctx *tctx, *cctx;
-  float *logits, *past, *x, *plogits, *trailing;
+  float *logits, *past, *x, *plogits, *trailing, *work;
   int *history;
   int nhist, cap_hist, trailing_rows, step;
+  q3o_sampling sampling;
 };
+
+void q3o_frame_set_sampling(q3o_frame *f, const q3o_sampling *s) { f->sampling = *s; }
 
 q3o_frame *q3o_frame_create(q3o_stack *talker, q3o_stack *cp,
                             const q3o_frame_tables *t, int max_positions) {
@@ -580,6 +777,7 @@ q3o_frame *q3o_frame_create(q3o_stack *talker, q3o_stack *cp,
   f->cctx = q3o_ctx_create(cp, t->groups);
   f->logits = (float *)calloc(t->vocab, sizeof(float));
   f->plogits = (float *)calloc(t->cp_vocab, sizeof(float));
+  f->work = (float *)calloc(t->vocab, sizeof(float));
   f->past = (float *)calloc(H, sizeof(float));
   f->x = (float *)calloc(2 * H, sizeof(float));
   f->cap_hist = 64;
@@ -593,6 +791,7 @@ void q3o_frame_destroy(q3o_frame *f) {
   q3o_ctx_destroy(f->cctx);
   free(f->logits);
   free(f->plogits);
+  free(f->work);
   free(f->past);
   free(f->x);
   free(f->history);
@@ -626,7 +825,14 @@ static void add_row(const float *emb, int id, int H, float *y) {
 int q3o_frame_next(q3o_frame *f, int *codes) {
   const int H = f->talker->cfg.hidden;
   const q3o_frame_tables *t = &f->t;
-  const int code = q3o_choose_code0(f->logits, t->vocab, t->eos, f->history, f->nhist, t->penalty);
+  const q3o_sampling *sp = &f->sampling;
+  const uint64_t frame = (uint64_t)f->nhist;
+  code0_scores(f->logits, t->vocab, t->eos, f->history, f->nhist, t->penalty, f->work);
+  const int code =
+      sp->do_sample
+          ? q3o_sample(f->work, t->vocab, sp->temperature, sp->top_k, sp->top_p,
+                       q3o_draw_uniform(sp->seed, frame, 0))
+          : q3o_argmax(f->work, t->vocab);
   if (code == t->eos) return 0;
   codes[0] = code;
   if (f->nhist == f->cap_hist) {
@@ -648,7 +854,11 @@ int q3o_frame_next(q3o_frame *f, int *codes) {
       q3o_forward_embeds(f->cctx, f->x, 1, normed, NULL);
     }
     q3o_head(t->cp_heads[g], cdt, caq, t->cp_vocab, H, normed, f->plogits);
-    codes[g + 1] = q3o_argmax(f->plogits, t->cp_vocab);
+    codes[g + 1] =
+        sp->sub_do_sample
+            ? q3o_sample(f->plogits, t->cp_vocab, sp->sub_temperature, sp->sub_top_k,
+                         sp->sub_top_p, q3o_draw_uniform(sp->seed ^ 0x5DEECE66Dull, frame, g + 1))
+            : q3o_argmax(f->plogits, t->cp_vocab);
   }
   free(normed);
   /* the next talker input: the 16 embeddings, plus the text (or tts_pad) */

@@ -132,6 +132,32 @@ float q3o_expf(float x);
 int q3o_choose_code0(const float *logits, int vocab, int eos, const int *history,
                      int nhistory, float penalty);
 
+/* Philox4x64-10 (Salmon et al., SC 2011): out = the block of counter ctr
+   under key */
+void q3o_philox4x64(const uint64_t ctr[4], const uint64_t key[2], uint64_t out[4]);
+/* the sampler's uniform of draw (frame, group) under seed: counter (frame,
+   group, 0, 0), key (seed, 0), (first output >> 40) * 2^-24 */
+float q3o_draw_uniform(uint64_t seed, uint64_t frame, uint64_t group);
+/* the library's draw from x[n] (n <= 3072): temperature, top-k (0: off),
+   top-p (1: off; applied when 1 <= top_k <= 64), then u through the inverse
+   distribution in the library's evaluation order; returns the index */
+int q3o_sample(const float *x, int n, float temperature, int top_k, float top_p, float u);
+
+/* TQwenSampling (talker.pas:60-70) without the repetition penalty (a frame
+   table); seed: the sentence seed (the sub-sampler uses seed xor 0x5DEECE66D,
+   talker.pas:585) */
+typedef struct {
+  int32_t do_sample;
+  float temperature;
+  int32_t top_k;
+  float top_p;
+  int32_t sub_do_sample;
+  float sub_temperature;
+  int32_t sub_top_k;
+  float sub_top_p;
+  uint64_t seed;
+} q3o_sampling;
+
 /* frame step: the talker and code-predictor stacks, their heads, the tables */
 typedef struct {
   const void *talker_head; /* [vocab][hidden] */
@@ -156,6 +182,10 @@ int q3o_frame_next(q3o_frame *f, int *codes);
 const float *q3o_frame_logits(const q3o_frame *f);
 const float *q3o_frame_past_hidden(const q3o_frame *f);
 q3o_ctx *q3o_frame_talker_ctx(q3o_frame *f);
+/* the choosers of q3o_frame_next: argmax (the default) or the draws of
+   q3o_sample with the uniforms of q3o_draw_uniform (code 0: seed, group 0;
+   code g: seed ^ 0x5DEECE66D, group g; frame = frames emitted before) */
+void q3o_frame_set_sampling(q3o_frame *f, const q3o_sampling *s);
 
 #ifdef __cplusplus
 }

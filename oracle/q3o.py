@@ -45,6 +45,16 @@ class FrameTables(ctypes.Structure):
     ]
 
 
+class Sampling(ctypes.Structure):
+    _fields_ = [
+        ("do_sample", ctypes.c_int32), ("temperature", ctypes.c_float),
+        ("top_k", ctypes.c_int32), ("top_p", ctypes.c_float),
+        ("sub_do_sample", ctypes.c_int32), ("sub_temperature", ctypes.c_float),
+        ("sub_top_k", ctypes.c_int32), ("sub_top_p", ctypes.c_float),
+        ("seed", ctypes.c_uint64),
+    ]
+
+
 _lib = None
 
 
@@ -84,6 +94,14 @@ def lib():
             "q3o_frame_next": (ctypes.c_int, [_P, _IP]),
             "q3o_frame_logits": (_FP, [_P]),
             "q3o_frame_past_hidden": (_FP, [_P]),
+            "q3o_philox4x64": (None, [ctypes.POINTER(ctypes.c_uint64),
+                                      ctypes.POINTER(ctypes.c_uint64),
+                                      ctypes.POINTER(ctypes.c_uint64)]),
+            "q3o_draw_uniform": (ctypes.c_float, [ctypes.c_uint64, ctypes.c_uint64,
+                                                  ctypes.c_uint64]),
+            "q3o_sample": (ctypes.c_int, [_FP, ctypes.c_int, ctypes.c_float, ctypes.c_int,
+                                          ctypes.c_float, ctypes.c_float]),
+            "q3o_frame_set_sampling": (None, [_P, ctypes.POINTER(Sampling)]),
             "q3o_text_project": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                                 ctypes.c_int, _FP, _FP, _FP, _FP, _IP,
                                                 ctypes.c_int, _FP]),
@@ -159,6 +177,25 @@ def choose_code0(logits, eos, history, penalty):
     h = np.ascontiguousarray(history, dtype=np.int32)
     return lib().q3o_choose_code0(_fp(lg), lg.size, eos, h.ctypes.data_as(_IP), h.size,
                                   ctypes.c_float(penalty))
+
+
+def philox4x64(ctr, key):
+    """Philox4x64-10 block of counter ctr (4 x uint64) under key (2 x uint64)."""
+    c = (ctypes.c_uint64 * 4)(*[int(x) for x in ctr])
+    k = (ctypes.c_uint64 * 2)(*[int(x) for x in key])
+    o = (ctypes.c_uint64 * 4)()
+    lib().q3o_philox4x64(c, k, o)
+    return [int(x) for x in o]
+
+
+def draw_uniform(seed, frame, group):
+    return float(lib().q3o_draw_uniform(seed, frame, group))
+
+
+def sample(x, temperature=1.0, top_k=0, top_p=1.0, u=0.5):
+    """The library's draw from x (n <= 3072) with uniform u."""
+    x = _f32(x)
+    return int(lib().q3o_sample(_fp(x), x.size, temperature, top_k, top_p, u))
 
 
 def text_project(emb, fc1_w, fc1_b, fc2_w, fc2_b, ids):
@@ -319,6 +356,14 @@ class Frame:
                                    0 if tr is None else tr.shape[0])
         if rc:
             raise ValueError("q3o_frame_start failed")
+
+    def set_sampling(self, do_sample=False, temperature=1.0, top_k=0, top_p=1.0,
+                     sub_do_sample=False, sub_temperature=1.0, sub_top_k=0, sub_top_p=1.0,
+                     seed=1):
+        self._sampling = Sampling(int(do_sample), temperature, top_k, top_p,
+                                  int(sub_do_sample), sub_temperature, sub_top_k, sub_top_p,
+                                  seed)
+        lib().q3o_frame_set_sampling(self.h, ctypes.byref(self._sampling))
 
     def next(self):
         codes = np.empty(self.groups, dtype=np.int32)
