@@ -70,9 +70,9 @@ void Work::ensure(const q3h_stack *s, int rows, int splits, int head_rows) {
     pn = std::max(pn, (size_t)gemm_i8_chunks(NQ) * pr * H);
     pn = std::max(pn, (size_t)gemm_i8_chunks(I) * pr * H);
     gpart = (float *)dev_alloc(sizeof(float) * pn);
-  } else if (c.dtype == Q3H_F32) {
-    // K-slice sums of the f32 products over up to 16 rows
-    gpart = (float *)dev_alloc(sizeof(float) * kF32Slices * std::min<size_t>(R, 16) * H);
+  } else {
+    // K-slice sums of the products of o_proj and down (f32 activations)
+    gpart = (float *)dev_alloc(sizeof(float) * kF32Slices * R * H);
   }
 }
 
@@ -189,16 +189,17 @@ static void run_layers_partial(const q3h_stack *s, Work &w, int M, bool fused,
   }
 }
 
-// f32 stacks over a few rows (batched decode): the matrix-core products, with
-// o_proj and down (N = hidden, 64 tiles of 16 rows) cut into K slices so that
-// they fill the chip; each slice sum is added to the residual in slice order
-// by the kernel that also applies the next RMSNorm, whose output feeds the
-// next product directly.
+// f32 activations on the matrix cores (f32 weights at any row count, Q8_0
+// weights over more rows than the matrix-vector kernels take): o_proj and
+// down (N = hidden: too few weight-row tiles to fill the chip) are cut into K
+// slices; each slice sum is added to the residual in slice order by the
+// kernel that also applies the next RMSNorm, whose output feeds the next
+// product directly.
 bool f32_slice_path(const q3h_stack *s, int M) {
   const q3h_stack_config &c = s->cfg;
   const int NQ = c.heads * c.head_dim, I = c.intermediate, H = c.hidden;
   const int ldq = NQ + 2 * c.kv_heads * c.head_dim;
-  return c.dtype == Q3H_F32 && !c.act_q8 && M <= 16 && gemm_f32_supported(ldq, H) &&
+  return !c.act_q8 && (c.dtype == Q3H_F32 || M > kGemvRows) && gemm_f32_supported(ldq, H) &&
          gemm_f32_supported(2 * I, H) && gemm_f32_slices_supported(H, NQ) &&
          gemm_f32_slices_supported(H, I);
 }

@@ -147,10 +147,13 @@ __global__ __launch_bounds__(64 * (KK / KC)) void k_gemm_f32(const float *__rest
 // are issued before the MFMAs of chunk c. Operands as in k_gemm_f32 (lane l:
 // row l % 16, columns 4 (l / 16) .. + 3 of each 16-column step); the result
 // tile of a wave is complete, so the epilogue needs no reduction.
+//
+// K-slices: workgroup z takes columns z kc .. z kc + kc - 1 (kc = K without a
+// split); EPI_PART stores its sums to slice z of y [gridDim.z][M][ldy].
 template <int WN, int EPI>
 __global__ __launch_bounds__(64 * WN) void k_gemm_f32_m64(const float *__restrict__ w,
                                                           const float *__restrict__ x, int ldx,
-                                                          int M, int N, int K,
+                                                          int M, int N, int K, int kc,
                                                           float *__restrict__ y, int ldy) {
   constexpr int NT = 64 * WN, XS = 36;  // threads; LDS row stride (floats, padded)
   constexpr int XF4 = 64 * 32 / 4 / NT;  // float4 of an activation chunk per thread
@@ -158,14 +161,15 @@ __global__ __launch_bounds__(64 * WN) void k_gemm_f32_m64(const float *__restric
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * 16 * WN + 16 * wave, m0 = blockIdx.y * 64;
-  const float *wr = w + (size_t)min(n0 + r, N - 1) * K + 4 * g;
+  const int kz = blockIdx.z * kc;
+  const float *wr = w + (size_t)min(n0 + r, N - 1) * K + kz + 4 * g;
   // activation chunk loads: float4 f = t + NT i of the 64 x 8 float4 chunk
   const float *xr[XF4];
   int xo[XF4];
 #pragma unroll
   for (int i = 0; i < XF4; i++) {
     const int f = t + NT * i, row = f >> 3, c4 = f & 7;
-    xr[i] = x + (size_t)min(m0 + row, M - 1) * ldx + 4 * c4;
+    xr[i] = x + (size_t)min(m0 + row, M - 1) * ldx + kz + 4 * c4;
     xo[i] = row * XS + 4 * c4;
   }
   float4 xn[XF4], wn[2], wc[2];
@@ -184,7 +188,7 @@ __global__ __launch_bounds__(64 * WN) void k_gemm_f32_m64(const float *__restric
   wc[0] = wn[0];
   wc[1] = wn[1];
   __syncthreads();
-  const int nc = K / 32;
+  const int nc = kc / 32;
   for (int c = 0; c < nc; c++) {
     const int b = c & 1;
     if (c + 1 < nc) load(32 * (c + 1));
@@ -223,6 +227,8 @@ __global__ __launch_bounds__(64 * WN) void k_gemm_f32_m64(const float *__restric
           y[(size_t)m * ldy + n] += v;
         else if (EPI == EPI_ADD_SILU)
           y[(size_t)m * ldy + n] = silu_clamp_f(y[(size_t)m * ldy + n] + v);
+        else if (EPI == EPI_PART)
+          y[((size_t)blockIdx.z * M + m) * ldy + n] = v;
         else
           y[(size_t)m * ldy + n] = v;
       }
@@ -384,17 +390,20 @@ void launch_t(const Mat &W, const float *x, int ldx, int M, int epi, float *y, i
 
 template <int WN>
 void launch_m64(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
-                hipStream_t st) {
-  const dim3 grid(W.N / (16 * WN), (M + 63) / 64), block(64 * WN);
+                hipStream_t st, int ks = 1) {
+  const dim3 grid(W.N / (16 * WN), (M + 63) / 64, ks), block(64 * WN);
+  const int kc = W.K / ks;
 #define Q3H_G(E)                                                                               \
-  hipLaunchKernelGGL((k_gemm_f32_m64<WN, E>), grid, block, 0, st, W.f, x, ldx, M, W.N, W.K, y, \
-                     ldy)
+  hipLaunchKernelGGL((k_gemm_f32_m64<WN, E>), grid, block, 0, st, W.f, x, ldx, M, W.N, W.K, kc, \
+                     y, ldy)
   if (epi == EPI_STORE)
     Q3H_G(EPI_STORE);
   else if (epi == EPI_ADD)
     Q3H_G(EPI_ADD);
   else if (epi == EPI_ADD_SILU)
     Q3H_G(EPI_ADD_SILU);
+  else if (epi == EPI_PART)
+    Q3H_G(EPI_PART);
   else
     Q3H_G(EPI_SWIGLU);
 #undef Q3H_G
@@ -440,10 +449,23 @@ bool gemm_f32_slices_supported(int N, int K) {
 
 void launch_gemm_f32_part(const Mat &W, const float *x, int ldx, int M, float *part,
                           hipStream_t st) {
-  if (W.f)
-    launch_t<1, false>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
-  else
-    launch_t<1, true>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
+  if (W.f) {
+    if (M > 64 && W.N % 64 == 0)
+      launch_m64<4>(W, x, ldx, M, EPI_PART, part, W.N, st, kF32Slices);
+    else if (M <= 16)
+      launch_t<1, false>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
+    else if (M <= 32)
+      launch_t<2, false>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
+    else
+      launch_t<4, false>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
+  } else {
+    if (M <= 16)
+      launch_t<1, true>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
+    else if (M <= 32)
+      launch_t<2, true>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
+    else
+      launch_t<4, true>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
+  }
 }
 
 void launch_resid_norm(float *h, const float *part, int M, int K, const float *norm_w,
