@@ -89,6 +89,36 @@ def build_model(dev, seed, max_positions, act_q8, dtype=q3h.Q8_0):
     return ts, cs, tables, f32
 
 
+def load_from_bf16(dev, f32, act_q8, dtype=q3h.Q8_0):
+    """The load path of the reference (safetensors BF16 rows -> device weights,
+    lm.pas:244-308): both stacks and their 16 heads created from BF16 host
+    rows, widened and quantized on the device. Seconds of the creation calls
+    (the host BF16 rows prepared beforehand, untimed)."""
+    b = synth.to_bf16_bits
+
+    def rows(layers):
+        return [{k: (b(v) if k.startswith("w") else v) for k, v in L.items()} for L in layers]
+    tl, cl = rows(f32["tl"]), rows(f32["cl"])
+    th, ch = b(f32["th"]), [b(h) for h in f32["ch"]]
+    nbytes = sum(v.nbytes for L in tl + cl for k, v in L.items() if k.startswith("w"))
+    nbytes += th.nbytes + sum(h.nbytes for h in ch)
+    t0 = time.perf_counter()
+    ts = q3h.Stack(dev, dict(synth.TALKER, dtype=dtype, kv_f16=0, act_q8=act_q8,
+                             max_positions=64), tl, f32["tf"], q3h.BF16)
+    cs = q3h.Stack(dev, dict(synth.PREDICTOR, dtype=dtype, kv_f16=0, act_q8=act_q8,
+                             max_positions=16), cl, f32["cf"], q3h.BF16)
+    ts.add_head(th, q3h.BF16)
+    for h in ch:
+        cs.add_head(h, q3h.BF16)
+    dt = time.perf_counter() - t0
+    ts.destroy()
+    cs.destroy()
+    log(f"load from BF16 rows: {dt:.2f} s ({nbytes / 1e9:.2f} GB of BF16 weights)")
+    return dict(seconds=round(dt, 3), bf16_bytes=int(nbytes),
+                what="talker (28 layers) + code predictor (5 layers) + 16 heads, BF16 host rows "
+                     "-> Q8_0 on the device")
+
+
 def prompts(seed, workload, n):
     if workload == "frame_b1":
         return [synth.prompt(seed, PROMPT_ROWS)]
@@ -421,6 +451,7 @@ def main():
     log(f"sampled: {sampled['frames_per_s']:.1f} frames/s, {sampled['ms_per_step']:.3f} ms per step")
 
     frame.destroy()
+    load = load_from_bf16(dev, f32, act_q8) if b1 else None
     text_start = None
     if b1 and not args.no_text:
         text_start = start_from_text(dev, ts, cs, tables, args.seed, max_pos,
@@ -473,6 +504,7 @@ def main():
         "long_context_attention": long_attn,
         "start_from_text": text_start,
         "sampled": sampled,
+        "load_from_bf16": load,
     }
     print(json.dumps(out), flush=True)
     return 0

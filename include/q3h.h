@@ -67,7 +67,10 @@ typedef struct {
 } q3h_layer_weights;
 
 typedef struct {
-  int32_t src_dtype;               /* Q3H_F32 or Q3H_Q8_0 (ggml blocks) */
+  int32_t src_dtype;               /* Q3H_F32, Q3H_Q8_0 (ggml blocks) or Q3H_BF16 (the
+                                      safetensors rows as stored: widened and, for a
+                                      Q8_0 stack, quantized on the device, the
+                                      conversion of lm.pas:244-308) */
   const q3h_layer_weights *layers; /* [layers] */
   const float *final_norm;         /* [hidden] */
 } q3h_weights;
@@ -92,8 +95,9 @@ const char *q3h_last_error(void);
    quantizes or repacks) the host weights, so they may be freed on return ---- */
 int q3h_stack_create(q3h_device *dev, const q3h_stack_config *cfg,
                      const q3h_weights *w, q3h_stack **out);
-/* TQwenLmHeads.Add (lm.pas:277-308): a head [rows][hidden] in src_dtype,
-   stored in the stack's dtype; *index receives its number (0, 1, ...) */
+/* TQwenLmHeads.Add (lm.pas:277-308): a head [rows][hidden] in src_dtype
+   (Q3H_F32, Q3H_Q8_0 or Q3H_BF16), stored in the stack's dtype; *index
+   receives its number (0, 1, ...) */
 int q3h_stack_add_head(q3h_stack *s, const void *w, int rows, int src_dtype,
                        int *index);
 /* StackBytes (lm.pas:182-197) of the layers on the device, heads excluded */

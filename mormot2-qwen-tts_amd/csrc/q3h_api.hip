@@ -450,7 +450,8 @@ extern "C" int q3h_device_close(q3h_device *dev) {
 namespace {
 
 size_t src_row_bytes(int src_dtype, int K) {
-  return src_dtype == Q3H_Q8_0 ? (size_t)(K / 32) * 34 : (size_t)K * 4;
+  return src_dtype == Q3H_Q8_0 ? (size_t)(K / 32) * 34
+                               : (size_t)K * (src_dtype == Q3H_BF16 ? 2 : 4);
 }
 
 Mat alloc_mat(int N, int K, int dtype, int64_t &bytes) {
@@ -482,14 +483,15 @@ void upload_rows(Mat &m, int dtype, const void *src, int src_dtype, int rows, in
   require(src != nullptr, Q3H_E_ARG, "a weight matrix is NULL");
   const size_t bytes = src_row_bytes(src_dtype, K) * rows;
   check_hip(hipMemcpyAsync(staging, src, bytes, hipMemcpyHostToDevice, st), "upload");
+  const bool bf16 = src_dtype == Q3H_BF16;
   if (dtype == Q3H_Q8_0) {
-    if (src_dtype == Q3H_F32)
-      launch_quantize_q8((const float *)staging, rows, K, m.q, m.d, stride, off, st);
-    else
+    if (src_dtype == Q3H_Q8_0)
       launch_repack_q8((const uint8_t *)staging, rows, K, m.q, m.d, stride, off, st);
+    else
+      launch_quantize_q8(staging, bf16, rows, K, m.q, m.d, stride, off, st);
   } else {
-    require(src_dtype == Q3H_F32, Q3H_E_ARG, "f32 stacks take f32 weights");
-    launch_copy_rows_f32((const float *)staging, rows, K, m.f, stride, off, st);
+    require(src_dtype != Q3H_Q8_0, Q3H_E_ARG, "f32 stacks take f32 or BF16 weights");
+    launch_copy_rows_f32(staging, bf16, rows, K, m.f, stride, off, st);
   }
   check_hip(hipGetLastError(), "conversion kernel");
   // the staging buffer is reused by the next matrix
@@ -543,10 +545,10 @@ extern "C" int q3h_stack_create(q3h_device *dev, const q3h_stack_config *cfg,
     require(c.head_dim == 128, Q3H_E_ARG, "q3h_stack_create: head_dim must be 128");
     require(c.dtype == Q3H_F32 || c.dtype == Q3H_Q8_0, Q3H_E_ARG,
             "q3h_stack_create: dtype must be Q3H_F32 or Q3H_Q8_0");
-    require(w->src_dtype == Q3H_F32 || w->src_dtype == Q3H_Q8_0, Q3H_E_ARG,
-            "q3h_stack_create: src_dtype must be Q3H_F32 or Q3H_Q8_0");
-    require(c.dtype == Q3H_Q8_0 || w->src_dtype == Q3H_F32, Q3H_E_ARG,
-            "q3h_stack_create: an f32 stack takes f32 weights");
+    require(w->src_dtype == Q3H_F32 || w->src_dtype == Q3H_Q8_0 || w->src_dtype == Q3H_BF16,
+            Q3H_E_ARG, "q3h_stack_create: src_dtype must be Q3H_F32, Q3H_Q8_0 or Q3H_BF16");
+    require(c.dtype == Q3H_Q8_0 || w->src_dtype != Q3H_Q8_0, Q3H_E_ARG,
+            "q3h_stack_create: an f32 stack takes f32 or BF16 weights");
     require(c.max_positions > 0, Q3H_E_ARG, "q3h_stack_create: max_positions <= 0");
     require(c.max_positions <= attn_max_positions(c.kv_f16 != 0), Q3H_E_ARG,
             "q3h_stack_create: max_positions above " +
@@ -650,10 +652,10 @@ extern "C" int q3h_stack_add_head(q3h_stack *s, const void *w, int rows, int src
                                   int *index) {
   return guard([&] {
     require(s && w && index && rows > 0, Q3H_E_ARG, "q3h_stack_add_head: invalid argument");
-    require(src_dtype == Q3H_F32 || src_dtype == Q3H_Q8_0, Q3H_E_ARG,
-            "q3h_stack_add_head: src_dtype must be Q3H_F32 or Q3H_Q8_0");
-    require(s->cfg.dtype == Q3H_Q8_0 || src_dtype == Q3H_F32, Q3H_E_ARG,
-            "q3h_stack_add_head: an f32 stack takes f32 heads");
+    require(src_dtype == Q3H_F32 || src_dtype == Q3H_Q8_0 || src_dtype == Q3H_BF16, Q3H_E_ARG,
+            "q3h_stack_add_head: src_dtype must be Q3H_F32, Q3H_Q8_0 or Q3H_BF16");
+    require(s->cfg.dtype == Q3H_Q8_0 || src_dtype != Q3H_Q8_0, Q3H_E_ARG,
+            "q3h_stack_add_head: an f32 stack takes f32 or BF16 heads");
     require(!s->cfg.act_q8 || rows % 16 == 0, Q3H_E_ARG,
             "q3h_stack_add_head: an act_q8 stack takes heads of a multiple of 16 rows");
     check_hip(hipSetDevice(s->dev->ordinal), "hipSetDevice");

@@ -199,12 +199,13 @@ void launch_attn_o_cp(const Mat &wo, const float *qkv, void *k_layer, int v_off,
 void launch_rmsnorm_rows(const float *x, int ldx, int M, int K, const float *w, float eps,
                          float *y, int ldy, hipStream_t st);
 
-void launch_quantize_q8(const float *src, int rows, int K, int8_t *q, _Float16 *d,
+// weight conversion at load: src rows of K f32 (or BF16 when bf16) values
+void launch_quantize_q8(const void *src, bool bf16, int rows, int K, int8_t *q, _Float16 *d,
                         int row_stride, int row_off, hipStream_t st);
 void launch_repack_q8(const uint8_t *blocks, int rows, int K, int8_t *q, _Float16 *d,
                       int row_stride, int row_off, hipStream_t st);
-void launch_copy_rows_f32(const float *src, int rows, int K, float *dst, int row_stride,
-                          int row_off, hipStream_t st);
+void launch_copy_rows_f32(const void *src, bool bf16, int rows, int K, float *dst,
+                          int row_stride, int row_off, hipStream_t st);
 void launch_kv_fill(const float *src, int layers, int kvh, int len, int hd, void *dst,
                     int max_pos, bool kv16, hipStream_t st);
 void launch_kv_read(const void *src, int layer, int kvh, int len, int hd, int max_pos,

@@ -396,18 +396,28 @@ void launch_rmsnorm_rows(const float *x, int ldx, int M, int K, const float *w, 
 // copies; dst row = src row * row_stride + row_off (fused QKV, interleaved
 // gate/up).
 
-__global__ void k_quantize_q8(const float *src, int rows, int K, int8_t *q, _Float16 *d,
+// a source element widened to f32 (BF16: the high half of an f32, exact)
+template <bool BF16>
+__device__ __forceinline__ float src_elem(const void *src, size_t i) {
+  if constexpr (BF16)
+    return __uint_as_float((uint32_t) static_cast<const uint16_t *>(src)[i] << 16);
+  else
+    return static_cast<const float *>(src)[i];
+}
+
+template <bool BF16>
+__global__ void k_quantize_q8(const void *src, int rows, int K, int8_t *q, _Float16 *d,
                               int row_stride, int row_off) {
   const int nb = K >> 5;
   const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= (size_t)rows * nb) return;
   const int r = (int)(b / nb), i = (int)(b % nb);
-  const float *x = src + (size_t)r * K + i * 32;
+  const size_t x0 = (size_t)r * K + i * 32;
   float v[32];
   float amax = 0.f;
 #pragma unroll
   for (int j = 0; j < 32; j++) {
-    v[j] = x[j];
+    v[j] = src_elem<BF16>(src, x0 + j);
     const float a = fabsf(v[j]);
     amax = amax > a ? amax : a;
   }
@@ -435,19 +445,25 @@ __global__ void k_repack_q8(const uint8_t *blocks, int rows, int K, int8_t *q, _
   for (int j = 0; j < 32; j++) qo[j] = (int8_t)src[2 + j];
 }
 
-__global__ void k_copy_rows_f32(const float *src, int rows, int K, float *dst,
-                                int row_stride, int row_off) {
+template <bool BF16>
+__global__ void k_copy_rows_f32(const void *src, int rows, int K, float *dst, int row_stride,
+                                int row_off) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (size_t)rows * K) return;
   const int r = (int)(i / K), k = (int)(i % K);
-  dst[((size_t)r * row_stride + row_off) * K + k] = src[i];
+  dst[((size_t)r * row_stride + row_off) * K + k] = src_elem<BF16>(src, i);
 }
 
-void launch_quantize_q8(const float *src, int rows, int K, int8_t *q, _Float16 *d,
+void launch_quantize_q8(const void *src, bool bf16, int rows, int K, int8_t *q, _Float16 *d,
                         int row_stride, int row_off, hipStream_t st) {
   const size_t n = (size_t)rows * (K >> 5);
-  hipLaunchKernelGGL(k_quantize_q8, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, src,
-                     rows, K, q, d, row_stride, row_off);
+  const dim3 grid((unsigned)((n + 255) / 256));
+  if (bf16)
+    hipLaunchKernelGGL(k_quantize_q8<true>, grid, dim3(256), 0, st, src, rows, K, q, d,
+                       row_stride, row_off);
+  else
+    hipLaunchKernelGGL(k_quantize_q8<false>, grid, dim3(256), 0, st, src, rows, K, q, d,
+                       row_stride, row_off);
 }
 
 void launch_repack_q8(const uint8_t *blocks, int rows, int K, int8_t *q, _Float16 *d,
@@ -457,11 +473,16 @@ void launch_repack_q8(const uint8_t *blocks, int rows, int K, int8_t *q, _Float1
                      rows, K, q, d, row_stride, row_off);
 }
 
-void launch_copy_rows_f32(const float *src, int rows, int K, float *dst, int row_stride,
-                          int row_off, hipStream_t st) {
+void launch_copy_rows_f32(const void *src, bool bf16, int rows, int K, float *dst,
+                          int row_stride, int row_off, hipStream_t st) {
   const size_t n = (size_t)rows * K;
-  hipLaunchKernelGGL(k_copy_rows_f32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, src,
-                     rows, K, dst, row_stride, row_off);
+  const dim3 grid((unsigned)((n + 255) / 256));
+  if (bf16)
+    hipLaunchKernelGGL(k_copy_rows_f32<true>, grid, dim3(256), 0, st, src, rows, K, dst,
+                       row_stride, row_off);
+  else
+    hipLaunchKernelGGL(k_copy_rows_f32<false>, grid, dim3(256), 0, st, src, rows, K, dst,
+                       row_stride, row_off);
 }
 
 // K/V fill / read (long-context setups, tests): src [layers][kvh][len][hd]
