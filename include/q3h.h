@@ -45,6 +45,7 @@ typedef struct q3h_stack q3h_stack;
 typedef struct q3h_context q3h_context;
 typedef struct q3h_frame q3h_frame;
 typedef struct q3h_text_proj q3h_text_proj;
+typedef struct q3h_codec q3h_codec;
 
 /* TDecoderConfig (mormot.ai.tts.qwen.lm.pas:184-191) + TQwen3Vulkan.KvF16
    (lm.pas:353) + the numerics of the Q8_0 products */
@@ -266,6 +267,54 @@ typedef struct {
 int q3h_frame_start_text(q3h_frame *f, int stream, q3h_text_proj *t, const q3h_start_ids *sp,
                          const int32_t *ids, int n_ids, const int32_t *codec, int n_codec,
                          int non_streaming);
+
+/* ---- the 12 Hz decoder's back part: replaces TQwenCodecVulkan's GPU pass
+   (src/tts/mormot.ai.tts.qwen.codec.vulkan.pas:568-652) ---- */
+
+/* the tensors of the back part (TQwenCodec.Create, codec.pas:644-751), f32,
+   host memory, in their safetensors layouts (decoder.* of the speech
+   tokenizer); the library repacks and copies them */
+typedef struct {
+  const float *a1_alpha, *a1_beta; /* block.{2+r}.act1.alpha / beta [dim] */
+  const float *c1_w, *c1_b;        /* block.{2+r}.conv1.conv [dim][dim][7], [dim] */
+  const float *a2_alpha, *a2_beta; /* block.{2+r}.act2 */
+  const float *c2_w, *c2_b;        /* block.{2+r}.conv2.conv [dim][dim][1], [dim] */
+} q3h_codec_res;
+
+typedef struct {
+  const float *act_alpha, *act_beta; /* decoder.{i+1}.block.0 [in] */
+  const float *up_w, *up_b;          /* block.1.conv [in][out][2 rate], [out] */
+  q3h_codec_res res[3];              /* dilations 1, 3, 9 */
+} q3h_codec_block;
+
+typedef struct {
+  const float *up_w[2], *up_b[2];     /* upsample.i.0.conv [1024][1024][2], [1024] */
+  const float *dw_w[2], *dw_b[2];     /* upsample.i.1.dwconv.conv [1024][1][7], [1024] */
+  const float *norm_w[2], *norm_b[2]; /* upsample.i.1.norm [1024] */
+  const float *pw1_w[2], *pw1_b[2];   /* upsample.i.1.pwconv1 [4096][1024], [4096] */
+  const float *pw2_w[2], *pw2_b[2];   /* upsample.i.1.pwconv2 [1024][4096], [1024] */
+  const float *gamma[2];              /* upsample.i.1.gamma [1024] */
+  const float *conv0_w, *conv0_b;     /* decoder.0.conv [1536][1024][7], [1536] */
+  q3h_codec_block block[4];           /* decoder.1 .. 4 (rates 8, 5, 4, 3) */
+  const float *out_alpha, *out_beta;  /* decoder.5 [96] */
+  const float *out_w, *out_b;         /* decoder.6.conv [1][96][7], [1] */
+} q3h_codec_weights;
+
+/* TQwenCodecVulkan.CreateVulkan's upload (codec.vulkan.pas:166-237):
+   max_frames frames per device pass (1..64; longer inputs run in passes, as
+   CHUNK_FRAMES does) */
+int q3h_codec_create(q3h_device *dev, const q3h_codec_weights *w, int max_frames,
+                     q3h_codec **out);
+/* TQwenCodecVulkan.Reset (codec.vulkan.pas:455-488): every history to zeros */
+int q3h_codec_reset(q3h_codec *c);
+/* TQwenCodecVulkan.Back (codec.vulkan.pas:633-652): x [frames][1024] (the
+   transformer output) -> pcm [frames * 1920] in [-1, 1]. Causal: each
+   convolution keeps the last rows of its input for the next call, and every
+   output sums its terms in one order whatever the frames per call, so
+   decoding 1 + 3 frames or 4 at once gives the same samples. */
+int q3h_codec_back(q3h_codec *c, const float *x, int frames, float *pcm);
+int64_t q3h_codec_bytes(const q3h_codec *c);
+int q3h_codec_destroy(q3h_codec *c);
 
 /* ---- helpers ---- */
 

@@ -97,6 +97,25 @@ class Sampling(ctypes.Structure):
     ]
 
 
+class CodecRes(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in
+                ("a1_alpha", "a1_beta", "c1_w", "c1_b", "a2_alpha", "a2_beta", "c2_w", "c2_b")]
+
+
+class CodecBlock(ctypes.Structure):
+    _fields_ = [("act_alpha", ctypes.c_void_p), ("act_beta", ctypes.c_void_p),
+                ("up_w", ctypes.c_void_p), ("up_b", ctypes.c_void_p), ("res", CodecRes * 3)]
+
+
+class CodecWeights(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p * 2) for n in
+                ("up_w", "up_b", "dw_w", "dw_b", "norm_w", "norm_b", "pw1_w", "pw1_b", "pw2_w",
+                 "pw2_b", "gamma")] + [
+        ("conv0_w", ctypes.c_void_p), ("conv0_b", ctypes.c_void_p), ("block", CodecBlock * 4),
+        ("out_alpha", ctypes.c_void_p), ("out_beta", ctypes.c_void_p),
+        ("out_w", ctypes.c_void_p), ("out_b", ctypes.c_void_p)]
+
+
 class StartIds(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in
                 ("tts_bos", "tts_eos", "tts_pad", "codec_pad", "codec_bos")]
@@ -140,6 +159,11 @@ SIGNATURES = {
     "q3h_text_project": (_I, [_P, _IP, _I, _FP]),
     "q3h_text_destroy": (_I, [_P]),
     "q3h_frame_set_sampling": (_I, [_P, ctypes.POINTER(Sampling)]),
+    "q3h_codec_create": (_I, [_P, ctypes.POINTER(CodecWeights), _I, ctypes.POINTER(_P)]),
+    "q3h_codec_reset": (_I, [_P]),
+    "q3h_codec_back": (_I, [_P, _FP, _I, _FP]),
+    "q3h_codec_bytes": (ctypes.c_int64, [_P]),
+    "q3h_codec_destroy": (_I, [_P]),
     "q3h_frame_start_text": (_I, [_P, _I, _P, ctypes.POINTER(StartIds), _IP, _I, _IP, _I, _I]),
     "q3h_quantize_row_q8_0": (_I, [_FP, _P, ctypes.c_int64]),
     "q3h_stack_time_gemv": (_I, [_P, _I, _I, _I, _FP, ctypes.POINTER(_I),
@@ -404,6 +428,62 @@ class TextProj:
     def destroy(self):
         if self.h:
             _check(lib().q3h_text_destroy(self.h))
+            self.h = None
+
+
+class Codec:
+    """The back part of the 12 Hz decoder on the device (TQwenCodecVulkan:
+    Back / Reset, codec.vulkan.pas:455-488, 633-652). w: dict of the
+    decoder.* tensors (f32, safetensors layouts; see synth.codec_weights)."""
+
+    def __init__(self, dev, w, max_frames=16):
+        keep = []
+
+        def ptr(a):
+            if a is None:
+                return None  # NULL: the library reports the missing tensor
+            a = np.ascontiguousarray(a, dtype=np.float32)
+            keep.append(a)
+            return a.ctypes.data
+
+        s = CodecWeights()
+        for name in ("up_w", "up_b", "dw_w", "dw_b", "norm_w", "norm_b", "pw1_w", "pw1_b",
+                     "pw2_w", "pw2_b", "gamma"):
+            arr = getattr(s, name)
+            for i in range(2):
+                arr[i] = ptr(w[name][i])
+        s.conv0_w, s.conv0_b = ptr(w["conv0_w"]), ptr(w["conv0_b"])
+        for i, b in enumerate(w["block"]):
+            blk = s.block[i]
+            blk.act_alpha, blk.act_beta = ptr(b["act_alpha"]), ptr(b["act_beta"])
+            blk.up_w, blk.up_b = ptr(b["up_w"]), ptr(b["up_b"])
+            for r, rw in enumerate(b["res"]):
+                for k, v in rw.items():
+                    setattr(blk.res[r], k, ptr(v))
+        s.out_alpha, s.out_beta = ptr(w["out_alpha"]), ptr(w["out_beta"])
+        s.out_w, s.out_b = ptr(w["out_w"]), ptr(w["out_b"])
+        h = _P()
+        _check(lib().q3h_codec_create(dev.h, ctypes.byref(s), max_frames, ctypes.byref(h)))
+        self.h = h
+
+    def back(self, x):
+        """x [frames][1024] -> pcm [frames * 1920]."""
+        x = _f32(x)
+        frames = x.shape[0]
+        pcm = np.empty(frames * 1920, dtype=np.float32)
+        _check(lib().q3h_codec_back(self.h, _fp(x), frames, _fp(pcm)))
+        return pcm
+
+    def reset(self):
+        _check(lib().q3h_codec_reset(self.h))
+
+    @property
+    def bytes(self):
+        return lib().q3h_codec_bytes(self.h)
+
+    def destroy(self):
+        if self.h:
+            _check(lib().q3h_codec_destroy(self.h))
             self.h = None
 
 

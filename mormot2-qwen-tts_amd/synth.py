@@ -138,3 +138,60 @@ def lcg_rows(count, seed=12345):
         s = (s * 1664525 + 1013904223) & 0xFFFFFFFF
         out[i] = np.float32((np.float64(s >> 8) / (1 << 24) - 0.5) * 0.2)
     return out, s
+
+
+CODEC_LATENT = 1024
+CODEC_DIM = 1536
+CODEC_RATES = (8, 5, 4, 3)
+FRAME_SAMPLES = 1920
+
+
+def codec_weights(seed):
+    """The back part of the 12 Hz decoder (decoder.* tensors of the speech
+    tokenizer) in their safetensors layouts, f32, scaled so that activations
+    stay of order one through the blocks (convolutions N(0, 1 / fan_in) times
+    a factor, SnakeBeta log-parameters N(0, 0.1), ConvNeXt gamma 0.1)."""
+    L, D = CODEC_LATENT, CODEC_DIM
+
+    def n(name, shape, std):
+        return normal(seed, "codec." + name, shape, std)
+
+    w = dict(up_w=[], up_b=[], dw_w=[], dw_b=[], norm_w=[], norm_b=[], pw1_w=[], pw1_b=[],
+             pw2_w=[], pw2_b=[], gamma=[])
+    for i in range(2):
+        p = f"upsample.{i}."
+        w["up_w"].append(n(p + "0.conv.weight", (L, L, 2), 1.0 / np.sqrt(L)))
+        w["up_b"].append(n(p + "0.conv.bias", (L,), 0.01))
+        w["dw_w"].append(n(p + "1.dwconv.conv.weight", (L, 1, 7), 0.5 / np.sqrt(7)))
+        w["dw_b"].append(n(p + "1.dwconv.conv.bias", (L,), 0.01))
+        w["norm_w"].append((1.0 + n(p + "1.norm.weight", (L,), 0.1)).astype(np.float32))
+        w["norm_b"].append(n(p + "1.norm.bias", (L,), 0.1))
+        w["pw1_w"].append(n(p + "1.pwconv1.weight", (4 * L, L), 1.0 / np.sqrt(L)))
+        w["pw1_b"].append(n(p + "1.pwconv1.bias", (4 * L,), 0.01))
+        w["pw2_w"].append(n(p + "1.pwconv2.weight", (L, 4 * L), 1.0 / np.sqrt(4 * L)))
+        w["pw2_b"].append(n(p + "1.pwconv2.bias", (L,), 0.01))
+        w["gamma"].append((0.1 + n(p + "1.gamma", (L,), 0.02)).astype(np.float32))
+    w["conv0_w"] = n("decoder.0.conv.weight", (D, L, 7), 1.0 / np.sqrt(7 * L))
+    w["conv0_b"] = n("decoder.0.conv.bias", (D,), 0.01)
+    w["block"] = []
+    for i, rate in enumerate(CODEC_RATES):
+        cin, cout = D >> i, D >> (i + 1)
+        p = f"decoder.{i + 1}.block."
+        b = dict(act_alpha=n(p + "0.alpha", (cin,), 0.1), act_beta=n(p + "0.beta", (cin,), 0.1),
+                 up_w=n(p + "1.conv.weight", (cin, cout, 2 * rate), 1.0 / np.sqrt(2 * cin)),
+                 up_b=n(p + "1.conv.bias", (cout,), 0.01), res=[])
+        for r in range(3):
+            q = f"{p}{r + 2}."
+            b["res"].append(dict(
+                a1_alpha=n(q + "act1.alpha", (cout,), 0.1), a1_beta=n(q + "act1.beta", (cout,), 0.1),
+                c1_w=n(q + "conv1.conv.weight", (cout, cout, 7), 0.5 / np.sqrt(7 * cout)),
+                c1_b=n(q + "conv1.conv.bias", (cout,), 0.01),
+                a2_alpha=n(q + "act2.alpha", (cout,), 0.1), a2_beta=n(q + "act2.beta", (cout,), 0.1),
+                c2_w=n(q + "conv2.conv.weight", (cout, cout, 1), 0.5 / np.sqrt(cout)),
+                c2_b=n(q + "conv2.conv.bias", (cout,), 0.01)))
+        w["block"].append(b)
+    w["out_alpha"] = n("decoder.5.alpha", (D >> 4,), 0.1)
+    w["out_beta"] = n("decoder.5.beta", (D >> 4,), 0.1)
+    w["out_w"] = n("decoder.6.conv.weight", (1, D >> 4, 7), 0.05 / np.sqrt(7 * (D >> 4)))
+    w["out_b"] = n("decoder.6.conv.bias", (1,), 0.01)
+    return w

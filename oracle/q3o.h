@@ -187,6 +187,47 @@ q3o_ctx *q3o_frame_talker_ctx(q3o_frame *f);
    code g: seed ^ 0x5DEECE66D, group g; frame = frames emitted before) */
 void q3o_frame_set_sampling(q3o_frame *f, const q3o_sampling *s);
 
+/* ---- the 12 Hz decoder's back part (q3o_codec.c) ---- */
+
+/* the tensors of TQwenCodec's back part (codec.pas:644-751), f32, in the
+   safetensors layouts (decoder.* of the speech tokenizer) */
+typedef struct {
+  const float *a1_alpha, *a1_beta; /* block.{2+r}.act1 [dim] */
+  const float *c1_w, *c1_b;        /* block.{2+r}.conv1.conv [dim][dim][7], [dim] */
+  const float *a2_alpha, *a2_beta; /* act2 */
+  const float *c2_w, *c2_b;        /* conv2.conv [dim][dim][1], [dim] */
+} q3o_codec_res;
+
+typedef struct {
+  const float *act_alpha, *act_beta; /* decoder.{i+1}.block.0 [in] */
+  const float *up_w, *up_b;          /* block.1.conv [in][out][2 rate], [out] */
+  q3o_codec_res res[3];              /* dilations 1, 3, 9 */
+} q3o_codec_block;
+
+typedef struct {
+  const float *up_w[2], *up_b[2];     /* upsample.i.0.conv [1024][1024][2], [1024] */
+  const float *dw_w[2], *dw_b[2];     /* upsample.i.1.dwconv.conv [1024][1][7], [1024] */
+  const float *norm_w[2], *norm_b[2]; /* upsample.i.1.norm [1024] */
+  const float *pw1_w[2], *pw1_b[2];   /* upsample.i.1.pwconv1 [4096][1024], [4096] */
+  const float *pw2_w[2], *pw2_b[2];   /* upsample.i.1.pwconv2 [1024][4096], [1024] */
+  const float *gamma[2];              /* upsample.i.1.gamma [1024] */
+  const float *conv0_w, *conv0_b;     /* decoder.0.conv [1536][1024][7], [1536] */
+  q3o_codec_block block[4];           /* decoder.1 .. 4: 1536 -> 768 -> 384 -> 192 -> 96 */
+  const float *out_alpha, *out_beta;  /* decoder.5 [96] */
+  const float *out_w, *out_b;         /* decoder.6.conv [1][96][7], [1] */
+} q3o_codec_weights;
+
+typedef struct q3o_codec q3o_codec;
+
+/* TQwenCodec's back part (codec.pas:1040-1083); the weights are referenced,
+   not copied */
+q3o_codec *q3o_codec_create(const q3o_codec_weights *w);
+/* TQwenCodec.Reset: the histories back to zeros */
+void q3o_codec_reset(q3o_codec *c);
+/* x [frames][1024] (the transformer output) -> pcm [frames * 1920] */
+void q3o_codec_back(q3o_codec *c, const float *x, int frames, float *pcm);
+void q3o_codec_destroy(q3o_codec *c);
+
 #ifdef __cplusplus
 }
 #endif

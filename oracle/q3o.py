@@ -55,6 +55,78 @@ class Sampling(ctypes.Structure):
     ]
 
 
+class CodecRes(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in
+                ("a1_alpha", "a1_beta", "c1_w", "c1_b", "a2_alpha", "a2_beta", "c2_w", "c2_b")]
+
+
+class CodecBlock(ctypes.Structure):
+    _fields_ = [("act_alpha", ctypes.c_void_p), ("act_beta", ctypes.c_void_p),
+                ("up_w", ctypes.c_void_p), ("up_b", ctypes.c_void_p), ("res", CodecRes * 3)]
+
+
+class CodecWeights(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p * 2) for n in
+                ("up_w", "up_b", "dw_w", "dw_b", "norm_w", "norm_b", "pw1_w", "pw1_b", "pw2_w",
+                 "pw2_b", "gamma")] + [
+        ("conv0_w", ctypes.c_void_p), ("conv0_b", ctypes.c_void_p), ("block", CodecBlock * 4),
+        ("out_alpha", ctypes.c_void_p), ("out_beta", ctypes.c_void_p),
+        ("out_w", ctypes.c_void_p), ("out_b", ctypes.c_void_p)]
+
+
+def codec_struct(w, cls_w=None, cls_b=None, cls_r=None):
+    """(struct, keep-alive list) of the codec weight dict w (synth.codec_weights
+    layout) in the q3o_codec_weights / q3h_codec_weights layout."""
+    cls_w = cls_w or CodecWeights
+    keep = []
+
+    def ptr(a):
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        keep.append(a)
+        return a.ctypes.data
+
+    s = cls_w()
+    for name in ("up_w", "up_b", "dw_w", "dw_b", "norm_w", "norm_b", "pw1_w", "pw1_b", "pw2_w",
+                 "pw2_b", "gamma"):
+        arr = getattr(s, name)
+        for i in range(2):
+            arr[i] = ptr(w[name][i])
+    s.conv0_w, s.conv0_b = ptr(w["conv0_w"]), ptr(w["conv0_b"])
+    for i, b in enumerate(w["block"]):
+        blk = s.block[i]
+        blk.act_alpha, blk.act_beta = ptr(b["act_alpha"]), ptr(b["act_beta"])
+        blk.up_w, blk.up_b = ptr(b["up_w"]), ptr(b["up_b"])
+        for r, rw in enumerate(b["res"]):
+            for k, v in rw.items():
+                setattr(blk.res[r], k, ptr(v))
+    s.out_alpha, s.out_beta = ptr(w["out_alpha"]), ptr(w["out_beta"])
+    s.out_w, s.out_b = ptr(w["out_w"]), ptr(w["out_b"])
+    return s, keep
+
+
+class Codec:
+    """TQwenCodec's back part (codec.pas:1040-1083) on the CPU."""
+
+    def __init__(self, w):
+        self._s, self._keep = codec_struct(w)
+        self.h = lib().q3o_codec_create(ctypes.byref(self._s))
+
+    def reset(self):
+        lib().q3o_codec_reset(self.h)
+
+    def back(self, x):
+        x = _f32(x)
+        frames = x.shape[0]
+        pcm = np.empty(frames * 1920, dtype=np.float32)
+        lib().q3o_codec_back(self.h, _fp(x), frames, _fp(pcm))
+        return pcm
+
+    def destroy(self):
+        if self.h:
+            lib().q3o_codec_destroy(self.h)
+            self.h = None
+
+
 _lib = None
 
 
@@ -102,6 +174,10 @@ def lib():
             "q3o_sample": (ctypes.c_int, [_FP, ctypes.c_int, ctypes.c_float, ctypes.c_int,
                                           ctypes.c_float, ctypes.c_float]),
             "q3o_frame_set_sampling": (None, [_P, ctypes.POINTER(Sampling)]),
+            "q3o_codec_create": (_P, [ctypes.POINTER(CodecWeights)]),
+            "q3o_codec_reset": (None, [_P]),
+            "q3o_codec_back": (None, [_P, _FP, ctypes.c_int, _FP]),
+            "q3o_codec_destroy": (None, [_P]),
             "q3o_text_project": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                                 ctypes.c_int, _FP, _FP, _FP, _FP, _IP,
                                                 ctypes.c_int, _FP]),
