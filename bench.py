@@ -29,6 +29,8 @@ Beside it:
   long_context_attention (frame_b1)  the talker with an f16 K/V cache
                 prefilled to 2048 / 4096 / 8192 positions: 32 decode steps
                 each, and the decode attention kernels' GB/s;
+  codec_back (frame_b1)  the 12 Hz decoder's back part (2.46 GMAC per frame)
+                over 156 frames: passes of 16 frames and one frame per call;
   start_from_text (frame_b1)  time to the first frame from token ids: the
                 text projection, the prefill rows built on the device, the
                 talker prefill and one frame step (a 40-token sentence).
@@ -51,6 +53,7 @@ import q3h  # noqa: E402
 import synth  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+F32_MFMA_PEAK_TFLOPS = 157.3
 F32_PROMPT_ROWS = 512
 # HBM bytes per launch of the single-row Q8_0 products of one talker decode
 # step, from rocprofv3 FETCH_SIZE + WRITE_SIZE passes scaled by a plain copy
@@ -259,6 +262,68 @@ def long_context_attention(dev, f32, tables, seed, steps=32, iters=10):
                 kv="f16", steps_per_length=steps, results=out)
 
 
+def codec_macs_per_frame():
+    """Multiply-adds of the decoder's back part per frame (every convolution:
+    rows per frame x taps x in x out; transposed convolutions as the causal
+    convolutions the library runs)."""
+    L, D = synth.CODEC_LATENT, synth.CODEC_DIM
+    m = 1 * L * 2 * L + 2 * L * 2 * L  # two transposed convolutions 2 / 2
+    m += (2 + 4) * (2 * L * 4 * L + 7 * L)  # ConvNeXt pointwise pair + depthwise
+    m += 4 * 7 * L * D  # input convolution
+    rows = 4
+    for i, rate in enumerate(synth.CODEC_RATES):
+        cin, cout = D >> i, D >> (i + 1)
+        m += rows * 2 * cin * rate * cout  # transposed convolution, 2 taps
+        rows *= rate
+        m += 3 * rows * (7 * cout * cout + cout * cout)  # residual units
+    return m + rows * 7 * (D >> 4)
+
+
+def codec_back(dev, seed, frames=156, cpu=True):
+    """The 12 Hz decoder's back part (TQwenCodecVulkan.Back): `frames` frames of
+    N(0,1) transformer rows decoded in passes of 16 frames (the reference's
+    CHUNK_FRAMES) and one frame per call (streaming), host rows in and PCM out;
+    frames/s, real-time factor at 12.5 frames per second, and the matrix-core
+    rate (2 x multiply-adds / time against the f32 peak)."""
+    w = synth.codec_weights(seed)
+    c = q3h.Codec(dev, w, max_frames=16)
+    x = synth.prompt(seed + 90, frames)
+    macs = codec_macs_per_frame()
+    out = dict(frames=frames, macs_per_frame=int(macs))
+    for name, step in (("passes_of_16", 16), ("one_frame_per_call", 1)):
+        c.reset()
+        c.back(x[:step])  # warm-up
+        c.reset()
+        t0 = time.perf_counter()
+        for f in range(0, frames, step):
+            c.back(x[f:f + step])
+        dt = time.perf_counter() - t0
+        fps = frames / dt
+        tf = 2 * macs * fps / 1e12
+        out[name] = dict(frames_per_s=round(fps, 1), ms_per_frame=round(1e3 / fps, 3),
+                         real_time_factor=round(fps / 12.5, 1), tflops=round(tf, 2),
+                         mfma_frac=round(tf / F32_MFMA_PEAK_TFLOPS, 4))
+        log(f"codec back ({name}): {fps:.1f} frames/s, {1e3 / fps:.3f} ms per frame, "
+            f"{tf:.1f} TFLOP/s")
+    c.destroy()
+    if cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import q3o  # the checker's restatement, timed as the CPU baseline
+        threads = min(16, len(os.sched_getaffinity(0)))
+        q3o.set_threads(threads)
+        oc = q3o.Codec(w)
+        n = 2
+        t0 = time.perf_counter()
+        oc.back(x[:n])
+        dt = time.perf_counter() - t0
+        oc.destroy()
+        out["cpu_baseline"] = dict(value=round(n / dt, 3), unit="frames/s", cores=threads,
+                                   kind="port", sample=f"{n} frames, oracle back part "
+                                   "(C + OpenMP, double sums)")
+        log(f"codec back on the CPU (oracle): {n / dt:.2f} frames/s")
+    return out
+
+
 TEXT_VOCAB_BENCH = 16384  # rows of the synthetic text table (one row gathered per token)
 TEXT_TOKENS = 40
 
@@ -377,6 +442,10 @@ def main():
                     help="skip the long-context attention measurement (frame_b1)")
     ap.add_argument("--no-text", action="store_true",
                     help="skip the time-to-first-frame measurement from token ids (frame_b1)")
+    ap.add_argument("--no-codec", action="store_true",
+                    help="skip the decoder back-part measurement (frame_b1)")
+    ap.add_argument("--codec-only", action="store_true",
+                    help="only the decoder back-part measurement (profiling runs)")
     ap.add_argument("--no-roofline", action="store_true",
                     help="skip the matrix-vector roofline measurement (its kernel-attached "
                          "events are not for runs under a kernel tracer)")
@@ -394,6 +463,13 @@ def main():
         return 2
     if args.copy_only:
         return copy_calibration()
+    if args.codec_only:
+        if not q3h.available():
+            raise RuntimeError("no gfx950 device")
+        dev = q3h.Device(0)
+        print(json.dumps({"codec_back": codec_back(dev, args.seed, cpu=False)}), flush=True)
+        dev.close()
+        return 0
     if args.long_attn_only:
         if not q3h.available():
             raise RuntimeError("no gfx950 device")
@@ -456,6 +532,9 @@ def main():
     if b1 and not args.no_text:
         text_start = start_from_text(dev, ts, cs, tables, args.seed, max_pos,
                                      use_graph=not args.no_graph)
+    codec = None
+    if b1 and not args.no_codec:
+        codec = codec_back(dev, args.seed, cpu=not args.no_cpu)
     long_attn = None
     if b1 and not args.no_long_attn:
         long_attn = long_context_attention(dev, f32, tables, args.seed)
@@ -505,6 +584,7 @@ def main():
         "start_from_text": text_start,
         "sampled": sampled,
         "load_from_bf16": load,
+        "codec_back": codec,
     }
     print(json.dumps(out), flush=True)
     return 0

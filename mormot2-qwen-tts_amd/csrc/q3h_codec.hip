@@ -55,8 +55,31 @@ struct ConvArgs {
   const float *g;  // layer scale [n] (CE_SCALED_RES)
   float *z;        // SnakeBeta of the output [T][n] or null
   const float *sa, *sib;  // e^alpha, 1 / (e^beta + 1e-9), indexed by column % sc
+  float *part;            // K-slice sums [gridDim.z][T][n] when the K walk is split
   int cin, taps, dil, T, n, sc;
 };
+
+// chunks of 32 K columns per K slice: a product whose K walk is longer runs
+// as ceil(chunks / kSliceChunks) slices, summed in slice order by
+// k_conv_reduce (a fixed split per layer: the sums do not depend on T)
+constexpr int kSliceChunks = 16;
+
+// the epilogue of one output: bias, GELU / residual / layer scale, then the
+// stores (y, and SnakeBeta of the value to z)
+template <int EPI>
+__device__ __forceinline__ void conv_out(const ConvArgs &a, int m, int n, float acc) {
+  const size_t o = (size_t)m * a.n + n;
+  float v = acc + a.b[n];
+  if (EPI == CE_GELU) v = 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+  if (EPI == CE_RES) v = a.r[o] + v;
+  if (EPI == CE_SCALED_RES) v = a.r[o] + a.g[n] * v;
+  if (a.y) a.y[o] = v;
+  if (a.z) {
+    const int sc = n % a.sc;
+    const float s = sinf(v * a.sa[sc]);
+    a.z[o] = v + a.sib[sc] * (s * s);
+  }
+}
 
 // one workgroup: output rows m0 .. m0 + 63, columns n0 .. n0 + 16 WN - 1
 template <int WN, int EPI>
@@ -67,7 +90,8 @@ __global__ __launch_bounds__(64 * WN) void k_conv_gemm(ConvArgs a) {
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * 16 * WN + 16 * wave, m0 = blockIdx.y * 64;
-  const int K = a.taps * a.cin, cpk = a.cin / 32, nch = a.taps * cpk;
+  const int K = a.taps * a.cin, cpk = a.cin / 32;
+  const int q0 = blockIdx.z * kSliceChunks, q1 = min(a.taps * cpk, q0 + kSliceChunks);
   const float *wr = a.w + (size_t)min(n0 + r, a.n - 1) * K + 4 * g;
   int xrow[XF4], xcol[XF4], xo[XF4];
 #pragma unroll
@@ -89,15 +113,15 @@ __global__ __launch_bounds__(64 * WN) void k_conv_gemm(ConvArgs a) {
   v4f acc[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
-  load(0);
+  load(q0);
 #pragma unroll
   for (int i = 0; i < XF4; i++) *reinterpret_cast<float4 *>(&xs[0][xo[i]]) = xn[i];
   wc[0] = wn[0];
   wc[1] = wn[1];
   __syncthreads();
-  for (int q = 0; q < nch; q++) {
-    const int b = q & 1;
-    if (q + 1 < nch) load(q + 1);
+  for (int q = q0; q < q1; q++) {
+    const int b = (q - q0) & 1;
+    if (q + 1 < q1) load(q + 1);
 #pragma unroll
     for (int s = 0; s < 2; s++) {
 #pragma unroll
@@ -109,7 +133,7 @@ __global__ __launch_bounds__(64 * WN) void k_conv_gemm(ConvArgs a) {
         acc[tm] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.w, wc[s].w, acc[tm], 0, 0, 0);
       }
     }
-    if (q + 1 < nch) {
+    if (q + 1 < q1) {
 #pragma unroll
       for (int i = 0; i < XF4; i++) *reinterpret_cast<float4 *>(&xs[b ^ 1][xo[i]]) = xn[i];
       wc[0] = wn[0];
@@ -120,27 +144,28 @@ __global__ __launch_bounds__(64 * WN) void k_conv_gemm(ConvArgs a) {
   // lane l holds (m = m0 + 16 tm + 4 g + q, n = n0 + r)
   const int n = n0 + r;
   if (n >= a.n) return;
-  const float bias = a.b[n];
-  const float gm = EPI == CE_SCALED_RES ? a.g[n] : 0.f;
-  const int sc = a.z ? n % a.sc : 0;
-  const float sa = a.z ? a.sa[sc] : 0.f, sib = a.z ? a.sib[sc] : 0.f;
 #pragma unroll
   for (int tm = 0; tm < 4; tm++)
 #pragma unroll
     for (int q = 0; q < 4; q++) {
       const int m = m0 + 16 * tm + 4 * g + q;
       if (m >= a.T) continue;
-      const size_t o = (size_t)m * a.n + n;
-      float v = acc[tm][q] + bias;
-      if (EPI == CE_GELU) v = 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
-      if (EPI == CE_RES) v = a.r[o] + v;
-      if (EPI == CE_SCALED_RES) v = a.r[o] + gm * v;
-      if (a.y) a.y[o] = v;
-      if (a.z) {
-        const float s = sinf(v * sa);
-        a.z[o] = v + sib * (s * s);
-      }
+      if (gridDim.z > 1)
+        a.part[((size_t)blockIdx.z * a.T + m) * a.n + n] = acc[tm][q];
+      else
+        conv_out<EPI>(a, m, n, acc[tm][q]);
     }
+}
+
+// the slices of a split product added in slice order, then the epilogue
+template <int EPI>
+__global__ __launch_bounds__(256) void k_conv_reduce(ConvArgs a, int S) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)a.T * a.n) return;
+  const size_t plane = (size_t)a.T * a.n;
+  float v = a.part[i];
+  for (int s = 1; s < S; s++) v += a.part[s * plane + i];
+  conv_out<EPI>(a, (int)(i / a.n), (int)(i % a.n), v);
 }
 
 // ConvNeXt's causal depthwise convolution (kernel 7) and LayerNorm (eps 1e-6)
@@ -210,16 +235,30 @@ struct HistEntry {
 // One workgroup per sequence: rows T .. T + past - 1 move to 0 .. past - 1,
 // in blocks of min(T, past) rows from the top (a block never reads what an
 // earlier block wrote, nor what it writes itself).
+// (the loads of a block are all issued before its stores: up to 32 values
+// per thread, 8192 per block, more than any history holds)
 __global__ __launch_bounds__(256) void k_save_hist(const HistEntry *__restrict__ e, int frames) {
   const HistEntry h = e[blockIdx.x];
   const int T = frames * h.mult;
   const int B = min(T, h.past);
   for (int d0 = 0; d0 < h.past; d0 += B) {
     const int rows = min(B, h.past - d0);
-    const size_t n = (size_t)rows * h.cols;
+    const int n = rows * h.cols;
     float *dst = h.buf + (size_t)d0 * h.cols;
     const float *src = h.buf + (size_t)(d0 + T) * h.cols;
-    for (size_t i = threadIdx.x; i < n; i += 256) dst[i] = src[i];
+    for (int base = 0; base < n; base += 32 * 256) {
+      float v[32];
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
+        const int i = base + j * 256 + threadIdx.x;
+        v[j] = i < n ? src[i] : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
+        const int i = base + j * 256 + threadIdx.x;
+        if (i < n) dst[i] = v[j];
+      }
+    }
     __syncthreads();
   }
 }
@@ -277,6 +316,7 @@ struct q3h_codec {
   float *x_in = nullptr, *s_nx[2] = {nullptr, nullptr}, *x_mid = nullptr, *hn = nullptr,
         *gbuf = nullptr, *s_c0 = nullptr, *s_up[4] = {}, *xres[4] = {}, *s_r1[4][3] = {},
         *s_c2 = nullptr, *s_out = nullptr, *pcm = nullptr;
+  float *part = nullptr;  // K-slice sums of the split products
   HistEntry *hist = nullptr;
   std::vector<HistEntry> hist_host;
   std::mutex mu;
@@ -377,6 +417,12 @@ float *copy_vec(q3h_codec *c, const float *p, int n, const char *what) {
   return upload_f(c, std::vector<float>(p, p + n));
 }
 
+// the K slices of a layer's product (fixed per layer)
+int slices(const DConv &d) {
+  const int nch = d.taps * d.cin / 32;
+  return (nch + kSliceChunks - 1) / kSliceChunks;
+}
+
 // y / z of a product over T output rows of sequence x
 void conv(q3h_codec *c, const DConv &d, const float *x, int T, float *y, int epi,
           const float *r = nullptr, const float *g = nullptr, float *z = nullptr,
@@ -397,8 +443,10 @@ void conv(q3h_codec *c, const DConv &d, const float *x, int T, float *y, int epi
   a.T = T;
   a.n = d.n;
   a.sc = sc;
+  a.part = c->part;
+  const int S = slices(d);
   const int wn = d.n % 64 == 0 ? 4 : 2;
-  const dim3 grid(d.n / (16 * wn), (T + 63) / 64);
+  const dim3 grid(d.n / (16 * wn), (T + 63) / 64, S);
 #define Q3H_C(WN, E) hipLaunchKernelGGL((k_conv_gemm<WN, E>), grid, dim3(64 * WN), 0, c->stream, a)
 #define Q3H_E(WN)                          \
   do {                                     \
@@ -417,6 +465,17 @@ void conv(q3h_codec *c, const DConv &d, const float *x, int T, float *y, int epi
     Q3H_E(2);
 #undef Q3H_E
 #undef Q3H_C
+  if (S > 1) {
+    const dim3 rg((unsigned)(((size_t)T * d.n + 255) / 256));
+    if (epi == CE_BIAS)
+      hipLaunchKernelGGL(k_conv_reduce<CE_BIAS>, rg, dim3(256), 0, c->stream, a, S);
+    else if (epi == CE_GELU)
+      hipLaunchKernelGGL(k_conv_reduce<CE_GELU>, rg, dim3(256), 0, c->stream, a, S);
+    else if (epi == CE_RES)
+      hipLaunchKernelGGL(k_conv_reduce<CE_RES>, rg, dim3(256), 0, c->stream, a, S);
+    else
+      hipLaunchKernelGGL(k_conv_reduce<CE_SCALED_RES>, rg, dim3(256), 0, c->stream, a, S);
+  }
 }
 
 // one pass of F <= max_frames frames: x already in c->x_in, pcm to c->pcm
@@ -567,6 +626,28 @@ extern "C" int q3h_codec_create(q3h_device *dev, const q3h_codec_weights *w, int
     c->s_out = calloc_dev<float>(c, (6 + rin * F) * 96);
     h.push_back({c->s_out, 6, 96, (int)rin});
     c->pcm = calloc_dev<float>(c, rin * F);
+    // the split products' slices: the largest S x T x n of any layer
+    size_t pmax = 0;
+    auto need_part = [&](const DConv &d, size_t T) {
+      const int S = slices(d);
+      if (S > 1) pmax = std::max(pmax, (size_t)S * T * d.n);
+    };
+    for (int i = 0; i < 2; i++) {
+      need_part(c->up[i], (i + 1) * F);
+      need_part(c->next[i].pw1, 2 * (i + 1) * F);
+      need_part(c->next[i].pw2, 2 * (i + 1) * F);
+    }
+    need_part(c->conv0, 4 * F);
+    size_t rr = 4;
+    for (int b = 0; b < 4; b++) {
+      need_part(c->blocks[b].up, rr * F);
+      rr *= c->blocks[b].rate;
+      for (int u = 0; u < 3; u++) {
+        need_part(c->blocks[b].res[u].c1, rr * F);
+        need_part(c->blocks[b].res[u].c2, rr * F);
+      }
+    }
+    c->part = calloc_dev<float>(c, pmax);
     c->hist = calloc_dev<HistEntry>(c, h.size());
     check_hip(hipMemcpy(c->hist, h.data(), sizeof(HistEntry) * h.size(), hipMemcpyHostToDevice),
               "codec init");
