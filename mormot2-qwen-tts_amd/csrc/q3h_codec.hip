@@ -81,22 +81,26 @@ __device__ __forceinline__ void conv_out(const ConvArgs &a, int m, int n, float 
   }
 }
 
-// one workgroup: output rows m0 .. m0 + 63, columns n0 .. n0 + 16 WN - 1
-template <int WN, int EPI>
+// one workgroup: output rows m0 .. m0 + 16 TM - 1, columns n0 .. n0 + 16 WN
+// - 1 (the row tile follows T; every output's sum has the same order in any
+// tile: a sum of the same MFMAs over the same chunks)
+template <int WN, int TM, int EPI>
 __global__ __launch_bounds__(64 * WN) void k_conv_gemm(ConvArgs a) {
-  constexpr int NT = 64 * WN, XS = 36;
-  constexpr int XF4 = 64 * 32 / 4 / NT;
-  __shared__ float xs[2][64 * XS];
+  constexpr int NT = 64 * WN, XS = 36, MR = 16 * TM;
+  constexpr int NF4 = MR * 32 / 4;                  // float4 of an activation chunk
+  constexpr int XF4 = NF4 >= NT ? NF4 / NT : 1;     // per thread
+  __shared__ float xs[2][MR * XS];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int n0 = blockIdx.x * 16 * WN + 16 * wave, m0 = blockIdx.y * 64;
+  const int n0 = blockIdx.x * 16 * WN + 16 * wave, m0 = blockIdx.y * MR;
   const int K = a.taps * a.cin, cpk = a.cin / 32;
   const int q0 = blockIdx.z * kSliceChunks, q1 = min(a.taps * cpk, q0 + kSliceChunks);
   const float *wr = a.w + (size_t)min(n0 + r, a.n - 1) * K + 4 * g;
   int xrow[XF4], xcol[XF4], xo[XF4];
+  const bool xact = NF4 >= NT || t < NF4;  // threads that move activations
 #pragma unroll
   for (int i = 0; i < XF4; i++) {
-    const int f = t + NT * i, row = f >> 3, c4 = f & 7;
+    const int f = min(t + NT * i, NF4 - 1), row = f >> 3, c4 = f & 7;
     xrow[i] = min(m0 + row, a.T - 1);
     xcol[i] = 4 * c4;
     xo[i] = row * XS + 4 * c4;
@@ -110,12 +114,13 @@ __global__ __launch_bounds__(64 * WN) void k_conv_gemm(ConvArgs a) {
     wn[0] = ld4(wr + 32 * q);
     wn[1] = ld4(wr + 32 * q + 16);
   };
-  v4f acc[4];
+  v4f acc[TM];
 #pragma unroll
-  for (int i = 0; i < 4; i++) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < TM; i++) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
   load(q0);
+  if (xact)
 #pragma unroll
-  for (int i = 0; i < XF4; i++) *reinterpret_cast<float4 *>(&xs[0][xo[i]]) = xn[i];
+    for (int i = 0; i < XF4; i++) *reinterpret_cast<float4 *>(&xs[0][xo[i]]) = xn[i];
   wc[0] = wn[0];
   wc[1] = wn[1];
   __syncthreads();
@@ -125,7 +130,7 @@ __global__ __launch_bounds__(64 * WN) void k_conv_gemm(ConvArgs a) {
 #pragma unroll
     for (int s = 0; s < 2; s++) {
 #pragma unroll
-      for (int tm = 0; tm < 4; tm++) {
+      for (int tm = 0; tm < TM; tm++) {
         const float4 xa = *reinterpret_cast<const float4 *>(&xs[b][(16 * tm + r) * XS + 16 * s + 4 * g]);
         acc[tm] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.x, wc[s].x, acc[tm], 0, 0, 0);
         acc[tm] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.y, wc[s].y, acc[tm], 0, 0, 0);
@@ -134,8 +139,9 @@ __global__ __launch_bounds__(64 * WN) void k_conv_gemm(ConvArgs a) {
       }
     }
     if (q + 1 < q1) {
+      if (xact)
 #pragma unroll
-      for (int i = 0; i < XF4; i++) *reinterpret_cast<float4 *>(&xs[b ^ 1][xo[i]]) = xn[i];
+        for (int i = 0; i < XF4; i++) *reinterpret_cast<float4 *>(&xs[b ^ 1][xo[i]]) = xn[i];
       wc[0] = wn[0];
       wc[1] = wn[1];
     }
@@ -145,7 +151,7 @@ __global__ __launch_bounds__(64 * WN) void k_conv_gemm(ConvArgs a) {
   const int n = n0 + r;
   if (n >= a.n) return;
 #pragma unroll
-  for (int tm = 0; tm < 4; tm++)
+  for (int tm = 0; tm < TM; tm++)
 #pragma unroll
     for (int q = 0; q < 4; q++) {
       const int m = m0 + 16 * tm + 4 * g + q;
@@ -209,21 +215,34 @@ __global__ __launch_bounds__(256) void k_dw_ln(const float *__restrict__ x,
   }
 }
 
-// the output convolution (96 -> 1, kernel 7) and the clamp: x [6 + T][96]
+// the output convolution (96 -> 1, kernel 7) and the clamp: x [6 + T][96].
+// Four lanes per sample, lane j over channels 24 j .. 24 j + 23 of the 7
+// rows, the four sums joined as (p0 + p1) + (p2 + p3).
 __global__ __launch_bounds__(256) void k_conv_out(const float *__restrict__ x,
                                                   const float *__restrict__ w,
                                                   float b, int T, float *__restrict__ pcm) {
-  const int t = blockIdx.x * 256 + threadIdx.x;
-  if (t >= T) return;
+  const int t = blockIdx.x * 64 + (threadIdx.x >> 2), j = threadIdx.x & 3;
+  const int tc = min(t, T - 1);
   float acc = 0.f;
+#pragma unroll
   for (int k = 0; k < 7; k++) {
-    const float *xr = x + (size_t)(t + k) * 96;
-    const float *wk = w + k * 96;
-#pragma unroll 8
-    for (int c = 0; c < 96; c++) acc = fmaf(wk[c], xr[c], acc);
+    const float *xr = x + (size_t)(tc + k) * 96 + 24 * j;
+    const float *wk = w + k * 96 + 24 * j;
+#pragma unroll
+    for (int c = 0; c < 24; c += 4) {
+      const float4 xv = *reinterpret_cast<const float4 *>(xr + c);
+      const float4 wv = *reinterpret_cast<const float4 *>(wk + c);
+      acc = fmaf(wv.x, xv.x, acc);
+      acc = fmaf(wv.y, xv.y, acc);
+      acc = fmaf(wv.z, xv.z, acc);
+      acc = fmaf(wv.w, xv.w, acc);
+    }
   }
-  const float v = acc + b;
-  pcm[t] = fminf(1.0f, fmaxf(-1.0f, v));
+  const float p1 = __shfl_xor(acc, 1, 64);
+  const float s01 = (j & 1) ? p1 + acc : acc + p1;  // p0 + p1 (p2 + p3) in both lanes
+  const float s23 = __shfl_xor(s01, 2, 64);
+  const float v = ((j & 2) ? s23 + s01 : s01 + s23) + b;
+  if (j == 0 && t < T) pcm[t] = fminf(1.0f, fmaxf(-1.0f, v));
 }
 
 // a sequence buffer whose last `past` rows become its history
@@ -319,6 +338,8 @@ struct q3h_codec {
   float *part = nullptr;  // K-slice sums of the split products
   HistEntry *hist = nullptr;
   std::vector<HistEntry> hist_host;
+  // the kernels of a pass of F frames, captured once per F and replayed
+  std::vector<hipGraphExec_t> exec;  // [max_frames + 1]
   std::mutex mu;
 };
 
@@ -446,23 +467,35 @@ void conv(q3h_codec *c, const DConv &d, const float *x, int T, float *y, int epi
   a.part = c->part;
   const int S = slices(d);
   const int wn = d.n % 64 == 0 ? 4 : 2;
-  const dim3 grid(d.n / (16 * wn), (T + 63) / 64, S);
-#define Q3H_C(WN, E) hipLaunchKernelGGL((k_conv_gemm<WN, E>), grid, dim3(64 * WN), 0, c->stream, a)
-#define Q3H_E(WN)                          \
+  const int tm = T <= 16 ? 1 : (T <= 32 ? 2 : 4);
+  const dim3 grid(d.n / (16 * wn), (T + 16 * tm - 1) / (16 * tm), S);
+#define Q3H_C(WN, TM, E) \
+  hipLaunchKernelGGL((k_conv_gemm<WN, TM, E>), grid, dim3(64 * WN), 0, c->stream, a)
+#define Q3H_E(WN, TM)                      \
   do {                                     \
     if (epi == CE_BIAS)                    \
-      Q3H_C(WN, CE_BIAS);                  \
+      Q3H_C(WN, TM, CE_BIAS);              \
     else if (epi == CE_GELU)               \
-      Q3H_C(WN, CE_GELU);                  \
+      Q3H_C(WN, TM, CE_GELU);              \
     else if (epi == CE_RES)                \
-      Q3H_C(WN, CE_RES);                   \
+      Q3H_C(WN, TM, CE_RES);               \
     else                                   \
-      Q3H_C(WN, CE_SCALED_RES);            \
+      Q3H_C(WN, TM, CE_SCALED_RES);        \
+  } while (0)
+#define Q3H_T(WN)         \
+  do {                    \
+    if (tm == 1)          \
+      Q3H_E(WN, 1);       \
+    else if (tm == 2)     \
+      Q3H_E(WN, 2);       \
+    else                  \
+      Q3H_E(WN, 4);       \
   } while (0)
   if (wn == 4)
-    Q3H_E(4);
+    Q3H_T(4);
   else
-    Q3H_E(2);
+    Q3H_T(2);
+#undef Q3H_T
 #undef Q3H_E
 #undef Q3H_C
   if (S > 1) {
@@ -528,15 +561,32 @@ void pass(q3h_codec *c, int F) {
            sn, co);
     }
   }
-  hipLaunchKernelGGL(k_conv_out, dim3((rows + 255) / 256), dim3(256), 0, st, c->s_out, c->out_w,
+  hipLaunchKernelGGL(k_conv_out, dim3((rows + 63) / 64), dim3(256), 0, st, c->s_out, c->out_w,
                      c->out_b, rows, c->pcm);
   hipLaunchKernelGGL(k_save_hist, dim3((unsigned)c->hist_host.size()), dim3(256), 0, st, c->hist,
                      F);
   check_hip(hipGetLastError(), "codec kernels");
 }
 
+// the pass of F frames as one graph launch (captured at its first use)
+void run_pass(q3h_codec *c, int F) {
+  hipGraphExec_t &e = c->exec[F];
+  if (!e) {
+    hipGraph_t g = nullptr;
+    check_hip(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "capture");
+    pass(c, F);
+    check_hip(hipStreamEndCapture(c->stream, &g), "end capture");
+    const hipError_t r = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    check_hip(r, "instantiate");
+  }
+  check_hip(hipGraphLaunch(e, c->stream), "graph launch");
+}
+
 void codec_release(q3h_codec *c) {
   if (c->stream) (void)hipStreamSynchronize(c->stream);
+  for (hipGraphExec_t e : c->exec)
+    if (e) (void)hipGraphExecDestroy(e);
   for (void *p : c->allocs) dev_free(p);
   if (c->stream) (void)hipStreamDestroy(c->stream);
 }
@@ -554,6 +604,7 @@ extern "C" int q3h_codec_create(q3h_device *dev, const q3h_codec_weights *w, int
     c = new q3h_codec();
     c->dev = dev;
     c->max_frames = max_frames;
+    c->exec.assign(max_frames + 1, nullptr);
     check_hip(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
     const int L = kLatent;
     for (int i = 0; i < 2; i++) {
@@ -686,7 +737,7 @@ extern "C" int q3h_codec_back(q3h_codec *c, const float *x, int frames, float *p
       check_hip(hipMemcpyAsync(c->x_in, x + (size_t)f0 * kLatent, sizeof(float) * F * kLatent,
                                hipMemcpyHostToDevice, c->stream),
                 "upload x");
-      pass(c, F);
+      run_pass(c, F);
       check_hip(hipMemcpyAsync(pcm + (size_t)f0 * kFrameSamples, c->pcm,
                                sizeof(float) * F * kFrameSamples, hipMemcpyDeviceToHost, c->stream),
                 "download pcm");
