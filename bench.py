@@ -66,17 +66,17 @@ def log(msg):
     print(f"bench: {msg}", file=sys.stderr, flush=True)
 
 
-def build_model(dev, seed, max_positions, act_q8, dtype=q3h.Q8_0):
+def build_model(dev, seed, max_positions, act_q8, dtype=q3h.Q8_0, kv16=0):
     """Talker + code predictor + heads on the device, from f32 weights that the
     library quantizes to Q8_0 (bit-exact ggml quantize_row_q8_0_ref) or keeps
     in f32 (dtype F32); act_q8: activations quantized per 32-block too (int8
     MFMA products)."""
     t0 = time.time()
     tl, tf = synth.stack_weights(seed, "talker.model.", synth.TALKER)
-    ts = q3h.Stack(dev, dict(synth.TALKER, dtype=dtype, kv_f16=0, act_q8=act_q8,
+    ts = q3h.Stack(dev, dict(synth.TALKER, dtype=dtype, kv_f16=kv16, act_q8=act_q8,
                              max_positions=max_positions), tl, tf, q3h.F32)
     cl, cf = synth.stack_weights(seed, "talker.code_predictor.model.", synth.PREDICTOR)
-    cs = q3h.Stack(dev, dict(synth.PREDICTOR, dtype=dtype, kv_f16=0, act_q8=act_q8,
+    cs = q3h.Stack(dev, dict(synth.PREDICTOR, dtype=dtype, kv_f16=kv16, act_q8=act_q8,
                              max_positions=16), cl, cf, q3h.F32)
     th = synth.talker_head(seed)
     ts.add_head(th, q3h.F32)
@@ -442,6 +442,9 @@ def main():
                     help="skip the long-context attention measurement (frame_b1)")
     ap.add_argument("--no-text", action="store_true",
                     help="skip the time-to-first-frame measurement from token ids (frame_b1)")
+    ap.add_argument("--kv16", action="store_true",
+                    help="K/V caches in half floats (the reference's KvF16 option, lm.pas:353); "
+                         "the default is its f32 cache")
     ap.add_argument("--no-codec", action="store_true",
                     help="skip the decoder back-part measurement (frame_b1)")
     ap.add_argument("--codec-only", action="store_true",
@@ -494,7 +497,7 @@ def main():
     dev = q3h.Device(0)
     act_q8 = 0 if (b1 or f32w) else 1
     ts, cs, tables, f32 = build_model(dev, args.seed, max_pos, act_q8,
-                                      q3h.F32 if f32w else q3h.Q8_0)
+                                      q3h.F32 if f32w else q3h.Q8_0, int(args.kv16))
     if args.gemv_only:
         roofline = gemv_roofline(ts, args)
         print(json.dumps({"roofline": roofline}), flush=True)
@@ -573,7 +576,7 @@ def main():
                    PROMPT_ROWS if b1 else (F32_PROMPT_ROWS if f32w else "U[16,256]"),
                    "frames": steps, "talker_layers": 28, "cp_layers": 5, "hidden": 1024,
                    "heads": "16q/8kv x 128", "ffn": 3072, "weights": "f32" if f32w else "Q8_0",
-                   "kv": "f32", "activations": "q8_0 (int8 MFMA)" if act_q8 else "f32"},
+                   "kv": "f16" if args.kv16 else "f32", "activations": "q8_0 (int8 MFMA)" if act_q8 else "f32"},
         "prefill_ms": round(1e3 * prefill_s, 2),
         "step_us_p50": round(1e6 * float(np.median(lat)), 1),
         "step_us_p99": round(1e6 * float(np.percentile(lat, 99)), 1),
