@@ -474,7 +474,17 @@ Mat alloc_mat(int N, int K, int dtype, int64_t &bytes) {
 void free_mat(Mat &m) {
   dev_free(m.q);  // the scales share this allocation
   dev_free(m.f);
+  dev_free(m.x3);
   m = Mat();
+}
+
+// the split-bf16 planes of an f32 layer matrix (the operands of the prefill
+// products); their bytes go to aux
+void make_x3(Mat &m, int64_t &aux, hipStream_t st) {
+  m.x3 = (uint16_t *)dev_alloc((size_t)3 * m.N * m.K * 2);
+  aux += (int64_t)3 * m.N * m.K * 2;
+  launch_split3(m, st);
+  check_hip(hipGetLastError(), "split3");
 }
 
 // Upload rows x K of host matrix src (src_dtype) into rows r*stride+off of m.
@@ -595,6 +605,8 @@ extern "C" int q3h_stack_create(q3h_device *dev, const q3h_stack_config *cfg,
         upload_rows(L.gu, c.dtype, lw.wgate, w->src_dtype, I, H, 2, 0, staging, s->stream);
         upload_rows(L.gu, c.dtype, lw.wup, w->src_dtype, I, H, 2, 1, staging, s->stream);
         upload_rows(L.down, c.dtype, lw.wdown, w->src_dtype, H, I, 1, 0, staging, s->stream);
+        if (c.dtype == Q3H_F32 && c.max_positions > 64)
+          for (Mat *m : {&L.qkv, &L.o, &L.gu, &L.down}) make_x3(*m, s->aux_bytes, s->stream);
         L.in_norm = upload_vec(lw.input_norm, H, "input_layernorm");
         L.post_norm = upload_vec(lw.post_norm, H, "post_attention_layernorm");
         // q_norm and k_norm side by side, then the RMSNorm epsilon:
@@ -637,7 +649,7 @@ extern "C" int q3h_stack_create(q3h_device *dev, const q3h_stack_config *cfg,
       throw;
     }
     dev_free(staging);
-    dev->bytes += s->bytes;
+    dev->bytes += s->bytes + s->aux_bytes;
     dev->stacks++;
     *out = s;
   });
@@ -687,7 +699,7 @@ extern "C" int q3h_stack_destroy(q3h_stack *s) {
     require(s->contexts.load() == 0, Q3H_E_STATE,
             "q3h_stack_destroy: contexts or frames still use this stack");
     check_hip(hipSetDevice(s->dev->ordinal), "hipSetDevice");
-    s->dev->bytes -= s->bytes + s->head_bytes;
+    s->dev->bytes -= s->bytes + s->head_bytes + s->aux_bytes;
     s->dev->stacks--;
     destroy_stack(s);
     delete s;

@@ -125,6 +125,7 @@ struct q3h_stack {
   float *rope_cs = nullptr;  // [max_positions][head_dim / 2] (cos, sin)
   std::vector<q3h::Mat> heads;
   int64_t bytes = 0, head_bytes = 0;
+  int64_t aux_bytes = 0;  // the split-bf16 planes of f32 layers (not in StackBytes)
   std::atomic<int> contexts{0};
   std::mutex mu;
   hipStream_t stream = nullptr;  // uploads

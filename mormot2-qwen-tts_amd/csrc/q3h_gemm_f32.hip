@@ -235,6 +235,167 @@ __global__ __launch_bounds__(64 * WN) void k_gemm_f32_m64(const float *__restric
     }
 }
 
+// f32 x f32 products on the bf16 matrix cores, exact to the fp32 rounding of
+// the sum: each operand split into three bf16 parts, x = x_hi + x_mid + x_lo
+// (the top 8 significant bits, the next 8, the last 8: exact, as an f32
+// significand has 24 bits), and the six part products whose weight is at
+// least 2^-16 of x w accumulated in fp32 (hi hi, hi mid, mid hi, hi lo,
+// lo hi, mid mid; each bf16 product is exact in fp32). The dropped three
+// weigh below 2^-23 of the product, under its fp32 rounding.
+//
+// v_mfma_f32_16x16x32_bf16: lane l holds A[l % 16][8 (l / 16) .. + 7] and
+// B[8 (l / 16) .. + 7][l % 16] (8 bf16 each) and receives
+// D[4 (l / 16) + r][l % 16]. The tile and pipeline are those of
+// k_gemm_f32_m64: 64 activation rows x 16 WN weight rows per workgroup, a 32-
+// column chunk at a time; the activations are split as they go to LDS (three
+// bf16 planes, double buffered), the weights come pre-split (Mat::x3) to
+// registers one chunk ahead. 24 MFMAs per wave and chunk instead of 32 of
+// the f32 kind, each a sixteenth of the cycles per flop.
+typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void split3(float x, uint32_t &h, uint32_t &m, uint32_t &l) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t hb = u & 0xffff0000u;
+  const float r1 = x - __uint_as_float(hb);
+  const uint32_t mb = __float_as_uint(r1) & 0xffff0000u;
+  const float r2 = r1 - __uint_as_float(mb);
+  h = hb >> 16;
+  m = mb >> 16;
+  l = __float_as_uint(r2) >> 16;
+}
+
+template <int WN, int EPI>
+__global__ __launch_bounds__(64 * WN) void k_gemm_x3_m64(const uint16_t *__restrict__ w3,
+                                                         const float *__restrict__ x, int ldx,
+                                                         int M, int N, int K, int kc,
+                                                         float *__restrict__ y, int ldy) {
+  constexpr int NT = 64 * WN;
+  constexpr int NB = 1;                  // 16-column weight tiles per wave
+  constexpr int XS = 40;                 // LDS row stride, bf16 (80 bytes)
+  constexpr int XF4 = 64 * 32 / 4 / NT;  // float4 of an activation chunk per thread
+  __shared__ uint16_t xs[2][3][64 * XS];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16 * NB * WN + 16 * NB * wave, m0 = blockIdx.y * 64;
+  const int kz = blockIdx.z * kc;
+  const size_t plane = (size_t)N * K;
+  const uint16_t *wr[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++) wr[j] = w3 + (size_t)min(n0 + 16 * j + r, N - 1) * K + kz + 8 * g;
+  const float *xr[XF4];
+  int xo[XF4];
+#pragma unroll
+  for (int i = 0; i < XF4; i++) {
+    const int f = t + NT * i, row = f >> 3, c4 = f & 7;
+    xr[i] = x + (size_t)min(m0 + row, M - 1) * ldx + kz + 4 * c4;
+    xo[i] = row * XS + 4 * c4;
+  }
+  float4 xn[XF4];
+  u32x4v wn[NB][3], wc[NB][3];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < XF4; i++) xn[i] = ld4(xr[i] + k0);
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+      for (int p = 0; p < 3; p++)
+        wn[j][p] = *reinterpret_cast<const u32x4v *>(wr[j] + p * plane + k0);
+  };
+  // the chunk's activations into the three planes of LDS buffer b
+  auto stage = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < XF4; i++) {
+      uint32_t h[4], m[4], l[4];
+      split3(xn[i].x, h[0], m[0], l[0]);
+      split3(xn[i].y, h[1], m[1], l[1]);
+      split3(xn[i].z, h[2], m[2], l[2]);
+      split3(xn[i].w, h[3], m[3], l[3]);
+      *reinterpret_cast<uint2 *>(&xs[b][0][xo[i]]) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+      *reinterpret_cast<uint2 *>(&xs[b][1][xo[i]]) = make_uint2(m[0] | (m[1] << 16), m[2] | (m[3] << 16));
+      *reinterpret_cast<uint2 *>(&xs[b][2][xo[i]]) = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+    }
+  };
+  v4f acc[NB][4];
+#pragma unroll
+  for (int j = 0; j < NB; j++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[j][i] = v4f{0.f, 0.f, 0.f, 0.f};
+  load(0);
+  stage(0);
+#pragma unroll
+  for (int j = 0; j < NB; j++)
+#pragma unroll
+    for (int p = 0; p < 3; p++) wc[j][p] = wn[j][p];
+  __syncthreads();
+  const int nc = kc / 32;
+  for (int c = 0; c < nc; c++) {
+    const int b = c & 1;
+    if (c + 1 < nc) load(32 * (c + 1));
+#pragma unroll
+    for (int tm = 0; tm < 4; tm++) {
+      const int o = (16 * tm + r) * XS + 8 * g;
+      const bf8v ah = __builtin_bit_cast(bf8v, *reinterpret_cast<const u32x4v *>(&xs[b][0][o]));
+      const bf8v am = __builtin_bit_cast(bf8v, *reinterpret_cast<const u32x4v *>(&xs[b][1][o]));
+      const bf8v al = __builtin_bit_cast(bf8v, *reinterpret_cast<const u32x4v *>(&xs[b][2][o]));
+#pragma unroll
+      for (int j = 0; j < NB; j++) {
+        const bf8v bh = __builtin_bit_cast(bf8v, wc[j][0]), bm = __builtin_bit_cast(bf8v, wc[j][1]),
+                   bl = __builtin_bit_cast(bf8v, wc[j][2]);
+        v4f a = acc[j][tm];
+        a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, bm, a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, bh, a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bm, a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, a, 0, 0, 0);
+        acc[j][tm] = a;
+      }
+    }
+    if (c + 1 < nc) {
+      stage(b ^ 1);
+#pragma unroll
+      for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int p = 0; p < 3; p++) wc[j][p] = wn[j][p];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    const int n = n0 + 16 * j + r;
+#pragma unroll
+    for (int tm = 0; tm < 4; tm++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int m = m0 + 16 * tm + 4 * g + q;
+        const float v = acc[j][tm][q];
+        if (EPI == EPI_SWIGLU) {
+          const float u = __shfl_xor(v, 1);
+          if (m < M && (r & 1) == 0) y[(size_t)m * ldy + n / 2] = silu_mul_f(v, u);
+        } else if (m < M) {
+          if (EPI == EPI_ADD)
+            y[(size_t)m * ldy + n] += v;
+          else if (EPI == EPI_PART)
+            y[((size_t)blockIdx.z * M + m) * ldy + n] = v;
+          else
+            y[(size_t)m * ldy + n] = v;
+        }
+      }
+  }
+}
+
+// the three bf16 planes of an f32 matrix
+__global__ void k_split3(const float *__restrict__ f, size_t n, uint16_t *__restrict__ x3) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  uint32_t h, m, l;
+  split3(f[i], h, m, l);
+  x3[i] = (uint16_t)h;
+  x3[n + i] = (uint16_t)m;
+  x3[2 * n + i] = (uint16_t)l;
+}
+
 // The same products with Q8_0 weights (int8 quants [N][K], then fp16 scales
 // [N][K/32]) and f32 activations: a 64-column step per load, lane l taking
 // the 16 quants 16 (l / 16) .. + 15 of its row (one 16-byte load) and the
@@ -393,6 +554,22 @@ void launch_m64(const Mat &W, const float *x, int ldx, int M, int epi, float *y,
                 hipStream_t st, int ks = 1) {
   const dim3 grid(W.N / (16 * WN), (M + 63) / 64, ks), block(64 * WN);
   const int kc = W.K / ks;
+  if (W.x3 && epi != EPI_ADD_SILU) {
+    const dim3 gx(W.N / (16 * WN), (M + 63) / 64, ks);  // one 16-column tile per wave
+#define Q3H_X(E)                                                                              \
+  hipLaunchKernelGGL((k_gemm_x3_m64<WN, E>), gx, block, 0, st, W.x3, x, ldx, M, W.N, W.K, kc, \
+                     y, ldy)
+    if (epi == EPI_STORE)
+      Q3H_X(EPI_STORE);
+    else if (epi == EPI_ADD)
+      Q3H_X(EPI_ADD);
+    else if (epi == EPI_PART)
+      Q3H_X(EPI_PART);
+    else
+      Q3H_X(EPI_SWIGLU);
+#undef Q3H_X
+    return;
+  }
 #define Q3H_G(E)                                                                               \
   hipLaunchKernelGGL((k_gemm_f32_m64<WN, E>), grid, block, 0, st, W.f, x, ldx, M, W.N, W.K, kc, \
                      y, ldy)
@@ -429,6 +606,11 @@ void launch_m(const Mat &W, const float *x, int ldx, int M, int epi, float *y, i
 }
 
 }  // namespace
+
+void launch_split3(const Mat &m, hipStream_t st) {
+  const size_t n = (size_t)m.N * m.K;
+  hipLaunchKernelGGL(k_split3, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, m.f, n, m.x3);
+}
 
 bool gemm_f32_supported(int N, int K) {
   return N % 16 == 0 && (K == 1024 || K == 2048 || K == 3072);

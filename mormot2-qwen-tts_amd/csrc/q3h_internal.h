@@ -16,6 +16,10 @@ struct Mat {
   int8_t *q = nullptr;
   _Float16 *d = nullptr;
   float *f = nullptr;
+  // f32 matrices of stacks that prefill many rows: the same values as three
+  // bf16 planes [3][N][K] (w = hi + mid + lo exactly), the operands of the
+  // split-bf16 matrix-core products (null: not made)
+  uint16_t *x3 = nullptr;
 };
 
 // Per-row view of a K/V cache for the attention kernels. k, v: the cache of
@@ -85,6 +89,8 @@ bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st, hipEvent_t 
 // (Q8_0 weights, f32 activations: the same products, weights dequantized as
 // they load; taken for more than kGemvRows rows)
 bool gemm_f32_supported(int N, int K);
+// the three bf16 planes of m.f into m.x3 (allocated by the caller)
+void launch_split3(const Mat &m, hipStream_t st);
 constexpr int kGemvRows = 4;
 void launch_gemm_f32(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
                      hipStream_t st);
