@@ -315,7 +315,8 @@ void run_layers(const q3h_stack *s, Work &w, int M, int positions, bool fused, h
   }
 }
 
-void run_cp_fused(const q3h_stack *s, Work &w, const q3h_context *ctx, int pos, hipStream_t st) {
+void run_cp_fused(const q3h_stack *s, Work &w, const q3h_context *ctx, int pos, hipStream_t st,
+                  const CodeSrc *src) {
   const q3h_stack_config &c = s->cfg;
   const int H = c.hidden, hd = c.head_dim, NQ = c.heads * hd, NKV = c.kv_heads * hd;
   const int I = c.intermediate, ldq = NQ + 2 * NKV;
@@ -326,8 +327,13 @@ void run_cp_fused(const q3h_stack *s, Work &w, const q3h_context *ctx, int pos, 
   const float *rope_row = s->rope_cs + (size_t)pos * hd;  // (cos, sin) x head_dim / 2
   for (int l = 0; l < c.layers; l++) {
     const Layer &L = s->layers[l];
-    launch_gemv(make_gemv(L.qkv, w.h, H, 1, L.in_norm, c.rms_eps, w.qkv, ldq), EPI_STORE, true,
-                st);
+    const GemvArgs qa = make_gemv(L.qkv, w.h, H, 1, L.in_norm, c.rms_eps, w.qkv, ldq);
+    if (l == 0 && src)
+      require(launch_gemv_q8_code(qa, src->logits, src->vocab, src->rows, src->code_out, w.h,
+                                  src->alive, st),
+              Q3H_E_ARG, "code-predictor input: shape not supported on the device");
+    else
+      launch_gemv(qa, EPI_STORE, true, st);
     void *kl = static_cast<char *>(ctx->k) + l * per_layer * esz;
     launch_attn_o_cp(L.o, w.qkv, kl, v_off, w.h, L.q_norm, rope_row, pos, kv16, st);
     launch_gemv(make_gemv(L.gu, w.h, H, 1, L.post_norm, c.rms_eps, w.act, I), EPI_SWIGLU, true,

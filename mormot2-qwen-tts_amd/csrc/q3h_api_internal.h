@@ -97,8 +97,18 @@ bool cp_fused_supported(const q3h_stack_config &c);
 // one new row at position pos of a code-predictor context (16 positions)
 // through the layers of stack s, attention fused into o_proj; the row is in
 // w.h and stays there (cp_fused_supported(s->cfg), ctx->max_pos == 16)
+// src (optional): the row is chosen on the device instead, by the first
+// product (launch_gemv_q8_code: the argmax of src->logits, row of src->rows,
+// code to src->code_out), and written to w.h by that product
+struct CodeSrc {
+  const float *logits;
+  int vocab;
+  const float *rows;
+  int *code_out;
+  const int *alive;
+};
 void run_cp_fused(const struct ::q3h_stack *s, Work &w, const struct ::q3h_context *ctx,
-                  int pos, hipStream_t st);
+                  int pos, hipStream_t st, const CodeSrc *src = nullptr);
 
 // options of run_layers (the first two: the int8 path over few rows, partial_path)
 struct LayerIO {

@@ -64,14 +64,6 @@ struct FrameDev {
 
 constexpr int kArgBlock = 1024;
 
-// (value, index) maximum with the first index winning ties
-__device__ __forceinline__ void argmax_merge(float &v, int &i, float v2, int i2) {
-  if (v2 > v || (v2 == v && i2 < i)) {
-    v = v2;
-    i = i2;
-  }
-}
-
 __device__ int block_argmax(float v, int i) {
   __shared__ float sv[kArgBlock / 64];
   __shared__ int si[kArgBlock / 64];
@@ -218,7 +210,8 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_argmax(const float *__restrict
   float bv = -INFINITY;
   int bi = 0x7fffffff;
   for (int i = tid; i < cp_vocab; i += kArgBlock) argmax_merge(bv, bi, lg[i], i);
-  const int code = block_argmax(bv, bi);
+  // (no maximum only when every logit is NaN: row cp_vocab - 1 of the table)
+  const int code = min(block_argmax(bv, bi), cp_vocab - 1);
   if (tid == 0) codes[(size_t)s * groups + g + 1] = code;
   if (g + 1 < groups - 1) {
     const float *emb = pred_emb + ((size_t)g * cp_vocab + code) * H;
@@ -452,6 +445,10 @@ void enqueue_step(q3h_frame *f, int positions, hipStream_t st) {
   // one stream on the Qwen3-TTS shapes: steps 1.. run the fused single-row
   // path (positions are fixed: step g adds position g + 1)
   const bool fused = n == 1 && cp_fused_supported(cp->cfg) && f->cctx[0]->max_pos == 16;
+  // greedy on that path: the argmax of head g and the next input row are taken
+  // by the first product of forward g + 1 (one launch fewer per group)
+  const bool code_in_product =
+      fused && !fd.sp.do_sample && (c.cp_vocab == 2048 || c.cp_vocab == 3072);
   for (int g = 0; g < c.groups - 1; g++) {
     const int R = g == 0 ? 2 : 1;
     if (cq) {
@@ -470,7 +467,9 @@ void enqueue_step(q3h_frame *f, int positions, hipStream_t st) {
       continue;
     }
     if (fused && g > 0) {
-      run_cp_fused(cp, f->cw, f->cctx[0], g + 1, st);
+      const CodeSrc src{fd.cp_logits, fd.cp_vocab,
+                        fd.pred_emb + (size_t)(g - 1) * fd.cp_vocab * H, fd.codes + g, fd.alive};
+      run_cp_fused(cp, f->cw, f->cctx[0], g + 1, st, code_in_product ? &src : nullptr);
     } else {
       launch_prep(f->c_arr, fd.alive, n, R, f->cw.rd, st);
       run_layers(cp, f->cw, n * R, c.groups, R == 1, st);
@@ -483,7 +482,7 @@ void enqueue_step(q3h_frame *f, int positions, hipStream_t st) {
       hipLaunchKernelGGL(k_cp_sample, dim3(n), dim3(kArgBlock), 0, st, fd.cp_logits, fd.alive,
                          fd.pred_emb, fd.cp_h, fd.codes, fd.cp_vocab, fd.groups, fd.H, g, fd.sp,
                          fd.seeds, (const int *)fd.nframes);
-    else
+    else if (!code_in_product || g + 1 == c.groups - 1)
       hipLaunchKernelGGL(k_cp_argmax, dim3(n), dim3(kArgBlock), 0, st, fd.cp_logits, fd.alive,
                          fd.pred_emb, fd.cp_h, fd.codes, fd.cp_vocab, fd.groups, fd.H, g);
   }

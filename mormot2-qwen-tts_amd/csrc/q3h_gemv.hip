@@ -305,6 +305,122 @@ __global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq
   }
 }
 
+// The single-row product (EPI_STORE, RMSNorm prologue) whose activation row
+// is chosen on the device: row `code` of rows [vocab][K], code the argmax of
+// logits [vocab] (the smallest index among equal maxima: ChooseCode). Every
+// wave finds the argmax itself from L2-resident logits, so there is still no
+// barrier; the logit loads go out before the weight loads, so the argmax
+// waits only for them and the row's load overlaps the weight stream. The
+// first wave of workgroup 0 also writes, when *alive, the code and the raw row
+// (h_out): what k_cp_argmax writes for the next code-predictor forward. The
+// product equals k_gemv_q8v on that row. Arguments: the first 14 dwords are
+// preloaded into SGPRs; h_out and alive, used only at the end, come after.
+template <int R, int C, int W, int V4>
+__global__ __launch_bounds__(W * 64) void k_gemv_q8v_code(
+    const int8_t *__restrict__ wq, const float *__restrict__ logits,
+    const float *__restrict__ rows, const float *__restrict__ norm_w, float *__restrict__ y,
+    int N, float eps, int *__restrict__ code_out, float *__restrict__ h_out,
+    const int *__restrict__ alive) {
+  constexpr int K = C * 1024, NB = K / 32;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * W + wave) * R;
+  const _Float16 *__restrict__ wd = reinterpret_cast<const _Float16 *>(wq + (size_t)N * K);
+  float4 lg[V4];
+#pragma unroll
+  for (int i = 0; i < V4; i++) lg[i] = reinterpret_cast<const float4 *>(logits)[i * 64 + lane];
+  __builtin_amdgcn_sched_barrier(0);
+  int4 wv[R][C];
+  float sc[R][C];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int row = min(row0 + r, N - 1);
+    const int8_t *q = wq + (size_t)row * K + lane * 16;
+    const _Float16 *d = wd + (size_t)row * NB + (lane >> 1);
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+      wv[r][c] = *reinterpret_cast<const int4 *>(q + c * 1024);
+      sc[r][c] = (float)d[c * 32];
+    }
+  }
+  float4 wn[C][4];
+#pragma unroll
+  for (int c = 0; c < C; c++)
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      wn[c][i] = reinterpret_cast<const float4 *>(norm_w + c * 1024 + lane * 16)[i];
+  __builtin_amdgcn_sched_barrier(0);
+  // the argmax: element 4 (64 i + lane) + e of lane's loads
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+#pragma unroll
+  for (int i = 0; i < V4; i++) {
+    const float e4[4] = {lg[i].x, lg[i].y, lg[i].z, lg[i].w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) argmax_merge(bv, bi, e4[e], 4 * (i * 64 + lane) + e);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float v2 = __shfl_xor(bv, off, 64);
+    const int i2 = __shfl_xor(bi, off, 64);
+    argmax_merge(bv, bi, v2, i2);
+  }
+  // (no maximum only when every logit is NaN: row vocab - 1, not an index past the table)
+  const int code = min(__builtin_amdgcn_readfirstlane(bi), V4 * 256 - 1);
+  const float *x = rows + (size_t)code * K;
+  float4 xv[C][4];
+#pragma unroll
+  for (int c = 0; c < C; c++)
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      xv[c][i] = reinterpret_cast<const float4 *>(x + c * 1024 + lane * 16)[i];
+  if (blockIdx.x == 0 && wave == 0 && *alive) {
+    if (lane == 0) *code_out = code;
+#pragma unroll
+    for (int c = 0; c < C; c++)
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        reinterpret_cast<float4 *>(h_out + c * 1024 + lane * 16)[i] = xv[c][i];
+  }
+  // RMSNorm factor and w * x as k_gemv_q8v computes them
+  float ss0 = 0.f, ss1 = 0.f;
+#pragma unroll
+  for (int c = 0; c < C; c++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float4 v = xv[c][i];
+      ss0 = fmaf(v.x, v.x, fmaf(v.y, v.y, ss0));
+      ss1 = fmaf(v.z, v.z, fmaf(v.w, v.w, ss1));
+    }
+  const float ss = wave_sum_dpp(ss0 + ss1);
+  const float inv = 1.0f / sqrtf(ss * (1.0f / K) + eps);
+#pragma unroll
+  for (int c = 0; c < C; c++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float4 v = xv[c][i], w = wn[c][i];
+      xv[c][i] = make_float4(w.x * v.x, w.y * v.y, w.z * v.z, w.w * v.w);
+    }
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    acc[r] = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+      float p0 = dot4_i8(wv[r][c].x, xv[c][0], 0.f);
+      float p1 = dot4_i8(wv[r][c].y, xv[c][1], 0.f);
+      p0 = dot4_i8(wv[r][c].z, xv[c][2], p0);
+      p1 = dot4_i8(wv[r][c].w, xv[c][3], p1);
+      acc[r] = fmaf(sc[r][c], p0 + p1, acc[r]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; r++) acc[r] = wave_sum_dpp(acc[r]) * inv;
+  if (lane != 0 || row0 >= N) return;
+#pragma unroll
+  for (int r = 0; r < R; r++)
+    if (row0 + r < N) y[row0 + r] = acc[r];
+}
+
 // ev0 / ev1 (optional): events recorded at the start and the end of the
 // kernel's own execution (hipExtLaunchKernelGGL), for measurement
 template <int R, int C>
@@ -362,6 +478,34 @@ void launch_rc(const GemvArgs &a, int epi, int waves, hipStream_t st, hipEvent_t
 }
 
 }  // namespace
+
+bool launch_gemv_q8_code(const GemvArgs &a, const float *logits, int vocab, const float *rows,
+                         int *code_out, float *h_out, const int *alive, hipStream_t st) {
+  if (reinterpret_cast<const int8_t *>(a.wd) != a.wq + (size_t)a.N * a.K) return false;
+  if (a.M != 1 || a.K != 1024 || a.norm_w == nullptr || a.N % 1024 != 0) return false;
+  const int R = a.N / 1024;  // 256 workgroups of 4 waves
+  const dim3 grid(256), block(256);
+#define Q3H_C(RR, V4)                                                                             \
+  hipLaunchKernelGGL((k_gemv_q8v_code<RR, 1, 4, V4>), grid, block, 0, st, a.wq, logits, rows,     \
+                     a.norm_w, a.y, a.N, a.eps, code_out, h_out, alive)
+#define Q3H_C_V(RR)          \
+  if (vocab == 2048)         \
+    Q3H_C(RR, 8);            \
+  else if (vocab == 3072)    \
+    Q3H_C(RR, 12);           \
+  else                       \
+    return false
+  switch (R) {
+    case 1: Q3H_C_V(1); break;
+    case 2: Q3H_C_V(2); break;
+    case 3: Q3H_C_V(3); break;
+    case 4: Q3H_C_V(4); break;
+    default: return false;
+  }
+#undef Q3H_C_V
+#undef Q3H_C
+  return true;
+}
 
 bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st, hipEvent_t ev0,
                          hipEvent_t ev1) {

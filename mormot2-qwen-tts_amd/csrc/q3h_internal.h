@@ -83,6 +83,13 @@ void launch_gemv(const GemvArgs &a, int epi, bool q8, hipStream_t st);
 // false when the shape is not one it takes (nothing launched)
 bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st, hipEvent_t ev0 = nullptr,
                          hipEvent_t ev1 = nullptr);
+// the single-row product with an RMSNorm prologue (M == 1, K == 1024, N a
+// multiple of 1024 up to 4096) over row `code` of rows [vocab][K], code = the
+// argmax of logits [vocab] (vocab 2048 or 3072; the smallest index among
+// equal maxima); when *alive, the code goes to *code_out and the raw row to
+// h_out [K]. false when the shape is not one it takes (nothing launched)
+bool launch_gemv_q8_code(const GemvArgs &a, const float *logits, int vocab, const float *rows,
+                         int *code_out, float *h_out, const int *alive, hipStream_t st);
 // the f32 matrix-core products (q3h_gemm_f32.hip): y[m][n] (+)= W[n] . x[m]
 // for f32 W [N][K] (N % 16 == 0, K in {1024, 2048, 3072}); epi EPI_* (SwiGLU:
 // interleaved gate / up rows, y [M][N / 2])

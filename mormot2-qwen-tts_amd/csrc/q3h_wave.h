@@ -98,4 +98,12 @@ __device__ __forceinline__ float group16_sum_dpp(float v) {
   return v;
 }
 
+// (value, index) maximum with the first index winning ties
+__device__ __forceinline__ void argmax_merge(float &v, int &i, float v2, int i2) {
+  if (v2 > v || (v2 == v && i2 < i)) {
+    v = v2;
+    i = i2;
+  }
+}
+
 }  // namespace q3h
