@@ -46,6 +46,39 @@ def test_frame_b1_q8_16_frames(full, synth):
     of.destroy()
 
 
+def test_frame_b1_cp_ties_take_the_first_index(device, synth, monkeypatch):
+    """Every code-predictor head with rows 2k and 2k + 1 equal, so each logit
+    ties with its neighbour: ChooseCode must take the even index of the
+    maximal pair. At batch 1 the argmax of heads 0-13 runs inside the next
+    q/k/v product, one per wave, and head 14 in its own kernel."""
+    orig = synth.cp_head
+
+    def paired(seed, g):
+        h = np.array(orig(seed, g), copy=True)
+        h[1::2] = h[0::2]
+        return h
+
+    monkeypatch.setattr(synth, "cp_head", paired)
+    m = Model(device, seed=23, talker_layers=2, cp_layers=2, max_positions=128)
+    fr = m.frame(n_streams=1, max_positions=128)
+    of = m.oracle_frame(max_positions=128)
+    try:
+        pre = synth.prompt(23, 20)
+        fr.start(0, pre)
+        of.start(pre)
+        for i in range(4):
+            codes, alive = fr.step()
+            ref = of.next()
+            print(f"frame {i}: {codes[0].tolist()}", flush=True)
+            assert alive[0] == 1
+            assert np.array_equal(codes[0], ref), (i, codes[0], ref)
+            assert np.all(codes[0][1:] % 2 == 0), codes[0]
+    finally:
+        fr.destroy()
+        of.destroy()
+        m.destroy()
+
+
 def test_frame_graph_equals_eager(full, synth):
     m = full
     pre = synth.prompt(9, 20)
