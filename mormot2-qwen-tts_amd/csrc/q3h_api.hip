@@ -342,6 +342,26 @@ void run_cp_fused(const q3h_stack *s, Work &w, const q3h_context *ctx, int pos, 
   }
 }
 
+void run_cp_fused_first(const q3h_stack *s, Work &w, const q3h_context *ctx, hipStream_t st) {
+  const q3h_stack_config &c = s->cfg;
+  const int H = c.hidden, hd = c.head_dim, NQ = c.heads * hd, NKV = c.kv_heads * hd;
+  const int I = c.intermediate, ldq = NQ + 2 * NKV;
+  const bool kv16 = c.kv_f16 != 0;
+  const size_t per_layer = (size_t)c.kv_heads * ctx->max_pos * hd;
+  const int v_off = (int)(per_layer * c.layers);
+  const size_t esz = kv16 ? 2 : 4;
+  for (int l = 0; l < c.layers; l++) {
+    const Layer &L = s->layers[l];
+    launch_gemv(make_gemv(L.qkv, w.h, H, 2, L.in_norm, c.rms_eps, w.qkv, ldq), EPI_STORE, true,
+                st);
+    void *kl = static_cast<char *>(ctx->k) + l * per_layer * esz;
+    launch_attn2_o_cp(L.o, w.qkv, ldq, kl, v_off, w.h, L.q_norm, s->rope_cs, kv16, st);
+    launch_gemv(make_gemv(L.gu, w.h, H, 2, L.post_norm, c.rms_eps, w.act, I), EPI_SWIGLU, true,
+                st);
+    launch_gemv(make_gemv(L.down, w.act, I, 2, nullptr, 0.f, w.h, H), EPI_ADD, true, st);
+  }
+}
+
 GemvArgs make_gemv(const Mat &W, const float *x, int ldx, int M, const float *norm_w,
                    float eps, float *y, int ldy) {
   GemvArgs a{};

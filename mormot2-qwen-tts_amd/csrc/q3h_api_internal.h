@@ -110,6 +110,12 @@ struct CodeSrc {
 void run_cp_fused(const struct ::q3h_stack *s, Work &w, const struct ::q3h_context *ctx,
                   int pos, hipStream_t st, const CodeSrc *src = nullptr);
 
+// the first step of a code-predictor context (its two rows, positions 0 and
+// 1, in w.h) through the layers, attention fused into o_proj; the rows stay
+// in w.h (cp_fused_supported(s->cfg), ctx->max_pos == 16)
+void run_cp_fused_first(const struct ::q3h_stack *s, Work &w, const struct ::q3h_context *ctx,
+                        hipStream_t st);
+
 // options of run_layers (the first two: the int8 path over few rows, partial_path)
 struct LayerIO {
   bool input_quantized = false;       // w.xa already holds layer 0's normed, quantized input

@@ -294,6 +294,110 @@ __global__ __launch_bounds__(NT) void k_attn_o_cp(const int8_t *__restrict__ wo,
   if (lane == 0) h[row] = hr + acc;
 }
 
+// The first step of a code-predictor context: its two rows (positions 0 and
+// 1: the talker's normed state and the embedding of code 0) in one launch,
+// with no cached positions to read. Per workgroup, wave w = kv head w: QK-norm
+// + RoPE of both rows' queries and keys, the K/V of both positions appended
+// (workgroup 0), the causal attention (row 0 attends to itself: its output is
+// v0; row 1 softmax over positions 0 and 1), then h[r][row] += Wo[row] .
+// attention of row r for the wave's Wo row. qkv: the two q/k/v rows, ldq
+// apart; rope: the (cos, sin) rows of positions 0 and 1.
+template <typename KV>
+__global__ __launch_bounds__(NT) void k_attn2_o_cp(const int8_t *__restrict__ wo,
+                                                   const float *__restrict__ qkv, int ldq,
+                                                   KV *__restrict__ kl, float *__restrict__ h,
+                                                   const float *__restrict__ qkn,
+                                                   const float2 *__restrict__ rope, int v_off) {
+  __shared__ float att[2][NQ];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int row = blockIdx.x * ROWS + w;
+  const _Float16 *wd = reinterpret_cast<const _Float16 *>(wo + (size_t)HID * NQ);
+  int4 wv[2];
+  float sc[2];
+#pragma unroll
+  for (int c = 0; c < 2; c++) {
+    wv[c] = *reinterpret_cast<const int4 *>(wo + (size_t)row * NQ + c * 1024 + lane * 16);
+    sc[c] = (float)wd[(size_t)row * NBO + c * 32 + (lane >> 1)];
+  }
+  const float hr0 = h[row], hr1 = h[HID + row];
+  float xq[2][GRP][2], xk[2][2], xv[2][2];
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    const float *x = qkv + (size_t)r * ldq;
+#pragma unroll
+    for (int j = 0; j < GRP; j++) {
+      xq[r][j][0] = x[(w * GRP + j) * HD + lane];
+      xq[r][j][1] = x[(w * GRP + j) * HD + lane + 64];
+    }
+    xk[r][0] = x[NQ + w * HD + lane];
+    xk[r][1] = x[NQ + w * HD + lane + 64];
+    xv[r][0] = x[NQ + KVH * HD + w * HD + lane];
+    xv[r][1] = x[NQ + KVH * HD + w * HD + lane + 64];
+  }
+  const float qn0 = qkn[lane], qn1 = qkn[lane + 64];
+  const float kn0 = qkn[HD + lane], kn1 = qkn[HD + lane + 64];
+  const float eps = qkn[2 * HD];
+  const float2 cs0 = rope[lane], cs1 = rope[HD / 2 + lane];
+  __builtin_amdgcn_sched_barrier(0);
+
+  // keys and values as the cache holds them
+  float k[2][2], v[2][2];
+  KV *kh = kl + (size_t)w * P * HD;
+  KV *vh = kl + v_off + (size_t)w * P * HD;
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    float x0 = xk[r][0], x1 = xk[r][1];
+    norm_rope(x0, x1, kn0, kn1, r ? cs1 : cs0, eps);
+    const KV k0 = (KV)x0, k1 = (KV)x1, v0 = (KV)xv[r][0], v1 = (KV)xv[r][1];
+    k[r][0] = (float)k0;
+    k[r][1] = (float)k1;
+    v[r][0] = (float)v0;
+    v[r][1] = (float)v1;
+    if (blockIdx.x == 0) {
+      kh[(size_t)r * HD + lane] = k0;
+      kh[(size_t)r * HD + lane + 64] = k1;
+      vh[(size_t)r * HD + lane] = v0;
+      vh[(size_t)r * HD + lane + 64] = v1;
+    }
+  }
+  const float scale = (float)(1.0 / sqrt((double)HD));
+#pragma unroll
+  for (int j = 0; j < GRP; j++) {
+    const int o = (w * GRP + j) * HD;
+    // row 0: softmax over its own position: the value itself
+    att[0][o + lane] = v[0][0];
+    att[0][o + lane + 64] = v[0][1];
+    // row 1: positions 0 and 1
+    float q0 = xq[1][j][0], q1 = xq[1][j][1];
+    norm_rope(q0, q1, qn0, qn1, cs1, eps);
+    const float s0 = wave_sum_dpp(fmaf(q0, k[0][0], q1 * k[0][1])) * scale;
+    const float s1 = wave_sum_dpp(fmaf(q0, k[1][0], q1 * k[1][1])) * scale;
+    const float mx = fmaxf(s0, s1);
+    const float e0 = __expf(s0 - mx), e1 = __expf(s1 - mx);
+    const float inv = 1.0f / (e0 + e1);
+    att[1][o + lane] = fmaf(e0, v[0][0], e1 * v[1][0]) * inv;
+    att[1][o + lane + 64] = fmaf(e0, v[0][1], e1 * v[1][1]) * inv;
+  }
+  __syncthreads();
+
+  // h[r][row] += Wo[row] . att[r]
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const float4 *xp = reinterpret_cast<const float4 *>(att[r] + c * 1024 + lane * 16);
+      float p0 = dot4(wv[c].x, xp[0], 0.f);
+      float p1 = dot4(wv[c].y, xp[1], 0.f);
+      p0 = dot4(wv[c].z, xp[2], p0);
+      p1 = dot4(wv[c].w, xp[3], p1);
+      acc = fmaf(sc[c], p0 + p1, acc);
+    }
+    acc = wave_sum_dpp(acc);
+    if (lane == 0) h[(size_t)r * HID + row] = (r ? hr1 : hr0) + acc;
+  }
+}
+
 }  // namespace
 
 bool cp_fused_supported(const q3h_stack_config &c) {
@@ -312,6 +416,19 @@ void launch_attn_o_cp(const Mat &wo, const float *qkv, void *k_layer, int v_off,
   else
     hipLaunchKernelGGL(k_attn_o_cp<float>, grid, block, 0, st, wo.q, qkv,
                        static_cast<float *>(k_layer), h, qkn, rope, pos, v_off);
+}
+
+void launch_attn2_o_cp(const Mat &wo, const float *qkv, int ldq, void *k_layer, int v_off,
+                       float *h, const float *qkn, const float *rope_rows, bool kv16,
+                       hipStream_t st) {
+  const dim3 grid(HID / ROWS), block(NT);
+  const float2 *rope = reinterpret_cast<const float2 *>(rope_rows);
+  if (kv16)
+    hipLaunchKernelGGL(k_attn2_o_cp<_Float16>, grid, block, 0, st, wo.q, qkv, ldq,
+                       static_cast<_Float16 *>(k_layer), h, qkn, rope, v_off);
+  else
+    hipLaunchKernelGGL(k_attn2_o_cp<float>, grid, block, 0, st, wo.q, qkv, ldq,
+                       static_cast<float *>(k_layer), h, qkn, rope, v_off);
 }
 
 }  // namespace q3h

@@ -442,8 +442,9 @@ void enqueue_step(q3h_frame *f, int positions, hipStream_t st) {
   else
     hipLaunchKernelGGL(k_choose_code0<false>, dim3(n), dim3(kArgBlock), 0, st, fd);
   // code predictor: 2 rows per stream, then one row per group
-  // one stream on the Qwen3-TTS shapes: steps 1.. run the fused single-row
-  // path (positions are fixed: step g adds position g + 1)
+  // one stream on the Qwen3-TTS shapes: step 0 runs the fused two-row path,
+  // steps 1.. the fused single-row path (positions are fixed: step g adds
+  // position g + 1)
   const bool fused = n == 1 && cp_fused_supported(cp->cfg) && f->cctx[0]->max_pos == 16;
   // greedy on that path: the argmax of head g and the next input row are taken
   // by the first product of forward g + 1 (one launch fewer per group)
@@ -466,7 +467,9 @@ void enqueue_step(q3h_frame *f, int positions, hipStream_t st) {
         hipLaunchKernelGGL(k_cp_next<false>, dim3(n), dim3(kArgBlock), 0, st, fd, g);
       continue;
     }
-    if (fused && g > 0) {
+    if (fused && g == 0) {
+      run_cp_fused_first(cp, f->cw, f->cctx[0], st);
+    } else if (fused) {
       const CodeSrc src{fd.cp_logits, fd.cp_vocab,
                         fd.pred_emb + (size_t)(g - 1) * fd.cp_vocab * H, fd.codes + g, fd.alive};
       run_cp_fused(cp, f->cw, f->cctx[0], g + 1, st, code_in_product ? &src : nullptr);

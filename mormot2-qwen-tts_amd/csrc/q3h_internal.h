@@ -209,6 +209,13 @@ void launch_attn_o_cp(const Mat &wo, const float *qkv, void *k_layer, int v_off,
                       const float *qkn, const float *rope_row, int pos, bool kv16,
                       hipStream_t st);
 
+// the same for the first step of a code-predictor context: its two rows at
+// positions 0 and 1 (qkv rows ldq apart, h rows [2][1024], rope_rows the
+// (cos, sin) rows of positions 0 and 1), no cached positions read
+void launch_attn2_o_cp(const Mat &wo, const float *qkv, int ldq, void *k_layer, int v_off,
+                       float *h, const float *qkn, const float *rope_rows, bool kv16,
+                       hipStream_t st);
+
 void launch_rmsnorm_rows(const float *x, int ldx, int M, int K, const float *w, float eps,
                          float *y, int ldy, hipStream_t st);
 
