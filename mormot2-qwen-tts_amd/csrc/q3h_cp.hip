@@ -23,6 +23,8 @@
 // [1024][2048] followed by their fp16 scales [1024][64].
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "q3h.h"
 #include "q3h_internal.h"
 #include "q3h_math.h"
@@ -82,7 +84,9 @@ __device__ __forceinline__ void cvt8(const u32x4 (&r)[2], float (&o)[8]) {
     for (int e = 0; e < 4; e++) o[4 * i + e] = __uint_as_float(r[i][e]);
 }
 
-template <typename KV>
+// NJ: cached positions per lane (4 NJ >= pos; slots past pos weigh exactly 0,
+// so any such NJ gives the same sums)
+template <typename KV, int NJ>
 __global__ __launch_bounds__(NT) void k_attn_o_cp(const int8_t *__restrict__ wo,
                                                   const float *__restrict__ qkv,
                                                   KV *__restrict__ kl, float *__restrict__ h,
@@ -90,7 +94,7 @@ __global__ __launch_bounds__(NT) void k_attn_o_cp(const int8_t *__restrict__ wo,
                                                   const float2 *__restrict__ rope, int pos,
                                                   int v_off) {
   constexpr int LW = sizeof(KV) / 2;  // 16-byte loads per 8 elements
-  constexpr int NJ = P / 4;           // positions per lane
+  static_assert(NJ >= 1 && 4 * NJ <= P, "positions per lane");
   __shared__ float att[NQ];
   __shared__ float qs[KVH][GRP][HD];
   __shared__ float kvs[KVH][2][HD];  // the new key and value of each kv head
@@ -410,12 +414,26 @@ void launch_attn_o_cp(const Mat &wo, const float *qkv, void *k_layer, int v_off,
                       hipStream_t st) {
   const dim3 grid(HID / ROWS), block(NT);
   const float2 *rope = reinterpret_cast<const float2 *>(rope_row);
-  if (kv16)
-    hipLaunchKernelGGL(k_attn_o_cp<_Float16>, grid, block, 0, st, wo.q, qkv,
-                       static_cast<_Float16 *>(k_layer), h, qkn, rope, pos, v_off);
-  else
-    hipLaunchKernelGGL(k_attn_o_cp<float>, grid, block, 0, st, wo.q, qkv,
-                       static_cast<float *>(k_layer), h, qkn, rope, pos, v_off);
+  // the cached positions 0 .. pos - 1 in 4 NJ lane slots (pos is fixed per
+  // code-predictor step, so each step's launch reads only what it attends to)
+  const int nj = std::min(std::max((pos + 3) / 4, 1), P / 4);
+#define Q3H_AOC(KV, NJ)                                                                     \
+  hipLaunchKernelGGL((k_attn_o_cp<KV, NJ>), grid, block, 0, st, wo.q, qkv,                  \
+                     static_cast<KV *>(k_layer), h, qkn, rope, pos, v_off)
+#define Q3H_AOC_NJ(KV) \
+  switch (nj) {        \
+    case 1: Q3H_AOC(KV, 1); break; \
+    case 2: Q3H_AOC(KV, 2); break; \
+    case 3: Q3H_AOC(KV, 3); break; \
+    default: Q3H_AOC(KV, 4); break; \
+  }
+  if (kv16) {
+    Q3H_AOC_NJ(_Float16)
+  } else {
+    Q3H_AOC_NJ(float)
+  }
+#undef Q3H_AOC_NJ
+#undef Q3H_AOC
 }
 
 void launch_attn2_o_cp(const Mat &wo, const float *qkv, int ldq, void *k_layer, int v_off,
