@@ -87,8 +87,9 @@ constexpr int kSampleThreads = 1024;
 constexpr int kSampleMaxNPT = 3;  // up to 3072 values
 
 struct SampleShared {
-  int hist[256];
+  int hist[2][256];  // the radix passes alternate between the two
   uint32_t prefix, remaining;
+  int exact;  // the selected bucket holds exactly the values still wanted
   float fred[kSampleThreads / 64];
   int cnt;
   uint32_t ck[64];
@@ -132,27 +133,36 @@ __device__ int block_sample(const float (&x)[NPT], int n, const SampleParams &p,
     key[j] = order_key(v[j]);
     kept[j] = in;
   }
-  // 2. top-k: the k-th largest key by a radix select, 8 bits per pass
+  // 2. top-k: the k-th largest key by a radix select, 8 bits per pass. A pass
+  // whose selected bucket holds exactly the values still wanted ends the
+  // select: every key of that bucket is kept, so the bucket's lowest key (the
+  // prefix with zero low bits) keeps the same set as the exact k-th key.
   const bool topk = p.top_k >= 1 && p.top_k < n;
   if (topk) {
     if (t == 0) {
       sh.prefix = 0;
       sh.remaining = (uint32_t)p.top_k;
+      sh.exact = 0;
     }
+    for (int b = t; b < 512; b += kSampleThreads) sh.hist[b >> 8][b & 255] = 0;
+    __syncthreads();
     for (int pass = 0; pass < 4; pass++) {
       const int shift = 24 - 8 * pass;
       const uint32_t hmask = pass == 0 ? 0u : (0xFFFFFFFFu << (shift + 8));
-      for (int b = t; b < 256; b += kSampleThreads) sh.hist[b] = 0;
-      __syncthreads();
+      int *hist = sh.hist[pass & 1];
       const uint32_t prefix = sh.prefix;
 #pragma unroll
       for (int j = 0; j < NPT; j++)
-        if (kept[j] && (key[j] & hmask) == prefix) atomicAdd(&sh.hist[(key[j] >> shift) & 255], 1);
+        if (kept[j] && (key[j] & hmask) == prefix) atomicAdd(&hist[(key[j] >> shift) & 255], 1);
       __syncthreads();
+      if (wave == 1) {  // the other buffer, for the next pass
+        int *nxt = sh.hist[(pass + 1) & 1];
+        for (int b = lane; b < 256; b += 64) nxt[b] = 0;
+      }
       if (wave == 0) {
         // lane l: buckets 4 l .. 4 l + 3 (larger buckets in larger lanes)
-        const int h[4] = {sh.hist[4 * lane], sh.hist[4 * lane + 1], sh.hist[4 * lane + 2],
-                          sh.hist[4 * lane + 3]};
+        const int h[4] = {hist[4 * lane], hist[4 * lane + 1], hist[4 * lane + 2],
+                          hist[4 * lane + 3]};
         const int mine = h[0] + h[1] + h[2] + h[3];
         int suf = mine;  // inclusive suffix sum over the lanes >= this one
         for (int off = 1; off < 64; off <<= 1) {
@@ -163,18 +173,22 @@ __device__ int block_sample(const float (&x)[NPT], int n, const SampleParams &p,
         const uint32_t rem = sh.remaining;
         if ((uint32_t)above < rem && rem <= (uint32_t)(above + mine)) {
           int acc = above, d = 4 * lane;
+          int hd = 0;
           for (int q = 3; q >= 0; q--) {
             if ((uint32_t)(acc + h[q]) >= rem) {
               d = 4 * lane + q;
+              hd = h[q];
               break;
             }
             acc += h[q];
           }
           sh.prefix = prefix | ((uint32_t)d << shift);
           sh.remaining = rem - (uint32_t)acc;
+          sh.exact = (uint32_t)hd == rem - (uint32_t)acc;
         }
       }
       __syncthreads();
+      if (sh.exact) break;  // uniform
     }
     const uint32_t tau = sh.prefix;
 #pragma unroll
