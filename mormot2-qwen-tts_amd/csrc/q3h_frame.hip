@@ -593,7 +593,8 @@ extern "C" int q3h_frame_create(q3h_stack *talker, q3h_stack *cp, const q3h_fram
     d.max_trailing = c.max_frames;
     d.logits = falloc<float>(f, (size_t)n * c.vocab);
     d.past = falloc<float>(f, (size_t)n * H);
-    d.codes = falloc<int>(f, (size_t)n * c.groups);
+    // codes [n][groups] then alive [n]: one download per step
+    d.codes = falloc<int>(f, (size_t)n * (c.groups + 1));
     d.seen = falloc<uint8_t>(f, (size_t)n * c.vocab);
     d.seeds = falloc<uint64_t>(f, n);
     d.sp0 = d.sp = SampleParams{0, 1.0f, 0, 1.0f};  // greedy until q3h_frame_set_sampling
@@ -601,7 +602,7 @@ extern "C" int q3h_frame_create(q3h_stack *talker, q3h_stack *cp, const q3h_fram
     f->sampling.top_p = f->sampling.sub_top_p = 1.0f;
     d.nframes = falloc<int>(f, n);
     d.step = falloc<int>(f, n);
-    d.alive = falloc<int>(f, n);
+    d.alive = d.codes + (size_t)n * c.groups;
     d.trailing = falloc<float>(f, (size_t)n * c.max_frames * H);
     d.trailing_rows = falloc<int>(f, n);
     d.codec_emb = f->codec_emb;
@@ -880,12 +881,10 @@ extern "C" int q3h_frame_step(q3h_frame *f, int32_t *codes, int32_t *alive) {
       enqueue_step(f, maxlen, f->stream);
       check_hip(hipGetLastError(), "frame kernels");
     }
-    check_hip(hipMemcpyAsync(f->pinned, f->fd.codes, sizeof(int32_t) * n * c.groups,
+    // the codes and, right after them, the alive flags
+    check_hip(hipMemcpyAsync(f->pinned, f->fd.codes, sizeof(int32_t) * n * (c.groups + 1),
                              hipMemcpyDeviceToHost, f->stream),
               "download codes");
-    check_hip(hipMemcpyAsync(f->pinned + n * c.groups, f->fd.alive, sizeof(int32_t) * n,
-                             hipMemcpyDeviceToHost, f->stream),
-              "download alive");
     check_hip(hipStreamSynchronize(f->stream), "frame step sync");
     for (int s = 0; s < n; s++) {
       const bool live = f->started[s] && f->pinned[n * c.groups + s] != 0;
