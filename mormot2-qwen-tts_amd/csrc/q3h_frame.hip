@@ -294,10 +294,12 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
 }
 
 // the next talker input: codec_emb[code 0] + sum_g pred_emb[g-1][code g] +
-// (trailing[step] or tts_pad), summed in that order.
+// (trailing[step] or tts_pad), summed in that order; and its row descriptor.
 __global__ void k_talker_input(FrameDev f) {
   const int s = blockIdx.y;
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  // the row's descriptor: position = the context length (inactive: -1)
+  if (c == 0) f.t_rd[s] = row_desc(f.t_ctx[s], f.alive[s] ? f.t_ctx[s]->len : -1);
   if (c >= f.H || !f.alive[s]) return;
   const int *codes = f.codes + (size_t)s * f.groups;
   float x = f.codec_emb[(size_t)codes[0] * f.H + c];
@@ -358,16 +360,14 @@ __global__ __launch_bounds__(256) void k_start_rows(const int2 *__restrict__ pla
   for (int c = threadIdx.x; c < H; c += 256) dst[c] = add ? src[c] + add[c] : src[c];
 }
 
-// the end of a step: the frame count of every running stream; the int8 path
-// also advances the talker length here (as launch_advance does otherwise)
+// the end of a step: the frame count and the talker context length of every
+// running stream
 __global__ void k_frame_end(FrameDev f) {
   const int s = blockIdx.x * blockDim.x + threadIdx.x;
   if (s < f.n && f.alive[s]) {
     f.step[s] += 1;
-    if (f.t_xq) {
-      CtxDev *c = f.t_ctx[s];
-      c->len = min(c->len + 1, c->max_pos);
-    }
+    CtxDev *c = f.t_ctx[s];  // the talker context took the step's row
+    c->len = min(c->len + 1, c->max_pos);
   }
 }
 
@@ -497,7 +497,6 @@ void enqueue_step(q3h_frame *f, int positions, hipStream_t st) {
     run_layers(tk, f->tw, n, positions, true, st, io);
   } else {
     hipLaunchKernelGGL(k_talker_input, dim3((H + 255) / 256, n), dim3(256), 0, st, fd);
-    launch_prep(f->t_arr, fd.alive, n, 1, f->tw.rd, st);
     run_layers(tk, f->tw, n, positions, true, st);
   }
   const Mat &th = tk->heads[c.talker_head];
@@ -508,7 +507,6 @@ void enqueue_step(q3h_frame *f, int positions, hipStream_t st) {
     launch_rmsnorm_rows(f->tw.h, H, n, H, tk->final_norm, tk->cfg.rms_eps, fd.past, H, st);
     linear(tk, f->tw, th, fd.past, H, n, nullptr, fd.logits, c.vocab, EPI_STORE, nullptr, st);
   }
-  if (!tq) launch_advance(f->t_arr, fd.alive, n, 1, st);
   hipLaunchKernelGGL(k_frame_end, dim3((n + 63) / 64), dim3(64), 0, st, fd);
 }
 
