@@ -79,6 +79,33 @@ def test_frame_b1_cp_ties_take_the_first_index(device, synth, monkeypatch):
         m.destroy()
 
 
+def test_frame_b1_half_float_kv(device, synth):
+    """Half-float K/V caches (the reference's KvF16) on the batch-1 frame:
+    the fused code-predictor kernels on f16 caches (the two-row first step and
+    the single-row steps) and the talker's f16 attention, against the oracle
+    with the same cache rounding."""
+    m = Model(device, seed=29, talker_layers=2, cp_layers=2, kv_f16=1, max_positions=128)
+    fr = m.frame(n_streams=1, max_positions=128)
+    of = m.oracle_frame(max_positions=128)
+    try:
+        pre = synth.prompt(29, 24)
+        fr.start(0, pre)
+        of.start(pre)
+        for i in range(6):
+            codes, alive = fr.step()
+            ref = of.next()
+            lg, _ = fr.state(0)
+            olg, _ = of.state()
+            print(f"frame {i}: rel {rel(lg, olg):.2e}", flush=True)
+            assert alive[0] == 1
+            assert np.array_equal(codes[0], ref), (i, codes[0], ref)
+            assert rel(lg, olg) < 1e-3
+    finally:
+        fr.destroy()
+        of.destroy()
+        m.destroy()
+
+
 def test_frame_graph_equals_eager(full, synth):
     m = full
     pre = synth.prompt(9, 20)
