@@ -153,19 +153,70 @@ def run_gpu(frame, pre, steps, warmup):
     return total, lat, np.stack(codes)
 
 
+def cpu_info():
+    """The host CPU as /proc/cpuinfo names it, and the vector ISA the oracle
+    is built for (-march=x86-64-v3: AVX2, FMA, F16C) with the wider
+    extensions the CPU also has."""
+    model, flags = "unknown", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and model == "unknown":
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags") and not flags:
+                    flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    extra = [x for x in ("avx512f", "avx512_vnni", "avx512_bf16", "amx_tile") if x in flags]
+    return dict(cpu_model=model, isa="x86-64-v3 (AVX2, FMA, F16C) build" +
+                (f"; the CPU also has {', '.join(extra)}" if extra else ""))
+
+
+def cpu_thread_counts():
+    """The host cores this job may use (at most 16: one GPU's share of the
+    box) and the reference's default worker count for them,
+    (2 nproc + 2) / 3 (mormot.ai.tts.qwen.talker.pas:316-317)."""
+    share = min(16, len(os.sched_getaffinity(0)))
+    return sorted({max(1, (2 * share + 2) // 3), share})
+
+
 def cpu_baseline(f32, tables, pre, gpu_codes, budget_s, max_frames, act_q8, f32w=False):
     """The oracle's frame step on the host cores (same weights, same prompt of
     stream 0, same weight and activation modes), frames timed until budget_s
-    is spent."""
+    is spent, at each of cpu_thread_counts(); value: the faster."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import q3o  # the checker's restatement, timed as the CPU baseline
 
-    threads = min(16, len(os.sched_getaffinity(0)))
-    q3o.set_threads(threads)
-    q = q3o.quantize_q8_0
+    q3o.set_threads(max(cpu_thread_counts()))
+    ot, oc, frame = oracle_model(q3o, f32, tables, act_q8, f32w,
+                                 pre[0].shape[0] + max_frames + 8)
+    sweep = [cpu_frames(q3o, frame, pre, gpu_codes, budget_s, max_frames, threads)
+             for threads in cpu_thread_counts()]
+    ot.destroy()
+    oc.destroy()
+    best = max(sweep, key=lambda r: r["value"])
+    n = max(r["frames"] for r in sweep)
+    equal = all(r["codes_equal"] for r in sweep)
+    act = "int8 activations" if act_q8 else "f32 activations"
+    wts = "f32 weights" if f32w else "Q8_0 weights"
+    out = dict(value=round(best["value"], 3), unit="frames/s", cores=best["threads"],
+               kind="port",
+               sample=f"frame step of stream 0, {wts}, {act} (oracle, C + OpenMP), "
+                      f"{pre[0].shape[0]} prompt rows (prefill untimed), the first frames for "
+                      f"about {budget_s:.0f} s at each thread count",
+               threads_sweep=[dict(threads=r["threads"], frames_per_s=round(r["value"], 3),
+                                   frames=r["frames"], seconds=round(r["seconds"], 2))
+                              for r in sweep],
+               thread_counts="(2 nproc + 2) / 3 (talker.pas:316-317) and nproc, nproc = "
+                             "min(16, host cores available)")
+    out.update(cpu_info())
+    return out, n, equal
 
-    if f32w:
-        q = lambda v: v  # noqa: E731
+
+def oracle_model(q3o, f32, tables, act_q8, f32w, max_positions):
+    """The oracle's stacks and a frame factory over the same weights (Q8_0
+    blocks from the same quantizer as the device's, or f32)."""
+    q = (lambda v: v) if f32w else q3o.quantize_q8_0
 
     def qlayers(layers):
         return [{k: (q(v) if k.startswith("w") else v) for k, v in L.items()} for L in layers]
@@ -173,9 +224,19 @@ def cpu_baseline(f32, tables, pre, gpu_codes, budget_s, max_frames, act_q8, f32w
     wt = q3o.F32 if f32w else q3o.Q8_0
     ot = q3o.Stack(synth.TALKER, qlayers(f32["tl"]), f32["tf"], wt, act_q8=act_q8)
     oc = q3o.Stack(synth.PREDICTOR, qlayers(f32["cl"]), f32["cf"], wt, act_q8=act_q8)
-    fr = q3o.Frame(ot, oc, q(f32["th"]), [q(h) for h in f32["ch"]], tables["codec_emb"],
-                   tables["pred_emb"], tables["tts_pad"],
-                   max_positions=pre[0].shape[0] + max_frames + 8)
+    th, ch = q(f32["th"]), [q(h) for h in f32["ch"]]
+
+    def frame():
+        return q3o.Frame(ot, oc, th, ch, tables["codec_emb"], tables["pred_emb"],
+                         tables["tts_pad"], max_positions=max_positions)
+    return ot, oc, frame
+
+
+def cpu_frames(q3o, frame, pre, gpu_codes, budget_s, max_frames, threads):
+    """Frames of stream 0 on `threads` host threads until budget_s is spent
+    (at least 2), and whether their codes equal the GPU's."""
+    q3o.set_threads(threads)
+    fr = frame()
     fr.start(pre[0])
     n = 0
     equal = True
@@ -185,14 +246,9 @@ def cpu_baseline(f32, tables, pre, gpu_codes, budget_s, max_frames, act_q8, f32w
         equal = equal and n < len(gpu_codes) and np.array_equal(c, gpu_codes[n][0])
         n += 1
     dt = time.perf_counter() - t0
-    for o in (fr, ot, oc):
-        o.destroy()
-    act = "int8 activations" if act_q8 else "f32 activations"
-    wts = "f32 weights" if f32w else "Q8_0 weights"
-    return dict(value=n / dt, unit="frames/s", cores=threads, kind="port",
-                sample=f"frame step of stream 0, {wts}, {act} (oracle, C + OpenMP), "
-                       f"{pre[0].shape[0]} prompt rows (prefill untimed), first {n} frames, "
-                       f"{dt:.1f} s"), n, equal
+    fr.destroy()
+    log(f"cpu baseline: {n / dt:.2f} frames/s on {threads} threads ({n} frames)")
+    return dict(value=n / dt, threads=threads, frames=n, seconds=dt, codes_equal=equal)
 
 
 def gemv_roofline(ts, args):
@@ -213,6 +269,126 @@ def gemv_roofline(ts, args):
                 kernel="k_gemv_q8v (Q8_0 matrix-vector products of one talker decode step)",
                 bytes_per_launch=int(per_launch), us_per_launch=round(us, 3),
                 graph_wall_us_per_launch=None if wall is None else round(wall, 3))
+
+
+# algorithmic weight bytes of one frame step: talker layers + head, and 15
+# code-predictor forwards each with its head (Q8_0, 34 bytes per 32 weights)
+FRAME_WEIGHT_BYTES = 1759083520
+KV_BYTES_PER_POSITION = {"f32": 229376, "f16": 114688}  # talker, 28 layers
+B32_STREAMS, B32_FRAMES = 32, 128
+CONFIG2_FRAMES = 156
+
+
+def batched_b32(dev, f32, tables, args):
+    """Batched serving (32 streams, prompt lengths uniform in [16, 256]
+    seeded, 128 frames, Q8_0 weights, activations quantized per 32-block so
+    the products run on the int8 matrix cores): whole-job frames/s with the
+    codes of all streams in host memory after each step, and the algorithmic
+    HBM bytes of a step (the weights once, the talker K/V of every stream at
+    its context length; the code predictor's K/V is under 1 % and left out)
+    over the step time."""
+    n, steps, warmup = B32_STREAMS, B32_FRAMES, 3
+    pre = prompts(args.seed, "frame_b32", n)
+    lens = np.array([p.shape[0] for p in pre])
+    max_pos = int(lens.max()) + steps + warmup + 8
+    kv = "f16" if args.kv16 else "f32"
+    t0 = time.time()
+    ts = q3h.Stack(dev, dict(synth.TALKER, dtype=q3h.Q8_0, kv_f16=int(args.kv16), act_q8=1,
+                             max_positions=max_pos), f32["tl"], f32["tf"], q3h.F32)
+    cs = q3h.Stack(dev, dict(synth.PREDICTOR, dtype=q3h.Q8_0, kv_f16=int(args.kv16), act_q8=1,
+                             max_positions=16), f32["cl"], f32["cf"], q3h.F32)
+    ts.add_head(f32["th"], q3h.F32)
+    for h in f32["ch"]:
+        cs.add_head(h, q3h.F32)
+    frame = q3h.Frame(ts, cs, tables["codec_emb"], tables["pred_emb"], tables["tts_pad"],
+                      n_streams=n, max_positions=max_pos, max_frames=steps + warmup + 8,
+                      use_graph=not args.no_graph)
+    log(f"batched b32: int8 stacks on the device in {time.time() - t0:.1f} s")
+    total, lat, codes = run_gpu(frame, pre, steps, warmup)
+    fps = n * steps / total
+    # positions read per step, averaged over the steps (the row's own included)
+    positions = float(np.mean([np.sum(lens + i + 1) for i in range(steps)]))
+    step_bytes = FRAME_WEIGHT_BYTES + KV_BYTES_PER_POSITION[kv] * positions
+    gbs = step_bytes / (total / steps) / 1e9
+    out = dict(frames_per_s=round(fps, 2), streams=n, frames=steps,
+               ms_per_step=round(1e3 * total / steps, 4),
+               step_us_p50=round(1e6 * float(np.median(lat)), 1),
+               step_us_p99=round(1e6 * float(np.percentile(lat, 99)), 1),
+               prefill_ms=round(1e3 * run_gpu.prefill_s, 2),
+               prompt_rows="U[16,256] (seeded)", activations="q8_0 (int8 MFMA)", kv=kv,
+               hbm_bytes_per_step=int(step_bytes), hbm_gbs=round(gbs, 1),
+               hbm_frac=round(gbs / HBM_PEAK_GBS, 4))
+    log(f"batched b32: {fps:.1f} frames/s, {1e3 * total / steps:.3f} ms per step, "
+        f"{gbs:.0f} GB/s algorithmic")
+    frame.destroy()
+    ts.destroy()
+    cs.destroy()
+    if not args.no_cpu:
+        cpu, nf, equal = cpu_baseline(f32, tables, pre, codes, args.cpu_seconds / 2, steps, 1)
+        out["cpu_baseline"] = cpu
+        out["parity"] = dict(frames=nf, codes_equal_stream0=bool(equal))
+    return out
+
+
+def talker_decode_b1(dev, ts, f32, tables, seed, args, steps=64, rows=PROMPT_ROWS):
+    """Talker-only greedy decode at batch 1 (Q8_0 weights, f32 K/V): a
+    48-row prefill of N(0, 1) rows, then 64 steps whose input is the codec
+    embedding of the argmax of the 3072-code head (q3h_forward_embeds per
+    step: host row in, logits out, so the rate includes PCIe)."""
+    ctx = q3h.Context(ts, rows + steps + 8)
+    codec = tables["codec_emb"]
+    pre = synth.prompt(seed + 9, rows)
+    codes = []
+    lg, _ = ctx.forward(pre, head=0, want_normed=False)
+    lat = np.empty(steps)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        a = time.perf_counter()
+        c = int(np.argmax(lg))
+        codes.append(c)
+        lg, _ = ctx.forward(codec[c][None], head=0, want_normed=False)
+        lat[i] = time.perf_counter() - a
+    total = time.perf_counter() - t0
+    ctx.destroy()
+    out = dict(steps=steps, prompt_rows=rows, steps_per_s=round(steps / total, 1),
+               step_us_p50=round(1e6 * float(np.median(lat)), 1),
+               step_us_p99=round(1e6 * float(np.percentile(lat, 99)), 1),
+               note="host row in and 3072 logits out per step (PCIe-inclusive)")
+    log(f"talker decode b1: {steps / total:.0f} steps/s, p50 {1e6 * np.median(lat):.0f} us")
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import q3o  # the checker's restatement, timed as the CPU baseline
+        q = q3o.quantize_q8_0
+        ot = q3o.Stack(synth.TALKER, [{k: (q(v) if k.startswith("w") else v)
+                                       for k, v in L.items()} for L in f32["tl"]],
+                       f32["tf"], q3o.Q8_0)
+        th = q(f32["th"])
+        sweep, equal, n_max = [], True, 0
+        for threads in cpu_thread_counts():
+            q3o.set_threads(threads)
+            oc = q3o.Ctx(ot, rows + steps + 8)
+            st = oc.forward(pre)
+            n = 0
+            t0 = time.perf_counter()
+            while n < steps and (n < 2 or time.perf_counter() - t0 < args.cpu_seconds / 4):
+                c = int(np.argmax(ot.head(th, st)))
+                equal = equal and c == codes[n]
+                st = oc.forward(codec[c][None])
+                n += 1
+            dt = time.perf_counter() - t0
+            oc.destroy()
+            n_max = max(n_max, n)
+            sweep.append(dict(threads=threads, steps_per_s=round(n / dt, 3), steps=n))
+            log(f"talker decode on the CPU: {n / dt:.2f} steps/s on {threads} threads")
+        ot.destroy()
+        best = max(sweep, key=lambda r: r["steps_per_s"])
+        out["cpu_baseline"] = dict(value=best["steps_per_s"], unit="steps/s",
+                                   cores=best["threads"], kind="port",
+                                   sample=f"the first steps of the same decode (oracle, C + "
+                                          f"OpenMP), about {args.cpu_seconds / 4:.0f} s per "
+                                          "thread count", threads_sweep=sweep, **cpu_info())
+        out["parity"] = dict(steps=n_max, codes_equal=bool(equal))
+    return out
 
 
 LONG_LENGTHS = (2048, 4096, 8192)
@@ -433,7 +609,8 @@ def main():
     ap.add_argument("--workload", choices=["frame_b1", "frame_b32", "f32_b8"], default="frame_b1")
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--gemv-iters", type=int, default=50)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+                    help="seconds of oracle frames per thread count (CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the kernels directly instead of replaying hipGraphs "
@@ -445,6 +622,10 @@ def main():
     ap.add_argument("--kv16", action="store_true",
                     help="K/V caches in half floats (the reference's KvF16 option, lm.pas:353); "
                          "the default is its f32 cache")
+    ap.add_argument("--no-b32", action="store_true",
+                    help="skip the 32-stream int8 sub-record of the default run")
+    ap.add_argument("--no-talker", action="store_true",
+                    help="skip the talker-only decode sub-record of the default run")
     ap.add_argument("--no-codec", action="store_true",
                     help="skip the decoder back-part measurement (frame_b1)")
     ap.add_argument("--codec-only", action="store_true",
@@ -493,7 +674,7 @@ def main():
         raise RuntimeError("no gfx950 device")
     pre = prompts(args.seed, args.workload, n)
     maxlen = max(p.shape[0] for p in pre)
-    max_pos = maxlen + max(steps, warmup) + 8
+    max_pos = maxlen + max(steps, warmup, CONFIG2_FRAMES if b1 else 0) + 8
     dev = q3h.Device(0)
     act_q8 = 0 if (b1 or f32w) else 1
     ts, cs, tables, f32 = build_model(dev, args.seed, max_pos, act_q8,
@@ -506,7 +687,8 @@ def main():
         dev.close()
         return 0
     frame = q3h.Frame(ts, cs, tables["codec_emb"], tables["pred_emb"], tables["tts_pad"],
-                      n_streams=n, max_positions=max_pos, max_frames=max(steps, warmup) + 8,
+                      n_streams=n, max_positions=max_pos,
+                      max_frames=max(steps, warmup, CONFIG2_FRAMES) + 8,
                       use_graph=not args.no_graph)
     log(f"{args.workload}: {n} stream(s), warm-up {warmup}, timing {steps} steps")
     total, lat, codes = run_gpu(frame, pre, steps, warmup)
@@ -515,6 +697,15 @@ def main():
     log(f"{fps:.1f} frames/s, {1e3 * total / steps:.3f} ms per step "
         f"(p50 {1e6 * np.median(lat):.0f} us, p99 {1e6 * np.percentile(lat, 99):.0f} us); "
         f"prefill of {n} stream(s) {1e3 * prefill_s:.1f} ms")
+
+    full = None
+    if b1 and steps != CONFIG2_FRAMES:
+        # the whole sentence of the configuration (context 48 -> 204)
+        f_total, f_lat, _ = run_gpu(frame, pre, CONFIG2_FRAMES, 0)
+        full = dict(frames=CONFIG2_FRAMES, frames_per_s=round(CONFIG2_FRAMES / f_total, 2),
+                    ms_per_step=round(1e3 * f_total / CONFIG2_FRAMES, 4),
+                    step_us_p50=round(1e6 * float(np.median(f_lat)), 1))
+        log(f"{CONFIG2_FRAMES} frames: {full['frames_per_s']:.1f} frames/s")
 
     roofline = gemv_roofline(ts, args) if not (f32w or args.no_roofline) else None
 
@@ -530,6 +721,9 @@ def main():
     log(f"sampled: {sampled['frames_per_s']:.1f} frames/s, {sampled['ms_per_step']:.3f} ms per step")
 
     frame.destroy()
+    talker_b1 = talker_decode_b1(dev, ts, f32, tables, args.seed, args) \
+        if (b1 and not args.no_talker) else None
+    b32 = batched_b32(dev, f32, tables, args) if (b1 and not args.no_b32) else None
     load = load_from_bf16(dev, f32, act_q8) if b1 else None
     text_start = None
     if b1 and not args.no_text:
@@ -580,6 +774,9 @@ def main():
         "prefill_ms": round(1e3 * prefill_s, 2),
         "step_us_p50": round(1e6 * float(np.median(lat)), 1),
         "step_us_p99": round(1e6 * float(np.percentile(lat, 99)), 1),
+        "frame_b1_156_frames": full,
+        "batched_b32": b32,
+        "talker_decode_b1": talker_b1,
         "roofline": roofline,
         "cpu_baseline": cpu,
         "parity": parity,

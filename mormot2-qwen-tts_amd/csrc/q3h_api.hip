@@ -1165,9 +1165,7 @@ extern "C" int q3h_stack_time_gemv(q3h_stack *s, int head, int iters, int mode,
       ms = (float)total;
     } else {
       if (mode == 1) {
-        check_hip(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "capture");
-        enqueue(false);
-        check_hip(hipStreamEndCapture(st, &graph), "end capture");
+        graph = capture_graph(st, [&] { enqueue(false); });
         check_hip(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "instantiate");
       }
       auto once = [&] {

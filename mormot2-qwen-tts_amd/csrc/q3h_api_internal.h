@@ -51,6 +51,26 @@ int guard(F &&f) {
   }
 }
 
+// Captures what enqueue() launches on stream st into a new graph. When
+// enqueue throws, the capture is ended and its partial graph destroyed before
+// the error goes on, so the stream leaves capture mode and later calls work.
+template <class F>
+hipGraph_t capture_graph(hipStream_t st, F &&enqueue) {
+  check_hip(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+  try {
+    enqueue();
+  } catch (...) {
+    hipGraph_t partial = nullptr;
+    (void)hipStreamEndCapture(st, &partial);
+    if (partial) (void)hipGraphDestroy(partial);
+    (void)hipGetLastError();
+    throw;
+  }
+  hipGraph_t g = nullptr;
+  check_hip(hipStreamEndCapture(st, &g), "hipStreamEndCapture");
+  return g;
+}
+
 struct Layer {
   Mat qkv;   // [q; k; v] rows
   Mat o;     // [hidden][heads * head_dim]

@@ -572,10 +572,7 @@ void pass(q3h_codec *c, int F) {
 void run_pass(q3h_codec *c, int F) {
   hipGraphExec_t &e = c->exec[F];
   if (!e) {
-    hipGraph_t g = nullptr;
-    check_hip(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "capture");
-    pass(c, F);
-    check_hip(hipStreamEndCapture(c->stream, &g), "end capture");
+    hipGraph_t g = capture_graph(c->stream, [&] { pass(c, F); });
     const hipError_t r = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
     check_hip(r, "instantiate");

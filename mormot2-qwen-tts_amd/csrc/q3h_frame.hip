@@ -136,7 +136,7 @@ __global__ __launch_bounds__(kArgBlock) void k_choose_code0(FrameDev f) {
       float bv = -INFINITY;
       int bi = 0x7fffffff;
       for (int i = tid; i < f.vocab; i += kArgBlock) argmax_merge(bv, bi, score(i), i);
-      code = block_argmax(bv, bi);
+      code = first_max_code(block_argmax(bv, bi), score(0));
     }
     int *codes = f.codes + (size_t)s * f.groups;
     if (code == f.eos) {
@@ -210,8 +210,7 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_argmax(const float *__restrict
   float bv = -INFINITY;
   int bi = 0x7fffffff;
   for (int i = tid; i < cp_vocab; i += kArgBlock) argmax_merge(bv, bi, lg[i], i);
-  // (no maximum only when every logit is NaN: row cp_vocab - 1 of the table)
-  const int code = min(block_argmax(bv, bi), cp_vocab - 1);
+  const int code = first_max_code(block_argmax(bv, bi), lg[0]);
   if (tid == 0) codes[(size_t)s * groups + g + 1] = code;
   if (g + 1 < groups - 1) {
     const float *emb = pred_emb + ((size_t)g * cp_vocab + code) * H;
@@ -281,7 +280,7 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
     float bv = -INFINITY;
     int bi = 0x7fffffff;
     for (int i = tid; i < f.cp_vocab; i += kArgBlock) argmax_merge(bv, bi, logit(i), i);
-    code = block_argmax(bv, bi);
+    code = first_max_code(block_argmax(bv, bi), logit(0));
   }
   if (tid == 0) f.codes[(size_t)s * f.groups + g + 1] = code;
   if (next) {
@@ -866,10 +865,7 @@ extern "C" int q3h_frame_step(q3h_frame *f, int32_t *codes, int32_t *alive) {
         // the capture leave their extra splits empty)
         const int cap = maxlen <= 256 ? 256 : ((maxlen + 255) / 256 + 1) * 256;
         const int cap_positions = std::min(c.max_positions, cap);
-        check_hip(hipStreamBeginCapture(f->stream, hipStreamCaptureModeThreadLocal),
-                  "hipStreamBeginCapture");
-        enqueue_step(f, cap_positions, f->stream);
-        check_hip(hipStreamEndCapture(f->stream, &f->graph), "hipStreamEndCapture");
+        f->graph = capture_graph(f->stream, [&] { enqueue_step(f, cap_positions, f->stream); });
         check_hip(hipGraphInstantiate(&f->exec, f->graph, nullptr, nullptr, 0),
                   "hipGraphInstantiate");
         f->graph_positions = cap_positions;

@@ -364,8 +364,9 @@ __global__ __launch_bounds__(W * 64) void k_gemv_q8v_code(
     const int i2 = __shfl_xor(bi, off, 64);
     argmax_merge(bv, bi, v2, i2);
   }
-  // (no maximum only when every logit is NaN: row vocab - 1, not an index past the table)
-  const int code = min(__builtin_amdgcn_readfirstlane(bi), V4 * 256 - 1);
+  const int code = first_max_code(__builtin_amdgcn_readfirstlane(bi),
+                                  __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(
+                                                                __builtin_bit_cast(int, lg[0].x))));
   const float *x = rows + (size_t)code * K;
   float4 xv[C][4];
 #pragma unroll

@@ -28,7 +28,11 @@
 //     the walk: the first segment s with r + B_s > target (r the sum of the
 //     segments before, accumulated in order), in it the first thread, in it
 //     the first index; when a level finds none (rounding at the top end), the
-//     last index with w > 0 in the range of that level.
+//     last index with w > 0 in the range of that level;
+//  6. when that finds no index either (every w is 0 or NaN, which only NaN or
+//     infinite scores cause), the greedy code of x: its first maximum, NaN
+//     never winning, 0 when x[0] is NaN or nothing is a maximum
+//     (first_max_code), so the result is always an index of the table.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -36,6 +40,7 @@
 #include <cstdint>
 
 #include "q3h_math.h"
+#include "q3h_wave.h"
 
 namespace q3h {
 
@@ -101,6 +106,7 @@ struct SampleShared {
   float B[64];
   float W[kSampleThreads * kSampleMaxNPT];
   int pick;
+  int fidx[kSampleThreads / 64];
 };
 
 // the last index in [lo, hi) with W > 0 (-1: none), over one wave
@@ -331,7 +337,32 @@ __device__ int block_sample(const float (&x)[NPT], int n, const SampleParams &p,
     if (lane == 0) sh.pick = pick;
   }
   __syncthreads();
-  const int code = sh.pick;
+  int code = sh.pick;
+  if (code < 0) {
+    // 6. no code drawn (every weight 0 or NaN: NaN or infinite scores): the
+    // greedy choice over x, first_max_code's rule (uniform branch)
+    float bv = -__builtin_inff();
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < NPT; j++)
+      if (base + j < n) argmax_merge(bv, bi, x[j], base + j);
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float v2 = __shfl_xor(bv, off, 64);
+      const int i2 = __shfl_xor(bi, off, 64);
+      argmax_merge(bv, bi, v2, i2);
+    }
+    __syncthreads();
+    if (lane == 0) {
+      sh.fred[wave] = bv;
+      sh.fidx[wave] = bi;
+    }
+    if (t == 0) sh.cv[0] = x[0];  // thread 0 holds index 0
+    __syncthreads();
+    bv = sh.fred[0];
+    bi = sh.fidx[0];
+    for (int q = 1; q < kSampleThreads / 64; q++) argmax_merge(bv, bi, sh.fred[q], sh.fidx[q]);
+    code = first_max_code(bi, sh.cv[0]);
+  }
   __syncthreads();  // the shared state is reused by the next call
   return code;
 }

@@ -106,4 +106,13 @@ __device__ __forceinline__ void argmax_merge(float &v, int &i, float v2, int i2)
   }
 }
 
+// The code of a first-max argmax as tests/test.tts.qwen.lm.pas:109-117 runs
+// it (result 0, moved to i only when p[i] > p[result]), from the reduction of
+// argmax_merge over every (p[i], i) starting at (-inf, 0x7fffffff): a NaN
+// never wins, a NaN p[0] keeps 0 (nothing compares greater), and no maximum
+// at all (every value NaN) is 0 as well. Always an index of the table.
+__device__ __forceinline__ int first_max_code(int bi, float p0) {
+  return (bi == 0x7fffffff || p0 != p0) ? 0 : bi;
+}
+
 }  // namespace q3h

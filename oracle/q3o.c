@@ -212,14 +212,16 @@ static inline int32_t idot32(const int8_t *a, const int8_t *b) {
   return s;
 }
 
-/* Y[m][n] (+)= W[n] . X[m]; W [N][K] f32 or Q8_0 blocks; X [M][K] */
-static void linear(const void *W, int dtype, int act_q8, int N, int K,
-                   const float *X, int M, float *Y, int ldy, int add) {
+/* Y[m][n] (+)= W[n] . X[m]; W [N][K] f32 or Q8_0 blocks; X [M][K]; the
+ * quantized activations (act_q8) also to xq_out [M][K / 32] when non-null */
+static void linear_q(const void *W, int dtype, int act_q8, int N, int K,
+                     const float *X, int M, float *Y, int ldy, int add, void *xq_out) {
   const int nb = K / 32;
   q3o_block_q8_0 *xq = NULL;
   if (dtype == Q3O_Q8_0 && act_q8) {
     xq = (q3o_block_q8_0 *)malloc(sizeof(q3o_block_q8_0) * (size_t)nb * M);
     for (int m = 0; m < M; m++) q3o_quantize_row_q8_0(X + (size_t)m * K, xq + (size_t)m * nb, K);
+    if (xq_out) memcpy(xq_out, xq, sizeof(q3o_block_q8_0) * (size_t)nb * M);
   }
 #pragma omp parallel
   {
@@ -274,6 +276,11 @@ static void linear(const void *W, int dtype, int act_q8, int N, int K,
     free(scale);
   }
   free(xq);
+}
+
+static void linear(const void *W, int dtype, int act_q8, int N, int K,
+                   const float *X, int M, float *Y, int ldy, int add) {
+  linear_q(W, dtype, act_q8, N, K, X, M, Y, ldy, add, NULL);
 }
 
 /* ------------------------------------------------------------------ */
@@ -383,7 +390,23 @@ int q3o_ctx_fill(q3o_ctx *c, const float *k, const float *v, int len) {
 
 int q3o_forward_embeds(q3o_ctx *c, const float *x, int rows, float *normed_last,
                        float *layer_out) {
+  return q3o_forward_embeds_traced(c, x, rows, normed_last, layer_out, NULL);
+}
+
+/* the trace slot of layer l for a tensor of n values (or blocks) per row */
+#define TRACE_F(ptr, l, n) ((ptr) ? (ptr) + ((size_t)(l) * rows) * (size_t)(n) : NULL)
+#define TRACE_B(ptr, l, n) \
+  ((ptr) ? (void *)((q3o_block_q8_0 *)(ptr) + ((size_t)(l) * rows) * (size_t)(n)) : NULL)
+
+static void trace_copy(float *dst, const float *src, size_t n) {
+  if (dst) memcpy(dst, src, sizeof(float) * n);
+}
+
+int q3o_forward_embeds_traced(q3o_ctx *c, const float *x, int rows, float *normed_last,
+                              float *layer_out, const q3o_trace *t) {
   const q3o_config *q = &c->s->cfg;
+  const q3o_trace none = {0};
+  if (!t) t = &none;
   if (rows <= 0) return 0;
   if (c->len + rows > c->max_pos) return -1;
   const int H = q->hidden, D = q->head_dim, NQ = q->heads * D, NKV = q->kv_heads * D;
@@ -397,13 +420,23 @@ int q3o_forward_embeds(q3o_ctx *c, const float *x, int rows, float *normed_last,
   float *att = (float *)malloc(sizeof(float) * rows * NQ);
   float *gb = (float *)malloc(sizeof(float) * rows * I);
   float *ub = (float *)malloc(sizeof(float) * rows * I);
+  float *pb = (float *)malloc(sizeof(float) * rows * H);
+  const int NQKV = NQ + 2 * NKV;
   memcpy(h, x, sizeof(float) * rows * H);
   for (int l = 0; l < q->layers; l++) {
     const q3o_layer *L = &c->s->layers[l];
     for (int r = 0; r < rows; r++) rmsnorm(h + r * H, L->input_norm, H, q->rms_eps, xn + r * H);
-    linear(L->wq, q->dtype, q->act_q8, NQ, H, xn, rows, qb, NQ, 0);
+    trace_copy(TRACE_F(t->x_qkv, l, H), xn, (size_t)rows * H);
+    linear_q(L->wq, q->dtype, q->act_q8, NQ, H, xn, rows, qb, NQ, 0, TRACE_B(t->b_qkv, l, H / 32));
     linear(L->wk, q->dtype, q->act_q8, NKV, H, xn, rows, kb, NKV, 0);
     linear(L->wv, q->dtype, q->act_q8, NKV, H, xn, rows, vb, NKV, 0);
+    if (t->y_qkv)
+      for (int r = 0; r < rows; r++) {
+        float *y = TRACE_F(t->y_qkv, l, NQKV) + (size_t)r * NQKV;
+        memcpy(y, qb + r * NQ, sizeof(float) * NQ);
+        memcpy(y + NQ, kb + r * NKV, sizeof(float) * NKV);
+        memcpy(y + NQ + NKV, vb + r * NKV, sizeof(float) * NKV);
+      }
     for (int r = 0; r < rows; r++) {
       const int pos = c->len + r;
       for (int hh = 0; hh < q->heads; hh++) {
@@ -453,15 +486,26 @@ int q3o_forward_embeds(q3o_ctx *c, const float *x, int rows, float *normed_last,
         free(sc);
       }
     }
-    linear(L->wo, q->dtype, q->act_q8, H, NQ, att, rows, h, H, 1);
+    /* o_proj, then the residual: h + (W_o . att), one rounding of the sum */
+    trace_copy(TRACE_F(t->x_o, l, NQ), att, (size_t)rows * NQ);
+    linear_q(L->wo, q->dtype, q->act_q8, H, NQ, att, rows, pb, H, 0, TRACE_B(t->b_o, l, NQ / 32));
+    trace_copy(TRACE_F(t->y_o, l, H), pb, (size_t)rows * H);
+    for (int i = 0; i < rows * H; i++) h[i] += pb[i];
     for (int r = 0; r < rows; r++) rmsnorm(h + r * H, L->post_norm, H, q->rms_eps, xn + r * H);
-    linear(L->wgate, q->dtype, q->act_q8, I, H, xn, rows, gb, I, 0);
+    trace_copy(TRACE_F(t->x_gu, l, H), xn, (size_t)rows * H);
+    linear_q(L->wgate, q->dtype, q->act_q8, I, H, xn, rows, gb, I, 0, TRACE_B(t->b_gu, l, H / 32));
     linear(L->wup, q->dtype, q->act_q8, I, H, xn, rows, ub, I, 0);
+    trace_copy(TRACE_F(t->y_gate, l, I), gb, (size_t)rows * I);
+    trace_copy(TRACE_F(t->y_up, l, I), ub, (size_t)rows * I);
     for (int i = 0; i < rows * I; i++) {
       const float g = gb[i];
       gb[i] = g / (1.0f + q3o_expf(-g)) * ub[i];
     }
-    linear(L->wdown, q->dtype, q->act_q8, H, I, gb, rows, h, H, 1);
+    trace_copy(TRACE_F(t->x_down, l, I), gb, (size_t)rows * I);
+    linear_q(L->wdown, q->dtype, q->act_q8, H, I, gb, rows, pb, H, 0,
+             TRACE_B(t->b_down, l, I / 32));
+    trace_copy(TRACE_F(t->y_down, l, H), pb, (size_t)rows * H);
+    for (int i = 0; i < rows * H; i++) h[i] += pb[i];
     if (layer_out) memcpy(layer_out + (size_t)l * rows * H, h, sizeof(float) * rows * H);
   }
   if (normed_last) rmsnorm(h + (size_t)(rows - 1) * H, c->s->final_norm, H, q->rms_eps, normed_last);
@@ -474,6 +518,7 @@ int q3o_forward_embeds(q3o_ctx *c, const float *x, int rows, float *normed_last,
   free(att);
   free(gb);
   free(ub);
+  free(pb);
   return 0;
 }
 
@@ -531,6 +576,8 @@ int q3o_text_project(const void *emb, int emb_dtype, int vocab, int text_hidden,
 /* ------------------------------------------------------------------ */
 /* code choice (greedy)                                                */
 
+/* tests/test.tts.qwen.lm.pas:109-117: result 0, moved to i only when p[i] >
+ * p[result]; so a NaN never wins and a NaN p[0] keeps 0 */
 int q3o_argmax(const float *p, int n) {
   int r = 0;
   for (int i = 1; i < n; i++)
@@ -731,6 +778,9 @@ int q3o_sample(const float *x, int n, float temperature, int top_k, float top_p,
   free(W);
   free(key);
   free(kept);
+  /* no code drawn (every weight 0 or NaN: NaN or infinite scores): the greedy
+   * code of x, so the result is always an index of the table */
+  if (pick < 0) pick = q3o_argmax(x, n);
   return pick;
 }
 

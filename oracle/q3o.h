@@ -30,7 +30,13 @@
  *    (tests/data/infer-ref/qwen3-tts-lm: predictor.codes = argmax of each row)
  *    plus brute-force checks of the logits processors on tiny vectors.
  *  - Q8_0 stack numerics (activation quantization or not) of the un-vendored
- *    mormot2-ai engine: parity unpinned (both modes are provided).
+ *    mormot2-ai engine: parity unpinned (both modes are provided); the int8
+ *    layer's composition (which inputs are quantized, the block products and
+ *    their order) is checked op by op against numpy through
+ *    q3o_forward_embeds_traced;
+ *  - the frame step (q3o_frame_*): marker tables through zero-weight stacks
+ *    (closed-form codes and decoded states) and a composition of NextFrame
+ *    over transformers' Qwen3 decoder.
  */
 #ifndef Q3O_H
 #define Q3O_H
@@ -106,6 +112,27 @@ int q3o_ctx_fill(q3o_ctx *c, const float *k, const float *v, int len);
    returns 0, or -1 when the context would overflow */
 int q3o_forward_embeds(q3o_ctx *c, const float *x, int rows, float *normed_last,
                        float *layer_out);
+
+/* the operands of every product of a forward, per layer l (each pointer
+   nullable; [layers][rows][n] row-major, blocks as ggml block_q8_0):
+   x_*: the f32 input of the product (the normed row, the attention output,
+   the post-attention normed row, SwiGLU's output); b_*: the Q8_0 blocks of
+   that input the int8 products read (act_q8 stacks only); y_*: the product's
+   output, before any residual add (q/k/v before QK-norm and RoPE) */
+typedef struct {
+  float *x_qkv, *y_qkv;   /* [H], [NQ + 2 NKV] (q, k, v side by side) */
+  void *b_qkv;            /* [H / 32] */
+  float *x_o, *y_o;       /* [NQ], [H] */
+  void *b_o;              /* [NQ / 32] */
+  float *x_gu, *y_gate, *y_up; /* [H], [I], [I] */
+  void *b_gu;             /* [H / 32] */
+  float *x_down, *y_down; /* [I], [H] */
+  void *b_down;           /* [I / 32] */
+} q3o_trace;
+
+/* q3o_forward_embeds with the operands of its products written to *t */
+int q3o_forward_embeds_traced(q3o_ctx *c, const float *x, int rows, float *normed_last,
+                              float *layer_out, const q3o_trace *t);
 
 /* logits[rows_out] = W[rows_out][hidden] . state, W f32 or Q8_0 */
 void q3o_head(const void *w, int dtype, int act_q8, int rows_out, int hidden,

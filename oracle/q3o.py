@@ -55,6 +55,12 @@ class Sampling(ctypes.Structure):
     ]
 
 
+class Trace(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in
+                ("x_qkv", "y_qkv", "b_qkv", "x_o", "y_o", "b_o", "x_gu", "y_gate", "y_up",
+                 "b_gu", "x_down", "y_down", "b_down")]
+
+
 class CodecRes(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in
                 ("a1_alpha", "a1_beta", "c1_w", "c1_b", "a2_alpha", "a2_beta", "c2_w", "c2_b")]
@@ -154,6 +160,8 @@ def lib():
             "q3o_ctx_v": (_FP, [_P, ctypes.c_int]),
             "q3o_ctx_fill": (ctypes.c_int, [_P, _FP, _FP, ctypes.c_int]),
             "q3o_forward_embeds": (ctypes.c_int, [_P, _FP, ctypes.c_int, _FP, _FP]),
+            "q3o_forward_embeds_traced": (ctypes.c_int, [_P, _FP, ctypes.c_int, _FP, _FP,
+                                                         ctypes.POINTER(Trace)]),
             "q3o_head": (None, [_P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _FP,
                                 _FP]),
             "q3o_argmax": (ctypes.c_int, [_FP, ctypes.c_int]),
@@ -388,6 +396,38 @@ class Ctx:
         if rc:
             raise ValueError("q3o_forward_embeds: context overflow")
         return (normed, lo) if layer_out else normed
+
+    def forward_traced(self, x):
+        """forward(x) with the operands of every product: a dict of arrays
+        [layers][rows][n] (x_*, y_* f32; b_* the Q8_0 blocks as uint8 rows of
+        34-byte blocks, act_q8 stacks), plus "normed" (the last row's)."""
+        x = _f32(x)
+        if x.ndim == 1:
+            x = x[None, :]
+        rows, H = x.shape
+        d = self.stack.dims
+        Lr = (d["layers"], rows)
+        NQ, NKV, I = d["heads"] * d["head_dim"], d["kv_heads"] * d["head_dim"], d["intermediate"]
+        out = dict(x_qkv=np.zeros(Lr + (H,), np.float32),
+                   y_qkv=np.zeros(Lr + (NQ + 2 * NKV,), np.float32),
+                   x_o=np.zeros(Lr + (NQ,), np.float32), y_o=np.zeros(Lr + (H,), np.float32),
+                   x_gu=np.zeros(Lr + (H,), np.float32), y_gate=np.zeros(Lr + (I,), np.float32),
+                   y_up=np.zeros(Lr + (I,), np.float32), x_down=np.zeros(Lr + (I,), np.float32),
+                   y_down=np.zeros(Lr + (H,), np.float32),
+                   b_qkv=np.zeros(Lr + (H // 32 * 34,), np.uint8),
+                   b_o=np.zeros(Lr + (NQ // 32 * 34,), np.uint8),
+                   b_gu=np.zeros(Lr + (H // 32 * 34,), np.uint8),
+                   b_down=np.zeros(Lr + (I // 32 * 34,), np.uint8))
+        t = Trace(**{k: v.ctypes.data for k, v in out.items()})
+        normed = np.empty(H, dtype=np.float32)
+        lo = np.empty((d["layers"], rows, H), dtype=np.float32)
+        rc = lib().q3o_forward_embeds_traced(self.h, _fp(x), rows, _fp(normed), _fp(lo),
+                                             ctypes.byref(t))
+        if rc:
+            raise ValueError("q3o_forward_embeds: context overflow")
+        out["normed"] = normed
+        out["layer_out"] = lo
+        return out
 
     def fill(self, k, v):
         k, v = _f32(k), _f32(v)

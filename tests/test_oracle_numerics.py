@@ -117,6 +117,30 @@ def test_argmax_first_max_wins(q3o):
     assert q3o.argmax(np.array([5], np.float32)) == 0
 
 
+def test_argmax_nan_rule(q3o):
+    """The reference's ArgMax (tests/test.tts.qwen.lm.pas:109-117) keeps
+    result 0 and moves only on p[i] > p[result]: a NaN never wins, a NaN p[0]
+    keeps 0 (nothing compares greater than it), every value NaN gives 0. The
+    device choosers follow the same rule, so a code is always a table row."""
+    def ref_argmax(p):  # the Pascal loop, literally
+        r = 0
+        for i in range(1, len(p)):
+            if p[i] > p[r]:
+                r = i
+        return r
+    nan = np.nan
+    cases = [[1, nan, 3, 2], [nan, 5, 7], [nan, nan, nan], [-np.inf, nan, -1, -1],
+             [2, 2, nan, 2], [nan], [-np.inf, -np.inf]]
+    for c in cases:
+        p = np.array(c, np.float32)
+        assert q3o.argmax(p) == ref_argmax(p), c
+    rng = np.random.default_rng(3)
+    for _ in range(200):
+        p = rng.standard_normal(37).astype(np.float32)
+        p[rng.random(37) < 0.2] = np.nan
+        assert q3o.argmax(p) == ref_argmax(p)
+
+
 def test_reference_fixture_codes_are_argmax(q3o):
     f = np.load(os.path.join(GOLDEN, "qwen3_tts_lm_fixture.npz"))
     codes = f["predictor_codes"]

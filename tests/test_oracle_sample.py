@@ -105,6 +105,22 @@ def test_sample_closed_forms(q3o):
     assert all(q3o.sample(y, 0.9, 50, 0.9, u) == 1234 for u in (0.0, 0.5, 0.9999))
 
 
+def test_sample_without_a_draw_falls_back_to_the_greedy_code(q3o):
+    """NaN or +inf scores leave no positive weight (e^(NaN) and e^(inf - inf)
+    are NaN): the draw then returns the greedy code of the scores (the
+    reference ArgMax rule), never -1, whatever the uniform."""
+    x = np.zeros(2048, np.float32)
+    x[:] = np.nan
+    assert all(q3o.sample(x, 0.9, 50, 1.0, u) == 0 for u in (0.0, 0.5, 0.9999))
+    y = np.zeros(3072, np.float32)
+    y[77] = np.inf
+    assert all(q3o.sample(y, 1.0, 0, 1.0, u) == 77 for u in (0.0, 0.5, 0.9999))
+    z = np.linspace(-1, 1, 2048).astype(np.float32)
+    z[0] = np.nan
+    z[900] = np.inf
+    assert q3o.sample(z, 1.0, 0, 1.0, 0.3) == 0  # a NaN first value keeps code 0
+
+
 def test_frame_sampling_top_k_1_is_greedy(q3o, synth):
     """Sampling with top-k 1 on both choosers reproduces the greedy frames
     (reduced widths so that the oracle runs in a second)."""
