@@ -10,6 +10,7 @@
 // needs more position splits).
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
 #include <cstring>
 #include <random>
 #include <string>
@@ -374,20 +375,32 @@ __global__ void k_frame_end(FrameDev f) {
 
 using namespace q3h;
 
+// A slice of a frame's streams (first .. first + n - 1) with its own work
+// buffers, HIP stream and captured step. The slices of one frame run their
+// steps concurrently: every kernel of the batched step is latency-bound, so
+// two chains of them on two queues overlap where one chain waits. Each
+// stream's arithmetic does not depend on the other rows of its products, so
+// the codes do not depend on the slicing.
+struct FrameSlice {
+  int first = 0, n = 0;
+  Work tw, cw;
+  FrameDev fd{};  // the view of the slice's streams
+  hipStream_t stream = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  int graph_positions = 0;  // attention positions the captured graph covers
+};
+
 struct q3h_frame {
   q3h_stack *talker = nullptr, *cp = nullptr;
   q3h_frame_config cfg{};
   int H = 0;
   std::vector<q3h_context *> tctx, cctx;
   CtxDev **t_arr = nullptr, **c_arr = nullptr;
-  Work tw, cw;
-  FrameDev fd{};
+  FrameDev fd{};  // every stream: the state arrays the slices view
+  std::vector<FrameSlice> slices;
   float *codec_emb = nullptr, *pred_emb = nullptr, *tts_pad = nullptr;
   std::vector<int> started, host_len, max_trailing_rows;
-  hipStream_t stream = nullptr;
-  hipGraph_t graph = nullptr;
-  hipGraphExec_t exec = nullptr;
-  int graph_positions = 0;  // attention positions the captured graph covers
   int32_t *pinned = nullptr;  // [n][groups] codes + [n] alive
   std::vector<void *> allocs;
   // the choosers (TQwenTalker.Sampling) and the source of sentence seeds when
@@ -402,9 +415,25 @@ struct q3h_frame {
 
 namespace {
 
+void drop_graphs(q3h_frame *f) {
+  for (FrameSlice &sl : f->slices) {
+    if (sl.exec) (void)hipGraphExecDestroy(sl.exec);
+    if (sl.graph) (void)hipGraphDestroy(sl.graph);
+    sl.exec = nullptr;
+    sl.graph = nullptr;
+    sl.graph_positions = 0;
+  }
+}
+
+// every slice's work done (the frame's state may be read or changed)
+void sync_slices(q3h_frame *f) {
+  for (FrameSlice &sl : f->slices) check_hip(hipStreamSynchronize(sl.stream), "frame sync");
+}
+
 void frame_release(q3h_frame *f) {
-  if (f->exec) (void)hipGraphExecDestroy(f->exec);
-  if (f->graph) (void)hipGraphDestroy(f->graph);
+  for (FrameSlice &sl : f->slices)
+    if (sl.stream) (void)hipStreamSynchronize(sl.stream);
+  drop_graphs(f);
   for (auto *c : f->tctx) {
     c->s->contexts--;
     free_context(c);
@@ -413,13 +442,82 @@ void frame_release(q3h_frame *f) {
     c->s->contexts--;
     free_context(c);
   }
-  f->tw.release();
-  f->cw.release();
+  for (FrameSlice &sl : f->slices) {
+    sl.tw.release();
+    sl.cw.release();
+    if (sl.stream) (void)hipStreamDestroy(sl.stream);
+  }
   for (void *p : f->allocs) dev_free(p);
   dev_free(f->start_plan);
   dev_free(f->start_proj);
   if (f->pinned) (void)hipHostFree(f->pinned);
-  if (f->stream) (void)hipStreamDestroy(f->stream);
+}
+
+// The view of streams first .. first + n - 1 of the frame's state, with the
+// slice's work buffers (the int8 path's folded inputs when `partial`).
+FrameDev slice_view(const q3h_frame *f, FrameSlice &sl, bool cp_partial, bool t_partial) {
+  const q3h_frame_config &c = f->cfg;
+  const size_t first = sl.first, H = f->H;
+  FrameDev d = f->fd;
+  d.n = sl.n;
+  d.logits += first * c.vocab;
+  d.past += first * H;
+  d.codes += first * c.groups;
+  d.seen += first * c.vocab;
+  d.nframes += first;
+  d.step += first;
+  d.alive += first;
+  d.trailing += first * c.max_frames * H;
+  d.trailing_rows += first;
+  d.seeds += first;
+  d.cp_h = sl.cw.h;
+  d.t_h = sl.tw.h;
+  d.cp_logits = sl.cw.logits;
+  d.cp_ctx = f->c_arr + first;
+  d.cp_rd = sl.cw.rd;
+  d.t_rd = sl.tw.rd;
+  d.t_ctx = f->t_arr + first;
+  d.cp_xq = nullptr;
+  d.cp_part = nullptr;
+  d.cp_hch = 0;
+  d.t_xq = nullptr;
+  if (cp_partial) {
+    d.cp_xq = sl.cw.xa.q;
+    d.cp_norm0 = f->cp->layers[0].in_norm;
+    d.cp_eps = f->cp->cfg.rms_eps;
+    d.cp_part = sl.cw.gpart;
+    d.cp_hch = gemm_i8_chunks(f->H);
+  }
+  if (t_partial) {
+    d.t_xq = sl.tw.xa.q;
+    d.t_norm0 = f->talker->layers[0].in_norm;
+    d.t_eps = f->talker->cfg.rms_eps;
+  }
+  return d;
+}
+
+// the views of every slice, again after the frame-wide parameters changed
+// (the captured steps hold them as kernel arguments: captured again)
+void refresh_slices(q3h_frame *f) {
+  const q3h_frame_config &c = f->cfg;
+  int nmax = 0;
+  for (const FrameSlice &sl : f->slices) nmax = std::max(nmax, sl.n);
+  const bool cp_partial =
+      partial_path(f->cp, 2 * nmax) && f->cp->heads[c.cp_heads[0]].N % 16 == 0;
+  const bool t_partial = partial_path(f->talker, nmax) && f->H <= 4096;
+  for (FrameSlice &sl : f->slices) sl.fd = slice_view(f, sl, cp_partial, t_partial);
+  drop_graphs(f);
+}
+
+// The number of slices of a frame of n streams: two for the int8 path at 8
+// or more streams (its kernels take the same time for 8 .. 64 rows), one
+// otherwise. Q3H_FRAME_SLICES (1..4) overrides it, for measurements.
+int slice_count(const q3h_stack *talker, int n) {
+  if (const char *e = std::getenv("Q3H_FRAME_SLICES")) {
+    const int v = std::atoi(e);
+    if (v >= 1 && v <= 4) return std::min(v, n);
+  }
+  return (n >= 8 && partial_path(talker, n)) ? 2 : 1;
 }
 
 template <class T>
@@ -429,12 +527,16 @@ T *falloc(q3h_frame *f, size_t n) {
   return p;
 }
 
-// The step's kernel sequence on stream st (captured into the graph).
-void enqueue_step(q3h_frame *f, int positions, hipStream_t st) {
+// The step's kernel sequence of slice sl on stream st (captured into the
+// slice's graph).
+void enqueue_step(q3h_frame *f, FrameSlice &sl, int positions, hipStream_t st) {
   const q3h_frame_config &c = f->cfg;
-  const int n = c.n_streams, H = f->H;
+  const int n = sl.n, H = f->H;
   q3h_stack *cp = f->cp, *tk = f->talker;
-  FrameDev fd = f->fd;
+  const FrameDev fd = sl.fd;
+  Work &cw = sl.cw, &tw = sl.tw;
+  CtxDev **c_arr = f->c_arr + sl.first;
+  q3h_context *cctx0 = f->cctx[sl.first];
   const bool cq = fd.cp_xq != nullptr, tq = fd.t_xq != nullptr;  // the folded int8 paths
   if (fd.sp0.do_sample)
     hipLaunchKernelGGL(k_choose_code0<true>, dim3(n), dim3(kArgBlock), 0, st, fd);
@@ -444,7 +546,7 @@ void enqueue_step(q3h_frame *f, int positions, hipStream_t st) {
   // one stream on the Qwen3-TTS shapes: step 0 runs the fused two-row path,
   // steps 1.. the fused single-row path (positions are fixed: step g adds
   // position g + 1)
-  const bool fused = n == 1 && cp_fused_supported(cp->cfg) && f->cctx[0]->max_pos == 16;
+  const bool fused = n == 1 && cp_fused_supported(cp->cfg) && cctx0->max_pos == 16;
   // greedy on that path: the argmax of head g and the next input row are taken
   // by the first product of forward g + 1 (one launch fewer per group)
   const bool code_in_product =
@@ -458,8 +560,8 @@ void enqueue_step(q3h_frame *f, int positions, hipStream_t st) {
       LayerIO io;
       io.input_quantized = true;
       io.final_norm = cp->final_norm;
-      run_layers(cp, f->cw, n * R, c.groups, R == 1, st, io);
-      launch_gemm_i8_partial(cp->heads[c.cp_heads[g]], f->cw.xa, n * R, f->cw.gpart, st);
+      run_layers(cp, cw, n * R, c.groups, R == 1, st, io);
+      launch_gemm_i8_partial(cp->heads[c.cp_heads[g]], cw.xa, n * R, cw.gpart, st);
       if (fd.sp.do_sample)
         hipLaunchKernelGGL(k_cp_next<true>, dim3(n), dim3(kArgBlock), 0, st, fd, g);
       else
@@ -467,19 +569,19 @@ void enqueue_step(q3h_frame *f, int positions, hipStream_t st) {
       continue;
     }
     if (fused && g == 0) {
-      run_cp_fused_first(cp, f->cw, f->cctx[0], st);
+      run_cp_fused_first(cp, cw, cctx0, st);
     } else if (fused) {
       const CodeSrc src{fd.cp_logits, fd.cp_vocab,
                         fd.pred_emb + (size_t)(g - 1) * fd.cp_vocab * H, fd.codes + g, fd.alive};
-      run_cp_fused(cp, f->cw, f->cctx[0], g + 1, st, code_in_product ? &src : nullptr);
+      run_cp_fused(cp, cw, cctx0, g + 1, st, code_in_product ? &src : nullptr);
     } else {
-      launch_prep(f->c_arr, fd.alive, n, R, f->cw.rd, st);
-      run_layers(cp, f->cw, n * R, c.groups, R == 1, st);
-      launch_advance(f->c_arr, fd.alive, n, R, st);
+      launch_prep(c_arr, fd.alive, n, R, cw.rd, st);
+      run_layers(cp, cw, n * R, c.groups, R == 1, st);
+      launch_advance(c_arr, fd.alive, n, R, st);
     }
     // final norm of each stream's last row + head g, one launch
-    linear(cp, f->cw, cp->heads[c.cp_heads[g]], f->cw.h + (size_t)(R - 1) * H, R * H, n,
-           cp->final_norm, f->cw.logits, c.cp_vocab, EPI_STORE, nullptr, st);
+    linear(cp, cw, cp->heads[c.cp_heads[g]], cw.h + (size_t)(R - 1) * H, R * H, n,
+           cp->final_norm, cw.logits, c.cp_vocab, EPI_STORE, nullptr, st);
     if (fd.sp.do_sample)
       hipLaunchKernelGGL(k_cp_sample, dim3(n), dim3(kArgBlock), 0, st, fd.cp_logits, fd.alive,
                          fd.pred_emb, fd.cp_h, fd.codes, fd.cp_vocab, fd.groups, fd.H, g, fd.sp,
@@ -493,18 +595,18 @@ void enqueue_step(q3h_frame *f, int positions, hipStream_t st) {
     hipLaunchKernelGGL(k_talker_input_q, dim3(n), dim3(kArgBlock), 0, st, fd);
     LayerIO io;
     io.input_quantized = true;
-    run_layers(tk, f->tw, n, positions, true, st, io);
+    run_layers(tk, tw, n, positions, true, st, io);
   } else {
     hipLaunchKernelGGL(k_talker_input, dim3((H + 255) / 256, n), dim3(256), 0, st, fd);
-    run_layers(tk, f->tw, n, positions, true, st);
+    run_layers(tk, tw, n, positions, true, st);
   }
   const Mat &th = tk->heads[c.talker_head];
   if (n == 1) {  // final norm fused into the head, the normed state written alongside
-    linear(tk, f->tw, th, f->tw.h, H, 1, tk->final_norm, fd.logits, c.vocab, EPI_STORE, fd.past,
+    linear(tk, tw, th, tw.h, H, 1, tk->final_norm, fd.logits, c.vocab, EPI_STORE, fd.past,
            st);
   } else {
-    launch_rmsnorm_rows(f->tw.h, H, n, H, tk->final_norm, tk->cfg.rms_eps, fd.past, H, st);
-    linear(tk, f->tw, th, fd.past, H, n, nullptr, fd.logits, c.vocab, EPI_STORE, nullptr, st);
+    launch_rmsnorm_rows(tw.h, H, n, H, tk->final_norm, tk->cfg.rms_eps, fd.past, H, st);
+    linear(tk, tw, th, fd.past, H, n, nullptr, fd.logits, c.vocab, EPI_STORE, nullptr, st);
   }
   hipLaunchKernelGGL(k_frame_end, dim3((n + 63) / 64), dim3(64), 0, st, fd);
 }
@@ -549,7 +651,6 @@ extern "C" int q3h_frame_create(q3h_stack *talker, q3h_stack *cp, const q3h_fram
     f->cfg = c;
     const int n = c.n_streams, H = talker->cfg.hidden;
     f->H = H;
-    check_hip(hipStreamCreateWithFlags(&f->stream, hipStreamNonBlocking), "hipStreamCreate");
     for (int s = 0; s < n; s++) {
       f->tctx.push_back(new_context(talker, c.max_positions));
       f->cctx.push_back(new_context(cp, c.groups));
@@ -565,8 +666,18 @@ extern "C" int q3h_frame_create(q3h_stack *talker, q3h_stack *cp, const q3h_fram
               "frame init");
     check_hip(hipMemcpy(f->c_arr, ca.data(), sizeof(CtxDev *) * n, hipMemcpyHostToDevice),
               "frame init");
-    f->tw.ensure(talker, n, attention_splits_upto(talker, c.max_positions), c.vocab);
-    f->cw.ensure(cp, 2 * n, 1, c.cp_vocab);
+    // the slices: consecutive runs of streams, the first ones one longer
+    const int ns = slice_count(talker, n);
+    f->slices.resize(ns);
+    for (int k = 0, first = 0; k < ns; k++) {
+      FrameSlice &sl = f->slices[k];
+      sl.first = first;
+      sl.n = n / ns + (k < n % ns ? 1 : 0);
+      first += sl.n;
+      check_hip(hipStreamCreateWithFlags(&sl.stream, hipStreamNonBlocking), "hipStreamCreate");
+      sl.tw.ensure(talker, sl.n, attention_splits_upto(talker, c.max_positions), c.vocab);
+      sl.cw.ensure(cp, 2 * sl.n, 1, c.cp_vocab);
+    }
     f->codec_emb = falloc<float>(f, (size_t)c.vocab * H);
     check_hip(hipMemcpy(f->codec_emb, codec_emb, sizeof(float) * c.vocab * H,
                         hipMemcpyHostToDevice),
@@ -605,25 +716,9 @@ extern "C" int q3h_frame_create(q3h_stack *talker, q3h_stack *cp, const q3h_fram
     d.codec_emb = f->codec_emb;
     d.pred_emb = f->pred_emb;
     d.tts_pad = f->tts_pad;
-    d.cp_h = f->cw.h;
-    d.t_h = f->tw.h;
-    d.cp_logits = f->cw.logits;
     d.cp_ctx = f->c_arr;
-    d.cp_rd = f->cw.rd;
-    d.t_rd = f->tw.rd;
     d.t_ctx = f->t_arr;
-    if (partial_path(cp, 2 * n) && cp->heads[c.cp_heads[0]].N % 16 == 0) {
-      d.cp_xq = f->cw.xa.q;
-      d.cp_norm0 = cp->layers[0].in_norm;
-      d.cp_eps = cp->cfg.rms_eps;
-      d.cp_part = f->cw.gpart;
-      d.cp_hch = gemm_i8_chunks(H);
-    }
-    if (partial_path(talker, n) && H <= 4096) {
-      d.t_xq = f->tw.xa.q;
-      d.t_norm0 = talker->layers[0].in_norm;
-      d.t_eps = talker->cfg.rms_eps;
-    }
+    refresh_slices(f);
     check_hip(hipMemset(d.alive, 0, sizeof(int) * n), "frame init");
     check_hip(hipMemset(const_cast<uint64_t *>(d.seeds), 0, sizeof(uint64_t) * n), "frame init");
     check_hip(hipMemset(d.codes, 0xff, sizeof(int) * n * c.groups), "frame init");
@@ -656,7 +751,7 @@ void start_stream(q3h_frame *f, int stream, int rows, int trailing_rows, Fill &&
           "q3h_frame_start: more trailing rows than max_frames");
   require(rows <= c.max_positions, Q3H_E_CAPACITY, "q3h_frame_start: prefill too long");
   check_hip(hipSetDevice(f->talker->dev->ordinal), "hipSetDevice");
-  check_hip(hipStreamSynchronize(f->stream), "frame sync");
+  sync_slices(f);
   q3h_context *tc = f->tctx[stream];
   set_len(tc, 0, tc->stream);
   // the prefill through the single-context path, outputs kept on the device
@@ -715,18 +810,15 @@ extern "C" int q3h_frame_set_sampling(q3h_frame *f, const q3h_sampling *sp) {
     check(sp->sub_do_sample, sp->sub_temperature, sp->sub_top_k, sp->sub_top_p, c.cp_vocab,
           "code predictor");
     check_hip(hipSetDevice(f->talker->dev->ordinal), "hipSetDevice");
-    check_hip(hipStreamSynchronize(f->stream), "frame sync");
+    sync_slices(f);
     f->sampling = *sp;
     auto params = [](int on, float t, int k, float p) {
       return on ? SampleParams{1, t, k, p} : SampleParams{0, 1.0f, 0, 1.0f};
     };
     f->fd.sp0 = params(sp->do_sample, sp->temperature, sp->top_k, sp->top_p);
     f->fd.sp = params(sp->sub_do_sample, sp->sub_temperature, sp->sub_top_k, sp->sub_top_p);
-    // the parameters are kernel arguments of the captured step: capture again
-    if (f->exec) (void)hipGraphExecDestroy(f->exec);
-    if (f->graph) (void)hipGraphDestroy(f->graph);
-    f->exec = nullptr;
-    f->graph = nullptr;
+    // the parameters are kernel arguments of the captured steps: capture again
+    refresh_slices(f);
   });
 }
 
@@ -807,7 +899,7 @@ extern "C" int q3h_frame_start_text(q3h_frame *f, int stream, q3h_text_proj *t,
     text_ensure(t, np);
     const int need = std::max(np, (int)plan.size());
     if (need > f->start_cap) {
-      check_hip(hipStreamSynchronize(f->stream), "frame sync");
+      sync_slices(f);
       dev_free(f->start_plan);
       dev_free(f->start_proj);
       f->start_plan = nullptr;
@@ -839,47 +931,59 @@ extern "C" int q3h_frame_step(q3h_frame *f, int32_t *codes, int32_t *alive) {
     const q3h_frame_config &c = f->cfg;
     const int n = c.n_streams;
     bool any = false;
-    int maxlen = 0;
     for (int s = 0; s < n; s++) {
       if (!f->started[s]) continue;
       any = true;
       require(f->host_len[s] + 1 <= c.max_positions, Q3H_E_CAPACITY,
               "q3h_frame_step: a stream reached max_positions");
-      maxlen = std::max(maxlen, f->host_len[s] + 1);
     }
     require(any, Q3H_E_STATE, "q3h_frame_step: no stream was started");
     check_hip(hipSetDevice(f->talker->dev->ordinal), "hipSetDevice");
-    if (c.use_graph) {
-      if (!f->exec || maxlen > f->graph_positions) {
-        if (f->exec) {
-          (void)hipGraphExecDestroy(f->exec);
-          f->exec = nullptr;
+    for (FrameSlice &sl : f->slices) {
+      // the longest context of the slice's running streams
+      int slen = 0;
+      for (int s = sl.first; s < sl.first + sl.n; s++)
+        if (f->started[s]) slen = std::max(slen, f->host_len[s] + 1);
+      if (slen == 0) continue;  // no stream of the slice runs (its codes read as -1)
+      if (c.use_graph) {
+        if (!sl.exec || slen > sl.graph_positions) {
+          if (sl.exec) {
+            (void)hipGraphExecDestroy(sl.exec);
+            sl.exec = nullptr;
+          }
+          if (sl.graph) {
+            (void)hipGraphDestroy(sl.graph);
+            sl.graph = nullptr;
+          }
+          // capture with headroom so that the graph is rebuilt rarely: the
+          // attention covers up to 256 positions in one split, beyond that up
+          // to 256 positions more than the longest context (rows shorter than
+          // the capture leave their extra splits empty)
+          const int cap = slen <= 256 ? 256 : ((slen + 255) / 256 + 1) * 256;
+          const int cap_positions = std::min(c.max_positions, cap);
+          sl.graph = capture_graph(sl.stream, [&] { enqueue_step(f, sl, cap_positions, sl.stream); });
+          check_hip(hipGraphInstantiate(&sl.exec, sl.graph, nullptr, nullptr, 0),
+                    "hipGraphInstantiate");
+          sl.graph_positions = cap_positions;
         }
-        if (f->graph) {
-          (void)hipGraphDestroy(f->graph);
-          f->graph = nullptr;
-        }
-        // capture with headroom so that the graph is rebuilt rarely: the
-        // attention covers up to 256 positions in one split, beyond that up
-        // to 256 positions more than the longest context (rows shorter than
-        // the capture leave their extra splits empty)
-        const int cap = maxlen <= 256 ? 256 : ((maxlen + 255) / 256 + 1) * 256;
-        const int cap_positions = std::min(c.max_positions, cap);
-        f->graph = capture_graph(f->stream, [&] { enqueue_step(f, cap_positions, f->stream); });
-        check_hip(hipGraphInstantiate(&f->exec, f->graph, nullptr, nullptr, 0),
-                  "hipGraphInstantiate");
-        f->graph_positions = cap_positions;
+        check_hip(hipGraphLaunch(sl.exec, sl.stream), "hipGraphLaunch");
+      } else {
+        enqueue_step(f, sl, slen, sl.stream);
+        check_hip(hipGetLastError(), "frame kernels");
       }
-      check_hip(hipGraphLaunch(f->exec, f->stream), "hipGraphLaunch");
-    } else {
-      enqueue_step(f, maxlen, f->stream);
-      check_hip(hipGetLastError(), "frame kernels");
+      // the slice's codes and alive flags, into the same places of the pinned copy
+      check_hip(hipMemcpyAsync(f->pinned + (size_t)sl.first * c.groups,
+                               f->fd.codes + (size_t)sl.first * c.groups,
+                               sizeof(int32_t) * sl.n * c.groups, hipMemcpyDeviceToHost,
+                               sl.stream),
+                "download codes");
+      check_hip(hipMemcpyAsync(f->pinned + (size_t)n * c.groups + sl.first,
+                               f->fd.alive + sl.first, sizeof(int32_t) * sl.n,
+                               hipMemcpyDeviceToHost, sl.stream),
+                "download alive");
     }
-    // the codes and, right after them, the alive flags
-    check_hip(hipMemcpyAsync(f->pinned, f->fd.codes, sizeof(int32_t) * n * (c.groups + 1),
-                             hipMemcpyDeviceToHost, f->stream),
-              "download codes");
-    check_hip(hipStreamSynchronize(f->stream), "frame step sync");
+    for (FrameSlice &sl : f->slices)
+      check_hip(hipStreamSynchronize(sl.stream), "frame step sync");
     for (int s = 0; s < n; s++) {
       const bool live = f->started[s] && f->pinned[n * c.groups + s] != 0;
       if (codes)
@@ -901,7 +1005,7 @@ extern "C" int q3h_frame_state(q3h_frame *f, int stream, float *logits, float *p
     require(f != nullptr, Q3H_E_ARG, "q3h_frame_state: NULL frame");
     require(stream >= 0 && stream < f->cfg.n_streams, Q3H_E_ARG, "q3h_frame_state: bad stream");
     check_hip(hipSetDevice(f->talker->dev->ordinal), "hipSetDevice");
-    check_hip(hipStreamSynchronize(f->stream), "frame sync");
+    sync_slices(f);
     if (logits)
       check_hip(hipMemcpy(logits, f->fd.logits + (size_t)stream * f->cfg.vocab,
                           sizeof(float) * f->cfg.vocab, hipMemcpyDeviceToHost),
@@ -917,7 +1021,7 @@ extern "C" int q3h_frame_destroy(q3h_frame *f) {
   return guard([&] {
     require(f != nullptr, Q3H_E_ARG, "q3h_frame_destroy: NULL frame");
     check_hip(hipSetDevice(f->talker->dev->ordinal), "hipSetDevice");
-    check_hip(hipStreamSynchronize(f->stream), "frame sync");
+    sync_slices(f);
     frame_release(f);
     delete f;
   });
