@@ -51,14 +51,14 @@ def q8model(device):
 
 
 def test_q8_talker_prefill_and_greedy_decode(q8model, q3h, q3o, synth):
-    """Talker only, Q8_0, batch 1: 48 prompt rows then greedy steps whose
-    input is codec_emb[code] (the talker-only workload)."""
+    """Talker only, Q8_0, batch 1 (the talker-only workload at its size): 48
+    prompt rows then 64 greedy steps whose input is codec_emb[code]."""
     m = q8model
     ctx = q3h.Context(m.ts, 256)
     octx = q3o.Ctx(m.ot, 256)
     x = synth.prompt(5, 48)
     worst = 0.0
-    for step in range(9):
+    for step in range(65):
         print(f"talker step {step}", flush=True)
         lg, st = ctx.forward(x, head=0)
         ost = octx.forward(x)
@@ -70,7 +70,7 @@ def test_q8_talker_prefill_and_greedy_decode(q8model, q3h, q3o, synth):
         assert int(np.argmax(lg[:2048])) == code, (step, top2_margin(olg[:2048]))
         x = m.codec_emb[code][None]
     print(f"worst relative error {worst:.2e}")
-    assert ctx.length == octx.length == 48 + 8
+    assert ctx.length == octx.length == 48 + 64
     ctx.destroy()
     octx.destroy()
 
@@ -145,10 +145,11 @@ def test_batch_equals_single(q8model, q3h, synth):
 
 # (positions, f16 cache): the split shapes of the long-context kernel -
 # 64-position splits up to 1024 positions, then 128 (f16 up to 12288, f32);
+# 2048, 4096 and 8192 are the long-context workload's lengths;
 # 1024 + 1 and 8192 + 1 positions leave a last split of one position; 12300
 # takes the 256-position f16 splits
-@pytest.mark.parametrize("L,kv16", [(300, 1), (1024, 1), (2100, 1), (8192, 1), (12300, 1),
-                                    (300, 0), (2100, 0)])
+@pytest.mark.parametrize("L,kv16", [(300, 1), (1024, 1), (2048, 1), (2100, 1), (4096, 1),
+                                    (8192, 1), (12300, 1), (300, 0), (2100, 0)])
 def test_long_context_decode(device, q3h, q3o, synth, L, kv16):
     """Split attention: K/V prefilled with N(0,1) values, then decode steps,
     against the oracle with the same cache."""

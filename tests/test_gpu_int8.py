@@ -144,3 +144,42 @@ def test_int8_full_model_16_frames(device, synth):
         for of in ofs:
             of.destroy()
         m.destroy()
+
+
+def test_int8_frame_32_streams_long_prompts(device, synth):
+    """The batched serving workload's shapes at reduced depth (talker 4
+    layers, code predictor 2, real widths): 32 streams with prompt lengths
+    uniform in [16, 256] from the workload's generator, 14 frames, so that
+    contexts pass 256 positions (more than one round of the attention's key
+    loop); two slices of 16 streams. Bit-exact against the oracle."""
+    rng = np.random.Generator(np.random.PCG64(1))
+    lens = rng.integers(16, 257, size=32)
+    frames = 14
+    assert lens.max() + frames > 256
+    m = Model(device, seed=17, talker_layers=4, cp_layers=2, act_q8=1, norm_std=0.1,
+              max_positions=300)
+    fr = m.frame(n_streams=32, max_positions=300, max_frames=16)
+    ofs = []
+    try:
+        for s, L in enumerate(lens):
+            pre = synth.prompt(1000 + s, int(L))
+            fr.start(s, pre)
+            of = m.oracle_frame(max_positions=300)
+            of.start(pre)
+            ofs.append(of)
+        for i in range(frames):
+            codes, alive = fr.step()
+            print(f"frame {i}: longest context {int(lens.max()) + i + 1}", flush=True)
+            for s, of in enumerate(ofs):
+                ref = of.next()
+                assert alive[s] == 1
+                assert np.array_equal(codes[s], ref), (i, s, codes[s], ref)
+                lg, past = fr.state(s)
+                olg, opast = of.state()
+                assert np.array_equal(lg, olg) and np.array_equal(past, opast), (
+                    i, s, rel(lg, olg))
+    finally:
+        fr.destroy()
+        for of in ofs:
+            of.destroy()
+        m.destroy()
