@@ -148,6 +148,24 @@ int q3h_context_time_attention(q3h_context *c, int iters, float *us_per_launch,
 int q3h_forward_embeds(q3h_context *c, const float *x, int rows, int head,
                        float *logits, float *normed_last);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+   memory (code under HIP graph capture, tight serving loops, harnesses that
+   forbid hipMalloc): q3h_forward_embeds with the same arguments and results,
+   but its work buffers are carved from one static device array of
+   Q3H_NOALLOC_SCRATCH_BYTES per GPU (set up by q3h_device_open) instead of
+   the context's own buffers, which q3h_forward_embeds grows with hipMalloc.
+   Calls no allocating routine. rows <= Q3H_NOALLOC_MAX_ROWS, and the
+   buffers of the call (they grow with rows and, for long contexts, with the
+   attention splits of length + rows positions) must fit the array: otherwise
+   Q3H_E_CAPACITY and nothing is computed. Every call on one GPU shares that
+   GPU's array, which keeps the last call's contents (no kernel reads a
+   buffer before writing it); calls on one device are serialized by a lock
+   of the device, since overlapping calls would race on the array. */
+#define Q3H_NOALLOC_MAX_ROWS 64
+#define Q3H_NOALLOC_SCRATCH_BYTES (16 << 20)
+int q3h_forward_embeds_noalloc(q3h_context *c, const float *x, int rows, int head,
+                               float *logits, float *normed_last);
+
 /* no reference counterpart (the reference is single-stream): one row per
    context, n contexts of the same stack at their own positions;
    x [n][hidden]; heads [n] (or NULL: no logits); logits [n][head rows of

@@ -40,40 +40,63 @@ void dev_free(void *p) {
 // ---------------------------------------------------------------------------
 // work buffers of a forward over M rows
 
-void Work::ensure(const q3h_stack *s, int rows, int splits, int head_rows) {
+// Every buffer of a Work for R rows, `splits` attention splits per row and
+// head_rows logits per row, in one order: each(slot, bytes) per buffer.
+template <class Each>
+void work_fields(const q3h_stack *s, size_t R, int splits, int head_rows, Work &w, Each &&each) {
   const q3h_stack_config &c = s->cfg;
-  const int H = c.hidden, NQ = c.heads * c.head_dim, NKV = c.kv_heads * c.head_dim;
-  const int I = c.intermediate;
+  const size_t H = c.hidden, NQ = (size_t)c.heads * c.head_dim;
+  const size_t NKV = (size_t)c.kv_heads * c.head_dim, I = c.intermediate;
+  each((void **)&w.h, sizeof(float) * R * H);
+  each((void **)&w.qkv, sizeof(float) * R * (NQ + 2 * NKV));
+  each((void **)&w.att, sizeof(float) * R * NQ);
+  each((void **)&w.act, sizeof(float) * R * I);
+  each((void **)&w.normed, sizeof(float) * R * H);
+  each((void **)&w.logits, sizeof(float) * R * (head_rows > 0 ? head_rows : 1));
+  each((void **)&w.rd, sizeof(RowDesc) * R);
+  each((void **)&w.part, sizeof(float) * R * c.heads * splits * (c.head_dim + 2));
+  each((void **)&w.ctx_arr, sizeof(CtxDev *) * R);
+  if (c.act_q8) {
+    const int maxK = std::max(std::max((int)H, (int)NQ), (int)I);
+    each((void **)&w.xa.q, qact_bytes((int)R, maxK));
+    each((void **)&w.xb.q, qact_bytes((int)R, maxK));
+    // chunk partials of the products over up to kPartialRows rows
+    const size_t pr = std::min<size_t>(R, kPartialRows);
+    const size_t ldq = NQ + 2 * NKV;
+    size_t pn = (size_t)gemm_i8_chunks((int)H) * pr * std::max(ldq, (size_t)2 * I);
+    pn = std::max(pn, (size_t)gemm_i8_chunks((int)NQ) * pr * H);
+    pn = std::max(pn, (size_t)gemm_i8_chunks((int)I) * pr * H);
+    each((void **)&w.gpart, sizeof(float) * pn);
+  } else {
+    // K-slice sums of the products of o_proj and down (f32 activations)
+    each((void **)&w.gpart, sizeof(float) * kF32Slices * R * H);
+  }
+}
+
+void Work::ensure(const q3h_stack *s, int rows, int splits, int head_rows) {
   if (rows <= rows_cap && splits <= splits_cap && head_rows <= head_cap) return;
   release();
   rows_cap = rows > rows_cap ? rows : rows_cap;
   splits_cap = splits > splits_cap ? splits : splits_cap;
   head_cap = head_rows > head_cap ? head_rows : head_cap;
-  const size_t R = rows_cap;
-  h = (float *)dev_alloc(sizeof(float) * R * H);
-  qkv = (float *)dev_alloc(sizeof(float) * R * (NQ + 2 * NKV));
-  att = (float *)dev_alloc(sizeof(float) * R * NQ);
-  act = (float *)dev_alloc(sizeof(float) * R * I);
-  normed = (float *)dev_alloc(sizeof(float) * R * H);
-  logits = (float *)dev_alloc(sizeof(float) * R * (head_cap > 0 ? head_cap : 1));
-  rd = (RowDesc *)dev_alloc(sizeof(RowDesc) * R);
-  part = (float *)dev_alloc(sizeof(float) * R * c.heads * splits_cap * (c.head_dim + 2));
-  ctx_arr = (CtxDev **)dev_alloc(sizeof(CtxDev *) * R);
-  if (c.act_q8) {
-    const int maxK = std::max(std::max(H, NQ), I);
-    xa.q = (int8_t *)dev_alloc(qact_bytes((int)R, maxK));
-    xb.q = (int8_t *)dev_alloc(qact_bytes((int)R, maxK));
-    // chunk partials of the products over up to kPartialRows rows
-    const size_t pr = std::min<size_t>(R, kPartialRows);
-    const size_t ldq = NQ + 2 * NKV;
-    size_t pn = (size_t)gemm_i8_chunks(H) * pr * std::max(ldq, (size_t)2 * I);
-    pn = std::max(pn, (size_t)gemm_i8_chunks(NQ) * pr * H);
-    pn = std::max(pn, (size_t)gemm_i8_chunks(I) * pr * H);
-    gpart = (float *)dev_alloc(sizeof(float) * pn);
-  } else {
-    // K-slice sums of the products of o_proj and down (f32 activations)
-    gpart = (float *)dev_alloc(sizeof(float) * kF32Slices * R * H);
-  }
+  work_fields(s, rows_cap, splits_cap, head_cap, *this,
+              [](void **slot, size_t bytes) { *slot = dev_alloc(bytes); });
+}
+
+bool work_carve(const q3h_stack *s, int rows, int splits, int head_rows, void *base, size_t cap,
+                Work &w) {
+  size_t off = 0;
+  bool fits = true;
+  work_fields(s, rows, splits, head_rows, w, [&](void **slot, size_t bytes) {
+    off = (off + 255) & ~(size_t)255;
+    fits = fits && off + bytes <= cap;
+    *slot = fits ? (char *)base + off : nullptr;
+    off += bytes;
+  });
+  w.rows_cap = rows;
+  w.splits_cap = splits;
+  w.head_cap = head_rows;
+  return fits;
 }
 
 void Work::release() {
@@ -433,6 +456,11 @@ extern "C" int q3h_device_available(void) {
   return 0;
 }
 
+// The work buffers of q3h_forward_embeds_noalloc: one static array, a copy
+// per GPU. Host code never uses its name as an address: q3h_device_open
+// takes each GPU's address of it (hipGetSymbolAddress) into dev->scratch.
+static __device__ __align__(256) unsigned char scratch[Q3H_NOALLOC_SCRATCH_BYTES];
+
 extern "C" int q3h_device_open(int ordinal, q3h_device **out) {
   return guard([&] {
     require(out != nullptr, Q3H_E_ARG, "q3h_device_open: out is NULL");
@@ -447,10 +475,14 @@ extern "C" int q3h_device_open(int ordinal, q3h_device **out) {
     check_hip(hipFree(nullptr), "hipFree(0)");
     hipDeviceProp_t p;
     check_hip(hipGetDeviceProperties(&p, ordinal), "hipGetDeviceProperties");
+    // this GPU's copy of the scratch array (the device is current)
+    void *scratch_ptr = nullptr;
+    check_hip(hipGetSymbolAddress(&scratch_ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress");
     q3h_device *d = new q3h_device();
     d->ordinal = ordinal;
     d->name = p.name;
     d->cus = p.multiProcessorCount;
+    d->scratch = scratch_ptr;
     *out = d;
   });
 }
@@ -956,52 +988,97 @@ extern "C" int q3h_context_time_attention(q3h_context *c, int iters, float *us_p
 // ---------------------------------------------------------------------------
 // forward
 
+namespace {
+
+// the checks of q3h_forward_embeds (false: rows <= 0, nothing to do)
+bool forward_args(const q3h_context *c, const float *x, int rows, int head, const char *who) {
+  require(c != nullptr, Q3H_E_ARG, std::string(who) + ": NULL context");
+  if (rows <= 0) return false;
+  require(x != nullptr, Q3H_E_ARG, std::string(who) + ": x is NULL");
+  const q3h_stack *s = c->s;
+  require(head >= -1 && head < (int)s->heads.size(), Q3H_E_ARG,
+          std::string(who) + ": no head " + std::to_string(head));
+  require(c->len + rows <= c->max_pos, Q3H_E_CAPACITY,
+          std::string(who) + ": " + std::to_string(c->len) + " + " + std::to_string(rows) +
+              " positions exceed the context's " + std::to_string(c->max_pos));
+  return true;
+}
+
+// TQwenLm.Forward on the work buffers w (sized for rows, the attention splits
+// of length + rows positions and the head's rows): blocks until the outputs
+// are in host memory
+void forward_rows(q3h_context *c, Work &w, const float *x, int rows, int head, float *logits,
+                  float *normed_last) {
+  q3h_stack *s = c->s;
+  const q3h_stack_config &cf = s->cfg;
+  const int H = cf.hidden;
+  const int head_rows = head >= 0 ? s->heads[head].N : 0;
+  const int positions = c->len + rows;
+  hipStream_t st = c->stream;
+  check_hip(hipMemcpyAsync(w.h, x, sizeof(float) * rows * H, hipMemcpyHostToDevice, st),
+            "upload x");
+  launch_prep(c->dev_arr, nullptr, 1, rows, w.rd, st);
+  LayerIO io;
+  io.single_context = true;
+  run_layers(s, w, rows, positions, rows == 1, st, io);
+  // final norm of the last row, fused into the head product when there is one
+  if (head >= 0) {
+    linear(s, w, s->heads[head], w.h + (size_t)(rows - 1) * H, H, 1, s->final_norm, w.logits,
+           head_rows, EPI_STORE, w.normed, st);
+  } else {
+    launch_rmsnorm_rows(w.h + (size_t)(rows - 1) * H, H, 1, H, s->final_norm, cf.rms_eps,
+                        w.normed, H, st);
+  }
+  launch_advance(c->dev_arr, nullptr, 1, rows, st);
+  check_hip(hipGetLastError(), "forward kernels");
+  if (normed_last)
+    check_hip(hipMemcpyAsync(normed_last, w.normed, sizeof(float) * H, hipMemcpyDeviceToHost,
+                             st),
+              "download state");
+  if (logits && head >= 0)
+    check_hip(hipMemcpyAsync(logits, w.logits, sizeof(float) * head_rows, hipMemcpyDeviceToHost,
+                             st),
+              "download logits");
+  check_hip(hipStreamSynchronize(st), "forward sync");
+  c->len += rows;
+}
+
+}  // namespace
+
 extern "C" int q3h_forward_embeds(q3h_context *c, const float *x, int rows, int head,
                                   float *logits, float *normed_last) {
   return guard([&] {
-    require(c != nullptr, Q3H_E_ARG, "q3h_forward_embeds: NULL context");
-    if (rows <= 0) return;
-    require(x != nullptr, Q3H_E_ARG, "q3h_forward_embeds: x is NULL");
+    if (!forward_args(c, x, rows, head, "q3h_forward_embeds")) return;
     q3h_stack *s = c->s;
-    const q3h_stack_config &cf = s->cfg;
-    require(head >= -1 && head < (int)s->heads.size(), Q3H_E_ARG,
-            "q3h_forward_embeds: no head " + std::to_string(head));
-    require(c->len + rows <= c->max_pos, Q3H_E_CAPACITY,
-            "q3h_forward_embeds: " + std::to_string(c->len) + " + " + std::to_string(rows) +
-                " positions exceed the context's " + std::to_string(c->max_pos));
     check_hip(hipSetDevice(s->dev->ordinal), "hipSetDevice");
-    const int H = cf.hidden;
     const int head_rows = head >= 0 ? s->heads[head].N : 0;
-    const int positions = c->len + rows;
-    Work &w = c->w;
-    w.ensure(s, rows, attention_splits(s, positions), head_rows);
-    hipStream_t st = c->stream;
-    check_hip(hipMemcpyAsync(w.h, x, sizeof(float) * rows * H, hipMemcpyHostToDevice, st),
-              "upload x");
-    launch_prep(c->dev_arr, nullptr, 1, rows, w.rd, st);
-    LayerIO io;
-    io.single_context = true;
-    run_layers(s, w, rows, positions, rows == 1, st, io);
-    // final norm of the last row, fused into the head product when there is one
-    if (head >= 0) {
-      linear(s, w, s->heads[head], w.h + (size_t)(rows - 1) * H, H, 1, s->final_norm, w.logits,
-             head_rows, EPI_STORE, w.normed, st);
-    } else {
-      launch_rmsnorm_rows(w.h + (size_t)(rows - 1) * H, H, 1, H, s->final_norm, cf.rms_eps,
-                          w.normed, H, st);
-    }
-    launch_advance(c->dev_arr, nullptr, 1, rows, st);
-    check_hip(hipGetLastError(), "forward kernels");
-    if (normed_last)
-      check_hip(hipMemcpyAsync(normed_last, w.normed, sizeof(float) * H, hipMemcpyDeviceToHost,
-                               st),
-                "download state");
-    if (logits && head >= 0)
-      check_hip(hipMemcpyAsync(logits, w.logits, sizeof(float) * head_rows,
-                               hipMemcpyDeviceToHost, st),
-                "download logits");
-    check_hip(hipStreamSynchronize(st), "forward sync");
-    c->len += rows;
+    c->w.ensure(s, rows, attention_splits(s, c->len + rows), head_rows);
+    forward_rows(c, c->w, x, rows, head, logits, normed_last);
+  });
+}
+
+extern "C" int q3h_forward_embeds_noalloc(q3h_context *c, const float *x, int rows, int head,
+                                          float *logits, float *normed_last) {
+  return guard([&] {
+    if (!forward_args(c, x, rows, head, "q3h_forward_embeds_noalloc")) return;
+    require(rows <= Q3H_NOALLOC_MAX_ROWS, Q3H_E_CAPACITY,
+            "q3h_forward_embeds_noalloc: " + std::to_string(rows) + " rows exceed " +
+                std::to_string(Q3H_NOALLOC_MAX_ROWS));
+    q3h_stack *s = c->s;
+    q3h_device *dev = s->dev;
+    require(dev->scratch != nullptr, Q3H_E_STATE,
+            "q3h_forward_embeds_noalloc: the device has no scratch array");
+    const int head_rows = head >= 0 ? s->heads[head].N : 0;
+    Work w;  // a view of the array: owns nothing
+    require(work_carve(s, rows, attention_splits(s, c->len + rows), head_rows, dev->scratch,
+                       Q3H_NOALLOC_SCRATCH_BYTES, w),
+            Q3H_E_CAPACITY,
+            "q3h_forward_embeds_noalloc: the work buffers of " + std::to_string(rows) +
+                " rows at " + std::to_string(c->len + rows) + " positions exceed the " +
+                std::to_string(Q3H_NOALLOC_SCRATCH_BYTES) + "-byte scratch array");
+    std::lock_guard<std::mutex> lk(dev->scratch_mu);
+    check_hip(hipSetDevice(dev->ordinal), "hipSetDevice");
+    forward_rows(c, w, x, rows, head, logits, normed_last);
   });
 }
 

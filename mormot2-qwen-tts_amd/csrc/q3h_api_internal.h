@@ -17,6 +17,10 @@ struct q3h_device {
   std::string name;
   std::atomic<int64_t> bytes{0};
   std::atomic<int> stacks{0};
+  // the device address of this GPU's copy of the static scratch array of
+  // q3h_forward_embeds_noalloc, and the lock its calls take
+  void *scratch = nullptr;
+  std::mutex scratch_mu;
 };
 
 namespace q3h {
@@ -98,6 +102,12 @@ struct Work {
   void ensure(const struct ::q3h_stack *s, int rows, int splits, int head_rows);
   void release();
 };
+
+// w's buffers for (rows, splits, head_rows) carved from [base, base + cap),
+// each at a 256-byte boundary (w owns nothing: never release it); false when
+// they do not fit
+bool work_carve(const struct ::q3h_stack *s, int rows, int splits, int head_rows, void *base,
+                size_t cap, Work &w);
 
 // attention splits (the partial buffer) for contexts of up to `positions`
 int attention_splits(const struct ::q3h_stack *s, int positions);

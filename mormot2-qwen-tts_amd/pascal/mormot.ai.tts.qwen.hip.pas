@@ -32,6 +32,9 @@ const
   Q3H_E_STATE = -4;
   Q3H_E_NODEV = -5;
 
+  Q3H_NOALLOC_MAX_ROWS = 64;
+  Q3H_NOALLOC_SCRATCH_BYTES = 16 shl 20;
+
 type
   PPSingle = ^PSingle;
 
@@ -152,6 +155,11 @@ function q3h_context_time_attention(c: q3h_context; iters: integer;
 
 { the forward: TQwenLm.Forward (lm.pas:391-408), the head on the device }
 function q3h_forward_embeds(c: q3h_context; x: PSingle; rows, head: integer;
+  logits, normed_last: PSingle): integer; cdecl; external LIBQ3H;
+/// no counterpart in the reference: q3h_forward_embeds for callers that
+// cannot allocate device memory (work buffers in a static device array of
+// Q3H_NOALLOC_SCRATCH_BYTES per GPU; rows <= Q3H_NOALLOC_MAX_ROWS)
+function q3h_forward_embeds_noalloc(c: q3h_context; x: PSingle; rows, head: integer;
   logits, normed_last: PSingle): integer; cdecl; external LIBQ3H;
 function q3h_forward_embeds_batch(ctxs: Pq3h_context; n: integer; x: PSingle;
   heads: PInteger; logits, normed: PSingle): integer; cdecl; external LIBQ3H;

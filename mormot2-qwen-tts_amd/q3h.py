@@ -23,6 +23,8 @@ Q8_0 = 1
 BF16 = 2
 
 E_ARG, E_HIP, E_CAPACITY, E_STATE, E_NODEV = -1, -2, -3, -4, -5
+NOALLOC_MAX_ROWS = 64  # Q3H_NOALLOC_MAX_ROWS
+NOALLOC_SCRATCH_BYTES = 16 << 20  # Q3H_NOALLOC_SCRATCH_BYTES
 
 
 class Q3HError(RuntimeError):
@@ -147,6 +149,7 @@ SIGNATURES = {
     "q3h_context_read_kv": (_I, [_P, _I, _FP, _FP]),
     "q3h_context_time_attention": (_I, [_P, _I, _FP, ctypes.POINTER(ctypes.c_int64)]),
     "q3h_forward_embeds": (_I, [_P, _FP, _I, _I, _FP, _FP]),
+    "q3h_forward_embeds_noalloc": (_I, [_P, _FP, _I, _I, _FP, _FP]),
     "q3h_forward_embeds_batch": (_I, [ctypes.POINTER(_P), _I, _FP, _IP, _FP, _FP]),
     "q3h_frame_create": (_I, [_P, _P, ctypes.POINTER(FrameConfig), _FP,
                               ctypes.POINTER(_FP), _FP, ctypes.POINTER(_P)]),
@@ -313,8 +316,10 @@ class Context:
             _check(n)
         return n
 
-    def forward(self, x, head=-1, want_logits=True, want_normed=True):
-        """x [rows][hidden]; returns (logits or None, normed_last or None)."""
+    def forward(self, x, head=-1, want_logits=True, want_normed=True, noalloc=False):
+        """x [rows][hidden]; returns (logits or None, normed_last or None).
+        noalloc: through q3h_forward_embeds_noalloc (work buffers in the
+        device's static scratch array, at most NOALLOC_MAX_ROWS rows)."""
         x = _f32(x)
         if x.ndim == 1:
             x = x[None, :]
@@ -324,7 +329,8 @@ class Context:
             logits = np.empty(self.stack.head_rows[head], dtype=np.float32)
         normed = np.empty(hidden, dtype=np.float32) if want_normed else None
         # an unknown head index goes to the library, which reports it
-        _check(lib().q3h_forward_embeds(self.h, _fp(x), rows, head, _fp(logits), _fp(normed)))
+        fn = lib().q3h_forward_embeds_noalloc if noalloc else lib().q3h_forward_embeds
+        _check(fn(self.h, _fp(x), rows, head, _fp(logits), _fp(normed)))
         return logits, normed
 
     def fill_kv(self, k, v):
