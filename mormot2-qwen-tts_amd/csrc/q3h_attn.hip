@@ -13,6 +13,8 @@
 // own context) get the QK-norm (q_norm / k_norm), RoPE and the K/V append in
 // the prologue; rows that add several positions of one context at once
 // (prefill) run the separate append kernel first and these kernels unfused.
+#include <algorithm>
+
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
@@ -70,7 +72,10 @@ __device__ __forceinline__ void cvt8(const u32x4 (&r)[2], float (&o)[8]) {
 
 // Contexts of up to 256 positions (the frame step's talker and code
 // predictor at batch sizes that take the f32 path): one workgroup of NTS
-// threads per (query head h, row m), kv head h / GRP. The thread mapping of
+// threads per (query head h, row m), kv head h / GRP, covering NJ NTS / 16
+// positions (the launch sizes NJ to the positions it must cover, in steps of
+// 64: the load instructions, issued for every covered position, are most of
+// the kernel's time at these lengths). The thread mapping of
 // the split kernel below: thread t owns dims 8 (t % 16) .. + 7 of positions
 // t / 16 + (NTS / 16) j, so each load instruction of a wave reads 4 whole
 // consecutive cache rows (coalesced), scores are 8-term chains summed over a
@@ -86,14 +91,14 @@ __device__ __forceinline__ void cvt8(const u32x4 (&r)[2], float (&o)[8]) {
 //     prologue's vectors) instead of through the cache, so the cache rows
 //     read here are the positions before pos;
 //   - softmax in two passes over the workgroup (maximum, then sum).
-template <typename KV, bool FUSED, int GRP, int NTS>
+template <typename KV, bool FUSED, int GRP, int NTS, int NJ>
 __global__ __launch_bounds__(NTS) void k_attn_short(const RowDesc *__restrict__ rd,
                                                     const float *__restrict__ qkv,
                                                     const float2 *__restrict__ rope_cs,
                                                     const float *__restrict__ qkn,
                                                     float *__restrict__ outp, int layer, int kvh) {
-  constexpr int PG = NTS / 16;         // position groups
-  constexpr int NJ = kSplit / PG;      // positions per thread
+  constexpr int PG = NTS / 16;         // position groups (NJ positions per thread)
+  static_assert(NJ * PG <= kSplit, "at most 256 positions");
   constexpr int LW = sizeof(KV) / 2;   // 16-byte loads per 8 elements
   constexpr int NWV = NTS / 64;
   static_assert(NWV >= 3, "prologue waves");
@@ -753,8 +758,17 @@ int launch_g(const AttnArgs &a, int M, int positions, hipStream_t st, const hipE
   Q3H_LAUNCH((k_attn_split<KV, FUSED, G, P, T>), dim3(a.kvh, S, M), dim3(T), st, ev0, ev1,      \
              a.rd, a.qkv, a.rope_cs, a.qkn, a.layer, a.kvh, S, a.part)
   if (sh.len == kSplit && sh.threads == 0) {
-    Q3H_LAUNCH((k_attn_short<KV, FUSED, G, 512>), dim3(a.heads, M), dim3(512), st, ev0, ev1,
-               a.rd, a.qkv, a.rope_cs, a.qkn, a.out, a.layer, a.kvh);
+    // 32 position groups: 2 positions per thread for every 64 covered
+#define Q3H_SH(NJ)                                                                          \
+  Q3H_LAUNCH((k_attn_short<KV, FUSED, G, 512, NJ>), dim3(a.heads, M), dim3(512), st, ev0, ev1, \
+             a.rd, a.qkv, a.rope_cs, a.qkn, a.out, a.layer, a.kvh)
+    switch ((std::max(positions, 1) + 63) / 64) {
+      case 1: Q3H_SH(2); break;
+      case 2: Q3H_SH(4); break;
+      case 3: Q3H_SH(6); break;
+      default: Q3H_SH(8); break;
+    }
+#undef Q3H_SH
   } else if (sh.len == 64) {
     Q3H_S(64, 256);
   } else if constexpr (sizeof(KV) == 2) {

@@ -10,6 +10,7 @@
 // needs more position splits).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <random>
@@ -386,9 +387,8 @@ struct FrameSlice {
   Work tw, cw;
   FrameDev fd{};  // the view of the slice's streams
   hipStream_t stream = nullptr;
-  hipGraph_t graph = nullptr;
-  hipGraphExec_t exec = nullptr;
-  int graph_positions = 0;  // attention positions the captured graph covers
+  // the captured steps, by the attention positions each covers (ascending)
+  std::vector<std::pair<int, hipGraphExec_t>> graphs;
 };
 
 struct q3h_frame {
@@ -417,12 +417,18 @@ namespace {
 
 void drop_graphs(q3h_frame *f) {
   for (FrameSlice &sl : f->slices) {
-    if (sl.exec) (void)hipGraphExecDestroy(sl.exec);
-    if (sl.graph) (void)hipGraphDestroy(sl.graph);
-    sl.exec = nullptr;
-    sl.graph = nullptr;
-    sl.graph_positions = 0;
+    for (auto &g : sl.graphs) (void)hipGraphExecDestroy(g.second);
+    sl.graphs.clear();
   }
+}
+
+// The attention positions a captured step covers for contexts of up to len
+// positions: up to 256 in steps of 64 (the single-workgroup attention loads
+// what it covers), beyond that in steps of 256 with one step of headroom (the
+// split attention leaves extra splits empty); at most max_positions.
+int graph_cover(int len, int max_positions) {
+  const int cap = len <= 256 ? (len + 63) / 64 * 64 : ((len + 255) / 256 + 1) * 256;
+  return std::min(max_positions, cap);
 }
 
 // every slice's work done (the frame's state may be read or changed)
@@ -946,27 +952,35 @@ extern "C" int q3h_frame_step(q3h_frame *f, int32_t *codes, int32_t *alive) {
         if (f->started[s]) slen = std::max(slen, f->host_len[s] + 1);
       if (slen == 0) continue;  // no stream of the slice runs (its codes read as -1)
       if (c.use_graph) {
-        if (!sl.exec || slen > sl.graph_positions) {
-          if (sl.exec) {
-            (void)hipGraphExecDestroy(sl.exec);
-            sl.exec = nullptr;
+        // the captured step that covers slen; on the first capture every
+        // cover up to 256 positions is captured too, so that growing
+        // contexts switch graphs without capturing again
+        auto find = [&]() -> hipGraphExec_t {
+          for (auto &g : sl.graphs)
+            if (g.first >= slen) return g.second;
+          return nullptr;
+        };
+        hipGraphExec_t exec = find();
+        if (!exec) {
+          std::vector<int> covers = {graph_cover(slen, c.max_positions)};
+          if (sl.graphs.empty())
+            for (int p = 64; p <= 256; p += 64)
+              if (p > slen) covers.push_back(graph_cover(p, c.max_positions));
+          std::sort(covers.begin(), covers.end());
+          covers.erase(std::unique(covers.begin(), covers.end()), covers.end());
+          for (int cover : covers) {
+            hipGraph_t graph =
+                capture_graph(sl.stream, [&] { enqueue_step(f, sl, cover, sl.stream); });
+            hipGraphExec_t e = nullptr;
+            const hipError_t r = hipGraphInstantiate(&e, graph, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(graph);
+            check_hip(r, "hipGraphInstantiate");
+            sl.graphs.emplace_back(cover, e);
           }
-          if (sl.graph) {
-            (void)hipGraphDestroy(sl.graph);
-            sl.graph = nullptr;
-          }
-          // capture with headroom so that the graph is rebuilt rarely: the
-          // attention covers up to 256 positions in one split, beyond that up
-          // to 256 positions more than the longest context (rows shorter than
-          // the capture leave their extra splits empty)
-          const int cap = slen <= 256 ? 256 : ((slen + 255) / 256 + 1) * 256;
-          const int cap_positions = std::min(c.max_positions, cap);
-          sl.graph = capture_graph(sl.stream, [&] { enqueue_step(f, sl, cap_positions, sl.stream); });
-          check_hip(hipGraphInstantiate(&sl.exec, sl.graph, nullptr, nullptr, 0),
-                    "hipGraphInstantiate");
-          sl.graph_positions = cap_positions;
+          std::sort(sl.graphs.begin(), sl.graphs.end());
+          exec = find();
         }
-        check_hip(hipGraphLaunch(sl.exec, sl.stream), "hipGraphLaunch");
+        check_hip(hipGraphLaunch(exec, sl.stream), "hipGraphLaunch");
       } else {
         enqueue_step(f, sl, slen, sl.stream);
         check_hip(hipGetLastError(), "frame kernels");
