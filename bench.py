@@ -251,10 +251,12 @@ def cpu_frames(q3o, frame, pre, gpu_codes, budget_s, max_frames, threads):
     return dict(value=n / dt, threads=threads, frames=n, seconds=dt, codes_equal=equal)
 
 
-def gemv_roofline(ts, args):
+def gemv_roofline(ts, args, cs=None):
     """The dominant kernel: the Q8_0 matrix-vector products of one talker
     decode step. achieved = algorithmic bytes per launch / the kernels' own
-    average execution time (events attached to each launch)."""
+    average execution time (events attached to each launch). With cs: the
+    same for one code-predictor forward (5 layers + one 2048-row head, 85.8 MB:
+    after the first pass its weights stay in the 256 MB Infinity Cache)."""
     us, launches, nbytes = ts.time_gemv(head=0, iters=args.gemv_iters, mode=2)
     per_launch = nbytes / launches
     achieved = per_launch / (us * 1e-6) / 1e9
@@ -263,12 +265,23 @@ def gemv_roofline(ts, args):
         wall, _, _ = ts.time_gemv(head=0, iters=args.gemv_iters, mode=1)
     log(f"gemv: {launches} launches/step, kernel {us:.2f} us/launch "
         f"({achieved:.0f} GB/s), graph wall {wall if wall is None else round(wall, 2)} us/launch")
-    return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                frac=round(achieved / HBM_PEAK_GBS, 4), traffic=GEMV_TRAFFIC_PER_LAUNCH,
-                traffic_source="profiles/gemv_q8_decode_step_traffic.md",
-                kernel="k_gemv_q8v (Q8_0 matrix-vector products of one talker decode step)",
-                bytes_per_launch=int(per_launch), us_per_launch=round(us, 3),
-                graph_wall_us_per_launch=None if wall is None else round(wall, 3))
+    out = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+               frac=round(achieved / HBM_PEAK_GBS, 4), traffic=GEMV_TRAFFIC_PER_LAUNCH,
+               traffic_source="profiles/gemv_q8_decode_step_traffic.md",
+               kernel="k_gemv_q8v (Q8_0 matrix-vector products of one talker decode step)",
+               bytes_per_launch=int(per_launch), us_per_launch=round(us, 3),
+               graph_wall_us_per_launch=None if wall is None else round(wall, 3))
+    if cs is not None:
+        cus, cl, cb = cs.time_gemv(head=0, iters=args.gemv_iters, mode=2)
+        cwall = None if args.no_graph else cs.time_gemv(head=0, iters=args.gemv_iters, mode=1)[0]
+        cgbs = cb / cl / (cus * 1e-6) / 1e9
+        log(f"gemv (code predictor, cache-resident): {cl} launches/step, kernel {cus:.2f} "
+            f"us/launch ({cgbs:.0f} GB/s), graph wall {cwall} us/launch")
+        out["code_predictor"] = dict(launches=cl, bytes_per_launch=int(cb / cl),
+                                     us_per_launch=round(cus, 3), achieved_gbs=round(cgbs, 1),
+                                     graph_wall_us_per_launch=None if cwall is None
+                                     else round(cwall, 3))
+    return out
 
 
 # algorithmic weight bytes of one frame step: talker layers + head, and 15
@@ -635,6 +648,12 @@ def main():
                          "events are not for runs under a kernel tracer)")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the matrix-vector roofline measurement (profiling runs)")
+    ap.add_argument("--gemv-stack", choices=["talker", "code", "both"], default="talker",
+                    help="with --gemv-only: the stack whose products are timed (code: the "
+                         "code predictor)")
+    ap.add_argument("--gemv-mode", type=int, choices=[0, 1, 2], default=2,
+                    help="with --gemv-only: 0 direct launches (tracers, counters), 1 graph "
+                         "replay, 2 events attached to each launch")
     ap.add_argument("--long-attn-only", action="store_true",
                     help="only the long-context attention measurement (profiling runs)")
     ap.add_argument("--copy-only", action="store_true",
@@ -680,8 +699,18 @@ def main():
     ts, cs, tables, f32 = build_model(dev, args.seed, max_pos, act_q8,
                                       q3h.F32 if f32w else q3h.Q8_0, int(args.kv16))
     if args.gemv_only:
-        roofline = gemv_roofline(ts, args)
-        print(json.dumps({"roofline": roofline}), flush=True)
+        # the products of one decode step of the chosen stack(s), iters times
+        # (mode 0 direct launches for kernel tracers and counters, 1 graph
+        # replay, 2 events attached to each launch)
+        out = {}
+        for name, st in (("talker", ts), ("code_predictor", cs)):
+            if args.gemv_stack not in (name.split("_")[0], "both"):
+                continue
+            us, n_l, nb = st.time_gemv(head=0, iters=args.gemv_iters, mode=args.gemv_mode)
+            out[name] = dict(launches=n_l, bytes_per_launch=int(nb / n_l),
+                             us_per_launch=round(us, 3), mode=args.gemv_mode)
+            log(f"gemv {name}: {n_l} launches, {us:.2f} us per launch (mode {args.gemv_mode})")
+        print(json.dumps({"gemv": out}), flush=True)
         ts.destroy()
         cs.destroy()
         dev.close()
@@ -707,7 +736,8 @@ def main():
                     step_us_p50=round(1e6 * float(np.median(f_lat)), 1))
         log(f"{CONFIG2_FRAMES} frames: {full['frames_per_s']:.1f} frames/s")
 
-    roofline = gemv_roofline(ts, args) if not (f32w or args.no_roofline) else None
+    roofline = gemv_roofline(ts, args, cs if b1 else None) \
+        if not (f32w or args.no_roofline) else None
 
     # the same frames drawn with the qwen_tts default sampling (temperature 0.9,
     # top-k 50 on both choosers, talker.pas:208-216): the sampler's cost

@@ -166,6 +166,17 @@ int q3h_forward_embeds(q3h_context *c, const float *x, int rows, int head,
 int q3h_forward_embeds_noalloc(q3h_context *c, const float *x, int rows, int head,
                                float *logits, float *normed_last);
 
+/* TQwenLm.Forward with TQwenLm.Probe set (lm.pas:139-142, 380-389: the
+   probe receives the output of every layer, "name.layerN", then the normed
+   state): q3h_forward_embeds, plus layer_out [layers][rows][hidden] (host
+   f32, nullable) receiving the raw output of each layer for every row (the
+   residual stream after the layer's down projection), so that a difference
+   against another implementation can be located at a layer. The outputs are
+   those of q3h_forward_embeds; the copies add one device-to-device copy per
+   layer. */
+int q3h_forward_embeds_probe(q3h_context *c, const float *x, int rows, int head,
+                             float *logits, float *normed_last, float *layer_out);
+
 /* no reference counterpart (the reference is single-stream): one row per
    context, n contexts of the same stack at their own positions;
    x [n][hidden]; heads [n] (or NULL: no logits); logits [n][head rows of

@@ -159,6 +159,14 @@ void linear(const q3h_stack *s, Work &w, const Mat &W, const float *x, int ldx, 
   }
 }
 
+// the residual stream after layer l into the probe buffer (when one is set)
+static void probe_layer(const LayerIO &io, const Work &w, int l, int M, int H, hipStream_t st) {
+  if (io.layer_out)
+    check_hip(hipMemcpyAsync(io.layer_out + (size_t)l * M * H, w.h, sizeof(float) * M * H,
+                             hipMemcpyDeviceToDevice, st),
+              "probe copy");
+}
+
 // The int8 path over M <= kPartialRows rows: every product leaves its chunk
 // partials (one wave per 16 rows and 256 columns over the whole chip), and
 // the consumer adds them in chunk order: the attention prologue (q/k/v, decode
@@ -209,6 +217,7 @@ static void run_layers_partial(const q3h_stack *s, Work &w, int M, bool fused,
     const float *nw = next ? s->layers[l + 1].in_norm : io.final_norm;
     launch_residual_quantize(w.h, w.gpart, gemm_i8_chunks(I), M, H, nw, eps,
                              nw ? &w.xa : nullptr, st);
+    probe_layer(io, w, l, M, H, st);
   }
 }
 
@@ -228,7 +237,8 @@ bool f32_slice_path(const q3h_stack *s, int M) {
 }
 
 static void run_layers_f32(const q3h_stack *s, Work &w, int M, int positions, bool fused,
-                           bool single_context, hipStream_t st) {
+                           const LayerIO &io, hipStream_t st) {
+  const bool single_context = io.single_context;
   const q3h_stack_config &c = s->cfg;
   const int H = c.hidden, hd = c.head_dim, NQ = c.heads * hd, NKV = c.kv_heads * hd;
   const int I = c.intermediate, ldq = NQ + 2 * NKV;
@@ -262,6 +272,7 @@ static void run_layers_f32(const q3h_stack *s, Work &w, int M, int positions, bo
     launch_gemm_f32_part(L.down, w.act, I, M, w.gpart, st);
     const float *next = l + 1 < c.layers ? s->layers[l + 1].in_norm : nullptr;
     launch_resid_norm(w.h, w.gpart, M, H, next, eps, w.normed, st);
+    probe_layer(io, w, l, M, H, st);
   }
 }
 
@@ -282,7 +293,7 @@ void run_layers(const q3h_stack *s, Work &w, int M, int positions, bool fused, h
     return;
   }
   if (f32_slice_path(s, M)) {
-    run_layers_f32(s, w, M, positions, fused, io.single_context, st);
+    run_layers_f32(s, w, M, positions, fused, io, st);
     return;
   }
   for (int l = 0; l < c.layers; l++) {
@@ -307,6 +318,7 @@ void run_layers(const q3h_stack *s, Work &w, int M, int positions, bool fused, h
       launch_gemm_i8(L.o, w.xa, M, EPI_ADD, w.h, H, st);
       linear(s, w, L.gu, w.h, H, M, L.post_norm, w.act, I, EPI_SWIGLU, nullptr, st);
       linear(s, w, L.down, w.act, I, M, nullptr, w.h, H, EPI_ADD, nullptr, st);
+      probe_layer(io, w, l, M, H, st);
       continue;
     }
     // QK-norm, RoPE, K/V append (in the attention prologue when fused)
@@ -335,6 +347,7 @@ void run_layers(const q3h_stack *s, Work &w, int M, int positions, bool fused, h
     linear(s, w, L.gu, w.h, H, M, L.post_norm, w.act, I, EPI_SWIGLU, nullptr, st);
     // down + residual
     linear(s, w, L.down, w.act, I, M, nullptr, w.h, H, EPI_ADD, nullptr, st);
+    probe_layer(io, w, l, M, H, st);
   }
 }
 
@@ -800,6 +813,7 @@ q3h_context *new_context(q3h_stack *s, int max_positions) {
 
 void free_context(q3h_context *ctx) {
   ctx->w.release();
+  dev_free(ctx->probe);
   dev_free(ctx->k);  // the values share this allocation
   dev_free(ctx->dev);
   dev_free(ctx->dev_arr);
@@ -1008,7 +1022,7 @@ bool forward_args(const q3h_context *c, const float *x, int rows, int head, cons
 // of length + rows positions and the head's rows): blocks until the outputs
 // are in host memory
 void forward_rows(q3h_context *c, Work &w, const float *x, int rows, int head, float *logits,
-                  float *normed_last) {
+                  float *normed_last, float *layer_out = nullptr) {
   q3h_stack *s = c->s;
   const q3h_stack_config &cf = s->cfg;
   const int H = cf.hidden;
@@ -1020,6 +1034,18 @@ void forward_rows(q3h_context *c, Work &w, const float *x, int rows, int head, f
   launch_prep(c->dev_arr, nullptr, 1, rows, w.rd, st);
   LayerIO io;
   io.single_context = true;
+  const size_t probe_bytes = sizeof(float) * cf.layers * rows * H;
+  if (layer_out) {
+    if (c->probe_bytes < probe_bytes) {
+      check_hip(hipStreamSynchronize(st), "probe sync");
+      dev_free(c->probe);
+      c->probe = nullptr;
+      c->probe_bytes = 0;
+      c->probe = (float *)dev_alloc(probe_bytes);
+      c->probe_bytes = probe_bytes;
+    }
+    io.layer_out = c->probe;
+  }
   run_layers(s, w, rows, positions, rows == 1, st, io);
   // final norm of the last row, fused into the head product when there is one
   if (head >= 0) {
@@ -1039,6 +1065,9 @@ void forward_rows(q3h_context *c, Work &w, const float *x, int rows, int head, f
     check_hip(hipMemcpyAsync(logits, w.logits, sizeof(float) * head_rows, hipMemcpyDeviceToHost,
                              st),
               "download logits");
+  if (layer_out)
+    check_hip(hipMemcpyAsync(layer_out, c->probe, probe_bytes, hipMemcpyDeviceToHost, st),
+              "download layer outputs");
   check_hip(hipStreamSynchronize(st), "forward sync");
   c->len += rows;
 }
@@ -1054,6 +1083,18 @@ extern "C" int q3h_forward_embeds(q3h_context *c, const float *x, int rows, int 
     const int head_rows = head >= 0 ? s->heads[head].N : 0;
     c->w.ensure(s, rows, attention_splits(s, c->len + rows), head_rows);
     forward_rows(c, c->w, x, rows, head, logits, normed_last);
+  });
+}
+
+extern "C" int q3h_forward_embeds_probe(q3h_context *c, const float *x, int rows, int head,
+                                        float *logits, float *normed_last, float *layer_out) {
+  return guard([&] {
+    if (!forward_args(c, x, rows, head, "q3h_forward_embeds_probe")) return;
+    q3h_stack *s = c->s;
+    check_hip(hipSetDevice(s->dev->ordinal), "hipSetDevice");
+    const int head_rows = head >= 0 ? s->heads[head].N : 0;
+    c->w.ensure(s, rows, attention_splits(s, c->len + rows), head_rows);
+    forward_rows(c, c->w, x, rows, head, logits, normed_last, layer_out);
   });
 }
 

@@ -151,6 +151,7 @@ struct LayerIO {
   bool input_quantized = false;       // w.xa already holds layer 0's normed, quantized input
   const float *final_norm = nullptr;  // after the last layer: RMSNorm with it, quantized into w.xa
   bool single_context = false;        // the rows are consecutive positions of one context
+  float *layer_out = nullptr;         // [layers][M][hidden] device: w.h after each layer
 };
 // whether run_layers takes the int8 partial-product path for M rows of stack s
 bool partial_path(const struct ::q3h_stack *s, int M);
@@ -186,6 +187,8 @@ struct q3h_context {
   q3h::CtxDev **dev_arr = nullptr;  // {dev}
   hipStream_t stream = nullptr;
   q3h::Work w;
+  float *probe = nullptr;  // the layer outputs of q3h_forward_embeds_probe
+  size_t probe_bytes = 0;
 };
 
 // the text projection (q3h_text.hip)
