@@ -19,9 +19,10 @@
 //    operations), times 1/sqrt(128);
 //  - softmax: maximum, exp_ieee(s - max), double sum, inv = (float)(1/sum),
 //    weights s * inv;
-//  - values: 4 chains of fused multiply-adds over the positions p = j mod 4
-//    (a thread per chain and pair of dims, 512 coalesced bytes per key and
-//    wave), joined as (c0 + c1) + (c2 + c3);
+//  - values: 8 chains of fused multiply-adds over the positions p = j mod 8
+//    (wave w runs chain w % 8 for 128 / (waves / 8) of the dims, 512
+//    coalesced bytes per key and wave), joined as ((c0 + c1) + (c2 + c3)) +
+//    ((c4 + c5) + (c6 + c7));
 //  - the head's 128 outputs quantized per 32-block (ggml quantize_row_q8_0_ref
 //    semantics) into the operand tiles of the int8 product.
 // The attention itself follows src/tts/mormot.ai.tts.qwen.lm.pas (TQwenLm.
@@ -37,7 +38,7 @@ namespace q3h {
 namespace {
 
 constexpr int HD = 128;
-constexpr int NT = 512;
+constexpr int NCH = 8;  // value chains
 
 template <typename KV>
 __device__ __forceinline__ void load8(const KV *p, float (&o)[8]) {
@@ -104,15 +105,18 @@ __device__ __forceinline__ float row16_tree(float v) {
 // read of its K/V; nch > 0: the q/k/v come as nch chunk partials. SU / VU:
 // the key rounds of the score loop / the positions of the value chains whose
 // loads are issued together (deeper for long contexts).
-template <typename KV, bool FUSED, int GRP, int SU, int VU>
+template <typename KV, bool FUSED, int GRP, int SU, int VU, int NT>
 __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *qkv,
                                                const float *qkn, const float2 *rope_cs,
                                                int8_t *xq, int ldq, int layer, int nch) {
+  constexpr int NWV = NT / 64;
+  constexpr int DPW = 16 / NWV;  // dims per lane in the value chains (2 or 1)
+  static_assert(NWV % NCH == 0 && DPW * 64 * (NWV / NCH) == HD, "8 chains over 128 dims");
   extern __shared__ float sc[];  // [GRP][L]: scores, then e^(score - max)
   __shared__ float qs[GRP][HD], kn[HD], vn[HD];
-  __shared__ float cv[4][GRP][HD];
-  __shared__ float redf[GRP][NT / 64];
-  __shared__ double redd[GRP][NT / 64];
+  __shared__ float cv[NCH][GRP][HD];
+  __shared__ float redf[GRP][NWV];
+  __shared__ double redd[GRP][NWV];
   const int g = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
   const int kvh = gridDim.x, heads = kvh * GRP, M = gridDim.y;
   const int lane = t & 63, wave = t >> 6;
@@ -135,11 +139,12 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
   const KV *vc = reinterpret_cast<const KV *>(d.v) + head_off;
   constexpr int KG = NT / 16;
   const int kg = t >> 4, li = t & 15;
-  const int ch = wave & 3, dim = (wave >> 2) * 64 + lane;
+  // value chain ch over positions ch, ch + 8, ...; dims dim0 + 64 e, e < DPW
+  const int ch = wave % NCH, dim0 = (wave / NCH) * 64 + lane;
 
   if (FUSED) {
     // vector j: query head g GRP + j (j < GRP), the new k (j == GRP), v (GRP + 1)
-    for (int j = wave; j < GRP + 2; j += NT / 64) {
+    for (int j = wave; j < GRP + 2; j += NWV) {
       const int col = j < GRP ? (g * GRP + j) * HD : j == GRP ? NQ + g * HD : NQ + (kvh + g) * HD;
       float x0, x1;
       qkv_pair(qkv, ldq, nch, M, m, col + lane, x0, x1);
@@ -233,7 +238,7 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
     for (int j = 0; j < GRP; j++) {
       float v = redf[j][0];
 #pragma unroll
-      for (int w = 1; w < NT / 64; w++) v = fmaxf(v, redf[j][w]);
+      for (int w = 1; w < NWV; w++) v = fmaxf(v, redf[j][w]);
       mx[j] = v;
     }
     double sum[GRP];
@@ -256,35 +261,44 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
     for (int j = 0; j < GRP; j++) {
       double s2 = 0.0;
 #pragma unroll
-      for (int w = 0; w < NT / 64; w++) s2 += redd[j][w];
+      for (int w = 0; w < NWV; w++) s2 += redd[j][w];
       inv[j] = (float)(1.0 / s2);
     }
   }
 
-  // values: chain ch = wave % 4 over positions p = ch mod 4, dim (wave / 4) 64
-  // + lane, every head of the group; the loads of VU positions issued together
+  // values: chain ch = wave % 8 over positions p = ch mod 8, dims dim0 + 64 e,
+  // every head of the group; the loads of VU positions issued together
   {
-    float c[GRP];
+    float c[DPW][GRP];
 #pragma unroll
-    for (int j = 0; j < GRP; j++) c[j] = 0.f;
-    const float vnd = FUSED ? vn[dim] : 0.f;
-    for (int p0 = ch; p0 < L; p0 += 4 * VU) {
-      float v[VU];
+    for (int e = 0; e < DPW; e++)
 #pragma unroll
-      for (int u = 0; u < VU; u++) v[u] = (float)vc[(size_t)min(p0 + 4 * u, L - 1) * HD + dim];
+      for (int j = 0; j < GRP; j++) c[e][j] = 0.f;
+    float vnd[DPW];
+#pragma unroll
+    for (int e = 0; e < DPW; e++) vnd[e] = FUSED ? vn[dim0 + 64 * e] : 0.f;
+    for (int p0 = ch; p0 < L; p0 += NCH * VU) {
+      float v[VU][DPW];
+#pragma unroll
+      for (int u = 0; u < VU; u++)
+#pragma unroll
+        for (int e = 0; e < DPW; e++)
+          v[u][e] = (float)vc[(size_t)min(p0 + NCH * u, L - 1) * HD + dim0 + 64 * e];
       // the new position: its own v; past L: zero (the clamped load may have
       // read the new row before it was written)
 #pragma unroll
       for (int u = 0; u < VU; u++) {
-        const int p = p0 + 4 * u;
-        v[u] = p >= L ? 0.f : FUSED && p == pos ? vnd : v[u];
+        const int p = p0 + NCH * u;
+#pragma unroll
+        for (int e = 0; e < DPW; e++)
+          v[u][e] = p >= L ? 0.f : FUSED && p == pos ? vnd[e] : v[u][e];
       }
       // weights of the round read together; past L a zero weight times a zero
       // value adds an exact zero to the chain
       float wgt[VU][GRP];
 #pragma unroll
       for (int u = 0; u < VU; u++) {
-        const int p = p0 + 4 * u;  // the same for the whole wave
+        const int p = p0 + NCH * u;  // the same for the whole wave
 #pragma unroll
         for (int j = 0; j < GRP; j++) {
           const float e = sc[j * L + min(p, L - 1)];
@@ -294,18 +308,23 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
 #pragma unroll
       for (int u = 0; u < VU; u++)
 #pragma unroll
-        for (int j = 0; j < GRP; j++) c[j] = fmaf(wgt[u][j], v[u], c[j]);
+        for (int j = 0; j < GRP; j++)
+#pragma unroll
+          for (int e = 0; e < DPW; e++) c[e][j] = fmaf(wgt[u][j], v[u][e], c[e][j]);
     }
 #pragma unroll
-    for (int j = 0; j < GRP; j++) cv[ch][j][dim] = c[j];
+    for (int j = 0; j < GRP; j++)
+#pragma unroll
+      for (int e = 0; e < DPW; e++) cv[ch][j][dim0 + 64 * e] = c[e][j];
   }
   __syncthreads();
 
   // quantize each head's 128 outputs per 32-block (a 32-lane half-wave each)
   for (int i = t; i < GRP * HD; i += NT) {
     const int j = i / HD, k = i % HD, h = g * GRP + j;
-    const float o =
-        __fadd_rn(__fadd_rn(cv[0][j][k], cv[1][j][k]), __fadd_rn(cv[2][j][k], cv[3][j][k]));
+    const float o = __fadd_rn(
+        __fadd_rn(__fadd_rn(cv[0][j][k], cv[1][j][k]), __fadd_rn(cv[2][j][k], cv[3][j][k])),
+        __fadd_rn(__fadd_rn(cv[4][j][k], cv[5][j][k]), __fadd_rn(cv[6][j][k], cv[7][j][k])));
     float amax = fabsf(o);
 #pragma unroll
     for (int s2 = 16; s2 >= 1; s2 >>= 1) amax = fmaxf(amax, __shfl_xor(amax, s2));
@@ -324,14 +343,14 @@ bool attn_x_supported(int heads, int kvh, int head_dim, int max_positions) {
          (size_t)max_positions * (heads / kvh) <= (size_t)kAttnXMaxPositions;
 }
 
-template <typename KV, bool F, int SU, int VU>
+template <typename KV, bool F, int SU, int VU, int NT>
 void attn_x_grp(const AttnArgs &a, int M, int nch, const QAct &xa, int max_positions,
                 hipStream_t st) {
   const dim3 grid(a.kvh, M);
   const int grp = a.heads / a.kvh;
   const size_t lds = sizeof(float) * (size_t)grp * max_positions;
 #define Q3H_ATTNX(G)                                                                           \
-  hipLaunchKernelGGL((k_attn_x<KV, F, G, SU, VU>), grid, dim3(NT), lds, st, a.rd, a.qkv,      \
+  hipLaunchKernelGGL((k_attn_x<KV, F, G, SU, VU, NT>), grid, dim3(NT), lds, st, a.rd, a.qkv,  \
                      a.qkn, a.rope_cs, xa.q, a.ldq, a.layer, nch)
   if (grp == 1)
     Q3H_ATTNX(1);
@@ -342,14 +361,19 @@ void attn_x_grp(const AttnArgs &a, int M, int nch, const QAct &xa, int max_posit
 #undef Q3H_ATTNX
 }
 
-// short contexts (the code predictor's 16 positions): one round of each loop
+// short contexts (the code predictor's 16 positions): 512 threads, one round
+// of each loop; longer ones 128 values per round, and 1024 threads for the
+// decode rows (a prefill launches a workgroup per row already; results do not
+// depend on the thread count)
 template <typename KV, bool F>
 void attn_x_len(const AttnArgs &a, int M, int nch, const QAct &xa, int max_positions,
                 hipStream_t st) {
-  if (max_positions <= NT / 16)
-    attn_x_grp<KV, F, 1, 4>(a, M, nch, xa, max_positions, st);
+  if (max_positions <= 32)
+    attn_x_grp<KV, F, 1, 4, 512>(a, M, nch, xa, max_positions, st);
+  else if (F)
+    attn_x_grp<KV, F, 8, 16, 1024>(a, M, nch, xa, max_positions, st);
   else
-    attn_x_grp<KV, F, 8, 32>(a, M, nch, xa, max_positions, st);
+    attn_x_grp<KV, F, 8, 16, 512>(a, M, nch, xa, max_positions, st);
 }
 
 void launch_attn_x(const AttnArgs &a, int M, bool fused, bool kv16, int qkv_chunks,

@@ -474,14 +474,17 @@ int q3o_forward_embeds_traced(q3o_ctx *c, const float *x, int rows, float *norme
         }
         const float inv = (float)(1.0 / sum);
         float *o = att + r * NQ + hh * D;
-        float *ch = (float *)calloc((size_t)4 * D, sizeof(float));
+        /* 8 chains over the positions p mod 8, joined as a balanced tree */
+        float *ch = (float *)calloc((size_t)8 * D, sizeof(float));
         for (int p = 0; p < n; p++) {
           const float *vc = c->v + kv_off(c, l, g, p);
           const float w = sc[p] * inv;
-          float *cj = ch + (size_t)(p & 3) * D;
+          float *cj = ch + (size_t)(p & 7) * D;
           for (int d = 0; d < D; d++) cj[d] = fmaf(w, vc[d], cj[d]);
         }
-        for (int d = 0; d < D; d++) o[d] = (ch[d] + ch[D + d]) + (ch[2 * D + d] + ch[3 * D + d]);
+        for (int d = 0; d < D; d++)
+          o[d] = ((ch[d] + ch[D + d]) + (ch[2 * D + d] + ch[3 * D + d])) +
+                 ((ch[4 * D + d] + ch[5 * D + d]) + (ch[6 * D + d] + ch[7 * D + d]));
         free(ch);
         free(sc);
       }
