@@ -24,6 +24,7 @@
 #include <hip/hip_runtime.h>
 
 #include "q3h_api_internal.h"
+#include "q3h_math.h"
 
 namespace q3h {
 namespace {
@@ -39,6 +40,24 @@ __device__ __forceinline__ float silu_mul_f(float g, float u) { return g / (1.0f
 // SiLU of the text projection: 0 below -80 (where e^-v would overflow)
 __device__ __forceinline__ float silu_clamp_f(float v) {
   return v < -80.0f ? 0.0f : v / (1.0f + expf(-v));
+}
+
+typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+
+// 8 Q8_0 quants (two dwords, little-endian bytes) as 8 bf16: the high halves
+// of their f32 values, exact (at most 8 significant bits)
+__device__ __forceinline__ bf8v q8_bf16x8(uint2 w) {
+  const uint32_t w2[2] = {w.x, w.y};
+  u32x4v o;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t word = w2[i >> 1], sh = 16 * (i & 1);
+    const uint32_t f0 = __float_as_uint((float)(int8_t)(word >> sh));
+    const uint32_t f1 = __float_as_uint((float)(int8_t)(word >> (sh + 8)));
+    o[i] = (f0 >> 16) | (f1 & 0xffff0000u);
+  }
+  return __builtin_bit_cast(bf8v, o);
 }
 
 // the sums of a tile, met in LDS (red[wave][t][q][lane]: the MFMA result
@@ -251,20 +270,6 @@ __global__ __launch_bounds__(64 * WN) void k_gemm_f32_m64(const float *__restric
 // bf16 planes, double buffered), the weights come pre-split (Mat::x3) to
 // registers one chunk ahead. 24 MFMAs per wave and chunk instead of 32 of
 // the f32 kind, each a sixteenth of the cycles per flop.
-typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
-typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ void split3(float x, uint32_t &h, uint32_t &m, uint32_t &l) {
-  const uint32_t u = __float_as_uint(x);
-  const uint32_t hb = u & 0xffff0000u;
-  const float r1 = x - __uint_as_float(hb);
-  const uint32_t mb = __float_as_uint(r1) & 0xffff0000u;
-  const float r2 = r1 - __uint_as_float(mb);
-  h = hb >> 16;
-  m = mb >> 16;
-  l = __float_as_uint(r2) >> 16;
-}
-
 template <int WN, int EPI>
 __global__ __launch_bounds__(64 * WN) void k_gemm_x3_m64(const uint16_t *__restrict__ w3,
                                                          const float *__restrict__ x, int ldx,
@@ -397,74 +402,104 @@ __global__ void k_split3(const float *__restrict__ f, size_t n, uint16_t *__rest
 }
 
 // The same products with Q8_0 weights (int8 quants [N][K], then fp16 scales
-// [N][K/32]) and f32 activations: a 64-column step per load, lane l taking
-// the 16 quants 16 (l / 16) .. + 15 of its row (one 16-byte load) and the
-// scale of their 32-block, the 16 activations of the same columns of its
-// activation row (four 16-byte loads); MFMA i of the step takes column
-// 16 (l / 16) + i in k slot l / 16, the weight as quant x scale in fp32 (the
-// dequantized weight, exactly). The epilogues are those of k_gemm_f32.
+// [N][K/32]) and f32 activations, on the bf16 matrix cores. A quant is an
+// integer of at most 8 significant bits, exact in bf16; an activation is
+// split exactly into three bf16 parts (split3). One 32-block of 16 weight
+// rows and 16 activation rows is three v_mfma_f32_16x16x32_bf16 (low, middle,
+// high part, each adding exact products in fp32) into a block sum, which is
+// scaled by the weight row's fp16 block scale and added to the row's fp32
+// sum: y = sum over blocks of d * (sum over the block of x q).
+//
+// Lane l holds, per block, the 8 quants 8 (l / 16) .. + 7 of weight row
+// n0 + l % 16 (one 8-byte load) and the same 8 columns of activation row
+// m0 + 16 t + l % 16 of each tile t (two 16-byte loads), and receives
+// D[4 (l / 16) + q][l % 16]: the output layout of k_gemm_f32, whose
+// epilogues this kernel shares. A workgroup owns 16 weight rows and TM tiles
+// of 16 activation rows; its waves take NBW blocks each. A wave issues the
+// loads of all its weights and scales first, then of its activations D
+// blocks ahead of the arithmetic, so that it waits for few memory round
+// trips. (Its time is the activation loads: every workgroup reads all M rows
+// over its K range; k_gemm_q8x_m64 shares them over 64 weight rows.)
+template <int KK>
+constexpr int q8x_blocks_per_wave() {
+  return KK <= 1024 ? 4 : KK / 256;  // at most 8 waves
+}
+
 template <int TM, int KK, int EPI>
-__global__ __launch_bounds__(64 * (KK / KC)) void k_gemm_q8f(const int8_t *__restrict__ wq,
-                                                             const float *__restrict__ x,
-                                                             int ldx, int M, int N, int K,
-                                                             float *__restrict__ y, int ldy) {
-  constexpr int KW = KK / KC;  // waves
-  constexpr int ST = KC / 64;  // 64-column steps per wave
-  constexpr int D = TM == 1 ? ST : 2;
+__global__ __launch_bounds__(64 * (KK / (32 * q8x_blocks_per_wave<KK>()))) void k_gemm_q8x(
+    const int8_t *__restrict__ wq, const float *__restrict__ x, int ldx, int M, int N, int K,
+    float *__restrict__ y, int ldy) {
+  constexpr int NBW = q8x_blocks_per_wave<KK>();
+  constexpr int KW = KK / (32 * NBW);     // waves
+  constexpr int D = NBW < 4 ? NBW : 4;    // blocks in flight
   __shared__ float red[KW][TM][4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n0 = blockIdx.x * 16, m0 = blockIdx.y * (TM * 16);
   const int r = lane & 15, g = lane >> 4;
-  const int kb = blockIdx.z * KK + wave * KC + 16 * g;
+  const int kw = blockIdx.z * KK + wave * (32 * NBW);  // the wave's first column
   const int row = min(n0 + r, N - 1);
-  const int8_t *wr = wq + (size_t)row * K + kb;
-  const _Float16 *dr = reinterpret_cast<const _Float16 *>(wq + (size_t)N * K) + (size_t)row * (K / 32) +
-                       kb / 32;
+  const int8_t *wr = wq + (size_t)row * K + kw + 8 * g;
+  const _Float16 *dr =
+      reinterpret_cast<const _Float16 *>(wq + (size_t)N * K) + (size_t)row * (K / 32) + kw / 32;
+  uint2 wv[NBW];
+#pragma unroll
+  for (int b = 0; b < NBW; b++) wv[b] = *reinterpret_cast<const uint2 *>(wr + 32 * b);
+  uint32_t dw[NBW / 2];  // the block scales, 4 per 8-byte load
+#pragma unroll
+  for (int i = 0; i < NBW / 4; i++) {
+    const uint2 t = *reinterpret_cast<const uint2 *>(dr + 4 * i);
+    dw[2 * i] = t.x;
+    dw[2 * i + 1] = t.y;
+  }
   const float *xr[TM];
 #pragma unroll
-  for (int t = 0; t < TM; t++) xr[t] = x + (size_t)min(m0 + 16 * t + r, M - 1) * ldx + kb;
+  for (int t = 0; t < TM; t++) xr[t] = x + (size_t)min(m0 + 16 * t + r, M - 1) * ldx + kw + 8 * g;
 
-  v4f acc[TM];
+  u32x4v xb[D][TM][2];
+  auto load = [&](int b, int c) {
 #pragma unroll
-  for (int t = 0; t < TM; t++) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
-  int4 wb[D];
-  _Float16 db[D];
-  float4 xb[D][TM][4];
-  auto load = [&](int s, int c) {
-    wb[c] = *reinterpret_cast<const int4 *>(wr + 64 * s);
-    db[c] = dr[2 * s];
-#pragma unroll
-    for (int t = 0; t < TM; t++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) xb[c][t][i] = ld4(xr[t] + 64 * s + 4 * i);
+    for (int t = 0; t < TM; t++) {
+      xb[c][t][0] = *reinterpret_cast<const u32x4v *>(xr[t] + 32 * b);
+      xb[c][t][1] = *reinterpret_cast<const u32x4v *>(xr[t] + 32 * b + 4);
+    }
   };
 #pragma unroll
   for (int s = 0; s < D; s++) load(s, s);
+  v4f acc[TM];
 #pragma unroll
-  for (int s = 0; s < ST; s++) {
-    const int c = s % D;
-    const int4 wc = wb[c];
-    const float dc = (float)db[c];
-    float4 xc[TM][4];
+  for (int t = 0; t < TM; t++) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < TM; t++)
+  for (int b = 0; b < NBW; b++) {
+    const int c = b % D;
+    u32x4v xc[TM][2];
 #pragma unroll
-      for (int i = 0; i < 4; i++) xc[t][i] = xb[c][t][i];
-    if (s + D < ST) load(s + D, c);
+    for (int t = 0; t < TM; t++) {
+      xc[t][0] = xb[c][t][0];
+      xc[t][1] = xb[c][t][1];
+    }
+    if (b + D < NBW) load(b + D, c);
     __builtin_amdgcn_sched_barrier(0);
-    const int wv[4] = {wc.x, wc.y, wc.z, wc.w};
+    const bf8v bw = q8_bf16x8(wv[b]);
+    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(dw[b >> 1] >> (16 * (b & 1))));
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      float wf[4];
+    for (int t = 0; t < TM; t++) {
+      u32x4v ph, pm, pl;
 #pragma unroll
-      for (int b = 0; b < 4; b++) wf[b] = (float)(int8_t)(wv[i] >> (8 * b)) * dc;
-#pragma unroll
-      for (int t = 0; t < TM; t++) {
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[t][i].x, wf[0], acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[t][i].y, wf[1], acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[t][i].z, wf[2], acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[t][i].w, wf[3], acc[t], 0, 0, 0);
+      for (int i = 0; i < 4; i++) {
+        const u32x4v &src = xc[t][i >> 1];
+        uint32_t h0, m0_, l0, h1, m1, l1;
+        split3(__uint_as_float(src[2 * (i & 1)]), h0, m0_, l0);
+        split3(__uint_as_float(src[2 * (i & 1) + 1]), h1, m1, l1);
+        ph[i] = h0 | (h1 << 16);
+        pm[i] = m0_ | (m1 << 16);
+        pl[i] = l0 | (l1 << 16);
       }
+      v4f s = v4f{0.f, 0.f, 0.f, 0.f};
+      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8v, pl), bw, s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8v, pm), bw, s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8v, ph), bw, s, 0, 0, 0);
+#pragma unroll
+      for (int q = 0; q < 4; q++) acc[t][q] = fmaf(d, s[q], acc[t][q]);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -474,6 +509,129 @@ __global__ __launch_bounds__(64 * (KK / KC)) void k_gemm_q8f(const int8_t *__res
     for (int q = 0; q < 4; q++) red[wave][t][q][lane] = acc[t][q];
   __syncthreads();
   epilogue<TM, KW, EPI>(red, m0, n0, M, y, ldy);
+}
+
+// Q8_0 products over many rows with the activations staged in LDS: a
+// workgroup of WN waves owns 64 activation rows and 16 WN weight rows (wave w:
+// rows n0 + 16 w .. + 15) over the K range of its slice, so each activation
+// chunk crosses the vector memory path once per 16 WN weight rows instead of
+// once per 16 (k_gemm_q8x). Per 64-column chunk (two 32-blocks): the 64 x 64
+// activations are split into three bf16 planes in LDS (double buffered, one
+// barrier per chunk), each wave's quants and block scales go to registers one
+// chunk ahead; per block and 16-row tile three v_mfma_f32_16x16x32_bf16 (low,
+// middle, high part) into the block sum, scaled by the block scale into the
+// fp32 sum, as in k_gemm_q8x. Lane l holds weight row n0 + 16 w + l % 16 and
+// receives rows 4 (l / 16) + q of each tile: a wave's sums are complete, the
+// epilogue stores them directly. Used above 64 rows: with fewer, its
+// N / (16 WN) workgroups leave most CUs idle.
+template <int WN, int EPI>
+__global__ __launch_bounds__(64 * WN) void k_gemm_q8x_m64(const int8_t *__restrict__ wq,
+                                                          const float *__restrict__ x, int ldx,
+                                                          int M, int N, int K, int kc,
+                                                          float *__restrict__ y, int ldy) {
+  constexpr int NT = 64 * WN;
+  constexpr int CW = 64;                  // chunk columns
+  constexpr int XS = CW + 8;              // LDS row stride, bf16 (144 bytes)
+  constexpr int SF = 64 * CW / 4 / NT;    // float4 of a chunk per thread
+  __shared__ uint16_t xs[2][3][64 * XS];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16 * WN + 16 * wave, m0 = blockIdx.y * 64;
+  const int kz = blockIdx.z * kc;
+  const int row = min(n0 + r, N - 1);
+  const int8_t *wr = wq + (size_t)row * K + kz + 8 * g;
+  const _Float16 *dr =
+      reinterpret_cast<const _Float16 *>(wq + (size_t)N * K) + (size_t)row * (K / 32) + kz / 32;
+  // this thread's float4 of a chunk: global and LDS offsets
+  const float *xg[SF];
+  int lo[SF];
+#pragma unroll
+  for (int i = 0; i < SF; i++) {
+    const int f = t + NT * i, rw = f / (CW / 4), c4 = f % (CW / 4);
+    xg[i] = x + (size_t)min(m0 + rw, M - 1) * ldx + kz + 4 * c4;
+    lo[i] = rw * XS + 4 * c4;
+  }
+  float4 xn[SF];
+  uint2 wn[2], wc[2];
+  uint32_t dn, dc;  // the chunk's two block scales
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < SF; i++) xn[i] = ld4(xg[i] + k0);
+    wn[0] = *reinterpret_cast<const uint2 *>(wr + k0);
+    wn[1] = *reinterpret_cast<const uint2 *>(wr + k0 + 32);
+    dn = *reinterpret_cast<const uint32_t *>(dr + k0 / 32);
+  };
+  auto stage = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < SF; i++) {
+      uint32_t h[4], md[4], l[4];
+      split3(xn[i].x, h[0], md[0], l[0]);
+      split3(xn[i].y, h[1], md[1], l[1]);
+      split3(xn[i].z, h[2], md[2], l[2]);
+      split3(xn[i].w, h[3], md[3], l[3]);
+      *reinterpret_cast<uint2 *>(&xs[b][0][lo[i]]) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+      *reinterpret_cast<uint2 *>(&xs[b][1][lo[i]]) = make_uint2(md[0] | (md[1] << 16), md[2] | (md[3] << 16));
+      *reinterpret_cast<uint2 *>(&xs[b][2][lo[i]]) = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+    }
+  };
+  v4f acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+  load(0);
+  stage(0);
+  wc[0] = wn[0];
+  wc[1] = wn[1];
+  dc = dn;
+  __syncthreads();
+  const int nc = kc / CW;
+  for (int c = 0; c < nc; c++) {
+    const int b = c & 1;
+    if (c + 1 < nc) load(CW * (c + 1));
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++) {
+      const bf8v bw = q8_bf16x8(wc[kb]);
+      const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(dc >> (16 * kb)));
+#pragma unroll
+      for (int tm = 0; tm < 4; tm++) {
+        const int o = (16 * tm + r) * XS + 32 * kb + 8 * g;
+        const bf8v ah = __builtin_bit_cast(bf8v, *reinterpret_cast<const u32x4v *>(&xs[b][0][o]));
+        const bf8v am = __builtin_bit_cast(bf8v, *reinterpret_cast<const u32x4v *>(&xs[b][1][o]));
+        const bf8v al = __builtin_bit_cast(bf8v, *reinterpret_cast<const u32x4v *>(&xs[b][2][o]));
+        v4f sm = v4f{0.f, 0.f, 0.f, 0.f};
+        sm = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bw, sm, 0, 0, 0);
+        sm = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, bw, sm, 0, 0, 0);
+        sm = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bw, sm, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; q++) acc[tm][q] = fmaf(d, sm[q], acc[tm][q]);
+      }
+    }
+    if (c + 1 < nc) {
+      stage(b ^ 1);
+      wc[0] = wn[0];
+      wc[1] = wn[1];
+      dc = dn;
+    }
+    __syncthreads();
+  }
+  const int n = n0 + r;
+#pragma unroll
+  for (int tm = 0; tm < 4; tm++)
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int m = m0 + 16 * tm + 4 * g + q;
+      const float v = acc[tm][q];
+      if (EPI == EPI_SWIGLU) {
+        const float u = __shfl_xor(v, 1);  // up: the odd row after its gate
+        if (m < M && (r & 1) == 0) y[(size_t)m * ldy + n / 2] = silu_mul_f(v, u);
+      } else if (m < M) {
+        if (EPI == EPI_ADD)
+          y[(size_t)m * ldy + n] += v;
+        else if (EPI == EPI_PART)
+          y[((size_t)blockIdx.z * M + m) * ldy + n] = v;
+        else
+          y[(size_t)m * ldy + n] = v;
+      }
+    }
 }
 
 // h[m] += slices 0 .. S-1 of part [S][M][K], added in slice order; then, with
@@ -507,19 +665,13 @@ __global__ __launch_bounds__(256) void k_resid_norm(float *__restrict__ h,
   for (int k = t; k < K; k += 256) xn[(size_t)m * K + k] = w[k] * (hr[k] * inv);
 }
 
-template <int TM, int KK, bool Q8>
+template <int TM, int KK>
 void launch_tk(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy, int ks,
                hipStream_t st) {
   const dim3 grid(W.N / 16, (M + 16 * TM - 1) / (16 * TM), ks), block(64 * (KK / KC));
-#define Q3H_G(E)                                                                              \
-  do {                                                                                        \
-    if constexpr (Q8)                                                                         \
-      hipLaunchKernelGGL((k_gemm_q8f<TM, KK, E>), grid, block, 0, st, W.q, x, ldx, M, W.N, W.K, \
-                         y, ldy);                                                             \
-    else                                                                                      \
-      hipLaunchKernelGGL((k_gemm_f32<TM, KK, E>), grid, block, 0, st, W.f, x, ldx, M, W.N, W.K, \
-                         y, ldy);                                                             \
-  } while (0)
+#define Q3H_G(E)                                                                            \
+  hipLaunchKernelGGL((k_gemm_f32<TM, KK, E>), grid, block, 0, st, W.f, x, ldx, M, W.N, W.K, \
+                     y, ldy)
   if (epi == EPI_STORE)
     Q3H_G(EPI_STORE);
   else if (epi == EPI_ADD)
@@ -528,24 +680,23 @@ void launch_tk(const Mat &W, const float *x, int ldx, int M, int epi, float *y, 
     Q3H_G(EPI_SWIGLU);
   else if (epi == EPI_PART)
     Q3H_G(EPI_PART);
-  else if constexpr (!Q8 && KK >= 1024)
-    hipLaunchKernelGGL((k_gemm_f32<TM, KK, EPI_ADD_SILU>), grid, block, 0, st, W.f, x, ldx, M,
-                       W.N, W.K, y, ldy);
+  else if constexpr (KK >= 1024)
+    Q3H_G(EPI_ADD_SILU);
   else
-    require(false, Q3H_E_ARG, "EPI_ADD_SILU takes f32 weights over the whole K");
+    require(false, Q3H_E_ARG, "EPI_ADD_SILU takes the whole K");
 #undef Q3H_G
 }
 
-template <int TM, bool Q8>
+template <int TM>
 void launch_t(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy, int ks,
               hipStream_t st) {
   switch (W.K / ks) {
-    case 256: launch_tk<TM, 256, Q8>(W, x, ldx, M, epi, y, ldy, ks, st); break;
-    case 512: launch_tk<TM, 512, Q8>(W, x, ldx, M, epi, y, ldy, ks, st); break;
-    case 768: launch_tk<TM, 768, Q8>(W, x, ldx, M, epi, y, ldy, ks, st); break;
-    case 1024: launch_tk<TM, 1024, Q8>(W, x, ldx, M, epi, y, ldy, ks, st); break;
-    case 2048: launch_tk<TM, 2048, Q8>(W, x, ldx, M, epi, y, ldy, ks, st); break;
-    default: launch_tk<TM, 3072, Q8>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 256: launch_tk<TM, 256>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 512: launch_tk<TM, 512>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 768: launch_tk<TM, 768>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 1024: launch_tk<TM, 1024>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 2048: launch_tk<TM, 2048>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    default: launch_tk<TM, 3072>(W, x, ldx, M, epi, y, ldy, ks, st); break;
   }
 }
 
@@ -586,23 +737,101 @@ void launch_m64(const Mat &W, const float *x, int ldx, int M, int epi, float *y,
 #undef Q3H_G
 }
 
-template <bool Q8>
+// Q8_0 weights: k_gemm_q8x over the whole K (KK = K: every epilogue but
+// EPI_ADD_SILU) or over K slices of KK <= 1024 columns (EPI_PART)
+template <int TM, int KK>
+void launch_q8x_k(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
+                  int ks, hipStream_t st) {
+  const dim3 grid(W.N / 16, (M + 16 * TM - 1) / (16 * TM), ks),
+      block(64 * (KK / (32 * q8x_blocks_per_wave<KK>())));
+#define Q3H_Q(E)                                                                             \
+  hipLaunchKernelGGL((k_gemm_q8x<TM, KK, E>), grid, block, 0, st, W.q, x, ldx, M, W.N, W.K, \
+                     y, ldy)
+  if (epi == EPI_PART) {
+    if constexpr (KK <= 1024)
+      Q3H_Q(EPI_PART);
+    else
+      require(false, Q3H_E_ARG, "Q8_0 K slices take at most 1024 columns");
+  } else if constexpr (KK >= 1024) {
+    if (epi == EPI_STORE)
+      Q3H_Q(EPI_STORE);
+    else if (epi == EPI_ADD)
+      Q3H_Q(EPI_ADD);
+    else if (epi == EPI_SWIGLU)
+      Q3H_Q(EPI_SWIGLU);
+    else
+      require(false, Q3H_E_ARG, "EPI_ADD_SILU takes f32 weights");
+  } else {
+    require(false, Q3H_E_ARG, "Q8_0 products over a K slice store partial sums only");
+  }
+#undef Q3H_Q
+}
+
+template <int TM>
+void launch_q8x_t(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
+                  int ks, hipStream_t st) {
+  switch (W.K / ks) {
+    case 256: launch_q8x_k<TM, 256>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 512: launch_q8x_k<TM, 512>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 768: launch_q8x_k<TM, 768>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 1024: launch_q8x_k<TM, 1024>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 2048: launch_q8x_k<TM, 2048>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    default: launch_q8x_k<TM, 3072>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+  }
+}
+
+constexpr int kQ8M64Waves = 4;  // 64 weight rows per workgroup
+
+void launch_q8x_m64(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
+                    int ks, hipStream_t st) {
+  constexpr int WN = kQ8M64Waves;
+  const dim3 grid(W.N / (16 * WN), (M + 63) / 64, ks), block(64 * WN);
+  const int kc = W.K / ks;
+#define Q3H_Q(E)                                                                           \
+  hipLaunchKernelGGL((k_gemm_q8x_m64<WN, E>), grid, block, 0, st, W.q, x, ldx, M, W.N, W.K, \
+                     kc, y, ldy)
+  if (epi == EPI_STORE)
+    Q3H_Q(EPI_STORE);
+  else if (epi == EPI_ADD)
+    Q3H_Q(EPI_ADD);
+  else if (epi == EPI_SWIGLU)
+    Q3H_Q(EPI_SWIGLU);
+  else if (epi == EPI_PART)
+    Q3H_Q(EPI_PART);
+  else
+    require(false, Q3H_E_ARG, "EPI_ADD_SILU takes f32 weights");
+#undef Q3H_Q
+}
+
+// Q8_0 weights, f32 activations [M][ldx], over K slices of K / ks columns
+void launch_q8x(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy, int ks,
+                hipStream_t st) {
+  if (M > 64 && W.N % (16 * kQ8M64Waves) == 0 && (W.K / ks) % 64 == 0) {
+    launch_q8x_m64(W, x, ldx, M, epi, y, ldy, ks, st);
+  } else if (M <= 16) {
+    launch_q8x_t<1>(W, x, ldx, M, epi, y, ldy, ks, st);
+  } else if (M <= 32) {
+    launch_q8x_t<2>(W, x, ldx, M, epi, y, ldy, ks, st);
+  } else {
+    launch_q8x_t<4>(W, x, ldx, M, epi, y, ldy, ks, st);
+  }
+}
+
 void launch_m(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
               hipStream_t st) {
-  if (!Q8 && M > 32 && epi != EPI_PART && W.N % 64 == 0 && (W.N / 64) * ((M + 63) / 64) >= 256) {
+  if (M > 32 && epi != EPI_PART && W.N % 64 == 0 && (W.N / 64) * ((M + 63) / 64) >= 256) {
     // many rows and wide products: 64-row tiles over the whole K (at least
     // 1024 waves; narrower products keep the K split over waves below, whose
     // waves each take a quarter to a twelfth of K)
     launch_m64<4>(W, x, ldx, M, epi, y, ldy, st);
     return;
   }
-  // (Q8_0, K = 3072: 32-row tiles, the 64-row tile's registers would spill)
   if (M <= 16)
-    launch_t<1, Q8>(W, x, ldx, M, epi, y, ldy, 1, st);
-  else if (M <= 32 || (Q8 && W.K == 3072))
-    launch_t<2, Q8>(W, x, ldx, M, epi, y, ldy, 1, st);
+    launch_t<1>(W, x, ldx, M, epi, y, ldy, 1, st);
+  else if (M <= 32)
+    launch_t<2>(W, x, ldx, M, epi, y, ldy, 1, st);
   else
-    launch_t<4, Q8>(W, x, ldx, M, epi, y, ldy, 1, st);
+    launch_t<4>(W, x, ldx, M, epi, y, ldy, 1, st);
 }
 
 }  // namespace
@@ -619,9 +848,9 @@ bool gemm_f32_supported(int N, int K) {
 void launch_gemm_f32(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
                      hipStream_t st) {
   if (W.f)
-    launch_m<false>(W, x, ldx, M, epi, y, ldy, st);
+    launch_m(W, x, ldx, M, epi, y, ldy, st);
   else
-    launch_m<true>(W, x, ldx, M, epi, y, ldy, st);
+    launch_q8x(W, x, ldx, M, epi, y, ldy, 1, st);
 }
 
 bool gemm_f32_slices_supported(int N, int K) {
@@ -631,23 +860,16 @@ bool gemm_f32_slices_supported(int N, int K) {
 
 void launch_gemm_f32_part(const Mat &W, const float *x, int ldx, int M, float *part,
                           hipStream_t st) {
-  if (W.f) {
-    if (M > 64 && W.N % 64 == 0)
-      launch_m64<4>(W, x, ldx, M, EPI_PART, part, W.N, st, kF32Slices);
-    else if (M <= 16)
-      launch_t<1, false>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
-    else if (M <= 32)
-      launch_t<2, false>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
-    else
-      launch_t<4, false>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
-  } else {
-    if (M <= 16)
-      launch_t<1, true>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
-    else if (M <= 32)
-      launch_t<2, true>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
-    else
-      launch_t<4, true>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
-  }
+  if (!W.f)
+    launch_q8x(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
+  else if (M > 64 && W.N % 64 == 0)
+    launch_m64<4>(W, x, ldx, M, EPI_PART, part, W.N, st, kF32Slices);
+  else if (M <= 16)
+    launch_t<1>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
+  else if (M <= 32)
+    launch_t<2>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
+  else
+    launch_t<4>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
 }
 
 void launch_resid_norm(float *h, const float *part, int M, int K, const float *norm_w,

@@ -93,8 +93,9 @@ bool launch_gemv_q8_code(const GemvArgs &a, const float *logits, int vocab, cons
 // the f32 matrix-core products (q3h_gemm_f32.hip): y[m][n] (+)= W[n] . x[m]
 // for f32 W [N][K] (N % 16 == 0, K in {1024, 2048, 3072}); epi EPI_* (SwiGLU:
 // interleaved gate / up rows, y [M][N / 2])
-// (Q8_0 weights, f32 activations: the same products, weights dequantized as
-// they load; taken for more than kGemvRows rows)
+// (Q8_0 weights, f32 activations: the same products on the bf16 matrix cores,
+// the quants exact in bf16 and the activations split exactly into three bf16
+// parts; taken for more than kGemvRows rows)
 bool gemm_f32_supported(int N, int K);
 // the three bf16 planes of m.f into m.x3 (allocated by the caller)
 void launch_split3(const Mat &m, hipStream_t st);
@@ -216,6 +217,8 @@ void launch_attn2_o_cp(const Mat &wo, const float *qkv, int ldq, void *k_layer, 
                        float *h, const float *qkn, const float *rope_rows, bool kv16,
                        hipStream_t st);
 
+// y [M][ldy] = RMSNorm of the rows x [M][ldx] with w (double sum of
+// squares)
 void launch_rmsnorm_rows(const float *x, int ldx, int M, int K, const float *w, float eps,
                          float *y, int ldy, hipStream_t st);
 

@@ -44,4 +44,19 @@ __device__ __forceinline__ void rope_pair(float &a, float &b, float c, float s) 
   b = fmaf(b0, c, __fmul_rn(a0, s));
 }
 
+// x = hi + mid + lo exactly, each a bf16 (returned as its 16 bits in the low
+// half): hi the top 8 significant bits of x, mid the next 8, lo the last 8
+// (an f32 significand has 24; each difference is exact in f32). The
+// operands of the split-bf16 matrix-core products.
+__device__ __forceinline__ void split3(float x, uint32_t &h, uint32_t &m, uint32_t &l) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t hb = u & 0xffff0000u;
+  const float r1 = x - __uint_as_float(hb);
+  const uint32_t mb = __float_as_uint(r1) & 0xffff0000u;
+  const float r2 = r1 - __uint_as_float(mb);
+  h = hb >> 16;
+  m = mb >> 16;
+  l = __float_as_uint(r2) >> 16;
+}
+
 }  // namespace q3h
