@@ -637,7 +637,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const RowDesc *__restrict_
                                                       float *__restrict__ outp) {
   __shared__ float ms[4][16], ls[4][16];
   __shared__ float os[4][8][4][64];
-  const int h = blockIdx.x, q0 = blockIdx.y * 16, g = h / GRP;
+  // the tiles with the most keys first (the last query rows): the light ones
+  // fill the CUs at the end instead of the heavy ones running alone
+  const int h = blockIdx.x, q0 = (gridDim.y - 1 - blockIdx.y) * 16, g = h / GRP;
   const int heads = GRP * kvh;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int r16 = lane & 15, gq = lane >> 4;
