@@ -122,9 +122,9 @@ def load_from_bf16(dev, f32, act_q8, dtype=q3h.Q8_0):
                      "-> Q8_0 on the device")
 
 
-def prompts(seed, workload, n):
+def prompts(seed, workload, n, rows=PROMPT_ROWS):
     if workload == "frame_b1":
-        return [synth.prompt(seed, PROMPT_ROWS)]
+        return [synth.prompt(seed, rows)]
     if workload == "f32_b8":
         return [synth.prompt(seed + 2000 + s, F32_PROMPT_ROWS) for s in range(n)]
     rng = np.random.Generator(np.random.PCG64(seed))
@@ -656,6 +656,9 @@ def main():
                          "replay, 2 events attached to each launch")
     ap.add_argument("--long-attn-only", action="store_true",
                     help="only the long-context attention measurement (profiling runs)")
+    ap.add_argument("--prompt-rows", type=int, default=PROMPT_ROWS,
+                    help="frame_b1: prompt rows of the prefill (profiling the prefill products "
+                         "at other sizes; the measured workload is 48)")
     ap.add_argument("--copy-only", action="store_true",
                     help="only a plain copy kernel of known size (calibrates the FETCH_SIZE "
                          "and WRITE_SIZE counters of profiling runs)")
@@ -691,7 +694,7 @@ def main():
     warmup = args.warmup
     if not q3h.available():
         raise RuntimeError("no gfx950 device")
-    pre = prompts(args.seed, args.workload, n)
+    pre = prompts(args.seed, args.workload, n, args.prompt_rows)
     maxlen = max(p.shape[0] for p in pre)
     max_pos = maxlen + max(steps, warmup, CONFIG2_FRAMES if b1 else 0) + 8
     dev = q3h.Device(0)
@@ -797,7 +800,7 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded N(0,0.02) weights, N(0,1) prompt embeddings)",
         "config": {"workload": args.workload, "graph": not args.no_graph, "streams": n, "prompt_rows":
-                   PROMPT_ROWS if b1 else (F32_PROMPT_ROWS if f32w else "U[16,256]"),
+                   args.prompt_rows if b1 else (F32_PROMPT_ROWS if f32w else "U[16,256]"),
                    "frames": steps, "talker_layers": 28, "cp_layers": 5, "hidden": 1024,
                    "heads": "16q/8kv x 128", "ffn": 3072, "weights": "f32" if f32w else "Q8_0",
                    "kv": "f16" if args.kv16 else "f32", "activations": "q8_0 (int8 MFMA)" if act_q8 else "f32"},

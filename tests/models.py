@@ -12,7 +12,8 @@ class Model:
     oracle, from one seed."""
 
     def __init__(self, device, seed, talker_layers=28, cp_layers=5, dtype=q3h.Q8_0,
-                 act_q8=0, kv_f16=0, norm_std=0.0, max_positions=512, cp_heads=15):
+                 act_q8=0, kv_f16=0, norm_std=0.0, max_positions=512, cp_heads=15,
+                 heads=None):
         self.seed = seed
         self.dtype = dtype
         self.tdims = dict(synth.TALKER, layers=talker_layers)
@@ -25,6 +26,8 @@ class Model:
         q = quant or (lambda a: a)
         self.th = q(synth.talker_head(seed))
         self.ch = [q(synth.cp_head(seed, g)) for g in range(cp_heads)]
+        if heads is not None:  # (talker head, code-predictor heads) -> the same, edited
+            self.th, self.ch = heads(self.th, self.ch)
         self.codec_emb = synth.codec_embedding(seed)
         self.pred_emb = [synth.pred_embedding(seed, g) for g in range(15)]
         self.tts_pad = synth.tts_pad(seed)

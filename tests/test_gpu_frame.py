@@ -225,3 +225,73 @@ def test_f32_prefill_512_and_batch8_frames(device, synth):
         for of in ofs:
             of.destroy()
         m.destroy()
+
+
+def _nan_rows(head, rows):
+    """Q8_0 head bytes (ggml blocks: fp16 scale, then 32 quants) with every
+    block scale of `rows` set to an fp16 NaN: those rows' logits are NaN."""
+    b = np.array(head, copy=True)
+    blk = b.reshape(b.shape[0], -1, 34)
+    blk[rows, :, 0] = 0x00
+    blk[rows, :, 1] = 0x7E
+    return b
+
+
+@pytest.mark.parametrize("n_streams", [1, 2])
+@pytest.mark.parametrize("sampled", [False, True], ids=["greedy", "sampled"])
+def test_frame_nan_logits_keep_codes_in_the_tables(device, synth, n_streams, sampled):
+    """NaN logits choose codes by the reference's first-max rule
+    (tests/test.tts.qwen.lm.pas:109-117: result 0, moved only on p[i] >
+    p[result]), never an index outside the tables. Talker head: logit 0 NaN,
+    so code 0 stays. Code-predictor heads: head 0 with logit 5 NaN (a NaN never
+    wins), head 1 with logit 0 NaN (code 0), heads 2 and 14 all NaN (code 0;
+    head 14's argmax runs in its own kernel at batch 1, heads 0-13 inside the
+    next product). Sampled: a NaN key orders above every finite one, so top-k
+    keeps it and the weights' sum is NaN: no comparison with the target holds,
+    and the walk takes the last positive weight; with every weight NaN (heads 2
+    and 14) nothing is drawn and the greedy choice, 0, is the code. Codes equal
+    the oracle's, frame for frame."""
+    print(f"case n_streams={n_streams} sampled={sampled}", flush=True)
+
+    def heads(th, ch):
+        ch = list(ch)
+        ch[0] = _nan_rows(ch[0], [5])
+        ch[1] = _nan_rows(ch[1], [0])
+        ch[2] = _nan_rows(ch[2], slice(None))
+        ch[14] = _nan_rows(ch[14], slice(None))
+        return _nan_rows(th, [0]), ch
+
+    m = Model(device, seed=31, talker_layers=2, cp_layers=2, max_positions=128, heads=heads)
+    fr = m.frame(n_streams=n_streams, max_positions=128)
+    sp = dict(do_sample=True, temperature=0.9, top_k=50, top_p=1.0, sub_do_sample=True,
+              sub_temperature=0.9, sub_top_k=50, sub_top_p=1.0) if sampled else {}
+    fr.set_sampling(seed=77, **sp)
+    ofs = []
+    try:
+        for s in range(n_streams):
+            pre = synth.prompt(31 + s, 12 + 5 * s)
+            fr.start(s, pre)
+            of = m.oracle_frame(max_positions=128)
+            of.set_sampling(seed=77, **sp)
+            of.start(pre)
+            ofs.append(of)
+        for i in range(5):
+            codes, alive = fr.step()
+            print(f"frame {i}: {codes[:, :4].tolist()}", flush=True)
+            for s, of in enumerate(ofs):
+                ref = of.next()
+                assert alive[s] == 1
+                assert np.all((codes[s] >= 0) & (codes[s] < 2048)), codes[s]
+                assert np.array_equal(codes[s], ref), (i, s, codes[s], ref)
+                assert codes[s][3] == 0 and codes[s][15] == 0
+                if not sampled:
+                    assert codes[s][0] == 0 and codes[s][2] == 0
+                lg, _ = fr.state(s)
+                olg, _ = of.state()
+                assert np.isnan(lg[0]) and np.isnan(olg[0])
+                assert rel(lg[1:], olg[1:]) < 1e-3
+    finally:
+        fr.destroy()
+        for of in ofs:
+            of.destroy()
+        m.destroy()
