@@ -503,100 +503,107 @@ __global__ __launch_bounds__(NTL) void k_attn_split(const RowDesc *__restrict__ 
   }
 }
 
-// The splits of (kv head g, row m) merged, with the new position of a fused
-// row: out = sum_s c_s acc_s / sum_s c_s sum_s, c_s = exp(max_s - max).
-// 1024 threads: thread (q, h, d) adds the splits q, q + Q, ... (Q = 1024 /
-// (GRP * 128)) for dim d of query head h, 16 loads at a time; the maxima
-// and the c_s are computed once per (head, split) in LDS; the Q partial sums
-// meet in LDS. The new position (FUSED): its key and value from the cache
-// (appended by split 0), the query head from slot S; its score is the
-// 128-dim dot of the two (wave sums), its weight exp(score - max).
+// The splits of (query head h, row m) merged, with the new position of a
+// fused row: out = sum_s c_s acc_s / sum_s c_s sum_s, c_s = exp(max_s - max).
+// 512 threads, thread (q, d) adding the splits q, q + 4, ... for dim d, 16
+// loads at a time, all issued first with the splits' maxima and sums. Every
+// wave finds the maximum and the c_s of all splits itself (a lane per split,
+// wave reductions) into its own row of LDS, read back by that wave only, so
+// the block meets twice: for the new position's score (fused: the 128-dim dot
+// of the query head in slot S with the new key, the halves of waves 0 and 1)
+// and for the four split groups' sums, added in group order.
 template <typename KV, bool FUSED, int GRP>
-__global__ __launch_bounds__(1024) void k_attn_merge(const RowDesc *__restrict__ rd,
-                                                     const float *__restrict__ part,
-                                                     float *__restrict__ outp, int layer, int kvh,
-                                                     int S) {
-  constexpr int NO = GRP * HD, Q = 1024 / NO, U = 16;
-  __shared__ float cw[GRP][kMaxSplitsLong], cl[GRP][kMaxSplitsLong];
-  __shared__ float red[Q][NO];
-  __shared__ float qk[GRP][2], mxs[GRP], den[GRP];
-  const int g = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
-  const int q = t / NO, o = t % NO, h = o / HD, dd = o % HD;
+__global__ __launch_bounds__(512) void k_attn_merge(const RowDesc *__restrict__ rd,
+                                                    const float *__restrict__ part,
+                                                    float *__restrict__ outp, int layer, int kvh,
+                                                    int S) {
+  constexpr int NQ = 4, U = 16, NW = 8, SPL = kMaxSplitsLong / 64;
+  __shared__ float cw[NW][kMaxSplitsLong];
+  __shared__ float red[NQ - 1][HD];
+  __shared__ float qk[2];
+  const int h = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
+  const int q = t / HD, dd = t % HD;
   const int lane = t & 63, wave = t >> 6;
-  const int heads = GRP * kvh;
+  const int heads = GRP * kvh, g = h / GRP;
   const size_t slot = HD + 2;
-  const float *pm = part + ((size_t)m * heads + g * GRP) * (S + 1) * slot;
-  const float *ph = pm + (size_t)h * (S + 1) * slot + dd;
-  float *out = outp + ((size_t)m * heads + g * GRP) * HD;
-  // the first U splits of this thread, issued with the maxima and sums
+  const float *p0 = part + ((size_t)m * heads + h) * (S + 1) * slot;
+  const float *ph = p0 + dd;
+  float *out = outp + ((size_t)m * heads + h) * HD;
   float a[U];
 #pragma unroll
-  for (int u = 0; u < U; u++) a[u] = ph[(size_t)min(q + Q * u, S - 1) * slot];
+  for (int u = 0; u < U; u++) a[u] = ph[(size_t)min(q + NQ * u, S - 1) * slot];
+  float mv[SPL], lv[SPL];
+#pragma unroll
+  for (int j = 0; j < SPL; j++) {
+    const int sp = min(lane + 64 * j, S - 1);
+    mv[j] = p0[(size_t)sp * slot + HD];
+    lv[j] = p0[(size_t)sp * slot + HD + 1];
+  }
   float qv = 0.f;
   if (FUSED) qv = ph[(size_t)S * slot];
-  for (int i = t; i < GRP * S; i += 1024) {
-    const float *pp = pm + ((size_t)(i / S) * (S + 1) + i % S) * slot;
-    cw[i / S][i % S] = pp[HD];
-    cl[i / S][i % S] = pp[HD + 1];
-  }
   const RowDesc d = rd[m];
-  if (d.pos < 0) {  // inactive row: zeros
-    if (q == 0) out[o] = 0.f;
+  if (d.pos < 0) {  // inactive row (the same for the whole block): zeros
+    if (q == 0) out[dd] = 0.f;
     return;
   }
-  float kn = 0.f, vn = 0.f;
+  const float scale = (float)(1.0 / sqrt((double)HD));
+  float score = -INFINITY, vn = 0.f;
   if (FUSED) {
     const size_t off = (((size_t)layer * kvh + g) * d.max_pos + d.pos) * HD + dd;
-    kn = (float)reinterpret_cast<const KV *>(d.k)[off];
+    const float kn = (float)reinterpret_cast<const KV *>(d.k)[off];
     vn = (float)reinterpret_cast<const KV *>(d.v)[off];
-    // threads of group q = 0: head h's dims in waves 2h and 2h + 1
-    const float v = wave_sum_dpp(qv * kn);
-    if (q == 0 && lane == 0) qk[h][dd >> 6] = v;
+    if (q == 0) {  // waves 0 and 1: dims 0-63 and 64-127
+      const float v = wave_sum_dpp(qv * kn);
+      if (lane == 0) qk[wave] = v;
+    }
+    __syncthreads();
+    score = (qk[0] + qk[1]) * scale;
   }
-  __syncthreads();
-  const float scale = (float)(1.0 / sqrt((double)HD));
-  // wave hh < GRP: the maximum of head hh over its splits and the new position
-  if (wave < GRP) {
-    float v = FUSED ? (qk[wave][0] + qk[wave][1]) * scale : -INFINITY;
-    for (int i = lane; i < S; i += 64) v = fmaxf(v, cw[wave][i]);
-    v = wave_max_dpp(v);
-    if (lane == 0) mxs[wave] = v;
+  // this wave: the maximum over the splits (and the new position), the c_s
+  // into its own LDS row, the denominator
+  float mx = score;
+#pragma unroll
+  for (int j = 0; j < SPL; j++)
+    if (lane + 64 * j < S) mx = fmaxf(mx, mv[j]);
+  mx = wave_max_dpp(mx);
+  float den = 0.f;
+#pragma unroll
+  for (int j = 0; j < SPL; j++) {
+    const int sp = lane + 64 * j;
+    if (sp < S) {
+      const float c = rescale(mv[j], mx);
+      cw[wave][sp] = c;
+      den = fmaf(lv[j], c, den);
+    }
   }
-  __syncthreads();
-  for (int i = t; i < GRP * S; i += 1024) {
-    const int hh = i / S, k = i % S;
-    cw[hh][k] = rescale(cw[hh][k], mxs[hh]);
-  }
-  __syncthreads();
-  if (wave < GRP) {
-    float v = 0.f;
-    for (int i = lane; i < S; i += 64) v = fmaf(cl[wave][i], cw[wave][i], v);
-    v = wave_sum_dpp(v);
-    if (lane == 0) den[wave] = v;
-  }
+  den = wave_sum_dpp(den);
+  // the row is this wave's own: its LDS accesses are done in order
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   float acc = 0.f;
   for (int k0 = 0;; k0 += U) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      const int sp = q + Q * (k0 + u);
-      acc = sp < S ? fmaf(a[u], cw[h][min(sp, S - 1)], acc) : acc;
+      const int sp = q + NQ * (k0 + u);
+      acc = sp < S ? fmaf(a[u], cw[wave][min(sp, S - 1)], acc) : acc;
     }
-    if (q + Q * (k0 + U) >= S) break;
+    if (q + NQ * (k0 + U) >= S) break;
 #pragma unroll
-    for (int u = 0; u < U; u++) a[u] = ph[(size_t)min(q + Q * (k0 + U + u), S - 1) * slot];
+    for (int u = 0; u < U; u++) a[u] = ph[(size_t)min(q + NQ * (k0 + U + u), S - 1) * slot];
   }
-  red[q][o] = acc;
+  if (q > 0) red[q - 1][dd] = acc;
   __syncthreads();
   if (q == 0) {
 #pragma unroll
-    for (int i = 1; i < Q; i++) acc += red[i][o];
-    float l = den[h];
+    for (int i = 0; i < NQ - 1; i++) acc += red[i][dd];
+    float l = den;
     if (FUSED) {
-      const float c = __expf((qk[h][0] + qk[h][1]) * scale - mxs[h]);
+      const float c = __expf(score - mx);
       l += c;
       acc = fmaf(c, vn, acc);
     }
-    out[o] = l > 0.f ? acc / l : 0.f;
+    out[dd] = l > 0.f ? acc / l : 0.f;
   }
 }
 
@@ -783,7 +790,7 @@ int launch_g(const AttnArgs &a, int M, int positions, hipStream_t st, const hipE
   }
 #undef Q3H_S
   if (sh.threads == 0) return 1;
-  Q3H_LAUNCH((k_attn_merge<KV, FUSED, G>), dim3(a.kvh, M), dim3(1024), st, ev ? ev[2] : nullptr,
+  Q3H_LAUNCH((k_attn_merge<KV, FUSED, G>), dim3(a.heads, M), dim3(512), st, ev ? ev[2] : nullptr,
              ev ? ev[3] : nullptr, a.rd, a.part, a.out, a.layer, a.kvh, S);
   return 2;
 }
