@@ -337,10 +337,20 @@ void run_layers(const q3h_stack *s, Work &w, int M, int positions, bool fused, h
     at.rope_cs = reinterpret_cast<const float2 *>(s->rope_cs);
     at.out = w.att;
     at.part = w.part;
-    if (!fused && io.single_context && M >= kPrefillRows)
+    if (!fused && io.single_context && M >= kPrefillRows) {
       launch_attn_prefill(at, M, kv16, st);
-    else
+    } else if (attn_merge_o_supported(at, L.o, M, positions, kv16)) {
+      // one decode row over a split context: the splits' merge in the o_proj
+      // product (+ residual)
+      launch_attn(at, M, positions, fused, kv16, st, nullptr, false);
+      launch_attn_merge_o(at, L.o, w.h, positions, fused, kv16, st);
+      linear(s, w, L.gu, w.h, H, M, L.post_norm, w.act, I, EPI_SWIGLU, nullptr, st);
+      linear(s, w, L.down, w.act, I, M, nullptr, w.h, H, EPI_ADD, nullptr, st);
+      probe_layer(io, w, l, M, H, st);
+      continue;
+    } else {
       launch_attn(at, M, positions, fused, kv16, st);
+    }
     // o_proj + residual
     linear(s, w, L.o, w.att, NQ, M, nullptr, w.h, H, EPI_ADD, nullptr, st);
     // RMSNorm + gate/up + SwiGLU

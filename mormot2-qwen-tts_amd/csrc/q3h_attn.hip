@@ -607,6 +607,186 @@ __global__ __launch_bounds__(512) void k_attn_merge(const RowDesc *__restrict__ 
   }
 }
 
+// 4 quants (one dword) times 4 activations, added to acc
+__device__ __forceinline__ float dot4_q8(int w, float4 x, float acc) {
+  acc = fmaf((float)(int8_t)(w), x.x, acc);
+  acc = fmaf((float)(int8_t)(w >> 8), x.y, acc);
+  acc = fmaf((float)(int8_t)(w >> 16), x.z, acc);
+  acc = fmaf((float)(int8_t)(w >> 24), x.w, acc);
+  return acc;
+}
+
+// o_proj of one decode row with the split attention's merge in its prologue
+// (up to 16 SR splits): every workgroup merges the splits of all 16 query
+// heads into LDS, then computes its Q8_0 rows of y += W_o x as k_gemv_q8v
+// does (a wave per row, 16 quants per lane and 1024-column chunk, its scales,
+// a wave sum). Thread t merges head t / 16, dims 8 (t % 16) .. + 7: the 16
+// threads of a head hold the splits' maxima and sums (split t % 16 + 16 r),
+// meet in 16-lane DPP reductions for the maximum (with the new position's
+// score when fused: the query head from slot S times the new key) and the
+// denominator, and pass the weights c_s = exp(max_s - max) by lane shuffles;
+// the first 16 splits' outputs are loaded with everything else, before the
+// maximum is known (one memory round trip), the next 16 after. x goes to LDS in k_gemv_q8w's
+// bank-conflict-free order (element c 1024 + l 16 + 4 i + e in float4 slot
+// (c 4 + i) 64 + l). Replaces k_attn_merge + the o_proj product: one launch
+// and one dependent round trip fewer per layer; each workgroup re-reads the
+// partials (16 heads x S x 130 floats, from L2), which bounds S.
+template <typename KV, bool FUSED, int GRP, int SR, int R>
+__global__ __launch_bounds__(256) void k_attn_merge_o(const int8_t *__restrict__ wq,
+                                                      const RowDesc *__restrict__ rd,
+                                                      const float *__restrict__ part,
+                                                      float *__restrict__ y, int N, int layer,
+                                                      int kvh, int S) {
+  constexpr int C = 2, K = C * 1024, NB = K / 32;  // 16 query heads of 128
+  __shared__ float4 xs[K / 4];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int h = t >> 4, j = t & 15, g = h / GRP;
+  const size_t slot = HD + 2;
+  // 1. this wave's R weight rows (4 R per workgroup)
+  const int row0 = (blockIdx.x * 4 + wave) * R;
+  const _Float16 *dsc = reinterpret_cast<const _Float16 *>(wq + (size_t)N * K);
+  int4 wv[R][C];
+  float sc[R][C], yres[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int row = min(row0 + r, N - 1);
+    const int8_t *qw = wq + (size_t)row * K + lane * 16;
+    const _Float16 *dw = dsc + (size_t)row * NB + (lane >> 1);
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+      wv[r][c] = *reinterpret_cast<const int4 *>(qw + c * 1024);
+      sc[r][c] = (float)dw[c * 32];
+    }
+    yres[r] = y[row];
+  }
+  // 2. the merge's inputs: head h's split maxima and sums, the query head
+  const float *p0 = part + (size_t)h * (S + 1) * slot;
+  float mv[SR], lv[SR];
+#pragma unroll
+  for (int r = 0; r < SR; r++) {
+    const int sp = min(j + 16 * r, S - 1);
+    mv[r] = p0[(size_t)sp * slot + HD];
+    lv[r] = p0[(size_t)sp * slot + HD + 1];
+  }
+  float qh[8];
+  if (FUSED) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float2 v = *reinterpret_cast<const float2 *>(p0 + (size_t)S * slot + 8 * j + 2 * e);
+      qh[2 * e] = v.x;
+      qh[2 * e + 1] = v.y;
+    }
+  }
+  // the first 16 splits' outputs (this thread's 8 dims), with the rest
+  float2 a[16][4];
+#pragma unroll
+  for (int u = 0; u < 16; u++) {
+    if (u < S) {  // (S is the same for the whole workgroup)
+      const float *ps = p0 + (size_t)u * slot + 8 * j;
+#pragma unroll
+      for (int e = 0; e < 4; e++) a[u][e] = *reinterpret_cast<const float2 *>(ps + 2 * e);
+    }
+  }
+  const RowDesc d = rd[0];
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) x[e] = 0.f;
+  if (d.pos >= 0) {  // (an inactive row adds nothing)
+    const float scale = (float)(1.0 / sqrt((double)HD));
+    float score = -INFINITY, vn[8];
+    if (FUSED) {
+      const size_t off = (((size_t)layer * kvh + g) * d.max_pos + d.pos) * HD + 8 * j;
+      const KV *kr = reinterpret_cast<const KV *>(d.k) + off;
+      const KV *vr = reinterpret_cast<const KV *>(d.v) + off;
+      float dot = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        dot = fmaf(qh[e], (float)kr[e], dot);
+        vn[e] = (float)vr[e];
+      }
+      score = group16_sum_dpp(dot) * scale;
+    }
+    float mx = score;
+#pragma unroll
+    for (int r = 0; r < SR; r++)
+      if (j + 16 * r < S) mx = fmaxf(mx, mv[r]);
+    mx = fmaxf(mx, dpp_f_keep<kQuadXor1>(mx));
+    mx = fmaxf(mx, dpp_f_keep<kQuadXor2>(mx));
+    mx = fmaxf(mx, dpp_f_keep<kHalfMirror>(mx));
+    mx = fmaxf(mx, dpp_f_keep<kRowMirror>(mx));
+    float cw[SR], den = 0.f;
+#pragma unroll
+    for (int r = 0; r < SR; r++) {
+      cw[r] = j + 16 * r < S ? rescale(mv[r], mx) : 0.f;
+      den = fmaf(lv[r], cw[r], den);
+    }
+    den = group16_sum_dpp(den);
+    const int base = lane & ~15;
+#pragma unroll
+    for (int r = 0; r < SR; r++) {
+      if (r > 0) {  // splits 16 r .. min(16 r + 15, S - 1)
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+          if (16 * r + u < S) {
+            const float *ps = p0 + (size_t)(16 * r + u) * slot + 8 * j;
+#pragma unroll
+            for (int e = 0; e < 4; e++) a[u][e] = *reinterpret_cast<const float2 *>(ps + 2 * e);
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 16; u++) {
+        const int s = 16 * r + u;
+        const float c = __shfl(cw[r], base | u);
+        if (s < S) {
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            x[2 * e] = fmaf(c, a[u][e].x, x[2 * e]);
+            x[2 * e + 1] = fmaf(c, a[u][e].y, x[2 * e + 1]);
+          }
+        }
+      }
+    }
+    float l = den;
+    if (FUSED) {
+      const float cn = __expf(score - mx);
+      l += cn;
+#pragma unroll
+      for (int e = 0; e < 8; e++) x[e] = fmaf(cn, vn[e], x[e]);
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) x[e] = l > 0.f ? x[e] * inv : 0.f;
+  }
+  // x into LDS: elements k0 .. k0 + 7, k0 = 128 h + 8 j
+  {
+    const int k0 = 128 * h + 8 * j, c = k0 >> 10, l = (k0 & 1023) >> 4, i0 = (k0 & 15) >> 2;
+    xs[(c * 4 + i0) * 64 + l] = make_float4(x[0], x[1], x[2], x[3]);
+    xs[(c * 4 + i0 + 1) * 64 + l] = make_float4(x[4], x[5], x[6], x[7]);
+  }
+  __syncthreads();
+  // 3. the rows' dot products
+  float4 xl[C][4];
+#pragma unroll
+  for (int c = 0; c < C; c++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) xl[c][i] = xs[(c * 4 + i) * 64 + lane];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+      float p0s = dot4_q8(wv[r][c].x, xl[c][0], 0.f);
+      float p1s = dot4_q8(wv[r][c].y, xl[c][1], 0.f);
+      p0s = dot4_q8(wv[r][c].z, xl[c][2], p0s);
+      p1s = dot4_q8(wv[r][c].w, xl[c][3], p1s);
+      acc = fmaf(sc[r][c], p0s + p1s, acc);
+    }
+    acc = wave_sum_dpp(acc);
+    if (lane == 0 && row0 + r < N) y[row0 + r] = yres[r] + acc;
+  }
+}
+
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 // 4 cache elements as f32 (16 bytes of f32, 8 of f16)
@@ -759,7 +939,8 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const RowDesc *__restrict_
   } while (0)
 
 template <typename KV, bool FUSED, int G>
-int launch_g(const AttnArgs &a, int M, int positions, hipStream_t st, const hipEvent_t *ev) {
+int launch_g(const AttnArgs &a, int M, int positions, hipStream_t st, const hipEvent_t *ev,
+             bool merge) {
   const hipEvent_t ev0 = ev ? ev[0] : nullptr, ev1 = ev ? ev[1] : nullptr;
   const SplitShape sh = attn_split_shape(positions, sizeof(KV) == 2);
   const int S = (positions + sh.len - 1) / sh.len;
@@ -789,18 +970,44 @@ int launch_g(const AttnArgs &a, int M, int positions, hipStream_t st, const hipE
     Q3H_S(128, 512);
   }
 #undef Q3H_S
-  if (sh.threads == 0) return 1;
+  if (sh.threads == 0 || !merge) return 1;
   Q3H_LAUNCH((k_attn_merge<KV, FUSED, G>), dim3(a.heads, M), dim3(512), st, ev ? ev[2] : nullptr,
              ev ? ev[3] : nullptr, a.rd, a.part, a.out, a.layer, a.kvh, S);
   return 2;
 }
 
 template <typename KV, bool FUSED>
-int launch_kv(const AttnArgs &a, int M, int positions, hipStream_t st, const hipEvent_t *ev) {
+int launch_kv(const AttnArgs &a, int M, int positions, hipStream_t st, const hipEvent_t *ev,
+              bool merge) {
   const int grp = a.heads / a.kvh;
-  if (grp == 1) return launch_g<KV, FUSED, 1>(a, M, positions, st, ev);
-  if (grp == 2) return launch_g<KV, FUSED, 2>(a, M, positions, st, ev);
-  return launch_g<KV, FUSED, 4>(a, M, positions, st, ev);
+  if (grp == 1) return launch_g<KV, FUSED, 1>(a, M, positions, st, ev, merge);
+  if (grp == 2) return launch_g<KV, FUSED, 2>(a, M, positions, st, ev, merge);
+  return launch_g<KV, FUSED, 4>(a, M, positions, st, ev, merge);
+}
+
+constexpr int kMergeORows = 1;  // weight rows per wave
+
+template <typename KV, bool FUSED, int G>
+void launch_mo(const AttnArgs &a, const Mat &wo, float *y, int S, hipStream_t st) {
+  constexpr int R = kMergeORows;
+  const dim3 grid((wo.N + 4 * R - 1) / (4 * R)), block(256);
+  if (S <= 16)
+    hipLaunchKernelGGL((k_attn_merge_o<KV, FUSED, G, 1, R>), grid, block, 0, st, wo.q, a.rd,
+                       a.part, y, wo.N, a.layer, a.kvh, S);
+  else
+    hipLaunchKernelGGL((k_attn_merge_o<KV, FUSED, G, 2, R>), grid, block, 0, st, wo.q, a.rd,
+                       a.part, y, wo.N, a.layer, a.kvh, S);
+}
+
+template <typename KV, bool FUSED>
+void launch_mo_kv(const AttnArgs &a, const Mat &wo, float *y, int S, hipStream_t st) {
+  const int grp = a.heads / a.kvh;
+  if (grp == 1)
+    launch_mo<KV, FUSED, 1>(a, wo, y, S, st);
+  else if (grp == 2)
+    launch_mo<KV, FUSED, 2>(a, wo, y, S, st);
+  else
+    launch_mo<KV, FUSED, 4>(a, wo, y, S, st);
 }
 
 }  // namespace
@@ -826,12 +1033,30 @@ int attn_max_positions(bool kv16) {
 }
 
 int launch_attn(const AttnArgs &a, int M, int positions, bool fused, bool kv16, hipStream_t st,
-                const hipEvent_t *ev) {
+                const hipEvent_t *ev, bool merge) {
   if (kv16)
-    return fused ? launch_kv<_Float16, true>(a, M, positions, st, ev)
-                 : launch_kv<_Float16, false>(a, M, positions, st, ev);
-  return fused ? launch_kv<float, true>(a, M, positions, st, ev)
-               : launch_kv<float, false>(a, M, positions, st, ev);
+    return fused ? launch_kv<_Float16, true>(a, M, positions, st, ev, merge)
+                 : launch_kv<_Float16, false>(a, M, positions, st, ev, merge);
+  return fused ? launch_kv<float, true>(a, M, positions, st, ev, merge)
+               : launch_kv<float, false>(a, M, positions, st, ev, merge);
+}
+
+bool attn_merge_o_supported(const AttnArgs &a, const Mat &wo, int M, int positions, bool kv16) {
+  const SplitShape sh = attn_split_shape(positions, kv16);
+  const int S = (positions + sh.len - 1) / sh.len;
+  return M == 1 && wo.q != nullptr && wo.K == a.heads * HD && a.heads == 16 && wo.N % 4 == 0 &&
+         sh.threads != 0 && S <= kMergeOMaxSplits;
+}
+
+void launch_attn_merge_o(const AttnArgs &a, const Mat &wo, float *y, int positions, bool fused,
+                         bool kv16, hipStream_t st) {
+  const SplitShape sh = attn_split_shape(positions, kv16);
+  const int S = (positions + sh.len - 1) / sh.len;
+  if (kv16)
+    fused ? launch_mo_kv<_Float16, true>(a, wo, y, S, st)
+          : launch_mo_kv<_Float16, false>(a, wo, y, S, st);
+  else
+    fused ? launch_mo_kv<float, true>(a, wo, y, S, st) : launch_mo_kv<float, false>(a, wo, y, S, st);
 }
 
 }  // namespace q3h

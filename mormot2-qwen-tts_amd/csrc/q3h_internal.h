@@ -187,8 +187,19 @@ int attn_max_positions(bool kv16);
 // included). Returns the kernels launched (1, or 2 with the split merge); ev
 // (optional, measurement): 4 events, the start and end of each kernel's own
 // execution
+// merge == false: the split kernel alone when the context is split (its
+// partials left for launch_attn_merge_o)
 int launch_attn(const AttnArgs &a, int M, int positions, bool fused, bool kv16, hipStream_t st,
-                const hipEvent_t *ev = nullptr);
+                const hipEvent_t *ev = nullptr, bool merge = true);
+// one decode row's o_proj (Q8_0 W_o [N][16 x 128]) with the split attention's
+// merge in its prologue: y [N] += W_o x, x merged from a.part (the split
+// kernel of launch_attn(..., merge = false) launched before); for contexts
+// cut into at most kMergeOMaxSplits splits (the caller checks
+// attn_merge_o_supported)
+constexpr int kMergeOMaxSplits = 32;
+bool attn_merge_o_supported(const AttnArgs &a, const Mat &wo, int M, int positions, bool kv16);
+void launch_attn_merge_o(const AttnArgs &a, const Mat &wo, float *y, int positions, bool fused,
+                         bool kv16, hipStream_t st);
 
 // attention of the int8 path (q3h_attnx.hip): the rows of a (fused: each the
 // one new position of its own context, QK-norm / RoPE / K/V append in the
