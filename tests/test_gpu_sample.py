@@ -80,6 +80,52 @@ def test_sampling_single_stream(device, dtype):
         m.destroy()
 
 
+def _exact_bucket_head(head):
+    """Q8_0 head bytes whose logits put the top 50 in one radix bucket, for
+    any hidden state: rows 0-49 all equal to row 200, rows 50-99 its negation,
+    every other row's quants 0. One of the two groups has 50 equal positive
+    logits, every other logit is 0 or negative, so the first 8-bit pass of the
+    top-k select finds a bucket holding exactly the 50 values still wanted."""
+    b = np.array(head, copy=True)
+    blk = b.reshape(b.shape[0], -1, 34)
+    src = blk[200].copy()
+    neg = src.copy()
+    q = neg[:, 2:].view(np.int8)
+    q[:] = -q  # the quants lie in [-127, 127]
+    blk[0:50] = src
+    blk[50:100] = neg
+    blk[100:, :, 2:] = 0
+    return b
+
+
+@pytest.mark.parametrize("n_streams", [1, 3])
+def test_sampling_top_k_bucket_exact_in_the_first_pass(device, n_streams):
+    """The device top-k stops its radix select at the first pass whose bucket
+    holds exactly the values still wanted (q3h_sample.h); the oracle takes
+    the exact k-th key by sorting. Code-predictor heads 0 and 1 built so that
+    the first pass is exact: the codes equal the oracle's and come from the
+    positive group."""
+
+    def heads(th, ch):
+        ch = list(ch)
+        ch[0] = _exact_bucket_head(ch[0])
+        ch[1] = _exact_bucket_head(ch[1])
+        return th, ch
+
+    m = Model(device, seed=37, talker_layers=2, cp_layers=1, norm_std=0.1, max_positions=96,
+              heads=heads)
+    try:
+        sp = dict(do_sample=True, temperature=0.9, top_k=50, top_p=1.0, sub_do_sample=True,
+                  sub_temperature=0.9, sub_top_k=50, sub_top_p=1.0)
+        codes = _run(m, sp, seed=4242, n_streams=n_streams, lens=[20, 28, 36][:n_streams],
+                     frames=6, exact=False)
+        assert np.all((codes[:, :, 1] < 100) & (codes[:, :, 2] < 100)), codes[:, :, 1:3]
+        # within the group the draw picks any of the 50 equal logits
+        assert len(np.unique(codes[:, :, 1])) > 1
+    finally:
+        m.destroy()
+
+
 def test_sampling_top_k_1_is_greedy_and_seeds(device):
     m = Model(device, seed=23, talker_layers=2, cp_layers=1, norm_std=0.1, max_positions=96)
     pre = np.random.default_rng(5).standard_normal((24, 1024)).astype(np.float32)
