@@ -39,11 +39,6 @@ namespace {
 
 constexpr int kMaxWaves = 16;
 constexpr int kMaxRowsX = 4;  // activation rows per launch
-#ifdef Q3H_GEMV_LDS_M1
-constexpr bool kLdsSingleRow = true;  // single rows staged in LDS too
-#else
-constexpr bool kLdsSingleRow = false;
-#endif
 
 __device__ __forceinline__ float wave_sum_f(float v) { return wave_sum_dpp(v); }
 
@@ -517,7 +512,7 @@ bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st, hipEvent_t 
   if (a.K != 1024 && a.K != 2048 && a.K != 3072) return false;
   if (a.N % 256 != 0) return false;
   const int rpb = a.N / 256;  // rows per workgroup, 256 workgroups
-  if (a.M == 1 && !kLdsSingleRow) {
+  if (a.M == 1) {
     // measured on the Qwen3-TTS shapes: one wave per SIMD (R = rpb / 4 rows
     // per wave) for the plain products; the gate/up pairs (SwiGLU) run as
     // 2-row waves (12 per workgroup), which keeps more loads in flight
