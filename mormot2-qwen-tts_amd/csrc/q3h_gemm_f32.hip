@@ -414,8 +414,9 @@ __global__ void k_split3(const float *__restrict__ f, size_t n, uint16_t *__rest
 // n0 + l % 16 (one 8-byte load) and the same 8 columns of activation row
 // m0 + 16 t + l % 16 of each tile t (two 16-byte loads), and receives
 // D[4 (l / 16) + q][l % 16]: the output layout of k_gemm_f32, whose
-// epilogues this kernel shares. A workgroup owns 16 weight rows and TM tiles
-// of 16 activation rows; its waves take NBW blocks each. A wave issues the
+// epilogues this kernel shares. A workgroup owns 16 NB weight rows and TM
+// tiles of 16 activation rows (the activations split once for the NB weight
+// tiles); its waves take NBW blocks each. A wave issues the
 // loads of all its weights and scales first, then of its activations D
 // blocks ahead of the arithmetic, so that it waits for few memory round
 // trips. (Its time is the activation loads: every workgroup reads all M rows
@@ -425,31 +426,34 @@ constexpr int q8x_blocks_per_wave() {
   return KK <= 1024 ? 4 : KK / 256;  // at most 8 waves
 }
 
-template <int TM, int KK, int EPI>
+template <int TM, int KK, int EPI, int NB>
 __global__ __launch_bounds__(64 * (KK / (32 * q8x_blocks_per_wave<KK>()))) void k_gemm_q8x(
     const int8_t *__restrict__ wq, const float *__restrict__ x, int ldx, int M, int N, int K,
     float *__restrict__ y, int ldy) {
   constexpr int NBW = q8x_blocks_per_wave<KK>();
   constexpr int KW = KK / (32 * NBW);     // waves
   constexpr int D = NBW < 4 ? NBW : 4;    // blocks in flight
-  __shared__ float red[KW][TM][4][64];
+  __shared__ float red[NB][KW][TM][4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n0 = blockIdx.x * 16, m0 = blockIdx.y * (TM * 16);
+  const int n0 = blockIdx.x * 16 * NB, m0 = blockIdx.y * (TM * 16);
   const int r = lane & 15, g = lane >> 4;
   const int kw = blockIdx.z * KK + wave * (32 * NBW);  // the wave's first column
-  const int row = min(n0 + r, N - 1);
-  const int8_t *wr = wq + (size_t)row * K + kw + 8 * g;
-  const _Float16 *dr =
-      reinterpret_cast<const _Float16 *>(wq + (size_t)N * K) + (size_t)row * (K / 32) + kw / 32;
-  uint2 wv[NBW];
+  uint2 wv[NB][NBW];
+  uint32_t dw[NB][NBW / 2];  // the block scales, 4 per 8-byte load
 #pragma unroll
-  for (int b = 0; b < NBW; b++) wv[b] = *reinterpret_cast<const uint2 *>(wr + 32 * b);
-  uint32_t dw[NBW / 2];  // the block scales, 4 per 8-byte load
+  for (int j = 0; j < NB; j++) {
+    const int row = min(n0 + 16 * j + r, N - 1);
+    const int8_t *wr = wq + (size_t)row * K + kw + 8 * g;
+    const _Float16 *dr =
+        reinterpret_cast<const _Float16 *>(wq + (size_t)N * K) + (size_t)row * (K / 32) + kw / 32;
 #pragma unroll
-  for (int i = 0; i < NBW / 4; i++) {
-    const uint2 t = *reinterpret_cast<const uint2 *>(dr + 4 * i);
-    dw[2 * i] = t.x;
-    dw[2 * i + 1] = t.y;
+    for (int b = 0; b < NBW; b++) wv[j][b] = *reinterpret_cast<const uint2 *>(wr + 32 * b);
+#pragma unroll
+    for (int i = 0; i < NBW / 4; i++) {
+      const uint2 t = *reinterpret_cast<const uint2 *>(dr + 4 * i);
+      dw[j][2 * i] = t.x;
+      dw[j][2 * i + 1] = t.y;
+    }
   }
   const float *xr[TM];
 #pragma unroll
@@ -465,9 +469,11 @@ __global__ __launch_bounds__(64 * (KK / (32 * q8x_blocks_per_wave<KK>()))) void 
   };
 #pragma unroll
   for (int s = 0; s < D; s++) load(s, s);
-  v4f acc[TM];
+  v4f acc[NB][TM];
 #pragma unroll
-  for (int t = 0; t < TM; t++) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < NB; j++)
+#pragma unroll
+    for (int t = 0; t < TM; t++) acc[j][t] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int b = 0; b < NBW; b++) {
     const int c = b % D;
@@ -479,8 +485,13 @@ __global__ __launch_bounds__(64 * (KK / (32 * q8x_blocks_per_wave<KK>()))) void 
     }
     if (b + D < NBW) load(b + D, c);
     __builtin_amdgcn_sched_barrier(0);
-    const bf8v bw = q8_bf16x8(wv[b]);
-    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(dw[b >> 1] >> (16 * (b & 1))));
+    bf8v bw[NB];
+    float d[NB];
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      bw[j] = q8_bf16x8(wv[j][b]);
+      d[j] = (float)__builtin_bit_cast(_Float16, (uint16_t)(dw[j][b >> 1] >> (16 * (b & 1))));
+    }
 #pragma unroll
     for (int t = 0; t < TM; t++) {
       u32x4v ph, pm, pl;
@@ -494,21 +505,27 @@ __global__ __launch_bounds__(64 * (KK / (32 * q8x_blocks_per_wave<KK>()))) void 
         pm[i] = m0_ | (m1 << 16);
         pl[i] = l0 | (l1 << 16);
       }
-      v4f s = v4f{0.f, 0.f, 0.f, 0.f};
-      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8v, pl), bw, s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8v, pm), bw, s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8v, ph), bw, s, 0, 0, 0);
 #pragma unroll
-      for (int q = 0; q < 4; q++) acc[t][q] = fmaf(d, s[q], acc[t][q]);
+      for (int j = 0; j < NB; j++) {
+        v4f s = v4f{0.f, 0.f, 0.f, 0.f};
+        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8v, pl), bw[j], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8v, pm), bw[j], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8v, ph), bw[j], s, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; q++) acc[j][t][q] = fmaf(d[j], s[q], acc[j][t][q]);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
   }
 #pragma unroll
-  for (int t = 0; t < TM; t++)
+  for (int j = 0; j < NB; j++)
 #pragma unroll
-    for (int q = 0; q < 4; q++) red[wave][t][q][lane] = acc[t][q];
+    for (int t = 0; t < TM; t++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) red[j][wave][t][q][lane] = acc[j][t][q];
   __syncthreads();
-  epilogue<TM, KW, EPI>(red, m0, n0, M, y, ldy);
+#pragma unroll
+  for (int j = 0; j < NB; j++) epilogue<TM, KW, EPI>(red[j], m0, n0 + 16 * j, M, y, ldy);
 }
 
 // Q8_0 products over many rows with the activations staged in LDS: a
@@ -739,13 +756,13 @@ void launch_m64(const Mat &W, const float *x, int ldx, int M, int epi, float *y,
 
 // Q8_0 weights: k_gemm_q8x over the whole K (KK = K: every epilogue but
 // EPI_ADD_SILU) or over K slices of KK <= 1024 columns (EPI_PART)
-template <int TM, int KK>
+template <int TM, int KK, int NB>
 void launch_q8x_k(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
                   int ks, hipStream_t st) {
-  const dim3 grid(W.N / 16, (M + 16 * TM - 1) / (16 * TM), ks),
+  const dim3 grid(W.N / (16 * NB), (M + 16 * TM - 1) / (16 * TM), ks),
       block(64 * (KK / (32 * q8x_blocks_per_wave<KK>())));
-#define Q3H_Q(E)                                                                             \
-  hipLaunchKernelGGL((k_gemm_q8x<TM, KK, E>), grid, block, 0, st, W.q, x, ldx, M, W.N, W.K, \
+#define Q3H_Q(E)                                                                                 \
+  hipLaunchKernelGGL((k_gemm_q8x<TM, KK, E, NB>), grid, block, 0, st, W.q, x, ldx, M, W.N, W.K, \
                      y, ldy)
   if (epi == EPI_PART) {
     if constexpr (KK <= 1024)
@@ -767,16 +784,19 @@ void launch_q8x_k(const Mat &W, const float *x, int ldx, int M, int epi, float *
 #undef Q3H_Q
 }
 
-template <int TM>
+// NB 16-row weight tiles per wave: two over more than 16 rows (each
+// activation load then feeds twice the matrix-core work: 48-row prefill
+// 1.92 -> 1.85 ms), one below (8 rows: 1.03 against 1.07 ms with two)
+template <int TM, int NB>
 void launch_q8x_t(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
                   int ks, hipStream_t st) {
   switch (W.K / ks) {
-    case 256: launch_q8x_k<TM, 256>(W, x, ldx, M, epi, y, ldy, ks, st); break;
-    case 512: launch_q8x_k<TM, 512>(W, x, ldx, M, epi, y, ldy, ks, st); break;
-    case 768: launch_q8x_k<TM, 768>(W, x, ldx, M, epi, y, ldy, ks, st); break;
-    case 1024: launch_q8x_k<TM, 1024>(W, x, ldx, M, epi, y, ldy, ks, st); break;
-    case 2048: launch_q8x_k<TM, 2048>(W, x, ldx, M, epi, y, ldy, ks, st); break;
-    default: launch_q8x_k<TM, 3072>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 256: launch_q8x_k<TM, 256, NB>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 512: launch_q8x_k<TM, 512, NB>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 768: launch_q8x_k<TM, 768, NB>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 1024: launch_q8x_k<TM, 1024, NB>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    case 2048: launch_q8x_k<TM, 2048, 1>(W, x, ldx, M, epi, y, ldy, ks, st); break;
+    default: launch_q8x_k<TM, 3072, 1>(W, x, ldx, M, epi, y, ldy, ks, st); break;
   }
 }
 
@@ -809,11 +829,16 @@ void launch_q8x(const Mat &W, const float *x, int ldx, int M, int epi, float *y,
   if (M > 64 && W.N % (16 * kQ8M64Waves) == 0 && (W.K / ks) % 64 == 0) {
     launch_q8x_m64(W, x, ldx, M, epi, y, ldy, ks, st);
   } else if (M <= 16) {
-    launch_q8x_t<1>(W, x, ldx, M, epi, y, ldy, ks, st);
+    launch_q8x_t<1, 1>(W, x, ldx, M, epi, y, ldy, ks, st);
+  } else if (W.N % 32 != 0) {
+    if (M <= 32)
+      launch_q8x_t<2, 1>(W, x, ldx, M, epi, y, ldy, ks, st);
+    else
+      launch_q8x_t<4, 1>(W, x, ldx, M, epi, y, ldy, ks, st);
   } else if (M <= 32) {
-    launch_q8x_t<2>(W, x, ldx, M, epi, y, ldy, ks, st);
+    launch_q8x_t<2, 2>(W, x, ldx, M, epi, y, ldy, ks, st);
   } else {
-    launch_q8x_t<4>(W, x, ldx, M, epi, y, ldy, ks, st);
+    launch_q8x_t<4, 2>(W, x, ldx, M, epi, y, ldy, ks, st);
   }
 }
 
