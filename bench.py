@@ -185,7 +185,7 @@ def cpu_baseline(f32, tables, pre, gpu_codes, budget_s, max_frames, act_q8, f32w
     stream 0, same weight and activation modes), frames timed until budget_s
     is spent, at each of cpu_thread_counts(); value: the faster."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import q3o  # the checker's restatement, timed as the CPU baseline
+    import q3o  # the oracle, timed as the CPU baseline
 
     q3o.set_threads(max(cpu_thread_counts()))
     ot, oc, frame = oracle_model(q3o, f32, tables, act_q8, f32w,
@@ -370,7 +370,7 @@ def talker_decode_b1(dev, ts, f32, tables, seed, args, steps=64, rows=PROMPT_ROW
     log(f"talker decode b1: {steps / total:.0f} steps/s, p50 {1e6 * np.median(lat):.0f} us")
     if not args.no_cpu:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
-        import q3o  # the checker's restatement, timed as the CPU baseline
+        import q3o  # the oracle, timed as the CPU baseline
         q = q3o.quantize_q8_0
         ot = q3o.Stack(synth.TALKER, [{k: (q(v) if k.startswith("w") else v)
                                        for k, v in L.items()} for L in f32["tl"]],
@@ -497,7 +497,7 @@ def codec_back(dev, seed, frames=156, cpu=True):
     c.destroy()
     if cpu:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
-        import q3o  # the checker's restatement, timed as the CPU baseline
+        import q3o  # the oracle, timed as the CPU baseline
         threads = min(16, len(os.sched_getaffinity(0)))
         q3o.set_threads(threads)
         oc = q3o.Codec(w)
@@ -582,7 +582,7 @@ def cpu_text_projection(tables, ids, budget_s=2.0):
     """The oracle's TextProject of the same ids on the host cores (the
     reference's CPU text projection), timed until budget_s is spent."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import q3o  # the checker's restatement, timed as the CPU baseline
+    import q3o  # the oracle, timed as the CPU baseline
 
     threads = min(16, len(os.sched_getaffinity(0)))
     q3o.set_threads(threads)
@@ -664,7 +664,7 @@ def main():
                          "and WRITE_SIZE counters of profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+        print(f"bench.py: this library runs on one GPU; --gpus {args.gpus} is not supported "
               "(independent streams would shard across GPUs with no exchange)", file=sys.stderr)
         return 2
     if args.copy_only:

@@ -1,7 +1,7 @@
 /* q3o.c - CPU restatement of the Qwen3-TTS frame step (the oracle).
  *
- * TEST INFRASTRUCTURE ONLY: the checker of libq3h, never part of the product
- * path. See q3o.h for what each function restates (reference file:line) and
+ * TEST INFRASTRUCTURE ONLY: what the tests compare libq3h against, never part
+ * of the product path. See q3o.h for what each function restates (reference file:line) and
  * how it is pinned.
  *
  * Arithmetic conventions. The mathematics is the reference's; the order of

@@ -1,7 +1,7 @@
 /* q3o.h - CPU restatement of the Qwen3-TTS frame step (the oracle).
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker of the HIP library
- * (libq3h): only tests/, __graft_entry__.smoke() and the cpu_baseline leg of
+ * TEST INFRASTRUCTURE ONLY. The tests compare the HIP library (libq3h)
+ * against this one: only tests/, __graft_entry__.smoke() and the cpu_baseline leg of
  * bench.py may load it. The product path never links or calls it.
  *
  * What it restates (reference files, relative to the reference checkout):

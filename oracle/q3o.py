@@ -1,7 +1,8 @@
 """ctypes binding of the oracle (oracle/q3o.c).
 
 TEST INFRASTRUCTURE ONLY: loaded by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py, as the checker; never by the product path.
+cpu_baseline leg of bench.py, as the reference results; never by the product
+path.
 """
 import ctypes
 import os

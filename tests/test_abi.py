@@ -28,7 +28,7 @@ def test_exports_every_declared_symbol(q3h):
 
 def test_device_open_without_gpu_fails_cleanly(q3h):
     if q3h.available():
-        return  # a GPU box: covered by the gpu tests
+        return  # a machine with a GPU: covered by the gpu tests
     h = ctypes.c_void_p()
     rc = q3h.lib().q3h_device_open(0, ctypes.byref(h))
     assert rc == q3h.E_NODEV
