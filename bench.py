@@ -173,8 +173,8 @@ def cpu_info():
 
 
 def cpu_thread_counts():
-    """The host cores this job may use (at most 16: one GPU's share of the
-    box) and the reference's default worker count for them,
+    """The host cores this job may use (at most 16: one GPU's share of an
+    8-GPU host) and the reference's default worker count for them,
     (2 nproc + 2) / 3 (mormot.ai.tts.qwen.talker.pas:316-317)."""
     share = min(16, len(os.sched_getaffinity(0)))
     return sorted({max(1, (2 * share + 2) // 3), share})
