@@ -125,12 +125,7 @@ int attention_splits(const q3h_stack *s, int positions) {
 }
 
 int attention_splits_upto(const q3h_stack *s, int positions) {
-  // the split length grows with the context, so the count peaks at the top
-  // of each length's range
-  int n = 1;
-  for (int p : {2048, 4096, positions})
-    n = std::max(n, attention_splits(s, std::min(p, positions)));
-  return n;
+  return attn_splits_upto(positions, s->cfg.kv_f16 != 0);
 }
 
 void linear(const q3h_stack *s, Work &w, const Mat &W, const float *x, int ldx, int M,

@@ -272,22 +272,29 @@ constexpr int kMaxSplitsLong = 256;
 // load instruction of a wave reads 4 whole consecutive rows, and a
 // position's key and value sit in the same lanes, so its softmax weights
 // never leave the registers.
+// The waves of a workgroup meet once, at the end. Its loads are all in
+// flight together and arrive over the whole time the cache streams, so a
+// wave computes its scores and values as its own data arrives; the
+// workgroup-wide maximum before the exponentials (two more block barriers)
+// left that arithmetic waiting for the slowest wave, after the stream.
 //   - the split covers the positions before pos (FUSED: the new position
 //     pos is added by the merge) or up to pos (rows whose K/V were appended
 //     beforehand); every key and value is loaded before the prologue, at
 //     positions clamped into the covered range (a context's cache starts as
 //     zeros, so a row read there is finite, and its weight is 0);
-//   - prologue (FUSED): waves take the GRP query heads, and in split 0 the
-//     new key and value of the row (RMSNorm with q_norm / k_norm, RoPE);
-//     split 0 appends the key and value to the cache and leaves the normed
-//     query heads in the partial buffer for the merge;
+//   - prologue (FUSED): every wave norms and rotates the GRP query heads
+//     itself (RMSNorm with q_norm, RoPE) and takes its 8 dims of each through
+//     its own rows of LDS; in split 0, wave h leaves query head h in the
+//     partial buffer for the merge, and the last two waves append the row's
+//     key (k_norm, RoPE) and value to the cache;
 //   - scores: an 8-term chain per lane, summed over the 16 lanes of a DPP
 //     row, one DPP stage at a time over all of the thread's sums;
-//   - softmax per query head over the split (maximum, exp, sum);
+//   - softmax per query head over the wave's positions (maximum, exp, sum);
 //   - values: 8 dims x GRP heads of partial outputs per lane, summed over the
-//     position groups of a wave (lane shuffles), then over the waves in LDS;
-//   - (max, sum, unnormalized output) per query head and split go to the
-//     partial buffer [M][heads][S + 1][HD + 2] (slot S: the query head).
+//     position groups of a wave (lane shuffles);
+//   - the waves' (maximum, sum, output) meet in LDS, rescaled to the split's
+//     maximum, and go to the partial buffer [M][heads][S + 1][HD + 2] (slot
+//     S: the query head).
 // The kernel boundary makes the partials of every workgroup visible to the
 // merge (a device-scope fence and ticket per workgroup, the alternative, was
 // measured here at 10-30 us per launch on long contexts).
@@ -301,11 +308,11 @@ __global__ __launch_bounds__(NTL) void k_attn_split(const RowDesc *__restrict__ 
   constexpr int NJ = P / PG;          // positions per thread
   constexpr int LW = sizeof(KV) / 2;  // 16-byte loads per 8 elements
   constexpr int NWV = NTL / 64;
-  constexpr int IT = GRP + 2, RND = (IT + NWV - 1) / NWV;  // prologue items, rounds
   static_assert(NJ * PG == P, "split size");
-  __shared__ float qs[GRP][HD];
-  __shared__ float red[2][GRP][NWV];
-  __shared__ float po[NWV][GRP][HD];
+  static_assert(NWV >= 2 && GRP <= NWV, "a wave per query head, two for the append");
+  __shared__ float qw[FUSED ? NWV : 1][GRP][HD];  // each wave's normed query heads
+  __shared__ float wmx[NWV][GRP], wsum[NWV][GRP];  // each wave's maximum and sum
+  __shared__ float po[NWV][GRP][HD];               // each wave's output
   const int g = blockIdx.x, s = blockIdx.y, m = blockIdx.z;
   const int heads = GRP * kvh, ldq = (heads + 2 * kvh) * HD;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -313,21 +320,35 @@ __global__ __launch_bounds__(NTL) void k_attn_split(const RowDesc *__restrict__ 
   const float *row = qkv + (size_t)m * ldq;
   // loads in the order of their use: the prologue's (the q / k / v row needs
   // no descriptor), the keys, the values
-  float x0[RND], x1[RND];
+  float q[GRP][8];          // the thread's 8 dims of each query head
+  float x0[GRP], x1[GRP];   // FUSED: query head h as (dim lane, dim lane + 64)
+  float a0 = 0.f, a1 = 0.f;  // FUSED, split 0: the row's key or value
   float wq0 = 1.f, wq1 = 1.f, wk0 = 1.f, wk1 = 1.f, eps = 0.f;
+  const bool app = FUSED && s == 0 && wave >= NWV - 2;  // appends the key (NWV - 2) / value
   if (FUSED) {
 #pragma unroll
-    for (int r = 0; r < RND; r++) {
-      const int it = min(wave + NWV * r, IT - 1);
-      const int col = it < GRP ? (g * GRP + it) * HD : (heads + (it - GRP) * kvh + g) * HD;
-      x0[r] = row[col + lane];
-      x1[r] = row[col + lane + 64];
+    for (int h = 0; h < GRP; h++) {
+      x0[h] = row[(g * GRP + h) * HD + lane];
+      x1[h] = row[(g * GRP + h) * HD + lane + 64];
+    }
+    if (app) {
+      const int col = (heads + (wave - (NWV - 2)) * kvh + g) * HD;
+      a0 = row[col + lane];
+      a1 = row[col + lane + 64];
     }
     wq0 = qkn[lane];
     wq1 = qkn[lane + 64];
     wk0 = qkn[HD + lane];
     wk1 = qkn[HD + lane + 64];
     eps = qkn[2 * HD];
+  } else {
+#pragma unroll
+    for (int h = 0; h < GRP; h++) {
+      const float4 *p = reinterpret_cast<const float4 *>(row + (g * GRP + h) * HD + 8 * r16);
+      const float4 u = p[0], v = p[1];
+      q[h][0] = u.x, q[h][1] = u.y, q[h][2] = u.z, q[h][3] = u.w;
+      q[h][4] = v.x, q[h][5] = v.y, q[h][6] = v.z, q[h][7] = v.w;
+    }
   }
   const RowDesc d = rd[m];
   if (d.pos < 0) return;  // inactive row (the merge writes its zeros)
@@ -360,36 +381,37 @@ __global__ __launch_bounds__(NTL) void k_attn_split(const RowDesc *__restrict__ 
   float *pm = part + ((size_t)m * heads + g * GRP) * (S + 1) * slot;  // head h at h (S + 1) slot
   if (FUSED) {
 #pragma unroll
-    for (int r = 0; r < RND; r++) {
-      const int it = wave + NWV * r;
-      if (it < GRP) {
-        norm_rope(x0[r], x1[r], wq0, wq1, cs, eps);
-        qs[it][lane] = x0[r];
-        qs[it][lane + 64] = x1[r];
-        if (s == 0) {
-          float *qo = pm + ((size_t)it * (S + 1) + S) * slot;
-          qo[lane] = x0[r];
-          qo[lane + 64] = x1[r];
-        }
-      } else if (it < IT && s == 0) {
-        if (it == GRP) norm_rope(x0[r], x1[r], wk0, wk1, cs, eps);
-        KV *dst = (it == GRP ? kc : vc) + (size_t)pos * HD;
-        dst[lane] = (KV)x0[r];
-        dst[lane + 64] = (KV)x1[r];
+    for (int h = 0; h < GRP; h++) {
+      norm_rope(x0[h], x1[h], wq0, wq1, cs, eps);
+      qw[wave][h][lane] = x0[h];
+      qw[wave][h][lane + 64] = x1[h];
+      if (s == 0 && wave == h) {
+        float *qo = pm + ((size_t)h * (S + 1) + S) * slot;
+        qo[lane] = x0[h];
+        qo[lane + 64] = x1[h];
       }
     }
-  } else {
-    for (int i = t; i < GRP * HD; i += NTL) qs[i / HD][i % HD] = row[(size_t)g * GRP * HD + i];
+    if (app) {
+      if (wave == NWV - 2) norm_rope(a0, a1, wk0, wk1, cs, eps);
+      KV *dst = (wave == NWV - 2 ? kc : vc) + (size_t)pos * HD;
+      dst[lane] = (KV)a0;
+      dst[lane + 64] = (KV)a1;
+    }
+    // the wave's own rows of LDS: ordered within the wave, no block barrier
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int h = 0; h < GRP; h++) {
+      const float4 *p = reinterpret_cast<const float4 *>(&qw[wave][h][8 * r16]);
+      const float4 u = p[0], v = p[1];
+      q[h][0] = u.x, q[h][1] = u.y, q[h][2] = u.z, q[h][3] = u.w;
+      q[h][4] = v.x, q[h][5] = v.y, q[h][6] = v.z, q[h][7] = v.w;
+    }
   }
-  __syncthreads();
 
   // scores
   const float scale = (float)(1.0 / sqrt((double)HD));
-  float q[GRP][8];
-#pragma unroll
-  for (int h = 0; h < GRP; h++)
-#pragma unroll
-    for (int e = 0; e < 8; e++) q[h][e] = qs[h][8 * r16 + e];
   float sc[GRP][NJ];
 #pragma unroll
   for (int j = 0; j < NJ; j++) {
@@ -419,8 +441,8 @@ __global__ __launch_bounds__(NTL) void k_attn_split(const RowDesc *__restrict__ 
   for (int h = 0; h < GRP; h++)
 #pragma unroll
     for (int j = 0; j < NJ; j++) sc[h][j] += dpp_f<kRowMirror>(sc[h][j]);
-  // softmax over the split, per query head
-  float mx[GRP], sum[GRP];
+  // softmax over the wave's positions, per query head
+  float mw[GRP], lw[GRP];
 #pragma unroll
   for (int h = 0; h < GRP; h++) {
     float v = -INFINITY;
@@ -430,24 +452,15 @@ __global__ __launch_bounds__(NTL) void k_attn_split(const RowDesc *__restrict__ 
       v = fmaxf(v, sc[h][j]);
     }
     v = wave_max_dpp(v);
-    if (lane == 0) red[0][h][wave] = v;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int h = 0; h < GRP; h++) {
-    float v = red[0][h][0];
-#pragma unroll
-    for (int w = 1; w < NWV; w++) v = fmaxf(v, red[0][h][w]);
-    mx[h] = v;
-    const float ref = v == -INFINITY ? 0.f : v;  // an empty split: weights 0
+    mw[h] = v;
+    const float ref = v == -INFINITY ? 0.f : v;  // no position here: weights 0
     float ls = 0.f;
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
       sc[h][j] = __expf(sc[h][j] - ref);
       ls += sc[h][j];
     }
-    ls = wave_sum_dpp(r16 == 0 ? ls : 0.f);
-    if (lane == 0) red[1][h][wave] = ls;
+    lw[h] = wave_sum_dpp(r16 == 0 ? ls : 0.f);
   }
   // values
   float o[GRP][8];
@@ -465,7 +478,7 @@ __global__ __launch_bounds__(NTL) void k_attn_split(const RowDesc *__restrict__ 
       for (int e = 0; e < 8; e++) o[h][e] = fmaf(sc[h][j], v8[e], o[h][e]);
   }
   // the 4 position groups of a wave (lanes l, l + 16, l + 32, l + 48), then
-  // the waves through LDS
+  // the waves through LDS, each rescaled to the split's maximum
 #pragma unroll
   for (int h = 0; h < GRP; h++)
 #pragma unroll
@@ -481,24 +494,31 @@ __global__ __launch_bounds__(NTL) void k_attn_split(const RowDesc *__restrict__ 
       dst[1] = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
     }
   }
-  __syncthreads();
+  if (lane == 0) {
 #pragma unroll
-  for (int h = 0; h < GRP; h++) {
-    float v = 0.f;
-#pragma unroll
-    for (int w = 0; w < NWV; w++) v += red[1][h][w];
-    sum[h] = v;
+    for (int h = 0; h < GRP; h++) {
+      wmx[wave][h] = mw[h];
+      wsum[wave][h] = lw[h];
+    }
   }
+  __syncthreads();
   for (int i = t; i < GRP * HD; i += NTL) {
     const int h = i / HD, dd = i % HD;
-    float acc = 0.f;
+    float mx = wmx[0][h];
 #pragma unroll
-    for (int u = 0; u < NWV; u++) acc += po[u][h][dd];
+    for (int w = 1; w < NWV; w++) mx = fmaxf(mx, wmx[w][h]);
+    float acc = 0.f, sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWV; w++) {
+      const float c = rescale(wmx[w][h], mx);
+      acc = fmaf(c, po[w][h][dd], acc);
+      sum = fmaf(c, wsum[w][h], sum);
+    }
     float *pp = pm + ((size_t)h * (S + 1) + s) * slot;
     pp[dd] = acc;
     if (dd == 0) {
-      pp[HD] = sum[h] > 0.f ? mx[h] : -INFINITY;
-      pp[HD + 1] = sum[h];
+      pp[HD] = sum > 0.f ? mx : -INFINITY;
+      pp[HD + 1] = sum;
     }
   }
 }
@@ -942,11 +962,11 @@ template <typename KV, bool FUSED, int G>
 int launch_g(const AttnArgs &a, int M, int positions, hipStream_t st, const hipEvent_t *ev,
              bool merge) {
   const hipEvent_t ev0 = ev ? ev[0] : nullptr, ev1 = ev ? ev[1] : nullptr;
-  const SplitShape sh = attn_split_shape(positions, sizeof(KV) == 2);
+  const SplitShape sh = attn_split_shape(positions, sizeof(KV) == 2, !merge);
   const int S = (positions + sh.len - 1) / sh.len;
-#define Q3H_S(P, T)                                                                           \
-  Q3H_LAUNCH((k_attn_split<KV, FUSED, G, P, T>), dim3(a.kvh, S, M), dim3(T), st, ev0, ev1,      \
-             a.rd, a.qkv, a.rope_cs, a.qkn, a.layer, a.kvh, S, a.part)
+#define Q3H_S(NJ)                                                                             \
+  Q3H_LAUNCH((k_attn_split<KV, FUSED, G, 16 * NJ, 256>), dim3(a.kvh, S, M), dim3(256), st, ev0, \
+             ev1, a.rd, a.qkv, a.rope_cs, a.qkn, a.layer, a.kvh, S, a.part)
   if (sh.len == kSplit && sh.threads == 0) {
     // 32 position groups: 2 positions per thread for every 64 covered
 #define Q3H_SH(NJ)                                                                          \
@@ -959,15 +979,27 @@ int launch_g(const AttnArgs &a, int M, int positions, hipStream_t st, const hipE
       default: Q3H_SH(8); break;
     }
 #undef Q3H_SH
-  } else if (sh.len == 64) {
-    Q3H_S(64, 256);
-  } else if constexpr (sizeof(KV) == 2) {
-    if (sh.len == 128)
-      Q3H_S(128, 256);
-    else
-      Q3H_S(256, 512);
   } else {
-    Q3H_S(128, 512);
+    switch (sh.len / 16) {
+      case 2: Q3H_S(2); break;
+      case 3: Q3H_S(3); break;
+      case 4: Q3H_S(4); break;
+      case 5: Q3H_S(5); break;
+      case 6: Q3H_S(6); break;
+      case 7: Q3H_S(7); break;
+      default:
+        if constexpr (sizeof(KV) == 2) {
+          if (sh.len / 16 == 8)
+            Q3H_S(8);
+          else if (sh.len / 16 == 9)
+            Q3H_S(9);
+          else
+            Q3H_S(16);
+        } else {
+          Q3H_S(8);
+        }
+        break;
+    }
   }
 #undef Q3H_S
   if (sh.threads == 0 || !merge) return 1;
@@ -1012,25 +1044,58 @@ void launch_mo_kv(const AttnArgs &a, const Mat &wo, float *y, int S, hipStream_t
 
 }  // namespace
 
-// (split length, threads) measured best on the talker shapes (28 layers, so
-// that the cache streams from HBM) among 64-256 positions x 256-1024 threads
-SplitShape attn_split_shape(int positions, bool kv16) {
+// The split length for contexts of `positions` positions: a multiple of the
+// 16 positions of one block (nj blocks per split, 256 threads). The splits of
+// kv head g are workgroups g, g + kvh, ...: with 8 kv heads they share one
+// XCD's 32 CUs, so a launch takes ceil(S / 32) rounds of a split's time, and
+// S = 33 or 65 left one CU per XCD with an extra split (measured here: 4096
+// positions 7.8 -> 6.3 us, 8192 positions 10.6 -> 9.6 us with S = 29 / 57
+// instead of 33 / 65). nj minimizes rounds x (nj + 2), the 2 standing for a
+// workgroup's fixed work (descriptor, prologue, reductions, stores), ties to
+// the fewer splits; nj <= 9 (f16) or 6 (f32) while the splits fit
+// kMaxSplitsLong, longer contexts take 16 (f16) or 8 (f32) blocks per split.
+SplitShape attn_split_shape(int positions, bool kv16, bool fold) {
   if (positions <= kSplit) return {kSplit, 0};  // one workgroup per query head
-  if (positions <= 1024) return {64, 256};
-  if (kv16) return positions <= 12288 ? SplitShape{128, 256} : SplitShape{256, 512};
-  return {128, 512};
+  const int blocks = (positions + 15) / 16;
+  const int njmax = kv16 ? 9 : 6;
+  // merged in o_proj: each of its workgroups reads all the splits' partials
+  // (2048 positions: 15 splits of 144 instead of 27 of 80, 0.6 us per layer)
+  if (fold && (blocks + njmax - 1) / njmax <= kMergeOMaxSplits) return {16 * njmax, 256};
+  int best = 0, cost = 0;
+  for (int nj = 2; nj <= njmax; nj++) {
+    const int S = (blocks + nj - 1) / nj;
+    if (S > kMaxSplitsLong) continue;
+    const int c = (S + 31) / 32 * (nj + 2);
+    if (best == 0 || c <= cost) best = nj, cost = c;
+  }
+  // more than kMaxSplitsLong splits of njmax blocks: 16 (f16) or 8 (f32)
+  // blocks per split, up to attn_max_positions
+  if (best == 0) best = kv16 ? 16 : 8;
+  return {16 * best, 256};
 }
 
 int attn_splits(int positions, bool kv16) {
   if (positions < 1) return 1;
-  const SplitShape sh = attn_split_shape(positions, kv16);
-  // the split kernel's partial slots: one per split and one for the query head
-  return sh.threads == 0 ? 1 : (positions + sh.len - 1) / sh.len + 1;
+  // the split kernel's partial slots: one per split and one for the query
+  // head, for either shape
+  int n = 1;
+  for (bool fold : {false, true}) {
+    const SplitShape sh = attn_split_shape(positions, kv16, fold);
+    if (sh.threads != 0) n = std::max(n, (positions + sh.len - 1) / sh.len + 1);
+  }
+  return n;
 }
 
-int attn_max_positions(bool kv16) {
-  return kMaxSplitsLong * attn_split_shape(1 << 30, kv16).len;
+int attn_splits_upto(int positions, bool kv16) {
+  // the split length changes with the context, so the count is not monotonic:
+  // the most over every length up to positions (within a block of 16, the
+  // count is largest at the block's last position)
+  int n = attn_splits(positions, kv16);
+  for (int p = 16; p < positions; p += 16) n = std::max(n, attn_splits(p, kv16));
+  return n;
 }
+
+int attn_max_positions(bool kv16) { return kMaxSplitsLong * 16 * (kv16 ? 16 : 8); }
 
 int launch_attn(const AttnArgs &a, int M, int positions, bool fused, bool kv16, hipStream_t st,
                 const hipEvent_t *ev, bool merge) {
@@ -1042,7 +1107,7 @@ int launch_attn(const AttnArgs &a, int M, int positions, bool fused, bool kv16, 
 }
 
 bool attn_merge_o_supported(const AttnArgs &a, const Mat &wo, int M, int positions, bool kv16) {
-  const SplitShape sh = attn_split_shape(positions, kv16);
+  const SplitShape sh = attn_split_shape(positions, kv16, true);
   const int S = (positions + sh.len - 1) / sh.len;
   return M == 1 && wo.q != nullptr && wo.K == a.heads * HD && a.heads == 16 && wo.N % 4 == 0 &&
          sh.threads != 0 && S <= kMergeOMaxSplits;
@@ -1050,7 +1115,7 @@ bool attn_merge_o_supported(const AttnArgs &a, const Mat &wo, int M, int positio
 
 void launch_attn_merge_o(const AttnArgs &a, const Mat &wo, float *y, int positions, bool fused,
                          bool kv16, hipStream_t st) {
-  const SplitShape sh = attn_split_shape(positions, kv16);
+  const SplitShape sh = attn_split_shape(positions, kv16, true);
   const int S = (positions + sh.len - 1) / sh.len;
   if (kv16)
     fused ? launch_mo_kv<_Float16, true>(a, wo, y, S, st)

@@ -169,15 +169,20 @@ struct AttnArgs {
   float *part;   // [M][heads][attn_splits slots][head_dim + 2]
 };
 // how the decode attention cuts contexts of up to `positions` positions: len
-// positions per split, threads per workgroup (0: one workgroup per query
-// head over at most 256 positions, no split)
+// positions per split (a multiple of 16), threads per workgroup (0: one
+// workgroup per query head over at most 256 positions, no split); fold: the
+// splits are merged by the o_proj product (launch_attn_merge_o), which
+// re-reads every split's partials in each of its workgroups, so it takes the
+// longest splits while they number at most kMergeOMaxSplits
 struct SplitShape {
   int len, threads;
 };
-SplitShape attn_split_shape(int positions, bool kv16);
+SplitShape attn_split_shape(int positions, bool kv16, bool fold = false);
 // partial-buffer slots per (row, query head): the splits and the query head
 // (1 when one workgroup covers the context)
 int attn_splits(int positions, bool kv16);
+// the most slots any context of up to `positions` positions needs
+int attn_splits_upto(int positions, bool kv16);
 // prefill attention on the matrix cores: the M rows of one context at
 // positions rd[0].pos + m, their K/V already appended, q normed and rotated
 void launch_attn_prefill(const AttnArgs &a, int M, bool kv16, hipStream_t st);
@@ -188,7 +193,7 @@ int attn_max_positions(bool kv16);
 // (optional, measurement): 4 events, the start and end of each kernel's own
 // execution
 // merge == false: the split kernel alone when the context is split (its
-// partials left for launch_attn_merge_o)
+// partials left for launch_attn_merge_o; the fold shape)
 int launch_attn(const AttnArgs &a, int M, int positions, bool fused, bool kv16, hipStream_t st,
                 const hipEvent_t *ev = nullptr, bool merge = true);
 // one decode row's o_proj (Q8_0 W_o [N][16 x 128]) with the split attention's

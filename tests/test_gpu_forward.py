@@ -143,24 +143,32 @@ def test_batch_equals_single(q8model, q3h, synth):
         c.destroy()
 
 
-# (positions, f16 cache): the split shapes of the long-context kernel -
-# 64-position splits up to 1024 positions, then 128 (f16 up to 12288, f32);
-# 2048, 4096 and 8192 are the long-context workload's lengths;
-# 1024 + 1 and 8192 + 1 positions leave a last split of one position; 12300
-# takes the 256-position f16 splits
-@pytest.mark.parametrize("L,kv16", [(300, 1), (1024, 1), (2048, 1), (2100, 1), (4096, 1),
-                                    (8192, 1), (12300, 1), (300, 0), (2100, 0)])
-def test_long_context_decode(device, q3h, q3o, synth, L, kv16):
+# (positions, f16 cache, kv heads): the split shapes of the long-context
+# kernel - nj blocks of 16 positions per split. With 16 query heads (8 kv
+# heads, the talker's) a decode row whose context takes at most 32 splits of
+# the longest length (9 blocks f16, 6 f32) merges them in the o_proj product;
+# with 8 query heads (4 kv heads) the length follows the context (f16: nj = 2
+# at 300, 3 at 1100, 4 at 1600, 5 at 2100, 6 at 2800, 7 at 3300, 8 at 3800,
+# 9 at 4096 / 8192 / 12300, 16 beyond 36864; f32: 2, 3, 4, 5, 6, and 8 beyond
+# 24576) and a merge kernel joins the splits; 2048, 4096 and 8192 are the
+# long-context workload's lengths; the longest cases take 2 kv heads to keep
+# the cache small
+@pytest.mark.parametrize("L,kv16,kvh", [(300, 1, 4), (1100, 1, 4), (1600, 1, 4), (2100, 1, 4),
+                                        (2800, 1, 4), (3300, 1, 4), (3800, 1, 4), (4096, 1, 4),
+                                        (2048, 1, 8), (4096, 1, 8), (8192, 1, 8), (12300, 1, 8),
+                                        (37000, 1, 2), (300, 0, 4), (1100, 0, 4), (1600, 0, 4),
+                                        (2100, 0, 4), (2800, 0, 4), (2100, 0, 8), (25000, 0, 2)])
+def test_long_context_decode(device, q3h, q3o, synth, L, kv16, kvh):
     """Split attention: K/V prefilled with N(0,1) values, then decode steps,
     against the oracle with the same cache."""
-    print(f"case L={L} kv16={kv16}", flush=True)
-    dims = dict(synth.TALKER, layers=2)
+    print(f"case L={L} kv16={kv16} kv_heads={kvh}", flush=True)
+    dims = dict(synth.TALKER, layers=2, heads=2 * kvh, kv_heads=kvh)
     layers, f = synth.stack_weights(3, "talker.model.", dims, norm_std=0.1,
                                     quantize=q3o.quantize_q8_0)
     st = q3h.Stack(device, dict(dims, dtype=q3h.Q8_0, kv_f16=kv16, act_q8=0,
                                 max_positions=L + 8), layers, f, q3h.Q8_0)
     ost = q3o.Stack(dims, layers, f, q3o.Q8_0, kv_f16=kv16)
-    kv = synth.normal(9, "kv", (2, 2, 8, L, 128), 1.0)
+    kv = synth.normal(9, "kv", (2, 2, kvh, L, 128), 1.0)
     ctx, octx = q3h.Context(st, L + 8), q3o.Ctx(ost, L + 8)
     ctx.fill_kv(kv[0], kv[1])
     octx.fill(kv[0], kv[1])
@@ -176,7 +184,8 @@ def test_long_context_decode(device, q3h, q3o, synth, L, kv16):
     assert ctx.length == L + 3
     # the timing entry leaves the context as it was
     us, nbytes = ctx.time_attention(iters=2)
-    assert us > 0 and nbytes == 2 * (2 if kv16 else 4) * 1024 * (L + 4) + 4 * (4096 + 2048)
+    ldq, nq = (dims["heads"] + 2 * kvh) * 128, dims["heads"] * 128
+    assert us > 0 and nbytes == 2 * (2 if kv16 else 4) * kvh * 128 * (L + 4) + 4 * (ldq + nq)
     assert ctx.length == L + 3
     x = synth.prompt(60, 1)
     _, s = ctx.forward(x)
@@ -185,6 +194,41 @@ def test_long_context_decode(device, q3h, q3o, synth, L, kv16):
     st.destroy()
     octx.destroy()
     ost.destroy()
+
+
+# a chunk of a few rows (fewer than the prefill kernel takes) appended to a
+# long context: the split kernel reads the rows' keys and values from the
+# cache (appended before it), each row over its own causal length
+@pytest.mark.parametrize("L,kv16,rows", [(700, 1, 5), (2100, 1, 3), (2100, 0, 7)])
+def test_long_context_chunk_of_rows(device, q3h, q3o, synth, L, kv16, rows):
+    print(f"case L={L} kv16={kv16} rows={rows}", flush=True)
+    dims = dict(synth.TALKER, layers=2)
+    layers, f = synth.stack_weights(5, "talker.model.", dims, norm_std=0.1,
+                                    quantize=q3o.quantize_q8_0)
+    st = q3h.Stack(device, dict(dims, dtype=q3h.Q8_0, kv_f16=kv16, act_q8=0,
+                                max_positions=L + 16), layers, f, q3h.Q8_0)
+    ost = q3o.Stack(dims, layers, f, q3o.Q8_0, kv_f16=kv16)
+    kv = synth.normal(11, "kv", (2, 2, 8, L, 128), 1.0)
+    ctx, octx = q3h.Context(st, L + 16), q3o.Ctx(ost, L + 16)
+    try:
+        ctx.fill_kv(kv[0], kv[1])
+        octx.fill(kv[0], kv[1])
+        tol = 1e-3 if kv16 else 1e-4
+        x = synth.prompt(80, rows)
+        _, s = ctx.forward(x)
+        assert rel(s, octx.forward(x)) < tol
+        # the rows' layer outputs, each row over its own length
+        x = synth.prompt(81, rows)
+        _, normed, lo = ctx.forward_probe(x)
+        onormed, olo = octx.forward(x, layer_out=True)
+        for l in range(dims["layers"]):
+            assert rel(lo[l], olo[l]) < tol, (l, rel(lo[l], olo[l]))
+        assert ctx.length == L + 2 * rows
+    finally:
+        ctx.destroy()
+        octx.destroy()
+        st.destroy()
+        ost.destroy()
 
 
 def test_long_context_batch_ragged(device, q3h, q3o, synth):
