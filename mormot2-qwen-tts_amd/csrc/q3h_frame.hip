@@ -296,21 +296,42 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
 
 // the next talker input: codec_emb[code 0] + sum_g pred_emb[g-1][code g] +
 // (trailing[step] or tts_pad), summed in that order; and its row descriptor.
+// element c of stream s's next talker input: codec_emb[code 0] +
+// pred_emb[g - 1][code g] for g = 1 .. groups - 1 + (trailing[step] or
+// tts_pad), added in that order. The codes (at most 16) are read first and
+// every row's element is loaded before the first add, so the sum waits for
+// one round of loads instead of one per group.
+__device__ __forceinline__ float talker_input_elem(const FrameDev &f, int s, int c) {
+  constexpr int G = 16;  // the most groups a frame takes
+  const int *codes = f.codes + (size_t)s * f.groups;
+  const int st = f.step[s];
+  const float *tail = st < f.trailing_rows[s]
+                          ? f.trailing + ((size_t)s * f.max_trailing + st) * f.H
+                          : f.tts_pad;
+  int code[G];
+#pragma unroll
+  for (int g = 0; g < G; g++) code[g] = g < f.groups ? codes[g] : 0;
+  float e[G];
+#pragma unroll
+  for (int g = 0; g < G; g++)
+    e[g] = g == 0 ? f.codec_emb[(size_t)code[0] * f.H + c]
+           : g < f.groups ? f.pred_emb[((size_t)(g - 1) * f.cp_vocab + code[g]) * f.H + c]
+                          : 0.f;
+  const float t = tail[c];
+  float x = e[0];
+#pragma unroll
+  for (int g = 1; g < G; g++)
+    if (g < f.groups) x = x + e[g];
+  return x + t;
+}
+
 __global__ void k_talker_input(FrameDev f) {
   const int s = blockIdx.y;
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
   // the row's descriptor: position = the context length (inactive: -1)
   if (c == 0) f.t_rd[s] = row_desc(f.t_ctx[s], f.alive[s] ? f.t_ctx[s]->len : -1);
   if (c >= f.H || !f.alive[s]) return;
-  const int *codes = f.codes + (size_t)s * f.groups;
-  float x = f.codec_emb[(size_t)codes[0] * f.H + c];
-  for (int g = 1; g < f.groups; g++)
-    x = x + f.pred_emb[((size_t)(g - 1) * f.cp_vocab + codes[g]) * f.H + c];
-  const int st = f.step[s];
-  if (st < f.trailing_rows[s])
-    x = x + f.trailing[((size_t)s * f.max_trailing + st) * f.H + c];
-  else
-    x = x + f.tts_pad[c];
+  const float x = talker_input_elem(f, s, c);
   f.t_h[(size_t)s * f.H + c] = x;
 }
 
@@ -326,16 +347,8 @@ __global__ __launch_bounds__(kArgBlock) void k_talker_input_q(FrameDev f) {
     quant_row_block(nullptr, nullptr, 0.f, f.H, s, f.n, f.t_xq, red);
     return;
   }
-  const int *codes = f.codes + (size_t)s * f.groups;
-  const int st = f.step[s];
   for (int c = tid; c < f.H; c += kArgBlock) {
-    float x = f.codec_emb[(size_t)codes[0] * f.H + c];
-    for (int g = 1; g < f.groups; g++)
-      x = x + f.pred_emb[((size_t)(g - 1) * f.cp_vocab + codes[g]) * f.H + c];
-    if (st < f.trailing_rows[s])
-      x = x + f.trailing[((size_t)s * f.max_trailing + st) * f.H + c];
-    else
-      x = x + f.tts_pad[c];
+    const float x = talker_input_elem(f, s, c);
     f.t_h[(size_t)s * f.H + c] = x;
     xs[c] = x;
   }
