@@ -68,8 +68,14 @@ void work_fields(const q3h_stack *s, size_t R, int splits, int head_rows, Work &
     pn = std::max(pn, (size_t)gemm_i8_chunks((int)I) * pr * H);
     each((void **)&w.gpart, sizeof(float) * pn);
   } else {
-    // K-slice sums of the products of o_proj and down (f32 activations)
-    each((void **)&w.gpart, sizeof(float) * kF32Slices * R * H);
+    // K-slice sums of the products of o_proj and down (f32 activations); up
+    // to kQ8SliceRows rows, the 256-column slices of Q8_0 q/k/v, o_proj and
+    // down
+    const size_t sr = std::min<size_t>(R, kQ8SliceRows), ldq = NQ + 2 * NKV;
+    size_t pn = kF32Slices * R * H;
+    pn = std::max(pn, sr * (H / 256) * ldq);
+    pn = std::max(pn, sr * std::max(NQ / 256, I / 256) * H);
+    each((void **)&w.gpart, sizeof(float) * pn);
   }
 }
 
@@ -242,10 +248,18 @@ static void run_layers_f32(const q3h_stack *s, Work &w, int M, int positions, bo
   launch_rmsnorm_rows(w.h, H, M, H, s->layers[0].in_norm, eps, w.normed, H, st);
   for (int l = 0; l < c.layers; l++) {
     const Layer &L = s->layers[l];
-    launch_gemm_f32(L.qkv, w.normed, H, M, EPI_STORE, w.qkv, ldq, st);
-    if (!fused)
+    // q/k/v as K slices (Q8_0, 17-64 rows of a prefill) added by the append
+    const int qs = fused ? 0 : q8x_slices(L.qkv, M);
+    if (qs > 0 && qs <= kRopeMaxSlices) {
+      launch_gemm_f32_part(L.qkv, w.normed, H, M, w.gpart, st);
       launch_qk_rope_append(w.qkv, ldq, w.rd, M, l, c.heads, c.kv_heads, hd, L.q_norm,
-                            L.k_norm, eps, s->rope_cs, kv16, st);
+                            L.k_norm, eps, s->rope_cs, kv16, st, w.gpart, qs);
+    } else {
+      launch_gemm_f32(L.qkv, w.normed, H, M, EPI_STORE, w.qkv, ldq, st);
+      if (!fused)
+        launch_qk_rope_append(w.qkv, ldq, w.rd, M, l, c.heads, c.kv_heads, hd, L.q_norm,
+                              L.k_norm, eps, s->rope_cs, kv16, st);
+    }
     AttnArgs at{};
     at.qkv = w.qkv;
     at.ldq = ldq;
@@ -261,12 +275,12 @@ static void run_layers_f32(const q3h_stack *s, Work &w, int M, int positions, bo
       launch_attn_prefill(at, M, kv16, st);
     else
       launch_attn(at, M, positions, fused, kv16, st);
-    launch_gemm_f32_part(L.o, w.att, NQ, M, w.gpart, st);
-    launch_resid_norm(w.h, w.gpart, M, H, L.post_norm, eps, w.normed, st);
+    const int so = launch_gemm_f32_part(L.o, w.att, NQ, M, w.gpart, st);
+    launch_resid_norm(w.h, w.gpart, M, H, L.post_norm, eps, w.normed, so, st);
     launch_gemm_f32(L.gu, w.normed, H, M, EPI_SWIGLU, w.act, I, st);
-    launch_gemm_f32_part(L.down, w.act, I, M, w.gpart, st);
+    const int sd = launch_gemm_f32_part(L.down, w.act, I, M, w.gpart, st);
     const float *next = l + 1 < c.layers ? s->layers[l + 1].in_norm : nullptr;
-    launch_resid_norm(w.h, w.gpart, M, H, next, eps, w.normed, st);
+    launch_resid_norm(w.h, w.gpart, M, H, next, eps, w.normed, sd, st);
     probe_layer(io, w, l, M, H, st);
   }
 }

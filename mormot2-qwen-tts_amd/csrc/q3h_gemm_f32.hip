@@ -423,7 +423,7 @@ __global__ void k_split3(const float *__restrict__ f, size_t n, uint16_t *__rest
 // over its K range; k_gemm_q8x_m64 shares them over 64 weight rows.)
 template <int KK>
 constexpr int q8x_blocks_per_wave() {
-  return KK <= 1024 ? 4 : KK / 256;  // at most 8 waves
+  return KK <= 256 ? 2 : KK <= 1024 ? 4 : KK / 256;  // 4 to 8 waves
 }
 
 template <int TM, int KK, int EPI, int NB>
@@ -439,7 +439,7 @@ __global__ __launch_bounds__(64 * (KK / (32 * q8x_blocks_per_wave<KK>()))) void 
   const int r = lane & 15, g = lane >> 4;
   const int kw = blockIdx.z * KK + wave * (32 * NBW);  // the wave's first column
   uint2 wv[NB][NBW];
-  uint32_t dw[NB][NBW / 2];  // the block scales, 4 per 8-byte load
+  uint32_t dw[NB][NBW / 2];  // the block scales, 2 per dword
 #pragma unroll
   for (int j = 0; j < NB; j++) {
     const int row = min(n0 + 16 * j + r, N - 1);
@@ -448,11 +448,15 @@ __global__ __launch_bounds__(64 * (KK / (32 * q8x_blocks_per_wave<KK>()))) void 
         reinterpret_cast<const _Float16 *>(wq + (size_t)N * K) + (size_t)row * (K / 32) + kw / 32;
 #pragma unroll
     for (int b = 0; b < NBW; b++) wv[j][b] = *reinterpret_cast<const uint2 *>(wr + 32 * b);
+    if constexpr (NBW == 2) {
+      dw[j][0] = *reinterpret_cast<const uint32_t *>(dr);
+    } else {
 #pragma unroll
-    for (int i = 0; i < NBW / 4; i++) {
-      const uint2 t = *reinterpret_cast<const uint2 *>(dr + 4 * i);
-      dw[j][2 * i] = t.x;
-      dw[j][2 * i + 1] = t.y;
+      for (int i = 0; i < NBW / 4; i++) {
+        const uint2 t = *reinterpret_cast<const uint2 *>(dr + 4 * i);
+        dw[j][2 * i] = t.x;
+        dw[j][2 * i + 1] = t.y;
+      }
     }
   }
   const float *xr[TM];
@@ -663,15 +667,27 @@ __global__ __launch_bounds__(256) void k_resid_norm(float *__restrict__ h,
   const int m = blockIdx.x, t = threadIdx.x;
   float *hr = h + (size_t)m * K;
   double ss = 0.0;
-  for (int k = t; k < K; k += 256) {
-    float a[S];
+  for (int k0 = 0; k0 < K; k0 += 1024) {
+    // four columns per thread, every load (clamped) issued before the sums
+    float a[4][S], hv[4];
 #pragma unroll
-    for (int s = 0; s < S; s++) a[s] = part[((size_t)s * M + m) * K + k];
-    float v = hr[k];
+    for (int i = 0; i < 4; i++) {
+      const int k = min(k0 + t + 256 * i, K - 1);
 #pragma unroll
-    for (int s = 0; s < S; s++) v += a[s];
-    hr[k] = v;
-    ss += (double)v * v;
+      for (int s = 0; s < S; s++) a[i][s] = part[((size_t)s * M + m) * K + k];
+      hv[i] = hr[k];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int k = k0 + t + 256 * i;
+      if (k < K) {
+        float v = hv[i];
+#pragma unroll
+        for (int s = 0; s < S; s++) v += a[i][s];
+        hr[k] = v;
+        ss += (double)v * v;
+      }
+    }
   }
   if (w == nullptr) return;
   for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
@@ -883,11 +899,19 @@ bool gemm_f32_slices_supported(int N, int K) {
   return N % 16 == 0 && K % kF32Slices == 0 && (kk == 256 || kk == 512 || kk == 768 || kk == 1024);
 }
 
-void launch_gemm_f32_part(const Mat &W, const float *x, int ldx, int M, float *part,
-                          hipStream_t st) {
-  if (!W.f)
-    launch_q8x(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
-  else if (M > 64 && W.N % 64 == 0)
+int q8x_slices(const Mat &W, int M) {
+  if (W.f || !W.q || M <= 16 || M > kQ8SliceRows || W.N % 32 != 0 || W.K % 256 != 0) return 0;
+  return W.K / 256 <= kMaxPartSlices ? W.K / 256 : 0;
+}
+
+int launch_gemm_f32_part(const Mat &W, const float *x, int ldx, int M, float *part,
+                         hipStream_t st) {
+  if (!W.f) {
+    const int ks = q8x_slices(W, M) ? W.K / 256 : kF32Slices;
+    launch_q8x(W, x, ldx, M, EPI_PART, part, W.N, ks, st);
+    return ks;
+  }
+  if (M > 64 && W.N % 64 == 0)
     launch_m64<4>(W, x, ldx, M, EPI_PART, part, W.N, st, kF32Slices);
   else if (M <= 16)
     launch_t<1>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
@@ -895,12 +919,20 @@ void launch_gemm_f32_part(const Mat &W, const float *x, int ldx, int M, float *p
     launch_t<2>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
   else
     launch_t<4>(W, x, ldx, M, EPI_PART, part, W.N, kF32Slices, st);
+  return kF32Slices;
 }
 
 void launch_resid_norm(float *h, const float *part, int M, int K, const float *norm_w,
-                       float eps, float *xn, hipStream_t st) {
-  hipLaunchKernelGGL(k_resid_norm<kF32Slices>, dim3(M), dim3(256), 0, st, h, part, M, K, norm_w,
-                     eps, xn);
+                       float eps, float *xn, int slices, hipStream_t st) {
+#define Q3H_RN(S)                                                                              \
+  hipLaunchKernelGGL(k_resid_norm<S>, dim3(M), dim3(256), 0, st, h, part, M, K, norm_w, eps, xn)
+  switch (slices) {
+    case 4: Q3H_RN(4); break;
+    case 8: Q3H_RN(8); break;
+    case 12: Q3H_RN(12); break;
+    default: require(false, Q3H_E_ARG, "launch_resid_norm: 4, 8 or 12 slices");
+  }
+#undef Q3H_RN
 }
 
 }  // namespace q3h

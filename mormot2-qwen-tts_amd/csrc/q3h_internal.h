@@ -102,18 +102,27 @@ void launch_split3(const Mat &m, hipStream_t st);
 constexpr int kGemvRows = 4;
 void launch_gemm_f32(const Mat &W, const float *x, int ldx, int M, int epi, float *y, int ldy,
                      hipStream_t st);
-// the same over M <= 16 rows with K cut into kF32Slices slices, one
-// workgroup per (16 rows, slice): the slices' sums go to part
-// [kF32Slices][M][N] (fills the chip when N / 16 is small)
+// the same with K cut into slices, one workgroup per (16 rows, slice): the
+// slices' sums go to part [slices][M][N] (fills the chip when N / 16 is
+// small). f32 weights: kF32Slices slices. Q8_0 weights over 17 to
+// kQ8SliceRows rows: slices of 256 columns (K / 256 of them, at most
+// kMaxPartSlices; 32 weight rows per workgroup), each workgroup then splitting
+// a quarter or less of the rows' activations (48 rows: q/k/v 11.1 -> 7.3 us,
+// o_proj 7.9 -> 5.3 us, down 9.7 -> 7.2 us); kF32Slices slices otherwise.
+// Returns the slice count.
 constexpr int kF32Slices = 4;
+constexpr int kQ8SliceRows = 64;
+constexpr int kMaxPartSlices = 12;
 bool gemm_f32_slices_supported(int N, int K);
-void launch_gemm_f32_part(const Mat &W, const float *x, int ldx, int M, float *part,
-                          hipStream_t st);
-// h [M][K] += the kF32Slices slices of part, in slice order; then, when
-// norm_w != nullptr, xn [M][K] = RMSNorm(h) with norm_w (double sum of
+int launch_gemm_f32_part(const Mat &W, const float *x, int ldx, int M, float *part,
+                         hipStream_t st);
+// K / 256 when W takes the 256-column slices over M rows, else 0
+int q8x_slices(const Mat &W, int M);
+// h [M][K] += the `slices` slices of part (4, 8 or 12), in slice order; then,
+// when norm_w != nullptr, xn [M][K] = RMSNorm(h) with norm_w (double sum of
 // squares)
 void launch_resid_norm(float *h, const float *part, int M, int K, const float *norm_w,
-                       float eps, float *xn, hipStream_t st);
+                       float eps, float *xn, int slices, hipStream_t st);
 // the int8 path (q3h_gemm.hip): shapes it takes (N % 16 == 0, K % 256 == 0,
 // K <= 3072)
 bool gemm_i8_supported(int N, int K);
@@ -150,9 +159,14 @@ void launch_prep(CtxDev *const *cs, const int *alive, int n, int R, RowDesc *rd,
                  hipStream_t st);
 void launch_advance(CtxDev *const *cs, const int *alive, int n, int R, hipStream_t st);
 
+// part != nullptr: the q/k/v rows are the sum of nsl <= kRopeMaxSlices K-slice
+// partials part [nsl][M][ldq], added in slice order (the normed and rotated q
+// heads still go to qkv)
+constexpr int kRopeMaxSlices = 4;
 void launch_qk_rope_append(float *qkv, int ldq, const RowDesc *rd, int M, int layer,
                            int heads, int kvh, int hd, const float *qn, const float *kn,
-                           float eps, const float *rope_cs, bool kv16, hipStream_t st);
+                           float eps, const float *rope_cs, bool kv16, hipStream_t st,
+                           const float *part = nullptr, int nsl = 0);
 
 // decode attention (q3h_attn.hip): rows m of qkv [M][ldq] with descriptors
 // rd; fused: each row is the one new position of its own context (QK-norm,

@@ -11,6 +11,7 @@
 //    of one head are contiguous, so a split of positions is one linear read.
 #include <hip/hip_runtime.h>
 
+#include "q3h_api_internal.h"
 #include "q3h_internal.h"
 #include "q3h_math.h"
 
@@ -314,7 +315,8 @@ void launch_advance(CtxDev *const *cs, const int *alive, int n, int R, hipStream
 template <typename KV>
 __global__ __launch_bounds__(kBlock) void k_qk_rope_append(
     float *qkv, int ldq, const RowDesc *rd, int layer, int heads, int kvh, int hd,
-    const float *qn, const float *kn, float eps, const float2 *rope_cs) {
+    const float *qn, const float *kn, float eps, const float2 *rope_cs, const float *part,
+    int nsl) {
   const int lane = threadIdx.x & 63;
   const int j = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
   const int m = blockIdx.y;
@@ -324,7 +326,26 @@ __global__ __launch_bounds__(kBlock) void k_qk_rope_append(
   const int half = hd >> 1;
   float *vec = qkv + (size_t)m * ldq + (size_t)j * hd;
   const bool on = lane < half;
-  float x0 = on ? vec[lane] : 0.f, x1 = on ? vec[lane + half] : 0.f;
+  float x0 = 0.f, x1 = 0.f;
+  if (nsl > 0) {
+    // the slices' loads issued together (clamped), added in slice order
+    const int M = gridDim.y;
+    float a0[kRopeMaxSlices], a1[kRopeMaxSlices];
+#pragma unroll
+    for (int z = 0; z < kRopeMaxSlices; z++) {
+      const float *p = part + ((size_t)min(z, nsl - 1) * M + m) * ldq + (size_t)j * hd;
+      a0[z] = on ? p[lane] : 0.f;
+      a1[z] = on ? p[lane + half] : 0.f;
+    }
+    x0 = a0[0];
+    x1 = a1[0];
+#pragma unroll
+    for (int z = 1; z < kRopeMaxSlices; z++)
+      if (z < nsl) x0 += a0[z], x1 += a1[z];
+  } else if (on) {
+    x0 = vec[lane];
+    x1 = vec[lane + half];
+  }
   if (j < heads + kvh) {
     const float *w = j < heads ? qn : kn;
     double ss = (double)x0 * x0 + (double)x1 * x1;
@@ -353,15 +374,19 @@ __global__ __launch_bounds__(kBlock) void k_qk_rope_append(
 
 void launch_qk_rope_append(float *qkv, int ldq, const RowDesc *rd, int M, int layer,
                            int heads, int kvh, int hd, const float *qn, const float *kn,
-                           float eps, const float *rope_cs, bool kv16, hipStream_t st) {
+                           float eps, const float *rope_cs, bool kv16, hipStream_t st,
+                           const float *part, int nsl) {
+  require(part == nullptr || (nsl >= 1 && nsl <= kRopeMaxSlices), Q3H_E_ARG,
+          "launch_qk_rope_append: 1 to 4 slices");
+  const int ns = part ? nsl : 0;
   const dim3 grid((heads + 2 * kvh + 3) / 4, M);
   const float2 *cs = reinterpret_cast<const float2 *>(rope_cs);
   if (kv16)
     hipLaunchKernelGGL(k_qk_rope_append<_Float16>, grid, dim3(kBlock), 0, st, qkv, ldq, rd,
-                       layer, heads, kvh, hd, qn, kn, eps, cs);
+                       layer, heads, kvh, hd, qn, kn, eps, cs, part, ns);
   else
     hipLaunchKernelGGL(k_qk_rope_append<float>, grid, dim3(kBlock), 0, st, qkv, ldq, rd,
-                       layer, heads, kvh, hd, qn, kn, eps, cs);
+                       layer, heads, kvh, hd, qn, kn, eps, cs, part, ns);
 }
 
 // ---------------------------------------------------------------------------
