@@ -853,6 +853,8 @@ void launch_q8x(const Mat &W, const float *x, int ldx, int M, int epi, float *y,
       launch_q8x_t<4, 1>(W, x, ldx, M, epi, y, ldy, ks, st);
   } else if (M <= 32) {
     launch_q8x_t<2, 2>(W, x, ldx, M, epi, y, ldy, ks, st);
+  } else if (M <= 48) {
+    launch_q8x_t<3, 2>(W, x, ldx, M, epi, y, ldy, ks, st);
   } else {
     launch_q8x_t<4, 2>(W, x, ldx, M, epi, y, ldy, ks, st);
   }
