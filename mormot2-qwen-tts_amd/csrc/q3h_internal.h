@@ -214,8 +214,10 @@ int launch_attn(const AttnArgs &a, int M, int positions, bool fused, bool kv16, 
 // merge in its prologue: y [N] += W_o x, x merged from a.part (the split
 // kernel of launch_attn(..., merge = false) launched before); for contexts
 // cut into at most kMergeOMaxSplits splits (the caller checks
-// attn_merge_o_supported)
-constexpr int kMergeOMaxSplits = 32;
+// attn_merge_o_supported). Every workgroup reads all the splits' partials, so
+// the fold gains less as splits are added: 15 splits 5.2 us against 3.7 + 3.2
+// us for the merge and the o_proj product, 29 splits 7.5 us against 3.6 + 3.2
+constexpr int kMergeOMaxSplits = 24;
 bool attn_merge_o_supported(const AttnArgs &a, const Mat &wo, int M, int positions, bool kv16);
 void launch_attn_merge_o(const AttnArgs &a, const Mat &wo, float *y, int positions, bool fused,
                          bool kv16, hipStream_t st);

@@ -145,8 +145,9 @@ def test_batch_equals_single(q8model, q3h, synth):
 
 # (positions, f16 cache, kv heads): the split shapes of the long-context
 # kernel - nj blocks of 16 positions per split. With 16 query heads (8 kv
-# heads, the talker's) a decode row whose context takes at most 32 splits of
-# the longest length (9 blocks f16, 6 f32) merges them in the o_proj product;
+# heads, the talker's) a decode row whose context takes at most 24 splits of
+# the longest length (9 blocks f16, 6 f32) merges them in the o_proj product
+# (2048: 15 splits, 3000: 21 splits, the second half of its split loads);
 # with 8 query heads (4 kv heads) the length follows the context (f16: nj = 2
 # at 300, 3 at 1100, 4 at 1600, 5 at 2100, 6 at 2800, 7 at 3300, 8 at 3800,
 # 9 at 4096 / 8192 / 12300, 16 beyond 36864; f32: 2, 3, 4, 5, 6, and 8 beyond
@@ -155,7 +156,8 @@ def test_batch_equals_single(q8model, q3h, synth):
 # the cache small
 @pytest.mark.parametrize("L,kv16,kvh", [(300, 1, 4), (1100, 1, 4), (1600, 1, 4), (2100, 1, 4),
                                         (2800, 1, 4), (3300, 1, 4), (3800, 1, 4), (4096, 1, 4),
-                                        (2048, 1, 8), (4096, 1, 8), (8192, 1, 8), (12300, 1, 8),
+                                        (2048, 1, 8), (3000, 1, 8), (4096, 1, 8), (8192, 1, 8),
+                                        (12300, 1, 8),
                                         (37000, 1, 2), (300, 0, 4), (1100, 0, 4), (1600, 0, 4),
                                         (2100, 0, 4), (2800, 0, 4), (2100, 0, 8), (25000, 0, 2)])
 def test_long_context_decode(device, q3h, q3o, synth, L, kv16, kvh):
