@@ -63,6 +63,7 @@ struct ConvArgs {
 // as ceil(chunks / kSliceChunks) slices, summed in slice order by
 // k_conv_reduce (a fixed split per layer: the sums do not depend on T)
 constexpr int kSliceChunks = 16;
+constexpr int kRingWorkgroups = 512;  // launches up to this size take k_conv_gemm_ring
 
 // the epilogue of one output: bias, GELU / residual / layer scale, then the
 // stores (y, and SnakeBeta of the value to z)
@@ -160,6 +161,105 @@ __global__ __launch_bounds__(64 * WN) void k_conv_gemm(ConvArgs a) {
         a.part[((size_t)blockIdx.z * a.T + m) * a.n + n] = acc[tm][q];
       else
         conv_out<EPI>(a, m, n, acc[tm][q]);
+    }
+}
+
+// k_conv_gemm for launches of few workgroups (a frame per call), where the
+// serial K walk is the time: the same tile and sums, the chunks of the slice
+// walked with the loads of D chunks in flight (a register ring,
+// the loop unrolled over the kSliceChunks chunks a slice can hold, loads at
+// clamped chunk indices so that none sits behind a branch); chunk i's
+// activations go through LDS buffer i & 1. The operands the loads need come
+// as plain arguments (preloaded in SGPRs); the epilogue's in a.
+template <int WN, int TM, int EPI>
+__global__ __launch_bounds__(64 * WN) void k_conv_gemm_ring(const float *__restrict__ x,
+                                                       const float *__restrict__ w, int cin,
+                                                       int taps, int dil, int T, int n,
+                                                       ConvArgs a) {
+  constexpr int NT = 64 * WN, XS = 36, MR = 16 * TM, D = 4;
+  constexpr int NF4 = MR * 32 / 4;                  // float4 of an activation chunk
+  constexpr int XF4 = NF4 >= NT ? NF4 / NT : 1;     // per thread
+  __shared__ float xs[2][MR * XS];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16 * WN + 16 * wave, m0 = blockIdx.y * MR;
+  const int K = taps * cin, cpk = cin / 32;
+  const int q0 = blockIdx.z * kSliceChunks, nq = min(taps * cpk - q0, kSliceChunks);
+  const float *wr = w + (size_t)min(n0 + r, n - 1) * K + 4 * g;
+  int xrow[XF4], xcol[XF4], xo[XF4];
+  const bool xact = NF4 >= NT || t < NF4;  // threads that move activations
+#pragma unroll
+  for (int i = 0; i < XF4; i++) {
+    const int f = min(t + NT * i, NF4 - 1), row = f >> 3, c4 = f & 7;
+    xrow[i] = min(m0 + row, T - 1);
+    xcol[i] = 4 * c4;
+    xo[i] = row * XS + 4 * c4;
+  }
+  float4 xn[D][XF4], wn[D][2];
+  // chunk q0 + i (clamped to the slice's last) into ring slot i % D
+  auto load = [&](int i) {
+    const int q = q0 + min(i, nq - 1), k = q / cpk, c0 = (q - k * cpk) * 32, sl = i % D;
+#pragma unroll
+    for (int j = 0; j < XF4; j++)
+      xn[sl][j] = ld4(x + (size_t)(xrow[j] + k * dil) * cin + c0 + xcol[j]);
+    wn[sl][0] = ld4(wr + 32 * q);
+    wn[sl][1] = ld4(wr + 32 * q + 16);
+  };
+  v4f acc[TM];
+#pragma unroll
+  for (int i = 0; i < TM; i++) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < D; i++) load(i);
+  if (xact)
+#pragma unroll
+    for (int j = 0; j < XF4; j++) *reinterpret_cast<float4 *>(&xs[0][xo[j]]) = xn[0][j];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kSliceChunks; i++) {
+    const int b = i & 1, sl = i % D, sn = (i + 1) % D;
+    const float4 wc[2] = {wn[sl][0], wn[sl][1]};
+    // chunk i + 1's activations to the other buffer, then chunk i + D's loads
+    // into the slot chunk i leaves
+    if (xact)
+#pragma unroll
+      for (int j = 0; j < XF4; j++) *reinterpret_cast<float4 *>(&xs[b ^ 1][xo[j]]) = xn[sn][j];
+    load(i + D);
+    if (i < nq) {
+      // the chunk's activation operands read from LDS before the MFMAs
+      float4 xa[2][TM];
+#pragma unroll
+      for (int s = 0; s < 2; s++)
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++)
+          xa[s][tm] =
+              *reinterpret_cast<const float4 *>(&xs[b][(16 * tm + r) * XS + 16 * s + 4 * g]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int s = 0; s < 2; s++) {
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++) {
+          acc[tm] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[s][tm].x, wc[s].x, acc[tm], 0, 0, 0);
+          acc[tm] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[s][tm].y, wc[s].y, acc[tm], 0, 0, 0);
+          acc[tm] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[s][tm].z, wc[s].z, acc[tm], 0, 0, 0);
+          acc[tm] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[s][tm].w, wc[s].w, acc[tm], 0, 0, 0);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  // lane l holds (m = m0 + 16 tm + 4 g + q, n = n0 + r)
+  const int nc = n0 + r;
+  if (nc >= n) return;
+#pragma unroll
+  for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int m = m0 + 16 * tm + 4 * g + q;
+      if (m >= T) continue;
+      if (gridDim.z > 1)
+        a.part[((size_t)blockIdx.z * T + m) * n + nc] = acc[tm][q];
+      else
+        conv_out<EPI>(a, m, nc, acc[tm][q]);
     }
 }
 
@@ -469,8 +569,18 @@ void conv(q3h_codec *c, const DConv &d, const float *x, int T, float *y, int epi
   const int wn = d.n % 64 == 0 ? 4 : 2;
   const int tm = T <= 16 ? 1 : (T <= 32 ? 2 : 4);
   const dim3 grid(d.n / (16 * wn), (T + 16 * tm - 1) / (16 * tm), S);
-#define Q3H_C(WN, TM, E) \
-  hipLaunchKernelGGL((k_conv_gemm<WN, TM, E>), grid, dim3(64 * WN), 0, c->stream, a)
+  // few workgroups: the deep load ring (a frame per call: 0.77 -> 0.68 ms per
+  // frame); the single-chunk lookahead otherwise (16-frame passes were 10-30 %
+  // slower on the ring)
+  const bool ring = (size_t)grid.x * grid.y * grid.z <= kRingWorkgroups;
+#define Q3H_C(WN, TM, E)                                                                     \
+  do {                                                                                       \
+    if (ring)                                                                                \
+      hipLaunchKernelGGL((k_conv_gemm_ring<WN, TM, E>), grid, dim3(64 * WN), 0, c->stream,   \
+                         a.x, a.w, a.cin, a.taps, a.dil, a.T, a.n, a);                       \
+    else                                                                                     \
+      hipLaunchKernelGGL((k_conv_gemm<WN, TM, E>), grid, dim3(64 * WN), 0, c->stream, a);    \
+  } while (0)
 #define Q3H_E(WN, TM)                      \
   do {                                     \
     if (epi == CE_BIAS)                    \
