@@ -74,7 +74,7 @@ void work_fields(const q3h_stack *s, size_t R, int splits, int head_rows, Work &
     const size_t sr = std::min<size_t>(R, kQ8SliceRows), ldq = NQ + 2 * NKV;
     size_t pn = kF32Slices * R * H;
     pn = std::max(pn, sr * (H / 256) * ldq);
-    pn = std::max(pn, sr * std::max(NQ / 256, I / 256) * H);
+    pn = std::max(pn, sr * std::min<size_t>(kMaxPartSlices, std::max(NQ, I) / 256) * H);
     each((void **)&w.gpart, sizeof(float) * pn);
   }
 }

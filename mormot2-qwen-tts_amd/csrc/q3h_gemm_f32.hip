@@ -903,7 +903,8 @@ bool gemm_f32_slices_supported(int N, int K) {
 
 int q8x_slices(const Mat &W, int M) {
   if (W.f || !W.q || M <= 16 || M > kQ8SliceRows || W.N % 32 != 0 || W.K % 256 != 0) return 0;
-  return W.K / 256 <= kMaxPartSlices ? W.K / 256 : 0;
+  const int ks = W.K / 256;  // a slice count launch_resid_norm takes
+  return ks <= 4 || ks == 6 || ks == 8 || ks == 12 ? ks : 0;
 }
 
 int launch_gemm_f32_part(const Mat &W, const float *x, int ldx, int M, float *part,
@@ -929,10 +930,14 @@ void launch_resid_norm(float *h, const float *part, int M, int K, const float *n
 #define Q3H_RN(S)                                                                              \
   hipLaunchKernelGGL(k_resid_norm<S>, dim3(M), dim3(256), 0, st, h, part, M, K, norm_w, eps, xn)
   switch (slices) {
+    case 1: Q3H_RN(1); break;
+    case 2: Q3H_RN(2); break;
+    case 3: Q3H_RN(3); break;
     case 4: Q3H_RN(4); break;
+    case 6: Q3H_RN(6); break;
     case 8: Q3H_RN(8); break;
     case 12: Q3H_RN(12); break;
-    default: require(false, Q3H_E_ARG, "launch_resid_norm: 4, 8 or 12 slices");
+    default: require(false, Q3H_E_ARG, "launch_resid_norm: 1-4, 6, 8 or 12 slices");
   }
 #undef Q3H_RN
 }

@@ -105,20 +105,20 @@ void launch_gemm_f32(const Mat &W, const float *x, int ldx, int M, int epi, floa
 // the same with K cut into slices, one workgroup per (16 rows, slice): the
 // slices' sums go to part [slices][M][N] (fills the chip when N / 16 is
 // small). f32 weights: kF32Slices slices. Q8_0 weights over 17 to
-// kQ8SliceRows rows: slices of 256 columns (K / 256 of them, at most
-// kMaxPartSlices; 32 weight rows per workgroup), each workgroup then splitting
+// kQ8SliceRows rows: slices of 256 columns (K / 256 of them: 1-4, 6, 8 or
+// 12; 32 weight rows per workgroup), each workgroup then splitting
 // a quarter or less of the rows' activations (48 rows: q/k/v 11.1 -> 7.3 us,
 // o_proj 7.9 -> 5.3 us, down 9.7 -> 7.2 us); kF32Slices slices otherwise.
 // Returns the slice count.
 constexpr int kF32Slices = 4;
 constexpr int kQ8SliceRows = 64;
-constexpr int kMaxPartSlices = 12;
+constexpr int kMaxPartSlices = 12;  // the most 256-column slices of a product
 bool gemm_f32_slices_supported(int N, int K);
 int launch_gemm_f32_part(const Mat &W, const float *x, int ldx, int M, float *part,
                          hipStream_t st);
 // K / 256 when W takes the 256-column slices over M rows, else 0
 int q8x_slices(const Mat &W, int M);
-// h [M][K] += the `slices` slices of part (4, 8 or 12), in slice order; then,
+// h [M][K] += the `slices` slices of part (1-4, 6, 8 or 12), in slice order; then,
 // when norm_w != nullptr, xn [M][K] = RMSNorm(h) with norm_w (double sum of
 // squares)
 void launch_resid_norm(float *h, const float *part, int M, int K, const float *norm_w,

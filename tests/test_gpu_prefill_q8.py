@@ -48,3 +48,29 @@ def test_q8_prefill_layers_match_the_oracle(device, chunks):
         oc.destroy()
         st.destroy()
         ost.destroy()
+
+
+# other shapes: 4 query / 2 kv heads (o_proj K = 512: 2 slices) and an
+# intermediate size of 1536 (down: 6 slices); 24 and 40 rows take the
+# 256-column slices, 8 rows the whole-K tiles
+def test_q8_prefill_other_slice_counts(device):
+    dims = dict(synth.TALKER, layers=2, heads=4, kv_heads=2, intermediate=1536)
+    layers, final = synth.stack_weights(44, "talker.model.", dims, norm_std=0.1,
+                                        quantize=q3o.quantize_q8_0)
+    st = q3h.Stack(device, dict(dims, dtype=q3h.Q8_0, kv_f16=0, act_q8=0, max_positions=128),
+                   layers, final, q3h.Q8_0)
+    ost = q3o.Stack(dims, layers, final, q3o.Q8_0, act_q8=0)
+    ctx, oc = q3h.Context(st, 128), q3o.Ctx(ost, 128)
+    try:
+        for i, rows in enumerate((24, 40, 8)):
+            x = synth.prompt(710 + i, rows)
+            _, normed, lo = ctx.forward_probe(x)
+            onormed, olo = oc.forward(x, layer_out=True)
+            for l in range(dims["layers"]):
+                assert rel(lo[l], olo[l]) < 1e-3, (rows, l, rel(lo[l], olo[l]))
+            assert rel(normed, onormed) < 1e-3
+    finally:
+        ctx.destroy()
+        oc.destroy()
+        st.destroy()
+        ost.destroy()
