@@ -87,6 +87,7 @@ void Work::ensure(const q3h_stack *s, int rows, int splits, int head_rows) {
   head_cap = head_rows > head_cap ? head_rows : head_cap;
   work_fields(s, rows_cap, splits_cap, head_cap, *this,
               [](void **slot, size_t bytes) { *slot = dev_alloc(bytes); });
+  gen++;
 }
 
 bool work_carve(const q3h_stack *s, int rows, int splits, int head_rows, void *base, size_t cap,
@@ -830,7 +831,13 @@ q3h_context *new_context(q3h_stack *s, int max_positions) {
   return ctx;
 }
 
+void drop_graphs(q3h_context *ctx) {
+  for (auto &g : ctx->graphs) (void)hipGraphExecDestroy(g.second);
+  ctx->graphs.clear();
+}
+
 void free_context(q3h_context *ctx) {
+  drop_graphs(ctx);
   ctx->w.release();
   dev_free(ctx->probe);
   dev_free(ctx->k);  // the values share this allocation
@@ -1037,20 +1044,69 @@ bool forward_args(const q3h_context *c, const float *x, int rows, int head, cons
   return true;
 }
 
-// TQwenLm.Forward on the work buffers w (sized for rows, the attention splits
-// of length + rows positions and the head's rows): blocks until the outputs
-// are in host memory
-void forward_rows(q3h_context *c, Work &w, const float *x, int rows, int head, float *logits,
-                  float *normed_last, float *layer_out = nullptr) {
+// the positions a forward of `rows` rows launches for: one row, the graph
+// cover of its length (so the captured single-row forward and the direct one
+// run the same launches); more rows, their exact count
+int forward_positions(const q3h_context *c, int rows) {
+  return rows == 1 ? graph_cover(c->len + 1, c->max_pos) : c->len + rows;
+}
+
+// the kernels of a forward: descriptors, layers, head (or final norm), the
+// device length
+void enqueue_forward(q3h_context *c, Work &w, int rows, int positions, int head,
+                     const LayerIO &io, hipStream_t st) {
   q3h_stack *s = c->s;
   const q3h_stack_config &cf = s->cfg;
   const int H = cf.hidden;
   const int head_rows = head >= 0 ? s->heads[head].N : 0;
-  const int positions = c->len + rows;
+  launch_prep(c->dev_arr, nullptr, 1, rows, w.rd, st);
+  run_layers(s, w, rows, positions, rows == 1, st, io);
+  // final norm of the last row, fused into the head product when there is one
+  if (head >= 0) {
+    linear(s, w, s->heads[head], w.h + (size_t)(rows - 1) * H, H, 1, s->final_norm, w.logits,
+           head_rows, EPI_STORE, w.normed, st);
+  } else {
+    launch_rmsnorm_rows(w.h + (size_t)(rows - 1) * H, H, 1, H, s->final_norm, cf.rms_eps,
+                        w.normed, H, st);
+  }
+  launch_advance(c->dev_arr, nullptr, 1, rows, st);
+}
+
+// the captured single-row forward of (head, cover) on c's Work buffers
+hipGraphExec_t forward_graph(q3h_context *c, int head, int positions) {
+  constexpr size_t kMaxGraphs = 32;  // per context: a code predictor's heads, a talker's covers
+  if (c->graphs_gen != c->w.gen || c->graphs.size() >= kMaxGraphs) {
+    drop_graphs(c);
+    c->graphs_gen = c->w.gen;
+  }
+  const uint64_t key = ((uint64_t)(uint32_t)(head + 1) << 32) | (uint32_t)positions;
+  for (auto &g : c->graphs)
+    if (g.first == key) return g.second;
+  LayerIO io;
+  io.single_context = true;
+  hipGraph_t graph =
+      capture_graph(c->stream, [&] { enqueue_forward(c, c->w, 1, positions, head, io, c->stream); });
+  hipGraphExec_t exec = nullptr;
+  const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  check_hip(e, "forward graph instantiate");
+  c->graphs.push_back({key, exec});
+  return exec;
+}
+
+// TQwenLm.Forward on the work buffers w (sized for rows, the attention splits
+// of forward_positions and the head's rows), replayed from a captured graph
+// when graph: blocks until the outputs are in host memory
+void forward_rows(q3h_context *c, Work &w, const float *x, int rows, int head, float *logits,
+                  float *normed_last, float *layer_out = nullptr, bool graph = false) {
+  q3h_stack *s = c->s;
+  const q3h_stack_config &cf = s->cfg;
+  const int H = cf.hidden;
+  const int head_rows = head >= 0 ? s->heads[head].N : 0;
+  const int positions = forward_positions(c, rows);
   hipStream_t st = c->stream;
   check_hip(hipMemcpyAsync(w.h, x, sizeof(float) * rows * H, hipMemcpyHostToDevice, st),
             "upload x");
-  launch_prep(c->dev_arr, nullptr, 1, rows, w.rd, st);
   LayerIO io;
   io.single_context = true;
   const size_t probe_bytes = sizeof(float) * cf.layers * rows * H;
@@ -1065,16 +1121,10 @@ void forward_rows(q3h_context *c, Work &w, const float *x, int rows, int head, f
     }
     io.layer_out = c->probe;
   }
-  run_layers(s, w, rows, positions, rows == 1, st, io);
-  // final norm of the last row, fused into the head product when there is one
-  if (head >= 0) {
-    linear(s, w, s->heads[head], w.h + (size_t)(rows - 1) * H, H, 1, s->final_norm, w.logits,
-           head_rows, EPI_STORE, w.normed, st);
-  } else {
-    launch_rmsnorm_rows(w.h + (size_t)(rows - 1) * H, H, 1, H, s->final_norm, cf.rms_eps,
-                        w.normed, H, st);
-  }
-  launch_advance(c->dev_arr, nullptr, 1, rows, st);
+  if (graph)
+    check_hip(hipGraphLaunch(forward_graph(c, head, positions), st), "forward graph launch");
+  else
+    enqueue_forward(c, w, rows, positions, head, io, st);
   check_hip(hipGetLastError(), "forward kernels");
   if (normed_last)
     check_hip(hipMemcpyAsync(normed_last, w.normed, sizeof(float) * H, hipMemcpyDeviceToHost,
@@ -1100,8 +1150,9 @@ extern "C" int q3h_forward_embeds(q3h_context *c, const float *x, int rows, int 
     q3h_stack *s = c->s;
     check_hip(hipSetDevice(s->dev->ordinal), "hipSetDevice");
     const int head_rows = head >= 0 ? s->heads[head].N : 0;
-    c->w.ensure(s, rows, attention_splits(s, c->len + rows), head_rows);
-    forward_rows(c, c->w, x, rows, head, logits, normed_last);
+    c->w.ensure(s, rows, attention_splits(s, forward_positions(c, rows)), head_rows);
+    // one row (a decode step): the forward replayed from a captured graph
+    forward_rows(c, c->w, x, rows, head, logits, normed_last, nullptr, rows == 1);
   });
 }
 
@@ -1112,7 +1163,7 @@ extern "C" int q3h_forward_embeds_probe(q3h_context *c, const float *x, int rows
     q3h_stack *s = c->s;
     check_hip(hipSetDevice(s->dev->ordinal), "hipSetDevice");
     const int head_rows = head >= 0 ? s->heads[head].N : 0;
-    c->w.ensure(s, rows, attention_splits(s, c->len + rows), head_rows);
+    c->w.ensure(s, rows, attention_splits(s, forward_positions(c, rows)), head_rows);
     forward_rows(c, c->w, x, rows, head, logits, normed_last, layer_out);
   });
 }
@@ -1130,8 +1181,8 @@ extern "C" int q3h_forward_embeds_noalloc(q3h_context *c, const float *x, int ro
             "q3h_forward_embeds_noalloc: the device has no scratch array");
     const int head_rows = head >= 0 ? s->heads[head].N : 0;
     Work w;  // a view of the array: owns nothing
-    require(work_carve(s, rows, attention_splits(s, c->len + rows), head_rows, dev->scratch,
-                       Q3H_NOALLOC_SCRATCH_BYTES, w),
+    require(work_carve(s, rows, attention_splits(s, forward_positions(c, rows)), head_rows,
+                       dev->scratch, Q3H_NOALLOC_SCRATCH_BYTES, w),
             Q3H_E_CAPACITY,
             "q3h_forward_embeds_noalloc: the work buffers of " + std::to_string(rows) +
                 " rows at " + std::to_string(c->len + rows) + " positions exceed the " +

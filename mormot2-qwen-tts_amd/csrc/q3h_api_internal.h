@@ -55,6 +55,18 @@ int guard(F &&f) {
   }
 }
 
+// The attention positions a captured step covers for contexts of up to len
+// positions: up to 256 in steps of 64 (the single-workgroup attention loads
+// what it covers), beyond that in steps of 256 with one step of headroom (the
+// split attention leaves extra splits empty); at most max_positions. A launch
+// sized for the cover gives the same sums at every length it covers up to 256
+// (the extra positions add exact zeros); beyond, the split count follows the
+// cover.
+inline int graph_cover(int len, int max_positions) {
+  const int cap = len <= 256 ? (len + 63) / 64 * 64 : ((len + 255) / 256 + 1) * 256;
+  return std::min(max_positions, cap);
+}
+
 // Captures what enqueue() launches on stream st into a new graph. When
 // enqueue throws, the capture is ended and its partial graph destroyed before
 // the error goes on, so the stream leaves capture mode and later calls work.
@@ -88,6 +100,7 @@ struct q3h_stack_fwd;
 // device buffers of one forward over up to rows_cap rows
 struct Work {
   int rows_cap = 0, splits_cap = 0, head_cap = 0;
+  unsigned gen = 0;  // counts the (re)allocations: graphs that captured the buffers check it
   float *h = nullptr;       // residual stream [rows][hidden]
   float *qkv = nullptr;     // [rows][q + k + v]
   float *att = nullptr;     // [rows][heads * head_dim]
@@ -189,6 +202,10 @@ struct q3h_context {
   q3h::Work w;
   float *probe = nullptr;  // the layer outputs of q3h_forward_embeds_probe
   size_t probe_bytes = 0;
+  // the captured single-row forwards, keyed by (head + 1) << 32 | cover, valid
+  // for the Work buffers of generation graphs_gen
+  std::vector<std::pair<uint64_t, hipGraphExec_t>> graphs;
+  unsigned graphs_gen = 0;
 };
 
 // the text projection (q3h_text.hip)

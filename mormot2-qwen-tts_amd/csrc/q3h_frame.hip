@@ -435,15 +435,6 @@ void drop_graphs(q3h_frame *f) {
   }
 }
 
-// The attention positions a captured step covers for contexts of up to len
-// positions: up to 256 in steps of 64 (the single-workgroup attention loads
-// what it covers), beyond that in steps of 256 with one step of headroom (the
-// split attention leaves extra splits empty); at most max_positions.
-int graph_cover(int len, int max_positions) {
-  const int cap = len <= 256 ? (len + 63) / 64 * 64 : ((len + 255) / 256 + 1) * 256;
-  return std::min(max_positions, cap);
-}
-
 // every slice's work done (the frame's state may be read or changed)
 void sync_slices(q3h_frame *f) {
   for (FrameSlice &sl : f->slices) check_hip(hipStreamSynchronize(sl.stream), "frame sync");
