@@ -21,10 +21,13 @@
 // in float4 slot (c*4 + i)*64 + l, so the 64 lanes of a wave read 64
 // consecutive float4 (no bank conflict).
 //
-// A single activation row (the batch-1 decode step) takes a variant with no
-// LDS and no barrier: each lane loads the 16 activations of each chunk that
-// its own quants multiply (a wave reads the whole row, from L2), the RMSNorm
-// sum of squares is a wave reduction, and every wave is independent. The
+// A single activation row (the batch-1 decode step) takes a variant without
+// the 1024-thread staging loop: every lane issues its activation (and norm
+// weight) loads, a share of the row per thread and coalesced, then all its
+// weight loads; the row is staged in LDS once per workgroup (the loads of the
+// row by each wave would cost the CU's load path more bytes than the weights
+// themselves), the RMSNorm sum of squares is a per-wave reduction joined in
+// LDS, one barrier, and each wave's dots read their columns from LDS. The
 // normed row can also be written out (xn_out, by the first wave), so the
 // final norm of a stack and its head are one launch.
 #include <hip/hip_ext.h>
@@ -181,22 +184,38 @@ __global__ __launch_bounds__(1024) void k_gemv_q8w(GemvArgs a) {
   }
 }
 
-// one activation row: no LDS, no barrier (see the header). Plain scalar
-// arguments (13 dwords, all preloaded in SGPRs), so the weight loads issue
-// without waiting on a scalar memory read; the scales are found after the
-// quants (wq + N*K). W (waves per workgroup) is an argument: blockDim is not
-// read. The residual of EPI_ADD is loaded with the weights, not at the end.
-template <int R, int C, int EPI>
+// one activation row (see the header): the row is loaded once per workgroup.
+// Plain scalar arguments (13 dwords, all preloaded in SGPRs), so the loads
+// issue without waiting on a scalar memory read; the scales are found after
+// the quants (wq + N*K). W (waves per workgroup) is an argument: blockDim is
+// not read. LW = min(W, 4) loader waves: thread t of them loads float4
+// t + 64*LW*j of the row (and of the RMSNorm weight), coalesced; waves past
+// LW repeat the loads of the first LW, so no branch sits before the weight
+// loads. The residual of EPI_ADD is loaded with the weights, not at the end.
+template <int R, int C, int EPI, int LW>
 __global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq,
                                                    const float *__restrict__ x,
                                                    const float *__restrict__ norm_w,
                                                    float *__restrict__ y, float *__restrict__ xn_out,
                                                    int N, int W, float eps) {
   constexpr int K = C * 1024, NB = K / 32;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int T = 64 * LW, J = C * 256 / T;  // loader threads, float4 per loader thread
+  __shared__ float4 xs[C * 256];               // w * x, slot (c*4 + i)*64 + l
+  __shared__ float ssw[LW];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row0 = (blockIdx.x * W + wave) * R;
   const _Float16 *__restrict__ wd = reinterpret_cast<const _Float16 *>(wq + (size_t)N * K);
+  const bool nrm = norm_w != nullptr;
 
+  // 1. the row (and the norm weight) first, then every weight load
+  const int t = tid % T;
+  float4 xv[J], wn[J];
+#pragma unroll
+  for (int j = 0; j < J; j++) xv[j] = reinterpret_cast<const float4 *>(x)[t + T * j];
+  if (nrm) {
+#pragma unroll
+    for (int j = 0; j < J; j++) wn[j] = reinterpret_cast<const float4 *>(norm_w)[t + T * j];
+  }
   int4 wv[R][C];
   float sc[R][C];
 #pragma unroll
@@ -210,21 +229,6 @@ __global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq
       sc[r][c] = (float)d[c * 32];
     }
   }
-  float4 xv[C][4];
-#pragma unroll
-  for (int c = 0; c < C; c++)
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-      xv[c][i] = reinterpret_cast<const float4 *>(x + c * 1024 + lane * 16)[i];
-  const bool nrm = norm_w != nullptr;
-  float4 wn[C][4];
-  if (nrm) {
-#pragma unroll
-    for (int c = 0; c < C; c++)
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-        wn[c][i] = reinterpret_cast<const float4 *>(norm_w + c * 1024 + lane * 16)[i];
-  }
   float yres[R];
   if (EPI == EPI_ADD) {
 #pragma unroll
@@ -232,49 +236,66 @@ __global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq
   }
   // every load above is issued before any arithmetic
   __builtin_amdgcn_sched_barrier(0);
+
+  // 2. while the weights are in flight: the loader waves stage w * x in LDS
+  // and sum the squares of x (fp32, per thread then per wave, then the LW
+  // wave sums in a fixed order)
+  float ss0 = 0.f, ss1 = 0.f;
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    const float4 v = xv[j];
+    ss0 = fmaf(v.x, v.x, fmaf(v.y, v.y, ss0));
+    ss1 = fmaf(v.z, v.z, fmaf(v.w, v.w, ss1));
+  }
+  if (wave < LW) {
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+      const int f = t + T * j;  // elements 4f .. 4f + 3
+      const int li = (((f >> 8) * 4 + (f & 3)) << 6) + ((f & 255) >> 2);
+      const float4 v = xv[j];
+      xs[li] = nrm ? make_float4(wn[j].x * v.x, wn[j].y * v.y, wn[j].z * v.z, wn[j].w * v.w) : v;
+    }
+  }
+  if (nrm) {
+    const float sw = wave_sum_dpp(ss0 + ss1);
+    if (wave < LW && lane == 0) ssw[wave] = sw;
+  }
+  __syncthreads();
   float inv = 1.f;
   if (nrm) {
-    // sum of squares in fp32 (16 C terms per lane, then the wave), the
-    // factor as 1 / sqrt in fp32
-    float ss0 = 0.f, ss1 = 0.f;
-#pragma unroll
-    for (int c = 0; c < C; c++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float4 v = xv[c][i];
-        ss0 = fmaf(v.x, v.x, fmaf(v.y, v.y, ss0));
-        ss1 = fmaf(v.z, v.z, fmaf(v.w, v.w, ss1));
-      }
-    const float ss = wave_sum_dpp(ss0 + ss1);
+    float ss = ssw[0];
+    if (LW == 2) ss += ssw[1 % LW];
+    if (LW == 4) ss = (ss + ssw[1 % LW]) + (ssw[2 % LW] + ssw[3 % LW]);
     inv = 1.0f / sqrtf(ss * (1.0f / K) + eps);
-#pragma unroll
-    for (int c = 0; c < C; c++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float4 v = xv[c][i], w = wn[c][i];
-        xv[c][i] = make_float4(w.x * v.x, w.y * v.y, w.z * v.z, w.w * v.w);
-      }
   }
+  // this lane's 16 columns of each chunk
+  float4 xl[C][4];
+#pragma unroll
+  for (int c = 0; c < C; c++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) xl[c][i] = xs[c * 256 + i * 64 + lane];
   if (xn_out != nullptr && blockIdx.x == 0 && wave == 0) {
 #pragma unroll
     for (int c = 0; c < C; c++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const float4 v = xv[c][i];
+        const float4 v = xl[c][i];
         reinterpret_cast<float4 *>(xn_out + c * 1024 + lane * 16)[i] =
             make_float4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
       }
   }
+
+  // 3. the dot products, a wave reduction, the epilogue
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; r++) {
     acc[r] = 0.f;
 #pragma unroll
     for (int c = 0; c < C; c++) {
-      float p0 = dot4_i8(wv[r][c].x, xv[c][0], 0.f);
-      float p1 = dot4_i8(wv[r][c].y, xv[c][1], 0.f);
-      p0 = dot4_i8(wv[r][c].z, xv[c][2], p0);
-      p1 = dot4_i8(wv[r][c].w, xv[c][3], p1);
+      float p0 = dot4_i8(wv[r][c].x, xl[c][0], 0.f);
+      float p1 = dot4_i8(wv[r][c].y, xl[c][1], 0.f);
+      p0 = dot4_i8(wv[r][c].z, xl[c][2], p0);
+      p1 = dot4_i8(wv[r][c].w, xl[c][3], p1);
       acc[r] = fmaf(sc[r][c], p0 + p1, acc[r]);
     }
   }
@@ -302,27 +323,40 @@ __global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq
 
 // The single-row product (EPI_STORE, RMSNorm prologue) whose activation row
 // is chosen on the device: row `code` of rows [vocab][K], code the argmax of
-// logits [vocab] (the smallest index among equal maxima: ChooseCode). Every
-// wave finds the argmax itself from L2-resident logits, so there is still no
-// barrier; the logit loads go out before the weight loads, so the argmax
-// waits only for them and the row's load overlaps the weight stream. The
-// first wave of workgroup 0 also writes, when *alive, the code and the raw row
-// (h_out): what k_cp_argmax writes for the next code-predictor forward. The
-// product equals k_gemv_q8v on that row. Arguments: the first 14 dwords are
-// preloaded into SGPRs; h_out and alive, used only at the end, come after.
+// logits [vocab] (the smallest index among equal maxima: ChooseCode). Each of
+// the 4 waves takes the argmax of a quarter of the L2-resident logits, the
+// quarters meet in LDS (the merge keeps the largest value and, among equal
+// ones, the smallest index, so its order does not matter), then the row is
+// loaded once per workgroup and staged as in k_gemv_q8v. The logit and
+// norm-weight loads go out before the weight loads, so the argmax waits only
+// for them and the row's load overlaps the weight stream. Workgroup 0 also
+// writes, when *alive, the code and the raw row (h_out): what k_cp_argmax
+// writes for the next code-predictor forward. The product equals k_gemv_q8v
+// on that row (the same sums in the same order). Arguments: the first 14
+// dwords are preloaded into SGPRs; h_out and alive, used only at the end,
+// come after.
 template <int R, int C, int W, int V4>
 __global__ __launch_bounds__(W * 64) void k_gemv_q8v_code(
     const int8_t *__restrict__ wq, const float *__restrict__ logits,
     const float *__restrict__ rows, const float *__restrict__ norm_w, float *__restrict__ y,
     int N, float eps, int *__restrict__ code_out, float *__restrict__ h_out,
     const int *__restrict__ alive) {
-  constexpr int K = C * 1024, NB = K / 32;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  static_assert(W == 4 && V4 % W == 0, "4 waves, each a quarter of the logits");
+  constexpr int K = C * 1024, NB = K / 32, VW = V4 / W;
+  __shared__ float4 xs[C * 256];  // w * x, slot (c*4 + i)*64 + l
+  __shared__ float ssw[W], amv[W], ap0;
+  __shared__ int ami[W];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row0 = (blockIdx.x * W + wave) * R;
   const _Float16 *__restrict__ wd = reinterpret_cast<const _Float16 *>(wq + (size_t)N * K);
-  float4 lg[V4];
+  // 1. this wave's quarter of the logits, the norm weight, then the weights
+  float4 lg[VW];
 #pragma unroll
-  for (int i = 0; i < V4; i++) lg[i] = reinterpret_cast<const float4 *>(logits)[i * 64 + lane];
+  for (int i = 0; i < VW; i++)
+    lg[i] = reinterpret_cast<const float4 *>(logits)[(wave * VW + i) * 64 + lane];
+  float4 wn[C];
+#pragma unroll
+  for (int j = 0; j < C; j++) wn[j] = reinterpret_cast<const float4 *>(norm_w)[tid + 256 * j];
   __builtin_amdgcn_sched_barrier(0);
   int4 wv[R][C];
   float sc[R][C];
@@ -337,21 +371,15 @@ __global__ __launch_bounds__(W * 64) void k_gemv_q8v_code(
       sc[r][c] = (float)d[c * 32];
     }
   }
-  float4 wn[C][4];
-#pragma unroll
-  for (int c = 0; c < C; c++)
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-      wn[c][i] = reinterpret_cast<const float4 *>(norm_w + c * 1024 + lane * 16)[i];
   __builtin_amdgcn_sched_barrier(0);
-  // the argmax: element 4 (64 i + lane) + e of lane's loads
+  // 2. the argmax: element 4 ((wave VW + i) 64 + lane) + e of the logits
   float bv = -INFINITY;
   int bi = 0x7fffffff;
 #pragma unroll
-  for (int i = 0; i < V4; i++) {
+  for (int i = 0; i < VW; i++) {
     const float e4[4] = {lg[i].x, lg[i].y, lg[i].z, lg[i].w};
 #pragma unroll
-    for (int e = 0; e < 4; e++) argmax_merge(bv, bi, e4[e], 4 * (i * 64 + lane) + e);
+    for (int e = 0; e < 4; e++) argmax_merge(bv, bi, e4[e], 4 * ((wave * VW + i) * 64 + lane) + e);
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
@@ -359,58 +387,64 @@ __global__ __launch_bounds__(W * 64) void k_gemv_q8v_code(
     const int i2 = __shfl_xor(bi, off, 64);
     argmax_merge(bv, bi, v2, i2);
   }
-  const int code = first_max_code(__builtin_amdgcn_readfirstlane(bi),
-                                  __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(
-                                                                __builtin_bit_cast(int, lg[0].x))));
-  const float *x = rows + (size_t)code * K;
-  float4 xv[C][4];
-#pragma unroll
-  for (int c = 0; c < C; c++)
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-      xv[c][i] = reinterpret_cast<const float4 *>(x + c * 1024 + lane * 16)[i];
-  if (blockIdx.x == 0 && wave == 0 && *alive) {
-    if (lane == 0) *code_out = code;
-#pragma unroll
-    for (int c = 0; c < C; c++)
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-        reinterpret_cast<float4 *>(h_out + c * 1024 + lane * 16)[i] = xv[c][i];
+  if (lane == 0) {
+    amv[wave] = bv;
+    ami[wave] = bi;
+    if (wave == 0) ap0 = lg[0].x;  // logits[0]
   }
-  // RMSNorm factor and w * x as k_gemv_q8v computes them
+  __syncthreads();
+  bv = -INFINITY;
+  bi = 0x7fffffff;
+#pragma unroll
+  for (int w = 0; w < W; w++) argmax_merge(bv, bi, amv[w], ami[w]);
+  const int code = first_max_code(bi, ap0);
+  // 3. the row, a quarter per wave (float4 tid + 256 j), staged as k_gemv_q8v
+  const float *x = rows + (size_t)code * K;
+  float4 xv[C];
+#pragma unroll
+  for (int j = 0; j < C; j++) xv[j] = reinterpret_cast<const float4 *>(x)[tid + 256 * j];
   float ss0 = 0.f, ss1 = 0.f;
 #pragma unroll
+  for (int j = 0; j < C; j++) {
+    const float4 v = xv[j];
+    ss0 = fmaf(v.x, v.x, fmaf(v.y, v.y, ss0));
+    ss1 = fmaf(v.z, v.z, fmaf(v.w, v.w, ss1));
+    const int f = tid + 256 * j;
+    const int li = (((f >> 8) * 4 + (f & 3)) << 6) + ((f & 255) >> 2);
+    xs[li] = make_float4(wn[j].x * v.x, wn[j].y * v.y, wn[j].z * v.z, wn[j].w * v.w);
+  }
+  const float sw = wave_sum_dpp(ss0 + ss1);
+  if (lane == 0) ssw[wave] = sw;
+  __syncthreads();
+  const float inv =
+      1.0f / sqrtf(((ssw[0] + ssw[1]) + (ssw[2] + ssw[3])) * (1.0f / K) + eps);
+  float4 xl[C][4];
+#pragma unroll
   for (int c = 0; c < C; c++)
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const float4 v = xv[c][i];
-      ss0 = fmaf(v.x, v.x, fmaf(v.y, v.y, ss0));
-      ss1 = fmaf(v.z, v.z, fmaf(v.w, v.w, ss1));
-    }
-  const float ss = wave_sum_dpp(ss0 + ss1);
-  const float inv = 1.0f / sqrtf(ss * (1.0f / K) + eps);
-#pragma unroll
-  for (int c = 0; c < C; c++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const float4 v = xv[c][i], w = wn[c][i];
-      xv[c][i] = make_float4(w.x * v.x, w.y * v.y, w.z * v.z, w.w * v.w);
-    }
+    for (int i = 0; i < 4; i++) xl[c][i] = xs[c * 256 + i * 64 + lane];
+  // 4. the dot products
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; r++) {
     acc[r] = 0.f;
 #pragma unroll
     for (int c = 0; c < C; c++) {
-      float p0 = dot4_i8(wv[r][c].x, xv[c][0], 0.f);
-      float p1 = dot4_i8(wv[r][c].y, xv[c][1], 0.f);
-      p0 = dot4_i8(wv[r][c].z, xv[c][2], p0);
-      p1 = dot4_i8(wv[r][c].w, xv[c][3], p1);
+      float p0 = dot4_i8(wv[r][c].x, xl[c][0], 0.f);
+      float p1 = dot4_i8(wv[r][c].y, xl[c][1], 0.f);
+      p0 = dot4_i8(wv[r][c].z, xl[c][2], p0);
+      p1 = dot4_i8(wv[r][c].w, xl[c][3], p1);
       acc[r] = fmaf(sc[r][c], p0 + p1, acc[r]);
     }
   }
 #pragma unroll
   for (int r = 0; r < R; r++) acc[r] = wave_sum_dpp(acc[r]) * inv;
+  // the code and the raw row, after every load of the product has been used
+  if (blockIdx.x == 0 && *alive) {
+    if (tid == 0) *code_out = code;
+#pragma unroll
+    for (int j = 0; j < C; j++) reinterpret_cast<float4 *>(h_out)[tid + 256 * j] = xv[j];
+  }
   if (lane != 0 || row0 >= N) return;
 #pragma unroll
   for (int r = 0; r < R; r++)
@@ -419,18 +453,18 @@ __global__ __launch_bounds__(W * 64) void k_gemv_q8v_code(
 
 // ev0 / ev1 (optional): events recorded at the start and the end of the
 // kernel's own execution (hipExtLaunchKernelGGL), for measurement
-template <int R, int C>
-void launch_v(const GemvArgs &a, int epi, int waves, hipStream_t st, hipEvent_t ev0 = nullptr,
-              hipEvent_t ev1 = nullptr) {
+template <int R, int C, int LW>
+void launch_vl(const GemvArgs &a, int epi, int waves, hipStream_t st, hipEvent_t ev0,
+               hipEvent_t ev1) {
   const dim3 grid(a.N / (waves * R)), block(64 * waves);
-#define Q3H_V(E)                                                                                \
-  do {                                                                                          \
-    if (ev0)                                                                                    \
-      hipExtLaunchKernelGGL((k_gemv_q8v<R, C, E>), grid, block, 0, st, ev0, ev1, 0, a.wq, a.x,  \
-                            a.norm_w, a.y, a.xn_out, a.N, waves, a.eps);                        \
-    else                                                                                        \
-      hipLaunchKernelGGL((k_gemv_q8v<R, C, E>), grid, block, 0, st, a.wq, a.x, a.norm_w, a.y,   \
-                         a.xn_out, a.N, waves, a.eps);                                          \
+#define Q3H_V(E)                                                                               \
+  do {                                                                                         \
+    if (ev0)                                                                                   \
+      hipExtLaunchKernelGGL((k_gemv_q8v<R, C, E, LW>), grid, block, 0, st, ev0, ev1, 0, a.wq, \
+                            a.x, a.norm_w, a.y, a.xn_out, a.N, waves, a.eps);                  \
+    else                                                                                       \
+      hipLaunchKernelGGL((k_gemv_q8v<R, C, E, LW>), grid, block, 0, st, a.wq, a.x, a.norm_w,  \
+                         a.y, a.xn_out, a.N, waves, a.eps);                                    \
   } while (0)
   if (epi == EPI_STORE)
     Q3H_V(EPI_STORE);
@@ -439,6 +473,17 @@ void launch_v(const GemvArgs &a, int epi, int waves, hipStream_t st, hipEvent_t 
   else if (R % 2 == 0)
     Q3H_V(EPI_SWIGLU);
 #undef Q3H_V
+}
+
+template <int R, int C>
+void launch_v(const GemvArgs &a, int epi, int waves, hipStream_t st, hipEvent_t ev0 = nullptr,
+              hipEvent_t ev1 = nullptr) {
+  if (waves >= 4)
+    launch_vl<R, C, 4>(a, epi, waves, st, ev0, ev1);
+  else if (waves >= 2)
+    launch_vl<R, C, 2>(a, epi, waves, st, ev0, ev1);
+  else
+    launch_vl<R, C, 1>(a, epi, waves, st, ev0, ev1);
 }
 
 template <int R, int C, int MR>

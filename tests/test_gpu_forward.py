@@ -143,6 +143,35 @@ def test_batch_equals_single(q8model, q3h, synth):
         c.destroy()
 
 
+def test_graph_forward_equals_direct(q8model, q3h, synth):
+    """A one-row q3h_forward_embeds replays a graph captured per (head,
+    position cover); the no-alloc forward launches the same kernels directly.
+    Bit for bit equal across covers (64, 128, 192, the 400-position cap past
+    256), with and without a head, and after the context's work buffers grow
+    between captures (the graphs captured on the old buffers are dropped)."""
+    m = q8model
+    a, b = q3h.Context(m.ts, 400), q3h.Context(m.ts, 400)
+    # (rows, head): one-row calls compared, the others identical direct launches
+    plan = [(3, 0), (1, 0), (1, -1), (1, 0), (40, -1), (1, 0), (1, -1), (100, 0), (1, 0),
+            (1, -1), (17, 0), (1, 0), (120, -1), (1, 0), (1, -1), (1, 0)]
+    seed = 60
+    for rows, head in plan:
+        x = synth.prompt(seed, rows)
+        seed += 1
+        print(f"rows {rows} head {head} at {a.length}", flush=True)
+        la, na = a.forward(x, head=head)
+        if rows == 1:
+            lb, nb = b.forward(x, head=head, noalloc=True)
+            assert np.array_equal(na, nb), (a.length, head)
+            if head >= 0:
+                assert np.array_equal(la, lb), (a.length, head)
+        else:
+            b.forward(x, head=head)
+    assert a.length == b.length == sum(r for r, _ in plan)
+    a.destroy()
+    b.destroy()
+
+
 # (positions, f16 cache, kv heads): the split shapes of the long-context
 # kernel - nj blocks of 16 positions per split. With 16 query heads (8 kv
 # heads, the talker's) a decode row whose context takes at most 24 splits of
