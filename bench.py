@@ -58,7 +58,7 @@ F32_PROMPT_ROWS = 512
 # HBM bytes per launch of the single-row Q8_0 products of one talker decode
 # step, from rocprofv3 FETCH_SIZE + WRITE_SIZE passes scaled by a plain copy
 # kernel of known size (profiles/gemv_q8_decode_step_traffic.md)
-GEMV_TRAFFIC_PER_LAUNCH = 4321175
+GEMV_TRAFFIC_PER_LAUNCH = 4320854
 PROMPT_ROWS = 48
 
 
@@ -253,29 +253,38 @@ def cpu_frames(q3o, frame, pre, gpu_codes, budget_s, max_frames, threads):
 
 def gemv_roofline(ts, args, cs=None):
     """The dominant kernel: the Q8_0 matrix-vector products of one talker
-    decode step. achieved = algorithmic bytes per launch / the kernels' own
-    average execution time (events attached to each launch). With cs: the
-    same for one code-predictor forward (5 layers + one 2048-row head, 85.8 MB:
-    after the first pass its weights stay in the 256 MB Infinity Cache)."""
-    us, launches, nbytes = ts.time_gemv(head=0, iters=args.gemv_iters, mode=2)
+    decode step. achieved = algorithmic bytes per launch / the average launch
+    duration: the products launched directly on their own stream, iters
+    passes between two HIP events recorded on that stream (mode 0 of
+    q3h_stack_time_gemv), so the gaps between launches count against the
+    kernels. Beside it: the same launches with an event pair attached to each
+    (mode 2: that timing adds its own cost to every launch) and the graph
+    replay's wall time per launch (mode 1). With cs: the same for one
+    code-predictor forward (5 layers + one 2048-row head, 85.8 MB: after the
+    first pass its weights stay in the 256 MB Infinity Cache)."""
+    us, launches, nbytes = ts.time_gemv(head=0, iters=args.gemv_iters, mode=0)
+    ev_us, _, _ = ts.time_gemv(head=0, iters=args.gemv_iters, mode=2)
     per_launch = nbytes / launches
     achieved = per_launch / (us * 1e-6) / 1e9
     wall = None
     if not args.no_graph:
         wall, _, _ = ts.time_gemv(head=0, iters=args.gemv_iters, mode=1)
-    log(f"gemv: {launches} launches/step, kernel {us:.2f} us/launch "
-        f"({achieved:.0f} GB/s), graph wall {wall if wall is None else round(wall, 2)} us/launch")
+    log(f"gemv: {launches} launches/step, {us:.2f} us/launch ({achieved:.0f} GB/s), "
+        f"events on each launch {ev_us:.2f} us, graph wall "
+        f"{wall if wall is None else round(wall, 2)} us/launch")
     out = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                frac=round(achieved / HBM_PEAK_GBS, 4), traffic=GEMV_TRAFFIC_PER_LAUNCH,
                traffic_source="profiles/gemv_q8_decode_step_traffic.md",
                kernel="k_gemv_q8v (Q8_0 matrix-vector products of one talker decode step)",
                bytes_per_launch=int(per_launch), us_per_launch=round(us, 3),
+               timing="direct launches between two events on their stream (gaps included)",
+               event_attached_us_per_launch=round(ev_us, 3),
                graph_wall_us_per_launch=None if wall is None else round(wall, 3))
     if cs is not None:
-        cus, cl, cb = cs.time_gemv(head=0, iters=args.gemv_iters, mode=2)
+        cus, cl, cb = cs.time_gemv(head=0, iters=args.gemv_iters, mode=0)
         cwall = None if args.no_graph else cs.time_gemv(head=0, iters=args.gemv_iters, mode=1)[0]
         cgbs = cb / cl / (cus * 1e-6) / 1e9
-        log(f"gemv (code predictor, cache-resident): {cl} launches/step, kernel {cus:.2f} "
+        log(f"gemv (code predictor, cache-resident): {cl} launches/step, {cus:.2f} "
             f"us/launch ({cgbs:.0f} GB/s), graph wall {cwall} us/launch")
         out["code_predictor"] = dict(launches=cl, bytes_per_launch=int(cb / cl),
                                      us_per_launch=round(cus, 3), achieved_gbs=round(cgbs, 1),
