@@ -559,12 +559,12 @@ bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st, hipEvent_t 
   const int rpb = a.N / 256;  // rows per workgroup, 256 workgroups
   if (a.M == 1) {
     // measured on the Qwen3-TTS shapes: one wave per SIMD (R = rpb / 4 rows
-    // per wave) for the plain products; the gate/up pairs (SwiGLU) run as
-    // 2-row waves (12 per workgroup), which keeps more loads in flight
+    // per wave) for the plain products; the gate/up pairs (SwiGLU) as 4-row
+    // waves (6 per workgroup: 3.47 us per launch against 3.78 for 2-row waves)
     int R1 = rpb / 4, W = 4;
     if (epi == EPI_SWIGLU) {
-      R1 = 2;
-      W = rpb / 2;
+      R1 = rpb % 4 == 0 ? 4 : 2;
+      W = rpb / R1;
     }
     if (R1 * W != rpb || W > kMaxWaves) return false;
     switch (R1) {
