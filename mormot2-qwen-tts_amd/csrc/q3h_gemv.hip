@@ -4,32 +4,29 @@
 // 6144 x 1024, down 1024 x 3072, heads 3072 / 2048 x 1024).
 //
 // One launch is 256 workgroups, one per CU: workgroup b owns N/256 consecutive
-// rows, spread over its waves (R rows per wave). The kernel is latency-bound
-// at these sizes (2-7 MB per launch), so its order of work is chosen to keep a
-// single memory round trip on the critical path:
-//   1. every lane issues all its weight loads first: for each of its rows and
-//      each 1024-column chunk, 16 quants (one dwordx4: a wave reads 1 KB of a
-//      row per instruction, coalesced) and the fp16 scale of their block;
-//   2. then the activation rows (and the RMSNorm weight) are loaded, w * x is
-//      staged in LDS and the sum of squares of x is reduced, while the weight
-//      loads are in flight;
+// rows, spread over its waves (R rows per wave), for M <= 4 activation rows.
+// The kernel is latency-bound at these sizes (2-7 MB per launch), so its
+// order of work is chosen to keep a single memory round trip on the critical
+// path:
+//   1. every lane issues its share of the activation rows (and of the RMSNorm
+//      weight) first, coalesced, then all its weight loads: for each of its
+//      rows and each 1024-column chunk, 16 quants (one dwordx4: a wave reads
+//      1 KB of a row per instruction) and the fp16 scale of their block;
+//   2. while the weights are in flight, w * x is staged in LDS once per
+//      workgroup and the sum of squares of x is reduced (per wave, then the
+//      loader waves' sums in a fixed order);
 //   3. one barrier, then the dot products from registers and LDS, a wave
 //      reduction, and the epilogue (store, residual add, or SwiGLU of an
 //      interleaved gate/up row pair). The RMSNorm factor multiplies the dot:
 //      W (w * x * inv) = inv * (W (w * x)).
+// Staging the rows once per workgroup matters: loaded by every wave, a row and
+// its norm weight cost each CU's load path more bytes than the weights
+// themselves (these loads hit L2, so HBM traffic does not show it).
 // LDS layout of the staged rows: element c*1024 + l*16 + 4*i + j of a row sits
 // in float4 slot (c*4 + i)*64 + l, so the 64 lanes of a wave read 64
-// consecutive float4 (no bank conflict).
-//
-// A single activation row (the batch-1 decode step) takes a variant without
-// the 1024-thread staging loop: every lane issues its activation (and norm
-// weight) loads, a share of the row per thread and coalesced, then all its
-// weight loads; the row is staged in LDS once per workgroup (the loads of the
-// row by each wave would cost the CU's load path more bytes than the weights
-// themselves), the RMSNorm sum of squares is a per-wave reduction joined in
-// LDS, one barrier, and each wave's dots read their columns from LDS. The
-// normed row can also be written out (xn_out, by the first wave), so the
-// final norm of a stack and its head are one launch.
+// consecutive float4 (no bank conflict). The normed row can also be written
+// out (xn_out, one row, by the first wave), so the final norm of a stack and
+// its head are one launch.
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
@@ -43,10 +40,6 @@ namespace {
 constexpr int kMaxWaves = 16;
 constexpr int kMaxRowsX = 4;  // activation rows per launch
 
-__device__ __forceinline__ float wave_sum_f(float v) { return wave_sum_dpp(v); }
-
-__device__ __forceinline__ double wave_sum_dd(double v) { return wave_sum_dpp_d(v); }
-
 __device__ __forceinline__ float dot4_i8(int w, float4 x, float acc) {
   acc = fmaf((float)(int8_t)(w), x.x, acc);
   acc = fmaf((float)(int8_t)(w >> 8), x.y, acc);
@@ -55,163 +48,45 @@ __device__ __forceinline__ float dot4_i8(int w, float4 x, float acc) {
   return acc;
 }
 
-template <int R, int C, int MR, int EPI>
-__global__ __launch_bounds__(1024) void k_gemv_q8w(GemvArgs a) {
-  extern __shared__ float4 xs4[];  // [MR][C * 256], permuted
-  __shared__ double ssp[kMaxWaves][MR];
-  constexpr int K = C * 1024, NB = K / 32;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int W = blockDim.x >> 6;
-  const int row0 = (blockIdx.x * W + wave) * R;
-  const int M = a.M;
-
-  // 1. weights of this wave's rows
-  int4 wv[R][C];
-  float sc[R][C];
-#pragma unroll
-  for (int r = 0; r < R; r++) {
-    const int row = min(row0 + r, a.N - 1);
-    const int8_t *q = a.wq + (size_t)row * K + lane * 16;
-    const _Float16 *d = a.wd + (size_t)row * NB + (lane >> 1);
-#pragma unroll
-    for (int c = 0; c < C; c++) {
-      wv[r][c] = *reinterpret_cast<const int4 *>(q + c * 1024);
-      sc[r][c] = (float)d[c * 32];
-    }
-  }
-
-  // 2. stage w * x, sum of squares of x
-  const bool nrm = a.norm_w != nullptr;
-  double ss[MR];
-#pragma unroll
-  for (int m = 0; m < MR; m++) ss[m] = 0.0;
-  for (int f = tid; f < K / 4; f += 64 * W) {
-    const int li = (((f >> 8) * 4 + (f & 3)) << 6) + ((f & 255) >> 2);
-    const float4 wn = nrm ? reinterpret_cast<const float4 *>(a.norm_w)[f]
-                          : make_float4(1.f, 1.f, 1.f, 1.f);
-#pragma unroll
-    for (int m = 0; m < MR; m++) {
-      if (m < M) {
-        const float4 v = reinterpret_cast<const float4 *>(a.x + (size_t)m * a.ldx)[f];
-        ss[m] += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z +
-                 (double)v.w * v.w;
-        xs4[m * (C * 256) + li] = make_float4(wn.x * v.x, wn.y * v.y, wn.z * v.z, wn.w * v.w);
-      }
-    }
-  }
-  if (nrm) {
-#pragma unroll
-    for (int m = 0; m < MR; m++) {
-      const double t = wave_sum_dd(ss[m]);
-      if (lane == 0) ssp[wave][m] = t;
-    }
-  }
-  __syncthreads();
-  float inv[MR];
-#pragma unroll
-  for (int m = 0; m < MR; m++) {
-    inv[m] = 1.f;
-    if (nrm && m < M) {
-      double t = 0.0;
-      for (int i = 0; i < W; i++) t += ssp[i][m];
-      inv[m] = (float)(1.0 / sqrt(t / K + (double)a.eps));
-    }
-  }
-  if (a.xn_out != nullptr && blockIdx.x == 0) {
-    // the normed last row: w * x * inv, back from the permuted layout
-    const int m = M - 1;
-    for (int f = tid; f < K / 4; f += 64 * W) {
-      const int li = (((f >> 8) * 4 + (f & 3)) << 6) + ((f & 255) >> 2);
-      const float4 v = xs4[m * (C * 256) + li];
-      const float iv = inv[0];  // xn_out is taken with a single row only
-      reinterpret_cast<float4 *>(a.xn_out)[f] = make_float4(v.x * iv, v.y * iv, v.z * iv, v.w * iv);
-    }
-  }
-  if (row0 >= a.N) return;
-
-  // 3. dot products
-  float acc[R][MR];
-#pragma unroll
-  for (int r = 0; r < R; r++)
-#pragma unroll
-    for (int m = 0; m < MR; m++) acc[r][m] = 0.f;
-#pragma unroll
-  for (int c = 0; c < C; c++) {
-#pragma unroll
-    for (int m = 0; m < MR; m++) {
-      if (m < M) {
-        const float4 *xp = xs4 + m * (C * 256) + c * 256 + lane;
-        const float4 x0 = xp[0], x1 = xp[64], x2 = xp[128], x3 = xp[192];
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-          float p0 = dot4_i8(wv[r][c].x, x0, 0.f);
-          float p1 = dot4_i8(wv[r][c].y, x1, 0.f);
-          p0 = dot4_i8(wv[r][c].z, x2, p0);
-          p1 = dot4_i8(wv[r][c].w, x3, p1);
-          acc[r][m] = fmaf(sc[r][c], p0 + p1, acc[r][m]);
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < R; r++)
-#pragma unroll
-    for (int m = 0; m < MR; m++) acc[r][m] = wave_sum_f(acc[r][m]) * inv[m];
-
-  // 4. epilogue (every lane holds the sums; lane 0 stores)
-  if (lane != 0) return;
-#pragma unroll
-  for (int m = 0; m < MR; m++) {
-    if (m >= M) break;
-    float *y = a.y + (size_t)m * a.ldy;
-    if (EPI == EPI_SWIGLU) {
-#pragma unroll
-      for (int p = 0; p < R / 2; p++) {
-        const float g = acc[2 * p][m], u = acc[2 * p + 1][m];
-        y[row0 / 2 + p] = g / (1.0f + expf(-g)) * u;
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < R; r++) {
-        if (row0 + r < a.N) {
-          if (EPI == EPI_ADD)
-            y[row0 + r] += acc[r][m];
-          else
-            y[row0 + r] = acc[r][m];
-        }
-      }
-    }
-  }
-}
-
-// one activation row (see the header): the row is loaded once per workgroup.
-// Plain scalar arguments (13 dwords, all preloaded in SGPRs), so the loads
-// issue without waiting on a scalar memory read; the scales are found after
-// the quants (wq + N*K). W (waves per workgroup) is an argument: blockDim is
-// not read. LW = min(W, 4) loader waves: thread t of them loads float4
-// t + 64*LW*j of the row (and of the RMSNorm weight), coalesced; waves past
-// LW repeat the loads of the first LW, so no branch sits before the weight
-// loads. The residual of EPI_ADD is loaded with the weights, not at the end.
-template <int R, int C, int EPI, int LW>
+// M <= MR activation rows (x rows ldx apart, y rows ldy apart; one row: the
+// batch-1 decode step), each loaded once per workgroup. Plain scalar
+// arguments: the first 14 dwords are preloaded in SGPRs (all the kernel reads
+// before its loads; one row reads neither M nor ldx / ldy), so the loads issue
+// without waiting on a scalar memory read; xn_out, read only at the end, comes
+// last. The scales are found after the quants (wq + N*K). W (waves per workgroup) is an argument: blockDim is not read.
+// LW = min(W, 4) loader waves: thread t of them loads float4 t + 64*LW*j of
+// each row (and of the RMSNorm weight), coalesced; waves past LW repeat the
+// loads of the first LW, and rows past M repeat row M - 1, so no branch sits
+// before the weight loads. The residual of EPI_ADD is loaded with the weights,
+// not at the end. Every row gets the same arithmetic in the same order as a
+// single row does, so a row's result does not depend on M. xn_out (the normed
+// row, by the first wave of workgroup 0) is taken with a single row only.
+template <int R, int C, int EPI, int LW, int MR>
 __global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq,
                                                    const float *__restrict__ x,
                                                    const float *__restrict__ norm_w,
-                                                   float *__restrict__ y, float *__restrict__ xn_out,
-                                                   int N, int W, float eps) {
+                                                   float *__restrict__ y, int N, int W, float eps,
+                                                   int ldx, int ldy, int M,
+                                                   float *__restrict__ xn_out) {
   constexpr int K = C * 1024, NB = K / 32;
   constexpr int T = 64 * LW, J = C * 256 / T;  // loader threads, float4 per loader thread
-  __shared__ float4 xs[C * 256];               // w * x, slot (c*4 + i)*64 + l
-  __shared__ float ssw[LW];
+  __shared__ float4 xs[MR][C * 256];           // w * x, slot (c*4 + i)*64 + l
+  __shared__ float ssw[MR][LW];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row0 = (blockIdx.x * W + wave) * R;
   const _Float16 *__restrict__ wd = reinterpret_cast<const _Float16 *>(wq + (size_t)N * K);
   const bool nrm = norm_w != nullptr;
 
-  // 1. the row (and the norm weight) first, then every weight load
+  // 1. the rows (and the norm weight) first, then every weight load
   const int t = tid % T;
-  float4 xv[J], wn[J];
+  float4 xv[MR][J], wn[J];
 #pragma unroll
-  for (int j = 0; j < J; j++) xv[j] = reinterpret_cast<const float4 *>(x)[t + T * j];
+  for (int m = 0; m < MR; m++) {
+    const float4 *xm =
+        reinterpret_cast<const float4 *>(MR == 1 ? x : x + (size_t)min(m, M - 1) * ldx);
+#pragma unroll
+    for (int j = 0; j < J; j++) xv[m][j] = xm[t + T * j];
+  }
   if (nrm) {
 #pragma unroll
     for (int j = 0; j < J; j++) wn[j] = reinterpret_cast<const float4 *>(norm_w)[t + T * j];
@@ -229,10 +104,13 @@ __global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq
       sc[r][c] = (float)d[c * 32];
     }
   }
-  float yres[R];
+  float yres[MR][R];
   if (EPI == EPI_ADD) {
 #pragma unroll
-    for (int r = 0; r < R; r++) yres[r] = y[min(row0 + r, N - 1)];
+    for (int m = 0; m < MR; m++)
+#pragma unroll
+      for (int r = 0; r < R; r++)
+        yres[m][r] = y[(MR == 1 ? 0 : (size_t)min(m, M - 1) * ldy) + min(row0 + r, N - 1)];
   }
   // every load above is issued before any arithmetic
   __builtin_amdgcn_sched_barrier(0);
@@ -240,82 +118,100 @@ __global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq
   // 2. while the weights are in flight: the loader waves stage w * x in LDS
   // and sum the squares of x (fp32, per thread then per wave, then the LW
   // wave sums in a fixed order)
-  float ss0 = 0.f, ss1 = 0.f;
 #pragma unroll
-  for (int j = 0; j < J; j++) {
-    const float4 v = xv[j];
-    ss0 = fmaf(v.x, v.x, fmaf(v.y, v.y, ss0));
-    ss1 = fmaf(v.z, v.z, fmaf(v.w, v.w, ss1));
-  }
-  if (wave < LW) {
+  for (int m = 0; m < MR; m++) {
+    float ss0 = 0.f, ss1 = 0.f;
 #pragma unroll
     for (int j = 0; j < J; j++) {
-      const int f = t + T * j;  // elements 4f .. 4f + 3
-      const int li = (((f >> 8) * 4 + (f & 3)) << 6) + ((f & 255) >> 2);
-      const float4 v = xv[j];
-      xs[li] = nrm ? make_float4(wn[j].x * v.x, wn[j].y * v.y, wn[j].z * v.z, wn[j].w * v.w) : v;
+      const float4 v = xv[m][j];
+      ss0 = fmaf(v.x, v.x, fmaf(v.y, v.y, ss0));
+      ss1 = fmaf(v.z, v.z, fmaf(v.w, v.w, ss1));
+    }
+    if (wave < LW) {
+#pragma unroll
+      for (int j = 0; j < J; j++) {
+        const int f = t + T * j;  // elements 4f .. 4f + 3
+        const int li = (((f >> 8) * 4 + (f & 3)) << 6) + ((f & 255) >> 2);
+        const float4 v = xv[m][j];
+        xs[m][li] =
+            nrm ? make_float4(wn[j].x * v.x, wn[j].y * v.y, wn[j].z * v.z, wn[j].w * v.w) : v;
+      }
+    }
+    if (nrm) {
+      const float sw = wave_sum_dpp(ss0 + ss1);
+      if (wave < LW && lane == 0) ssw[m][wave] = sw;
     }
   }
-  if (nrm) {
-    const float sw = wave_sum_dpp(ss0 + ss1);
-    if (wave < LW && lane == 0) ssw[wave] = sw;
-  }
   __syncthreads();
-  float inv = 1.f;
-  if (nrm) {
-    float ss = ssw[0];
-    if (LW == 2) ss += ssw[1 % LW];
-    if (LW == 4) ss = (ss + ssw[1 % LW]) + (ssw[2 % LW] + ssw[3 % LW]);
-    inv = 1.0f / sqrtf(ss * (1.0f / K) + eps);
+  float inv[MR];
+#pragma unroll
+  for (int m = 0; m < MR; m++) {
+    inv[m] = 1.f;
+    if (nrm) {
+      float ss = ssw[m][0];
+      if (LW == 2) ss += ssw[m][1 % LW];
+      if (LW == 4) ss = (ss + ssw[m][1 % LW]) + (ssw[m][2 % LW] + ssw[m][3 % LW]);
+      inv[m] = 1.0f / sqrtf(ss * (1.0f / K) + eps);
+    }
   }
-  // this lane's 16 columns of each chunk
-  float4 xl[C][4];
-#pragma unroll
-  for (int c = 0; c < C; c++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) xl[c][i] = xs[c * 256 + i * 64 + lane];
   if (xn_out != nullptr && blockIdx.x == 0 && wave == 0) {
 #pragma unroll
     for (int c = 0; c < C; c++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const float4 v = xl[c][i];
+        const float4 v = xs[0][c * 256 + i * 64 + lane];
         reinterpret_cast<float4 *>(xn_out + c * 1024 + lane * 16)[i] =
-            make_float4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
+            make_float4(v.x * inv[0], v.y * inv[0], v.z * inv[0], v.w * inv[0]);
       }
   }
 
-  // 3. the dot products, a wave reduction, the epilogue
-  float acc[R];
+  // 3. the dot products (this lane's 16 columns of each chunk, row by row),
+  // a wave reduction, the epilogue
+  float acc[MR][R];
 #pragma unroll
-  for (int r = 0; r < R; r++) {
-    acc[r] = 0.f;
+  for (int m = 0; m < MR; m++) {
+    float4 xl[C][4];
 #pragma unroll
-    for (int c = 0; c < C; c++) {
-      float p0 = dot4_i8(wv[r][c].x, xl[c][0], 0.f);
-      float p1 = dot4_i8(wv[r][c].y, xl[c][1], 0.f);
-      p0 = dot4_i8(wv[r][c].z, xl[c][2], p0);
-      p1 = dot4_i8(wv[r][c].w, xl[c][3], p1);
-      acc[r] = fmaf(sc[r][c], p0 + p1, acc[r]);
+    for (int c = 0; c < C; c++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) xl[c][i] = xs[m][c * 256 + i * 64 + lane];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      acc[m][r] = 0.f;
+#pragma unroll
+      for (int c = 0; c < C; c++) {
+        float p0 = dot4_i8(wv[r][c].x, xl[c][0], 0.f);
+        float p1 = dot4_i8(wv[r][c].y, xl[c][1], 0.f);
+        p0 = dot4_i8(wv[r][c].z, xl[c][2], p0);
+        p1 = dot4_i8(wv[r][c].w, xl[c][3], p1);
+        acc[m][r] = fmaf(sc[r][c], p0 + p1, acc[m][r]);
+      }
     }
   }
 #pragma unroll
-  for (int r = 0; r < R; r++) acc[r] = wave_sum_dpp(acc[r]) * inv;
+  for (int m = 0; m < MR; m++)
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[m][r] = wave_sum_dpp(acc[m][r]) * inv[m];
   if (lane != 0 || row0 >= N) return;
-  if (EPI == EPI_SWIGLU) {
 #pragma unroll
-    for (int p = 0; p < R / 2; p++) {
-      const float g = acc[2 * p], u = acc[2 * p + 1];
-      y[row0 / 2 + p] = g / (1.0f + expf(-g)) * u;
-    }
-  } else {
+  for (int m = 0; m < MR; m++) {
+    if (MR > 1 && m >= M) break;
+    float *ym = MR == 1 ? y : y + (size_t)m * ldy;
+    if (EPI == EPI_SWIGLU) {
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-      if (row0 + r < N) {
-        if (EPI == EPI_ADD)
-          y[row0 + r] = yres[r] + acc[r];
-        else
-          y[row0 + r] = acc[r];
+      for (int p = 0; p < R / 2; p++) {
+        const float g = acc[m][2 * p], u = acc[m][2 * p + 1];
+        ym[row0 / 2 + p] = g / (1.0f + expf(-g)) * u;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        if (row0 + r < N) {
+          if (EPI == EPI_ADD)
+            ym[row0 + r] = yres[m][r] + acc[m][r];
+          else
+            ym[row0 + r] = acc[m][r];
+        }
       }
     }
   }
@@ -453,18 +349,18 @@ __global__ __launch_bounds__(W * 64) void k_gemv_q8v_code(
 
 // ev0 / ev1 (optional): events recorded at the start and the end of the
 // kernel's own execution (hipExtLaunchKernelGGL), for measurement
-template <int R, int C, int LW>
+template <int R, int C, int LW, int MR>
 void launch_vl(const GemvArgs &a, int epi, int waves, hipStream_t st, hipEvent_t ev0,
                hipEvent_t ev1) {
   const dim3 grid(a.N / (waves * R)), block(64 * waves);
-#define Q3H_V(E)                                                                               \
-  do {                                                                                         \
-    if (ev0)                                                                                   \
-      hipExtLaunchKernelGGL((k_gemv_q8v<R, C, E, LW>), grid, block, 0, st, ev0, ev1, 0, a.wq, \
-                            a.x, a.norm_w, a.y, a.xn_out, a.N, waves, a.eps);                  \
-    else                                                                                       \
-      hipLaunchKernelGGL((k_gemv_q8v<R, C, E, LW>), grid, block, 0, st, a.wq, a.x, a.norm_w,  \
-                         a.y, a.xn_out, a.N, waves, a.eps);                                    \
+#define Q3H_V(E)                                                                                 \
+  do {                                                                                           \
+    if (ev0)                                                                                     \
+      hipExtLaunchKernelGGL((k_gemv_q8v<R, C, E, LW, MR>), grid, block, 0, st, ev0, ev1, 0, a.wq, \
+                            a.x, a.norm_w, a.y, a.N, waves, a.eps, a.ldx, a.ldy, a.M, a.xn_out); \
+    else                                                                                         \
+      hipLaunchKernelGGL((k_gemv_q8v<R, C, E, LW, MR>), grid, block, 0, st, a.wq, a.x, a.norm_w, \
+                         a.y, a.N, waves, a.eps, a.ldx, a.ldy, a.M, a.xn_out);                   \
   } while (0)
   if (epi == EPI_STORE)
     Q3H_V(EPI_STORE);
@@ -475,46 +371,39 @@ void launch_vl(const GemvArgs &a, int epi, int waves, hipStream_t st, hipEvent_t
 #undef Q3H_V
 }
 
-template <int R, int C>
-void launch_v(const GemvArgs &a, int epi, int waves, hipStream_t st, hipEvent_t ev0 = nullptr,
-              hipEvent_t ev1 = nullptr) {
-  if (waves >= 4)
-    launch_vl<R, C, 4>(a, epi, waves, st, ev0, ev1);
-  else if (waves >= 2)
-    launch_vl<R, C, 2>(a, epi, waves, st, ev0, ev1);
-  else
-    launch_vl<R, C, 1>(a, epi, waves, st, ev0, ev1);
-}
-
 template <int R, int C, int MR>
-void launch_w(const GemvArgs &a, int epi, int waves, hipStream_t st) {
-  const dim3 grid(a.N / (waves * R)), block(64 * waves);
-  const size_t lds = sizeof(float4) * MR * C * 256;
-  if (epi == EPI_STORE)
-    hipLaunchKernelGGL((k_gemv_q8w<R, C, MR, EPI_STORE>), grid, block, lds, st, a);
-  else if (epi == EPI_ADD)
-    hipLaunchKernelGGL((k_gemv_q8w<R, C, MR, EPI_ADD>), grid, block, lds, st, a);
-  else if (R % 2 == 0)
-    hipLaunchKernelGGL((k_gemv_q8w<R, C, MR, EPI_SWIGLU>), grid, block, lds, st, a);
+void launch_v(const GemvArgs &a, int epi, int waves, hipStream_t st, hipEvent_t ev0,
+              hipEvent_t ev1) {
+  if (waves >= 4)
+    launch_vl<R, C, 4, MR>(a, epi, waves, st, ev0, ev1);
+  else if (MR > 1)
+    return;  // not reached: more rows take 4 waves or more
+  else if (waves >= 2)
+    launch_vl<R, C, 2, 1>(a, epi, waves, st, ev0, ev1);
+  else
+    launch_vl<R, C, 1, 1>(a, epi, waves, st, ev0, ev1);
 }
 
-// the single-row kernel with W waves of R rows
-template <int R>
+// W waves of R rows, M <= MR activation rows
+template <int R, int MR>
 void launch_k(const GemvArgs &a, int epi, int W, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
   switch (a.K) {
-    case 1024: launch_v<R, 1>(a, epi, W, st, ev0, ev1); break;
-    case 2048: launch_v<R, 2>(a, epi, W, st, ev0, ev1); break;
-    default: launch_v<R, 3>(a, epi, W, st, ev0, ev1); break;
+    case 1024: launch_v<R, 1, MR>(a, epi, W, st, ev0, ev1); break;
+    case 2048: launch_v<R, 2, MR>(a, epi, W, st, ev0, ev1); break;
+    default: launch_v<R, 3, MR>(a, epi, W, st, ev0, ev1); break;
   }
 }
 
-template <int R, int MR>
-void launch_rc(const GemvArgs &a, int epi, int waves, hipStream_t st, hipEvent_t ev0,
-               hipEvent_t ev1) {
-  switch (a.K) {
-    case 1024: launch_w<R, 1, MR>(a, epi, waves, st); break;
-    case 2048: launch_w<R, 2, MR>(a, epi, waves, st); break;
-    default: launch_w<R, 3, MR>(a, epi, waves, st); break;
+// R1 rows per wave (1-4)
+template <int MR>
+bool launch_rows(const GemvArgs &a, int epi, int R1, int W, hipStream_t st, hipEvent_t ev0,
+                 hipEvent_t ev1) {
+  switch (R1) {
+    case 1: launch_k<1, MR>(a, epi, W, st, ev0, ev1); return true;
+    case 2: launch_k<2, MR>(a, epi, W, st, ev0, ev1); return true;
+    case 3: launch_k<3, MR>(a, epi, W, st, ev0, ev1); return true;
+    case 4: launch_k<4, MR>(a, epi, W, st, ev0, ev1); return true;
+    default: return false;
   }
 }
 
@@ -557,39 +446,20 @@ bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st, hipEvent_t 
   if (a.K != 1024 && a.K != 2048 && a.K != 3072) return false;
   if (a.N % 256 != 0) return false;
   const int rpb = a.N / 256;  // rows per workgroup, 256 workgroups
-  if (a.M == 1) {
-    // measured on the Qwen3-TTS shapes: one wave per SIMD (R = rpb / 4 rows
-    // per wave) for the plain products; the gate/up pairs (SwiGLU) as 4-row
-    // waves (6 per workgroup: 3.47 us per launch against 3.78 for 2-row waves)
-    int R1 = rpb / 4, W = 4;
-    if (epi == EPI_SWIGLU) {
-      R1 = rpb % 4 == 0 ? 4 : 2;
-      W = rpb / R1;
-    }
-    if (R1 * W != rpb || W > kMaxWaves) return false;
-    switch (R1) {
-      case 1: launch_k<1>(a, epi, W, st, ev0, ev1); return true;
-      case 2: launch_k<2>(a, epi, W, st, ev0, ev1); return true;
-      case 3: launch_k<3>(a, epi, W, st, ev0, ev1); return true;
-      case 4: launch_k<4>(a, epi, W, st, ev0, ev1); return true;
-      default: return false;
-    }
+  // measured on the Qwen3-TTS shapes, for one row and for two: one wave per
+  // SIMD (R = rpb / 4 rows per wave) for the plain products; the gate/up
+  // pairs (SwiGLU) as 4-row waves (6 per workgroup: 3.47 us per launch against
+  // 3.78 for 2-row waves at one row, 4.45 against 4.54 at two)
+  int R1 = rpb / 4, W = 4;
+  if (epi == EPI_SWIGLU) {
+    R1 = rpb % 4 == 0 ? 4 : 2;
+    W = rpb / R1;
   }
-  const int R = (epi == EPI_SWIGLU || rpb > 8) ? 2 : 1;
-  if (rpb % R != 0) return false;
-  const int waves = rpb / R;
-  if (waves < 1 || waves > kMaxWaves) return false;
-  const int MR = a.M == 1 ? 1 : (a.M == 2 ? 2 : 4);
-  if (R == 1) {
-    if (MR == 1) launch_rc<1, 1>(a, epi, waves, st, ev0, ev1);
-    else if (MR == 2) launch_rc<1, 2>(a, epi, waves, st, ev0, ev1);
-    else launch_rc<1, 4>(a, epi, waves, st, ev0, ev1);
-  } else {
-    if (MR == 1) launch_rc<2, 1>(a, epi, waves, st, ev0, ev1);
-    else if (MR == 2) launch_rc<2, 2>(a, epi, waves, st, ev0, ev1);
-    else launch_rc<2, 4>(a, epi, waves, st, ev0, ev1);
-  }
-  return true;
+  if (R1 < 1 || R1 * W != rpb || W > kMaxWaves) return false;
+  if (a.M == 1) return launch_rows<1>(a, epi, R1, W, st, ev0, ev1);
+  if (W < 4) return false;  // more rows: 4 loader waves
+  if (a.M == 2) return launch_rows<2>(a, epi, R1, W, st, ev0, ev1);
+  return launch_rows<4>(a, epi, R1, W, st, ev0, ev1);
 }
 
 }  // namespace q3h
