@@ -43,8 +43,8 @@ __device__ __forceinline__ float *scales_of(int8_t *xq, int M, int K) {
 }
 
 // The quantizer. One workgroup per activation row m < Mp and slice of its
-// 8-element chunks (gridDim.x == Mp, M rounded up to 16; gridDim.y slices): a
-// thread owns chunks j = blockIdx.y * 128 + t + i * 128 * gridDim.y, and the
+// 8-element chunks (gridDim.x == Mp, M rounded up to 16; gridDim.y == nsl
+// slices): a thread owns chunks j = blockIdx.y * 128 + t + i * 128 * nsl, and the
 // four chunks of a lane quad make one 32-block. Rows M..Mp-1 are written as
 // zeros. The row is
 //  SRC_X:      x[m][0..K) (row stride ld);
@@ -60,15 +60,18 @@ __device__ __forceinline__ float *scales_of(int8_t *xq, int M, int K) {
 enum { SRC_X = 0, SRC_ADD = 1, SRC_SWIGLU = 2 };
 
 // KC: chunks per thread (the row's chunks / (128 slices), rounded up); NC: the
-// partial slots read (ld <= NC; SRC_ADD and SRC_SWIGLU)
+// partial slots read (ld <= NC; SRC_ADD and SRC_SWIGLU). The arguments the
+// loads depend on (the slice count among them, instead of gridDim) sit in the
+// first 14 dwords, which arrive preloaded in SGPRs; xn_out, used only at the
+// end, comes last.
 template <int SRC, int KC, int NC>
 __global__ __launch_bounds__(kQuantThreads) void k_quant_act(float *x, const float *part,
                                                               int8_t *xq, const float *norm_w,
-                                                              float *xn_out, int M, int K,
-                                                              int ld, float eps) {
+                                                              int M, int K, int ld, float eps,
+                                                              int nsl, float *xn_out) {
   const int m = blockIdx.x, t = threadIdx.x;
-  const int mt16 = gridDim.x >> 4, nch = K >> 3, nb = K >> 5;
-  const int j0 = blockIdx.y * kQuantThreads + t, js = kQuantThreads * gridDim.y;
+  const int mt16 = (M + 15) >> 4, nch = K >> 3, nb = K >> 5;
+  const int j0 = blockIdx.y * kQuantThreads + t, js = kQuantThreads * nsl;
   float *dx = xq ? scales_of(xq, M, K) : nullptr;
   if (m >= M) {
     if (xq)
@@ -455,7 +458,7 @@ void quant_launch_nc(float *x, const float *part, int ld, int M, int K, const fl
   const dim3 grid(Mp, slices);
 #define Q3H_QUANT(KC)                                                                          \
   hipLaunchKernelGGL((k_quant_act<SRC, KC, NC>), grid, dim3(kQuantThreads), 0, st, x, part,    \
-                     out.q, norm_w, xn_out, M, K, ld, eps)
+                     out.q, norm_w, M, K, ld, eps, slices, xn_out)
   if (kc <= 1)
     Q3H_QUANT(1);
   else if (kc == 2)
