@@ -144,7 +144,11 @@ int q3h_context_time_attention(q3h_context *c, int iters, float *us_per_launch,
    length..length+rows-1; normed_last [hidden] (nullable) receives the
    final-normed state of the last row; head: an index of q3h_stack_add_head,
    or -1 for none; logits [head rows] (nullable). Blocks until the outputs
-   are in host memory. rows <= 0 does nothing (lm.pas:394-395). ---- */
+   are in host memory. rows <= 0 does nothing (lm.pas:394-395). One row
+   replays a HIP graph the context captures per (head, position cover)
+   (covers of 64 positions up to 256, of 256 beyond; at most 32 graphs per
+   context, dropped when its work buffers grow); the results are those of
+   the same launches made directly (q3h_forward_embeds_noalloc). ---- */
 int q3h_forward_embeds(q3h_context *c, const float *x, int rows, int head,
                        float *logits, float *normed_last);
 
