@@ -103,16 +103,9 @@ __global__ __launch_bounds__(NT) void k_attn_o_cp(const int8_t *__restrict__ wo,
   const int row = blockIdx.x * ROWS + w;  // this wave's o_proj row
   const _Float16 *wd = reinterpret_cast<const _Float16 *>(wo + (size_t)HID * NQ);
 
-  // 1. every load up front: the Wo row, the residual, the raw q/k/v of kv
-  // head w, the norm weights, the RoPE row, the cached keys and values
-  int4 wv[2];
-  float sc[2];
-#pragma unroll
-  for (int c = 0; c < 2; c++) {
-    wv[c] = *reinterpret_cast<const int4 *>(wo + (size_t)row * NQ + c * 1024 + lane * 16);
-    sc[c] = (float)wd[(size_t)row * NBO + c * 32 + (lane >> 1)];
-  }
-  const float hr = h[row];
+  // 1. every load up front, in the order of use (a wave's loads complete in
+  // issue order): the raw q/k/v of kv head w, the norm weights, the RoPE row,
+  // the cached keys, the cached values, then the Wo row and the residual
   float xq[GRP][2], xk[2], xv[2];
 #pragma unroll
   for (int j = 0; j < GRP; j++) {
@@ -147,6 +140,15 @@ __global__ __launch_bounds__(NT) void k_attn_o_cp(const int8_t *__restrict__ wo,
 #pragma unroll
     for (int e = 0; e < LW; e++) vr[j][e] = *reinterpret_cast<const u32x4 *>(vh + off + 4 * e);
   }
+  __builtin_amdgcn_sched_barrier(0);
+  int4 wv[2];
+  float sc[2];
+#pragma unroll
+  for (int c = 0; c < 2; c++) {
+    wv[c] = *reinterpret_cast<const int4 *>(wo + (size_t)row * NQ + c * 1024 + lane * 16);
+    sc[c] = (float)wd[(size_t)row * NBO + c * 32 + (lane >> 1)];
+  }
+  const float hr = h[row];
   __builtin_amdgcn_sched_barrier(0);
 
   // 2. QK-norm + RoPE; the new key and value rounded as the cache holds them
@@ -316,14 +318,9 @@ __global__ __launch_bounds__(NT) void k_attn2_o_cp(const int8_t *__restrict__ wo
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int row = blockIdx.x * ROWS + w;
   const _Float16 *wd = reinterpret_cast<const _Float16 *>(wo + (size_t)HID * NQ);
-  int4 wv[2];
-  float sc[2];
-#pragma unroll
-  for (int c = 0; c < 2; c++) {
-    wv[c] = *reinterpret_cast<const int4 *>(wo + (size_t)row * NQ + c * 1024 + lane * 16);
-    sc[c] = (float)wd[(size_t)row * NBO + c * 32 + (lane >> 1)];
-  }
-  const float hr0 = h[row], hr1 = h[HID + row];
+  // loads in the order of use (a wave's loads complete in issue order): the
+  // two rows' q/k/v, the norm weights and RoPE rows, then the Wo row and the
+  // residuals
   float xq[2][GRP][2], xk[2][2], xv[2][2];
 #pragma unroll
   for (int r = 0; r < 2; r++) {
@@ -342,6 +339,15 @@ __global__ __launch_bounds__(NT) void k_attn2_o_cp(const int8_t *__restrict__ wo
   const float kn0 = qkn[HD + lane], kn1 = qkn[HD + lane + 64];
   const float eps = qkn[2 * HD];
   const float2 cs0 = rope[lane], cs1 = rope[HD / 2 + lane];
+  __builtin_amdgcn_sched_barrier(0);
+  int4 wv[2];
+  float sc[2];
+#pragma unroll
+  for (int c = 0; c < 2; c++) {
+    wv[c] = *reinterpret_cast<const int4 *>(wo + (size_t)row * NQ + c * 1024 + lane * 16);
+    sc[c] = (float)wd[(size_t)row * NBO + c * 32 + (lane >> 1)];
+  }
+  const float hr0 = h[row], hr1 = h[HID + row];
   __builtin_amdgcn_sched_barrier(0);
 
   // keys and values as the cache holds them
