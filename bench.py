@@ -420,7 +420,9 @@ def long_context_attention(dev, f32, tables, seed, steps=32, iters=10):
     """Talker Q8_0 at batch 1 with an f16 K/V cache prefilled to 2048, 4096 and
     8192 positions (N(0,1) values from a seed): 32 greedy decode steps at each
     length (q3h_forward_embeds, host row in and logits out, so PCIe-inclusive),
-    then the decode attention kernels alone (events attached to each launch):
+    then the decode attention kernels alone (launched directly over the 28
+    layers, iters passes between two events on their stream, so the gaps
+    between the split kernel, the merge and the next layer count too):
     algorithmic bytes = the f16 K/V of every position read once (8 kv heads x
     128 dims x 2 x 2 B = 4 KB per position and layer)."""
     t0 = time.time()

@@ -125,11 +125,11 @@ int q3h_context_fill_kv(q3h_context *c, const float *k, const float *v, int len)
 int q3h_context_read_kv(q3h_context *c, int layer, float *k, float *v);
 /* no reference counterpart (measurement): the decode attention of every
    layer for one new row at position length (the attention kernels of
-   q3h_forward_embeds with rows = 1, fused QK-norm / RoPE / K/V append), run
-   iters times with events attached to each launch. us_per_launch: the
-   kernels' own average execution time per layer (with the merge of the
-   splits on long contexts: the sum of the two kernels, the launch gap
-   between them excluded); bytes_per_launch: algorithmic bytes
+   q3h_forward_embeds with rows = 1, fused QK-norm / RoPE / K/V append),
+   launched directly iters times over the layers on one stream.
+   us_per_launch: the time between two events around those launches per
+   layer (with the merge of the splits on long contexts: both kernels and the
+   gaps between launches); bytes_per_launch: algorithmic bytes
    (the cache of length positions read, the new key and value written, the
    q / k / v row read, the outputs written). The row's q / k / v are zeros;
    the key and value written at position length are scratch (the length does

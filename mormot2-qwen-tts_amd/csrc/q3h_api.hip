@@ -955,7 +955,7 @@ extern "C" int q3h_context_time_attention(q3h_context *c, int iters, float *us_p
                                           int64_t *bytes_per_launch) {
   Work w;
   hipStream_t st = nullptr;
-  std::vector<hipEvent_t> ev;  // a start and an end event per layer
+  hipEvent_t e0 = nullptr, e1 = nullptr;  // around the timed passes
   int rc = guard([&] {
     require(c && us_per_launch && bytes_per_launch && iters > 0, Q3H_E_ARG,
             "q3h_context_time_attention: invalid argument");
@@ -982,31 +982,26 @@ extern "C" int q3h_context_time_attention(q3h_context *c, int iters, float *us_p
     at.rope_cs = reinterpret_cast<const float2 *>(s->rope_cs);
     at.out = w.att;
     at.part = w.part;
-    ev.assign(4 * cf.layers, nullptr);
-    for (auto &e : ev) check_hip(hipEventCreate(&e), "event");
-    int kernels = 1;
-    auto pass = [&](bool timed) {
+    check_hip(hipEventCreate(&e0), "event");
+    check_hip(hipEventCreate(&e1), "event");
+    // the layers' attention launches, direct, on one stream: the time between
+    // two events around iters passes counts the gaps between launches too
+    auto pass = [&] {
       for (int l = 0; l < cf.layers; l++) {
         at.layer = l;
         at.qkn = s->layers[l].q_norm;
-        kernels = launch_attn(at, 1, positions, true, kv16, st, timed ? &ev[4 * l] : nullptr);
+        launch_attn(at, 1, positions, true, kv16, st, nullptr);
       }
     };
-    pass(false);  // warm-up
+    pass();  // warm-up
     check_hip(hipStreamSynchronize(st), "warm-up sync");
-    double total = 0.0;
-    for (int it = 0; it < iters; it++) {
-      pass(true);
-      check_hip(hipStreamSynchronize(st), "timed sync");
-      for (int l = 0; l < cf.layers; l++) {
-        float t = 0.f;
-        // the kernels' own execution (the split merge's included)
-        for (int k = 0; k < kernels; k++) {
-          check_hip(hipEventElapsedTime(&t, ev[4 * l + 2 * k], ev[4 * l + 2 * k + 1]), "elapsed");
-          total += t;
-        }
-      }
-    }
+    check_hip(hipEventRecord(e0, st), "event record");
+    for (int it = 0; it < iters; it++) pass();
+    check_hip(hipEventRecord(e1, st), "event record");
+    check_hip(hipEventSynchronize(e1), "timed sync");
+    float ms = 0.f;
+    check_hip(hipEventElapsedTime(&ms, e0, e1), "elapsed");
+    const double total = ms;
     check_hip(hipGetLastError(), "attention kernels");
     *us_per_launch = (float)(total * 1000.0 / ((double)iters * cf.layers));
     const int64_t es = kv16 ? 2 : 4;
@@ -1015,8 +1010,8 @@ extern "C" int q3h_context_time_attention(q3h_context *c, int iters, float *us_p
     *bytes_per_launch = 2 * es * (int64_t)NKV * c->len + 2 * es * NKV + 4 * (int64_t)ldq +
                         4 * (int64_t)NQ;
   });
-  for (auto e : ev)
-    if (e) (void)hipEventDestroy(e);
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
   if (st) {
     (void)hipStreamSynchronize(st);
     (void)hipStreamDestroy(st);
