@@ -233,8 +233,7 @@ __global__ __launch_bounds__(NTS) void k_attn_short(const RowDesc *__restrict__ 
   }
 #pragma unroll
   for (int e = 0; e < 8; e++) {
-    o[e] += __shfl_xor(o[e], 16);
-    o[e] += __shfl_xor(o[e], 32);
+    o[e] = rows4_sum(o[e]);
   }
   if (lane < 16) {
     float4 *dst = reinterpret_cast<float4 *>(&po[wave][8 * r16]);
@@ -483,8 +482,7 @@ __global__ __launch_bounds__(NTL) void k_attn_split(const RowDesc *__restrict__ 
   for (int h = 0; h < GRP; h++)
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-      o[h][e] += __shfl_xor(o[h][e], 16);
-      o[h][e] += __shfl_xor(o[h][e], 32);
+      o[h][e] = rows4_sum(o[h][e]);
     }
   if (lane < 16) {
 #pragma unroll
@@ -895,8 +893,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const RowDesc *__restrict_
       sc[r] = kb + 4 * gq + r <= pq ? sa[r] * scale : -INFINITY;
       bm = fmaxf(bm, sc[r]);
     }
-    bm = fmaxf(bm, __shfl_xor(bm, 16));
-    bm = fmaxf(bm, __shfl_xor(bm, 32));
+    bm = rows4_max(bm);
     const float m_new = fmaxf(m_run, bm);
     const float ref = m_new == -INFINITY ? 0.f : m_new;
     const float alpha = m_run == -INFINITY ? 0.f : __expf(m_run - ref);
@@ -906,8 +903,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const RowDesc *__restrict_
       sc[r] = __expf(sc[r] - ref);
       ps += sc[r];
     }
-    ps += __shfl_xor(ps, 16);
-    ps += __shfl_xor(ps, 32);
+    ps = rows4_sum(ps);
     l_run = fmaf(l_run, alpha, ps);
     m_run = m_new;
 #pragma unroll

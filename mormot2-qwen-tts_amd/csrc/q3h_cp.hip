@@ -268,8 +268,7 @@ __global__ __launch_bounds__(NT) void k_attn_o_cp(const int8_t *__restrict__ wo,
   for (int j = 0; j < GRP; j++)
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-      o[j][e] += __shfl_xor(o[j][e], 16);
-      o[j][e] += __shfl_xor(o[j][e], 32);
+      o[j][e] = rows4_sum(o[j][e]);
     }
   if (lane < 16) {
 #pragma unroll

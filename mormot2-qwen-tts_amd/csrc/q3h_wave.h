@@ -81,6 +81,32 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// v summed over the wave's four 16-lane rows at one place in the row (lanes
+// l, l ^ 16, l ^ 32, l ^ 48), in every lane: (v_l + v_l^16) + (v_l^32 +
+// v_l^48), the pairs in the same order as two xor shuffles by 16 and 32 add
+// them (an add commutes exactly), through gfx950's row swaps
+// (v_permlane16_swap: odd rows of the first operand with even rows of the
+// second; v_permlane32_swap: the upper half of the first with the lower half
+// of the second) instead of LDS permutes
+__device__ __forceinline__ float rows4_sum(float v) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  v = __builtin_bit_cast(float, (unsigned)a[0]) + __builtin_bit_cast(float, (unsigned)a[1]);
+  const unsigned w = __builtin_bit_cast(unsigned, v);
+  const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  return __builtin_bit_cast(float, (unsigned)b[0]) + __builtin_bit_cast(float, (unsigned)b[1]);
+}
+
+// the maximum over the same four lanes, in every lane
+__device__ __forceinline__ float rows4_max(float v) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  v = fmaxf(__builtin_bit_cast(float, (unsigned)a[0]), __builtin_bit_cast(float, (unsigned)a[1]));
+  const unsigned w = __builtin_bit_cast(unsigned, v);
+  const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  return fmaxf(__builtin_bit_cast(float, (unsigned)b[0]), __builtin_bit_cast(float, (unsigned)b[1]));
+}
+
 // sum over aligned groups of 8 lanes (lanes 8k..8k+7), in every lane of the group
 __device__ __forceinline__ float group8_sum_dpp(float v) {
   v += dpp_f<kQuadXor1>(v);
