@@ -839,6 +839,7 @@ void drop_graphs(q3h_context *ctx) {
 void free_context(q3h_context *ctx) {
   drop_graphs(ctx);
   ctx->w.release();
+  if (ctx->pin) (void)hipHostFree(ctx->pin);
   dev_free(ctx->probe);
   dev_free(ctx->k);  // the values share this allocation
   dev_free(ctx->dev);
@@ -1100,6 +1101,25 @@ void forward_rows(q3h_context *c, Work &w, const float *x, int rows, int head, f
   const int head_rows = head >= 0 ? s->heads[head].N : 0;
   const int positions = forward_positions(c, rows);
   hipStream_t st = c->stream;
+  // the replayed single-row forward copies through pinned host memory (a
+  // pageable copy is staged by the runtime on every call)
+  float *pin_x = nullptr, *pin_lg = nullptr, *pin_n = nullptr;
+  if (graph) {
+    const size_t need = (size_t)2 * H + head_rows;
+    if (c->pin_floats < need) {
+      if (c->pin) check_hip(hipHostFree(c->pin), "hipHostFree");
+      c->pin = nullptr;
+      c->pin_floats = 0;
+      check_hip(hipHostMalloc((void **)&c->pin, sizeof(float) * need, hipHostMallocDefault),
+                "hipHostMalloc");
+      c->pin_floats = need;
+    }
+    pin_x = c->pin;
+    pin_n = c->pin + H;
+    pin_lg = c->pin + 2 * H;
+    std::memcpy(pin_x, x, sizeof(float) * H);
+    x = pin_x;
+  }
   check_hip(hipMemcpyAsync(w.h, x, sizeof(float) * rows * H, hipMemcpyHostToDevice, st),
             "upload x");
   LayerIO io;
@@ -1122,17 +1142,21 @@ void forward_rows(q3h_context *c, Work &w, const float *x, int rows, int head, f
     enqueue_forward(c, w, rows, positions, head, io, st);
   check_hip(hipGetLastError(), "forward kernels");
   if (normed_last)
-    check_hip(hipMemcpyAsync(normed_last, w.normed, sizeof(float) * H, hipMemcpyDeviceToHost,
-                             st),
+    check_hip(hipMemcpyAsync(graph ? pin_n : normed_last, w.normed, sizeof(float) * H,
+                             hipMemcpyDeviceToHost, st),
               "download state");
   if (logits && head >= 0)
-    check_hip(hipMemcpyAsync(logits, w.logits, sizeof(float) * head_rows, hipMemcpyDeviceToHost,
-                             st),
+    check_hip(hipMemcpyAsync(graph ? pin_lg : logits, w.logits, sizeof(float) * head_rows,
+                             hipMemcpyDeviceToHost, st),
               "download logits");
   if (layer_out)
     check_hip(hipMemcpyAsync(layer_out, c->probe, probe_bytes, hipMemcpyDeviceToHost, st),
               "download layer outputs");
   check_hip(hipStreamSynchronize(st), "forward sync");
+  if (graph) {
+    if (normed_last) std::memcpy(normed_last, pin_n, sizeof(float) * H);
+    if (logits && head >= 0) std::memcpy(logits, pin_lg, sizeof(float) * head_rows);
+  }
   c->len += rows;
 }
 

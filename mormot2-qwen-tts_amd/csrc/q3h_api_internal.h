@@ -206,6 +206,10 @@ struct q3h_context {
   // for the Work buffers of generation graphs_gen
   std::vector<std::pair<uint64_t, hipGraphExec_t>> graphs;
   unsigned graphs_gen = 0;
+  // pinned host staging of a single-row forward: the input row, the logits,
+  // the normed state (hipHostMalloc'ed on first use, pin_floats floats)
+  float *pin = nullptr;
+  size_t pin_floats = 0;
 };
 
 // the text projection (q3h_text.hip)
