@@ -147,8 +147,9 @@ int q3h_context_time_attention(q3h_context *c, int iters, float *us_per_launch,
    are in host memory. rows <= 0 does nothing (lm.pas:394-395). One row
    replays a HIP graph the context captures per (head, position cover)
    (covers of 64 positions up to 256, of 256 beyond; at most 32 graphs per
-   context, dropped when its work buffers grow); the results are those of
-   the same launches made directly (q3h_forward_embeds_noalloc). ---- */
+   context, dropped when its work buffers grow) and copies its row, logits
+   and state through a pinned host buffer of the context; the results are
+   those of the same launches made directly (q3h_forward_embeds_noalloc). ---- */
 int q3h_forward_embeds(q3h_context *c, const float *x, int rows, int head,
                        float *logits, float *normed_last);
 
