@@ -65,6 +65,7 @@ struct FrameDev {
 };
 
 constexpr int kArgBlock = 1024;
+constexpr int kArgUnroll = 4;  // argmax rounds whose loads are issued together (4096 codes)
 
 __device__ int block_argmax(float v, int i) {
   __shared__ float sv[kArgBlock / 64];
@@ -115,17 +116,18 @@ __global__ __launch_bounds__(kArgBlock) void k_choose_code0(FrameDev f) {
     const float *lg = f.logits + (size_t)s * f.vocab;
     const uint8_t *seen = f.seen + (size_t)s * f.vocab;
     const int nf = f.nframes[s];
-    // the scores of ChooseCode0's logits processors
-    auto score = [&](int i) {
-      float v = lg[i];
+    // the scores of ChooseCode0's logits processors, of logit v of code i
+    // (seen: code i already returned)
+    auto score_v = [&](float v, bool sn, int i) {
       // 2048..3071 forbidden but eos; eos forbidden before 2 frames
       if (i >= f.vocab - 1024 && i != f.eos) v = -INFINITY;
       if (i == f.eos && nf < 2) v = -INFINITY;
       // repetition penalty, once per code already returned (not when forbidden)
-      if (seen[i] && v != -INFINITY && f.penalty != 1.0f)
+      if (sn && v != -INFINITY && f.penalty != 1.0f)
         v = v > 0.f ? __fdiv_rn(v, f.penalty) : v * f.penalty;
       return v;
     };
+    auto score = [&](int i) { return score_v(lg[i], seen[i] != 0, i); };
     if constexpr (SAMPLE) {
       float x[3];
 #pragma unroll
@@ -135,10 +137,29 @@ __global__ __launch_bounds__(kArgBlock) void k_choose_code0(FrameDev f) {
       }
       code = block_sample<3>(x, f.vocab, f.sp0, draw_uniform(f.seeds[s], (uint64_t)nf, 0), sh);
     } else {
+      // every logit this thread scores, and logit 0, loaded before the first
+      // merge (kArgUnroll rounds unrolled, indices past the vocabulary
+      // clamped and not merged; a larger vocabulary continues in a loop)
+      float lv[kArgUnroll];
+      uint8_t sv[kArgUnroll];
+#pragma unroll
+      for (int k = 0; k < kArgUnroll; k++) {
+        const int i = min(tid + k * kArgBlock, f.vocab - 1);
+        lv[k] = lg[i];
+        sv[k] = seen[i];
+      }
+      const float l0 = lg[0];
+      const uint8_t s0 = seen[0];
       float bv = -INFINITY;
       int bi = 0x7fffffff;
-      for (int i = tid; i < f.vocab; i += kArgBlock) argmax_merge(bv, bi, score(i), i);
-      code = first_max_code(block_argmax(bv, bi), score(0));
+#pragma unroll
+      for (int k = 0; k < kArgUnroll; k++) {
+        const int i = tid + k * kArgBlock;
+        if (i < f.vocab) argmax_merge(bv, bi, score_v(lv[k], sv[k] != 0, i), i);
+      }
+      for (int i = tid + kArgUnroll * kArgBlock; i < f.vocab; i += kArgBlock)
+        argmax_merge(bv, bi, score(i), i);
+      code = first_max_code(block_argmax(bv, bi), score_v(l0, s0 != 0, 0));
     }
     int *codes = f.codes + (size_t)s * f.groups;
     if (code == f.eos) {
@@ -209,10 +230,19 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_argmax(const float *__restrict
   const int s = blockIdx.x, tid = threadIdx.x;
   if (!alive[s]) return;
   const float *lg = cp_logits + (size_t)s * cp_vocab;
+  // every logit this thread merges, and logit 0, loaded before the first merge
+  float lv[kArgUnroll];
+#pragma unroll
+  for (int k = 0; k < kArgUnroll; k++) lv[k] = lg[min(tid + k * kArgBlock, cp_vocab - 1)];
+  const float l0 = lg[0];
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int i = tid; i < cp_vocab; i += kArgBlock) argmax_merge(bv, bi, lg[i], i);
-  const int code = first_max_code(block_argmax(bv, bi), lg[0]);
+#pragma unroll
+  for (int k = 0; k < kArgUnroll; k++)
+    if (tid + k * kArgBlock < cp_vocab) argmax_merge(bv, bi, lv[k], tid + k * kArgBlock);
+  for (int i = tid + kArgUnroll * kArgBlock; i < cp_vocab; i += kArgBlock)
+    argmax_merge(bv, bi, lg[i], i);
+  const int code = first_max_code(block_argmax(bv, bi), l0);
   if (tid == 0) codes[(size_t)s * groups + g + 1] = code;
   if (g + 1 < groups - 1) {
     const float *emb = pred_emb + ((size_t)g * cp_vocab + code) * H;
@@ -279,10 +309,35 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
   if constexpr (SAMPLE) {
     code = cp_draw(logit, f.cp_vocab, f.sp, f.seeds[s], f.nframes[s] - 1, g, sh_cp);
   } else {
+    // every partial of the logits this thread merges, and of logit 0, loaded
+    // before the first sum (as in k_choose_code0)
+    float pl[kArgUnroll][4], p0[4];
+#pragma unroll
+    for (int k = 0; k < kArgUnroll; k++) {
+      const int i = min(tid + k * kArgBlock, f.cp_vocab - 1);
+#pragma unroll
+      for (int c = 0; c < 4; c++)
+        pl[k][c] = f.cp_part[((size_t)min(c, f.cp_hch - 1) * rows + row) * f.cp_vocab + i];
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+      p0[c] = f.cp_part[((size_t)min(c, f.cp_hch - 1) * rows + row) * f.cp_vocab];
+    auto chunk_sum = [&](const float(&p4)[4]) {
+      float v = 0.f;
+#pragma unroll
+      for (int c = 0; c < 4; c++) v = c < f.cp_hch ? __fadd_rn(v, p4[c]) : v;
+      return v;
+    };
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int i = tid; i < f.cp_vocab; i += kArgBlock) argmax_merge(bv, bi, logit(i), i);
-    code = first_max_code(block_argmax(bv, bi), logit(0));
+#pragma unroll
+    for (int k = 0; k < kArgUnroll; k++) {
+      const int i = tid + k * kArgBlock;
+      if (i < f.cp_vocab) argmax_merge(bv, bi, chunk_sum(pl[k]), i);
+    }
+    for (int i = tid + kArgUnroll * kArgBlock; i < f.cp_vocab; i += kArgBlock)
+      argmax_merge(bv, bi, logit(i), i);
+    code = first_max_code(block_argmax(bv, bi), chunk_sum(p0));
   }
   if (tid == 0) f.codes[(size_t)s * f.groups + g + 1] = code;
   if (next) {
