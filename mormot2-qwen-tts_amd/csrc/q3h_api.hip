@@ -352,7 +352,7 @@ void run_layers(const q3h_stack *s, Work &w, int M, int positions, bool fused, h
     } else if (attn_merge_o_supported(at, L.o, M, positions, kv16)) {
       // one decode row over a split context: the splits' merge in the o_proj
       // product (+ residual)
-      launch_attn(at, M, positions, fused, kv16, st, nullptr, false);
+      launch_attn(at, M, positions, fused, kv16, st, false);
       launch_attn_merge_o(at, L.o, w.h, positions, fused, kv16, st);
       linear(s, w, L.gu, w.h, H, M, L.post_norm, w.act, I, EPI_SWIGLU, nullptr, st);
       linear(s, w, L.down, w.act, I, M, nullptr, w.h, H, EPI_ADD, nullptr, st);
@@ -991,7 +991,7 @@ extern "C" int q3h_context_time_attention(q3h_context *c, int iters, float *us_p
       for (int l = 0; l < cf.layers; l++) {
         at.layer = l;
         at.qkn = s->layers[l].q_norm;
-        launch_attn(at, 1, positions, true, kv16, st, nullptr);
+        launch_attn(at, 1, positions, true, kv16, st);
       }
     };
     pass();  // warm-up

@@ -946,28 +946,18 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const RowDesc *__restrict_
   }
 }
 
-#define Q3H_LAUNCH(KERNEL, GRID, BLOCK, ST, EV0, EV1, ...)                                      \
-  do {                                                                                          \
-    if (EV0)                                                                                    \
-      hipExtLaunchKernelGGL(KERNEL, GRID, BLOCK, 0, ST, EV0, EV1, 0, __VA_ARGS__);              \
-    else                                                                                        \
-      hipLaunchKernelGGL(KERNEL, GRID, BLOCK, 0, ST, __VA_ARGS__);                              \
-  } while (0)
-
 template <typename KV, bool FUSED, int G>
-int launch_g(const AttnArgs &a, int M, int positions, hipStream_t st, const hipEvent_t *ev,
-             bool merge) {
-  const hipEvent_t ev0 = ev ? ev[0] : nullptr, ev1 = ev ? ev[1] : nullptr;
+int launch_g(const AttnArgs &a, int M, int positions, hipStream_t st, bool merge) {
   const SplitShape sh = attn_split_shape(positions, sizeof(KV) == 2, !merge);
   const int S = (positions + sh.len - 1) / sh.len;
 #define Q3H_S(NJ)                                                                             \
-  Q3H_LAUNCH((k_attn_split<KV, FUSED, G, 16 * NJ, 256>), dim3(a.kvh, S, M), dim3(256), st, ev0, \
-             ev1, a.rd, a.qkv, a.rope_cs, a.qkn, a.layer, a.kvh, S, a.part)
+  hipLaunchKernelGGL((k_attn_split<KV, FUSED, G, 16 * NJ, 256>), dim3(a.kvh, S, M), dim3(256), 0, \
+                     st, a.rd, a.qkv, a.rope_cs, a.qkn, a.layer, a.kvh, S, a.part)
   if (sh.len == kSplit && sh.threads == 0) {
     // 32 position groups: 2 positions per thread for every 64 covered
 #define Q3H_SH(NJ)                                                                          \
-  Q3H_LAUNCH((k_attn_short<KV, FUSED, G, 512, NJ>), dim3(a.heads, M), dim3(512), st, ev0, ev1, \
-             a.rd, a.qkv, a.rope_cs, a.qkn, a.out, a.layer, a.kvh)
+  hipLaunchKernelGGL((k_attn_short<KV, FUSED, G, 512, NJ>), dim3(a.heads, M), dim3(512), 0, st, \
+                     a.rd, a.qkv, a.rope_cs, a.qkn, a.out, a.layer, a.kvh)
     switch ((std::max(positions, 1) + 63) / 64) {
       case 1: Q3H_SH(2); break;
       case 2: Q3H_SH(4); break;
@@ -999,18 +989,17 @@ int launch_g(const AttnArgs &a, int M, int positions, hipStream_t st, const hipE
   }
 #undef Q3H_S
   if (sh.threads == 0 || !merge) return 1;
-  Q3H_LAUNCH((k_attn_merge<KV, FUSED, G>), dim3(a.heads, M), dim3(512), st, ev ? ev[2] : nullptr,
-             ev ? ev[3] : nullptr, a.rd, a.part, a.out, a.layer, a.kvh, S);
+  hipLaunchKernelGGL((k_attn_merge<KV, FUSED, G>), dim3(a.heads, M), dim3(512), 0, st, a.rd,
+                     a.part, a.out, a.layer, a.kvh, S);
   return 2;
 }
 
 template <typename KV, bool FUSED>
-int launch_kv(const AttnArgs &a, int M, int positions, hipStream_t st, const hipEvent_t *ev,
-              bool merge) {
+int launch_kv(const AttnArgs &a, int M, int positions, hipStream_t st, bool merge) {
   const int grp = a.heads / a.kvh;
-  if (grp == 1) return launch_g<KV, FUSED, 1>(a, M, positions, st, ev, merge);
-  if (grp == 2) return launch_g<KV, FUSED, 2>(a, M, positions, st, ev, merge);
-  return launch_g<KV, FUSED, 4>(a, M, positions, st, ev, merge);
+  if (grp == 1) return launch_g<KV, FUSED, 1>(a, M, positions, st, merge);
+  if (grp == 2) return launch_g<KV, FUSED, 2>(a, M, positions, st, merge);
+  return launch_g<KV, FUSED, 4>(a, M, positions, st, merge);
 }
 
 constexpr int kMergeORows = 1;  // weight rows per wave
@@ -1094,12 +1083,12 @@ int attn_splits_upto(int positions, bool kv16) {
 int attn_max_positions(bool kv16) { return kMaxSplitsLong * 16 * (kv16 ? 16 : 8); }
 
 int launch_attn(const AttnArgs &a, int M, int positions, bool fused, bool kv16, hipStream_t st,
-                const hipEvent_t *ev, bool merge) {
+                bool merge) {
   if (kv16)
-    return fused ? launch_kv<_Float16, true>(a, M, positions, st, ev, merge)
-                 : launch_kv<_Float16, false>(a, M, positions, st, ev, merge);
-  return fused ? launch_kv<float, true>(a, M, positions, st, ev, merge)
-               : launch_kv<float, false>(a, M, positions, st, ev, merge);
+    return fused ? launch_kv<_Float16, true>(a, M, positions, st, merge)
+                 : launch_kv<_Float16, false>(a, M, positions, st, merge);
+  return fused ? launch_kv<float, true>(a, M, positions, st, merge)
+               : launch_kv<float, false>(a, M, positions, st, merge);
 }
 
 bool attn_merge_o_supported(const AttnArgs &a, const Mat &wo, int M, int positions, bool kv16) {

@@ -203,13 +203,11 @@ void launch_attn_prefill(const AttnArgs &a, int M, bool kv16, hipStream_t st);
 // the most positions the split kernel merges (splits per kv head are bounded)
 int attn_max_positions(bool kv16);
 // positions: the most positions any of the M rows attends to (its own
-// included). Returns the kernels launched (1, or 2 with the split merge); ev
-// (optional, measurement): 4 events, the start and end of each kernel's own
-// execution
+// included). Returns the kernels launched (1, or 2 with the split merge).
 // merge == false: the split kernel alone when the context is split (its
 // partials left for launch_attn_merge_o; the fold shape)
 int launch_attn(const AttnArgs &a, int M, int positions, bool fused, bool kv16, hipStream_t st,
-                const hipEvent_t *ev = nullptr, bool merge = true);
+                bool merge = true);
 // one decode row's o_proj (Q8_0 W_o [N][16 x 128]) with the split attention's
 // merge in its prologue: y [N] += W_o x, x merged from a.part (the split
 // kernel of launch_attn(..., merge = false) launched before); for contexts
