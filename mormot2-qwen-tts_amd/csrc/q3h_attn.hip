@@ -207,7 +207,9 @@ __global__ __launch_bounds__(NTS) void k_attn_short(const RowDesc *__restrict__ 
     sc[j] = pg + PG * j < n ? sc[j] * scale : -INFINITY;
     mx = fmaxf(mx, sc[j]);
   }
-  mx = wave_max_dpp(mx);
+  // the scores are alike across a 16-lane row (one position group): the
+  // wave's maximum and sum are those over its four rows
+  mx = rows4_max(mx);
   if (lane == 0) red[0][wave] = mx;
   __syncthreads();
   mx = red[0][0];
@@ -219,7 +221,7 @@ __global__ __launch_bounds__(NTS) void k_attn_short(const RowDesc *__restrict__ 
     sc[j] = __expf(sc[j] - mx);
     ls += sc[j];
   }
-  ls = wave_sum_dpp(r16 == 0 ? ls : 0.f);
+  ls = rows4_sum(ls);
   if (lane == 0) red[1][wave] = ls;
   float o[8];
 #pragma unroll
@@ -450,7 +452,7 @@ __global__ __launch_bounds__(NTL) void k_attn_split(const RowDesc *__restrict__ 
       sc[h][j] = position(j) < n ? sc[h][j] * scale : -INFINITY;
       v = fmaxf(v, sc[h][j]);
     }
-    v = wave_max_dpp(v);
+    v = rows4_max(v);  // alike across a 16-lane row: the four rows' maximum
     mw[h] = v;
     const float ref = v == -INFINITY ? 0.f : v;  // no position here: weights 0
     float ls = 0.f;
@@ -459,7 +461,7 @@ __global__ __launch_bounds__(NTL) void k_attn_split(const RowDesc *__restrict__ 
       sc[h][j] = __expf(sc[h][j] - ref);
       ls += sc[h][j];
     }
-    lw[h] = wave_sum_dpp(r16 == 0 ? ls : 0.f);
+    lw[h] = rows4_sum(ls);
   }
   // values
   float o[GRP][8];

@@ -243,7 +243,10 @@ __global__ __launch_bounds__(NT) void k_attn_o_cp(const int8_t *__restrict__ wo,
       s[j][i] = rg + 4 * i < pos ? s[j][i] * scale : -INFINITY;
       mx = fmaxf(mx, s[j][i]);
     }
-    mx = wave_max_dpp(mx);
+    // the scores are alike across a 16-lane row: the maximum and the sum over
+    // the wave are those over its four rows (the same values as the 64-lane
+    // reductions, the sum's pairs in the same grouping)
+    mx = rows4_max(mx);
     float ls = 0.f;
 #pragma unroll
     for (int i = 0; i < NJ; i++) {
@@ -251,7 +254,7 @@ __global__ __launch_bounds__(NT) void k_attn_o_cp(const int8_t *__restrict__ wo,
       ls += s[j][i];
     }
     sn[j] = __expf(sn[j] - mx);
-    den[j] = wave_sum_dpp(r16 == 0 ? ls : 0.f) + sn[j];
+    den[j] = rows4_sum(ls) + sn[j];
 #pragma unroll
     for (int e = 0; e < 8; e++) o[j][e] = 0.f;
   }
