@@ -54,7 +54,9 @@ void work_fields(const q3h_stack *s, size_t R, int splits, int head_rows, Work &
   each((void **)&w.normed, sizeof(float) * R * H);
   each((void **)&w.logits, sizeof(float) * R * (head_rows > 0 ? head_rows : 1));
   each((void **)&w.rd, sizeof(RowDesc) * R);
-  each((void **)&w.part, sizeof(float) * R * c.heads * splits * (c.head_dim + 2));
+  // attention partials; at least the code predictor's four o_proj partials
+  each((void **)&w.part,
+       sizeof(float) * std::max(R * c.heads * splits * (c.head_dim + 2), 4 * H));
   each((void **)&w.ctx_arr, sizeof(CtxDev *) * R);
   if (c.act_q8) {
     const int maxK = std::max(std::max((int)H, (int)NQ), (int)I);
@@ -391,9 +393,13 @@ void run_cp_fused(const q3h_stack *s, Work &w, const q3h_context *ctx, int pos, 
     else
       launch_gemv(qa, EPI_STORE, true, st);
     void *kl = static_cast<char *>(ctx->k) + l * per_layer * esz;
-    launch_attn_o_cp(L.o, w.qkv, kl, v_off, w.h, L.q_norm, rope_row, pos, kv16, st);
-    launch_gemv(make_gemv(L.gu, w.h, H, 1, L.post_norm, c.rms_eps, w.act, I), EPI_SWIGLU, true,
-                st);
+    // o_proj as four partials (one per kv-head pair), added with the residual
+    // in the gate/up product's prologue, which writes the new h
+    launch_attn_o_cp(L.o, w.qkv, kl, v_off, w.h, w.part, L.q_norm, rope_row, pos, kv16, st);
+    require(launch_gemv_q8_swiglu_parts(make_gemv(L.gu, w.part, H, 1, L.post_norm, c.rms_eps,
+                                                  w.act, I),
+                                        w.h, st),
+            Q3H_E_ARG, "code-predictor gate/up: shape not supported on the device");
     launch_gemv(make_gemv(L.down, w.act, I, 1, nullptr, 0.f, w.h, H), EPI_ADD, true, st);
   }
 }

@@ -1,26 +1,29 @@
-// q3h_cp.hip - the code predictor's single-row step, attention fused into the
-// output projection.
+// q3h_cp.hip - the code predictor's attention fused into the output
+// projection.
 //
 // A code-predictor context holds at most 16 positions (one frame's codes), so
 // its attention is cheap enough to be recomputed by every workgroup of the
-// o_proj product. One launch does, for the new row at position pos of one
-// context:
-//   QK-norm + RoPE of the 16 query heads and 8 keys (rows of the raw q/k/v
-//   product), the K/V append at pos (workgroup 0 writes it; every workgroup
-//   uses its own copy for that position), causal softmax attention over
-//   positions 0..pos, then h[rows] += Wo[rows] . attention for the workgroup's
-//   16 rows of Wo (Q8_0).
-// That is one launch instead of two (attention, o_proj) and no attention
-// output round trip through memory; every workgroup computes the same
-// attention, so the result does not depend on scheduling.
+// o_proj product: one launch instead of two (attention, o_proj) and no
+// attention output round trip through memory.
+//
+// The single-row step (k_attn_pair_cp) splits the product over the four
+// kv-head pairs: workgroup b computes the causal attention of pair b % 4 only
+// (QK-norm + RoPE of its 4 query heads and 2 keys, rows of the raw q/k/v
+// product; the K/V append at pos by the pair's first workgroup) and the
+// partial product of 16 Wo rows over the pair's 512 columns. The four
+// partials go to part [4][1024] (h added to the first); the gate/up product
+// that follows adds them in a fixed order, so the result does not depend on
+// scheduling.
+//
+// The first step of a context (k_attn2_o_cp, positions 0 and 1 in one launch)
+// keeps every kv head in each workgroup and adds its o_proj to h directly.
 //
 // Shape (the Qwen3-TTS code predictor): hidden 1024, 16 query heads and 8 kv
-// heads of 128, 16 positions. 128 workgroups of 8 waves; wave w serves kv
-// head w for the attention, then one row of Wo.
+// heads of 128, 16 positions.
 //
 // Layouts: K/V cache of the layer [8][16][128] (kl), values at kl + v_off;
-// q_norm, k_norm, then the RMSNorm epsilon (qkn); the RoPE (cos, sin) row of pos (rope); Wo quants
-// [1024][2048] followed by their fp16 scales [1024][64].
+// q_norm, k_norm, then the RMSNorm epsilon (qkn); the RoPE (cos, sin) row of
+// pos (rope); Wo quants [1024][2048] followed by their fp16 scales [1024][64].
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -84,222 +87,226 @@ __device__ __forceinline__ void cvt8(const u32x4 (&r)[2], float (&o)[8]) {
     for (int e = 0; e < 4; e++) o[4 * i + e] = __uint_as_float(r[i][e]);
 }
 
+// The single-row step split over the four kv-head pairs, so that a workgroup
+// computes the attention of one pair (4 query heads) instead of all 8 kv
+// heads: workgroup b serves pair p = b % 4 (Wo columns 512 p .. 512 p + 511)
+// and Wo rows 16 (b / 4) .. + 15; 256 workgroups of 4 waves, wave j = query
+// head 4 p + j (kv head 2 p + j / 2). It writes the partial product
+// part[p][row] = Wo[row][pair columns] . attention of the pair, with h[row]
+// added in pair 0; the next product (RMSNorm + gate/up) adds the four
+// partials in a fixed order, so the result does not depend on scheduling.
+// Per wave: QK-norm + RoPE of its query head and of its kv head's new key, the
+// K/V append at pos (the first workgroup of each pair, waves 0 and 2), the
+// causal softmax over 0 .. pos as in k_attn_o_cp for one query head, then 4
+// Wo rows of the pair's columns (two rows per 16-byte load, 32 lanes each).
+constexpr int PAIRS = KVH / 2, PCOLS = NQ / PAIRS;  // 512 columns of Wo per pair
+constexpr int PROWS = 16;                            // Wo rows per workgroup
+constexpr int PNT = 256;                             // 4 waves
+
+// Two values summed over the wave's four 16-lane rows in two stages, each
+// stage one row swap and one add for two registers (rows4_sum's pairs):
+// swap16_add(x, y) holds x's rows 0 + 1 in row 0, y's rows 0 + 1 in row 1,
+// x's rows 2 + 3 in row 2 and y's in row 3; swap32_add(x, y) holds x's rows
+// 0 + 2 and 1 + 3 in rows 0 and 1, y's in rows 2 and 3
+__device__ __forceinline__ float swap16_add(float x, float y) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, x),
+                                                  __builtin_bit_cast(unsigned, y), false, false);
+  return __builtin_bit_cast(float, (unsigned)a[0]) + __builtin_bit_cast(float, (unsigned)a[1]);
+}
+__device__ __forceinline__ float swap32_add(float x, float y) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x),
+                                                  __builtin_bit_cast(unsigned, y), false, false);
+  return __builtin_bit_cast(float, (unsigned)a[0]) + __builtin_bit_cast(float, (unsigned)a[1]);
+}
+
 // NJ: cached positions per lane (4 NJ >= pos; slots past pos weigh exactly 0,
 // so any such NJ gives the same sums)
 template <typename KV, int NJ>
-__global__ __launch_bounds__(NT) void k_attn_o_cp(const int8_t *__restrict__ wo,
-                                                  const float *__restrict__ qkv,
-                                                  KV *__restrict__ kl, float *__restrict__ h,
-                                                  const float *__restrict__ qkn,
-                                                  const float2 *__restrict__ rope, int pos,
-                                                  int v_off) {
-  constexpr int LW = sizeof(KV) / 2;  // 16-byte loads per 8 elements
+__global__ __launch_bounds__(PNT) void k_attn_pair_cp(const int8_t *__restrict__ wo,
+                                                      const float *__restrict__ qkv,
+                                                      KV *__restrict__ kl,
+                                                      const float *__restrict__ qkn,
+                                                      const float2 *__restrict__ rope, int pos,
+                                                      int v_off, const float *__restrict__ h,
+                                                      float *__restrict__ part) {
+  constexpr int LW = sizeof(KV) / 2;
   static_assert(NJ >= 1 && 4 * NJ <= P, "positions per lane");
-  __shared__ float att[NQ];
-  __shared__ float qs[KVH][GRP][HD];
-  __shared__ float kvs[KVH][2][HD];  // the new key and value of each kv head
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __shared__ float att[4 * HD];         // the pair's 4 query heads
+  __shared__ float qs[4][HD];
+  __shared__ float kvs[4][2][HD];       // each wave's copy of its kv head's new key, value
+  const int lane = threadIdx.x & 63, j = threadIdx.x >> 6;
   const int r16 = lane & 15, rg = lane >> 4;
-  const int row = blockIdx.x * ROWS + w;  // this wave's o_proj row
+  const int pair = blockIdx.x % PAIRS;
+  const int kh = 2 * pair + (j >> 1), qh = 4 * pair + j;
   const _Float16 *wd = reinterpret_cast<const _Float16 *>(wo + (size_t)HID * NQ);
 
   // 1. every load up front, in the order of use (a wave's loads complete in
-  // issue order): the raw q/k/v of kv head w, the norm weights, the RoPE row,
-  // the cached keys, the cached values, then the Wo row and the residual
-  float xq[GRP][2], xk[2], xv[2];
-#pragma unroll
-  for (int j = 0; j < GRP; j++) {
-    xq[j][0] = qkv[(w * GRP + j) * HD + lane];
-    xq[j][1] = qkv[(w * GRP + j) * HD + lane + 64];
-  }
-  xk[0] = qkv[NQ + w * HD + lane];
-  xk[1] = qkv[NQ + w * HD + lane + 64];
-  xv[0] = qkv[NQ + KVH * HD + w * HD + lane];
-  xv[1] = qkv[NQ + KVH * HD + w * HD + lane + 64];
+  // issue order): the raw q/k/v, the norm weights, the RoPE row, the cached
+  // keys, the cached values, then the Wo rows and the residual
+  const float xq0 = qkv[qh * HD + lane], xq1 = qkv[qh * HD + lane + 64];
+  const float xk0 = qkv[NQ + kh * HD + lane], xk1 = qkv[NQ + kh * HD + lane + 64];
+  const float xv0 = qkv[NQ + KVH * HD + kh * HD + lane];
+  const float xv1 = qkv[NQ + KVH * HD + kh * HD + lane + 64];
   const float qn0 = qkn[lane], qn1 = qkn[lane + 64];
   const float kn0 = qkn[HD + lane], kn1 = qkn[HD + lane + 64];
   const float eps = qkn[2 * HD];
   const float2 cs = rope[lane];
-  KV *kh = kl + (size_t)w * P * HD;
-  KV *vh = kl + v_off + (size_t)w * P * HD;
+  KV *kh_p = kl + (size_t)kh * P * HD;
+  KV *vh_p = kl + v_off + (size_t)kh * P * HD;
   // cached keys and values of positions 0 .. pos - 1: lane holds dims
-  // 8 (lane % 16) .. + 7 of positions lane / 16 + 4 j, so each load
+  // 8 (lane % 16) .. + 7 of positions lane / 16 + 4 i, so each load
   // instruction reads 4 whole rows; positions at or past pos are read at
   // pos - 1 (a context's cache starts as zeros: finite) and weighted 0
   const int last = max(pos - 1, 0);
   u32x4 kr[NJ][LW], vr[NJ][LW];
 #pragma unroll
-  for (int j = 0; j < NJ; j++) {
-    const size_t off = (size_t)min(rg + 4 * j, last) * HD + 8 * r16;
+  for (int i = 0; i < NJ; i++) {
+    const size_t off = (size_t)min(rg + 4 * i, last) * HD + 8 * r16;
 #pragma unroll
-    for (int e = 0; e < LW; e++) kr[j][e] = *reinterpret_cast<const u32x4 *>(kh + off + 4 * e);
+    for (int e = 0; e < LW; e++) kr[i][e] = *reinterpret_cast<const u32x4 *>(kh_p + off + 4 * e);
   }
 #pragma unroll
-  for (int j = 0; j < NJ; j++) {
-    const size_t off = (size_t)min(rg + 4 * j, last) * HD + 8 * r16;
+  for (int i = 0; i < NJ; i++) {
+    const size_t off = (size_t)min(rg + 4 * i, last) * HD + 8 * r16;
 #pragma unroll
-    for (int e = 0; e < LW; e++) vr[j][e] = *reinterpret_cast<const u32x4 *>(vh + off + 4 * e);
+    for (int e = 0; e < LW; e++) vr[i][e] = *reinterpret_cast<const u32x4 *>(vh_p + off + 4 * e);
   }
   __builtin_amdgcn_sched_barrier(0);
+  // Wo rows rb + 2 i + lane / 32 (i = 0, 1), columns 16 (lane % 32) .. + 15 of the pair
+  const int rb = (blockIdx.x / PAIRS) * PROWS + 4 * j;
   int4 wv[2];
-  float sc[2];
+  float sc[2], hr[2];
 #pragma unroll
-  for (int c = 0; c < 2; c++) {
-    wv[c] = *reinterpret_cast<const int4 *>(wo + (size_t)row * NQ + c * 1024 + lane * 16);
-    sc[c] = (float)wd[(size_t)row * NBO + c * 32 + (lane >> 1)];
+  for (int i = 0; i < 2; i++) {
+    const int row = rb + 2 * i + (lane >> 5);
+    wv[i] = *reinterpret_cast<const int4 *>(wo + (size_t)row * NQ + pair * PCOLS +
+                                            (lane & 31) * 16);
+    sc[i] = (float)wd[(size_t)row * NBO + pair * (PCOLS / 32) + ((lane & 31) >> 1)];
+    hr[i] = h[row];
   }
-  const float hr = h[row];
   __builtin_amdgcn_sched_barrier(0);
 
   // 2. QK-norm + RoPE; the new key and value rounded as the cache holds them
-#pragma unroll
-  for (int j = 0; j < GRP; j++) {
-    float x0 = xq[j][0], x1 = xq[j][1];
+  {
+    float x0 = xq0, x1 = xq1;
     norm_rope(x0, x1, qn0, qn1, cs, eps);
-    qs[w][j][lane] = x0;
-    qs[w][j][lane + 64] = x1;
+    qs[j][lane] = x0;
+    qs[j][lane + 64] = x1;
   }
   {
-    float x0 = xk[0], x1 = xk[1];
+    float x0 = xk0, x1 = xk1;
     norm_rope(x0, x1, kn0, kn1, cs, eps);
-    const KV k0 = (KV)x0, k1 = (KV)x1, v0 = (KV)xv[0], v1 = (KV)xv[1];
-    kvs[w][0][lane] = (float)k0;
-    kvs[w][0][lane + 64] = (float)k1;
-    kvs[w][1][lane] = (float)v0;
-    kvs[w][1][lane + 64] = (float)v1;
-    if (blockIdx.x == 0) {
-      kh[(size_t)pos * HD + lane] = k0;
-      kh[(size_t)pos * HD + lane + 64] = k1;
-      vh[(size_t)pos * HD + lane] = v0;
-      vh[(size_t)pos * HD + lane + 64] = v1;
+    const KV k0 = (KV)x0, k1 = (KV)x1, v0 = (KV)xv0, v1 = (KV)xv1;
+    kvs[j][0][lane] = (float)k0;
+    kvs[j][0][lane + 64] = (float)k1;
+    kvs[j][1][lane] = (float)v0;
+    kvs[j][1][lane + 64] = (float)v1;
+    if (blockIdx.x < PAIRS && (j & 1) == 0) {
+      kh_p[(size_t)pos * HD + lane] = k0;
+      kh_p[(size_t)pos * HD + lane + 64] = k1;
+      vh_p[(size_t)pos * HD + lane] = v0;
+      vh_p[(size_t)pos * HD + lane + 64] = v1;
     }
   }
   wave_lds_sync();
 
-  // 3. scores: an 8-term chain per lane summed over its 16-lane row; the
-  // new position's score from the prologue's key
+  // 3. scores: an 8-term chain per lane summed over its 16-lane row
   const float scale = (float)(1.0 / sqrt((double)HD));
-  float q[GRP][8], s[GRP][NJ], sn[GRP];
+  float q[8], s[NJ], sn;
 #pragma unroll
-  for (int j = 0; j < GRP; j++)
-#pragma unroll
-    for (int e = 0; e < 8; e++) q[j][e] = qs[w][j][8 * r16 + e];
+  for (int e = 0; e < 8; e++) q[e] = qs[j][8 * r16 + e];
 #pragma unroll
   for (int i = 0; i < NJ; i++) {
     float k8[8];
     cvt8(kr[i], k8);
-#pragma unroll
-    for (int j = 0; j < GRP; j++) {
-      float a = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; e++) a = fmaf(q[j][e], k8[e], a);
-      s[j][i] = a;
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < GRP; j++) {
     float a = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; e++) a = fmaf(q[j][e], kvs[w][0][8 * r16 + e], a);
-    sn[j] = a;
+    for (int e = 0; e < 8; e++) a = fmaf(q[e], k8[e], a);
+    s[i] = a;
+  }
+  {
+    float a = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) a = fmaf(q[e], kvs[j][0][8 * r16 + e], a);
+    sn = a;
   }
 #pragma unroll
-  for (int j = 0; j < GRP; j++) {
+  for (int i = 0; i < NJ; i++) s[i] += dpp_f<kQuadXor1>(s[i]);
+  sn += dpp_f<kQuadXor1>(sn);
 #pragma unroll
-    for (int i = 0; i < NJ; i++) s[j][i] += dpp_f<kQuadXor1>(s[j][i]);
-    sn[j] += dpp_f<kQuadXor1>(sn[j]);
-  }
+  for (int i = 0; i < NJ; i++) s[i] += dpp_f<kQuadXor2>(s[i]);
+  sn += dpp_f<kQuadXor2>(sn);
 #pragma unroll
-  for (int j = 0; j < GRP; j++) {
+  for (int i = 0; i < NJ; i++) s[i] += dpp_f<kHalfMirror>(s[i]);
+  sn += dpp_f<kHalfMirror>(sn);
 #pragma unroll
-    for (int i = 0; i < NJ; i++) s[j][i] += dpp_f<kQuadXor2>(s[j][i]);
-    sn[j] += dpp_f<kQuadXor2>(sn[j]);
-  }
-#pragma unroll
-  for (int j = 0; j < GRP; j++) {
-#pragma unroll
-    for (int i = 0; i < NJ; i++) s[j][i] += dpp_f<kHalfMirror>(s[j][i]);
-    sn[j] += dpp_f<kHalfMirror>(sn[j]);
-  }
-#pragma unroll
-  for (int j = 0; j < GRP; j++) {
-#pragma unroll
-    for (int i = 0; i < NJ; i++) s[j][i] += dpp_f<kRowMirror>(s[j][i]);
-    sn[j] += dpp_f<kRowMirror>(sn[j]);
-  }
+  for (int i = 0; i < NJ; i++) s[i] += dpp_f<kRowMirror>(s[i]);
+  sn += dpp_f<kRowMirror>(sn);
 
-  // 4. softmax over 0 .. pos and the outputs: lane holds 8 dims of its
-  // positions, the 4 row groups summed by lane shuffles
-  const float4 vn0 = *reinterpret_cast<const float4 *>(&kvs[w][1][8 * r16]);
-  const float4 vn1 = *reinterpret_cast<const float4 *>(&kvs[w][1][8 * r16 + 4]);
-  const float vn[8] = {vn0.x, vn0.y, vn0.z, vn0.w, vn1.x, vn1.y, vn1.z, vn1.w};
-  float o[GRP][8], den[GRP];
+  // 4. softmax over 0 .. pos; the outputs summed over the four rows and
+  // scattered: after the two swap stages lane (rg, r16) holds dims
+  // 8 r16 + rg and 8 r16 + 4 + rg
+  sn *= scale;
+  float mx = sn;
 #pragma unroll
-  for (int j = 0; j < GRP; j++) {
-    sn[j] *= scale;
-    float mx = sn[j];
-#pragma unroll
-    for (int i = 0; i < NJ; i++) {
-      s[j][i] = rg + 4 * i < pos ? s[j][i] * scale : -INFINITY;
-      mx = fmaxf(mx, s[j][i]);
-    }
-    // the scores are alike across a 16-lane row: the maximum and the sum over
-    // the wave are those over its four rows (the same values as the 64-lane
-    // reductions, the sum's pairs in the same grouping)
-    mx = rows4_max(mx);
-    float ls = 0.f;
-#pragma unroll
-    for (int i = 0; i < NJ; i++) {
-      s[j][i] = __expf(s[j][i] - mx);
-      ls += s[j][i];
-    }
-    sn[j] = __expf(sn[j] - mx);
-    den[j] = rows4_sum(ls) + sn[j];
-#pragma unroll
-    for (int e = 0; e < 8; e++) o[j][e] = 0.f;
+  for (int i = 0; i < NJ; i++) {
+    s[i] = rg + 4 * i < pos ? s[i] * scale : -INFINITY;
+    mx = fmaxf(mx, s[i]);
   }
+  mx = rows4_max(mx);
+  float ls = 0.f;
+#pragma unroll
+  for (int i = 0; i < NJ; i++) {
+    s[i] = __expf(s[i] - mx);
+    ls += s[i];
+  }
+  sn = __expf(sn - mx);
+  const float den = rows4_sum(ls) + sn;
+  float o[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) o[e] = 0.f;
 #pragma unroll
   for (int i = 0; i < NJ; i++) {
     float v8[8];
     cvt8(vr[i], v8);
 #pragma unroll
-    for (int j = 0; j < GRP; j++)
-#pragma unroll
-      for (int e = 0; e < 8; e++) o[j][e] = fmaf(s[j][i], v8[e], o[j][e]);
+    for (int e = 0; e < 8; e++) o[e] = fmaf(s[i], v8[e], o[e]);
   }
-#pragma unroll
-  for (int j = 0; j < GRP; j++)
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-      o[j][e] = rows4_sum(o[j][e]);
-    }
-  if (lane < 16) {
-#pragma unroll
-    for (int j = 0; j < GRP; j++) {
-      const float inv = 1.0f / den[j];
-      float r[8];
-#pragma unroll
-      for (int e = 0; e < 8; e++) r[e] = fmaf(sn[j], vn[e], o[j][e]) * inv;
-      float4 *dst = reinterpret_cast<float4 *>(&att[(w * GRP + j) * HD + 8 * r16]);
-      dst[0] = make_float4(r[0], r[1], r[2], r[3]);
-      dst[1] = make_float4(r[4], r[5], r[6], r[7]);
-    }
+  const float lo = swap32_add(swap16_add(o[0], o[1]), swap16_add(o[2], o[3]));
+  const float hi = swap32_add(swap16_add(o[4], o[5]), swap16_add(o[6], o[7]));
+  {
+    const float inv = 1.0f / den;
+    const int d = 8 * r16 + rg;
+    att[j * HD + d] = fmaf(sn, kvs[j][1][d], lo) * inv;
+    att[j * HD + d + 4] = fmaf(sn, kvs[j][1][d + 4], hi) * inv;
   }
   __syncthreads();
 
-  // 5. h[row] += Wo[row] . att
-  float acc = 0.f;
+  // 5. part[pair][row] = Wo[row][pair columns] . att (+ h[row] in pair 0)
+  float acc[2];
+  const float4 *xp = reinterpret_cast<const float4 *>(att + (lane & 31) * 16);
 #pragma unroll
-  for (int c = 0; c < 2; c++) {
-    const float4 *xp = reinterpret_cast<const float4 *>(att + c * 1024 + lane * 16);
-    float p0 = dot4(wv[c].x, xp[0], 0.f);
-    float p1 = dot4(wv[c].y, xp[1], 0.f);
-    p0 = dot4(wv[c].z, xp[2], p0);
-    p1 = dot4(wv[c].w, xp[3], p1);
-    acc = fmaf(sc[c], p0 + p1, acc);
+  for (int i = 0; i < 2; i++) {
+    float p0 = dot4(wv[i].x, xp[0], 0.f);
+    float p1 = dot4(wv[i].y, xp[1], 0.f);
+    p0 = dot4(wv[i].z, xp[2], p0);
+    p1 = dot4(wv[i].w, xp[3], p1);
+    acc[i] = sc[i] * (p0 + p1);
   }
-  acc = wave_sum_dpp(acc);
-  if (lane == 0) h[row] = hr + acc;
+#pragma unroll
+  for (int i = 0; i < 2; i++) acc[i] += dpp_f<kQuadXor1>(acc[i]);
+#pragma unroll
+  for (int i = 0; i < 2; i++) acc[i] += dpp_f<kQuadXor2>(acc[i]);
+#pragma unroll
+  for (int i = 0; i < 2; i++) acc[i] += dpp_f<kHalfMirror>(acc[i]);
+#pragma unroll
+  for (int i = 0; i < 2; i++) acc[i] += dpp_f<kRowMirror>(acc[i]);
+  // rows 0 / 2: row i = 0 of lanes 0-31 / 32-63; rows 1 / 3: row i = 1
+  const float tot = swap16_add(acc[0], acc[1]);
+  if (r16 == 0) {
+    const int i = rg & 1, row = rb + 2 * i + (rg >> 1);
+    part[pair * HID + row] = pair == 0 ? hr[i] + tot : tot;
+  }
 }
 
 // The first step of a code-predictor context: its two rows (positions 0 and
@@ -414,20 +421,20 @@ __global__ __launch_bounds__(NT) void k_attn2_o_cp(const int8_t *__restrict__ wo
 
 bool cp_fused_supported(const q3h_stack_config &c) {
   return c.dtype == Q3H_Q8_0 && !c.act_q8 && c.hidden == HID && c.heads == KVH * GRP && c.kv_heads == KVH &&
-         c.head_dim == HD;
+         c.head_dim == HD && gemv_q8_parts_supported(2 * c.intermediate, c.hidden);
 }
 
-void launch_attn_o_cp(const Mat &wo, const float *qkv, void *k_layer, int v_off, float *h,
-                      const float *qkn, const float *rope_row, int pos, bool kv16,
+void launch_attn_o_cp(const Mat &wo, const float *qkv, void *k_layer, int v_off, const float *h,
+                      float *part, const float *qkn, const float *rope_row, int pos, bool kv16,
                       hipStream_t st) {
-  const dim3 grid(HID / ROWS), block(NT);
+  const dim3 grid(PAIRS * (HID / PROWS)), block(PNT);
   const float2 *rope = reinterpret_cast<const float2 *>(rope_row);
   // the cached positions 0 .. pos - 1 in 4 NJ lane slots (pos is fixed per
   // code-predictor step, so each step's launch reads only what it attends to)
   const int nj = std::min(std::max((pos + 3) / 4, 1), P / 4);
 #define Q3H_AOC(KV, NJ)                                                                     \
-  hipLaunchKernelGGL((k_attn_o_cp<KV, NJ>), grid, block, 0, st, wo.q, qkv,                  \
-                     static_cast<KV *>(k_layer), h, qkn, rope, pos, v_off)
+  hipLaunchKernelGGL((k_attn_pair_cp<KV, NJ>), grid, block, 0, st, wo.q, qkv,               \
+                     static_cast<KV *>(k_layer), qkn, rope, pos, v_off, h, part)
 #define Q3H_AOC_NJ(KV) \
   switch (nj) {        \
     case 1: Q3H_AOC(KV, 1); break; \

@@ -61,13 +61,18 @@ __device__ __forceinline__ float dot4_i8(int w, float4 x, float acc) {
 // not at the end. Every row gets the same arithmetic in the same order as a
 // single row does, so a row's result does not depend on M. xn_out (the normed
 // row, by the first wave of workgroup 0) is taken with a single row only.
-template <int R, int C, int EPI, int LW, int MR>
+// NP = 4 (one row): x holds four partial rows K apart whose sum
+// (p0 + p1) + (p2 + p3) is the row; the loader waves of workgroup 0 write that
+// sum to x_out.
+template <int R, int C, int EPI, int LW, int MR, int NP = 0>
 __global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq,
                                                    const float *__restrict__ x,
                                                    const float *__restrict__ norm_w,
                                                    float *__restrict__ y, int N, int W, float eps,
                                                    int ldx, int ldy, int M,
-                                                   float *__restrict__ xn_out) {
+                                                   float *__restrict__ xn_out,
+                                                   float *__restrict__ x_out) {
+  static_assert(NP == 0 || (NP == 4 && MR == 1), "partial rows: one row of four parts");
   constexpr int K = C * 1024, NB = K / 32;
   constexpr int T = 64 * LW, J = C * 256 / T;  // loader threads, float4 per loader thread
   __shared__ float4 xs[MR][C * 256];           // w * x, slot (c*4 + i)*64 + l
@@ -79,13 +84,20 @@ __global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq
 
   // 1. the rows (and the norm weight) first, then every weight load
   const int t = tid % T;
-  float4 xv[MR][J], wn[J];
+  float4 xv[MR][J], wn[J], xp[NP > 0 ? NP : 1][J];
 #pragma unroll
   for (int m = 0; m < MR; m++) {
     const float4 *xm =
         reinterpret_cast<const float4 *>(MR == 1 ? x : x + (size_t)min(m, M - 1) * ldx);
+    if (NP > 0) {
 #pragma unroll
-    for (int j = 0; j < J; j++) xv[m][j] = xm[t + T * j];
+      for (int p = 0; p < NP; p++)
+#pragma unroll
+        for (int j = 0; j < J; j++) xp[p][j] = xm[p * (K / 4) + t + T * j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < J; j++) xv[m][j] = xm[t + T * j];
+    }
   }
   if (nrm) {
 #pragma unroll
@@ -114,6 +126,18 @@ __global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq
   }
   // every load above is issued before any arithmetic
   __builtin_amdgcn_sched_barrier(0);
+  if (NP > 0) {
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+      const float4 a = xp[0][j], b = xp[1 % NP][j], c = xp[2 % NP][j], d = xp[3 % NP][j];
+      xv[0][j] = make_float4((a.x + b.x) + (c.x + d.x), (a.y + b.y) + (c.y + d.y),
+                             (a.z + b.z) + (c.z + d.z), (a.w + b.w) + (c.w + d.w));
+    }
+    if (blockIdx.x == 0 && wave < LW) {
+#pragma unroll
+      for (int j = 0; j < J; j++) reinterpret_cast<float4 *>(x_out)[t + T * j] = xv[0][j];
+    }
+  }
 
   // 2. while the weights are in flight: the loader waves stage w * x in LDS
   // and sum the squares of x (fp32, per thread then per wave, then the LW
@@ -357,10 +381,11 @@ void launch_vl(const GemvArgs &a, int epi, int waves, hipStream_t st, hipEvent_t
   do {                                                                                           \
     if (ev0)                                                                                     \
       hipExtLaunchKernelGGL((k_gemv_q8v<R, C, E, LW, MR>), grid, block, 0, st, ev0, ev1, 0, a.wq, \
-                            a.x, a.norm_w, a.y, a.N, waves, a.eps, a.ldx, a.ldy, a.M, a.xn_out); \
+                            a.x, a.norm_w, a.y, a.N, waves, a.eps, a.ldx, a.ldy, a.M, a.xn_out, \
+                            nullptr);                                                            \
     else                                                                                         \
       hipLaunchKernelGGL((k_gemv_q8v<R, C, E, LW, MR>), grid, block, 0, st, a.wq, a.x, a.norm_w, \
-                         a.y, a.N, waves, a.eps, a.ldx, a.ldy, a.M, a.xn_out);                   \
+                         a.y, a.N, waves, a.eps, a.ldx, a.ldy, a.M, a.xn_out, nullptr);          \
   } while (0)
   if (epi == EPI_STORE)
     Q3H_V(EPI_STORE);
@@ -437,6 +462,43 @@ bool launch_gemv_q8_code(const GemvArgs &a, const float *logits, int vocab, cons
   return true;
 }
 
+// gate/up (SwiGLU) shapes: R1 rows per wave, W waves per workgroup, 256 workgroups
+static bool swiglu_shape(int N, int &R1, int &W) {
+  if (N % 256 != 0) return false;
+  const int rpb = N / 256;
+  R1 = rpb % 4 == 0 ? 4 : 2;
+  W = rpb / R1;
+  return R1 * W == rpb && W >= 1 && W <= kMaxWaves;
+}
+
+// four waves, all of them loaders of the partial rows, of N / 1024 rows each
+// (256 workgroups): at N = 6144 6-row waves took 1.470 ms per frame against
+// 1.485 for the plain products' 6 waves of 4 rows, whose two extra waves
+// repeat the loaders' 16 KB of partials
+bool gemv_q8_parts_supported(int N, int K) {
+  const int R1 = N / 1024;
+  return K == 1024 && N % 1024 == 0 && (R1 == 2 || R1 == 4 || R1 == 6);
+}
+
+bool launch_gemv_q8_swiglu_parts(const GemvArgs &a, float *x_out, hipStream_t st) {
+  if (reinterpret_cast<const int8_t *>(a.wd) != a.wq + (size_t)a.N * a.K) return false;
+  if (a.M != 1 || a.norm_w == nullptr || a.xn_out != nullptr || x_out == nullptr) return false;
+  if (!gemv_q8_parts_supported(a.N, a.K)) return false;
+  const int R1 = a.N / 1024, W = 4;
+  const dim3 grid(256), block(64 * W);
+#define Q3H_P(RR)                                                                                 \
+  hipLaunchKernelGGL((k_gemv_q8v<RR, 1, EPI_SWIGLU, 4, 1, 4>), grid, block, 0, st, a.wq, a.x,     \
+                     a.norm_w, a.y, a.N, W, a.eps, a.ldx, a.ldy, a.M, nullptr, x_out)
+  if (R1 == 6)
+    Q3H_P(6);
+  else if (R1 == 4)
+    Q3H_P(4);
+  else
+    Q3H_P(2);
+#undef Q3H_P
+  return true;
+}
+
 bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st, hipEvent_t ev0,
                          hipEvent_t ev1) {
   // the kernels find the scales right after the quants
@@ -451,10 +513,7 @@ bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st, hipEvent_t 
   // pairs (SwiGLU) as 4-row waves (6 per workgroup: 3.47 us per launch against
   // 3.78 for 2-row waves at one row, 4.45 against 4.54 at two)
   int R1 = rpb / 4, W = 4;
-  if (epi == EPI_SWIGLU) {
-    R1 = rpb % 4 == 0 ? 4 : 2;
-    W = rpb / R1;
-  }
+  if (epi == EPI_SWIGLU && !swiglu_shape(a.N, R1, W)) return false;
   if (R1 < 1 || R1 * W != rpb || W > kMaxWaves) return false;
   if (a.M == 1) return launch_rows<1>(a, epi, R1, W, st, ev0, ev1);
   if (W < 4) return false;  // more rows: 4 loader waves

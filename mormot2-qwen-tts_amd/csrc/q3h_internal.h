@@ -83,6 +83,12 @@ void launch_gemv(const GemvArgs &a, int epi, bool q8, hipStream_t st);
 // false when the shape is not one it takes (nothing launched)
 bool launch_gemv_q8_wide(const GemvArgs &a, int epi, hipStream_t st, hipEvent_t ev0 = nullptr,
                          hipEvent_t ev1 = nullptr);
+// the RMSNorm + gate/up + SwiGLU product of one row given as four partial
+// rows [4][K] at a.x (the code predictor's o_proj partials per kv-head pair),
+// added as (p0 + p1) + (p2 + p3); workgroup 0 writes the row to x_out. False
+// when the shape is not one of these kernels' (gemv_q8_parts_supported).
+bool gemv_q8_parts_supported(int N, int K);
+bool launch_gemv_q8_swiglu_parts(const GemvArgs &a, float *x_out, hipStream_t st);
 // the single-row product with an RMSNorm prologue (M == 1, K == 1024, N a
 // multiple of 1024 up to 4096) over row `code` of rows [vocab][K], code = the
 // argmax of logits [vocab] (vocab 2048 or 3072; the smallest index among
@@ -232,12 +238,14 @@ bool attn_x_supported(int heads, int kvh, int head_dim, int max_positions);
 void launch_attn_x(const AttnArgs &a, int M, bool fused, bool kv16, int qkv_chunks,
                    const QAct &xa, int max_positions, hipStream_t st);
 
-// the code predictor's fused attention + o_proj + residual (q3h_cp.hip):
-// one context of 16 positions, the new row at pos; k_layer: the layer's keys,
-// values at k_layer + v_off elements; qkn: [q_norm | k_norm | eps]; rope_row:
-// the (cos, sin) row of pos
-void launch_attn_o_cp(const Mat &wo, const float *qkv, void *k_layer, int v_off, float *h,
-                      const float *qkn, const float *rope_row, int pos, bool kv16,
+// the code predictor's fused attention + o_proj (q3h_cp.hip): one context
+// of 16 positions, the new row at pos; k_layer: the layer's keys, values at
+// k_layer + v_off elements; qkn: [q_norm | k_norm | eps]; rope_row: the
+// (cos, sin) row of pos. Writes part [4][1024]: the o_proj partial of each
+// kv-head pair, h added to the first (their sum, in the order
+// launch_gemv_q8_swiglu_parts takes, is h + o_proj)
+void launch_attn_o_cp(const Mat &wo, const float *qkv, void *k_layer, int v_off, const float *h,
+                      float *part, const float *qkn, const float *rope_row, int pos, bool kv16,
                       hipStream_t st);
 
 // the same for the first step of a code-predictor context: its two rows at
