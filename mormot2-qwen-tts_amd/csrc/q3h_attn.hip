@@ -233,14 +233,12 @@ __global__ __launch_bounds__(NTS) void k_attn_short(const RowDesc *__restrict__ 
 #pragma unroll
     for (int e = 0; e < 8; e++) o[e] = fmaf(sc[j], v8[e], o[e]);
   }
-#pragma unroll
-  for (int e = 0; e < 8; e++) {
-    o[e] = rows4_sum(o[e]);
-  }
-  if (lane < 16) {
-    float4 *dst = reinterpret_cast<float4 *>(&po[wave][8 * r16]);
-    dst[0] = make_float4(o[0], o[1], o[2], o[3]);
-    dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+  // summed over the wave's four position groups, scattered over its lanes
+  {
+    float lo, hi;
+    rows4_scatter8(o, lo, hi);
+    po[wave][8 * r16 + (lane >> 4)] = lo;
+    po[wave][8 * r16 + 4 + (lane >> 4)] = hi;
   }
   __syncthreads();
   if (t < HD) {
@@ -481,18 +479,11 @@ __global__ __launch_bounds__(NTL) void k_attn_split(const RowDesc *__restrict__ 
   // the 4 position groups of a wave (lanes l, l + 16, l + 32, l + 48), then
   // the waves through LDS, each rescaled to the split's maximum
 #pragma unroll
-  for (int h = 0; h < GRP; h++)
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-      o[h][e] = rows4_sum(o[h][e]);
-    }
-  if (lane < 16) {
-#pragma unroll
-    for (int h = 0; h < GRP; h++) {
-      float4 *dst = reinterpret_cast<float4 *>(&po[wave][h][8 * r16]);
-      dst[0] = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
-      dst[1] = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
-    }
+  for (int h = 0; h < GRP; h++) {
+    float lo, hi;
+    rows4_scatter8(o[h], lo, hi);
+    po[wave][h][8 * r16 + (lane >> 4)] = lo;
+    po[wave][h][8 * r16 + 4 + (lane >> 4)] = hi;
   }
   if (lane == 0) {
 #pragma unroll

@@ -103,22 +103,6 @@ constexpr int PAIRS = KVH / 2, PCOLS = NQ / PAIRS;  // 512 columns of Wo per pai
 constexpr int PROWS = 16;                            // Wo rows per workgroup
 constexpr int PNT = 256;                             // 4 waves
 
-// Two values summed over the wave's four 16-lane rows in two stages, each
-// stage one row swap and one add for two registers (rows4_sum's pairs):
-// swap16_add(x, y) holds x's rows 0 + 1 in row 0, y's rows 0 + 1 in row 1,
-// x's rows 2 + 3 in row 2 and y's in row 3; swap32_add(x, y) holds x's rows
-// 0 + 2 and 1 + 3 in rows 0 and 1, y's in rows 2 and 3
-__device__ __forceinline__ float swap16_add(float x, float y) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, x),
-                                                  __builtin_bit_cast(unsigned, y), false, false);
-  return __builtin_bit_cast(float, (unsigned)a[0]) + __builtin_bit_cast(float, (unsigned)a[1]);
-}
-__device__ __forceinline__ float swap32_add(float x, float y) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x),
-                                                  __builtin_bit_cast(unsigned, y), false, false);
-  return __builtin_bit_cast(float, (unsigned)a[0]) + __builtin_bit_cast(float, (unsigned)a[1]);
-}
-
 // NJ: cached positions per lane (4 NJ >= pos; slots past pos weigh exactly 0,
 // so any such NJ gives the same sums)
 template <typename KV, int NJ>
@@ -272,8 +256,8 @@ __global__ __launch_bounds__(PNT) void k_attn_pair_cp(const int8_t *__restrict__
 #pragma unroll
     for (int e = 0; e < 8; e++) o[e] = fmaf(s[i], v8[e], o[e]);
   }
-  const float lo = swap32_add(swap16_add(o[0], o[1]), swap16_add(o[2], o[3]));
-  const float hi = swap32_add(swap16_add(o[4], o[5]), swap16_add(o[6], o[7]));
+  float lo, hi;
+  rows4_scatter8(o, lo, hi);
   {
     const float inv = 1.0f / den;
     const int d = 8 * r16 + rg;

@@ -107,6 +107,28 @@ __device__ __forceinline__ float rows4_max(float v) {
   return fmaxf(__builtin_bit_cast(float, (unsigned)b[0]), __builtin_bit_cast(float, (unsigned)b[1]));
 }
 
+// Eight values o[0..7] summed over the wave's four 16-lane rows with the
+// pairs of rows4_sum, scattered: lane l of row r = l / 16 gets the sum of
+// o[r] in lo and of o[4 + r] in hi. Each stage is one row swap and one add
+// for two registers: permlane16_swap(x, y) added holds x's rows 0 + 1 in row
+// 0, y's in row 1, x's rows 2 + 3 in row 2, y's in row 3; permlane32_swap(x,
+// y) added holds x's rows 0 + 2 and 1 + 3 in rows 0 and 1, y's in rows 2, 3
+// (12 instructions where eight rows4_sum take 32 and their copies)
+__device__ __forceinline__ float swap16_add(float x, float y) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, x),
+                                                  __builtin_bit_cast(unsigned, y), false, false);
+  return __builtin_bit_cast(float, (unsigned)a[0]) + __builtin_bit_cast(float, (unsigned)a[1]);
+}
+__device__ __forceinline__ float swap32_add(float x, float y) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x),
+                                                  __builtin_bit_cast(unsigned, y), false, false);
+  return __builtin_bit_cast(float, (unsigned)a[0]) + __builtin_bit_cast(float, (unsigned)a[1]);
+}
+__device__ __forceinline__ void rows4_scatter8(const float (&o)[8], float &lo, float &hi) {
+  lo = swap32_add(swap16_add(o[0], o[1]), swap16_add(o[2], o[3]));
+  hi = swap32_add(swap16_add(o[4], o[5]), swap16_add(o[6], o[7]));
+}
+
 // sum over aligned groups of 8 lanes (lanes 8k..8k+7), in every lane of the group
 __device__ __forceinline__ float group8_sum_dpp(float v) {
   v += dpp_f<kQuadXor1>(v);
