@@ -254,40 +254,49 @@ def cpu_frames(q3o, frame, pre, gpu_codes, budget_s, max_frames, threads):
 def gemv_roofline(ts, args, cs=None):
     """The dominant kernel: the Q8_0 matrix-vector products of one talker
     decode step. achieved = algorithmic bytes per launch / the average launch
-    duration: the products launched directly on their own stream, iters
-    passes between two HIP events recorded on that stream (mode 0 of
-    q3h_stack_time_gemv), so the gaps between launches count against the
-    kernels. Beside it: the same launches with an event pair attached to each
-    (mode 2: that timing adds its own cost to every launch) and the graph
-    replay's wall time per launch (mode 1). With cs: the same for one
-    code-predictor forward (5 layers + one 2048-row head, 85.8 MB: after the
-    first pass its weights stay in the 256 MB Infinity Cache)."""
-    us, launches, nbytes = ts.time_gemv(head=0, iters=args.gemv_iters, mode=0)
+    duration: the step's products captured in a HIP graph on their own stream
+    and replayed iters times between two HIP events recorded on that stream
+    (mode 1 of q3h_stack_time_gemv), as the frame step runs them; the gaps
+    between launches count against the kernels. Beside it: the same products
+    launched directly between two events (mode 0: there the host's launch
+    rate can leave the device idle between kernels) and with an event pair
+    attached to each launch (mode 2: that timing adds its own cost to every
+    launch). With --no-graph the direct launches give the figure. With cs:
+    the same for one code-predictor forward (5 layers + one 2048-row head,
+    85.8 MB: after the first pass its weights stay in the 256 MB Infinity
+    Cache)."""
+    direct, launches, nbytes = ts.time_gemv(head=0, iters=args.gemv_iters, mode=0)
     ev_us, _, _ = ts.time_gemv(head=0, iters=args.gemv_iters, mode=2)
-    per_launch = nbytes / launches
-    achieved = per_launch / (us * 1e-6) / 1e9
     wall = None
     if not args.no_graph:
         wall, _, _ = ts.time_gemv(head=0, iters=args.gemv_iters, mode=1)
-    log(f"gemv: {launches} launches/step, {us:.2f} us/launch ({achieved:.0f} GB/s), "
-        f"events on each launch {ev_us:.2f} us, graph wall "
-        f"{wall if wall is None else round(wall, 2)} us/launch")
+    us = direct if wall is None else wall
+    per_launch = nbytes / launches
+    achieved = per_launch / (us * 1e-6) / 1e9
+    log(f"gemv: {launches} launches/step, {us:.2f} us/launch ({achieved:.0f} GB/s, "
+        f"{'direct launches' if wall is None else 'graph replay'}), direct launches "
+        f"{direct:.2f} us, events on each launch {ev_us:.2f} us")
     out = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                frac=round(achieved / HBM_PEAK_GBS, 4), traffic=GEMV_TRAFFIC_PER_LAUNCH,
                traffic_source="profiles/gemv_q8_decode_step_traffic.md",
                kernel="k_gemv_q8v (Q8_0 matrix-vector products of one talker decode step)",
                bytes_per_launch=int(per_launch), us_per_launch=round(us, 3),
-               timing="direct launches between two events on their stream (gaps included)",
+               timing=("direct launches between two events on their stream (gaps included)"
+                       if wall is None else "graph replay between two events on its stream "
+                       "(gaps included)"),
+               direct_us_per_launch=round(direct, 3),
                event_attached_us_per_launch=round(ev_us, 3),
                graph_wall_us_per_launch=None if wall is None else round(wall, 3))
     if cs is not None:
-        cus, cl, cb = cs.time_gemv(head=0, iters=args.gemv_iters, mode=0)
+        cdirect, cl, cb = cs.time_gemv(head=0, iters=args.gemv_iters, mode=0)
         cwall = None if args.no_graph else cs.time_gemv(head=0, iters=args.gemv_iters, mode=1)[0]
+        cus = cdirect if cwall is None else cwall
         cgbs = cb / cl / (cus * 1e-6) / 1e9
         log(f"gemv (code predictor, cache-resident): {cl} launches/step, {cus:.2f} "
-            f"us/launch ({cgbs:.0f} GB/s), graph wall {cwall} us/launch")
+            f"us/launch ({cgbs:.0f} GB/s), direct launches {cdirect:.2f} us")
         out["code_predictor"] = dict(launches=cl, bytes_per_launch=int(cb / cl),
                                      us_per_launch=round(cus, 3), achieved_gbs=round(cgbs, 1),
+                                     direct_us_per_launch=round(cdirect, 3),
                                      graph_wall_us_per_launch=None if cwall is None
                                      else round(cwall, 3))
     return out

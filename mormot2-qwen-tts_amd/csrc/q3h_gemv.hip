@@ -63,15 +63,14 @@ __device__ __forceinline__ float dot4_i8(int w, float4 x, float acc) {
 // row, by the first wave of workgroup 0) is taken with a single row only.
 // NP = 4 (one row): x holds four partial rows K apart whose sum
 // (p0 + p1) + (p2 + p3) is the row; the loader waves of workgroup 0 write that
-// sum to x_out.
+// sum (not normed) to xn_out. The argument list stays at 64 bytes.
 template <int R, int C, int EPI, int LW, int MR, int NP = 0>
 __global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq,
                                                    const float *__restrict__ x,
                                                    const float *__restrict__ norm_w,
                                                    float *__restrict__ y, int N, int W, float eps,
                                                    int ldx, int ldy, int M,
-                                                   float *__restrict__ xn_out,
-                                                   float *__restrict__ x_out) {
+                                                   float *__restrict__ xn_out) {
   static_assert(NP == 0 || (NP == 4 && MR == 1), "partial rows: one row of four parts");
   constexpr int K = C * 1024, NB = K / 32;
   constexpr int T = 64 * LW, J = C * 256 / T;  // loader threads, float4 per loader thread
@@ -135,7 +134,7 @@ __global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq
     }
     if (blockIdx.x == 0 && wave < LW) {
 #pragma unroll
-      for (int j = 0; j < J; j++) reinterpret_cast<float4 *>(x_out)[t + T * j] = xv[0][j];
+      for (int j = 0; j < J; j++) reinterpret_cast<float4 *>(xn_out)[t + T * j] = xv[0][j];
     }
   }
 
@@ -178,7 +177,7 @@ __global__ __launch_bounds__(1024) void k_gemv_q8v(const int8_t *__restrict__ wq
       inv[m] = 1.0f / sqrtf(ss * (1.0f / K) + eps);
     }
   }
-  if (xn_out != nullptr && blockIdx.x == 0 && wave == 0) {
+  if (NP == 0 && xn_out != nullptr && blockIdx.x == 0 && wave == 0) {
 #pragma unroll
     for (int c = 0; c < C; c++)
 #pragma unroll
@@ -381,11 +380,10 @@ void launch_vl(const GemvArgs &a, int epi, int waves, hipStream_t st, hipEvent_t
   do {                                                                                           \
     if (ev0)                                                                                     \
       hipExtLaunchKernelGGL((k_gemv_q8v<R, C, E, LW, MR>), grid, block, 0, st, ev0, ev1, 0, a.wq, \
-                            a.x, a.norm_w, a.y, a.N, waves, a.eps, a.ldx, a.ldy, a.M, a.xn_out, \
-                            nullptr);                                                            \
+                            a.x, a.norm_w, a.y, a.N, waves, a.eps, a.ldx, a.ldy, a.M, a.xn_out); \
     else                                                                                         \
       hipLaunchKernelGGL((k_gemv_q8v<R, C, E, LW, MR>), grid, block, 0, st, a.wq, a.x, a.norm_w, \
-                         a.y, a.N, waves, a.eps, a.ldx, a.ldy, a.M, a.xn_out, nullptr);          \
+                         a.y, a.N, waves, a.eps, a.ldx, a.ldy, a.M, a.xn_out);                   \
   } while (0)
   if (epi == EPI_STORE)
     Q3H_V(EPI_STORE);
@@ -488,7 +486,7 @@ bool launch_gemv_q8_swiglu_parts(const GemvArgs &a, float *x_out, hipStream_t st
   const dim3 grid(256), block(64 * W);
 #define Q3H_P(RR)                                                                                 \
   hipLaunchKernelGGL((k_gemv_q8v<RR, 1, EPI_SWIGLU, 4, 1, 4>), grid, block, 0, st, a.wq, a.x,     \
-                     a.norm_w, a.y, a.N, W, a.eps, a.ldx, a.ldy, a.M, nullptr, x_out)
+                     a.norm_w, a.y, a.N, W, a.eps, a.ldx, a.ldy, a.M, x_out)
   if (R1 == 6)
     Q3H_P(6);
   else if (R1 == 4)
