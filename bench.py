@@ -20,12 +20,19 @@ memory, so the wall clock of the K calls is the whole-job time.
 Beside it:
   roofline      the Q8_0 matrix-vector products of one talker decode step (28
                 layers x 4 products + the 3072-row head, 471.5 MB of weights,
-                more than the 256 MB Infinity Cache holds): the kernels' own
-                execution time from hipEvents attached to each launch on their
-                stream (the figure rocprofv3 reports per dispatch), and the
-                graph-replayed wall time per launch beside it;
+                more than the 256 MB Infinity Cache holds): the average launch
+                duration of the products captured in a HIP graph and replayed
+                between two HIP events on their stream (gaps included), with
+                direct launches and an event pair on each launch beside it,
+                the rocprofv3 trace's average of the same products, and the
+                bound one dependent launch of that many bytes can reach;
   cpu_baseline  the oracle (the C restatement of the same frame step) on the
                 host cores, on a bounded sample of the same workload;
+  batched_b32 (frame_b1)  32 streams, prompt rows uniform in [16, 256],
+                128 frames, int8 activations (int8 MFMA products);
+  f32_b8 (frame_b1)  f32 weights at batch 8: 8 x 512-row prefills, then 64
+                frames of f32 products, with the oracle's f32 frame step as
+                its CPU baseline and stream 0's codes against it;
   long_context_attention (frame_b1)  the talker with an f16 K/V cache
                 prefilled to 2048 / 4096 / 8192 positions: 32 decode steps
                 each, and the decode attention kernels' GB/s;
@@ -59,6 +66,14 @@ F32_PROMPT_ROWS = 512
 # step, from rocprofv3 FETCH_SIZE + WRITE_SIZE passes scaled by a plain copy
 # kernel of known size (profiles/gemv_q8_decode_step_traffic.md)
 GEMV_TRAFFIC_PER_LAUNCH = 4320854
+# the same products' average duration in a rocprofv3 kernel trace (5,876
+# direct dispatches; profiles/gemv_q8_decode_step_durations.md)
+GEMV_ROCPROF_US_PER_LAUNCH = 3.273
+# what one dependent launch of a product can reach on this part: an empty
+# kernel costs LAUNCH_FLOOR_US per dependent launch in a graph before any byte
+# moves, and HBM streams HBM_MARGINAL_GBS marginal (4 MB / 8 MB launches)
+LAUNCH_FLOOR_US = 1.54
+HBM_MARGINAL_GBS = 5700.0
 PROMPT_ROWS = 48
 
 
@@ -276,8 +291,25 @@ def gemv_roofline(ts, args, cs=None):
     log(f"gemv: {launches} launches/step, {us:.2f} us/launch ({achieved:.0f} GB/s, "
         f"{'direct launches' if wall is None else 'graph replay'}), direct launches "
         f"{direct:.2f} us, events on each launch {ev_us:.2f} us")
+    # the bound one launch of per_launch bytes can reach: the launch floor plus
+    # the bytes at the marginal HBM rate
+    attain_us = LAUNCH_FLOOR_US + per_launch / (HBM_MARGINAL_GBS * 1e3)
+    attain = per_launch / (attain_us * 1e-6) / 1e9
+    rp = per_launch / (GEMV_ROCPROF_US_PER_LAUNCH * 1e-6) / 1e9
     out = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                frac=round(achieved / HBM_PEAK_GBS, 4), traffic=GEMV_TRAFFIC_PER_LAUNCH,
+               frac_basis=("graph-replayed wall time per launch (gaps between launches "
+                           "included)" if wall is not None else "direct launches"),
+               rocprof=dict(us_per_launch=GEMV_ROCPROF_US_PER_LAUNCH, achieved=round(rp, 1),
+                            frac=round(rp / HBM_PEAK_GBS, 4),
+                            source="profiles/gemv_q8_decode_step_durations.md (kernel trace "
+                                   "of the same products, direct launches)"),
+               attainable_per_launch=dict(
+                   us=round(attain_us, 3), achieved=round(attain, 1),
+                   frac=round(attain / HBM_PEAK_GBS, 4),
+                   frac_reached=round(achieved / attain, 4),
+                   model=f"{LAUNCH_FLOOR_US} us per dependent launch (empty kernel in a graph) "
+                         f"+ bytes at {HBM_MARGINAL_GBS / 1e3:.1f} TB/s marginal HBM rate"),
                traffic_source="profiles/gemv_q8_decode_step_traffic.md",
                kernel="k_gemv_q8v (Q8_0 matrix-vector products of one talker decode step)",
                bytes_per_launch=int(per_launch), us_per_launch=round(us, 3),
@@ -305,6 +337,8 @@ def gemv_roofline(ts, args, cs=None):
 # algorithmic weight bytes of one frame step: talker layers + head, and 15
 # code-predictor forwards each with its head (Q8_0, 34 bytes per 32 weights)
 FRAME_WEIGHT_BYTES = 1759083520
+# the same in f32 (4 bytes per weight; norm vectors included)
+F32_FRAME_WEIGHT_BYTES = 6619626496
 KV_BYTES_PER_POSITION = {"f32": 229376, "f16": 114688}  # talker, 28 layers
 B32_STREAMS, B32_FRAMES = 32, 128
 CONFIG2_FRAMES = 156
@@ -356,6 +390,62 @@ def batched_b32(dev, f32, tables, args):
     cs.destroy()
     if not args.no_cpu:
         cpu, nf, equal = cpu_baseline(f32, tables, pre, codes, args.cpu_seconds / 2, steps, 1)
+        out["cpu_baseline"] = cpu
+        out["parity"] = dict(frames=nf, codes_equal_stream0=bool(equal))
+    return out
+
+
+F32_B8_STREAMS, F32_B8_FRAMES = 8, 64
+
+
+def f32_batch8(dev, f32, tables, args):
+    """The f32-weight path at batch 8 (the reference's /f32 mode): both stacks
+    and their heads in f32 on the device, 8 streams each prefilled with 512
+    N(0, 1) prompt rows (causal prefill attention, products on the split-bf16
+    matrix cores), then F32_B8_FRAMES frames of the 8 streams with f32
+    activations and f32 K/V. Reports the timed 8 x 512-row prefill, frames/s
+    over the frames with the codes of all streams in host memory after each
+    step, the algorithmic HBM bytes of a step (the f32 weights once, the
+    talker K/V of every stream) over the step time, stream 0's codes against
+    the oracle's f32 frame step, and the oracle's rate on the host cores."""
+    n, steps, warmup = F32_B8_STREAMS, F32_B8_FRAMES, 2
+    pre = prompts(args.seed, "f32_b8", n)
+    max_pos = F32_PROMPT_ROWS + steps + warmup + 8
+    t0 = time.time()
+    ts = q3h.Stack(dev, dict(synth.TALKER, dtype=q3h.F32, kv_f16=0, act_q8=0,
+                             max_positions=max_pos), f32["tl"], f32["tf"], q3h.F32)
+    cs = q3h.Stack(dev, dict(synth.PREDICTOR, dtype=q3h.F32, kv_f16=0, act_q8=0,
+                             max_positions=16), f32["cl"], f32["cf"], q3h.F32)
+    ts.add_head(f32["th"], q3h.F32)
+    for h in f32["ch"]:
+        cs.add_head(h, q3h.F32)
+    frame = q3h.Frame(ts, cs, tables["codec_emb"], tables["pred_emb"], tables["tts_pad"],
+                      n_streams=n, max_positions=max_pos, max_frames=steps + warmup + 8,
+                      use_graph=not args.no_graph)
+    log(f"f32 b8: f32 stacks on the device in {time.time() - t0:.1f} s "
+        f"({(ts.bytes + cs.bytes) / 1e9:.2f} GB of layers)")
+    total, lat, codes = run_gpu(frame, pre, steps, warmup)
+    fps = n * steps / total
+    positions = float(np.mean([n * (F32_PROMPT_ROWS + i + 1) for i in range(steps)]))
+    step_bytes = F32_FRAME_WEIGHT_BYTES + KV_BYTES_PER_POSITION["f32"] * positions
+    gbs = step_bytes / (total / steps) / 1e9
+    out = dict(frames_per_s=round(fps, 2), streams=n, frames=steps,
+               ms_per_step=round(1e3 * total / steps, 4),
+               step_us_p50=round(1e6 * float(np.median(lat)), 1),
+               step_us_p99=round(1e6 * float(np.percentile(lat, 99)), 1),
+               prefill_ms=round(1e3 * run_gpu.prefill_s, 2),
+               prefill="8 streams x 512 prompt rows, one q3h_frame_start each (timed together)",
+               prompt_rows=F32_PROMPT_ROWS, weights="f32", activations="f32", kv="f32",
+               hbm_bytes_per_step=int(step_bytes), hbm_gbs=round(gbs, 1),
+               hbm_frac=round(gbs / HBM_PEAK_GBS, 4))
+    log(f"f32 b8: {fps:.1f} frames/s, {1e3 * total / steps:.3f} ms per step, prefill of 8 x "
+        f"512 rows {1e3 * run_gpu.prefill_s:.1f} ms, {gbs:.0f} GB/s algorithmic")
+    frame.destroy()
+    ts.destroy()
+    cs.destroy()
+    if not args.no_cpu:
+        cpu, nf, equal = cpu_baseline(f32, tables, pre, codes, args.cpu_seconds / 2, steps, 0,
+                                      f32w=True)
         out["cpu_baseline"] = cpu
         out["parity"] = dict(frames=nf, codes_equal_stream0=bool(equal))
     return out
@@ -657,6 +747,8 @@ def main():
                          "the default is its f32 cache")
     ap.add_argument("--no-b32", action="store_true",
                     help="skip the 32-stream int8 sub-record of the default run")
+    ap.add_argument("--no-f32", action="store_true",
+                    help="skip the f32-weight batch-8 sub-record of the default run")
     ap.add_argument("--no-talker", action="store_true",
                     help="skip the talker-only decode sub-record of the default run")
     ap.add_argument("--no-codec", action="store_true",
@@ -777,6 +869,7 @@ def main():
     talker_b1 = talker_decode_b1(dev, ts, f32, tables, args.seed, args) \
         if (b1 and not args.no_talker) else None
     b32 = batched_b32(dev, f32, tables, args) if (b1 and not args.no_b32) else None
+    f32b8 = f32_batch8(dev, f32, tables, args) if (b1 and not args.no_f32) else None
     load = load_from_bf16(dev, f32, act_q8) if b1 else None
     text_start = None
     if b1 and not args.no_text:
@@ -829,6 +922,7 @@ def main():
         "step_us_p99": round(1e6 * float(np.percentile(lat, 99)), 1),
         "frame_b1_156_frames": full,
         "batched_b32": b32,
+        "f32_b8": f32b8,
         "talker_decode_b1": talker_b1,
         "roofline": roofline,
         "cpu_baseline": cpu,

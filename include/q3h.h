@@ -154,14 +154,17 @@ int q3h_forward_embeds(q3h_context *c, const float *x, int rows, int head,
                        float *logits, float *normed_last);
 
 /* No counterpart in the reference. For callers that cannot allocate device
-   memory (code under HIP graph capture, tight serving loops, harnesses that
-   forbid hipMalloc): q3h_forward_embeds with the same arguments and results,
+   memory (tight serving loops, harnesses that forbid hipMalloc); it is called
+   outside any stream capture, like q3h_forward_embeds: it launches on the
+   context's own stream, copies pageable host memory and blocks until the
+   outputs are in host memory. q3h_forward_embeds with the same arguments and results,
    but its work buffers are carved from one static device array of
    Q3H_NOALLOC_SCRATCH_BYTES per GPU (set up by q3h_device_open) instead of
    the context's own buffers, which q3h_forward_embeds grows with hipMalloc.
    Calls no allocating routine. rows <= Q3H_NOALLOC_MAX_ROWS, and the
-   buffers of the call (they grow with rows and, for long contexts, with the
-   attention splits of length + rows positions) must fit the array: otherwise
+   buffers of the call (they grow with rows and, for fewer than 16 rows of
+   an f32-activation stack over more than 256 positions, with the decode
+   attention's splits) must fit the array: otherwise
    Q3H_E_CAPACITY and nothing is computed. Every call on one GPU shares that
    GPU's array, which keeps the last call's contents (no kernel reads a
    buffer before writing it); calls on one device are serialized by a lock
@@ -173,14 +176,17 @@ int q3h_forward_embeds_noalloc(q3h_context *c, const float *x, int rows, int hea
 
 /* TQwenLm.Forward with TQwenLm.Probe set (lm.pas:139-142, 380-389: the
    probe receives the output of every layer, "name.layerN", then the normed
-   state): q3h_forward_embeds, plus layer_out [layers][rows][hidden] (host
-   f32, nullable) receiving the raw output of each layer for every row (the
-   residual stream after the layer's down projection), so that a difference
-   against another implementation can be located at a layer. The outputs are
-   those of q3h_forward_embeds; the copies add one device-to-device copy per
-   layer. */
+   state of every row, "name.out"): q3h_forward_embeds, plus layer_out
+   [layers][rows][hidden] (host f32, nullable) receiving the raw output of
+   each layer for every row (the residual stream after the layer's down
+   projection), so that a difference against another implementation can be
+   located at a layer, and normed_rows [rows][hidden] (host f32, nullable)
+   receiving the final RMSNorm of every row (normed_last is its last row).
+   The outputs are those of q3h_forward_embeds; the copies add one
+   device-to-device copy per layer. */
 int q3h_forward_embeds_probe(q3h_context *c, const float *x, int rows, int head,
-                             float *logits, float *normed_last, float *layer_out);
+                             float *logits, float *normed_last, float *layer_out,
+                             float *normed_rows);
 
 /* no reference counterpart (the reference is single-stream): one row per
    context, n contexts of the same stack at their own positions;

@@ -1053,6 +1053,15 @@ int forward_positions(const q3h_context *c, int rows) {
   return rows == 1 ? graph_cover(c->len + 1, c->max_pos) : c->len + rows;
 }
 
+// the attention splits whose partials a forward of `rows` rows keeps: none on
+// an int8 stack (its attention quantizes its output directly) or over
+// kPrefillRows rows or more (the causal prefill attention), else those of the
+// decode attention over forward_positions
+int forward_splits(const q3h_context *c, int rows) {
+  if (c->s->cfg.act_q8 || rows >= kPrefillRows) return 0;
+  return attention_splits(c->s, forward_positions(c, rows));
+}
+
 // the kernels of a forward: descriptors, layers, head (or final norm), the
 // device length
 void enqueue_forward(q3h_context *c, Work &w, int rows, int positions, int head,
@@ -1100,7 +1109,8 @@ hipGraphExec_t forward_graph(q3h_context *c, int head, int positions) {
 // of forward_positions and the head's rows), replayed from a captured graph
 // when graph: blocks until the outputs are in host memory
 void forward_rows(q3h_context *c, Work &w, const float *x, int rows, int head, float *logits,
-                  float *normed_last, float *layer_out = nullptr, bool graph = false) {
+                  float *normed_last, float *layer_out = nullptr, bool graph = false,
+                  float *normed_rows = nullptr) {
   q3h_stack *s = c->s;
   const q3h_stack_config &cf = s->cfg;
   const int H = cf.hidden;
@@ -1130,8 +1140,11 @@ void forward_rows(q3h_context *c, Work &w, const float *x, int rows, int head, f
             "upload x");
   LayerIO io;
   io.single_context = true;
-  const size_t probe_bytes = sizeof(float) * cf.layers * rows * H;
-  if (layer_out) {
+  // the probe's device buffer: the layer outputs [layers][rows][hidden], then
+  // the final-normed rows [rows][hidden]
+  const size_t layer_floats = (size_t)cf.layers * rows * H;
+  const size_t probe_bytes = sizeof(float) * (layer_floats + (size_t)rows * H);
+  if (layer_out || normed_rows) {
     if (c->probe_bytes < probe_bytes) {
       check_hip(hipStreamSynchronize(st), "probe sync");
       dev_free(c->probe);
@@ -1140,12 +1153,16 @@ void forward_rows(q3h_context *c, Work &w, const float *x, int rows, int head, f
       c->probe = (float *)dev_alloc(probe_bytes);
       c->probe_bytes = probe_bytes;
     }
-    io.layer_out = c->probe;
+    if (layer_out) io.layer_out = c->probe;
   }
   if (graph)
     check_hip(hipGraphLaunch(forward_graph(c, head, positions), st), "forward graph launch");
   else
     enqueue_forward(c, w, rows, positions, head, io, st);
+  // the final RMSNorm of every row (the probe's "norm" state, lm.pas:383-384)
+  if (normed_rows)
+    launch_rmsnorm_rows(w.h, H, rows, H, s->final_norm, cf.rms_eps, c->probe + layer_floats, H,
+                        st);
   check_hip(hipGetLastError(), "forward kernels");
   if (normed_last)
     check_hip(hipMemcpyAsync(graph ? pin_n : normed_last, w.normed, sizeof(float) * H,
@@ -1156,8 +1173,13 @@ void forward_rows(q3h_context *c, Work &w, const float *x, int rows, int head, f
                              hipMemcpyDeviceToHost, st),
               "download logits");
   if (layer_out)
-    check_hip(hipMemcpyAsync(layer_out, c->probe, probe_bytes, hipMemcpyDeviceToHost, st),
+    check_hip(hipMemcpyAsync(layer_out, c->probe, sizeof(float) * layer_floats,
+                             hipMemcpyDeviceToHost, st),
               "download layer outputs");
+  if (normed_rows)
+    check_hip(hipMemcpyAsync(normed_rows, c->probe + layer_floats, sizeof(float) * rows * H,
+                             hipMemcpyDeviceToHost, st),
+              "download normed rows");
   check_hip(hipStreamSynchronize(st), "forward sync");
   if (graph) {
     if (normed_last) std::memcpy(normed_last, pin_n, sizeof(float) * H);
@@ -1175,21 +1197,22 @@ extern "C" int q3h_forward_embeds(q3h_context *c, const float *x, int rows, int 
     q3h_stack *s = c->s;
     check_hip(hipSetDevice(s->dev->ordinal), "hipSetDevice");
     const int head_rows = head >= 0 ? s->heads[head].N : 0;
-    c->w.ensure(s, rows, attention_splits(s, forward_positions(c, rows)), head_rows);
+    c->w.ensure(s, rows, forward_splits(c, rows), head_rows);
     // one row (a decode step): the forward replayed from a captured graph
     forward_rows(c, c->w, x, rows, head, logits, normed_last, nullptr, rows == 1);
   });
 }
 
 extern "C" int q3h_forward_embeds_probe(q3h_context *c, const float *x, int rows, int head,
-                                        float *logits, float *normed_last, float *layer_out) {
+                                        float *logits, float *normed_last, float *layer_out,
+                                        float *normed_rows) {
   return guard([&] {
     if (!forward_args(c, x, rows, head, "q3h_forward_embeds_probe")) return;
     q3h_stack *s = c->s;
     check_hip(hipSetDevice(s->dev->ordinal), "hipSetDevice");
     const int head_rows = head >= 0 ? s->heads[head].N : 0;
-    c->w.ensure(s, rows, attention_splits(s, forward_positions(c, rows)), head_rows);
-    forward_rows(c, c->w, x, rows, head, logits, normed_last, layer_out);
+    c->w.ensure(s, rows, forward_splits(c, rows), head_rows);
+    forward_rows(c, c->w, x, rows, head, logits, normed_last, layer_out, false, normed_rows);
   });
 }
 
@@ -1206,7 +1229,7 @@ extern "C" int q3h_forward_embeds_noalloc(q3h_context *c, const float *x, int ro
             "q3h_forward_embeds_noalloc: the device has no scratch array");
     const int head_rows = head >= 0 ? s->heads[head].N : 0;
     Work w;  // a view of the array: owns nothing
-    require(work_carve(s, rows, attention_splits(s, forward_positions(c, rows)), head_rows,
+    require(work_carve(s, rows, forward_splits(c, rows), head_rows,
                        dev->scratch, Q3H_NOALLOC_SCRATCH_BYTES, w),
             Q3H_E_CAPACITY,
             "q3h_forward_embeds_noalloc: the work buffers of " + std::to_string(rows) +

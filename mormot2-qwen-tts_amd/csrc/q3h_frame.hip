@@ -1041,7 +1041,9 @@ extern "C" int q3h_frame_step(q3h_frame *f, int32_t *codes, int32_t *alive) {
         }
         check_hip(hipGraphLaunch(exec, sl.stream), "hipGraphLaunch");
       } else {
-        enqueue_step(f, sl, slen, sl.stream);
+        // the cover a captured step would use, so that both give the same sums
+        // (beyond 256 positions the split attention's shape follows the cover)
+        enqueue_step(f, sl, graph_cover(slen, c.max_positions), sl.stream);
         check_hip(hipGetLastError(), "frame kernels");
       }
       // the slice's codes and alive flags, into the same places of the pinned copy

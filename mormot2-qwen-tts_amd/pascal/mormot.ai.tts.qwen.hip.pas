@@ -157,9 +157,10 @@ function q3h_context_time_attention(c: q3h_context; iters: integer;
 function q3h_forward_embeds(c: q3h_context; x: PSingle; rows, head: integer;
   logits, normed_last: PSingle): integer; cdecl; external LIBQ3H;
 /// TQwenLm.Forward with its Probe (lm.pas:380-389): layer_out [layers][rows]
-// [hidden] receives the raw output of every layer
+// [hidden] receives the raw output of every layer (name.layerN), normed_rows
+// [rows][hidden] the final-normed state of every row (name.out)
 function q3h_forward_embeds_probe(c: q3h_context; x: PSingle; rows, head: integer;
-  logits, normed_last, layer_out: PSingle): integer; cdecl; external LIBQ3H;
+  logits, normed_last, layer_out, normed_rows: PSingle): integer; cdecl; external LIBQ3H;
 /// no counterpart in the reference: q3h_forward_embeds for callers that
 // cannot allocate device memory (work buffers in a static device array of
 // Q3H_NOALLOC_SCRATCH_BYTES per GPU; rows <= Q3H_NOALLOC_MAX_ROWS)

@@ -150,7 +150,7 @@ SIGNATURES = {
     "q3h_context_time_attention": (_I, [_P, _I, _FP, ctypes.POINTER(ctypes.c_int64)]),
     "q3h_forward_embeds": (_I, [_P, _FP, _I, _I, _FP, _FP]),
     "q3h_forward_embeds_noalloc": (_I, [_P, _FP, _I, _I, _FP, _FP]),
-    "q3h_forward_embeds_probe": (_I, [_P, _FP, _I, _I, _FP, _FP, _FP]),
+    "q3h_forward_embeds_probe": (_I, [_P, _FP, _I, _I, _FP, _FP, _FP, _FP]),
     "q3h_forward_embeds_batch": (_I, [ctypes.POINTER(_P), _I, _FP, _IP, _FP, _FP]),
     "q3h_frame_create": (_I, [_P, _P, ctypes.POINTER(FrameConfig), _FP,
                               ctypes.POINTER(_FP), _FP, ctypes.POINTER(_P)]),
@@ -336,7 +336,9 @@ class Context:
 
     def forward_probe(self, x, head=-1):
         """forward() with the probe of TQwenLm (lm.pas:380-389): returns
-        (logits or None, normed_last, layer_out [layers][rows][hidden])."""
+        (logits or None, normed_last, layer_out [layers][rows][hidden],
+        normed_rows [rows][hidden]): every layer's output ("name.layerN") and
+        the final-normed state of every row ("name.out")."""
         x = _f32(x)
         if x.ndim == 1:
             x = x[None, :]
@@ -346,9 +348,10 @@ class Context:
             logits = np.empty(self.stack.head_rows[head], dtype=np.float32)
         normed = np.empty(hidden, dtype=np.float32)
         lo = np.empty((self.stack.cfg["layers"], rows, hidden), dtype=np.float32)
+        nr = np.empty((rows, hidden), dtype=np.float32)
         _check(lib().q3h_forward_embeds_probe(self.h, _fp(x), rows, head, _fp(logits),
-                                              _fp(normed), _fp(lo)))
-        return logits, normed, lo
+                                              _fp(normed), _fp(lo), _fp(nr)))
+        return logits, normed, lo, nr
 
     def fill_kv(self, k, v):
         """k, v: float32 [layers][kv_heads][len][head_dim]."""

@@ -293,6 +293,10 @@ static void rmsnorm(const float *x, const float *w, int n, float eps, float *y) 
   for (int i = 0; i < n; i++) y[i] = w[i] * (x[i] * inv);
 }
 
+void q3o_rmsnorm_rows(const float *x, int rows, int n, const float *w, float eps, float *y) {
+  for (int r = 0; r < rows; r++) rmsnorm(x + (size_t)r * n, w, n, eps, y + (size_t)r * n);
+}
+
 static void rope(float *x, int d, int pos, float theta) {
   const int half = d / 2;
   for (int i = 0; i < half; i++) {

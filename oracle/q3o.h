@@ -110,6 +110,10 @@ int q3o_ctx_fill(q3o_ctx *c, const float *k, const float *v, int len);
 /* x [rows][hidden] at positions length..length+rows-1; normed_last [hidden]
    (nullable); layer_out [layers][rows][hidden] raw layer outputs (nullable);
    returns 0, or -1 when the context would overflow */
+/* the stack's RMSNorm (double sum of squares) of `rows` rows of n values:
+   the final norm of every row that TQwenLm's probe receives as name.out
+   (lm.pas:383-384) */
+void q3o_rmsnorm_rows(const float *x, int rows, int n, const float *w, float eps, float *y);
 int q3o_forward_embeds(q3o_ctx *c, const float *x, int rows, float *normed_last,
                        float *layer_out);
 

@@ -160,6 +160,8 @@ def lib():
             "q3o_ctx_k": (_FP, [_P, ctypes.c_int]),
             "q3o_ctx_v": (_FP, [_P, ctypes.c_int]),
             "q3o_ctx_fill": (ctypes.c_int, [_P, _FP, _FP, ctypes.c_int]),
+            "q3o_rmsnorm_rows": (None, [_FP, ctypes.c_int, ctypes.c_int, _FP, ctypes.c_float,
+                                        _FP]),
             "q3o_forward_embeds": (ctypes.c_int, [_P, _FP, ctypes.c_int, _FP, _FP]),
             "q3o_forward_embeds_traced": (ctypes.c_int, [_P, _FP, ctypes.c_int, _FP, _FP,
                                                          ctypes.POINTER(Trace)]),
@@ -223,6 +225,15 @@ def fp16_to_fp32(h):
     out = np.empty(h.shape, dtype=np.float32)
     lib().q3o_fp16_to_fp32_row(h.ctypes.data_as(_P), _fp(out), h.size)
     return out
+
+
+def rmsnorm_rows(x, w, eps=1e-6):
+    """The stack's RMSNorm of every row of x [rows][n] (double sums)."""
+    x, w = _f32(x), _f32(w)
+    x2 = x.reshape(-1, x.shape[-1])
+    y = np.empty_like(x2)
+    lib().q3o_rmsnorm_rows(_fp(x2), x2.shape[0], x2.shape[1], _fp(w), eps, _fp(y))
+    return y.reshape(x.shape)
 
 
 def quantize_q8_0(x):
@@ -376,6 +387,7 @@ class Stack:
 class Ctx:
     def __init__(self, stack, max_positions):
         self.stack = stack
+        self.max_positions = max_positions
         self.h = lib().q3o_ctx_create(stack.h, max_positions)
 
     def reset(self):
@@ -429,6 +441,20 @@ class Ctx:
         out["normed"] = normed
         out["layer_out"] = lo
         return out
+
+    def read_kv(self, layer):
+        """The cache of one layer for positions [0, length): (k, v) as f32
+        [kv_heads][length][head_dim] (copies; with kv_f16 the stored values
+        are the half-float roundings)."""
+        d = self.stack.dims
+        shape = (d["kv_heads"], self.max_positions, d["head_dim"])
+        n = self.length
+        out = []
+        for fn in (lib().q3o_ctx_k, lib().q3o_ctx_v):
+            p = fn(self.h, layer)
+            a = np.ctypeslib.as_array(p, shape=(int(np.prod(shape)),)).reshape(shape)
+            out.append(np.array(a[:, :n, :], copy=True))
+        return out[0], out[1]
 
     def fill(self, k, v):
         k, v = _f32(k), _f32(v)

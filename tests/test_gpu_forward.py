@@ -250,7 +250,7 @@ def test_long_context_chunk_of_rows(device, q3h, q3o, synth, L, kv16, rows):
         assert rel(s, octx.forward(x)) < tol
         # the rows' layer outputs, each row over its own length
         x = synth.prompt(81, rows)
-        _, normed, lo = ctx.forward_probe(x)
+        _, normed, lo, _ = ctx.forward_probe(x)
         onormed, olo = octx.forward(x, layer_out=True)
         for l in range(dims["layers"]):
             assert rel(lo[l], olo[l]) < tol, (l, rel(lo[l], olo[l]))

@@ -122,6 +122,28 @@ def test_frame_graph_equals_eager(full, synth):
     b.destroy()
 
 
+def test_frame_graph_equals_eager_split_attention(full, synth):
+    """Past 256 positions the talker's attention runs as splits whose count
+    follows the captured cover: a frame launched directly must take the same
+    cover, so graph replay and direct launches give the same bits."""
+    m = full
+    pre = synth.prompt(19, 300)
+    a = m.frame(use_graph=True, max_positions=512)
+    b = m.frame(use_graph=False, max_positions=512)
+    a.start(0, pre)
+    b.start(0, pre)
+    for i in range(4):
+        ca, _ = a.step()
+        cb, _ = b.step()
+        assert np.array_equal(ca, cb), i
+        la, pa = a.state(0)
+        lb, pb = b.state(0)
+        assert np.array_equal(la, lb), i
+        assert np.array_equal(pa, pb), i
+    a.destroy()
+    b.destroy()
+
+
 @pytest.fixture(scope="module")
 def small(device):
     m = Model(device, seed=3, talker_layers=4, cp_layers=2, norm_std=0.1, max_positions=128)

@@ -183,3 +183,77 @@ def test_int8_frame_32_streams_long_prompts(device, synth):
         for of in ofs:
             of.destroy()
         m.destroy()
+
+
+@pytest.fixture(scope="module")
+def small8h(device):
+    """The int8 path with half-float K/V caches (the reference's KvF16,
+    lm.pas:120-123, 352, which applies to any stack)."""
+    m = Model(device, seed=21, talker_layers=4, cp_layers=2, act_q8=1, kv_f16=1, norm_std=0.1,
+              max_positions=300)
+    yield m
+    m.destroy()
+
+
+def test_int8_f16_cache_prefill_then_decode(small8h, q3h, q3o, synth):
+    """int8 products with an f16 cache: a 40-row prefill, then single-row
+    decode steps with the head; logits and states bit-exact against the
+    oracle with the same cache precision, and the cache itself equal."""
+    m = small8h
+    ctx, octx = q3h.Context(m.ts, 64), q3o.Ctx(m.ot, 64)
+    try:
+        x = synth.prompt(31, 40)
+        for step in range(8):
+            print(f"int8 f16-cache step {step} rows {x.shape[0]}", flush=True)
+            lg, st = ctx.forward(x, head=0)
+            ost = octx.forward(x)
+            olg = m.ot.head(m.th, ost)
+            assert np.array_equal(lg, olg) and np.array_equal(st, ost), (
+                step, rel(lg, olg), rel(st, ost))
+            x = m.codec_emb[int(np.argmax(olg[:2048]))][None]
+        for layer in range(m.tdims["layers"]):
+            k, v = ctx.read_kv(layer)
+            ok, ov = octx.read_kv(layer)
+            assert np.array_equal(k, ok) and np.array_equal(v, ov), layer
+            # the values are half floats
+            assert np.array_equal(k, k.astype(np.float16).astype(np.float32))
+    finally:
+        ctx.destroy()
+        octx.destroy()
+
+
+def test_int8_f16_cache_frame_32_streams_past_256(small8h, synth):
+    """The batched frame step on int8 stacks with f16 caches: 32 streams with
+    prompt lengths uniform in [16, 256] (one raised to 252), 10 frames, so
+    that contexts pass 256 positions; codes, logits and states bit-exact
+    against the oracle."""
+    m = small8h
+    rng = np.random.Generator(np.random.PCG64(3))
+    lens = rng.integers(16, 257, size=32)
+    lens[7] = 252
+    frames = 10
+    assert lens.max() + frames > 256
+    fr = m.frame(n_streams=32, max_positions=300, max_frames=16)
+    ofs = []
+    try:
+        for s, L in enumerate(lens):
+            pre = synth.prompt(1100 + s, int(L))
+            fr.start(s, pre)
+            of = m.oracle_frame(max_positions=300)
+            of.start(pre)
+            ofs.append(of)
+        for i in range(frames):
+            codes, alive = fr.step()
+            print(f"f16 cache frame {i}: longest context {int(lens.max()) + i + 1}", flush=True)
+            for s, of in enumerate(ofs):
+                ref = of.next()
+                assert alive[s] == 1
+                assert np.array_equal(codes[s], ref), (i, s, codes[s], ref)
+                lg, past = fr.state(s)
+                olg, opast = of.state()
+                assert np.array_equal(lg, olg) and np.array_equal(past, opast), (
+                    i, s, rel(lg, olg))
+    finally:
+        fr.destroy()
+        for of in ofs:
+            of.destroy()

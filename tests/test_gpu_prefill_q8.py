@@ -34,7 +34,7 @@ def test_q8_prefill_layers_match_the_oracle(device, chunks):
     try:
         for i, rows in enumerate(chunks):
             x = synth.prompt(700 + i, rows)
-            _, normed, lo = ctx.forward_probe(x)
+            _, normed, lo, _ = ctx.forward_probe(x)
             onormed, olo = oc.forward(x, layer_out=True)
             for l in range(dims["layers"]):
                 r = rel(lo[l], olo[l])
@@ -64,7 +64,7 @@ def test_q8_prefill_other_slice_counts(device):
     try:
         for i, rows in enumerate((24, 40, 8)):
             x = synth.prompt(710 + i, rows)
-            _, normed, lo = ctx.forward_probe(x)
+            _, normed, lo, _ = ctx.forward_probe(x)
             onormed, olo = oc.forward(x, layer_out=True)
             for l in range(dims["layers"]):
                 assert rel(lo[l], olo[l]) < 1e-3, (rows, l, rel(lo[l], olo[l]))

@@ -1,9 +1,10 @@
-"""q3h_forward_embeds_probe: the raw output of every layer, as TQwenLm's
-probe reports them to the reference's tests (TOnQwenProbe, lm.pas:139-142,
-380-389; compared layer by layer in tests/test.tts.qwen.lm.pas:211-249).
-Here: the f32 stack's layers against the transformers goldens at 1e-4, the
-Q8_0 and int8 stacks' layers against the oracle's (1e-3; bit for bit on the
-int8 path), and the probed call's outputs equal to the plain call's."""
+"""q3h_forward_embeds_probe: the raw output of every layer and the final-normed
+state of every row, as TQwenLm's probe reports them to the reference's tests
+(TOnQwenProbe, lm.pas:139-142, 380-389: name.layerN and name.out; compared
+layer by layer in tests/test.tts.qwen.lm.pas:211-249). Here: the f32 stack's
+layers and normed rows against the transformers goldens at 1e-4, the Q8_0 and
+int8 stacks' against the oracle's (1e-3; bit for bit on the int8 path), and
+the probed call's outputs equal to the plain call's."""
 import os
 
 import numpy as np
@@ -33,10 +34,13 @@ def test_probe_layers_match_transformers(device, name):
     try:
         pos = 0
         for rows in g["schedule"].tolist():
-            _, normed, lo = ctx.forward_probe(g["x"][pos:pos + rows])
+            _, normed, lo, nr = ctx.forward_probe(g["x"][pos:pos + rows])
             for l in range(L - 1):  # the goldens keep every layer's output but the last
                 want = g["raw"][l][pos:pos + rows]
                 assert rel(lo[l], want) < 1e-4, (pos, l, rel(lo[l], want))
+            # the final-normed state of every row (the probe's name.out)
+            assert rel(nr, g["normed"][pos:pos + rows]) < 1e-4, (pos, rel(nr, g["normed"][pos:pos + rows]))
+            assert rel(nr[-1], normed) < 1e-6
             pos += rows
             assert rel(normed, g["normed"][pos - 1]) < 1e-4
     finally:
@@ -58,7 +62,7 @@ def test_probe_layers_match_the_oracle(device, act_q8):
     try:
         for i, rows in enumerate((20, 1, 1)):
             x = synth.prompt(600 + i, rows)
-            lg, normed, lo = a.forward_probe(x, head=0)
+            lg, normed, lo, nr = a.forward_probe(x, head=0)
             lg2, normed2 = b.forward(x, head=0)
             assert np.array_equal(lg, lg2) and np.array_equal(normed, normed2)  # probing changes nothing
             onormed, olo = oc.forward(x, layer_out=True)
@@ -67,6 +71,13 @@ def test_probe_layers_match_the_oracle(device, act_q8):
                     assert np.array_equal(lo[l], olo[l]), (i, l)
                 else:
                     assert rel(lo[l], olo[l]) < 1e-3, (i, l, rel(lo[l], olo[l]))
+            onr = q3o.rmsnorm_rows(olo[-1], final)
+            assert nr.shape == (rows, dims["hidden"])
+            if act_q8:
+                assert np.array_equal(nr, onr), i
+            else:
+                assert rel(nr, onr) < 1e-3, (i, rel(nr, onr))
+            assert rel(nr[-1], normed) < 1e-6
     finally:
         for c in (a, b, oc):
             c.destroy()

@@ -9,7 +9,8 @@
 - Q8_0 activations (int8 products) stay within the quantization noise, and
   turn fp32-level input differences into much larger output differences (the
   reason the GPU int8 path is checked bit for bit).
-- fp16 K/V cache stays close to the f32 cache.
+- fp16 K/V cache stays close to the f32 cache, and stores exactly the half-float
+  rounding of each layer's f32 keys and values.
 """
 import os
 
@@ -51,6 +52,10 @@ def test_f32_stack_matches_transformers(q3o, synth, name):
         allnormed = rmsnorm(lo[-1], final)
         assert rel(allnormed, g["normed"][pos:pos + rows]) < 2e-5
         assert rel(normed, g["normed"][pos + rows - 1]) < 2e-5
+        # the oracle's final norm of every row (the probe's name.out)
+        onormed = q3o.rmsnorm_rows(lo[-1], final)
+        assert rel(onormed, g["normed"][pos:pos + rows]) < 2e-5
+        assert np.array_equal(onormed[-1], normed)
         pos += rows
     assert ctx.length == pos
     ctx.destroy()
@@ -152,6 +157,40 @@ def test_kv_f16_close_to_f32(q3o, synth):
     assert 0 < rel(nb, na) < 1e-2
     for o in (a, b, s0, s1):
         o.destroy()
+
+
+@pytest.mark.parametrize("dtype,act_q8", [(0, 0), (1, 0), (1, 1)])
+def test_kv_f16_cache_is_the_rounded_f32_cache(q3o, synth, dtype, act_q8):
+    """The half-float cache (KvF16, lm.pas:120-123, 352) stores exactly the
+    IEEE round-to-nearest-even half of the key and of the value an f32 cache
+    would store, for every layer, K and V each on their own. Layer l's keys
+    and values depend only on layer l's input rows, so a one-layer stack of
+    layer l's weights with an f32 cache, fed the half-cache stack's own
+    layer l - 1 outputs in the same calls, computes the unrounded values; a
+    cache that rounded only K or only V, or rounded nothing, fails here."""
+    dims, L, f, s16 = small_stack(synth, q3o, 18, dtype, act_q8=act_q8, kv_f16=1)
+    x = synth.prompt(18, 11, dims["hidden"])
+    c16 = q3o.Ctx(s16, 16)
+    lo = np.concatenate([c16.forward(x[:7], layer_out=True)[1],
+                         c16.forward(x[7:], layer_out=True)[1]], axis=1)
+    for l in range(dims["layers"]):
+        d1 = dict(dims, layers=1)
+        s1 = q3o.Stack(d1, [L[l]], f, dtype, kv_f16=0, act_q8=act_q8)
+        c1 = q3o.Ctx(s1, 16)
+        rows = x if l == 0 else lo[l - 1]
+        c1.forward(rows[:7])
+        c1.forward(rows[7:])
+        k32, v32 = c1.read_kv(0)
+        k16, v16 = c16.read_kv(l)
+        assert k16.shape == k32.shape == (dims["kv_heads"], 11, dims["head_dim"])
+        for got, full, name in ((k16, k32, "k"), (v16, v32, "v")):
+            want = full.astype(np.float16).astype(np.float32)
+            assert np.array_equal(got, want), (l, name)
+            assert not np.array_equal(got, full), (l, name)  # the rounding happened
+        c1.destroy()
+        s1.destroy()
+    c16.destroy()
+    s16.destroy()
 
 
 def test_context_overflow_is_refused(q3o, synth):

@@ -66,6 +66,64 @@ def test_noalloc_equals_forward(device, name):
         st.destroy()
 
 
+def test_noalloc_long_context_equals_forward(device):
+    """Past 256 positions: one decode row (the attention splits merged in the
+    o_proj product), 3 rows (the splits merged into the attention output) and
+    a 16-row chunk (causal prefill attention, no split partials), each equal
+    bit for bit to q3h_forward_embeds on a context with the same cache."""
+    print("noalloc long context", flush=True)
+    dims = dict(synth.TALKER, layers=2)
+    layers, final = synth.stack_weights(25, "talker.model.", dims, norm_std=0.1,
+                                        quantize=q3o.quantize_q8_0)
+    st = q3h.Stack(device, dict(dims, dtype=q3h.Q8_0, kv_f16=0, act_q8=0, max_positions=1024),
+                   layers, final, q3h.Q8_0)
+    st.add_head(q3o.quantize_q8_0(synth.talker_head(25)), q3h.Q8_0)
+    a, b = q3h.Context(st, 1024), q3h.Context(st, 1024)
+    try:
+        pre = synth.prompt(530, 600)
+        a.forward(pre, head=-1, want_normed=False)
+        b.forward(pre, head=-1, want_normed=False)
+        for i, rows in enumerate((1, 3, 16, 1)):
+            x = synth.prompt(540 + i, rows)
+            la, na = a.forward(x, head=0)
+            lb, nb = b.forward(x, head=0, noalloc=True)
+            assert np.array_equal(la, lb) and np.array_equal(na, nb), (i, rows)
+            assert a.length == b.length
+    finally:
+        a.destroy()
+        b.destroy()
+        st.destroy()
+
+
+def test_noalloc_scratch_overflow(device):
+    """15 rows over 16,384 cached positions need about 21 MB of attention
+    partials, more than the scratch array holds: Q3H_E_CAPACITY, the context
+    unchanged, and the next call that fits still works."""
+    print("noalloc overflow", flush=True)
+    dims = dict(synth.TALKER, layers=1)
+    layers, final = synth.stack_weights(26, "talker.model.", dims)
+    L = 16384
+    st = q3h.Stack(device, dict(dims, dtype=q3h.Q8_0, kv_f16=0, act_q8=0, max_positions=L + 64),
+                   layers, final, q3h.F32)
+    c = q3h.Context(st, L + 64)
+    try:
+        rng = np.random.Generator(np.random.PCG64(26))
+        k = rng.standard_normal((1, dims["kv_heads"], L, dims["head_dim"]), dtype=np.float32)
+        v = rng.standard_normal((1, dims["kv_heads"], L, dims["head_dim"]), dtype=np.float32)
+        c.fill_kv(k, v)
+        del k, v
+        assert c.length == L
+        with pytest.raises(q3h.Q3HError) as e:
+            c.forward(synth.prompt(550, 15), noalloc=True)
+        assert e.value.code == q3h.E_CAPACITY and "scratch array" in str(e.value)
+        assert c.length == L
+        _, n1 = c.forward(synth.prompt(551, 16), noalloc=True)  # prefill attention: fits
+        assert c.length == L + 16 and np.isfinite(n1).all()
+    finally:
+        c.destroy()
+        st.destroy()
+
+
 def test_noalloc_limits(device):
     dims = dict(synth.TALKER, layers=1)
     layers, final = synth.stack_weights(24, "talker.model.", dims)
