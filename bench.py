@@ -33,6 +33,9 @@ Beside it:
   f32_b8 (frame_b1)  f32 weights at batch 8: 8 x 512-row prefills, then 64
                 frames of f32 products, with the oracle's f32 frame step as
                 its CPU baseline and stream 0's codes against it;
+  decode_attention_b1 (frame_b1)  the frame's talker decode attention at
+                batch 1 (f32 K/V) at 64, 126, 192 and 256 positions: us per
+                layer and GB/s;
   long_context_attention (frame_b1)  the talker with an f16 K/V cache
                 prefilled to 2048 / 4096 / 8192 positions: 32 decode steps
                 each, and the decode attention kernels' GB/s;
@@ -147,14 +150,30 @@ def prompts(seed, workload, n, rows=PROMPT_ROWS):
     return [synth.prompt(seed + 1000 + s, int(L)) for s, L in enumerate(lens)]
 
 
-def run_gpu(frame, pre, steps, warmup):
-    for s, p in enumerate(pre):
-        frame.start(s, p)
-    for _ in range(warmup):
-        frame.step()
+def start_all(frame, pre):
+    """Start every stream: one stream with q3h_frame_start, several with
+    q3h_frame_start_batch (their prefills overlapping on the device)."""
+    if len(pre) == 1:
+        frame.start(0, pre[0])
+    else:
+        frame.start_batch(list(range(len(pre))), pre)
+
+
+def start_one_by_one(frame, pre):
+    """Seconds of one q3h_frame_start per stream, each waited for (the
+    reference's way: one sentence at a time)."""
     t0 = time.perf_counter()
     for s, p in enumerate(pre):
         frame.start(s, p)
+    return time.perf_counter() - t0
+
+
+def run_gpu(frame, pre, steps, warmup):
+    start_all(frame, pre)
+    for _ in range(warmup):
+        frame.step()
+    t0 = time.perf_counter()
+    start_all(frame, pre)
     run_gpu.prefill_s = time.perf_counter() - t0
     lat = np.empty(steps)
     codes = []
@@ -370,6 +389,8 @@ def batched_b32(dev, f32, tables, args):
                       use_graph=not args.no_graph)
     log(f"batched b32: int8 stacks on the device in {time.time() - t0:.1f} s")
     total, lat, codes = run_gpu(frame, pre, steps, warmup)
+    prefill_s = run_gpu.prefill_s
+    seq_s = start_one_by_one(frame, pre)
     fps = n * steps / total
     # positions read per step, averaged over the steps (the row's own included)
     positions = float(np.mean([np.sum(lens + i + 1) for i in range(steps)]))
@@ -379,12 +400,15 @@ def batched_b32(dev, f32, tables, args):
                ms_per_step=round(1e3 * total / steps, 4),
                step_us_p50=round(1e6 * float(np.median(lat)), 1),
                step_us_p99=round(1e6 * float(np.percentile(lat, 99)), 1),
-               prefill_ms=round(1e3 * run_gpu.prefill_s, 2),
+               prefill_ms=round(1e3 * prefill_s, 2),
+               prefill="32 streams started together (q3h_frame_start_batch)",
+               prefill_one_by_one_ms=round(1e3 * seq_s, 2),
                prompt_rows="U[16,256] (seeded)", activations="q8_0 (int8 MFMA)", kv=kv,
                hbm_bytes_per_step=int(step_bytes), hbm_gbs=round(gbs, 1),
                hbm_frac=round(gbs / HBM_PEAK_GBS, 4))
     log(f"batched b32: {fps:.1f} frames/s, {1e3 * total / steps:.3f} ms per step, "
-        f"{gbs:.0f} GB/s algorithmic")
+        f"{gbs:.0f} GB/s algorithmic; prefill {1e3 * prefill_s:.1f} ms ({1e3 * seq_s:.1f} ms "
+        "one by one)")
     frame.destroy()
     ts.destroy()
     cs.destroy()
@@ -425,6 +449,8 @@ def f32_batch8(dev, f32, tables, args):
     log(f"f32 b8: f32 stacks on the device in {time.time() - t0:.1f} s "
         f"({(ts.bytes + cs.bytes) / 1e9:.2f} GB of layers)")
     total, lat, codes = run_gpu(frame, pre, steps, warmup)
+    prefill_s = run_gpu.prefill_s
+    seq_s = start_one_by_one(frame, pre)
     fps = n * steps / total
     positions = float(np.mean([n * (F32_PROMPT_ROWS + i + 1) for i in range(steps)]))
     step_bytes = F32_FRAME_WEIGHT_BYTES + KV_BYTES_PER_POSITION["f32"] * positions
@@ -433,13 +459,16 @@ def f32_batch8(dev, f32, tables, args):
                ms_per_step=round(1e3 * total / steps, 4),
                step_us_p50=round(1e6 * float(np.median(lat)), 1),
                step_us_p99=round(1e6 * float(np.percentile(lat, 99)), 1),
-               prefill_ms=round(1e3 * run_gpu.prefill_s, 2),
-               prefill="8 streams x 512 prompt rows, one q3h_frame_start each (timed together)",
+               prefill_ms=round(1e3 * prefill_s, 2),
+               prefill="8 streams x 512 prompt rows started together (q3h_frame_start_batch: "
+                       "the prefills overlap on the device)",
+               prefill_one_by_one_ms=round(1e3 * seq_s, 2),
                prompt_rows=F32_PROMPT_ROWS, weights="f32", activations="f32", kv="f32",
                hbm_bytes_per_step=int(step_bytes), hbm_gbs=round(gbs, 1),
                hbm_frac=round(gbs / HBM_PEAK_GBS, 4))
     log(f"f32 b8: {fps:.1f} frames/s, {1e3 * total / steps:.3f} ms per step, prefill of 8 x "
-        f"512 rows {1e3 * run_gpu.prefill_s:.1f} ms, {gbs:.0f} GB/s algorithmic")
+        f"512 rows {1e3 * prefill_s:.1f} ms ({1e3 * seq_s:.1f} ms one by one), {gbs:.0f} GB/s "
+        "algorithmic")
     frame.destroy()
     ts.destroy()
     cs.destroy()
@@ -559,6 +588,42 @@ def long_context_attention(dev, f32, tables, seed, steps=32, iters=10):
     log(f"long-context attention in {time.time() - t0:.1f} s")
     return dict(kernel="k_attn_split + k_attn_merge (f16 K/V, talker decode, per layer)",
                 kv="f16", steps_per_length=steps, results=out)
+
+
+SHORT_LENGTHS = (64, 126, 192, 256)
+
+
+def short_context_attention(dev, f32, seed, iters=20):
+    """The frame's talker decode attention at batch 1 (Q8_0 talker, f32 K/V,
+    the frame's cache type) with the cache filled to 63, 125, 191 and 255
+    positions (N(0,1) values from a seed), so that the new row is position 64,
+    126 (the 156-frame pass's average context), 192 and 256: the attention
+    kernel of the 28 layers launched directly iters times between two events
+    on its stream (gaps included); algorithmic bytes = the f32 K/V of every
+    cached position read once (8 kv heads x 128 dims x 2 x 4 B = 8 KB per
+    position and layer) + the new key and value, the q / k / v row and the
+    output."""
+    cap = max(SHORT_LENGTHS) + 8
+    ts = q3h.Stack(dev, dict(synth.TALKER, dtype=q3h.Q8_0, kv_f16=0, act_q8=0,
+                             max_positions=cap), f32["tl"], f32["tf"], q3h.F32)
+    rng = np.random.Generator(np.random.PCG64(seed + 78))
+    shape = (synth.TALKER["layers"], synth.TALKER["kv_heads"])
+    out = []
+    for L in SHORT_LENGTHS:
+        k = rng.standard_normal(shape + (L - 1, 128), dtype=np.float32)
+        v = rng.standard_normal(shape + (L - 1, 128), dtype=np.float32)
+        ctx = q3h.Context(ts, cap)
+        ctx.fill_kv(k, v)
+        us, nbytes = ctx.time_attention(iters=iters)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out.append(dict(positions=L, attention_us_per_layer=round(us, 3),
+                        attention_bytes_per_layer=int(nbytes), attention_gbs=round(gbs, 1),
+                        frac=round(gbs / HBM_PEAK_GBS, 4)))
+        log(f"short context {L}: attention {us:.2f} us/layer ({gbs:.0f} GB/s)")
+        ctx.destroy()
+    ts.destroy()
+    return dict(kernel="k_attn_short (f32 K/V, talker decode at batch 1, per layer)", kv="f32",
+                results=out)
 
 
 def codec_macs_per_frame():
@@ -768,6 +833,9 @@ def main():
                          "replay, 2 events attached to each launch")
     ap.add_argument("--long-attn-only", action="store_true",
                     help="only the long-context attention measurement (profiling runs)")
+    ap.add_argument("--short-attn-only", action="store_true",
+                    help="only the batch-1 talker decode attention at 64-256 positions "
+                         "(profiling runs)")
     ap.add_argument("--prompt-rows", type=int, default=PROMPT_ROWS,
                     help="frame_b1: prompt rows of the prefill (profiling the prefill products "
                          "at other sizes; the measured workload is 48)")
@@ -786,6 +854,16 @@ def main():
             raise RuntimeError("no gfx950 device")
         dev = q3h.Device(0)
         print(json.dumps({"codec_back": codec_back(dev, args.seed, cpu=False)}), flush=True)
+        dev.close()
+        return 0
+    if args.short_attn_only:
+        if not q3h.available():
+            raise RuntimeError("no gfx950 device")
+        dev = q3h.Device(0)
+        tl, tf = synth.stack_weights(args.seed, "talker.model.", synth.TALKER)
+        print(json.dumps({"decode_attention_b1":
+                          short_context_attention(dev, dict(tl=tl, tf=tf), args.seed)}),
+              flush=True)
         dev.close()
         return 0
     if args.long_attn_only:
@@ -879,7 +957,9 @@ def main():
     if b1 and not args.no_codec:
         codec = codec_back(dev, args.seed, cpu=not args.no_cpu)
     long_attn = None
+    short_attn = None
     if b1 and not args.no_long_attn:
+        short_attn = short_context_attention(dev, f32, args.seed)
         long_attn = long_context_attention(dev, f32, tables, args.seed)
 
     cpu = None
@@ -927,6 +1007,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "parity": parity,
+        "decode_attention_b1": short_attn,
         "long_context_attention": long_attn,
         "start_from_text": text_start,
         "sampled": sampled,

@@ -224,6 +224,17 @@ int q3h_frame_create(q3h_stack *talker, q3h_stack *cp, const q3h_frame_config *c
    [trailing_rows][hidden] (talker.pas:578-580) follows the frames */
 int q3h_frame_start(q3h_frame *f, int stream, const float *prefill, int rows,
                     const float *trailing, int trailing_rows);
+/* no reference counterpart (batched serving; the reference starts one
+   sentence at a time): q3h_frame_start for n distinct streams at once, each
+   prefill on its stream's own talker context and HIP stream so that the
+   prefills overlap on the device; blocks until all are done. streams [n];
+   prefill[i] [rows[i]][hidden]; trailing (nullable) and trailing_rows
+   (nullable: none) as q3h_frame_start's per stream. The results equal n
+   calls of q3h_frame_start. Every argument is checked before any prefill is
+   enqueued (a bad or repeated stream: Q3H_E_ARG, nothing started). */
+int q3h_frame_start_batch(q3h_frame *f, int n, const int *streams,
+                          const float *const *prefill, const int *rows,
+                          const float *const *trailing, const int *trailing_rows);
 /* one NextFrame for every started stream: codes [n_streams][groups] (-1 for a
    stream that has ended); alive [n_streams] (nullable) 1 while a stream runs,
    0 once its code 0 was eos. */

@@ -106,7 +106,11 @@ __global__ __launch_bounds__(NTS) void k_attn_short(const RowDesc *__restrict__ 
   __shared__ float red[2][NWV];
   __shared__ float po[NWV][HD];
   const int heads = GRP * kvh, ldq = (heads + 2 * kvh) * HD;
-  const int h = blockIdx.x, m = blockIdx.y, g = h / GRP;
+  // workgroup x takes query head GRP (x % kvh) + x / kvh: the GRP heads of kv
+  // head g are workgroups g, g + kvh, ..., which the dispatcher deals to one
+  // XCD when kvh is a multiple of 8, so the group's second read of the cache
+  // is served by that XCD's L2
+  const int g = blockIdx.x % kvh, h = g * GRP + blockIdx.x / kvh, m = blockIdx.y;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int r16 = t & 15, pg = t >> 4;
   const float *row = qkv + (size_t)m * ldq;
@@ -837,7 +841,10 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const RowDesc *__restrict_
   __shared__ float os[4][8][4][64];
   // the tiles with the most keys first (the last query rows): the light ones
   // fill the CUs at the end instead of the heavy ones running alone
-  const int h = blockIdx.x, q0 = (gridDim.y - 1 - blockIdx.y) * 16, g = h / GRP;
+  // query head GRP (x % kvh) + x / kvh: a kv head's query heads on one XCD
+  // (kvh a multiple of 8), sharing its L2
+  const int g = blockIdx.x % kvh, h = g * GRP + blockIdx.x / kvh;
+  const int q0 = (gridDim.y - 1 - blockIdx.y) * 16;
   const int heads = GRP * kvh;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int r16 = lane & 15, gq = lane >> 4;

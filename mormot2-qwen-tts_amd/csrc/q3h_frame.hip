@@ -802,21 +802,34 @@ extern "C" int q3h_frame_create(q3h_stack *talker, q3h_stack *cp, const q3h_fram
 
 namespace {
 
-// The talker part of TQwenTalker.Start (talker.pas:586-593) for stream
-// `stream`: reset, fill(prefill, trailing, st) writes the rows prefill
-// [rows][H] (the talker work buffer) and trailing [trailing_rows][H] (the
-// stream's trailing rows) on stream st, then the prefill runs and the
-// stream's state is reset.
-template <class Fill>
-void start_stream(q3h_frame *f, int stream, int rows, int trailing_rows, Fill &&fill) {
+// The host values a start copies to the device: kept until the start's
+// stream has been synchronized.
+struct StartVals {
+  uint64_t seed = 0;
+  int32_t zero = 0, one = 1, trailing_rows = 0;
+};
+
+// the checks of a start of stream `stream` with rows prefill rows
+void start_checks(const q3h_frame *f, int stream, int rows, int trailing_rows) {
   const q3h_frame_config &c = f->cfg;
   require(stream >= 0 && stream < c.n_streams, Q3H_E_ARG, "q3h_frame_start: bad stream");
   require(rows > 0, Q3H_E_ARG, "q3h_frame_start: empty prefill");
   require(trailing_rows >= 0 && trailing_rows <= c.max_frames, Q3H_E_ARG,
           "q3h_frame_start: more trailing rows than max_frames");
   require(rows <= c.max_positions, Q3H_E_CAPACITY, "q3h_frame_start: prefill too long");
-  check_hip(hipSetDevice(f->talker->dev->ordinal), "hipSetDevice");
-  sync_slices(f);
+}
+
+// The talker part of TQwenTalker.Start (talker.pas:586-593) for stream
+// `stream`, enqueued on its talker context's own HIP stream (the device is
+// current, the slices synchronized, the arguments checked): reset, fill
+// (prefill, trailing, st) writes the rows prefill [rows][H] (the context's
+// work buffer) and trailing [trailing_rows][H] (the stream's trailing rows)
+// on stream st, then the prefill runs and the stream's state is reset from
+// sv. start_finish completes it.
+template <class Fill>
+void start_enqueue(q3h_frame *f, int stream, int rows, int trailing_rows, StartVals &sv,
+                   Fill &&fill) {
+  const q3h_frame_config &c = f->cfg;
   q3h_context *tc = f->tctx[stream];
   set_len(tc, 0, tc->stream);
   // the prefill through the single-context path, outputs kept on the device
@@ -836,23 +849,38 @@ void start_stream(q3h_frame *f, int stream, int rows, int trailing_rows, Fill &&
          d.logits + (size_t)stream * c.vocab, c.vocab, EPI_STORE, past, st);
   launch_advance(tc->dev_arr, nullptr, 1, rows, st);
   check_hip(hipGetLastError(), "prefill kernels");
-  const int zero = 0, one = 1;
   // the sentence seed: the one of the settings, or a fresh one (Random64 shr 1)
-  const uint64_t seed = f->sampling.seed ? f->sampling.seed : (f->seed_rng() >> 1);
-  check_hip(hipMemcpyAsync(const_cast<uint64_t *>(d.seeds) + stream, &seed, 8,
+  sv.seed = f->sampling.seed ? f->sampling.seed : (f->seed_rng() >> 1);
+  sv.trailing_rows = trailing_rows;
+  check_hip(hipMemcpyAsync(const_cast<uint64_t *>(d.seeds) + stream, &sv.seed, 8,
                            hipMemcpyHostToDevice, st),
             "seed");
   check_hip(hipMemsetAsync(d.seen + (size_t)stream * c.vocab, 0, c.vocab, st), "reset seen");
-  check_hip(hipMemcpyAsync(d.nframes + stream, &zero, 4, hipMemcpyHostToDevice, st), "state");
-  check_hip(hipMemcpyAsync(d.step + stream, &zero, 4, hipMemcpyHostToDevice, st), "state");
-  check_hip(hipMemcpyAsync(d.trailing_rows + stream, &trailing_rows, 4, hipMemcpyHostToDevice,
-                           st),
+  check_hip(hipMemcpyAsync(d.nframes + stream, &sv.zero, 4, hipMemcpyHostToDevice, st), "state");
+  check_hip(hipMemcpyAsync(d.step + stream, &sv.zero, 4, hipMemcpyHostToDevice, st), "state");
+  check_hip(hipMemcpyAsync(d.trailing_rows + stream, &sv.trailing_rows, 4,
+                           hipMemcpyHostToDevice, st),
             "state");
-  check_hip(hipMemcpyAsync(d.alive + stream, &one, 4, hipMemcpyHostToDevice, st), "state");
-  check_hip(hipStreamSynchronize(st), "prefill sync");
+  check_hip(hipMemcpyAsync(d.alive + stream, &sv.one, 4, hipMemcpyHostToDevice, st), "state");
+}
+
+// waits for a start_enqueue of stream `stream` and marks the stream started
+void start_finish(q3h_frame *f, int stream, int rows) {
+  q3h_context *tc = f->tctx[stream];
+  check_hip(hipStreamSynchronize(tc->stream), "prefill sync");
   tc->len = rows;
   f->host_len[stream] = rows;
   f->started[stream] = 1;
+}
+
+template <class Fill>
+void start_stream(q3h_frame *f, int stream, int rows, int trailing_rows, Fill &&fill) {
+  start_checks(f, stream, rows, trailing_rows);
+  check_hip(hipSetDevice(f->talker->dev->ordinal), "hipSetDevice");
+  sync_slices(f);
+  StartVals sv;
+  start_enqueue(f, stream, rows, trailing_rows, sv, fill);
+  start_finish(f, stream, rows);
 }
 
 }  // namespace
@@ -903,6 +931,53 @@ extern "C" int q3h_frame_start(q3h_frame *f, int stream, const float *prefill, i
                                  hipMemcpyHostToDevice, st),
                   "upload trailing");
     });
+  });
+}
+
+extern "C" int q3h_frame_start_batch(q3h_frame *f, int n, const int *streams,
+                                     const float *const *prefill, const int *rows,
+                                     const float *const *trailing, const int *trailing_rows) {
+  return guard([&] {
+    require(f != nullptr, Q3H_E_ARG, "q3h_frame_start_batch: NULL frame");
+    require(n > 0 && streams && prefill && rows, Q3H_E_ARG,
+            "q3h_frame_start_batch: invalid argument");
+    // every start checked before any is enqueued
+    std::vector<char> seen(f->cfg.n_streams, 0);
+    for (int i = 0; i < n; i++) {
+      const int tr = trailing_rows ? trailing_rows[i] : 0;
+      start_checks(f, streams[i], rows[i], tr);
+      require(!seen[streams[i]], Q3H_E_ARG, "q3h_frame_start_batch: repeated stream");
+      seen[streams[i]] = 1;
+      require(prefill[i] != nullptr, Q3H_E_ARG, "q3h_frame_start_batch: NULL prefill");
+      require(tr == 0 || (trailing && trailing[i]), Q3H_E_ARG,
+              "q3h_frame_start_batch: trailing is NULL");
+    }
+    check_hip(hipSetDevice(f->talker->dev->ordinal), "hipSetDevice");
+    sync_slices(f);
+    const size_t H = f->H;
+    std::vector<StartVals> sv(n);
+    int enqueued = 0;
+    try {
+      for (int i = 0; i < n; i++) {
+        const int tr = trailing_rows ? trailing_rows[i] : 0;
+        start_enqueue(f, streams[i], rows[i], tr, sv[i],
+                      [&](float *pre, float *trail, hipStream_t st) {
+                        check_hip(hipMemcpyAsync(pre, prefill[i], sizeof(float) * rows[i] * H,
+                                                 hipMemcpyHostToDevice, st),
+                                  "upload prefill");
+                        if (tr > 0)
+                          check_hip(hipMemcpyAsync(trail, trailing[i], sizeof(float) * tr * H,
+                                                   hipMemcpyHostToDevice, st),
+                                    "upload trailing");
+                      });
+        enqueued++;
+      }
+    } catch (...) {
+      // the enqueued starts still read sv: let them end before it goes
+      for (int i = 0; i < enqueued; i++) (void)hipStreamSynchronize(f->tctx[streams[i]]->stream);
+      throw;
+    }
+    for (int i = 0; i < n; i++) start_finish(f, streams[i], rows[i]);
   });
 }
 

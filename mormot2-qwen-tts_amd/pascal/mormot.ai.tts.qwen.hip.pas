@@ -176,6 +176,11 @@ function q3h_frame_create(talker, cp: q3h_stack; cfg: Pq3h_frame_config;
 function q3h_frame_start(f: q3h_frame; stream: integer; prefill: PSingle;
   rows: integer; trailing: PSingle; trailing_rows: integer): integer;
   cdecl; external LIBQ3H;
+/// no counterpart in the reference (batched serving): the starts of n streams
+// at once, their prefills overlapping on the device
+function q3h_frame_start_batch(f: q3h_frame; n: integer; streams: PInteger;
+  prefill: PPSingle; rows: PInteger; trailing: PPSingle;
+  trailing_rows: PInteger): integer; cdecl; external LIBQ3H;
 function q3h_frame_step(f: q3h_frame; codes, alive: PInteger): integer;
   cdecl; external LIBQ3H;
 function q3h_frame_state(f: q3h_frame; stream: integer;

@@ -155,6 +155,9 @@ SIGNATURES = {
     "q3h_frame_create": (_I, [_P, _P, ctypes.POINTER(FrameConfig), _FP,
                               ctypes.POINTER(_FP), _FP, ctypes.POINTER(_P)]),
     "q3h_frame_start": (_I, [_P, _I, _FP, _I, _FP, _I]),
+    "q3h_frame_start_batch": (_I, [_P, _I, ctypes.POINTER(ctypes.c_int),
+                                   ctypes.POINTER(_FP), ctypes.POINTER(ctypes.c_int),
+                                   ctypes.POINTER(_FP), ctypes.POINTER(ctypes.c_int)]),
     "q3h_frame_step": (_I, [_P, _IP, _IP]),
     "q3h_frame_state": (_I, [_P, _I, _FP, _FP]),
     "q3h_frame_destroy": (_I, [_P]),
@@ -554,6 +557,21 @@ class Frame:
         t = _f32(trailing) if trailing is not None and len(trailing) else None
         _check(lib().q3h_frame_start(self.h, stream, _fp(p), p.shape[0], _fp(t),
                                      0 if t is None else t.shape[0]))
+
+    def start_batch(self, streams, prefills, trailings=None):
+        """q3h_frame_start_batch: the starts of several streams at once, their
+        prefills overlapping on the device (prefills[i] [rows][hidden],
+        trailings[i] None or [rows][hidden])."""
+        n = len(streams)
+        ps = [_f32(p) for p in prefills]
+        ts = [None] * n if trailings is None else \
+            [_f32(t) if t is not None and len(t) else None for t in trailings]
+        c_streams = (ctypes.c_int * n)(*[int(x) for x in streams])
+        c_pre = (_FP * n)(*[_fp(p) for p in ps])
+        c_rows = (ctypes.c_int * n)(*[p.shape[0] for p in ps])
+        c_tr = (_FP * n)(*[_fp(t) for t in ts])
+        c_trr = (ctypes.c_int * n)(*[0 if t is None else t.shape[0] for t in ts])
+        _check(lib().q3h_frame_start_batch(self.h, n, c_streams, c_pre, c_rows, c_tr, c_trr))
 
     def set_sampling(self, do_sample=False, temperature=1.0, top_k=0, top_p=1.0,
                      sub_do_sample=False, sub_temperature=1.0, sub_top_k=0, sub_top_p=1.0,

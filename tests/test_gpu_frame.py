@@ -151,6 +151,44 @@ def small(device):
     m.destroy()
 
 
+def test_frame_start_batch_equals_starts(small, synth, q3h):
+    """q3h_frame_start_batch (the prefills of several streams overlapping on
+    the device, in any stream order) leaves the states of one q3h_frame_start
+    per stream, and the frames that follow give the same codes; a repeated
+    stream is refused before anything starts."""
+    m = small
+    lens = [16, 40, 23, 57]
+    pres = [synth.prompt(70 + s, n) for s, n in enumerate(lens)]
+    trs = [None, synth.normal(71, "trailing", (2, 1024), 0.02), None,
+           synth.normal(73, "trailing", (1, 1024), 0.02)]
+    a = m.frame(n_streams=4, max_positions=128)
+    b = m.frame(n_streams=4, max_positions=128)
+    try:
+        for s in range(4):
+            a.start(s, pres[s], trs[s])
+        order = [3, 1, 0, 2]
+        b.start_batch(order, [pres[s] for s in order], [trs[s] for s in order])
+        for s in range(4):
+            la, pa = a.state(s)
+            lb, pb = b.state(s)
+            assert np.array_equal(la, lb) and np.array_equal(pa, pb), s
+        for i in range(3):
+            ca, _ = a.step()
+            cb, _ = b.step()
+            assert np.array_equal(ca, cb), i
+        c = m.frame(n_streams=4, max_positions=128)
+        with pytest.raises(q3h.Q3HError) as e:
+            c.start_batch([0, 0], [pres[0], pres[1]])
+        assert e.value.code == q3h.E_ARG and "repeated" in str(e.value)
+        with pytest.raises(q3h.Q3HError) as e:
+            c.step()
+        assert e.value.code == q3h.E_STATE
+        c.destroy()
+    finally:
+        a.destroy()
+        b.destroy()
+
+
 def test_frame_multi_stream(small, synth):
     m = small
     lens = [16, 40, 23]

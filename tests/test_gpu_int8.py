@@ -151,7 +151,9 @@ def test_int8_frame_32_streams_long_prompts(device, synth):
     layers, code predictor 2, real widths): 32 streams with prompt lengths
     uniform in [16, 256] from the workload's generator, 14 frames, so that
     contexts pass 256 positions (more than one round of the attention's key
-    loop); two slices of 16 streams. Bit-exact against the oracle."""
+    loop); two slices of 16 streams. The streams start together
+    (q3h_frame_start_batch, their prefills overlapping). Bit-exact against the
+    oracle."""
     rng = np.random.Generator(np.random.PCG64(1))
     lens = rng.integers(16, 257, size=32)
     frames = 14
@@ -161,9 +163,9 @@ def test_int8_frame_32_streams_long_prompts(device, synth):
     fr = m.frame(n_streams=32, max_positions=300, max_frames=16)
     ofs = []
     try:
-        for s, L in enumerate(lens):
-            pre = synth.prompt(1000 + s, int(L))
-            fr.start(s, pre)
+        pres = [synth.prompt(1000 + s, int(L)) for s, L in enumerate(lens)]
+        fr.start_batch(list(range(32)), pres)
+        for pre in pres:
             of = m.oracle_frame(max_positions=300)
             of.start(pre)
             ofs.append(of)
