@@ -814,35 +814,70 @@ __device__ __forceinline__ float4 ld4kv(const _Float16 *p) {
   return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
 }
 
+typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
+
+// eight f32 values split into three bf16 parts each (x = hi + mid + lo
+// exactly), each part packed as the 8 bf16 of one matrix-core operand
+__device__ __forceinline__ void split8(const float (&x)[8], u32x4 &h, u32x4 &m, u32x4 &l) {
+  uint32_t hh[8], mm[8], ll[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) split3(x[e], hh[e], mm[e], ll[e]);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    h[i] = hh[2 * i] | (hh[2 * i + 1] << 16);
+    m[i] = mm[2 * i] | (mm[2 * i + 1] << 16);
+    l[i] = ll[2 * i] | (ll[2 * i + 1] << 16);
+  }
+}
+
+// acc += A B for f32 operands given as three bf16 parts each: the six part
+// products of weight at least 2^-16 of the product (mid mid, lo hi, hi lo,
+// mid hi, hi mid, hi hi, smallest first), each exact in fp32; the three
+// dropped weigh below 2^-23 of the product, under its fp32 rounding
+__device__ __forceinline__ v4f mfma_x3(const u32x4 (&a)[3], const u32x4 (&b)[3], v4f acc) {
+  const bf8v ah = __builtin_bit_cast(bf8v, a[0]), am = __builtin_bit_cast(bf8v, a[1]),
+             al = __builtin_bit_cast(bf8v, a[2]);
+  const bf8v bh = __builtin_bit_cast(bf8v, b[0]), bm = __builtin_bit_cast(bf8v, b[1]),
+             bl = __builtin_bit_cast(bf8v, b[2]);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, bm, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, bh, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bm, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+  return acc;
+}
+
 // Prefill attention (rows m = 0 .. M-1 of one context at positions pos0 + m,
 // their keys and values already in the cache, q already normed and rotated):
-// causal softmax(q K^T / sqrt(128)) V on the matrix cores,
-// v_mfma_f32_16x16x4_f32 (fp32 operands and sums).
-// One workgroup of 4 waves per (query head h, tile of 16 query rows); wave w
-// takes the key blocks w, w + 4, ... (16 positions each) up to the tile's
-// last position and keeps its own running maximum, sum and output:
-//   - scores S^T = K Q^T: A = 16 keys, B = the 16 queries (both loaded 16
-//     bytes per lane, columns 4 (l / 16) .. + 3 of each 16-dim step, as the
-//     f32 products do); lane l receives S[query l % 16][key 4 (l / 16) + r];
-//   - online softmax per query (the 16 keys of a block are the 4 registers
-//     of lanes l, l ^ 16, l ^ 32, l ^ 48); keys after the query's position
-//     are masked;
-//   - O += P V: lane l's scores are already P in the A layout (query l % 16,
-//     k slot l / 16 = key 4 (l / 16) + r for k step r), B = V[key][dim]; the
-//     output tile (query 4 (l / 16) + r, dim 16 t + l % 16) is rescaled by
-//     the factor of its query, read from lane 4 (l / 16) + r;
-//   - the 4 waves' (max, sum, output) merged in LDS.
+// causal softmax(q K^T / sqrt(128)) V on the bf16 matrix cores
+// (v_mfma_f32_16x16x32_bf16, lane l holding A[l % 16][8 (l / 16) .. + 7] and
+// B[8 (l / 16) .. + 7][l % 16], receiving D[4 (l / 16) + r][l % 16]) with
+// every f32 operand split exactly into three bf16 parts (mfma_x3): 6 bf16
+// products per 32 dims or keys where f32 operands take 8 v_mfma_f32_16x16x4_f32
+// of twice the cycles each. One workgroup of 4 waves per (query head h, tile of
+// 16 query rows); wave w takes the 32-key blocks w, w + 4, ... up to the
+// tile's last position and keeps its own running maximum, sum and output:
+//   - scores S^T = K Q^T per 16-key half: A = 16 keys, B = the 16 queries, k =
+//     32 dims at a time (4 steps); lane l receives S[query l % 16][key
+//     16 half + 4 (l / 16) + r];
+//   - online softmax per query over the 32 keys (lanes l, l ^ 16, l ^ 32,
+//     l ^ 48 hold a query's keys); keys after the query's position masked;
+//   - O += P V with k = the 32 keys in the order the scores left them in the
+//     lanes: slot 8 (l / 16) + j is key 4 (l / 16) + j (j < 4) of the first
+//     half, 16 + 4 (l / 16) + j - 4 of the second, so lane l's eight scores
+//     are its A operand as they are, and its B operand the values of the same
+//     eight keys in dims 16 t + l % 16;
+//   - the 4 waves' (max, sum, output) merged in LDS; each output element
+//     rescaled to the largest of the waves' maxima.
 template <typename KV, int GRP>
-__global__ __launch_bounds__(256) void k_attn_prefill(const RowDesc *__restrict__ rd,
-                                                      const float *__restrict__ qkv, int ldq,
-                                                      int layer, int kvh, int M,
-                                                      float *__restrict__ outp) {
+__global__ __launch_bounds__(256) void k_attn_prefill_x3(const RowDesc *__restrict__ rd,
+                                                         const float *__restrict__ qkv, int ldq,
+                                                         int layer, int kvh, int M,
+                                                         float *__restrict__ outp) {
   __shared__ float ms[4][16], ls[4][16];
   __shared__ float os[4][8][4][64];
-  // the tiles with the most keys first (the last query rows): the light ones
-  // fill the CUs at the end instead of the heavy ones running alone
-  // query head GRP (x % kvh) + x / kvh: a kv head's query heads on one XCD
-  // (kvh a multiple of 8), sharing its L2
+  // the tiles with the most keys first; a kv head's query heads on one XCD
   const int g = blockIdx.x % kvh, h = g * GRP + blockIdx.x / kvh;
   const int q0 = (gridDim.y - 1 - blockIdx.y) * 16;
   const int heads = GRP * kvh;
@@ -855,53 +890,79 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const RowDesc *__restrict_
   const size_t head_off = ((size_t)layer * kvh + g) * d.max_pos * HD;
   const KV *kc = reinterpret_cast<const KV *>(d.k) + head_off;
   const KV *vc = reinterpret_cast<const KV *>(d.v) + head_off;
-  // this lane's query: row min(q0 + r16, M - 1), dims 16 s + 4 gq .. + 3
-  const float *qr = qkv + (size_t)min(q0 + r16, M - 1) * ldq + h * HD + 4 * gq;
-  float4 qf[8];
+  // this lane's query: row min(q0 + r16, M - 1), dims 32 c + 8 gq .. + 7
+  u32x4 qp[4][3];
+  {
+    const float *qr = qkv + (size_t)min(q0 + r16, M - 1) * ldq + h * HD + 8 * gq;
 #pragma unroll
-  for (int s = 0; s < 8; s++) qf[s] = *reinterpret_cast<const float4 *>(qr + 16 * s);
+    for (int c = 0; c < 4; c++) {
+      const float4 a = *reinterpret_cast<const float4 *>(qr + 32 * c);
+      const float4 b = *reinterpret_cast<const float4 *>(qr + 32 * c + 4);
+      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      split8(x, qp[c][0], qp[c][1], qp[c][2]);
+    }
+  }
   const float scale = (float)(1.0 / sqrt((double)HD));
   float m_run = -INFINITY, l_run = 0.f;
   v4f o[8];
 #pragma unroll
   for (int i = 0; i < 8; i++) o[i] = v4f{0.f, 0.f, 0.f, 0.f};
-  const int nblk = p_hi / 16 + 1;
+  const int nblk = p_hi / 32 + 1;
   for (int b = wave; b < nblk; b += 4) {
-    const int kb = 16 * b;
-    float4 kf[8];
-    const KV *kr = kc + (size_t)min(kb + r16, p_hi) * HD + 4 * gq;
+    const int kb = 32 * b;
+    // keys kb + 16 hf + r16, dims 32 c + 8 gq .. + 7; values of the lane's
+    // eight key slots, dims 16 i + r16
+    float4 kf[2][4][2];
 #pragma unroll
-    for (int s = 0; s < 8; s++) kf[s] = ld4kv(kr + 16 * s);
-    float vv[4][8];
+    for (int hf = 0; hf < 2; hf++) {
+      const KV *kr = kc + (size_t)min(kb + 16 * hf + r16, p_hi) * HD + 8 * gq;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const KV *vr = vc + (size_t)min(kb + 4 * gq + r, p_hi) * HD + r16;
-#pragma unroll
-      for (int i = 0; i < 8; i++) vv[r][i] = (float)vr[16 * i];
+      for (int c = 0; c < 4; c++) {
+        kf[hf][c][0] = ld4kv(kr + 32 * c);
+        kf[hf][c][1] = ld4kv(kr + 32 * c + 4);
+      }
     }
-    v4f sa = v4f{0.f, 0.f, 0.f, 0.f};
+    v4f sa[2];
 #pragma unroll
-    for (int s = 0; s < 8; s++) {
-      sa = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s].x, qf[s].x, sa, 0, 0, 0);
-      sa = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s].y, qf[s].y, sa, 0, 0, 0);
-      sa = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s].z, qf[s].z, sa, 0, 0, 0);
-      sa = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s].w, qf[s].w, sa, 0, 0, 0);
-    }
-    float sc[4], bm = -INFINITY;
+    for (int hf = 0; hf < 2; hf++) {
+      sa[hf] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      sc[r] = kb + 4 * gq + r <= pq ? sa[r] * scale : -INFINITY;
-      bm = fmaxf(bm, sc[r]);
+      for (int c = 0; c < 4; c++) {
+        const float x[8] = {kf[hf][c][0].x, kf[hf][c][0].y, kf[hf][c][0].z, kf[hf][c][0].w,
+                            kf[hf][c][1].x, kf[hf][c][1].y, kf[hf][c][1].z, kf[hf][c][1].w};
+        u32x4 kp[3];
+        split8(x, kp[0], kp[1], kp[2]);
+        sa[hf] = mfma_x3(kp, qp[c], sa[hf]);
+      }
     }
+    // the values, loaded once the keys are consumed (both in flight together
+    // would take the registers of a second wave per SIMD)
+    float vv[8][8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int key = kb + (j < 4 ? 4 * gq + j : 16 + 4 * gq + j - 4);
+      const KV *vr = vc + (size_t)min(key, p_hi) * HD + r16;
+#pragma unroll
+      for (int i = 0; i < 8; i++) vv[i][j] = (float)vr[16 * i];
+    }
+    float p[8], bm = -INFINITY;
+#pragma unroll
+    for (int hf = 0; hf < 2; hf++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float s = kb + 16 * hf + 4 * gq + r <= pq ? sa[hf][r] * scale : -INFINITY;
+        p[4 * hf + r] = s;
+        bm = fmaxf(bm, s);
+      }
     bm = rows4_max(bm);
     const float m_new = fmaxf(m_run, bm);
     const float ref = m_new == -INFINITY ? 0.f : m_new;
     const float alpha = m_run == -INFINITY ? 0.f : __expf(m_run - ref);
     float ps = 0.f;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      sc[r] = __expf(sc[r] - ref);
-      ps += sc[r];
+    for (int j = 0; j < 8; j++) {
+      p[j] = __expf(p[j] - ref);
+      ps += p[j];
     }
     ps = rows4_sum(ps);
     l_run = fmaf(l_run, alpha, ps);
@@ -912,11 +973,14 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const RowDesc *__restrict_
 #pragma unroll
       for (int i = 0; i < 8; i++) o[i][r] *= ar;
     }
+    u32x4 pp[3];
+    split8(p, pp[0], pp[1], pp[2]);
 #pragma unroll
-    for (int i = 0; i < 8; i++)
-#pragma unroll
-      for (int r = 0; r < 4; r++)
-        o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(sc[r], vv[r][i], o[i], 0, 0, 0);
+    for (int i = 0; i < 8; i++) {
+      u32x4 vp[3];
+      split8(vv[i], vp[0], vp[1], vp[2]);
+      o[i] = mfma_x3(pp, vp, o[i]);
+    }
   }
   if (gq == 0) {
     ms[wave][r16] = m_run;
@@ -1116,8 +1180,8 @@ void launch_attn_prefill(const AttnArgs &a, int M, bool kv16, hipStream_t st) {
   const dim3 grid(a.heads, (M + 15) / 16), block(256);
   const int grp = a.heads / a.kvh;
 #define Q3H_P(KV, G)                                                                         \
-  hipLaunchKernelGGL((k_attn_prefill<KV, G>), grid, block, 0, st, a.rd, a.qkv, a.ldq, a.layer, \
-                     a.kvh, M, a.out)
+  hipLaunchKernelGGL((k_attn_prefill_x3<KV, G>), grid, block, 0, st, a.rd, a.qkv, a.ldq,      \
+                     a.layer, a.kvh, M, a.out)
   if (kv16) {
     if (grp == 1) Q3H_P(_Float16, 1);
     else if (grp == 2) Q3H_P(_Float16, 2);
