@@ -14,6 +14,7 @@
 // the prologue; rows that add several positions of one context at once
 // (prefill) run the separate append kernel first and these kernels unfused.
 #include <algorithm>
+#include <type_traits>
 
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
@@ -292,7 +293,11 @@ constexpr int kMaxSplitsLong = 256;
 //     key (k_norm, RoPE) and value to the cache;
 //   - scores: an 8-term chain per lane, summed over the 16 lanes of a DPP
 //     row, one DPP stage at a time over all of the thread's sums;
-//   - softmax per query head over the wave's positions (maximum, exp, sum);
+//   - softmax per query head over the wave's positions, online over the two
+//     halves of the thread's positions (the loads are issued a half at a time,
+//     so the first half's scores, softmax and values run while the second
+//     half streams in): the running maximum, the sum and the output rescaled
+//     when the maximum grows;
 //   - values: 8 dims x GRP heads of partial outputs per lane, summed over the
 //     position groups of a wave (lane shuffles);
 //   - the waves' (maximum, sum, output) meet in LDS, rescaled to the split's
@@ -365,20 +370,27 @@ __global__ __launch_bounds__(NTL) void k_attn_split(const RowDesc *__restrict__ 
   auto position = [&](int j) { return (j * S + s) * PG + pg; };
   const float2 cs = FUSED ? rope_cs[(size_t)pos * (HD / 2) + lane] : make_float2(1.f, 0.f);
 
+  // the loads in two halves, each its keys then its values: loads return in
+  // issue order, so the first half's arithmetic waits for the first half only
+  // and runs while the second half streams in
+  constexpr int J0 = (NJ + 1) / 2;
   u32x4 kr[NJ][LW], vr[NJ][LW];
 #pragma unroll
-  for (int j = 0; j < NJ; j++) {
-    const KV *p = kc + (size_t)min(position(j), last) * HD + 8 * r16;
+  for (int half = 0; half < 2; half++) {
 #pragma unroll
-    for (int e = 0; e < LW; e++) kr[j][e] = gload16(p + e * 4);
+    for (int j = half ? J0 : 0; j < (half ? NJ : J0); j++) {
+      const KV *p = kc + (size_t)min(position(j), last) * HD + 8 * r16;
+#pragma unroll
+      for (int e = 0; e < LW; e++) kr[j][e] = gload16(p + e * 4);
+    }
+#pragma unroll
+    for (int j = half ? J0 : 0; j < (half ? NJ : J0); j++) {
+      const KV *p = vc + (size_t)min(position(j), last) * HD + 8 * r16;
+#pragma unroll
+      for (int e = 0; e < LW; e++) vr[j][e] = gload16(p + e * 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the halves issued in this order
   }
-#pragma unroll
-  for (int j = 0; j < NJ; j++) {
-    const KV *p = vc + (size_t)min(position(j), last) * HD + 8 * r16;
-#pragma unroll
-    for (int e = 0; e < LW; e++) vr[j][e] = gload16(p + e * 4);
-  }
-  __builtin_amdgcn_sched_barrier(0);
 
   const size_t slot = (HD + 2);
   float *pm = part + ((size_t)m * heads + g * GRP) * (S + 1) * slot;  // head h at h (S + 1) slot
@@ -413,73 +425,89 @@ __global__ __launch_bounds__(NTL) void k_attn_split(const RowDesc *__restrict__ 
     }
   }
 
-  // scores
+  // scores, softmax and values in two phases over the halves of the loads,
+  // an online softmax per wave and query head: the running maximum mw
+  // (alike across the wave), and lane partials of the sum (ls) and output (o)
+  // rescaled when the maximum grows
   const float scale = (float)(1.0 / sqrt((double)HD));
-  float sc[GRP][NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; j++) {
-    float k8[8];
-    cvt8(kr[j], k8);
-#pragma unroll
-    for (int h = 0; h < GRP; h++) {
-      float a = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; e++) a = fmaf(q[h][e], k8[e], a);
-      sc[h][j] = a;
-    }
-  }
-#pragma unroll
-  for (int h = 0; h < GRP; h++)
-#pragma unroll
-    for (int j = 0; j < NJ; j++) sc[h][j] += dpp_f<kQuadXor1>(sc[h][j]);
-#pragma unroll
-  for (int h = 0; h < GRP; h++)
-#pragma unroll
-    for (int j = 0; j < NJ; j++) sc[h][j] += dpp_f<kQuadXor2>(sc[h][j]);
-#pragma unroll
-  for (int h = 0; h < GRP; h++)
-#pragma unroll
-    for (int j = 0; j < NJ; j++) sc[h][j] += dpp_f<kHalfMirror>(sc[h][j]);
-#pragma unroll
-  for (int h = 0; h < GRP; h++)
-#pragma unroll
-    for (int j = 0; j < NJ; j++) sc[h][j] += dpp_f<kRowMirror>(sc[h][j]);
-  // softmax over the wave's positions, per query head
-  float mw[GRP], lw[GRP];
+  float mw[GRP], ls[GRP], o[GRP][8];
 #pragma unroll
   for (int h = 0; h < GRP; h++) {
-    float v = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-      sc[h][j] = position(j) < n ? sc[h][j] * scale : -INFINITY;
-      v = fmaxf(v, sc[h][j]);
-    }
-    v = rows4_max(v);  // alike across a 16-lane row: the four rows' maximum
-    mw[h] = v;
-    const float ref = v == -INFINITY ? 0.f : v;  // no position here: weights 0
-    float ls = 0.f;
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-      sc[h][j] = __expf(sc[h][j] - ref);
-      ls += sc[h][j];
-    }
-    lw[h] = rows4_sum(ls);
-  }
-  // values
-  float o[GRP][8];
-#pragma unroll
-  for (int h = 0; h < GRP; h++)
+    mw[h] = -INFINITY;
+    ls[h] = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; e++) o[h][e] = 0.f;
+  }
+  auto phase = [&](auto lo_c, auto hi_c) {
+    constexpr int LO = decltype(lo_c)::value, HI = decltype(hi_c)::value;
+    float sc[GRP][NJ];
 #pragma unroll
-  for (int j = 0; j < NJ; j++) {
-    float v8[8];
-    cvt8(vr[j], v8);
+    for (int j = LO; j < HI; j++) {
+      float k8[8];
+      cvt8(kr[j], k8);
+#pragma unroll
+      for (int h = 0; h < GRP; h++) {
+        float a = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) a = fmaf(q[h][e], k8[e], a);
+        sc[h][j] = a;
+      }
+    }
 #pragma unroll
     for (int h = 0; h < GRP; h++)
 #pragma unroll
-      for (int e = 0; e < 8; e++) o[h][e] = fmaf(sc[h][j], v8[e], o[h][e]);
-  }
+      for (int j = LO; j < HI; j++) sc[h][j] += dpp_f<kQuadXor1>(sc[h][j]);
+#pragma unroll
+    for (int h = 0; h < GRP; h++)
+#pragma unroll
+      for (int j = LO; j < HI; j++) sc[h][j] += dpp_f<kQuadXor2>(sc[h][j]);
+#pragma unroll
+    for (int h = 0; h < GRP; h++)
+#pragma unroll
+      for (int j = LO; j < HI; j++) sc[h][j] += dpp_f<kHalfMirror>(sc[h][j]);
+#pragma unroll
+    for (int h = 0; h < GRP; h++)
+#pragma unroll
+      for (int j = LO; j < HI; j++) sc[h][j] += dpp_f<kRowMirror>(sc[h][j]);
+#pragma unroll
+    for (int h = 0; h < GRP; h++) {
+      float v = -INFINITY;
+#pragma unroll
+      for (int j = LO; j < HI; j++) {
+        sc[h][j] = position(j) < n ? sc[h][j] * scale : -INFINITY;
+        v = fmaxf(v, sc[h][j]);
+      }
+      v = rows4_max(v);  // alike across a 16-lane row: the four rows' maximum
+      const float m_new = fmaxf(mw[h], v);
+      // no position so far: weights 0 whatever the reference
+      const float ref = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = mw[h] == -INFINITY ? 0.f : __expf(mw[h] - ref);
+      mw[h] = m_new;
+      float l = ls[h] * alpha;
+#pragma unroll
+      for (int e = 0; e < 8; e++) o[h][e] *= alpha;
+#pragma unroll
+      for (int j = LO; j < HI; j++) {
+        sc[h][j] = __expf(sc[h][j] - ref);
+        l += sc[h][j];
+      }
+      ls[h] = l;
+    }
+#pragma unroll
+    for (int j = LO; j < HI; j++) {
+      float v8[8];
+      cvt8(vr[j], v8);
+#pragma unroll
+      for (int h = 0; h < GRP; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[h][e] = fmaf(sc[h][j], v8[e], o[h][e]);
+    }
+  };
+  phase(std::integral_constant<int, 0>{}, std::integral_constant<int, J0>{});
+  phase(std::integral_constant<int, J0>{}, std::integral_constant<int, NJ>{});
+  float lw[GRP];
+#pragma unroll
+  for (int h = 0; h < GRP; h++) lw[h] = rows4_sum(ls[h]);
   // the 4 position groups of a wave (lanes l, l + 16, l + 32, l + 48), then
   // the waves through LDS, each rescaled to the split's maximum
 #pragma unroll
