@@ -137,8 +137,8 @@ __global__ __launch_bounds__(NTS) void k_attn_short(const RowDesc *__restrict__ 
   const int n = FUSED ? pos : pos + 1;  // positions read from the cache
   const int last = max(n - 1, 0);
   const size_t head_off = ((size_t)layer * kvh + g) * d.max_pos * HD;
-  KV *kc = reinterpret_cast<KV *>(d.k) + head_off;
-  KV *vc = reinterpret_cast<KV *>(d.v) + head_off;
+  KV *kc = global_ptr(reinterpret_cast<KV *>(d.k)) + head_off;
+  KV *vc = global_ptr(reinterpret_cast<KV *>(d.v)) + head_off;
   const float2 cs =
       FUSED && wave < 2 ? rope_cs[(size_t)pos * (HD / 2) + lane] : make_float2(1.f, 0.f);
   u32x4 kr[NJ][LW], vr[NJ][LW];
@@ -364,8 +364,8 @@ __global__ __launch_bounds__(NTL) void k_attn_split(const RowDesc *__restrict__ 
   const int n = FUSED ? pos : pos + 1;  // positions covered here
   const int last = max(n - 1, 0);
   const size_t head_off = ((size_t)layer * kvh + g) * d.max_pos * HD;
-  KV *kc = reinterpret_cast<KV *>(d.k) + head_off;
-  KV *vc = reinterpret_cast<KV *>(d.v) + head_off;
+  KV *kc = global_ptr(reinterpret_cast<KV *>(d.k)) + head_off;
+  KV *vc = global_ptr(reinterpret_cast<KV *>(d.v)) + head_off;
   // block j of this split: positions (j S + s) PG .. + PG - 1
   auto position = [&](int j) { return (j * S + s) * PG + pg; };
   const float2 cs = FUSED ? rope_cs[(size_t)pos * (HD / 2) + lane] : make_float2(1.f, 0.f);
@@ -593,8 +593,8 @@ __global__ __launch_bounds__(512) void k_attn_merge(const RowDesc *__restrict__ 
   float score = -INFINITY, vn = 0.f;
   if (FUSED) {
     const size_t off = (((size_t)layer * kvh + g) * d.max_pos + d.pos) * HD + dd;
-    const float kn = (float)reinterpret_cast<const KV *>(d.k)[off];
-    vn = (float)reinterpret_cast<const KV *>(d.v)[off];
+    const float kn = (float)global_ptr(reinterpret_cast<const KV *>(d.k))[off];
+    vn = (float)global_ptr(reinterpret_cast<const KV *>(d.v))[off];
     if (q == 0) {  // waves 0 and 1: dims 0-63 and 64-127
       const float v = wave_sum_dpp(qv * kn);
       if (lane == 0) qk[wave] = v;
@@ -739,8 +739,8 @@ __global__ __launch_bounds__(256) void k_attn_merge_o(const int8_t *__restrict__
     float score = -INFINITY, vn[8];
     if (FUSED) {
       const size_t off = (((size_t)layer * kvh + g) * d.max_pos + d.pos) * HD + 8 * j;
-      const KV *kr = reinterpret_cast<const KV *>(d.k) + off;
-      const KV *vr = reinterpret_cast<const KV *>(d.v) + off;
+      const KV *kr = global_ptr(reinterpret_cast<const KV *>(d.k)) + off;
+      const KV *vr = global_ptr(reinterpret_cast<const KV *>(d.v)) + off;
       float dot = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; e++) {
@@ -916,8 +916,8 @@ __global__ __launch_bounds__(256) void k_attn_prefill_x3(const RowDesc *__restri
   const int p_hi = pos0 + min(q0 + 15, M - 1);  // the tile's last position
   const int pq = pos0 + q0 + r16;              // this lane's query position
   const size_t head_off = ((size_t)layer * kvh + g) * d.max_pos * HD;
-  const KV *kc = reinterpret_cast<const KV *>(d.k) + head_off;
-  const KV *vc = reinterpret_cast<const KV *>(d.v) + head_off;
+  const KV *kc = global_ptr(reinterpret_cast<const KV *>(d.k)) + head_off;
+  const KV *vc = global_ptr(reinterpret_cast<const KV *>(d.v)) + head_off;
   // this lane's query: row min(q0 + r16, M - 1), dims 32 c + 8 gq .. + 7
   u32x4 qp[4][3];
   {

@@ -67,21 +67,29 @@ __device__ __forceinline__ float2 load2(const KV *p) {
 }
 
 // elements col and col + 64 of row m: the product's output, or (nch > 0)
-// its chunk partials [nch][M][ld] (nch <= 4) added in chunk order; all loads
-// issued together (clamped chunk indices, the extra ones not added)
-__device__ __forceinline__ void qkv_pair(const float *qkv, int ld, int nch, int M, int m, int col,
-                                         float &x0, float &x1) {
+// its chunk partials [nch][M][ld] (nch <= 4), loaded together (clamped chunk
+// indices; qkv_sum adds the first nch in chunk order)
+__device__ __forceinline__ void qkv_load(const float *qkv, int ld, int nch, int M, int m, int col,
+                                         float (&a)[4], float (&b)[4]) {
   if (nch == 0) {
-    x0 = qkv[(size_t)m * ld + col];
-    x1 = qkv[(size_t)m * ld + col + 64];
+    a[0] = qkv[(size_t)m * ld + col];
+    b[0] = qkv[(size_t)m * ld + col + 64];
     return;
   }
-  float a[4], b[4];
 #pragma unroll
   for (int c = 0; c < 4; c++) {
     const float *r = qkv + ((size_t)min(c, nch - 1) * M + m) * ld + col;
     a[c] = r[0];
     b[c] = r[64];
+  }
+}
+
+__device__ __forceinline__ void qkv_sum(int nch, const float (&a)[4], const float (&b)[4],
+                                        float &x0, float &x1) {
+  if (nch == 0) {
+    x0 = a[0];
+    x1 = b[0];
+    return;
   }
   x0 = x1 = 0.f;
 #pragma unroll
@@ -104,8 +112,12 @@ __device__ __forceinline__ float row16_tree(float v) {
 // grid (kv heads, M): the GRP query heads of kv head g = blockIdx.x share one
 // read of its K/V; nch > 0: the q/k/v come as nch chunk partials. SU / VU:
 // the key rounds of the score loop / the positions of the value chains whose
-// loads are issued together (deeper for long contexts).
-template <typename KV, bool FUSED, int GRP, int SU, int VU, int NT>
+// loads are issued together (deeper for long contexts). The first round of
+// keys (and, with PV, of values) is loaded right after the q/k/v loads, so
+// that it arrives during the prologue: the cache rows before the row's own
+// position were written by earlier launches, and the own position's key and
+// value are taken from the prologue in every round.
+template <typename KV, bool FUSED, int GRP, int SU, int VU, int NT, bool PV>
 __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *qkv,
                                                const float *qkn, const float2 *rope_cs,
                                                int8_t *xq, int ldq, int layer, int nch) {
@@ -135,19 +147,36 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
   }
   const int pos = d.pos, L = pos + 1;
   const size_t head_off = ((size_t)layer * kvh + g) * d.max_pos * HD;
-  const KV *kc = reinterpret_cast<const KV *>(d.k) + head_off;
-  const KV *vc = reinterpret_cast<const KV *>(d.v) + head_off;
+  const KV *kc = global_ptr(reinterpret_cast<const KV *>(d.k)) + head_off;
+  const KV *vc = global_ptr(reinterpret_cast<const KV *>(d.v)) + head_off;
   constexpr int KG = NT / 16;
   const int kg = t >> 4, li = t & 15;
   // value chain ch over positions ch, ch + 8, ...; dims dim0 + 64 e, e < DPW
   const int ch = wave % NCH, dim0 = (wave / NCH) * 64 + lane;
 
+  static_assert(GRP + 2 <= NWV, "one prologue vector per wave");
+  // vector j = wave: query head g GRP + j (j < GRP), the new k (j == GRP), v (GRP + 1)
+  const int j = wave;
+  const bool pj = FUSED && j < GRP + 2;
+  const int col = j < GRP ? (g * GRP + j) * HD : j == GRP ? NQ + g * HD : NQ + (kvh + g) * HD;
+  float pa[4], pb[4];
+  if (pj) qkv_load(qkv, ldq, nch, M, m, col + lane, pa, pb);
+  // the first round of keys (positions u KG + kg) and values (ch + NCH u),
+  // from clamped positions
+  float k8p[SU][8], vp[PV ? VU : 1][DPW];
+#pragma unroll
+  for (int u = 0; u < SU; u++) load8(kc + (size_t)min(u * KG + kg, L - 1) * HD + 8 * li, k8p[u]);
+  if constexpr (PV) {
+#pragma unroll
+    for (int u = 0; u < VU; u++)
+#pragma unroll
+      for (int e = 0; e < DPW; e++)
+        vp[u][e] = (float)vc[(size_t)min(ch + NCH * u, L - 1) * HD + dim0 + 64 * e];
+  }
   if (FUSED) {
-    // vector j: query head g GRP + j (j < GRP), the new k (j == GRP), v (GRP + 1)
-    for (int j = wave; j < GRP + 2; j += NWV) {
-      const int col = j < GRP ? (g * GRP + j) * HD : j == GRP ? NQ + g * HD : NQ + (kvh + g) * HD;
+    if (pj) {
       float x0, x1;
-      qkv_pair(qkv, ldq, nch, M, m, col + lane, x0, x1);
+      qkv_sum(nch, pa, pb, x0, x1);
       if (j <= GRP) {
         const float *w = qkn + (j < GRP ? 0 : HD);
         const float eps = qkn[2 * HD];
@@ -193,9 +222,16 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
       // unconditional loads from clamped positions (a guarded load would be
       // waited for on its own), then the new position's own k, zeros past L
       float k8[SU][8];
+      if (p0 == 0) {
 #pragma unroll
-      for (int u = 0; u < SU; u++)
-        load8(kc + (size_t)min(p0 + u * KG + kg, L - 1) * HD + 8 * li, k8[u]);
+        for (int u = 0; u < SU; u++)
+#pragma unroll
+          for (int e = 0; e < 8; e++) k8[u][e] = k8p[u][e];
+      } else {
+#pragma unroll
+        for (int u = 0; u < SU; u++)
+          load8(kc + (size_t)min(p0 + u * KG + kg, L - 1) * HD + 8 * li, k8[u]);
+      }
 #pragma unroll
       for (int u = 0; u < SU; u++) {
         const int p = p0 + u * KG + kg;
@@ -279,11 +315,18 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
     for (int e = 0; e < DPW; e++) vnd[e] = FUSED ? vn[dim0 + 64 * e] : 0.f;
     for (int p0 = ch; p0 < L; p0 += NCH * VU) {
       float v[VU][DPW];
+      if (PV && p0 == ch) {
 #pragma unroll
-      for (int u = 0; u < VU; u++)
+        for (int u = 0; u < VU; u++)
 #pragma unroll
-        for (int e = 0; e < DPW; e++)
-          v[u][e] = (float)vc[(size_t)min(p0 + NCH * u, L - 1) * HD + dim0 + 64 * e];
+          for (int e = 0; e < DPW; e++) v[u][e] = vp[PV ? u : 0][e];
+      } else {
+#pragma unroll
+        for (int u = 0; u < VU; u++)
+#pragma unroll
+          for (int e = 0; e < DPW; e++)
+            v[u][e] = (float)vc[(size_t)min(p0 + NCH * u, L - 1) * HD + dim0 + 64 * e];
+      }
       // the new position: its own v; past L: zero (the clamped load may have
       // read the new row before it was written)
 #pragma unroll
@@ -343,14 +386,14 @@ bool attn_x_supported(int heads, int kvh, int head_dim, int max_positions) {
          (size_t)max_positions * (heads / kvh) <= (size_t)kAttnXMaxPositions;
 }
 
-template <typename KV, bool F, int SU, int VU, int NT>
+template <typename KV, bool F, int SU, int VU, int NT, bool PV>
 void attn_x_grp(const AttnArgs &a, int M, int nch, const QAct &xa, int max_positions,
                 hipStream_t st) {
   const dim3 grid(a.kvh, M);
   const int grp = a.heads / a.kvh;
   const size_t lds = sizeof(float) * (size_t)grp * max_positions;
 #define Q3H_ATTNX(G)                                                                           \
-  hipLaunchKernelGGL((k_attn_x<KV, F, G, SU, VU, NT>), grid, dim3(NT), lds, st, a.rd, a.qkv,  \
+  hipLaunchKernelGGL((k_attn_x<KV, F, G, SU, VU, NT, PV>), grid, dim3(NT), lds, st, a.rd, a.qkv,  \
                      a.qkn, a.rope_cs, xa.q, a.ldq, a.layer, nch)
   if (grp == 1)
     Q3H_ATTNX(1);
@@ -369,11 +412,11 @@ template <typename KV, bool F>
 void attn_x_len(const AttnArgs &a, int M, int nch, const QAct &xa, int max_positions,
                 hipStream_t st) {
   if (max_positions <= 32)
-    attn_x_grp<KV, F, 1, 4, 512>(a, M, nch, xa, max_positions, st);
+    attn_x_grp<KV, F, 1, 4, 512, true>(a, M, nch, xa, max_positions, st);
   else if (F)
-    attn_x_grp<KV, F, 8, 16, 1024>(a, M, nch, xa, max_positions, st);
+    attn_x_grp<KV, F, 8, 16, 1024, false>(a, M, nch, xa, max_positions, st);
   else
-    attn_x_grp<KV, F, 8, 16, 512>(a, M, nch, xa, max_positions, st);
+    attn_x_grp<KV, F, 8, 16, 512, false>(a, M, nch, xa, max_positions, st);
 }
 
 void launch_attn_x(const AttnArgs &a, int M, bool fused, bool kv16, int qkv_chunks,

@@ -363,8 +363,8 @@ __global__ __launch_bounds__(256) void k_save_hist(const HistEntry *__restrict__
   for (int d0 = 0; d0 < h.past; d0 += B) {
     const int rows = min(B, h.past - d0);
     const int n = rows * h.cols;
-    float *dst = h.buf + (size_t)d0 * h.cols;
-    const float *src = h.buf + (size_t)(d0 + T) * h.cols;
+    float *dst = global_ptr(h.buf) + (size_t)d0 * h.cols;
+    const float *src = global_ptr(h.buf) + (size_t)(d0 + T) * h.cols;
     for (int base = 0; base < n; base += 32 * 256) {
       float v[32];
 #pragma unroll

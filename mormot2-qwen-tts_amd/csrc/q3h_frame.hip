@@ -94,6 +94,7 @@ __device__ int block_argmax(float v, int i) {
 
 // the descriptor of a row at position pos of context c (pos < 0: inactive)
 __device__ __forceinline__ RowDesc row_desc(const CtxDev *c, int pos) {
+  c = global_ptr(c);
   RowDesc d;
   d.k = c->k;
   d.v = c->v;
@@ -172,7 +173,7 @@ __global__ __launch_bounds__(kArgBlock) void k_choose_code0(FrameDev f) {
         codes[0] = code;
         f.seen[(size_t)s * f.vocab + code] = 1;
         f.nframes[s] = nf + 1;
-        f.cp_ctx[s]->len = 0;
+        global_ptr(f.cp_ctx[s])->len = 0;
       }
       float *x = f.cp_h + (size_t)s * 2 * f.H;
       const float *past = f.past + (size_t)s * f.H;
@@ -384,7 +385,7 @@ __global__ void k_talker_input(FrameDev f) {
   const int s = blockIdx.y;
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
   // the row's descriptor: position = the context length (inactive: -1)
-  if (c == 0) f.t_rd[s] = row_desc(f.t_ctx[s], f.alive[s] ? f.t_ctx[s]->len : -1);
+  if (c == 0) f.t_rd[s] = row_desc(f.t_ctx[s], f.alive[s] ? global_ptr(f.t_ctx[s])->len : -1);
   if (c >= f.H || !f.alive[s]) return;
   const float x = talker_input_elem(f, s, c);
   f.t_h[(size_t)s * f.H + c] = x;
@@ -407,7 +408,7 @@ __global__ __launch_bounds__(kArgBlock) void k_talker_input_q(FrameDev f) {
     f.t_h[(size_t)s * f.H + c] = x;
     xs[c] = x;
   }
-  if (tid == 0) f.t_rd[s] = row_desc(f.t_ctx[s], f.t_ctx[s]->len);
+  if (tid == 0) f.t_rd[s] = row_desc(f.t_ctx[s], global_ptr(f.t_ctx[s])->len);
   __syncthreads();
   quant_row_block(xs, f.t_norm0, f.t_eps, f.H, s, f.n, f.t_xq, red);
 }
@@ -435,7 +436,7 @@ __global__ void k_frame_end(FrameDev f) {
   const int s = blockIdx.x * blockDim.x + threadIdx.x;
   if (s < f.n && f.alive[s]) {
     f.step[s] += 1;
-    CtxDev *c = f.t_ctx[s];  // the talker context took the step's row
+    CtxDev *c = global_ptr(f.t_ctx[s]);  // the talker context took the step's row
     c->len = min(c->len + 1, c->max_pos);
   }
 }

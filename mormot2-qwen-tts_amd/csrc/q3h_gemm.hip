@@ -81,6 +81,18 @@ __global__ __launch_bounds__(kQuantThreads) void k_quant_act(float *x, const flo
       }
     return;
   }
+  // the norm weights of this thread's chunks, loaded first (they are read by
+  // every row, so they come from L2 before the partials arrive)
+  float4 wpre[KC][2];
+  if (norm_w) {
+    const float4 *wr = reinterpret_cast<const float4 *>(norm_w);
+#pragma unroll
+    for (int i = 0; i < KC; i++) {
+      const int jc = min(j0 + i * js, nch - 1);
+      wpre[i][0] = wr[2 * jc];
+      wpre[i][1] = wr[2 * jc + 1];
+    }
+  }
   // loads from clamped chunk / partial indices (a guarded load would be waited
   // for on its own); chunks past the row and partials past ld contribute zeros
   float v[KC][8];
@@ -163,12 +175,11 @@ __global__ __launch_bounds__(kQuantThreads) void k_quant_act(float *x, const flo
     __syncthreads();
     ss = red[0] + red[1];
     const float inv = (float)(1.0 / sqrt(ss / K + (double)eps));
-    const float4 *wr = reinterpret_cast<const float4 *>(norm_w);
 #pragma unroll
     for (int i = 0; i < KC; i++) {
       const int j = j0 + i * js;
       if (j < nch) {
-        const float4 a = wr[2 * j], b = wr[2 * j + 1];
+        const float4 a = wpre[i][0], b = wpre[i][1];
         const float w8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
         for (int e = 0; e < 8; e++) v[i][e] = w8[e] * (v[i][e] * inv);

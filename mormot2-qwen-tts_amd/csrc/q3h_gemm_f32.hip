@@ -657,33 +657,52 @@ __global__ __launch_bounds__(64 * WN) void k_gemm_q8x_m64(const int8_t *__restri
 
 // h[m] += slices 0 .. S-1 of part [S][M][K], added in slice order; then, with
 // a norm weight, xn[m] = w * (h[m] * inv), inv = 1 / sqrt(mean(h[m]^2) + eps)
-// (sum of squares in double). One workgroup per row.
+// (sum of squares in double). One workgroup per row, K <= 4096: a thread
+// holds columns t + 256 i of each 1024-column round in registers, and the norm
+// weights are loaded before the partials, so the normalization needs no
+// second trip to memory.
+constexpr int kResidNormRounds = 4;
+
 template <int S>
 __global__ __launch_bounds__(256) void k_resid_norm(float *__restrict__ h,
                                                     const float *__restrict__ part, int M,
                                                     int K, const float *__restrict__ w,
                                                     float eps, float *__restrict__ xn) {
+  constexpr int NR = kResidNormRounds;
   __shared__ double red[4];
   const int m = blockIdx.x, t = threadIdx.x;
   float *hr = h + (size_t)m * K;
+  float wv[NR][4];
+  if (w) {
+#pragma unroll
+    for (int r = 0; r < NR; r++)
+      if (1024 * r < K)
+#pragma unroll
+        for (int i = 0; i < 4; i++) wv[r][i] = w[min(1024 * r + t + 256 * i, K - 1)];
+  }
+  float hv[NR][4];
   double ss = 0.0;
-  for (int k0 = 0; k0 < K; k0 += 1024) {
+#pragma unroll
+  for (int r = 0; r < NR; r++) {
+    const int k0 = 1024 * r;
+    if (k0 >= K) break;
     // four columns per thread, every load (clamped) issued before the sums
-    float a[4][S], hv[4];
+    float a[4][S];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int k = min(k0 + t + 256 * i, K - 1);
 #pragma unroll
       for (int s = 0; s < S; s++) a[i][s] = part[((size_t)s * M + m) * K + k];
-      hv[i] = hr[k];
+      hv[r][i] = hr[k];
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int k = k0 + t + 256 * i;
-      if (k < K) {
-        float v = hv[i];
+      float v = hv[r][i];
 #pragma unroll
-        for (int s = 0; s < S; s++) v += a[i][s];
+      for (int s = 0; s < S; s++) v += a[i][s];
+      hv[r][i] = v;
+      if (k < K) {
         hr[k] = v;
         ss += (double)v * v;
       }
@@ -695,7 +714,15 @@ __global__ __launch_bounds__(256) void k_resid_norm(float *__restrict__ h,
   __syncthreads();
   const double tot = red[0] + red[1] + red[2] + red[3];
   const float inv = (float)(1.0 / sqrt(tot / K + (double)eps));
-  for (int k = t; k < K; k += 256) xn[(size_t)m * K + k] = w[k] * (hr[k] * inv);
+#pragma unroll
+  for (int r = 0; r < NR; r++) {
+    if (1024 * r >= K) break;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int k = 1024 * r + t + 256 * i;
+      if (k < K) xn[(size_t)m * K + k] = wv[r][i] * (hv[r][i] * inv);
+    }
+  }
 }
 
 template <int TM, int KK>
@@ -927,6 +954,7 @@ int launch_gemm_f32_part(const Mat &W, const float *x, int ldx, int M, float *pa
 
 void launch_resid_norm(float *h, const float *part, int M, int K, const float *norm_w,
                        float eps, float *xn, int slices, hipStream_t st) {
+  require(K <= 1024 * kResidNormRounds, Q3H_E_ARG, "launch_resid_norm: K above 4096");
 #define Q3H_RN(S)                                                                              \
   hipLaunchKernelGGL(k_resid_norm<S>, dim3(M), dim3(256), 0, st, h, part, M, K, norm_w, eps, xn)
   switch (slices) {

@@ -33,6 +33,15 @@ struct RowDesc {
   int pos;
 };
 
+// p as a pointer the compiler knows to be in device (global) memory. Pointers
+// read from memory (row descriptors, frame state) otherwise stay generic and
+// their accesses become flat loads / stores, which also count in lgkmcnt: a
+// wait for an LDS or scalar access then waits for them as well.
+template <typename T>
+__device__ __forceinline__ T *global_ptr(T *p) {
+  return (T *)(__attribute__((address_space(1))) T *)(uintptr_t)p;
+}
+
 // Context state that kernels read and advance on the device.
 struct CtxDev {
   void *k;

@@ -280,7 +280,7 @@ __global__ void k_prep(CtxDev *const *cs, const int *alive, int n, int R, RowDes
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n * R) return;
   const int s = i / R, r = i % R;
-  const CtxDev *c = cs[s];
+  const CtxDev *c = global_ptr(cs[s]);
   RowDesc d;
   d.k = c->k;
   d.v = c->v;
@@ -294,7 +294,7 @@ __global__ void k_advance(CtxDev *const *cs, const int *alive, int n, int R) {
   const int s = blockIdx.x * blockDim.x + threadIdx.x;
   if (s >= n) return;
   if (alive && !alive[s]) return;
-  CtxDev *c = cs[s];
+  CtxDev *c = global_ptr(cs[s]);
   c->len = min(c->len + R, c->max_pos);
 }
 
@@ -366,7 +366,7 @@ __global__ __launch_bounds__(kBlock) void k_qk_rope_append(
   }
   const int g = j < heads + kvh ? j - heads : j - heads - kvh;
   void *base = j < heads + kvh ? d.k : d.v;
-  KV *dst = reinterpret_cast<KV *>(base) +
+  KV *dst = global_ptr(reinterpret_cast<KV *>(base)) +
             (((size_t)layer * kvh + g) * d.max_pos + d.pos) * hd;
   dst[lane] = (KV)x0;
   dst[lane + half] = (KV)x1;
