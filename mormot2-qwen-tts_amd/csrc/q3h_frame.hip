@@ -575,15 +575,18 @@ void refresh_slices(q3h_frame *f) {
   drop_graphs(f);
 }
 
-// The number of slices of a frame of n streams: two for the int8 path at 8
-// or more streams (its kernels take the same time for 8 .. 64 rows), one
+// The number of slices of a frame of n streams: on the int8 path one slice
+// per 32 streams (its products take each 16-row tile as workgroups of their
+// own, so a slice of 32 streams costs a 16-stream slice's launches; at 16,
+// 24 and 32 streams one slice is 6 %, 1.5 % and 0.3 % faster than two, and the
+// code predictor's first step keeps at most 64 rows per slice), one
 // otherwise. Q3H_FRAME_SLICES (1..4) overrides it, for measurements.
 int slice_count(const q3h_stack *talker, int n) {
   if (const char *e = std::getenv("Q3H_FRAME_SLICES")) {
     const int v = std::atoi(e);
     if (v >= 1 && v <= 4) return std::min(v, n);
   }
-  return (n >= 8 && partial_path(talker, n)) ? 2 : 1;
+  return partial_path(talker, n) ? (n + 31) / 32 : 1;
 }
 
 template <class T>

@@ -222,6 +222,31 @@ __global__ __launch_bounds__(kQuantThreads) void k_quant_act(float *x, const flo
   }
 }
 
+// The fused multiply-add chains of 8 blocks from their operands: A av[i]
+// (16 weight rows), B bv[t][i] (16 activation rows of tile t), the weight
+// scales of the lane's 4 rows dwv[r][i] and the activation scales of its row
+// dxv[t][i]: acc[t][r] = fma((float)dot, d_w * d_x, acc) from 0 in block order.
+template <int TM>
+__device__ __forceinline__ void chains8(const long (&av)[8], const long (&bv)[TM][8],
+                                        const float (&dwv)[4][8], const float (&dxv)[TM][8],
+                                        float (&acc)[TM][4]) {
+#pragma unroll
+  for (int t = 0; t < TM; t++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) acc[t][r] = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+      const v4i ci =
+          __builtin_amdgcn_mfma_i32_16x16x32_i8(av[i], bv[t][i], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        acc[t][r] = fmaf((float)ci[r], __fmul_rn(dwv[r][i], dxv[t][i]), acc[t][r]);
+    }
+  }
+}
+
 // The chains of one 256-column chunk (blocks b0 .. b0 + 7, K % 256 == 0) for
 // 16 weight rows from n0 and the activation tiles mt0 .. mt0 + TM - 1:
 // acc[t][r] = output (n0 + 4 (lane / 16) + r, 16 (mt0 + t) + lane % 16); a
@@ -293,21 +318,7 @@ __device__ __forceinline__ void chunk_chains(const int8_t *wq, const int8_t *xq,
     for (int i = 0; i < 8; i++) av[i] = at[c][4 * i + g];  // row c, bytes 32 i + 8 g
   }
   __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int t = 0; t < TM; t++)
-#pragma unroll
-    for (int r = 0; r < 4; r++) acc[t][r] = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-#pragma unroll
-    for (int t = 0; t < TM; t++) {
-      const v4i ci =
-          __builtin_amdgcn_mfma_i32_16x16x32_i8(av[i], bv[t][i], v4i{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < 4; r++)
-        acc[t][r] = fmaf((float)ci[r], __fmul_rn(dwv[r][i], dxv[t][i]), acc[t][r]);
-    }
-  }
+  chains8<TM>(av, bv, dwv, dxv, acc);
 }
 
 // y[m][n] (+)= sum_b d_w[n][b] d_x[m][b] sum_{k in b} q_w[n][k] q_x[m][k].
@@ -361,21 +372,24 @@ __global__ __launch_bounds__(KW * 64) void k_gemm_i8(const int8_t *wq, const int
   }
 }
 
-// One wave per (16 weight rows, chunk), every activation row (M <= 16 TM):
-// part[chunk][m][n] = the chunk's chains.
+// One wave per (16 weight rows, chunk, TM activation tiles from TM z):
+// part[chunk][m][n] = the chunk's chains. The waves of one (weight rows,
+// chunk) over the row tiles are gridDim.x * gridDim.y workgroups apart (a
+// multiple of 8 for the Qwen3-TTS shapes), so they run on one XCD and share
+// the weight tile through its L2.
 template <int TM>
 __global__ __launch_bounds__(64) void k_gemm_i8p(const int8_t *wq, const int8_t *xq,
                                                   float *part, int N, int K, int M) {
   const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-  const int n0 = blockIdx.x * 16, ch = blockIdx.y;
+  const int n0 = blockIdx.x * 16, ch = blockIdx.y, mt0 = blockIdx.z * TM;
   const int mt16 = (M + 15) >> 4;
   const float *dx = scales_of(const_cast<int8_t *>(xq), M, K);
   __shared__ long at[16][33];
   float acc[TM][4];
-  chunk_chains<TM, true>(wq, xq, dx, N, K, n0, 0, mt16, ch * 8, at, acc);
+  chunk_chains<TM, true>(wq, xq, dx, N, K, n0, mt0, mt16, ch * 8, at, acc);
 #pragma unroll
   for (int t = 0; t < TM; t++) {
-    const int m = t * 16 + c;
+    const int m = (mt0 + t) * 16 + c;
     if (m < M)
       *reinterpret_cast<float4 *>(part + ((size_t)ch * M + m) * N + n0 + 4 * g) =
           make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
@@ -384,10 +398,13 @@ __global__ __launch_bounds__(64) void k_gemm_i8p(const int8_t *wq, const int8_t 
 
 // The gate/up product with SiLU(gate) * up and the quantization of the result
 // fused: a workgroup owns 64 gate/up rows, i.e. one 32-block of the output,
-// and its 4 chunks (a wave per (16 rows, chunk), K == 1024); the chunk chains
-// meet in LDS and are added in chunk order, then each row's block is
-// quantized into yq (M <= 16 TM rows; yq must not alias xq). The same values
-// as k_gemm_i8p followed by k_quant_act<SRC_SWIGLU>.
+// its 4 chunks (a wave per (16 rows, chunk), K == 1024) and the TM 16-row
+// activation tiles from TM blockIdx.y; the chunk chains meet in LDS and are
+// added in chunk order, then each row's block is quantized into yq (yq must
+// not alias xq). The same values as k_gemm_i8p followed by
+// k_quant_act<SRC_SWIGLU>. The workgroups of one output block over the row
+// tiles are gridDim.x apart (a multiple of 8 for the Qwen3-TTS shapes: one
+// XCD, one L2 for the weights).
 template <int TM>
 __global__ __launch_bounds__(1024) void k_gemm_i8_swq(const int8_t *wq, const int8_t *xq,
                                                       int8_t *yq, int N, int M) {
@@ -396,29 +413,30 @@ __global__ __launch_bounds__(1024) void k_gemm_i8_swq(const int8_t *wq, const in
   __shared__ long at[16][16][33];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int g = lane >> 4, c = lane & 15;
-  const int mt16 = (M + 15) >> 4;
+  const int mt16 = (M + 15) >> 4, mt0 = blockIdx.y * TM;
   const int tile = w & 3, ch = w >> 2;  // 16-row tile of the 64, chunk
   const int n0 = blockIdx.x * 64 + tile * 16;
   const float *dx = scales_of(const_cast<int8_t *>(xq), M, K);
   float acc[TM][4];
-  chunk_chains<TM, true>(wq, xq, dx, N, K, n0, 0, mt16, ch * 8, at[w], acc);
+  chunk_chains<TM, true>(wq, xq, dx, N, K, n0, mt0, mt16, ch * 8, at[w], acc);
 #pragma unroll
   for (int t = 0; t < TM; t++)
 #pragma unroll
     for (int r = 0; r < 4; r++) red[ch][tile * 16 + 4 * g + r][t * 16 + c] = acc[t][r];
   __syncthreads();
-  // output block b = blockIdx.x of every row, 32 lanes per row
+  // output block b = blockIdx.x of this workgroup's rows, 32 lanes per row
   const int KO = N >> 1, nbo = KO >> 5, b = blockIdx.x;
   float *dy = scales_of(yq, M, KO);
-  for (int idx = threadIdx.x; idx < mt16 * 16 * 32; idx += 1024) {
-    const int m = idx >> 5, j = idx & 31;
+  const int nrow = min(TM, mt16 - mt0) * 16;
+  for (int idx = threadIdx.x; idx < nrow * 32; idx += 1024) {
+    const int ml = idx >> 5, j = idx & 31, m = mt0 * 16 + ml;
     float o = 0.f;
     if (m < M) {
       float gs = 0.f, us = 0.f;
 #pragma unroll
       for (int v = 0; v < 4; v++) {
-        gs = __fadd_rn(gs, red[v][2 * j][m]);
-        us = __fadd_rn(us, red[v][2 * j + 1][m]);
+        gs = __fadd_rn(gs, red[v][2 * j][ml]);
+        us = __fadd_rn(us, red[v][2 * j + 1][ml]);
       }
       o = silu_mul_ieee(gs, us);
     }
@@ -529,26 +547,22 @@ void launch_gemm_i8(const Mat &W, const QAct &xa, int M, int epi, float *y, int 
     gemm_by_k<4>(W, xa, M, epi, y, ldy, st);
 }
 
+// Both products below take one 16-row activation tile per workgroup, the
+// tiles on a grid dimension of their own: a tile's waves do the work of a
+// 16-row product, and more rows add workgroups instead of lengthening each.
 bool launch_gemm_i8_swiglu_quantize(const Mat &W, const QAct &xa, int M, QAct out,
                                     hipStream_t st) {
-  if (M > 32 || W.K != 1024 || W.N % 64 != 0) return false;
-  if (M <= 16)
-    hipLaunchKernelGGL(k_gemm_i8_swq<1>, dim3(W.N / 64), dim3(1024), 0, st, W.q, xa.q, out.q,
-                       W.N, M);
-  else
-    hipLaunchKernelGGL(k_gemm_i8_swq<2>, dim3(W.N / 64), dim3(1024), 0, st, W.q, xa.q, out.q,
-                       W.N, M);
+  if (M > 64 || W.K != 1024 || W.N % 64 != 0) return false;
+  const int mt16 = (M + 15) >> 4;
+  hipLaunchKernelGGL(k_gemm_i8_swq<1>, dim3(W.N / 64, mt16), dim3(1024), 0, st, W.q, xa.q,
+                     out.q, W.N, M);
   return true;
 }
 
 void launch_gemm_i8_partial(const Mat &W, const QAct &xa, int M, float *part, hipStream_t st) {
-  const dim3 grid(W.N / 16, gemm_i8_chunks(W.K));
-  if (M <= 16)
-    hipLaunchKernelGGL(k_gemm_i8p<1>, grid, dim3(64), 0, st, W.q, xa.q, part, W.N, W.K, M);
-  else if (M <= 32)
-    hipLaunchKernelGGL(k_gemm_i8p<2>, grid, dim3(64), 0, st, W.q, xa.q, part, W.N, W.K, M);
-  else
-    hipLaunchKernelGGL(k_gemm_i8p<4>, grid, dim3(64), 0, st, W.q, xa.q, part, W.N, W.K, M);
+  const int mt16 = (M + 15) >> 4;
+  const dim3 grid(W.N / 16, gemm_i8_chunks(W.K), mt16);
+  hipLaunchKernelGGL(k_gemm_i8p<1>, grid, dim3(64), 0, st, W.q, xa.q, part, W.N, W.K, M);
 }
 
 }  // namespace q3h

@@ -160,7 +160,7 @@ void launch_gemm_i8_partial(const Mat &W, const QAct &xa, int M, float *part, hi
 void launch_residual_quantize(float *h, const float *part, int chunks, int M, int K,
                               const float *norm_w, float eps, const QAct *out, hipStream_t st);
 // the gate/up product, silu(gate) * up and its quantization into out in one
-// launch (M <= 32, K == 1024, N % 64 == 0; out must not alias xa); false
+// launch (M <= 64, K == 1024, N % 64 == 0; out must not alias xa); false
 // when the shape is not one it takes (nothing launched)
 bool launch_gemm_i8_swiglu_quantize(const Mat &W, const QAct &xa, int M, QAct out,
                                     hipStream_t st);

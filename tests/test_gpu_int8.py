@@ -78,14 +78,16 @@ def test_int8_batch_rows(small8, q3h, q3o, synth, n):
             c.destroy()
 
 
-def test_int8_frame_32_streams(small8, synth):
-    """The batched frame step with 32 streams: code-predictor products over
-    64 rows (the 2-row prefill of every stream) and 32 rows, the talker over
-    32 ragged contexts."""
+@pytest.mark.parametrize("n", [32, 48])
+def test_int8_frame_streams(small8, synth, n):
+    """The batched frame step with 32 streams (one slice): code-predictor
+    products over 64 rows (the 2-row prefill of every stream) and 32 rows, the
+    talker over 32 ragged contexts; and with 48 streams (two slices of 24,
+    each its own graph on its own HIP stream)."""
     m = small8
     rng = np.random.Generator(np.random.PCG64(5))
-    lens = rng.integers(16, 40, size=32)
-    fr = m.frame(n_streams=32, max_positions=64, max_frames=8)
+    lens = rng.integers(16, 40, size=n)
+    fr = m.frame(n_streams=n, max_positions=64, max_frames=8)
     ofs = []
     try:
         for s, L in enumerate(lens):
@@ -151,7 +153,7 @@ def test_int8_frame_32_streams_long_prompts(device, synth):
     layers, code predictor 2, real widths): 32 streams with prompt lengths
     uniform in [16, 256] from the workload's generator, 14 frames, so that
     contexts pass 256 positions (more than one round of the attention's key
-    loop); two slices of 16 streams. The streams start together
+    loop). The streams start together
     (q3h_frame_start_batch, their prefills overlapping). Bit-exact against the
     oracle."""
     rng = np.random.Generator(np.random.PCG64(1))
