@@ -166,23 +166,20 @@ __device__ int block_sample(const float (&x)[NPT], int n, const SampleParams &p,
         for (int b = lane; b < 256; b += 64) nxt[b] = 0;
       }
       if (wave == 0) {
-        // lane l: buckets 4 l .. 4 l + 3 (larger buckets in larger lanes)
-        const int h[4] = {hist[4 * lane], hist[4 * lane + 1], hist[4 * lane + 2],
-                          hist[4 * lane + 3]};
+        // lane l: buckets 4 (63 - l) .. + 3 (larger buckets in smaller lanes),
+        // so a prefix sum over the lanes counts this lane's buckets and every
+        // larger one
+        const int4 h4 = reinterpret_cast<const int4 *>(hist)[63 - lane];
+        const int h[4] = {h4.x, h4.y, h4.z, h4.w};
         const int mine = h[0] + h[1] + h[2] + h[3];
-        int suf = mine;  // inclusive suffix sum over the lanes >= this one
-        for (int off = 1; off < 64; off <<= 1) {
-          const int o = __shfl_down(suf, off, 64);
-          if (lane + off < 64) suf += o;
-        }
-        const int above = suf - mine;  // counts of the lanes above this one
+        const int above = wave_prefix_sum_i(mine) - mine;  // counts of the larger buckets
         const uint32_t rem = sh.remaining;
         if ((uint32_t)above < rem && rem <= (uint32_t)(above + mine)) {
-          int acc = above, d = 4 * lane;
+          int acc = above, d = 4 * (63 - lane);
           int hd = 0;
           for (int q = 3; q >= 0; q--) {
             if ((uint32_t)(acc + h[q]) >= rem) {
-              d = 4 * lane + q;
+              d = 4 * (63 - lane) + q;
               hd = h[q];
               break;
             }
@@ -205,7 +202,7 @@ __device__ int block_sample(const float (&x)[NPT], int n, const SampleParams &p,
 #pragma unroll
   for (int j = 0; j < NPT; j++)
     if (kept[j]) m = fmaxf(m, v[j]);
-  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  m = wave_max_dpp(m);
   if (lane == 0) sh.fred[wave] = m;
   __syncthreads();
   m = sh.fred[0];
@@ -274,7 +271,12 @@ __device__ int block_sample(const float (&x)[NPT], int n, const SampleParams &p,
         kept[j] = kept[j] && (key[j] > tk || (key[j] == tk && base + j <= ti));
     }
   }
-  // 5. the draw
+  // 5. the draw. B_s is summed in lane 16 s of its row from the row's A_t
+  // (DPP row shifts, in order); wave 0 runs the chain of the segment sums in
+  // every lane, lane q keeping the sum through segment q, so the first
+  // segment whose running sum passes the target is a ballot (the same sums
+  // and comparisons as a walk over the segments); the same over the threads
+  // of that segment
   float a = 0.0f;
 #pragma unroll
   for (int j = 0; j < NPT; j++) {
@@ -283,53 +285,59 @@ __device__ int block_sample(const float (&x)[NPT], int n, const SampleParams &p,
     a = __fadd_rn(a, w);
   }
   sh.A[t] = a;
-  __syncthreads();
-  if (t < 64) {
-    float b = 0.0f;
-    for (int q = 0; q < 16; q++) b = __fadd_rn(b, sh.A[16 * t + q]);
-    sh.B[t] = b;
-  }
+  float b = a;
+  b = __fadd_rn(b, row_shl_f<1>(a));
+  b = __fadd_rn(b, row_shl_f<2>(a));
+  b = __fadd_rn(b, row_shl_f<3>(a));
+  b = __fadd_rn(b, row_shl_f<4>(a));
+  b = __fadd_rn(b, row_shl_f<5>(a));
+  b = __fadd_rn(b, row_shl_f<6>(a));
+  b = __fadd_rn(b, row_shl_f<7>(a));
+  b = __fadd_rn(b, row_shl_f<8>(a));
+  b = __fadd_rn(b, row_shl_f<9>(a));
+  b = __fadd_rn(b, row_shl_f<10>(a));
+  b = __fadd_rn(b, row_shl_f<11>(a));
+  b = __fadd_rn(b, row_shl_f<12>(a));
+  b = __fadd_rn(b, row_shl_f<13>(a));
+  b = __fadd_rn(b, row_shl_f<14>(a));
+  b = __fadd_rn(b, row_shl_f<15>(a));
+  if ((lane & 15) == 0) sh.B[t >> 4] = b;
   __syncthreads();
   if (wave == 0) {
-    const float b = sh.B[lane];
-    float S = 0.0f;
-    for (int q = 0; q < 64; q++) S = __fadd_rn(S, lane_f(b, q));
-    const float target = __fmul_rn(u, S);
-    float r = 0.0f;
-    int seg = -1;
+    float r = 0.0f, mine = 0.0f;  // mine: B_0 + .. + B_lane, in order
+#pragma unroll
     for (int q = 0; q < 64; q++) {
-      const float bq = lane_f(b, q);
-      if (__fadd_rn(r, bq) > target) {
-        seg = q;
-        break;
-      }
-      r = __fadd_rn(r, bq);
+      r = __fadd_rn(r, sh.B[q]);
+      mine = lane == q ? r : mine;
     }
+    const float target = __fmul_rn(u, r);
+    const unsigned long long hit = __ballot(mine > target);
     int pick;
-    if (seg < 0) {
+    if (hit == 0) {
       pick = last_positive(sh.W, 0, kSampleThreads * NPT);
     } else {
-      const float at = lane < 16 ? sh.A[16 * seg + lane] : 0.0f;
-      int th = -1;
+      const int seg = __ffsll((long long)hit) - 1;
+      const float r0 = seg == 0 ? 0.0f : lane_f(mine, seg - 1);  // the sum before seg
+      float rr = r0, mine2 = 0.0f;
+#pragma unroll
       for (int q = 0; q < 16; q++) {
-        const float aq = lane_f(at, q);
-        if (__fadd_rn(r, aq) > target) {
-          th = 16 * seg + q;
-          break;
-        }
-        r = __fadd_rn(r, aq);
+        rr = __fadd_rn(rr, sh.A[16 * seg + q]);
+        mine2 = lane == q ? rr : mine2;
       }
-      if (th < 0) {
+      const unsigned long long hit2 = __ballot(lane < 16 && mine2 > target);
+      if (hit2 == 0) {
         pick = last_positive(sh.W, 16 * seg * NPT, 16 * (seg + 1) * NPT);
       } else {
+        const int tq = __ffsll((long long)hit2) - 1, th = 16 * seg + tq;
+        float r1 = tq == 0 ? r0 : lane_f(mine2, tq - 1);
         pick = -1;
         for (int j = 0; j < NPT; j++) {
           const float wj = sh.W[th * NPT + j];
-          if (__fadd_rn(r, wj) > target) {
+          if (__fadd_rn(r1, wj) > target) {
             pick = th * NPT + j;
             break;
           }
-          r = __fadd_rn(r, wj);
+          r1 = __fadd_rn(r1, wj);
         }
         if (pick < 0) pick = last_positive(sh.W, th * NPT, th * NPT + NPT);
       }

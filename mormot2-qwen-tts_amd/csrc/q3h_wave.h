@@ -62,6 +62,27 @@ __device__ __forceinline__ double wave_sum_dpp_d(double v) {
   return __builtin_bit_cast(double, ((long long)hi << 32) | (unsigned int)lo);
 }
 
+// inclusive prefix sum over the 64 lanes (lane i: lanes 0 .. i), exact for
+// integers: row scans by DPP row shifts, then the row totals broadcast by
+// row_bcast15 / row_bcast31
+__device__ __forceinline__ int wave_prefix_sum_i(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, kBcast15, 0xa, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, kBcast31, 0xc, 0xf, false);
+  return v;
+}
+
+// the value of lane l + K of the same 16-lane row (DPP row_shl:K; 0 past the
+// row's end)
+template <int K>
+__device__ __forceinline__ float row_shl_f(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x100 + K, 0xf, 0xf, true));
+}
+
 // DPP move where lanes outside the row mask keep their own value (the
 // identity of max)
 template <int CTRL, int ROW_MASK = 0xf>
