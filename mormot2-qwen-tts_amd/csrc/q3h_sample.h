@@ -92,7 +92,7 @@ constexpr int kSampleThreads = 1024;
 constexpr int kSampleMaxNPT = 3;  // up to 3072 values
 
 struct SampleShared {
-  int hist[2][256];  // the radix passes alternate between the two
+  alignas(16) int hist[2][512];  // the radix passes alternate between the two
   uint32_t prefix, remaining;
   int exact;  // the selected bucket holds exactly the values still wanted
   float fred[kSampleThreads / 64];
@@ -102,8 +102,10 @@ struct SampleShared {
   float cv[64];
   uint32_t th_key;
   int th_idx;
-  float A[kSampleThreads];
-  float B[64];
+  alignas(16) float A[kSampleThreads];
+  alignas(16) float B[64];
+  alignas(16) float P[64];   // B_0 + .. + B_q, in order
+  alignas(16) float P2[16];  // the same over one segment's A_t
   float W[kSampleThreads * kSampleMaxNPT];
   int pick;
   int fidx[kSampleThreads / 64];
@@ -139,7 +141,8 @@ __device__ int block_sample(const float (&x)[NPT], int n, const SampleParams &p,
     key[j] = order_key(v[j]);
     kept[j] = in;
   }
-  // 2. top-k: the k-th largest key by a radix select, 8 bits per pass. A pass
+  // 2. top-k: the k-th largest key by a radix select, 9 bits per pass (the
+  // first pass buckets by sign and exponent), 5 in the last. A pass
   // whose selected bucket holds exactly the values still wanted ends the
   // select: every key of that bucket is kept, so the bucket's lowest key (the
   // prefix with zero low bits) keeps the same set as the exact k-th key.
@@ -150,36 +153,38 @@ __device__ int block_sample(const float (&x)[NPT], int n, const SampleParams &p,
       sh.remaining = (uint32_t)p.top_k;
       sh.exact = 0;
     }
-    for (int b = t; b < 512; b += kSampleThreads) sh.hist[b >> 8][b & 255] = 0;
+    for (int b = t; b < 1024; b += kSampleThreads) sh.hist[b >> 9][b & 511] = 0;
     __syncthreads();
     for (int pass = 0; pass < 4; pass++) {
-      const int shift = 24 - 8 * pass;
-      const uint32_t hmask = pass == 0 ? 0u : (0xFFFFFFFFu << (shift + 8));
+      const int width = pass < 3 ? 9 : 5, shift = 32 - 9 * pass - width;
+      const uint32_t hmask = pass == 0 ? 0u : (0xFFFFFFFFu << (shift + width));
       int *hist = sh.hist[pass & 1];
       const uint32_t prefix = sh.prefix;
 #pragma unroll
       for (int j = 0; j < NPT; j++)
-        if (kept[j] && (key[j] & hmask) == prefix) atomicAdd(&hist[(key[j] >> shift) & 255], 1);
+        if (kept[j] && (key[j] & hmask) == prefix)
+          atomicAdd(&hist[(key[j] >> shift) & ((1u << width) - 1)], 1);
       __syncthreads();
       if (wave == 1) {  // the other buffer, for the next pass
         int *nxt = sh.hist[(pass + 1) & 1];
-        for (int b = lane; b < 256; b += 64) nxt[b] = 0;
+        for (int b = lane; b < 512; b += 64) nxt[b] = 0;
       }
       if (wave == 0) {
-        // lane l: buckets 4 (63 - l) .. + 3 (larger buckets in smaller lanes),
-        // so a prefix sum over the lanes counts this lane's buckets and every
-        // larger one
-        const int4 h4 = reinterpret_cast<const int4 *>(hist)[63 - lane];
-        const int h[4] = {h4.x, h4.y, h4.z, h4.w};
-        const int mine = h[0] + h[1] + h[2] + h[3];
-        const int above = wave_prefix_sum_i(mine) - mine;  // counts of the larger buckets
+        // lane l: buckets 8 (63 - l) .. + 7 (larger buckets in smaller lanes)
+        const int4 ha = reinterpret_cast<const int4 *>(hist)[2 * (63 - lane)];
+        const int4 hb = reinterpret_cast<const int4 *>(hist)[2 * (63 - lane) + 1];
+        const int h[8] = {ha.x, ha.y, ha.z, ha.w, hb.x, hb.y, hb.z, hb.w};
+        int mine = 0;
+#pragma unroll
+        for (int q = 0; q < 8; q++) mine += h[q];
+        const int above = wave_prefix_sum_i(mine) - mine;
         const uint32_t rem = sh.remaining;
         if ((uint32_t)above < rem && rem <= (uint32_t)(above + mine)) {
-          int acc = above, d = 4 * (63 - lane);
+          int acc = above, d = 8 * (63 - lane);
           int hd = 0;
-          for (int q = 3; q >= 0; q--) {
+          for (int q = 7; q >= 0; q--) {
             if ((uint32_t)(acc + h[q]) >= rem) {
-              d = 4 * (63 - lane) + q;
+              d = 8 * (63 - lane) + q;
               hd = h[q];
               break;
             }
@@ -304,12 +309,25 @@ __device__ int block_sample(const float (&x)[NPT], int n, const SampleParams &p,
   if ((lane & 15) == 0) sh.B[t >> 4] = b;
   __syncthreads();
   if (wave == 0) {
-    float r = 0.0f, mine = 0.0f;  // mine: B_0 + .. + B_lane, in order
+    float bq[64];
+#pragma unroll
+    for (int q = 0; q < 16; q++) {
+      const float4 f = reinterpret_cast<const float4 *>(sh.B)[q];
+      bq[4 * q] = f.x, bq[4 * q + 1] = f.y, bq[4 * q + 2] = f.z, bq[4 * q + 3] = f.w;
+    }
+    float r = 0.0f;
 #pragma unroll
     for (int q = 0; q < 64; q++) {
-      r = __fadd_rn(r, sh.B[q]);
-      mine = lane == q ? r : mine;
+      r = __fadd_rn(r, bq[q]);
+      bq[q] = r;
     }
+    if (lane == 0) {
+#pragma unroll
+      for (int q = 0; q < 16; q++)
+        reinterpret_cast<float4 *>(sh.P)[q] = make_float4(bq[4 * q], bq[4 * q + 1], bq[4 * q + 2], bq[4 * q + 3]);
+    }
+    __builtin_amdgcn_wave_barrier();
+    const float mine = sh.P[lane];
     const float target = __fmul_rn(u, r);
     const unsigned long long hit = __ballot(mine > target);
     int pick;
@@ -318,12 +336,25 @@ __device__ int block_sample(const float (&x)[NPT], int n, const SampleParams &p,
     } else {
       const int seg = __ffsll((long long)hit) - 1;
       const float r0 = seg == 0 ? 0.0f : lane_f(mine, seg - 1);  // the sum before seg
-      float rr = r0, mine2 = 0.0f;
+      float aq[16];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const float4 f = reinterpret_cast<const float4 *>(sh.A + 16 * seg)[q];
+        aq[4 * q] = f.x, aq[4 * q + 1] = f.y, aq[4 * q + 2] = f.z, aq[4 * q + 3] = f.w;
+      }
+      float rr = r0;
 #pragma unroll
       for (int q = 0; q < 16; q++) {
-        rr = __fadd_rn(rr, sh.A[16 * seg + q]);
-        mine2 = lane == q ? rr : mine2;
+        rr = __fadd_rn(rr, aq[q]);
+        aq[q] = rr;
       }
+      if (lane == 0) {
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+          reinterpret_cast<float4 *>(sh.P2)[q] = make_float4(aq[4 * q], aq[4 * q + 1], aq[4 * q + 2], aq[4 * q + 3]);
+      }
+      __builtin_amdgcn_wave_barrier();
+      const float mine2 = sh.P2[lane & 15];
       const unsigned long long hit2 = __ballot(lane < 16 && mine2 > target);
       if (hit2 == 0) {
         pick = last_positive(sh.W, 16 * seg * NPT, 16 * (seg + 1) * NPT);

@@ -84,8 +84,9 @@ def _exact_bucket_head(head):
     """Q8_0 head bytes whose logits put the top 50 in one radix bucket, for
     any hidden state: rows 0-49 all equal to row 200, rows 50-99 its negation,
     every other row's quants 0. One of the two groups has 50 equal positive
-    logits, every other logit is 0 or negative, so the first 8-bit pass of the
-    top-k select finds a bucket holding exactly the 50 values still wanted."""
+    logits, every other logit is 0 or negative, so the first pass of the top-k
+    select (sign and exponent) finds a bucket holding exactly the 50 values
+    still wanted."""
     b = np.array(head, copy=True)
     blk = b.reshape(b.shape[0], -1, 34)
     src = blk[200].copy()
