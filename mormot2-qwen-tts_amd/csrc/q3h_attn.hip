@@ -163,7 +163,7 @@ __global__ __launch_bounds__(NTS) void k_attn_short(const RowDesc *__restrict__ 
       qs[lane + 64] = x1;
     } else if (wave < 3) {
       if (wave == 1) norm_rope(x0, x1, w0, w1, cs, eps);
-      const KV y0 = (KV)x0, y1 = (KV)x1;
+      const KV y0 = to_cache<KV>(x0), y1 = to_cache<KV>(x1);
       kvn[wave - 1][lane] = (float)y0;
       kvn[wave - 1][lane + 64] = (float)y1;
       if (h % GRP == 0) {  // the group's first query head appends
@@ -409,8 +409,8 @@ __global__ __launch_bounds__(NTL) void k_attn_split(const RowDesc *__restrict__ 
     if (app) {
       if (wave == NWV - 2) norm_rope(a0, a1, wk0, wk1, cs, eps);
       KV *dst = (wave == NWV - 2 ? kc : vc) + (size_t)pos * HD;
-      dst[lane] = (KV)a0;
-      dst[lane + 64] = (KV)a1;
+      dst[lane] = to_cache<KV>(a0);
+      dst[lane + 64] = to_cache<KV>(a1);
     }
     // the wave's own rows of LDS: ordered within the wave, no block barrier
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -192,7 +192,7 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
         qs[j][lane] = x0;
         qs[j][lane + 64] = x1;
       } else {
-        const KV a0 = (KV)x0, a1 = (KV)x1;  // the cache's precision
+        const KV a0 = to_cache<KV>(x0), a1 = to_cache<KV>(x1);  // the cache's precision
         float *own = j == GRP ? kn : vn;
         own[lane] = (float)a0;
         own[lane + 64] = (float)a1;

@@ -180,7 +180,8 @@ __global__ __launch_bounds__(PNT) void k_attn_pair_cp(const int8_t *__restrict__
   {
     float x0 = xk0, x1 = xk1;
     norm_rope(x0, x1, kn0, kn1, cs, eps);
-    const KV k0 = (KV)x0, k1 = (KV)x1, v0 = (KV)xv0, v1 = (KV)xv1;
+    const KV k0 = to_cache<KV>(x0), k1 = to_cache<KV>(x1), v0 = to_cache<KV>(xv0),
+             v1 = to_cache<KV>(xv1);
     kvs[j][0][lane] = (float)k0;
     kvs[j][0][lane + 64] = (float)k1;
     kvs[j][1][lane] = (float)v0;
@@ -351,7 +352,8 @@ __global__ __launch_bounds__(NT) void k_attn2_o_cp(const int8_t *__restrict__ wo
   for (int r = 0; r < 2; r++) {
     float x0 = xk[r][0], x1 = xk[r][1];
     norm_rope(x0, x1, kn0, kn1, r ? cs1 : cs0, eps);
-    const KV k0 = (KV)x0, k1 = (KV)x1, v0 = (KV)xv[r][0], v1 = (KV)xv[r][1];
+    const KV k0 = to_cache<KV>(x0), k1 = to_cache<KV>(x1), v0 = to_cache<KV>(xv[r][0]),
+             v1 = to_cache<KV>(xv[r][1]);
     k[r][0] = (float)k0;
     k[r][1] = (float)k1;
     v[r][0] = (float)v0;

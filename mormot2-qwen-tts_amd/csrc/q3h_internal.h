@@ -42,6 +42,17 @@ __device__ __forceinline__ T *global_ptr(T *p) {
   return (T *)(__attribute__((address_space(1))) T *)(uintptr_t)p;
 }
 
+// x stored at the K/V cache's precision: its fp32 value rounded to KV. For a
+// half cache an empty asm keeps the compiler from folding the operation that
+// produced x (a RoPE fused multiply-add, a sum) into a mixed-precision
+// instruction that rounds once, straight to half, which can differ in the
+// last place
+template <typename KV>
+__device__ __forceinline__ KV to_cache(float x) {
+  if constexpr (sizeof(KV) == 2) asm volatile("" : "+v"(x));
+  return (KV)x;
+}
+
 // Context state that kernels read and advance on the device.
 struct CtxDev {
   void *k;

@@ -368,8 +368,8 @@ __global__ __launch_bounds__(kBlock) void k_qk_rope_append(
   void *base = j < heads + kvh ? d.k : d.v;
   KV *dst = global_ptr(reinterpret_cast<KV *>(base)) +
             (((size_t)layer * kvh + g) * d.max_pos + d.pos) * hd;
-  dst[lane] = (KV)x0;
-  dst[lane + half] = (KV)x1;
+  dst[lane] = to_cache<KV>(x0);
+  dst[lane + half] = to_cache<KV>(x1);
 }
 
 void launch_qk_rope_append(float *qkv, int ldq, const RowDesc *rd, int M, int layer,

@@ -83,11 +83,6 @@ __device__ __forceinline__ uint32_t order_key(float v) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// lane q's value (q uniform across the wave): a register read, no LDS trip
-__device__ __forceinline__ float lane_f(float v, int q) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), q));
-}
-
 constexpr int kSampleThreads = 1024;
 constexpr int kSampleMaxNPT = 3;  // up to 3072 values
 

@@ -62,6 +62,11 @@ __device__ __forceinline__ double wave_sum_dpp_d(double v) {
   return __builtin_bit_cast(double, ((long long)hi << 32) | (unsigned int)lo);
 }
 
+// lane q's value (q uniform across the wave): a register read, no LDS trip
+__device__ __forceinline__ float lane_f(float v, int q) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), q));
+}
+
 // inclusive prefix sum over the 64 lanes (lane i: lanes 0 .. i), exact for
 // integers: row scans by DPP row shifts, then the row totals broadcast by
 // row_bcast15 / row_bcast31
