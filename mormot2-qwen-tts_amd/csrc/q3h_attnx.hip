@@ -369,8 +369,7 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
         __fadd_rn(__fadd_rn(cv[0][j][k], cv[1][j][k]), __fadd_rn(cv[2][j][k], cv[3][j][k])),
         __fadd_rn(__fadd_rn(cv[4][j][k], cv[5][j][k]), __fadd_rn(cv[6][j][k], cv[7][j][k])));
     float amax = fabsf(o);
-#pragma unroll
-    for (int s2 = 16; s2 >= 1; s2 >>= 1) amax = fmaxf(amax, __shfl_xor(amax, s2));
+    amax = half_max_dpp(amax);
     const float dq = __fdiv_rn(amax, 127.0f);
     const float id = dq != 0.f ? __fdiv_rn(1.0f, dq) : 0.f;
     xq[qoff(h, k)] = (int8_t)(int)roundf(__fmul_rn(o, id));

@@ -206,8 +206,7 @@ __global__ __launch_bounds__(kQuantThreads) void k_quant_act(float *x, const flo
     for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[i][e]));
     // nch and the slice starts are multiples of 4, so a quad is wholly inside
     // or outside the row
-    amax = fmaxf(amax, __shfl_xor(amax, 1));
-    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    amax = quad_max_dpp(amax);
     if (j >= nch) continue;
     const float d = __fdiv_rn(amax, 127.0f);
     const float id = d != 0.f ? __fdiv_rn(1.0f, d) : 0.f;
@@ -441,8 +440,7 @@ __global__ __launch_bounds__(1024) void k_gemm_i8_swq(const int8_t *wq, const in
       o = silu_mul_ieee(gs, us);
     }
     float amax = fabsf(o);
-#pragma unroll
-    for (int s2 = 16; s2 >= 1; s2 >>= 1) amax = fmaxf(amax, __shfl_xor(amax, s2));
+    amax = half_max_dpp(amax);
     const float d = __fdiv_rn(amax, 127.0f);
     const float id = d != 0.f ? __fdiv_rn(1.0f, d) : 0.f;
     yq[qtile_offset(m, 32 * b + j, mt16)] = (int8_t)(int)roundf(__fmul_rn(o, id));

@@ -51,8 +51,7 @@ __device__ inline void quant_row_block(const float *x, const float *w, float eps
   float amax = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[e]));
-  amax = fmaxf(amax, __shfl_xor(amax, 1));
-  amax = fmaxf(amax, __shfl_xor(amax, 2));
+  amax = quad_max_dpp(amax);
   if (!on) return;
   const float d = __fdiv_rn(amax, 127.0f);
   const float id = d != 0.f ? __fdiv_rn(1.0f, d) : 0.f;

@@ -107,6 +107,23 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// maximum over the lane's quad (lanes 4 (l / 4) .. + 3), in every lane of it
+__device__ __forceinline__ float quad_max_dpp(float v) {
+  v = fmaxf(v, dpp_f_keep<kQuadXor1>(v));
+  return fmaxf(v, dpp_f_keep<kQuadXor2>(v));
+}
+
+// maximum over the lane's 32-lane half (rows 0-1 or 2-3): the row maximum by
+// DPP, then the other row's through gfx950's row swap (v_permlane16_swap)
+__device__ __forceinline__ float half_max_dpp(float v) {
+  v = quad_max_dpp(v);
+  v = fmaxf(v, dpp_f_keep<kHalfMirror>(v));
+  v = fmaxf(v, dpp_f_keep<kRowMirror>(v));
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, (unsigned)a[0]), __builtin_bit_cast(float, (unsigned)a[1]));
+}
+
 // v summed over the wave's four 16-lane rows at one place in the row (lanes
 // l, l ^ 16, l ^ 32, l ^ 48), in every lane: (v_l + v_l^16) + (v_l^32 +
 // v_l^48), the pairs in the same order as two xor shuffles by 16 and 32 add
