@@ -273,10 +273,10 @@ __device__ int block_sample(const float (&x)[NPT], int n, const SampleParams &p,
   }
   // 5. the draw. B_s is summed in lane 16 s of its row from the row's A_t
   // (DPP row shifts, in order); wave 0 runs the chain of the segment sums in
-  // every lane, lane q keeping the sum through segment q, so the first
-  // segment whose running sum passes the target is a ballot (the same sums
-  // and comparisons as a walk over the segments); the same over the threads
-  // of that segment
+  // registers and writes the running sums once, lane q reading the sum
+  // through segment q, so the first segment whose running sum passes the
+  // target is a ballot (the same sums and comparisons as a walk over the
+  // segments); the same over the threads of that segment
   float a = 0.0f;
 #pragma unroll
   for (int j = 0; j < NPT; j++) {
