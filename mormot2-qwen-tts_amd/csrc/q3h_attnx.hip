@@ -7,7 +7,7 @@
 // maximum), so this path computes every fp32 value in one documented order
 // instead of to a tolerance.
 //
-// One workgroup of 256 threads per (query head, row):
+// One workgroup per (kv head, row) for the kv head's query heads:
 //  - prologue (a decode row, one new position of its own context): q, k, v
 //    of the row (from the product's chunk partials, added in chunk order,
 //    when the product left them as partials); RMSNorm of q and of the new k
@@ -30,6 +30,7 @@
 // attention with head_dim 128, q head h reading kv head h / (heads / kv_heads).
 #include <hip/hip_runtime.h>
 
+#include "q3h_api_internal.h"
 #include "q3h_internal.h"
 #include "q3h_math.h"
 #include "q3h_wave.h"
@@ -120,7 +121,8 @@ __device__ __forceinline__ float row16_tree(float v) {
 template <typename KV, bool FUSED, int GRP, int SU, int VU, int NT, bool PV>
 __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *qkv,
                                                const float *qkn, const float2 *rope_cs,
-                                               int8_t *xq, int ldq, int layer, int nch) {
+                                               int8_t *xq, int layer, int nch, int kvh,
+                                               int M) {
   constexpr int NWV = NT / 64;
   constexpr int DPW = 16 / NWV;  // dims per lane in the value chains (2 or 1)
   static_assert(NWV % NCH == 0 && DPW * 64 * (NWV / NCH) == HD, "8 chains over 128 dims");
@@ -130,12 +132,22 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
   __shared__ float redf[GRP][NWV];
   __shared__ double redd[GRP][NWV];
   const int g = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
-  const int kvh = gridDim.x, heads = kvh * GRP, M = gridDim.y;
+  const int heads = kvh * GRP, ldq = (heads + 2 * kvh) * HD;
   const int lane = t & 63, wave = t >> 6;
   const int NQ = heads * HD, nbq = NQ >> 5, mt16 = (M + 15) >> 4;
   float *dx = reinterpret_cast<float *>(xq + (size_t)mt16 * 16 * NQ);
   // output k of query head h, row m: element (m, h * 128 + k) of the operand tiles
   auto qoff = [&](int h, int k) { return qtile_offset(m, h * HD + k, mt16); };
+  // vector j = wave: query head g GRP + j (j < GRP), the new k (j == GRP), v
+  // (GRP + 1); its loads depend on no descriptor, so they are issued first, by
+  // every wave (the waves past GRP + 1 load v again and do not use it: no
+  // divergent branch before the descriptor's scalar load)
+  static_assert(GRP + 2 <= NWV, "one prologue vector per wave");
+  const int j = wave;
+  const bool pj = FUSED && j < GRP + 2;
+  const int col = j < GRP ? (g * GRP + j) * HD : j == GRP ? NQ + g * HD : NQ + (kvh + g) * HD;
+  float pa[4], pb[4];
+  if (FUSED) qkv_load(qkv, ldq, nch, M, m, col + lane, pa, pb);
   const RowDesc d = rd[m];
   if (d.pos < 0) {  // inactive row: zero blocks
     for (int i = t; i < GRP * HD; i += NT) {
@@ -154,13 +166,6 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
   // value chain ch over positions ch, ch + 8, ...; dims dim0 + 64 e, e < DPW
   const int ch = wave % NCH, dim0 = (wave / NCH) * 64 + lane;
 
-  static_assert(GRP + 2 <= NWV, "one prologue vector per wave");
-  // vector j = wave: query head g GRP + j (j < GRP), the new k (j == GRP), v (GRP + 1)
-  const int j = wave;
-  const bool pj = FUSED && j < GRP + 2;
-  const int col = j < GRP ? (g * GRP + j) * HD : j == GRP ? NQ + g * HD : NQ + (kvh + g) * HD;
-  float pa[4], pb[4];
-  if (pj) qkv_load(qkv, ldq, nch, M, m, col + lane, pa, pb);
   // the first round of keys (positions u KG + kg) and values (ch + NCH u),
   // from clamped positions
   float k8p[SU][8], vp[PV ? VU : 1][DPW];
@@ -390,10 +395,14 @@ void attn_x_grp(const AttnArgs &a, int M, int nch, const QAct &xa, int max_posit
                 hipStream_t st) {
   const dim3 grid(a.kvh, M);
   const int grp = a.heads / a.kvh;
+  // the kernel takes the q/k/v row stride as (heads + 2 kv heads) * 128, so
+  // that its arguments fit the 14 dwords preloaded in SGPRs (the grid size,
+  // a hidden argument past them, would be a dependent load before the first)
+  require(a.ldq == (a.heads + 2 * a.kvh) * HD, Q3H_E_ARG, "attention: q/k/v rows not packed");
   const size_t lds = sizeof(float) * (size_t)grp * max_positions;
 #define Q3H_ATTNX(G)                                                                           \
   hipLaunchKernelGGL((k_attn_x<KV, F, G, SU, VU, NT, PV>), grid, dim3(NT), lds, st, a.rd, a.qkv,  \
-                     a.qkn, a.rope_cs, xa.q, a.ldq, a.layer, nch)
+                     a.qkn, a.rope_cs, xa.q, a.layer, nch, a.kvh, M)
   if (grp == 1)
     Q3H_ATTNX(1);
   else if (grp == 2)
@@ -415,7 +424,7 @@ void attn_x_len(const AttnArgs &a, int M, int nch, const QAct &xa, int max_posit
                 hipStream_t st) {
   if (max_positions <= 32)
     attn_x_grp<KV, F, 1, 4, 512, true>(a, M, nch, xa, max_positions, st);
-  else if (F)
+  else if constexpr (F)
     attn_x_grp<KV, F, 4, 8, 512, true>(a, M, nch, xa, max_positions, st);
   else
     attn_x_grp<KV, F, 8, 16, 512, false>(a, M, nch, xa, max_positions, st);
