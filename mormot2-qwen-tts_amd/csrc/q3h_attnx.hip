@@ -30,6 +30,8 @@
 // attention with head_dim 128, q head h reading kv head h / (heads / kv_heads).
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "q3h_api_internal.h"
 #include "q3h_internal.h"
 #include "q3h_math.h"
@@ -125,6 +127,9 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
                                                int M) {
   constexpr int NWV = NT / 64;
   constexpr int DPW = 16 / NWV;  // dims per lane in the value chains (2 or 1)
+  // the launch shapes for contexts of several rounds take unmasked rounds
+  // before the row's own position (the short-context shape keeps one code path)
+  constexpr bool LONG = SU > 1;
   static_assert(NWV % NCH == 0 && DPW * 64 * (NWV / NCH) == HD, "8 chains over 128 dims");
   extern __shared__ float sc[];  // [GRP][L]: scores, then e^(score - max)
   __shared__ float qs[GRP][HD], kn[HD], vn[HD];
@@ -237,25 +242,35 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
         for (int u = 0; u < SU; u++)
           load8(kc + (size_t)min(p0 + u * KG + kg, L - 1) * HD + 8 * li, k8[u]);
       }
+      // a round wholly before the row's own position needs no masks
+      auto round = [&](auto masked) {
+        constexpr bool MK = decltype(masked)::value;
+        if constexpr (MK) {
 #pragma unroll
-      for (int u = 0; u < SU; u++) {
-        const int p = p0 + u * KG + kg;
+          for (int u = 0; u < SU; u++) {
+            const int p = p0 + u * KG + kg;
 #pragma unroll
-        for (int e = 0; e < 8; e++)
-          k8[u][e] = p >= L ? 0.f : FUSED && p == pos ? kn8[e] : k8[u][e];
-      }
-#pragma unroll
-      for (int u = 0; u < SU; u++) {
-        const int p = p0 + u * KG + kg;
-#pragma unroll
-        for (int j = 0; j < GRP; j++) {
-          float a = 0.f;
-#pragma unroll
-          for (int e = 0; e < 8; e++) a = fmaf(qv[j][e], k8[u][e], a);
-          a = row16_tree(a);
-          if (p < L && li == 0) sc[j * L + p] = __fmul_rn(a, scale);
+            for (int e = 0; e < 8; e++)
+              k8[u][e] = p >= L ? 0.f : FUSED && p == pos ? kn8[e] : k8[u][e];
+          }
         }
-      }
+#pragma unroll
+        for (int u = 0; u < SU; u++) {
+          const int p = p0 + u * KG + kg;
+#pragma unroll
+          for (int j = 0; j < GRP; j++) {
+            float a = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) a = fmaf(qv[j][e], k8[u][e], a);
+            a = row16_tree(a);
+            if ((!MK || p < L) && li == 0) sc[j * L + p] = __fmul_rn(a, scale);
+          }
+        }
+      };
+      if (LONG && p0 + KG * SU <= (FUSED ? pos : L))
+        round(std::false_type{});
+      else
+        round(std::true_type{});
     }
   }
   __syncthreads();
@@ -333,32 +348,41 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
             v[u][e] = (float)vc[(size_t)min(p0 + NCH * u, L - 1) * HD + dim0 + 64 * e];
       }
       // the new position: its own v; past L: zero (the clamped load may have
-      // read the new row before it was written)
+      // read the new row before it was written); weights of the round read
+      // together, past L a zero weight times a zero value adds an exact zero to
+      // the chain. A round wholly before the row's own position needs no masks.
+      auto round = [&](auto masked) {
+        constexpr bool MK = decltype(masked)::value;
+        if constexpr (MK) {
 #pragma unroll
-      for (int u = 0; u < VU; u++) {
-        const int p = p0 + NCH * u;
+          for (int u = 0; u < VU; u++) {
+            const int p = p0 + NCH * u;
 #pragma unroll
-        for (int e = 0; e < DPW; e++)
-          v[u][e] = p >= L ? 0.f : FUSED && p == pos ? vnd[e] : v[u][e];
-      }
-      // weights of the round read together; past L a zero weight times a zero
-      // value adds an exact zero to the chain
-      float wgt[VU][GRP];
-#pragma unroll
-      for (int u = 0; u < VU; u++) {
-        const int p = p0 + NCH * u;  // the same for the whole wave
-#pragma unroll
-        for (int j = 0; j < GRP; j++) {
-          const float e = sc[j * L + min(p, L - 1)];
-          wgt[u][j] = p < L ? __fmul_rn(e, inv[j]) : 0.f;
+            for (int e = 0; e < DPW; e++)
+              v[u][e] = p >= L ? 0.f : FUSED && p == pos ? vnd[e] : v[u][e];
+          }
         }
-      }
+        float wgt[VU][GRP];
 #pragma unroll
-      for (int u = 0; u < VU; u++)
+        for (int u = 0; u < VU; u++) {
+          const int p = p0 + NCH * u;  // the same for the whole wave
 #pragma unroll
-        for (int j = 0; j < GRP; j++)
+          for (int j = 0; j < GRP; j++) {
+            const float e = sc[j * L + (MK ? min(p, L - 1) : p)];
+            wgt[u][j] = !MK || p < L ? __fmul_rn(e, inv[j]) : 0.f;
+          }
+        }
 #pragma unroll
-          for (int e = 0; e < DPW; e++) c[e][j] = fmaf(wgt[u][j], v[u][e], c[e][j]);
+        for (int u = 0; u < VU; u++)
+#pragma unroll
+          for (int j = 0; j < GRP; j++)
+#pragma unroll
+            for (int e = 0; e < DPW; e++) c[e][j] = fmaf(wgt[u][j], v[u][e], c[e][j]);
+      };
+      if (LONG && p0 + NCH * (VU - 1) < (FUSED ? pos : L))
+        round(std::false_type{});
+      else
+        round(std::true_type{});
     }
 #pragma unroll
     for (int j = 0; j < GRP; j++)
