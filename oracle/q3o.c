@@ -16,8 +16,9 @@
  *    into a chain over the 8 blocks of each 256-column chunk; the chunk sums
  *    added in chunk order;
  *  - attention scores: q . k as 16 partial chains (dims 8l .. 8l + 7) joined
- *    by a balanced pairwise tree; weighted values: 4 chains over the
- *    positions p = j mod 4, joined as (c0 + c1) + (c2 + c3);
+ *    by a balanced pairwise tree; weighted values: 8 chains over the
+ *    positions p = j mod 8, joined as ((c0 + c1) + (c2 + c3)) +
+ *    ((c4 + c5) + (c6 + c7));
  *  - e^x: q3o_expf (Cody-Waite reduction, Taylor series), in the softmax and
  *    in SiLU;
  *  - RMSNorm, softmax sums: double accumulation, results rounded to fp32 (the
