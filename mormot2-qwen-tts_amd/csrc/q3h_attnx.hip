@@ -276,8 +276,22 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
   __syncthreads();
 
   // softmax per head
-  float inv[GRP];
-  {
+  float inv[GRP], ew[GRP];
+  if constexpr (!LONG) {
+    // the one-round shape (covers of at most 32 positions): one wave holds a
+    // head's scores, one per lane, so every wave takes the maximum, the
+    // exponentials and the double sum itself (no barrier, no LDS trip) and
+    // keeps its lane's exponential for the value weights
+#pragma unroll
+    for (int j = 0; j < GRP; j++) {
+      const float sv = lane < L ? sc[j * L + lane] : -INFINITY;
+      const float mx = wave_max_dpp(sv);
+      ew[j] = lane < L ? exp_ieee(__fsub_rn(sv, mx)) : 0.f;
+      inv[j] = (float)(1.0 / wave_sum_dpp_d((double)ew[j]));
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < GRP; j++) ew[j] = 0.f;
     float mx[GRP];
 #pragma unroll
     for (int j = 0; j < GRP; j++) mx[j] = -INFINITY;
@@ -368,7 +382,7 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
           const int p = p0 + NCH * u;  // the same for the whole wave
 #pragma unroll
           for (int j = 0; j < GRP; j++) {
-            const float e = sc[j * L + (MK ? min(p, L - 1) : p)];
+            const float e = LONG ? sc[j * L + (MK ? min(p, L - 1) : p)] : lane_f(ew[j], min(p, L - 1));
             wgt[u][j] = !MK || p < L ? __fmul_rn(e, inv[j]) : 0.f;
           }
         }
