@@ -172,7 +172,7 @@ static void probe_layer(const LayerIO &io, const Work &w, int l, int M, int H, h
 }
 
 // The int8 path over M <= kPartialRows rows: every product leaves its chunk
-// partials (one wave per 16 rows and 256 columns over the whole chip), and
+// partials (one wave per 16 rows and 512 columns over the whole chip), and
 // the consumer adds them in chunk order: the attention prologue (q/k/v, decode
 // rows), the residual add + RMSNorm + quantization of the next input (o_proj,
 // down), SiLU(gate) * up + quantization (gate/up). Results equal the
@@ -291,7 +291,7 @@ static void run_layers_f32(const q3h_stack *s, Work &w, int M, int positions, bo
 // The layers of a stack over M rows of w.h, n contexts of R rows each (M =
 // n * R), their descriptors already in w.rd: the per-layer kernel sequence.
 bool partial_path(const q3h_stack *s, int M) {
-  return s->cfg.act_q8 && M <= kPartialRows && gemm_i8_chunks(s->cfg.hidden) <= 4;
+  return s->cfg.act_q8 && M <= kPartialRows && gemm_i8_chunks(s->cfg.hidden) <= kPartialSlots;
 }
 
 void run_layers(const q3h_stack *s, Work &w, int M, int positions, bool fused, hipStream_t st,

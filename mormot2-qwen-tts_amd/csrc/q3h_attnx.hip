@@ -70,24 +70,25 @@ __device__ __forceinline__ float2 load2(const KV *p) {
 }
 
 // elements col and col + 64 of row m: the product's output, or (nch > 0)
-// its chunk partials [nch][M][ld] (nch <= 4), loaded together (clamped chunk
-// indices; qkv_sum adds the first nch in chunk order)
+// its chunk partials [nch][M][ld] (nch <= kPartialSlots), loaded together
+// (clamped chunk indices; qkv_sum adds the first nch in chunk order)
+constexpr int NPS = kPartialSlots;
 __device__ __forceinline__ void qkv_load(const float *qkv, int ld, int nch, int M, int m, int col,
-                                         float (&a)[4], float (&b)[4]) {
+                                         float (&a)[NPS], float (&b)[NPS]) {
   if (nch == 0) {
     a[0] = qkv[(size_t)m * ld + col];
     b[0] = qkv[(size_t)m * ld + col + 64];
     return;
   }
 #pragma unroll
-  for (int c = 0; c < 4; c++) {
+  for (int c = 0; c < NPS; c++) {
     const float *r = qkv + ((size_t)min(c, nch - 1) * M + m) * ld + col;
     a[c] = r[0];
     b[c] = r[64];
   }
 }
 
-__device__ __forceinline__ void qkv_sum(int nch, const float (&a)[4], const float (&b)[4],
+__device__ __forceinline__ void qkv_sum(int nch, const float (&a)[NPS], const float (&b)[NPS],
                                         float &x0, float &x1) {
   if (nch == 0) {
     x0 = a[0];
@@ -96,7 +97,7 @@ __device__ __forceinline__ void qkv_sum(int nch, const float (&a)[4], const floa
   }
   x0 = x1 = 0.f;
 #pragma unroll
-  for (int c = 0; c < 4; c++) {
+  for (int c = 0; c < NPS; c++) {
     x0 = c < nch ? __fadd_rn(x0, a[c]) : x0;
     x1 = c < nch ? __fadd_rn(x1, b[c]) : x1;
   }
@@ -151,7 +152,7 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
   const int j = wave;
   const bool pj = FUSED && j < GRP + 2;
   const int col = j < GRP ? (g * GRP + j) * HD : j == GRP ? NQ + g * HD : NQ + (kvh + g) * HD;
-  float pa[4], pb[4];
+  float pa[NPS], pb[NPS];
   if (FUSED) qkv_load(qkv, ldq, nch, M, m, col + lane, pa, pb);
   const RowDesc d = rd[m];
   if (d.pos < 0) {  // inactive row: zero blocks

@@ -294,16 +294,17 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
     return;
   }
   const int R = g == 0 ? 2 : 1, rows = R * f.n, row = R * s + R - 1;
-  // the head's logit i: the chunk partials (cp_hch <= 4) loaded together,
-  // added in chunk order
+  // the head's logit i: the chunk partials (cp_hch <= kPartialSlots) loaded
+  // together, added in chunk order
+  constexpr int NPS = kPartialSlots;
   auto logit = [&](int i) {
-    float p4[4];
+    float p4[NPS];
 #pragma unroll
-    for (int c = 0; c < 4; c++)
+    for (int c = 0; c < NPS; c++)
       p4[c] = f.cp_part[((size_t)min(c, f.cp_hch - 1) * rows + row) * f.cp_vocab + i];
     float v = 0.f;
 #pragma unroll
-    for (int c = 0; c < 4; c++) v = c < f.cp_hch ? __fadd_rn(v, p4[c]) : v;
+    for (int c = 0; c < NPS; c++) v = c < f.cp_hch ? __fadd_rn(v, p4[c]) : v;
     return v;
   };
   int code;
@@ -312,21 +313,21 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
   } else {
     // every partial of the logits this thread merges, and of logit 0, loaded
     // before the first sum (as in k_choose_code0)
-    float pl[kArgUnroll][4], p0[4];
+    float pl[kArgUnroll][NPS], p0[NPS];
 #pragma unroll
     for (int k = 0; k < kArgUnroll; k++) {
       const int i = min(tid + k * kArgBlock, f.cp_vocab - 1);
 #pragma unroll
-      for (int c = 0; c < 4; c++)
+      for (int c = 0; c < NPS; c++)
         pl[k][c] = f.cp_part[((size_t)min(c, f.cp_hch - 1) * rows + row) * f.cp_vocab + i];
     }
 #pragma unroll
-    for (int c = 0; c < 4; c++)
+    for (int c = 0; c < NPS; c++)
       p0[c] = f.cp_part[((size_t)min(c, f.cp_hch - 1) * rows + row) * f.cp_vocab];
-    auto chunk_sum = [&](const float(&p4)[4]) {
+    auto chunk_sum = [&](const float(&p4)[NPS]) {
       float v = 0.f;
 #pragma unroll
-      for (int c = 0; c < 4; c++) v = c < f.cp_hch ? __fadd_rn(v, p4[c]) : v;
+      for (int c = 0; c < NPS; c++) v = c < f.cp_hch ? __fadd_rn(v, p4[c]) : v;
       return v;
     };
     float bv = -INFINITY;

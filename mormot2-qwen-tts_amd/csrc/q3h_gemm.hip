@@ -7,8 +7,8 @@
 // vec_dot_q8_0_q8_0).
 //
 // Evaluation order (fixed, so that the products equal a CPU evaluation in the
-// same order to the bit): per output, one fused multiply-add chain over the 8
-// blocks of each 256-column chunk, acc = fma((float)dot_b, d_w * d_x, acc)
+// same order to the bit): per output, one fused multiply-add chain over the
+// 16 blocks of each 512-column chunk, acc = fma((float)dot_b, d_w * d_x, acc)
 // from 0 in block order, and the chunk sums added in chunk order.
 //
 // Operand layouts (v_mfma_i32_16x16x32_i8, wave64): lane l holds 8 int8 of
@@ -36,7 +36,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kQuantThreads = 128;
 constexpr int kQuantChunks = 3;  // 8-element chunks per thread: K <= 3072
-constexpr int kMaxChunks = 12;   // 256-column chunks of a product: K <= 3072
+constexpr int kChunkBlocks = 16;  // 32-blocks per chunk of a product (512 columns)
+constexpr int kMaxChunks = 6;     // chunks of a product: K <= 3072
 
 __device__ __forceinline__ float *scales_of(int8_t *xq, int M, int K) {
   return reinterpret_cast<float *>(xq + (size_t)((M + 15) & ~15) * K);
@@ -52,7 +53,7 @@ __device__ __forceinline__ float *scales_of(int8_t *xq, int M, int K) {
 //              of a product with N = K, added in chunk order), written back
 //              to x (the residual stream, row stride K);
 //  SRC_SWIGLU: silu(sum_c part[c][m][2k]) * sum_c part[c][m][2k + 1] (c < ld
-//              <= 4 partials; gate / up interleaved, N = 2K).
+//              <= 2 partials; gate / up interleaved, N = 2K).
 // Then RMSNorm when norm_w != nullptr (one slice only): y = w * (x * inv),
 // inv = 1/sqrt(mean(x^2) + eps) with the sum of squares in double; xn_out,
 // when non-null, receives the (normed) row M - 1; and the Q8_0 blocks
@@ -221,20 +222,17 @@ __global__ __launch_bounds__(kQuantThreads) void k_quant_act(float *x, const flo
   }
 }
 
-// The fused multiply-add chains of 8 blocks from their operands: A av[i]
-// (16 weight rows), B bv[t][i] (16 activation rows of tile t), the weight
-// scales of the lane's 4 rows dwv[r][i] and the activation scales of its row
-// dxv[t][i]: acc[t][r] = fma((float)dot, d_w * d_x, acc) from 0 in block order.
-template <int TM>
-__device__ __forceinline__ void chains8(const long (&av)[8], const long (&bv)[TM][8],
-                                        const float (&dwv)[4][8], const float (&dxv)[TM][8],
-                                        float (&acc)[TM][4]) {
+// The fused multiply-add chains over NB blocks from their operands, continuing
+// acc: A av[i] (16 weight rows), B bv[t][i] (16 activation rows of tile t),
+// the weight scales of the lane's 4 rows dwv[r][i] and the activation scales
+// of its row dxv[t][i]: acc[t][r] = fma((float)dot, d_w * d_x, acc) in block
+// order.
+template <int TM, int NB>
+__device__ __forceinline__ void chains(const long (&av)[NB], const long (&bv)[TM][NB],
+                                       const float (&dwv)[4][NB], const float (&dxv)[TM][NB],
+                                       float (&acc)[TM][4]) {
 #pragma unroll
-  for (int t = 0; t < TM; t++)
-#pragma unroll
-    for (int r = 0; r < 4; r++) acc[t][r] = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
+  for (int i = 0; i < NB; i++) {
 #pragma unroll
     for (int t = 0; t < TM; t++) {
       const v4i ci =
@@ -246,78 +244,89 @@ __device__ __forceinline__ void chains8(const long (&av)[8], const long (&bv)[TM
   }
 }
 
-// The chains of one 256-column chunk (blocks b0 .. b0 + 7, K % 256 == 0) for
-// 16 weight rows from n0 and the activation tiles mt0 .. mt0 + TM - 1:
+// The chains of NB blocks (b0 .. b0 + NB - 1, K % 512 == 0), continuing acc,
+// for 16 weight rows from n0 and the activation tiles mt0 .. mt0 + TM - 1:
 // acc[t][r] = output (n0 + 4 (lane / 16) + r, 16 (mt0 + t) + lane % 16); a
 // tile past the last (mt16) repeats the last one and its outputs are not
 // stored. All loads are unconditional and issued before the first MFMA (a
 // guarded load would make the compiler wait for each one). LDSA: the weight
 // tile is read with 16-byte loads (4 rows x 256 bytes per instruction instead
-// of 16 rows x 32 bytes) and rearranged through the wave's own 16 x 33 longs
-// of LDS (at).
-template <int TM, bool LDSA>
+// of 16 rows x 32 bytes) and rearranged through the wave's own 16 x (4 NB + 1)
+// longs of LDS (at).
+template <int TM, bool LDSA, int NB>
 __device__ __forceinline__ void chunk_chains(const int8_t *wq, const int8_t *xq, const float *dx,
                                              int N, int K, int n0, int mt0, int mt16, int b0,
-                                             long (*at)[33], float (&acc)[TM][4]) {
+                                             long (*at)[4 * NB + 1], float (&acc)[TM][4]) {
+  static_assert(NB % 8 == 0, "whole 8-block groups");
+  constexpr int NH = NB / 8;  // 256-byte pieces of a weight row
   const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
   const int nb = K >> 5;
   const _Float16 *wd = reinterpret_cast<const _Float16 *>(wq + (size_t)N * K);
   const int4 *xq16 = reinterpret_cast<const int4 *>(xq);
-  long av[8], bv[TM][8];
-  float dwv[4][8], dxv[TM][8];
-  int4 araw[4];
+  long av[NB], bv[TM][NB];
+  float dwv[4][NB], dxv[TM][NB];
+  int4 araw[4 * NH];
   if (LDSA) {
 #pragma unroll
-    for (int i = 0; i < 4; i++)  // rows 4i + lane / 16, bytes 16 (lane % 16) of the chunk
-      araw[i] = *reinterpret_cast<const int4 *>(wq + (size_t)(n0 + 4 * i + (lane >> 4)) * K +
-                                                b0 * 32 + 16 * (lane & 15));
+    for (int i = 0; i < 4; i++)  // rows 4i + lane / 16, bytes 256 h + 16 (lane % 16) of the chunk
+#pragma unroll
+      for (int h = 0; h < NH; h++)
+        araw[i * NH + h] = *reinterpret_cast<const int4 *>(
+            wq + (size_t)(n0 + 4 * i + (lane >> 4)) * K + b0 * 32 + 256 * h + 16 * (lane & 15));
   } else {
     const int8_t *wr = wq + (size_t)(n0 + c) * K + 8 * g;
 #pragma unroll
-    for (int i = 0; i < 8; i++) av[i] = *reinterpret_cast<const long *>(wr + 32 * (b0 + i));
+    for (int i = 0; i < NB; i++) av[i] = *reinterpret_cast<const long *>(wr + 32 * (b0 + i));
   }
 #pragma unroll
   for (int t = 0; t < TM; t++) {
     const int tt = min(mt0 + t, mt16 - 1);
 #pragma unroll
-    for (int q = 0; q < 4; q++) {  // blocks b0 + 2q, b0 + 2q + 1
+    for (int q = 0; q < NB / 2; q++) {  // blocks b0 + 2q, b0 + 2q + 1
       const int4 v = xq16[((size_t)((b0 >> 1) + q) * mt16 + tt) * 64 + lane];
       bv[t][2 * q] = ((long)(unsigned)v.y << 32) | (unsigned)v.x;
       bv[t][2 * q + 1] = ((long)(unsigned)v.w << 32) | (unsigned)v.z;
     }
   }
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const uint4 u = *reinterpret_cast<const uint4 *>(wd + (size_t)(n0 + 4 * g + r) * nb + b0);
-    const unsigned uw[4] = {u.x, u.y, u.z, u.w};
+  for (int r = 0; r < 4; r++)
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      dwv[r][2 * i] = (float)__builtin_bit_cast(_Float16, (unsigned short)(uw[i] & 0xffff));
-      dwv[r][2 * i + 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(uw[i] >> 16));
+    for (int h = 0; h < NH; h++) {
+      const uint4 u =
+          *reinterpret_cast<const uint4 *>(wd + (size_t)(n0 + 4 * g + r) * nb + b0 + 8 * h);
+      const unsigned uw[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        dwv[r][8 * h + 2 * i] = (float)__builtin_bit_cast(_Float16, (unsigned short)(uw[i] & 0xffff));
+        dwv[r][8 * h + 2 * i + 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(uw[i] >> 16));
+      }
     }
-  }
 #pragma unroll
   for (int t = 0; t < TM; t++) {
     const int tt = min(mt0 + t, mt16 - 1);
     const float4 *dp = reinterpret_cast<const float4 *>(dx + (size_t)(tt * 16 + c) * nb + b0);
-    const float4 p = dp[0], q = dp[1];
-    dxv[t][0] = p.x, dxv[t][1] = p.y, dxv[t][2] = p.z, dxv[t][3] = p.w;
-    dxv[t][4] = q.x, dxv[t][5] = q.y, dxv[t][6] = q.z, dxv[t][7] = q.w;
+#pragma unroll
+    for (int q = 0; q < NB / 4; q++) {
+      const float4 p = dp[q];
+      dxv[t][4 * q] = p.x, dxv[t][4 * q + 1] = p.y, dxv[t][4 * q + 2] = p.z, dxv[t][4 * q + 3] = p.w;
+    }
   }
   if (LDSA) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int row = 4 * i + (lane >> 4), l2 = 2 * (lane & 15);
-      at[row][l2] = ((long)(unsigned)araw[i].y << 32) | (unsigned)araw[i].x;
-      at[row][l2 + 1] = ((long)(unsigned)araw[i].w << 32) | (unsigned)araw[i].z;
-    }
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int h = 0; h < NH; h++) {
+        const int row = 4 * i + (lane >> 4), l2 = 32 * h + 2 * (lane & 15);
+        at[row][l2] = ((long)(unsigned)araw[i * NH + h].y << 32) | (unsigned)araw[i * NH + h].x;
+        at[row][l2 + 1] = ((long)(unsigned)araw[i * NH + h].w << 32) | (unsigned)araw[i * NH + h].z;
+      }
     // the wave reads back only what it wrote itself (LDS keeps a wave's order)
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int i = 0; i < 8; i++) av[i] = at[c][4 * i + g];  // row c, bytes 32 i + 8 g
+    for (int i = 0; i < NB; i++) av[i] = at[c][4 * i + g];  // row c, bytes 32 i + 8 g
   }
   __builtin_amdgcn_sched_barrier(0);
-  chains8<TM>(av, bv, dwv, dxv, acc);
+  chains<TM, NB>(av, bv, dwv, dxv, acc);
 }
 
 // y[m][n] (+)= sum_b d_w[n][b] d_x[m][b] sum_{k in b} q_w[n][k] q_x[m][k].
@@ -330,15 +339,23 @@ __global__ __launch_bounds__(KW * 64) void k_gemm_i8(const int8_t *wq, const int
                                                       float *y, int N, int K, int M, int ldy) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int g = lane >> 4, c = lane & 15;
-  const int nb = K >> 5, nch = (nb + 7) >> 3;
+  const int nb = K >> 5, nch = nb / kChunkBlocks;
   const int mt16 = (M + 15) >> 4;
   const int n0 = blockIdx.x * 16, mt0 = blockIdx.y * TM;
   const float *dx = scales_of(const_cast<int8_t *>(xq), M, K);
   constexpr int LD = TM * 16 + 4;
   __shared__ float red[kMaxChunks][16][LD];
   for (int ch = w; ch < nch; ch += KW) {
+    // a chunk's chain as two passes of 8 blocks (the second continues it):
+    // TM tiles of 16 blocks would not fit the registers
     float acc[TM][4];
-    chunk_chains<TM, false>(wq, xq, dx, N, K, n0, mt0, mt16, ch * 8, nullptr, acc);
+#pragma unroll
+    for (int t = 0; t < TM; t++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) acc[t][r] = 0.f;
+    chunk_chains<TM, false, 8>(wq, xq, dx, N, K, n0, mt0, mt16, ch * kChunkBlocks, nullptr, acc);
+    chunk_chains<TM, false, 8>(wq, xq, dx, N, K, n0, mt0, mt16, ch * kChunkBlocks + 8, nullptr,
+                               acc);
 #pragma unroll
     for (int t = 0; t < TM; t++)
 #pragma unroll
@@ -383,9 +400,14 @@ __global__ __launch_bounds__(64) void k_gemm_i8p(const int8_t *wq, const int8_t 
   const int n0 = blockIdx.x * 16, ch = blockIdx.y, mt0 = blockIdx.z * TM;
   const int mt16 = (M + 15) >> 4;
   const float *dx = scales_of(const_cast<int8_t *>(xq), M, K);
-  __shared__ long at[16][33];
+  __shared__ long at[16][4 * kChunkBlocks + 1];
   float acc[TM][4];
-  chunk_chains<TM, true>(wq, xq, dx, N, K, n0, mt0, mt16, ch * 8, at, acc);
+#pragma unroll
+  for (int t = 0; t < TM; t++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) acc[t][r] = 0.f;
+  chunk_chains<TM, true, kChunkBlocks>(wq, xq, dx, N, K, n0, mt0, mt16, ch * kChunkBlocks, at,
+                                       acc);
 #pragma unroll
   for (int t = 0; t < TM; t++) {
     const int m = (mt0 + t) * 16 + c;
@@ -397,7 +419,7 @@ __global__ __launch_bounds__(64) void k_gemm_i8p(const int8_t *wq, const int8_t 
 
 // The gate/up product with SiLU(gate) * up and the quantization of the result
 // fused: a workgroup owns 64 gate/up rows, i.e. one 32-block of the output,
-// its 4 chunks (a wave per (16 rows, chunk), K == 1024) and the TM 16-row
+// its 2 chunks (a wave per (16 rows, chunk), K == 1024) and the TM 16-row
 // activation tiles from TM blockIdx.y; the chunk chains meet in LDS and are
 // added in chunk order, then each row's block is quantized into yq (yq must
 // not alias xq). The same values as k_gemm_i8p followed by
@@ -405,11 +427,11 @@ __global__ __launch_bounds__(64) void k_gemm_i8p(const int8_t *wq, const int8_t 
 // tiles are gridDim.x apart (a multiple of 8 for the Qwen3-TTS shapes: one
 // XCD, one L2 for the weights).
 template <int TM>
-__global__ __launch_bounds__(1024) void k_gemm_i8_swq(const int8_t *wq, const int8_t *xq,
-                                                      int8_t *yq, int N, int M) {
-  constexpr int K = 1024, LD = TM * 16 + 4;
-  __shared__ float red[4][64][LD];
-  __shared__ long at[16][16][33];
+__global__ __launch_bounds__(512) void k_gemm_i8_swq(const int8_t *wq, const int8_t *xq,
+                                                     int8_t *yq, int N, int M) {
+  constexpr int K = 1024, LD = TM * 16 + 4, NCH = K / (32 * kChunkBlocks);
+  __shared__ float red[NCH][64][LD];
+  __shared__ long at[4 * NCH][16][4 * kChunkBlocks + 1];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int g = lane >> 4, c = lane & 15;
   const int mt16 = (M + 15) >> 4, mt0 = blockIdx.y * TM;
@@ -417,7 +439,12 @@ __global__ __launch_bounds__(1024) void k_gemm_i8_swq(const int8_t *wq, const in
   const int n0 = blockIdx.x * 64 + tile * 16;
   const float *dx = scales_of(const_cast<int8_t *>(xq), M, K);
   float acc[TM][4];
-  chunk_chains<TM, true>(wq, xq, dx, N, K, n0, mt0, mt16, ch * 8, at[w], acc);
+#pragma unroll
+  for (int t = 0; t < TM; t++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) acc[t][r] = 0.f;
+  chunk_chains<TM, true, kChunkBlocks>(wq, xq, dx, N, K, n0, mt0, mt16, ch * kChunkBlocks, at[w],
+                                       acc);
 #pragma unroll
   for (int t = 0; t < TM; t++)
 #pragma unroll
@@ -427,13 +454,13 @@ __global__ __launch_bounds__(1024) void k_gemm_i8_swq(const int8_t *wq, const in
   const int KO = N >> 1, nbo = KO >> 5, b = blockIdx.x;
   float *dy = scales_of(yq, M, KO);
   const int nrow = min(TM, mt16 - mt0) * 16;
-  for (int idx = threadIdx.x; idx < nrow * 32; idx += 1024) {
+  for (int idx = threadIdx.x; idx < nrow * 32; idx += 64 * 4 * NCH) {
     const int ml = idx >> 5, j = idx & 31, m = mt0 * 16 + ml;
     float o = 0.f;
     if (m < M) {
       float gs = 0.f, us = 0.f;
 #pragma unroll
-      for (int v = 0; v < 4; v++) {
+      for (int v = 0; v < NCH; v++) {
         gs = __fadd_rn(gs, red[v][2 * j][ml]);
         us = __fadd_rn(us, red[v][2 * j + 1][ml]);
       }
@@ -467,13 +494,14 @@ void gemm_launch(const Mat &W, const QAct &xa, int M, int epi, float *y, int ldy
 
 template <int TM>
 void gemm_by_k(const Mat &W, const QAct &xa, int M, int epi, float *y, int ldy, hipStream_t st) {
-  const int nch = (W.K / 32 + 7) / 8;
-  if (TM <= 2 && nch >= 12)
-    gemm_launch<TM, (TM <= 2 ? 12 : 8)>(W, xa, M, epi, y, ldy, st);
-  else if (nch >= 8)
-    gemm_launch<TM, 8>(W, xa, M, epi, y, ldy, st);
-  else
+  // a wave per chunk
+  const int nch = W.K / (32 * kChunkBlocks);
+  if (nch >= 6)
+    gemm_launch<TM, 6>(W, xa, M, epi, y, ldy, st);
+  else if (nch >= 4)
     gemm_launch<TM, 4>(W, xa, M, epi, y, ldy, st);
+  else
+    gemm_launch<TM, 2>(W, xa, M, epi, y, ldy, st);
 }
 
 // slices > 1 only without a norm (each slice a whole number of 32-blocks)
@@ -498,21 +526,22 @@ void quant_launch_nc(float *x, const float *part, int ld, int M, int K, const fl
 template <int SRC>
 void quant_launch(float *x, const float *part, int ld, int M, int K, const float *norm_w,
                   float eps, const QAct &out, float *xn_out, hipStream_t st, int slices = 1) {
-  if (SRC == SRC_X || ld <= 4)
+  if (SRC == SRC_X || ld <= 2)
+    quant_launch_nc<SRC, 2>(x, part, ld, M, K, norm_w, eps, out, xn_out, st, slices);
+  else if (ld <= 4)
     quant_launch_nc<SRC, 4>(x, part, ld, M, K, norm_w, eps, out, xn_out, st, slices);
-  else if (ld <= 8)
-    quant_launch_nc<SRC, 8>(x, part, ld, M, K, norm_w, eps, out, xn_out, st, slices);
   else
-    quant_launch_nc<SRC, 12>(x, part, ld, M, K, norm_w, eps, out, xn_out, st, slices);
+    quant_launch_nc<SRC, 6>(x, part, ld, M, K, norm_w, eps, out, xn_out, st, slices);
 }
 
 }  // namespace
 
 bool gemm_i8_supported(int N, int K) {
-  return N > 0 && N % 16 == 0 && K > 0 && K % 256 == 0 && K <= kQuantThreads * kQuantChunks * 8;
+  return N > 0 && N % 16 == 0 && K > 0 && K % (32 * kChunkBlocks) == 0 &&
+         K <= kQuantThreads * kQuantChunks * 8;
 }
 
-int gemm_i8_chunks(int K) { return K / 256; }
+int gemm_i8_chunks(int K) { return K / (32 * kChunkBlocks); }
 
 size_t qact_bytes(int M, int K) {
   const size_t Mp = (M + 15) & ~15;
@@ -552,7 +581,7 @@ bool launch_gemm_i8_swiglu_quantize(const Mat &W, const QAct &xa, int M, QAct ou
                                     hipStream_t st) {
   if (M > 64 || W.K != 1024 || W.N % 64 != 0) return false;
   const int mt16 = (M + 15) >> 4;
-  hipLaunchKernelGGL(k_gemm_i8_swq<1>, dim3(W.N / 64, mt16), dim3(1024), 0, st, W.q, xa.q,
+  hipLaunchKernelGGL(k_gemm_i8_swq<1>, dim3(W.N / 64, mt16), dim3(512), 0, st, W.q, xa.q,
                      out.q, W.N, M);
   return true;
 }

@@ -162,6 +162,10 @@ void launch_gemm_i8(const Mat &W, const QAct &xa, int M, int epi, float *y, int 
 // the same chains for M <= kPartialRows, one wave per (16 rows, chunk):
 // part[gemm_i8_chunks(K)][M][N], to be added in chunk order by the consumer
 constexpr int kPartialRows = 64;
+// chunk partials a consumer of the batched products' partials reads (the
+// attention prologue, the code predictor's argmax): the chunks of a K of
+// at most 1024
+constexpr int kPartialSlots = 2;
 // rows from which a one-context forward takes the matrix-core prefill attention
 constexpr int kPrefillRows = 16;
 int gemm_i8_chunks(int K);

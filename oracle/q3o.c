@@ -13,7 +13,7 @@
  *  - Q8_0 weights with f32 activations: sum_b d_b * (sum_j q_j x_j);
  *  - Q8_0 weights with Q8_0 activations (ggml vec_dot_q8_0_q8_0): per block
  *    the exact int32 dot, times (dw_b * dx_b) (both scales via fp16), fused
- *    into a chain over the 8 blocks of each 256-column chunk; the chunk sums
+ *    into a chain over the 16 blocks of each 512-column chunk; the chunk sums
  *    added in chunk order;
  *  - attention scores: q . k as 16 partial chains (dims 8l .. 8l + 7) joined
  *    by a balanced pairwise tree; weighted values: 8 chains over the
@@ -253,9 +253,9 @@ static void linear_q(const void *W, int dtype, int act_q8, int N, int K,
           float acc = 0.0f;
           if (act_q8) {
             const q3o_block_q8_0 *x = xq + (size_t)m * nb;
-            for (int b0 = 0; b0 < nb; b0 += 8) {
+            for (int b0 = 0; b0 < nb; b0 += 16) {
               float part = 0.0f;
-              for (int b = b0; b < b0 + 8 && b < nb; b++) {
+              for (int b = b0; b < b0 + 16 && b < nb; b++) {
                 const int32_t s = idot32(w[b].qs, x[b].qs);
                 part = fmaf((float)s, q3o_fp16_to_fp32(w[b].d) * q3o_fp16_to_fp32(x[b].d),
                             part);

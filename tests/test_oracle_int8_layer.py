@@ -11,7 +11,7 @@ then checks, per layer:
     input, byte for byte (q/k/v: the input-normed row; o_proj: the attention
     output; gate / up: the post-attention normed row; down: SwiGLU's output);
   - every product equals the block-integer dot of those bytes with the weight
-    blocks, added per 256-column chunk as an fma chain and the chunks in order
+    blocks, added per 512-column chunk as an fma chain and the chunks in order
     (to the last bit but the double rounding of numpy's fma emulation);
   - every product input follows from the previous outputs by the Qwen3 layer:
     RMSNorm of the residual stream, QK-norm + RoPE + causal GQA softmax over
@@ -58,17 +58,17 @@ def blocks(b, n):
 
 
 def int8_product(wb, xb, K):
-    """y[m][n]: per 256-column chunk an fma chain acc = fma(dot, d_w d_x,
-    acc) over its 8 blocks, the chunk sums added in chunk order"""
+    """y[m][n]: per 512-column chunk an fma chain acc = fma(dot, d_w d_x,
+    acc) over its 16 blocks, the chunk sums added in chunk order"""
     dw, qw = blocks(wb, K)  # [N][nb], [N][nb][32]
     dx, qx = blocks(xb, K)  # [M][nb], [M][nb][32]
     dots = np.einsum("nbk,mbk->mnb", qw, qx)  # exact int32
     sc = f32(dx[:, None, :] * dw[None, :, :])
     nb = K // 32
     acc = np.zeros(dots.shape[:2], np.float32)
-    for b0 in range(0, nb, 8):
+    for b0 in range(0, nb, 16):
         part = np.zeros_like(acc)
-        for b in range(b0, min(b0 + 8, nb)):
+        for b in range(b0, min(b0 + 16, nb)):
             part = fma32(f32(dots[:, :, b]), sc[:, :, b], part)
         acc = f32(acc + part)
     return acc
