@@ -67,10 +67,12 @@ struct FrameDev {
 constexpr int kArgBlock = 1024;
 constexpr int kArgUnroll = 4;  // argmax rounds whose loads are issued together (4096 codes)
 
+// the block's (value, index) argmax; every thread merges the waves' results
+// itself (in wave order), so one barrier. Called once per kernel: its LDS is
+// not reused.
 __device__ int block_argmax(float v, int i) {
   __shared__ float sv[kArgBlock / 64];
   __shared__ int si[kArgBlock / 64];
-  __shared__ int res;
   for (int off = 32; off >= 1; off >>= 1) {
     const float v2 = __shfl_xor(v, off, 64);
     const int i2 = __shfl_xor(i, off, 64);
@@ -82,14 +84,10 @@ __device__ int block_argmax(float v, int i) {
     si[wave] = i;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    float bv = sv[0];
-    int bi = si[0];
-    for (int w = 1; w < (int)(blockDim.x >> 6); w++) argmax_merge(bv, bi, sv[w], si[w]);
-    res = bi;
-  }
-  __syncthreads();
-  return res;
+  float bv = sv[0];
+  int bi = si[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); w++) argmax_merge(bv, bi, sv[w], si[w]);
+  return bi;
 }
 
 // the descriptor of a row at position pos of context c (pos < 0: inactive)
@@ -109,9 +107,16 @@ __device__ __forceinline__ RowDesc row_desc(const CtxDev *c, int pos) {
 // inputs of both rows (zeros for a stream that does not run).
 template <bool SAMPLE>
 __global__ __launch_bounds__(kArgBlock) void k_choose_code0(FrameDev f) {
-  __shared__ double red[kArgBlock / 64];
+  __shared__ double red[2][kArgBlock / 64];
   __shared__ std::conditional_t<SAMPLE, SampleShared, char> sh;
   const int s = blockIdx.x, tid = threadIdx.x;
+  // the int8 path: this thread's chunks of the norm weights and of the past
+  // state (which does not depend on the code) loaded first
+  const bool q8 = f.cp_xq != nullptr;
+  float w8[8], pv[8], ev[8];
+  row_chunk8(q8 ? f.cp_norm0 : nullptr, f.H, w8);
+  row_chunk8(q8 ? f.past + (size_t)s * f.H : nullptr, f.H, pv);
+  row_chunk8(nullptr, f.H, ev);
   int code = -1;
   if (f.alive[s]) {
     const float *lg = f.logits + (size_t)s * f.vocab;
@@ -178,20 +183,34 @@ __global__ __launch_bounds__(kArgBlock) void k_choose_code0(FrameDev f) {
       float *x = f.cp_h + (size_t)s * 2 * f.H;
       const float *past = f.past + (size_t)s * f.H;
       const float *emb = f.codec_emb + (size_t)code * f.H;
-      for (int c = tid; c < f.H; c += kArgBlock) {
-        x[c] = past[c];
-        x[f.H + c] = emb[c];
+      if (q8) {  // the rows from registers (the embedding loaded once)
+        row_chunk8(emb, f.H, ev);
+        if (tid < (f.H >> 3)) {
+          float4 *xp = reinterpret_cast<float4 *>(x) + 2 * tid;
+          float4 *xe = reinterpret_cast<float4 *>(x + f.H) + 2 * tid;
+          xp[0] = make_float4(pv[0], pv[1], pv[2], pv[3]);
+          xp[1] = make_float4(pv[4], pv[5], pv[6], pv[7]);
+          xe[0] = make_float4(ev[0], ev[1], ev[2], ev[3]);
+          xe[1] = make_float4(ev[4], ev[5], ev[6], ev[7]);
+        }
+      } else {
+        for (int c = tid; c < f.H; c += kArgBlock) {
+          x[c] = past[c];
+          x[f.H + c] = emb[c];
+        }
       }
     }
   }
-  if (f.cp_xq) {
+  if (q8) {
+    // both rows quantized (zeros for a stream that does not run), each with
+    // its own reduction slots
     const bool live = code >= 0;
     if (tid < 2) f.cp_rd[2 * s + tid] = row_desc(f.cp_ctx[s], live ? tid : -1);
-    quant_row_block(live ? f.past + (size_t)s * f.H : nullptr, f.cp_norm0, f.cp_eps, f.H,
-                    2 * s, 2 * f.n, f.cp_xq, red);
-    __syncthreads();
-    quant_row_block(live ? f.codec_emb + (size_t)code * f.H : nullptr, f.cp_norm0, f.cp_eps,
-                    f.H, 2 * s + 1, 2 * f.n, f.cp_xq, red);
+    if (!live)
+#pragma unroll
+      for (int e = 0; e < 8; e++) pv[e] = 0.f;
+    quant_row_regs(pv, w8, live, f.cp_eps, f.H, 2 * s, 2 * f.n, f.cp_xq, red[0]);
+    quant_row_regs(ev, w8, live, f.cp_eps, f.H, 2 * s + 1, 2 * f.n, f.cp_xq, red[1]);
   }
 }
 
@@ -286,13 +305,6 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
   __shared__ std::conditional_t<SAMPLE, SampleShared, char> sh_cp;
   const int s = blockIdx.x, tid = threadIdx.x;
   const bool next = g + 1 < f.groups - 1;
-  if (!f.alive[s]) {
-    if (next) {
-      if (tid == 0) f.cp_rd[s] = row_desc(f.cp_ctx[s], -1);
-      quant_row_block(nullptr, nullptr, 0.f, f.H, s, f.n, f.cp_xq, red);
-    }
-    return;
-  }
   const int R = g == 0 ? 2 : 1, rows = R * f.n, row = R * s + R - 1;
   // the head's logit i: the chunk partials (cp_hch <= kPartialSlots) loaded
   // together, added in chunk order
@@ -307,13 +319,19 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
     for (int c = 0; c < NPS; c++) v = c < f.cp_hch ? __fadd_rn(v, p4[c]) : v;
     return v;
   };
-  int code;
-  if constexpr (SAMPLE) {
-    code = cp_draw(logit, f.cp_vocab, f.sp, f.seeds[s], f.nframes[s] - 1, g, sh_cp);
-  } else {
-    // every partial of the logits this thread merges, and of logit 0, loaded
-    // before the first sum (as in k_choose_code0)
-    float pl[kArgUnroll][NPS], p0[NPS];
+  auto chunk_sum = [&](const float(&p4)[NPS]) {
+    float v = 0.f;
+#pragma unroll
+    for (int c = 0; c < NPS; c++) v = c < f.cp_hch ? __fadd_rn(v, p4[c]) : v;
+    return v;
+  };
+  // issued before the stream's alive flag is known (the rows exist for every
+  // stream): this thread's chunk of the next input's norm weights and, for
+  // the argmax, every partial of the logits it merges and of logit 0
+  float w8[8];
+  row_chunk8(next ? f.cp_norm0 : nullptr, f.H, w8);
+  float pl[SAMPLE ? 1 : kArgUnroll][NPS], p0[NPS];
+  if constexpr (!SAMPLE) {
 #pragma unroll
     for (int k = 0; k < kArgUnroll; k++) {
       const int i = min(tid + k * kArgBlock, f.cp_vocab - 1);
@@ -324,12 +342,20 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
 #pragma unroll
     for (int c = 0; c < NPS; c++)
       p0[c] = f.cp_part[((size_t)min(c, f.cp_hch - 1) * rows + row) * f.cp_vocab];
-    auto chunk_sum = [&](const float(&p4)[NPS]) {
-      float v = 0.f;
-#pragma unroll
-      for (int c = 0; c < NPS; c++) v = c < f.cp_hch ? __fadd_rn(v, p4[c]) : v;
-      return v;
-    };
+  }
+  if (!f.alive[s]) {
+    if (next) {
+      if (tid == 0) f.cp_rd[s] = row_desc(f.cp_ctx[s], -1);
+      quant_row_block(nullptr, nullptr, 0.f, f.H, s, f.n, f.cp_xq, red);
+    }
+    return;
+  }
+  // the next row's descriptor does not depend on the code
+  if (next && tid == 0) f.cp_rd[s] = row_desc(f.cp_ctx[s], g + 2);
+  int code;
+  if constexpr (SAMPLE) {
+    code = cp_draw(logit, f.cp_vocab, f.sp, f.seeds[s], f.nframes[s] - 1, g, sh_cp);
+  } else {
     float bv = -INFINITY;
     int bi = 0x7fffffff;
 #pragma unroll
@@ -343,11 +369,16 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
   }
   if (tid == 0) f.codes[(size_t)s * f.groups + g + 1] = code;
   if (next) {
+    // the input row pred_emb[g][code], loaded once: to cp_h and quantized
     const float *emb = f.pred_emb + ((size_t)g * f.cp_vocab + code) * f.H;
-    float *x = f.cp_h + (size_t)s * f.H;
-    for (int c = tid; c < f.H; c += kArgBlock) x[c] = emb[c];
-    if (tid == 0) f.cp_rd[s] = row_desc(f.cp_ctx[s], g + 2);
-    quant_row_block(emb, f.cp_norm0, f.cp_eps, f.H, s, f.n, f.cp_xq, red);
+    float v[8];
+    row_chunk8(emb, f.H, v);
+    if (tid < (f.H >> 3)) {
+      float4 *x = reinterpret_cast<float4 *>(f.cp_h + (size_t)s * f.H) + 2 * tid;
+      x[0] = make_float4(v[0], v[1], v[2], v[3]);
+      x[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    quant_row_regs(v, w8, true, f.cp_eps, f.H, s, f.n, f.cp_xq, red);
   }
 }
 
@@ -399,6 +430,8 @@ __global__ __launch_bounds__(kArgBlock) void k_talker_input_q(FrameDev f) {
   __shared__ double red[kArgBlock / 64];
   __shared__ float xs[4096];
   const int s = blockIdx.x, tid = threadIdx.x;
+  float w8[8];  // this thread's chunk of the norm weights, loaded first
+  row_chunk8(f.t_norm0, f.H, w8);
   if (!f.alive[s]) {
     if (tid == 0) f.t_rd[s] = row_desc(f.t_ctx[s], -1);
     quant_row_block(nullptr, nullptr, 0.f, f.H, s, f.n, f.t_xq, red);
@@ -411,7 +444,9 @@ __global__ __launch_bounds__(kArgBlock) void k_talker_input_q(FrameDev f) {
   }
   if (tid == 0) f.t_rd[s] = row_desc(f.t_ctx[s], global_ptr(f.t_ctx[s])->len);
   __syncthreads();
-  quant_row_block(xs, f.t_norm0, f.t_eps, f.H, s, f.n, f.t_xq, red);
+  float v[8];
+  row_chunk8(xs, f.H, v);
+  quant_row_regs(v, w8, true, f.t_eps, f.H, s, f.n, f.t_xq, red);
 }
 
 // The rows of a device-side Start (TQwenTalker.Start, talker.pas:536-573):
