@@ -184,6 +184,8 @@ static void run_layers_partial(const q3h_stack *s, Work &w, int M, bool fused,
   const int I = c.intermediate, ldq = NQ + 2 * NKV;
   const bool kv16 = c.kv_f16 != 0;
   const float eps = c.rms_eps;
+  // rows in pairs of consecutive positions take the fused attention too
+  const bool pairs = io.row_pairs && M % 2 == 0 && attn_x_pairs_supported(c.max_positions);
   if (!io.input_quantized)
     launch_quantize_act(w.h, H, M, H, s->layers[0].in_norm, eps, w.xa, nullptr, st);
   for (int l = 0; l < c.layers; l++) {
@@ -196,10 +198,11 @@ static void run_layers_partial(const q3h_stack *s, Work &w, int M, bool fused,
     at.kvh = c.kv_heads;
     at.qkn = L.q_norm;
     at.rope_cs = reinterpret_cast<const float2 *>(s->rope_cs);
-    if (fused) {
+    if (fused || pairs) {
       launch_gemm_i8_partial(L.qkv, w.xa, M, w.gpart, st);
       at.qkv = w.gpart;
-      launch_attn_x(at, M, true, kv16, gemm_i8_chunks(H), w.xa, c.max_positions, st);
+      launch_attn_x(at, M, true, kv16, gemm_i8_chunks(H), w.xa, c.max_positions, st,
+                    !fused && pairs);
     } else {
       launch_gemm_i8(L.qkv, w.xa, M, EPI_STORE, w.qkv, ldq, st);
       launch_qk_rope_append(w.qkv, ldq, w.rd, M, l, c.heads, c.kv_heads, hd, L.q_norm,

@@ -165,6 +165,9 @@ struct LayerIO {
   const float *final_norm = nullptr;  // after the last layer: RMSNorm with it, quantized into w.xa
   bool single_context = false;        // the rows are consecutive positions of one context
   float *layer_out = nullptr;         // [layers][M][hidden] device: w.h after each layer
+  // the rows come in pairs, row 2i + 1 at the position after row 2i's in the
+  // same context (the int8 path over few rows then runs the fused attention)
+  bool row_pairs = false;
 };
 // whether run_layers takes the int8 partial-product path for M rows of stack s
 bool partial_path(const struct ::q3h_stack *s, int M);

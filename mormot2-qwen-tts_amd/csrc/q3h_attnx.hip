@@ -120,8 +120,12 @@ __device__ __forceinline__ float row16_tree(float v) {
 // keys (and, with PV, of values) is loaded right after the q/k/v loads, so
 // that it arrives during the prologue: the cache rows before the row's own
 // position were written by earlier launches, and the own position's key and
-// value are taken from the prologue in every round.
-template <typename KV, bool FUSED, int GRP, int SU, int VU, int NT, bool PV>
+// value are taken from the prologue in every round. PAIR (FUSED): rows come
+// in pairs, row 2i + 1 at the position after row 2i's in the same context;
+// the odd row's spare waves rebuild its pair row's key and value (the cache
+// row that row 2i's workgroup writes in this launch) from row 2i's partials
+// by the same code as that workgroup, so both rows run in one launch.
+template <typename KV, bool FUSED, int GRP, int SU, int VU, int NT, bool PV, bool PAIR>
 __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *qkv,
                                                const float *qkn, const float2 *rope_cs,
                                                int8_t *xq, int layer, int nch, int kvh,
@@ -134,6 +138,7 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
   static_assert(NWV % NCH == 0 && DPW * 64 * (NWV / NCH) == HD, "8 chains over 128 dims");
   extern __shared__ float sc[];  // [GRP][L]: scores, then e^(score - max)
   __shared__ float qs[GRP][HD], kn[HD], vn[HD];
+  __shared__ float kn2[PAIR ? HD : 1], vn2[PAIR ? HD : 1];  // the pair row's key, value
   __shared__ float cv[NCH][GRP][HD];
   __shared__ float redf[GRP][NWV];
   __shared__ double redd[GRP][NWV];
@@ -145,15 +150,19 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
   // output k of query head h, row m: element (m, h * 128 + k) of the operand tiles
   auto qoff = [&](int h, int k) { return qtile_offset(m, h * HD + k, mt16); };
   // vector j = wave: query head g GRP + j (j < GRP), the new k (j == GRP), v
-  // (GRP + 1); its loads depend on no descriptor, so they are issued first, by
-  // every wave (the waves past GRP + 1 load v again and do not use it: no
-  // divergent branch before the descriptor's scalar load)
-  static_assert(GRP + 2 <= NWV, "one prologue vector per wave");
+  // (GRP + 1), and with PAIR the pair row's k and v (GRP + 2, GRP + 3, of
+  // kind jv = j - 2); its loads depend on no descriptor, so they are issued
+  // first, by every wave (the waves past the last vector load v again and do
+  // not use it: no divergent branch before the descriptor's scalar load)
+  static_assert(GRP + (PAIR ? 4 : 2) <= NWV, "one prologue vector per wave");
   const int j = wave;
-  const bool pj = FUSED && j < GRP + 2;
-  const int col = j < GRP ? (g * GRP + j) * HD : j == GRP ? NQ + g * HD : NQ + (kvh + g) * HD;
+  const bool pairv = PAIR && j >= GRP + 2;
+  const int jv = pairv ? j - 2 : j;
+  const bool odd = PAIR && (m & 1);
+  const bool pj = FUSED && jv < GRP + 2;
+  const int col = jv < GRP ? (g * GRP + jv) * HD : jv == GRP ? NQ + g * HD : NQ + (kvh + g) * HD;
   float pa[NPS], pb[NPS];
-  if (FUSED) qkv_load(qkv, ldq, nch, M, m, col + lane, pa, pb);
+  if (FUSED) qkv_load(qkv, ldq, nch, M, pairv ? m & ~1 : m, col + lane, pa, pb);
   const RowDesc d = rd[m];
   if (d.pos < 0) {  // inactive row: zero blocks
     for (int i = t; i < GRP * HD; i += NT) {
@@ -164,6 +173,9 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
     return;
   }
   const int pos = d.pos, L = pos + 1;
+  // positions below clean hold rows written by earlier launches (the new
+  // position, and with PAIR the odd row's pair position, come from the prologue)
+  const int clean = FUSED ? pos - (odd ? 1 : 0) : L;
   const size_t head_off = ((size_t)layer * kvh + g) * d.max_pos * HD;
   const KV *kc = global_ptr(reinterpret_cast<const KV *>(d.k)) + head_off;
   const KV *vc = global_ptr(reinterpret_cast<const KV *>(d.v)) + head_off;
@@ -185,31 +197,34 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
         vp[u][e] = (float)vc[(size_t)min(ch + NCH * u, L - 1) * HD + dim0 + 64 * e];
   }
   if (FUSED) {
-    if (pj) {
+    if (pj && (!pairv || odd)) {
       float x0, x1;
       qkv_sum(nch, pa, pb, x0, x1);
-      if (j <= GRP) {
-        const float *w = qkn + (j < GRP ? 0 : HD);
+      if (jv <= GRP) {
+        const float *w = qkn + (jv < GRP ? 0 : HD);
         const float eps = qkn[2 * HD];
         double ss = (double)x0 * (double)x0 + (double)x1 * (double)x1;
         ss = wave_sum_dpp_d(ss);
         const float inv = (float)(1.0 / sqrt(ss / HD + (double)eps));
         x0 = w[lane] * (x0 * inv);
         x1 = w[lane + 64] * (x1 * inv);
-        const float2 cs = rope_cs[(size_t)pos * (HD / 2) + lane];
+        const int rp = pairv ? max(pos - 1, 0) : pos;
+        const float2 cs = rope_cs[(size_t)rp * (HD / 2) + lane];
         rope_pair(x0, x1, cs.x, cs.y);
       }
-      if (j < GRP) {
-        qs[j][lane] = x0;
-        qs[j][lane + 64] = x1;
+      if (jv < GRP) {
+        qs[jv][lane] = x0;
+        qs[jv][lane + 64] = x1;
       } else {
         const KV a0 = to_cache<KV>(x0), a1 = to_cache<KV>(x1);  // the cache's precision
-        float *own = j == GRP ? kn : vn;
+        float *own = jv == GRP ? (pairv ? kn2 : kn) : (pairv ? vn2 : vn);
         own[lane] = (float)a0;
         own[lane + 64] = (float)a1;
-        KV *dst = const_cast<KV *>(j == GRP ? kc : vc) + (size_t)pos * HD;
-        dst[lane] = a0;
-        dst[lane + 64] = a1;
+        if (!pairv) {
+          KV *dst = const_cast<KV *>(jv == GRP ? kc : vc) + (size_t)pos * HD;
+          dst[lane] = a0;
+          dst[lane + 64] = a1;
+        }
       }
     }
   } else {
@@ -222,13 +237,16 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
   // of SU positions are issued together
   const float scale = (float)(1.0 / __builtin_sqrt((double)HD));
   {
-    float qv[GRP][8], kn8[8];
+    float qv[GRP][8], kn8[8], kp8[8];
 #pragma unroll
     for (int j = 0; j < GRP; j++)
 #pragma unroll
       for (int e = 0; e < 8; e++) qv[j][e] = qs[j][8 * li + e];
 #pragma unroll
-    for (int e = 0; e < 8; e++) kn8[e] = FUSED ? kn[8 * li + e] : 0.f;
+    for (int e = 0; e < 8; e++) {
+      kn8[e] = FUSED ? kn[8 * li + e] : 0.f;
+      kp8[e] = PAIR ? kn2[8 * li + e] : 0.f;
+    }
     for (int p0 = 0; p0 < L; p0 += KG * SU) {
       // unconditional loads from clamped positions (a guarded load would be
       // waited for on its own), then the new position's own k, zeros past L
@@ -252,7 +270,10 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
             const int p = p0 + u * KG + kg;
 #pragma unroll
             for (int e = 0; e < 8; e++)
-              k8[u][e] = p >= L ? 0.f : FUSED && p == pos ? kn8[e] : k8[u][e];
+              k8[u][e] = p >= L               ? 0.f
+                         : FUSED && p == pos   ? kn8[e]
+                         : odd && p == pos - 1 ? kp8[e]
+                                               : k8[u][e];
           }
         }
 #pragma unroll
@@ -268,7 +289,7 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
           }
         }
       };
-      if (LONG && p0 + KG * SU <= (FUSED ? pos : L))
+      if (LONG && p0 + KG * SU <= clean)
         round(std::false_type{});
       else
         round(std::true_type{});
@@ -345,9 +366,12 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
     for (int e = 0; e < DPW; e++)
 #pragma unroll
       for (int j = 0; j < GRP; j++) c[e][j] = 0.f;
-    float vnd[DPW];
+    float vnd[DPW], vpd[DPW];
 #pragma unroll
-    for (int e = 0; e < DPW; e++) vnd[e] = FUSED ? vn[dim0 + 64 * e] : 0.f;
+    for (int e = 0; e < DPW; e++) {
+      vnd[e] = FUSED ? vn[dim0 + 64 * e] : 0.f;
+      vpd[e] = PAIR ? vn2[dim0 + 64 * e] : 0.f;
+    }
     for (int p0 = ch; p0 < L; p0 += NCH * VU) {
       float v[VU][DPW];
       if (PV && p0 == ch) {
@@ -374,7 +398,10 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
             const int p = p0 + NCH * u;
 #pragma unroll
             for (int e = 0; e < DPW; e++)
-              v[u][e] = p >= L ? 0.f : FUSED && p == pos ? vnd[e] : v[u][e];
+              v[u][e] = p >= L               ? 0.f
+                        : FUSED && p == pos   ? vnd[e]
+                        : odd && p == pos - 1 ? vpd[e]
+                                              : v[u][e];
           }
         }
         float wgt[VU][GRP];
@@ -394,7 +421,7 @@ __global__ __launch_bounds__(NT) void k_attn_x(const RowDesc *rd, const float *q
 #pragma unroll
             for (int e = 0; e < DPW; e++) c[e][j] = fmaf(wgt[u][j], v[u][e], c[e][j]);
       };
-      if (LONG && p0 + NCH * (VU - 1) < (FUSED ? pos : L))
+      if (LONG && p0 + NCH * (VU - 1) < clean)
         round(std::false_type{});
       else
         round(std::true_type{});
@@ -429,7 +456,7 @@ bool attn_x_supported(int heads, int kvh, int head_dim, int max_positions) {
          (size_t)max_positions * (heads / kvh) <= (size_t)kAttnXMaxPositions;
 }
 
-template <typename KV, bool F, int SU, int VU, int NT, bool PV>
+template <typename KV, bool F, int SU, int VU, int NT, bool PV, bool PAIR = false>
 void attn_x_grp(const AttnArgs &a, int M, int nch, const QAct &xa, int max_positions,
                 hipStream_t st) {
   const dim3 grid(a.kvh, M);
@@ -439,9 +466,9 @@ void attn_x_grp(const AttnArgs &a, int M, int nch, const QAct &xa, int max_posit
   // a hidden argument past them, would be a dependent load before the first)
   require(a.ldq == (a.heads + 2 * a.kvh) * HD, Q3H_E_ARG, "attention: q/k/v rows not packed");
   const size_t lds = sizeof(float) * (size_t)grp * max_positions;
-#define Q3H_ATTNX(G)                                                                           \
-  hipLaunchKernelGGL((k_attn_x<KV, F, G, SU, VU, NT, PV>), grid, dim3(NT), lds, st, a.rd, a.qkv,  \
-                     a.qkn, a.rope_cs, xa.q, a.layer, nch, a.kvh, M)
+#define Q3H_ATTNX(G)                                                                         \
+  hipLaunchKernelGGL((k_attn_x<KV, F, G, SU, VU, NT, PV, PAIR>), grid, dim3(NT), lds, st, a.rd, \
+                     a.qkv, a.qkn, a.rope_cs, xa.q, a.layer, nch, a.kvh, M)
   if (grp == 1)
     Q3H_ATTNX(1);
   else if (grp == 2)
@@ -460,8 +487,10 @@ void attn_x_grp(const AttnArgs &a, int M, int nch, const QAct &xa, int max_posit
 // per round. Results do not depend on the thread count or the round depths.
 template <typename KV, bool F>
 void attn_x_len(const AttnArgs &a, int M, int nch, const QAct &xa, int max_positions,
-                hipStream_t st) {
-  if (max_positions <= 32)
+                bool pairs, hipStream_t st) {
+  if (F && pairs)  // the short shape only (attn_x_pairs_supported)
+    attn_x_grp<KV, F, 1, 4, 512, true, true>(a, M, nch, xa, max_positions, st);
+  else if (max_positions <= 32)
     attn_x_grp<KV, F, 1, 4, 512, true>(a, M, nch, xa, max_positions, st);
   else if constexpr (F)
     attn_x_grp<KV, F, 4, 8, 512, true>(a, M, nch, xa, max_positions, st);
@@ -469,19 +498,23 @@ void attn_x_len(const AttnArgs &a, int M, int nch, const QAct &xa, int max_posit
     attn_x_grp<KV, F, 8, 16, 512, false>(a, M, nch, xa, max_positions, st);
 }
 
+bool attn_x_pairs_supported(int max_positions) { return max_positions <= 32; }
+
 void launch_attn_x(const AttnArgs &a, int M, bool fused, bool kv16, int qkv_chunks,
-                   const QAct &xa, int max_positions, hipStream_t st) {
+                   const QAct &xa, int max_positions, hipStream_t st, bool pairs) {
   const int nch = fused ? qkv_chunks : 0;
+  require(!pairs || (fused && M % 2 == 0 && attn_x_pairs_supported(max_positions)), Q3H_E_ARG,
+          "attention: row pairs need the fused short-context shape and an even row count");
   if (kv16) {
     if (fused)
-      attn_x_len<_Float16, true>(a, M, nch, xa, max_positions, st);
+      attn_x_len<_Float16, true>(a, M, nch, xa, max_positions, pairs, st);
     else
-      attn_x_len<_Float16, false>(a, M, nch, xa, max_positions, st);
+      attn_x_len<_Float16, false>(a, M, nch, xa, max_positions, false, st);
   } else {
     if (fused)
-      attn_x_len<float, true>(a, M, nch, xa, max_positions, st);
+      attn_x_len<float, true>(a, M, nch, xa, max_positions, pairs, st);
     else
-      attn_x_len<float, false>(a, M, nch, xa, max_positions, st);
+      attn_x_len<float, false>(a, M, nch, xa, max_positions, false, st);
   }
 }
 

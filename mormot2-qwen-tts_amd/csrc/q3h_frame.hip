@@ -665,6 +665,7 @@ void enqueue_step(q3h_frame *f, FrameSlice &sl, int positions, hipStream_t st) {
       LayerIO io;
       io.input_quantized = true;
       io.final_norm = cp->final_norm;
+      io.row_pairs = R == 2;  // rows 2s, 2s + 1: positions 0, 1 of stream s
       run_layers(cp, cw, n * R, c.groups, R == 1, st, io);
       launch_gemm_i8_partial(cp->heads[c.cp_heads[g]], cw.xa, n * R, cw.gpart, st);
       if (fd.sp.do_sample)

@@ -254,13 +254,16 @@ void launch_attn_merge_o(const AttnArgs &a, const Mat &wo, float *y, int positio
 // one new position of its own context, QK-norm / RoPE / K/V append in the
 // prologue), outputs quantized into xa for the o_proj product; positions up
 // to kAttnXMaxPositions / (heads / kv_heads) (the scores of a kv group held
-// in LDS). qkv_chunks in 1..4 (fused only):
+// in LDS). qkv_chunks in 1..kPartialSlots (fused only):
 // a.qkv holds the chunk partials [qkv_chunks][M][a.ldq] of the q/k/v product
-// instead of its rows, added in chunk order in the prologue.
+// instead of its rows, added in chunk order in the prologue. pairs (fused,
+// attn_x_pairs_supported): the rows come in pairs, row 2i + 1 at the position
+// after row 2i's in the same context (the code predictor's first step).
 constexpr int kAttnXMaxPositions = 8192;
 bool attn_x_supported(int heads, int kvh, int head_dim, int max_positions);
+bool attn_x_pairs_supported(int max_positions);
 void launch_attn_x(const AttnArgs &a, int M, bool fused, bool kv16, int qkv_chunks,
-                   const QAct &xa, int max_positions, hipStream_t st);
+                   const QAct &xa, int max_positions, hipStream_t st, bool pairs = false);
 
 // the code predictor's fused attention + o_proj (q3h_cp.hip): one context
 // of 16 positions, the new row at pos; k_layer: the layer's keys, values at
