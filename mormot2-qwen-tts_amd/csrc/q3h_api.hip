@@ -223,7 +223,7 @@ static void run_layers_partial(const q3h_stack *s, Work &w, int M, bool fused,
     const bool next = l + 1 < c.layers;
     const float *nw = next ? s->layers[l + 1].in_norm : io.final_norm;
     launch_residual_quantize(w.h, w.gpart, gemm_i8_chunks(I), M, H, nw, eps,
-                             nw ? &w.xa : nullptr, st);
+                             nw ? &w.xa : nullptr, st, next ? nullptr : io.final_normed);
     probe_layer(io, w, l, M, H, st);
   }
 }

@@ -163,6 +163,7 @@ void run_cp_fused_first(const struct ::q3h_stack *s, Work &w, const struct ::q3h
 struct LayerIO {
   bool input_quantized = false;       // w.xa already holds layer 0's normed, quantized input
   const float *final_norm = nullptr;  // after the last layer: RMSNorm with it, quantized into w.xa
+  float *final_normed = nullptr;      // [M][hidden] device: those normed rows (int8 path, few rows)
   bool single_context = false;        // the rows are consecutive positions of one context
   float *layer_out = nullptr;         // [layers][M][hidden] device: w.h after each layer
   // the rows come in pairs, row 2i + 1 at the position after row 2i's in the

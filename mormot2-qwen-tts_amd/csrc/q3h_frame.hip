@@ -32,6 +32,9 @@ struct FrameDev {
   float *logits;          // [n][vocab] talker logits
   float *past;            // [n][H] normed talker state
   int *codes;             // [n][groups]
+  // the host's pinned copy of the codes [n][groups] and alive flags [n]
+  // (coherent host memory, written by k_frame_end)
+  int32_t *host_codes, *host_alive;
   uint8_t *seen;          // [n][vocab]: codes already emitted (repetition penalty)
   int *nframes;           // [n]
   int *step;              // [n]
@@ -54,6 +57,7 @@ struct FrameDev {
   RowDesc *t_rd;           // [n]
   CtxDev *const *t_ctx;    // [n]
   int8_t *cp_xq, *t_xq;    // operand tiles of layer 0 of each stack
+  int t_fold;              // k_cp_next builds the talker input (int8 both, H <= kArgBlock)
   const float *cp_norm0, *t_norm0;
   float cp_eps, t_eps;
   const float *cp_part;    // head partials [cp_hch][rows][cp_vocab]
@@ -295,12 +299,27 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_sample(const float *__restrict
   }
 }
 
+// the last term of stream s's next talker input: its trailing text row for
+// this step, or tts_pad past them
+__device__ __forceinline__ const float *talker_tail(const FrameDev &f, int s) {
+  const int st = f.step[s];
+  return st < f.trailing_rows[s] ? f.trailing + ((size_t)s * f.max_trailing + st) * f.H
+                                 : f.tts_pad;
+}
+
 // The int8 path's k_cp_argmax: the head-g logits as the sum of the head's
 // chunk partials in chunk order (row R s + R - 1 of the step's R n rows),
 // ChooseCode for group g + 1, then the next step's input row pred_emb[g][code]
 // (to cp_h), its descriptor (position g + 2) and its quantized layer-0 input.
-template <bool SAMPLE>
+// FOLD (the last group's launch with t_fold: int8 talker, H <= kArgBlock; the
+// argmax variant, the sampler's registers leaving no room) also
+// builds the next talker input (k_talker_input_q's work): thread c loads
+// element c of every row whose code is known (codes 0 .. g) and of the tail
+// before the argmax, adds the new code's row after it, in talker_input_elem's
+// order, and writes the row, its descriptor and its quantized layer-0 input.
+template <bool SAMPLE, bool FOLD>
 __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
+  static_assert(!(SAMPLE && FOLD), "the talker input is folded into the argmax variant");
   __shared__ double red[kArgBlock / 64];
   __shared__ std::conditional_t<SAMPLE, SampleShared, char> sh_cp;
   const int s = blockIdx.x, tid = threadIdx.x;
@@ -330,6 +349,26 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
   // the argmax, every partial of the logits it merges and of logit 0
   float w8[8];
   row_chunk8(next ? f.cp_norm0 : nullptr, f.H, w8);
+  // the last group with t_fold: the talker's norm weights, and element tid of
+  // the tail and of the rows of codes 0 .. g (clamped codes: a stream that
+  // does not run loads valid rows it does not use)
+  __shared__ float xs[FOLD ? kArgBlock : 1];
+  constexpr bool fold = FOLD;
+  constexpr int G = FOLD ? 16 : 1;  // the most groups a frame takes
+  float tw8[8], te[G], tl = 0.f;
+  row_chunk8(fold ? f.t_norm0 : nullptr, f.H, tw8);
+  if constexpr (FOLD) {
+    const int *cd = f.codes + (size_t)s * f.groups;
+    const int c = min(tid, f.H - 1);
+#pragma unroll
+    for (int j = 0; j < G; j++) {
+      const int cj = j <= g ? max(cd[j], 0) : 0;
+      te[j] = j == 0 ? f.codec_emb[(size_t)cj * f.H + c]
+              : j <= g ? f.pred_emb[((size_t)(j - 1) * f.cp_vocab + cj) * f.H + c]
+                       : 0.f;
+    }
+    tl = talker_tail(f, s)[c];
+  }
   float pl[SAMPLE ? 1 : kArgUnroll][NPS], p0[NPS];
   if constexpr (!SAMPLE) {
 #pragma unroll
@@ -348,10 +387,16 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
       if (tid == 0) f.cp_rd[s] = row_desc(f.cp_ctx[s], -1);
       quant_row_block(nullptr, nullptr, 0.f, f.H, s, f.n, f.cp_xq, red);
     }
+    if (fold) {  // the talker row does not run: zero blocks
+      if (tid == 0) f.t_rd[s] = row_desc(f.t_ctx[s], -1);
+      quant_row_block(nullptr, nullptr, 0.f, f.H, s, f.n, f.t_xq, red);
+    }
     return;
   }
-  // the next row's descriptor does not depend on the code
+  // the next rows' descriptors do not depend on the code (the talker row's
+  // position: the context length)
   if (next && tid == 0) f.cp_rd[s] = row_desc(f.cp_ctx[s], g + 2);
+  if (fold && tid == 0) f.t_rd[s] = row_desc(f.t_ctx[s], global_ptr(f.t_ctx[s])->len);
   int code;
   if constexpr (SAMPLE) {
     code = cp_draw(logit, f.cp_vocab, f.sp, f.seeds[s], f.nframes[s] - 1, g, sh_cp);
@@ -368,9 +413,9 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
     code = first_max_code(block_argmax(bv, bi), chunk_sum(p0));
   }
   if (tid == 0) f.codes[(size_t)s * f.groups + g + 1] = code;
+  const float *emb = f.pred_emb + ((size_t)g * f.cp_vocab + code) * f.H;
   if (next) {
     // the input row pred_emb[g][code], loaded once: to cp_h and quantized
-    const float *emb = f.pred_emb + ((size_t)g * f.cp_vocab + code) * f.H;
     float v[8];
     row_chunk8(emb, f.H, v);
     if (tid < (f.H >> 3)) {
@@ -379,6 +424,25 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
       x[1] = make_float4(v[4], v[5], v[6], v[7]);
     }
     quant_row_regs(v, w8, true, f.cp_eps, f.H, s, f.n, f.cp_xq, red);
+  }
+  if constexpr (FOLD) {
+    // the next talker input: codec_emb[code 0] + pred_emb[j - 1][code j] for
+    // j = 1 .. g + 1 + the tail, added in that order
+    const int c = tid;
+    if (c < f.H) {
+      float x = te[0];
+#pragma unroll
+      for (int j = 1; j < G; j++)
+        if (j <= g) x = x + te[j];
+      x = x + emb[c];
+      x = x + tl;
+      f.t_h[(size_t)s * f.H + c] = x;
+      xs[c] = x;
+    }
+    __syncthreads();
+    float v[8];
+    row_chunk8(xs, f.H, v);
+    quant_row_regs(v, tw8, true, f.t_eps, f.H, s, f.n, f.t_xq, red);
   }
 }
 
@@ -392,10 +456,7 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
 __device__ __forceinline__ float talker_input_elem(const FrameDev &f, int s, int c) {
   constexpr int G = 16;  // the most groups a frame takes
   const int *codes = f.codes + (size_t)s * f.groups;
-  const int st = f.step[s];
-  const float *tail = st < f.trailing_rows[s]
-                          ? f.trailing + ((size_t)s * f.max_trailing + st) * f.H
-                          : f.tts_pad;
+  const float *tail = talker_tail(f, s);
   int code[G];
 #pragma unroll
   for (int g = 0; g < G; g++) code[g] = g < f.groups ? codes[g] : 0;
@@ -467,14 +528,22 @@ __global__ __launch_bounds__(256) void k_start_rows(const int2 *__restrict__ pla
 }
 
 // the end of a step: the frame count and the talker context length of every
-// running stream
+// running stream, and every stream's codes and alive flag into the host's
+// pinned copy (system-scope stores: in host memory when the kernel ends)
 __global__ void k_frame_end(FrameDev f) {
-  const int s = blockIdx.x * blockDim.x + threadIdx.x;
-  if (s < f.n && f.alive[s]) {
-    f.step[s] += 1;
-    CtxDev *c = global_ptr(f.t_ctx[s]);  // the talker context took the step's row
-    c->len = min(c->len + 1, c->max_pos);
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < f.n) {  // stream i
+    const int a = f.alive[i];
+    if (a) {
+      f.step[i] += 1;
+      CtxDev *c = global_ptr(f.t_ctx[i]);  // the talker context took the step's row
+      c->len = min(c->len + 1, c->max_pos);
+    }
+    __hip_atomic_store(f.host_alive + i, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
+  // code i of the slice's [n][groups] (consecutive threads, consecutive words)
+  if (i < f.n * f.groups)
+    __hip_atomic_store(f.host_codes + i, f.codes[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 }  // namespace q3h
@@ -565,6 +634,8 @@ FrameDev slice_view(const q3h_frame *f, FrameSlice &sl, bool cp_partial, bool t_
   d.logits += first * c.vocab;
   d.past += first * H;
   d.codes += first * c.groups;
+  d.host_codes = f->pinned + first * c.groups;
+  d.host_alive = f->pinned + (size_t)c.n_streams * c.groups + first;
   d.seen += first * c.vocab;
   d.nframes += first;
   d.step += first;
@@ -595,6 +666,7 @@ FrameDev slice_view(const q3h_frame *f, FrameSlice &sl, bool cp_partial, bool t_
     d.t_norm0 = f->talker->layers[0].in_norm;
     d.t_eps = f->talker->cfg.rms_eps;
   }
+  d.t_fold = cp_partial && t_partial && f->H <= kArgBlock;
   return d;
 }
 
@@ -669,9 +741,11 @@ void enqueue_step(q3h_frame *f, FrameSlice &sl, int positions, hipStream_t st) {
       run_layers(cp, cw, n * R, c.groups, R == 1, st, io);
       launch_gemm_i8_partial(cp->heads[c.cp_heads[g]], cw.xa, n * R, cw.gpart, st);
       if (fd.sp.do_sample)
-        hipLaunchKernelGGL(k_cp_next<true>, dim3(n), dim3(kArgBlock), 0, st, fd, g);
+        hipLaunchKernelGGL((k_cp_next<true, false>), dim3(n), dim3(kArgBlock), 0, st, fd, g);
+      else if (fd.t_fold && g + 1 == c.groups - 1)  // the last group: + the talker input
+        hipLaunchKernelGGL((k_cp_next<false, true>), dim3(n), dim3(kArgBlock), 0, st, fd, g);
       else
-        hipLaunchKernelGGL(k_cp_next<false>, dim3(n), dim3(kArgBlock), 0, st, fd, g);
+        hipLaunchKernelGGL((k_cp_next<false, false>), dim3(n), dim3(kArgBlock), 0, st, fd, g);
       continue;
     }
     if (fused && g == 0) {
@@ -697,24 +771,31 @@ void enqueue_step(q3h_frame *f, FrameSlice &sl, int positions, hipStream_t st) {
                          fd.pred_emb, fd.cp_h, fd.codes, fd.cp_vocab, fd.groups, fd.H, g);
   }
   // the talker
+  const Mat &th = tk->heads[c.talker_head];
   if (tq) {
-    hipLaunchKernelGGL(k_talker_input_q, dim3(n), dim3(kArgBlock), 0, st, fd);
+    // the last layer's residual kernel applies the final norm (the normed
+    // state to past) and quantizes the head input
+    // with t_fold the last (argmax) k_cp_next built the talker input
+    if (!(fd.t_fold && cq) || fd.sp.do_sample)
+      hipLaunchKernelGGL(k_talker_input_q, dim3(n), dim3(kArgBlock), 0, st, fd);
     LayerIO io;
     io.input_quantized = true;
+    io.final_norm = tk->final_norm;
+    io.final_normed = fd.past;
     run_layers(tk, tw, n, positions, true, st, io);
+    launch_gemm_i8(th, tw.xa, n, EPI_STORE, fd.logits, c.vocab, st);
   } else {
     hipLaunchKernelGGL(k_talker_input, dim3((H + 255) / 256, n), dim3(256), 0, st, fd);
     run_layers(tk, tw, n, positions, true, st);
+    if (n == 1) {  // final norm fused into the head, the normed state written alongside
+      linear(tk, tw, th, tw.h, H, 1, tk->final_norm, fd.logits, c.vocab, EPI_STORE, fd.past,
+             st);
+    } else {
+      launch_rmsnorm_rows(tw.h, H, n, H, tk->final_norm, tk->cfg.rms_eps, fd.past, H, st);
+      linear(tk, tw, th, fd.past, H, n, nullptr, fd.logits, c.vocab, EPI_STORE, nullptr, st);
+    }
   }
-  const Mat &th = tk->heads[c.talker_head];
-  if (n == 1) {  // final norm fused into the head, the normed state written alongside
-    linear(tk, tw, th, tw.h, H, 1, tk->final_norm, fd.logits, c.vocab, EPI_STORE, fd.past,
-           st);
-  } else {
-    launch_rmsnorm_rows(tw.h, H, n, H, tk->final_norm, tk->cfg.rms_eps, fd.past, H, st);
-    linear(tk, tw, th, fd.past, H, n, nullptr, fd.logits, c.vocab, EPI_STORE, nullptr, st);
-  }
-  hipLaunchKernelGGL(k_frame_end, dim3((n + 63) / 64), dim3(64), 0, st, fd);
+  hipLaunchKernelGGL(k_frame_end, dim3((n * c.groups + 63) / 64), dim3(64), 0, st, fd);
 }
 
 }  // namespace
@@ -824,12 +905,15 @@ extern "C" int q3h_frame_create(q3h_stack *talker, q3h_stack *cp, const q3h_fram
     d.tts_pad = f->tts_pad;
     d.cp_ctx = f->c_arr;
     d.t_ctx = f->t_arr;
+    // the host's copy of the codes and alive flags, written by the step's
+    // last kernel (coherent: the kernel's stores reach it uncached)
+    check_hip(hipHostMalloc((void **)&f->pinned, sizeof(int32_t) * n * (c.groups + 1),
+                            hipHostMallocCoherent),
+              "hipHostMalloc");
     refresh_slices(f);
     check_hip(hipMemset(d.alive, 0, sizeof(int) * n), "frame init");
     check_hip(hipMemset(const_cast<uint64_t *>(d.seeds), 0, sizeof(uint64_t) * n), "frame init");
     check_hip(hipMemset(d.codes, 0xff, sizeof(int) * n * c.groups), "frame init");
-    check_hip(hipHostMalloc((void **)&f->pinned, sizeof(int32_t) * n * (c.groups + 1)),
-              "hipHostMalloc");
     f->started.assign(n, 0);
     f->host_len.assign(n, 0);
     *out = f;
@@ -1162,16 +1246,8 @@ extern "C" int q3h_frame_step(q3h_frame *f, int32_t *codes, int32_t *alive) {
         enqueue_step(f, sl, graph_cover(slen, c.max_positions), sl.stream);
         check_hip(hipGetLastError(), "frame kernels");
       }
-      // the slice's codes and alive flags, into the same places of the pinned copy
-      check_hip(hipMemcpyAsync(f->pinned + (size_t)sl.first * c.groups,
-                               f->fd.codes + (size_t)sl.first * c.groups,
-                               sizeof(int32_t) * sl.n * c.groups, hipMemcpyDeviceToHost,
-                               sl.stream),
-                "download codes");
-      check_hip(hipMemcpyAsync(f->pinned + (size_t)n * c.groups + sl.first,
-                               f->fd.alive + sl.first, sizeof(int32_t) * sl.n,
-                               hipMemcpyDeviceToHost, sl.stream),
-                "download alive");
+      // the slice's codes and alive flags reach the pinned copy from the
+      // step's last kernel (k_frame_end)
     }
     for (FrameSlice &sl : f->slices)
       check_hip(hipStreamSynchronize(sl.stream), "frame step sync");

@@ -56,7 +56,8 @@ __device__ __forceinline__ float *scales_of(int8_t *xq, int M, int K) {
 //              <= 2 partials; gate / up interleaved, N = 2K).
 // Then RMSNorm when norm_w != nullptr (one slice only): y = w * (x * inv),
 // inv = 1/sqrt(mean(x^2) + eps) with the sum of squares in double; xn_out,
-// when non-null, receives the (normed) row M - 1; and the Q8_0 blocks
+// when non-null, receives the (normed) rows M - xn_rows .. M - 1 (row
+// M - xn_rows + r at xn_out + r K); and the Q8_0 blocks
 // (skipped when xq == nullptr). Partial loads are all issued before the sums.
 enum { SRC_X = 0, SRC_ADD = 1, SRC_SWIGLU = 2 };
 
@@ -69,7 +70,8 @@ template <int SRC, int KC, int NC>
 __global__ __launch_bounds__(kQuantThreads) void k_quant_act(float *x, const float *part,
                                                               int8_t *xq, const float *norm_w,
                                                               int M, int K, int ld, float eps,
-                                                              int nsl, float *xn_out) {
+                                                              int nsl, float *xn_out,
+                                                              int xn_rows) {
   const int m = blockIdx.x, t = threadIdx.x;
   const int mt16 = (M + 15) >> 4, nch = K >> 3, nb = K >> 5;
   const int j0 = blockIdx.y * kQuantThreads + t, js = kQuantThreads * nsl;
@@ -187,8 +189,8 @@ __global__ __launch_bounds__(kQuantThreads) void k_quant_act(float *x, const flo
       }
     }
   }
-  if (xn_out && m == M - 1) {
-    float4 *xo = reinterpret_cast<float4 *>(xn_out);
+  if (xn_out && m >= M - xn_rows) {
+    float4 *xo = reinterpret_cast<float4 *>(xn_out + (size_t)(m - (M - xn_rows)) * K);
 #pragma unroll
     for (int i = 0; i < KC; i++) {
       const int j = j0 + i * js;
@@ -507,13 +509,14 @@ void gemm_by_k(const Mat &W, const QAct &xa, int M, int epi, float *y, int ldy, 
 // slices > 1 only without a norm (each slice a whole number of 32-blocks)
 template <int SRC, int NC>
 void quant_launch_nc(float *x, const float *part, int ld, int M, int K, const float *norm_w,
-                     float eps, const QAct &out, float *xn_out, hipStream_t st, int slices) {
+                     float eps, const QAct &out, float *xn_out, int xn_rows, hipStream_t st,
+                     int slices) {
   const int Mp = (M + 15) & ~15;
   const int kc = (K / 8 + kQuantThreads * slices - 1) / (kQuantThreads * slices);
   const dim3 grid(Mp, slices);
 #define Q3H_QUANT(KC)                                                                          \
   hipLaunchKernelGGL((k_quant_act<SRC, KC, NC>), grid, dim3(kQuantThreads), 0, st, x, part,    \
-                     out.q, norm_w, M, K, ld, eps, slices, xn_out)
+                     out.q, norm_w, M, K, ld, eps, slices, xn_out, xn_rows)
   if (kc <= 1)
     Q3H_QUANT(1);
   else if (kc == 2)
@@ -525,13 +528,14 @@ void quant_launch_nc(float *x, const float *part, int ld, int M, int K, const fl
 
 template <int SRC>
 void quant_launch(float *x, const float *part, int ld, int M, int K, const float *norm_w,
-                  float eps, const QAct &out, float *xn_out, hipStream_t st, int slices = 1) {
+                  float eps, const QAct &out, float *xn_out, int xn_rows, hipStream_t st,
+                  int slices = 1) {
   if (SRC == SRC_X || ld <= 2)
-    quant_launch_nc<SRC, 2>(x, part, ld, M, K, norm_w, eps, out, xn_out, st, slices);
+    quant_launch_nc<SRC, 2>(x, part, ld, M, K, norm_w, eps, out, xn_out, xn_rows, st, slices);
   else if (ld <= 4)
-    quant_launch_nc<SRC, 4>(x, part, ld, M, K, norm_w, eps, out, xn_out, st, slices);
+    quant_launch_nc<SRC, 4>(x, part, ld, M, K, norm_w, eps, out, xn_out, xn_rows, st, slices);
   else
-    quant_launch_nc<SRC, 6>(x, part, ld, M, K, norm_w, eps, out, xn_out, st, slices);
+    quant_launch_nc<SRC, 6>(x, part, ld, M, K, norm_w, eps, out, xn_out, xn_rows, st, slices);
 }
 
 }  // namespace
@@ -550,18 +554,21 @@ size_t qact_bytes(int M, int K) {
 
 void launch_quantize_act(const float *x, int ldx, int M, int K, const float *norm_w, float eps,
                          QAct out, float *xn_out, hipStream_t st) {
-  quant_launch<SRC_X>(const_cast<float *>(x), nullptr, ldx, M, K, norm_w, eps, out, xn_out, st);
+  quant_launch<SRC_X>(const_cast<float *>(x), nullptr, ldx, M, K, norm_w, eps, out, xn_out, 1,
+                      st);
 }
 
 void launch_residual_quantize(float *h, const float *part, int chunks, int M, int K,
-                              const float *norm_w, float eps, const QAct *out, hipStream_t st) {
-  quant_launch<SRC_ADD>(h, part, chunks, M, K, norm_w, eps, out ? *out : QAct{}, nullptr, st);
+                              const float *norm_w, float eps, const QAct *out, hipStream_t st,
+                              float *normed) {
+  quant_launch<SRC_ADD>(h, part, chunks, M, K, norm_w, eps, out ? *out : QAct{}, normed, M, st);
 }
 
 void launch_swiglu_quantize(const float *part, int chunks, int M, int K, QAct out,
                             hipStream_t st) {
   const int slices = (K / 8 + kQuantThreads - 1) / kQuantThreads;
-  quant_launch<SRC_SWIGLU>(nullptr, part, chunks, M, K, nullptr, 0.f, out, nullptr, st, slices);
+  quant_launch<SRC_SWIGLU>(nullptr, part, chunks, M, K, nullptr, 0.f, out, nullptr, 0, st,
+                           slices);
 }
 
 void launch_gemm_i8(const Mat &W, const QAct &xa, int M, int epi, float *y, int ldy,

@@ -171,9 +171,11 @@ constexpr int kPrefillRows = 16;
 int gemm_i8_chunks(int K);
 void launch_gemm_i8_partial(const Mat &W, const QAct &xa, int M, float *part, hipStream_t st);
 // h [M][K] += the chunk partials of a product (in chunk order); then RMSNorm
-// with norm_w (when non-null) and quantization into *out (when non-null)
+// with norm_w (when non-null; every normed row also into normed [M][K] when
+// that is non-null) and quantization into *out (when non-null)
 void launch_residual_quantize(float *h, const float *part, int chunks, int M, int K,
-                              const float *norm_w, float eps, const QAct *out, hipStream_t st);
+                              const float *norm_w, float eps, const QAct *out, hipStream_t st,
+                              float *normed = nullptr);
 // the gate/up product, silu(gate) * up and its quantization into out in one
 // launch (M <= 64, K == 1024, N % 64 == 0; out must not alias xa); false
 // when the shape is not one it takes (nothing launched)
