@@ -584,19 +584,30 @@ void launch_gemm_i8(const Mat &W, const QAct &xa, int M, int epi, float *y, int 
 // Both products below take one 16-row activation tile per workgroup, the
 // tiles on a grid dimension of their own: a tile's waves do the work of a
 // 16-row product, and more rows add workgroups instead of lengthening each.
+// Above 32 rows a wave takes two tiles (its weights loaded once for both):
+// one tile per wave would put more workgroups than CUs on the gate/up product.
 bool launch_gemm_i8_swiglu_quantize(const Mat &W, const QAct &xa, int M, QAct out,
                                     hipStream_t st) {
   if (M > 64 || W.K != 1024 || W.N % 64 != 0) return false;
   const int mt16 = (M + 15) >> 4;
-  hipLaunchKernelGGL(k_gemm_i8_swq<1>, dim3(W.N / 64, mt16), dim3(512), 0, st, W.q, xa.q,
-                     out.q, W.N, M);
+  if (mt16 > 2)
+    hipLaunchKernelGGL(k_gemm_i8_swq<2>, dim3(W.N / 64, (mt16 + 1) / 2), dim3(512), 0, st, W.q,
+                       xa.q, out.q, W.N, M);
+  else
+    hipLaunchKernelGGL(k_gemm_i8_swq<1>, dim3(W.N / 64, mt16), dim3(512), 0, st, W.q, xa.q,
+                       out.q, W.N, M);
   return true;
 }
 
 void launch_gemm_i8_partial(const Mat &W, const QAct &xa, int M, float *part, hipStream_t st) {
   const int mt16 = (M + 15) >> 4;
-  const dim3 grid(W.N / 16, gemm_i8_chunks(W.K), mt16);
-  hipLaunchKernelGGL(k_gemm_i8p<1>, grid, dim3(64), 0, st, W.q, xa.q, part, W.N, W.K, M);
+  if (mt16 > 2) {
+    const dim3 grid(W.N / 16, gemm_i8_chunks(W.K), (mt16 + 1) / 2);
+    hipLaunchKernelGGL(k_gemm_i8p<2>, grid, dim3(64), 0, st, W.q, xa.q, part, W.N, W.K, M);
+  } else {
+    const dim3 grid(W.N / 16, gemm_i8_chunks(W.K), mt16);
+    hipLaunchKernelGGL(k_gemm_i8p<1>, grid, dim3(64), 0, st, W.q, xa.q, part, W.N, W.K, M);
+  }
 }
 
 }  // namespace q3h
