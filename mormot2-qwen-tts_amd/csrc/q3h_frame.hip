@@ -121,11 +121,27 @@ __global__ __launch_bounds__(kArgBlock) void k_choose_code0(FrameDev f) {
   row_chunk8(q8 ? f.cp_norm0 : nullptr, f.H, w8);
   row_chunk8(q8 ? f.past + (size_t)s * f.H : nullptr, f.H, pv);
   row_chunk8(nullptr, f.H, ev);
+  const float *lg = f.logits + (size_t)s * f.vocab;
+  const uint8_t *seen = f.seen + (size_t)s * f.vocab;
+  // the argmax's loads issued before the alive flag is known (every stream's
+  // rows exist): every logit this thread scores and its seen flag, logit 0,
+  // the frame count (kArgUnroll rounds unrolled, indices past the vocabulary
+  // clamped and not merged; a larger vocabulary continues in a loop)
+  float lv[SAMPLE ? 1 : kArgUnroll], l0 = 0.f;
+  uint8_t sv[SAMPLE ? 1 : kArgUnroll], s0 = 0;
+  if constexpr (!SAMPLE) {
+#pragma unroll
+    for (int k = 0; k < kArgUnroll; k++) {
+      const int i = min(tid + k * kArgBlock, f.vocab - 1);
+      lv[k] = lg[i];
+      sv[k] = seen[i];
+    }
+    l0 = lg[0];
+    s0 = seen[0];
+  }
+  const int nf = f.nframes[s];
   int code = -1;
   if (f.alive[s]) {
-    const float *lg = f.logits + (size_t)s * f.vocab;
-    const uint8_t *seen = f.seen + (size_t)s * f.vocab;
-    const int nf = f.nframes[s];
     // the scores of ChooseCode0's logits processors, of logit v of code i
     // (seen: code i already returned)
     auto score_v = [&](float v, bool sn, int i) {
@@ -147,19 +163,6 @@ __global__ __launch_bounds__(kArgBlock) void k_choose_code0(FrameDev f) {
       }
       code = block_sample<3>(x, f.vocab, f.sp0, draw_uniform(f.seeds[s], (uint64_t)nf, 0), sh);
     } else {
-      // every logit this thread scores, and logit 0, loaded before the first
-      // merge (kArgUnroll rounds unrolled, indices past the vocabulary
-      // clamped and not merged; a larger vocabulary continues in a loop)
-      float lv[kArgUnroll];
-      uint8_t sv[kArgUnroll];
-#pragma unroll
-      for (int k = 0; k < kArgUnroll; k++) {
-        const int i = min(tid + k * kArgBlock, f.vocab - 1);
-        lv[k] = lg[i];
-        sv[k] = seen[i];
-      }
-      const float l0 = lg[0];
-      const uint8_t s0 = seen[0];
       float bv = -INFINITY;
       int bi = 0x7fffffff;
 #pragma unroll
@@ -299,6 +302,30 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_sample(const float *__restrict
   }
 }
 
+// the end of a step for stream s (k_frame_end's work, by one workgroup): its
+// codes (code `code` at index `last`, the others from f.codes) and alive flag
+// into the host's pinned copy (system-scope stores: in host memory when the
+// kernel ends); a running stream's frame count and talker context length
+// advanced
+__device__ __forceinline__ void frame_end_stream(const FrameDev &f, int s, bool alive, int last,
+                                                 int code) {
+  const int t = threadIdx.x;
+  if (t < f.groups) {
+    const size_t i = (size_t)s * f.groups + t;
+    __hip_atomic_store(f.host_codes + i, t == last ? code : f.codes[i], __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+  if (t == 0) {
+    __hip_atomic_store(f.host_alive + s, alive ? 1 : 0, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+    if (alive) {
+      f.step[s] += 1;
+      CtxDev *c = global_ptr(f.t_ctx[s]);  // the talker context took the step's row
+      c->len = min(c->len + 1, c->max_pos);
+    }
+  }
+}
+
 // the last term of stream s's next talker input: its trailing text row for
 // this step, or tts_pad past them
 __device__ __forceinline__ const float *talker_tail(const FrameDev &f, int s) {
@@ -316,7 +343,9 @@ __device__ __forceinline__ const float *talker_tail(const FrameDev &f, int s) {
 // builds the next talker input (k_talker_input_q's work): thread c loads
 // element c of every row whose code is known (codes 0 .. g) and of the tail
 // before the argmax, adds the new code's row after it, in talker_input_elem's
-// order, and writes the row, its descriptor and its quantized layer-0 input.
+// order, and writes the row, its descriptor and its quantized layer-0 input;
+// and it does the stream's part of k_frame_end (the talker layers read the
+// row's descriptor, not the context length).
 template <bool SAMPLE, bool FOLD>
 __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
   static_assert(!(SAMPLE && FOLD), "the talker input is folded into the argmax variant");
@@ -387,9 +416,10 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
       if (tid == 0) f.cp_rd[s] = row_desc(f.cp_ctx[s], -1);
       quant_row_block(nullptr, nullptr, 0.f, f.H, s, f.n, f.cp_xq, red);
     }
-    if (fold) {  // the talker row does not run: zero blocks
+    if constexpr (FOLD) {  // the talker row does not run: zero blocks
       if (tid == 0) f.t_rd[s] = row_desc(f.t_ctx[s], -1);
       quant_row_block(nullptr, nullptr, 0.f, f.H, s, f.n, f.t_xq, red);
+      frame_end_stream(f, s, false, -1, 0);
     }
     return;
   }
@@ -443,11 +473,12 @@ __global__ __launch_bounds__(kArgBlock) void k_cp_next(FrameDev f, int g) {
     float v[8];
     row_chunk8(xs, f.H, v);
     quant_row_regs(v, tw8, true, f.t_eps, f.H, s, f.n, f.t_xq, red);
+    // after the barrier: every thread has read the frame count (the tail) and
+    // thread 0 the context length (the descriptor)
+    frame_end_stream(f, s, true, g + 1, code);
   }
 }
 
-// the next talker input: codec_emb[code 0] + sum_g pred_emb[g-1][code g] +
-// (trailing[step] or tts_pad), summed in that order; and its row descriptor.
 // element c of stream s's next talker input: codec_emb[code 0] +
 // pred_emb[g - 1][code g] for g = 1 .. groups - 1 + (trailing[step] or
 // tts_pad), added in that order. The codes (at most 16) are read first and
@@ -715,6 +746,8 @@ void enqueue_step(q3h_frame *f, FrameSlice &sl, int positions, hipStream_t st) {
   CtxDev **c_arr = f->c_arr + sl.first;
   q3h_context *cctx0 = f->cctx[sl.first];
   const bool cq = fd.cp_xq != nullptr, tq = fd.t_xq != nullptr;  // the folded int8 paths
+  // the last code-predictor argmax builds the talker input and ends the step
+  const bool fold_tail = cq && fd.t_fold && !fd.sp.do_sample;
   if (fd.sp0.do_sample)
     hipLaunchKernelGGL(k_choose_code0<true>, dim3(n), dim3(kArgBlock), 0, st, fd);
   else
@@ -742,7 +775,7 @@ void enqueue_step(q3h_frame *f, FrameSlice &sl, int positions, hipStream_t st) {
       launch_gemm_i8_partial(cp->heads[c.cp_heads[g]], cw.xa, n * R, cw.gpart, st);
       if (fd.sp.do_sample)
         hipLaunchKernelGGL((k_cp_next<true, false>), dim3(n), dim3(kArgBlock), 0, st, fd, g);
-      else if (fd.t_fold && g + 1 == c.groups - 1)  // the last group: + the talker input
+      else if (fold_tail && g + 1 == c.groups - 1)  // the last group: + the talker input
         hipLaunchKernelGGL((k_cp_next<false, true>), dim3(n), dim3(kArgBlock), 0, st, fd, g);
       else
         hipLaunchKernelGGL((k_cp_next<false, false>), dim3(n), dim3(kArgBlock), 0, st, fd, g);
@@ -776,8 +809,7 @@ void enqueue_step(q3h_frame *f, FrameSlice &sl, int positions, hipStream_t st) {
     // the last layer's residual kernel applies the final norm (the normed
     // state to past) and quantizes the head input
     // with t_fold the last (argmax) k_cp_next built the talker input
-    if (!(fd.t_fold && cq) || fd.sp.do_sample)
-      hipLaunchKernelGGL(k_talker_input_q, dim3(n), dim3(kArgBlock), 0, st, fd);
+    if (!fold_tail) hipLaunchKernelGGL(k_talker_input_q, dim3(n), dim3(kArgBlock), 0, st, fd);
     LayerIO io;
     io.input_quantized = true;
     io.final_norm = tk->final_norm;
@@ -795,7 +827,8 @@ void enqueue_step(q3h_frame *f, FrameSlice &sl, int positions, hipStream_t st) {
       linear(tk, tw, th, fd.past, H, n, nullptr, fd.logits, c.vocab, EPI_STORE, nullptr, st);
     }
   }
-  hipLaunchKernelGGL(k_frame_end, dim3((n * c.groups + 63) / 64), dim3(64), 0, st, fd);
+  if (!fold_tail)
+    hipLaunchKernelGGL(k_frame_end, dim3((n * c.groups + 63) / 64), dim3(64), 0, st, fd);
 }
 
 }  // namespace
