@@ -1243,6 +1243,9 @@ extern "C" int q3h_frame_step(q3h_frame *f, int32_t *codes, int32_t *alive) {
       for (int s = sl.first; s < sl.first + sl.n; s++)
         if (f->started[s]) slen = std::max(slen, f->host_len[s] + 1);
       if (slen == 0) continue;  // no stream of the slice runs (its codes read as -1)
+      // the int8 talker's step does not depend on the cover (its attention
+      // takes any context length): one graph, captured once for every length
+      if (sl.fd.t_xq) slen = c.max_positions;
       if (c.use_graph) {
         // the captured step that covers slen; on the first capture every
         // cover up to 256 positions is captured too, so that growing
