@@ -115,7 +115,7 @@ def test_frame_repetition_penalty_decides(device, name):
         cs.destroy()
 
 
-@pytest.mark.parametrize("name", ["q8_b1_graph", "q8_b1_direct", "q8_b3", "int8_b1"])
+@pytest.mark.parametrize("name", ["q8_b1_graph", "q8_b1_direct", "q8_b3", "int8_b1", "int8_b4"])
 def test_frame_eos_then_restart(device, name):
     """eos ends stream 0 (codes -1, alive 0) in the frame the reference's
     NextFrame returns false; at batch 1 the step that meets eos runs its whole
