@@ -515,6 +515,64 @@ __global__ void k_talker_input(FrameDev f) {
   f.t_h[(size_t)s * f.H + c] = x;
 }
 
+// k_cp_argmax of the last group (g + 1 == groups - 1) with k_talker_input's
+// and k_frame_end's work (greedy, f32 activations, H <= kArgBlock; one block
+// per stream): the argmax, then element tid of the next talker input (the
+// rows of codes 0 .. g and the tail loaded before the argmax, the new code's
+// row after it, added in talker_input_elem's order), the row's descriptor and
+// the stream's end of the step. The talker layers read the descriptor, not
+// the context length.
+__global__ __launch_bounds__(kArgBlock) void k_cp_argmax_end(FrameDev f, int g) {
+  const int s = blockIdx.x, tid = threadIdx.x;
+  const float *lg = f.cp_logits + (size_t)s * f.cp_vocab;
+  // the argmax's loads (every logit this thread merges, and logit 0), then
+  // element tid of the rows of the codes already chosen and of the tail
+  // (clamped codes: a stream that does not run loads valid rows it does not use)
+  float lv[kArgUnroll];
+#pragma unroll
+  for (int k = 0; k < kArgUnroll; k++) lv[k] = lg[min(tid + k * kArgBlock, f.cp_vocab - 1)];
+  const float l0 = lg[0];
+  constexpr int G = 16;  // the most groups a frame takes
+  const int *cd = f.codes + (size_t)s * f.groups;
+  const int c = min(tid, f.H - 1);
+  float te[G];
+#pragma unroll
+  for (int j = 0; j < G; j++) {
+    const int cj = j <= g ? max(cd[j], 0) : 0;
+    te[j] = j == 0 ? f.codec_emb[(size_t)cj * f.H + c]
+            : j <= g ? f.pred_emb[((size_t)(j - 1) * f.cp_vocab + cj) * f.H + c]
+                     : 0.f;
+  }
+  const float tl = talker_tail(f, s)[c];
+  if (!f.alive[s]) {
+    if (tid == 0) f.t_rd[s] = row_desc(f.t_ctx[s], -1);
+    frame_end_stream(f, s, false, -1, 0);
+    return;
+  }
+  if (tid == 0) f.t_rd[s] = row_desc(f.t_ctx[s], global_ptr(f.t_ctx[s])->len);
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+#pragma unroll
+  for (int k = 0; k < kArgUnroll; k++)
+    if (tid + k * kArgBlock < f.cp_vocab) argmax_merge(bv, bi, lv[k], tid + k * kArgBlock);
+  for (int i = tid + kArgUnroll * kArgBlock; i < f.cp_vocab; i += kArgBlock)
+    argmax_merge(bv, bi, lg[i], i);
+  const int code = first_max_code(block_argmax(bv, bi), l0);
+  if (tid == 0) f.codes[(size_t)s * f.groups + g + 1] = code;
+  if (tid < f.H) {
+    float x = te[0];
+#pragma unroll
+    for (int j = 1; j < G; j++)
+      if (j <= g) x = x + te[j];
+    x = x + f.pred_emb[((size_t)g * f.cp_vocab + code) * f.H + tid];
+    x = x + tl;
+    f.t_h[(size_t)s * f.H + tid] = x;
+  }
+  // every thread has read the frame count (the tail), thread 0 the length
+  __syncthreads();
+  frame_end_stream(f, s, true, g + 1, code);
+}
+
 // The int8 path's k_talker_input: one block per stream, the row also kept in
 // LDS for its descriptor (position = the context length) and its quantized
 // layer-0 input (H <= 4096).
@@ -747,7 +805,9 @@ void enqueue_step(q3h_frame *f, FrameSlice &sl, int positions, hipStream_t st) {
   q3h_context *cctx0 = f->cctx[sl.first];
   const bool cq = fd.cp_xq != nullptr, tq = fd.t_xq != nullptr;  // the folded int8 paths
   // the last code-predictor argmax builds the talker input and ends the step
+  // (int8: k_cp_next<false, true>; f32 activations: k_cp_argmax_end)
   const bool fold_tail = cq && fd.t_fold && !fd.sp.do_sample;
+  const bool fold_end = !cq && !tq && !fd.sp.do_sample && H <= kArgBlock;
   if (fd.sp0.do_sample)
     hipLaunchKernelGGL(k_choose_code0<true>, dim3(n), dim3(kArgBlock), 0, st, fd);
   else
@@ -799,6 +859,8 @@ void enqueue_step(q3h_frame *f, FrameSlice &sl, int positions, hipStream_t st) {
       hipLaunchKernelGGL(k_cp_sample, dim3(n), dim3(kArgBlock), 0, st, fd.cp_logits, fd.alive,
                          fd.pred_emb, fd.cp_h, fd.codes, fd.cp_vocab, fd.groups, fd.H, g, fd.sp,
                          fd.seeds, (const int *)fd.nframes);
+    else if (fold_end && g + 1 == c.groups - 1)
+      hipLaunchKernelGGL(k_cp_argmax_end, dim3(n), dim3(kArgBlock), 0, st, fd, g);
     else if (!code_in_product || g + 1 == c.groups - 1)
       hipLaunchKernelGGL(k_cp_argmax, dim3(n), dim3(kArgBlock), 0, st, fd.cp_logits, fd.alive,
                          fd.pred_emb, fd.cp_h, fd.codes, fd.cp_vocab, fd.groups, fd.H, g);
@@ -817,7 +879,8 @@ void enqueue_step(q3h_frame *f, FrameSlice &sl, int positions, hipStream_t st) {
     run_layers(tk, tw, n, positions, true, st, io);
     launch_gemm_i8(th, tw.xa, n, EPI_STORE, fd.logits, c.vocab, st);
   } else {
-    hipLaunchKernelGGL(k_talker_input, dim3((H + 255) / 256, n), dim3(256), 0, st, fd);
+    if (!fold_end)
+      hipLaunchKernelGGL(k_talker_input, dim3((H + 255) / 256, n), dim3(256), 0, st, fd);
     run_layers(tk, tw, n, positions, true, st);
     if (n == 1) {  // final norm fused into the head, the normed state written alongside
       linear(tk, tw, th, tw.h, H, 1, tk->final_norm, fd.logits, c.vocab, EPI_STORE, fd.past,
@@ -827,7 +890,7 @@ void enqueue_step(q3h_frame *f, FrameSlice &sl, int positions, hipStream_t st) {
       linear(tk, tw, th, fd.past, H, n, nullptr, fd.logits, c.vocab, EPI_STORE, nullptr, st);
     }
   }
-  if (!fold_tail)
+  if (!fold_tail && !fold_end)
     hipLaunchKernelGGL(k_frame_end, dim3((n * c.groups + 63) / 64), dim3(64), 0, st, fd);
 }
 
