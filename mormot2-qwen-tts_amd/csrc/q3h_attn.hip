@@ -92,17 +92,56 @@ __device__ __forceinline__ void cvt8(const u32x4 (&r)[2], float (&o)[8]) {
 //     prologue's vectors) instead of through the cache, so the cache rows
 //     read here are the positions before pos;
 //   - softmax in two passes over the workgroup (maximum, then sum).
+// Workgroups of k_attn_short past its query heads pull the cache rows that
+// the next layer's attention reads (positions [0, pos) of layer pf_layer,
+// keys and values of kv head g = i % kvh, i the workgroup's index among them)
+// into the L2 of the XCD that serves that attention's workgroups: the
+// dispatcher deals workgroup x to XCD x % 8, and this kernel's workgroup x of
+// kv head g has x % kvh == g, so with kvh a multiple of 8 and heads + i dealt
+// alike, the rows land where they are read. kPrefetchParts workgroups share a
+// kv head; each thread issues all of its 16-byte loads before using any, then
+// folds them into one value that an empty asm statement consumes (no store).
+constexpr int kPrefetchParts = 4;
+template <typename KV, int NTS>
+__device__ __forceinline__ void prefetch_next_layer(const RowDesc *__restrict__ rd, int pf_layer,
+                                                    int kvh, int i) {
+  const RowDesc d = rd[blockIdx.y];
+  if (d.pos <= 0) return;
+  const int g = i % kvh, part = i / kvh;
+  const size_t head_off = ((size_t)pf_layer * kvh + g) * d.max_pos * HD * sizeof(KV);
+  const char *kc = reinterpret_cast<const char *>(global_ptr(d.k)) + head_off;
+  const char *vc = reinterpret_cast<const char *>(global_ptr(d.v)) + head_off;
+  // 16-byte units of one tensor's rows [0, pos): at most 256 rows
+  const int units = d.pos * (HD * (int)sizeof(KV) / 16);
+  constexpr int PER = 2 * kSplit * (HD * (int)sizeof(KV) / 16) / (kPrefetchParts * NTS);
+  u32x4 r[PER];
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    const int u = min(part * NTS + (int)threadIdx.x + j * kPrefetchParts * NTS, 2 * units - 1);
+    r[j] = gload16(u < units ? kc + (size_t)u * 16 : vc + (size_t)(u - units) * 16);
+  }
+  unsigned f = 0;
+#pragma unroll
+  for (int j = 0; j < PER; j++) f ^= r[j].x ^ r[j].y ^ r[j].z ^ r[j].w;
+  asm volatile("" ::"v"(f));
+}
+
 template <typename KV, bool FUSED, int GRP, int NTS, int NJ>
 __global__ __launch_bounds__(NTS) void k_attn_short(const RowDesc *__restrict__ rd,
                                                     const float *__restrict__ qkv,
                                                     const float2 *__restrict__ rope_cs,
                                                     const float *__restrict__ qkn,
-                                                    float *__restrict__ outp, int layer, int kvh) {
+                                                    float *__restrict__ outp, int layer, int kvh,
+                                                    int pf_layer) {
   constexpr int PG = NTS / 16;         // position groups (NJ positions per thread)
   static_assert(NJ * PG <= kSplit, "at most 256 positions");
   constexpr int LW = sizeof(KV) / 2;   // 16-byte loads per 8 elements
   constexpr int NWV = NTS / 64;
   static_assert(NWV >= 3, "prologue waves");
+  if ((int)blockIdx.x >= GRP * kvh) {  // the next layer's cache rows (pf_layer >= 0)
+    prefetch_next_layer<KV, NTS>(rd, pf_layer, kvh, blockIdx.x - GRP * kvh);
+    return;
+  }
   __shared__ float qs[HD], kvn[2][HD];
   __shared__ float red[2][NWV];
   __shared__ float po[NWV][HD];
@@ -1046,10 +1085,13 @@ int launch_g(const AttnArgs &a, int M, int positions, hipStream_t st, bool merge
   hipLaunchKernelGGL((k_attn_split<KV, FUSED, G, 16 * NJ, 256>), dim3(a.kvh, S, M), dim3(256), 0, \
                      st, a.rd, a.qkv, a.rope_cs, a.qkn, a.layer, a.kvh, S, a.part)
   if (sh.len == kSplit && sh.threads == 0) {
+    // decode rows: extra workgroups pull the next layer's cache rows (above)
+    const int pf = FUSED && a.layer + 1 < a.layers ? a.layer + 1 : -1;
+    const int gx = a.heads + (pf >= 0 ? a.kvh * kPrefetchParts : 0);
     // 32 position groups: 2 positions per thread for every 64 covered
 #define Q3H_SH(NJ)                                                                          \
-  hipLaunchKernelGGL((k_attn_short<KV, FUSED, G, 512, NJ>), dim3(a.heads, M), dim3(512), 0, st, \
-                     a.rd, a.qkv, a.rope_cs, a.qkn, a.out, a.layer, a.kvh)
+  hipLaunchKernelGGL((k_attn_short<KV, FUSED, G, 512, NJ>), dim3(gx, M), dim3(512), 0, st,    \
+                     a.rd, a.qkv, a.rope_cs, a.qkn, a.out, a.layer, a.kvh, pf)
     switch ((std::max(positions, 1) + 63) / 64) {
       case 1: Q3H_SH(2); break;
       case 2: Q3H_SH(4); break;
