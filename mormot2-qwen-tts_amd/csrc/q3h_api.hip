@@ -352,7 +352,7 @@ void run_layers(const q3h_stack *s, Work &w, int M, int positions, bool fused, h
     at.rope_cs = reinterpret_cast<const float2 *>(s->rope_cs);
     at.out = w.att;
     at.part = w.part;
-    at.layers = c.layers;  // decode: the next layer's cache rows pulled into L2 ahead
+    at.layers = c.layers;  // decode: the next layer's cache rows loaded one launch ahead
     if (!fused && io.single_context && M >= kPrefillRows) {
       launch_attn_prefill(at, M, kv16, st);
     } else if (attn_merge_o_supported(at, L.o, M, positions, kv16)) {

@@ -92,15 +92,18 @@ __device__ __forceinline__ void cvt8(const u32x4 (&r)[2], float (&o)[8]) {
 //     prologue's vectors) instead of through the cache, so the cache rows
 //     read here are the positions before pos;
 //   - softmax in two passes over the workgroup (maximum, then sum).
-// Workgroups of k_attn_short past its query heads pull the cache rows that
-// the next layer's attention reads (positions [0, pos) of layer pf_layer,
-// keys and values of kv head g = i % kvh, i the workgroup's index among them)
-// into the L2 of the XCD that serves that attention's workgroups: the
-// dispatcher deals workgroup x to XCD x % 8, and this kernel's workgroup x of
-// kv head g has x % kvh == g, so with kvh a multiple of 8 and heads + i dealt
-// alike, the rows land where they are read. kPrefetchParts workgroups share a
-// kv head; each thread issues all of its 16-byte loads before using any, then
-// folds them into one value that an empty asm statement consumes (no store).
+// Workgroups of k_attn_short past its query heads load, one launch ahead, the
+// cache rows that the next layer's attention reads (positions [0, pos) of
+// layer pf_layer, keys and values of kv head g = i % kvh, i the workgroup's
+// index among them), on the XCD of that attention's workgroups (the
+// dispatcher deals workgroup x to XCD x % 8; workgroup x of kv head g has
+// x % kvh == g). The L2 does not keep them until then: in the batch-1 frame
+// each launch fetches its own rows past L2 again (FETCH_SIZE per launch = its
+// own rows + the next layer's), but those fetches complete sooner (3.95 against
+// 5.44 us per layer at 126 positions), as from the memory-side Infinity Cache
+// rather than HBM. kPrefetchParts workgroups share a kv head; each thread
+// issues all of its 16-byte loads before using any, then folds them into one
+// value that an empty asm statement consumes (no store).
 constexpr int kPrefetchParts = 4;
 template <typename KV, int NTS>
 __device__ __forceinline__ void prefetch_next_layer(const RowDesc *__restrict__ rd, int pf_layer,
@@ -1085,7 +1088,7 @@ int launch_g(const AttnArgs &a, int M, int positions, hipStream_t st, bool merge
   hipLaunchKernelGGL((k_attn_split<KV, FUSED, G, 16 * NJ, 256>), dim3(a.kvh, S, M), dim3(256), 0, \
                      st, a.rd, a.qkv, a.rope_cs, a.qkn, a.layer, a.kvh, S, a.part)
   if (sh.len == kSplit && sh.threads == 0) {
-    // decode rows: extra workgroups pull the next layer's cache rows (above)
+    // decode rows: extra workgroups load the next layer's cache rows ahead (above)
     const int pf = FUSED && a.layer + 1 < a.layers ? a.layer + 1 : -1;
     const int gx = a.heads + (pf >= 0 ? a.kvh * kPrefetchParts : 0);
     // 32 position groups: 2 positions per thread for every 64 covered

@@ -213,7 +213,7 @@ struct AttnArgs {
   const float2 *rope_cs;
   float *out;    // [M][heads * head_dim]
   float *part;   // [M][heads][attn_splits slots][head_dim + 2]
-  int layers;    // > layer + 1: a decode launch also pulls layer + 1's cache rows into L2
+  int layers;    // > layer + 1: a decode launch also loads layer + 1's cache rows ahead
 };
 // how the decode attention cuts contexts of up to `positions` positions: len
 // positions per split (a multiple of 16), threads per workgroup (0: one
